@@ -1,0 +1,307 @@
+"""Benchmark of the fused LoRA / RMSNorm / softmax hot path on one MI355X.
+
+A step is one forward + backward pass of the custom ops of one decoder layer
+(BASELINE.json config 4 by default: a Qwen2.5-1.5B-shaped layer, bf16,
+tokens 8 x 2048, hidden 1536, intermediate 8960, 12 q / 2 kv heads of 128,
+LoRA rank 16 / alpha 32 on all 7 projections, preceded by RMSNorm):
+
+  forward   RMSNorm(input_layernorm) -> LoRA q, k, v (with bias)
+            causal softmax over the [8, 12, 2048, 2048] attention scores
+            LoRA o_proj ; RMSNorm(post_attention_layernorm)
+            LoRA gate, up ; LoRA down
+  backward  the same ops in reverse (dX, dA, dB for every projection with W
+            frozen; dx, dw for both norms; dS for the softmax)
+
+The attention matmuls and the SiLU are not custom ops of the reference and
+are not part of the step; their outputs are synthetic tensors of the right
+shape. Inputs are synthetic (seeded normal / kaiming-uniform draws) and
+resident in HBM before timing starts.
+
+value = tokens / second of the timed steps. The roofline object is for the
+dominant kernel, the MFMA GEMM (base x.W^T / dY.W with the rank-r columns
+folded in), timed per launch with hipEvents on its stream by the library's
+profiling hook; achieved counts the base-product FLOPs only.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+FP32_PEAK_TFLOPS = 157.3
+
+CONFIGS = {
+    # name: tokens, hidden, intermediate, q heads, kv heads, head_dim, rank, alpha, dropout, batch, seq, dtype
+    "c3": dict(batch=16, seq=512, hidden=896, inter=None, heads=14, kv_heads=2, head_dim=64, rank=8, alpha=16,
+               dropout=0.0, projections=("q", "v"), norm=False, softmax=False, dtype="bf16",
+               workload="LoRA fwd+bwd, Qwen2.5-0.5B-shaped q_proj 896->896 + v_proj 896->128, r8, T=16x512"),
+    "c4": dict(batch=8, seq=2048, hidden=1536, inter=8960, heads=12, kv_heads=2, head_dim=128, rank=16, alpha=32,
+               dropout=0.0, projections=("q", "k", "v", "o", "gate", "up", "down"), norm=True, softmax=True,
+               dtype="bf16",
+               workload="Qwen2.5-1.5B-shaped decoder layer custom ops fwd+bwd: RMSNorm x2, LoRA r16 on 7 "
+                        "projections, causal softmax [8,12,2048,2048]; T=8x2048"),
+    "c5": dict(batch=4, seq=4096, hidden=3584, inter=18944, heads=28, kv_heads=4, head_dim=128, rank=64, alpha=128,
+               dropout=0.1, projections=("q", "k", "v", "o", "gate", "up", "down"), norm=True, softmax=True,
+               dtype="bf16",
+               workload="Qwen2.5-7B-shaped decoder layer custom ops fwd+bwd: RMSNorm x2, LoRA r64 p=0.1 on 7 "
+                        "projections, causal softmax [4,28,4096,4096]; T=4x4096"),
+}
+
+
+def proj_shapes(c):
+    h, kv = c["hidden"], c["kv_heads"] * c["head_dim"]
+    inter = c["inter"]
+    table = {
+        "q": (h, c["heads"] * c["head_dim"], True),
+        "k": (h, kv, True),
+        "v": (h, kv, True),
+        "o": (c["heads"] * c["head_dim"], h, False),
+        "gate": (h, inter, False),
+        "up": (h, inter, False),
+        "down": (inter, h, False),
+    }
+    return {p: table[p] for p in c["projections"]}
+
+
+class Layer:
+    """Device-resident tensors of one layer's custom ops."""
+
+    def __init__(self, mc, c, dev, seed=0):
+        import torch
+
+        self.mc, self.c, self.dev = mc, c, dev
+        self.T = c["batch"] * c["seq"]
+        dt = torch.bfloat16 if c["dtype"] == "bf16" else torch.float32
+        g = torch.Generator(device=dev).manual_seed(seed)
+        rn = lambda *s, std=1.0: (torch.randn(*s, generator=g, device=dev) * std)  # noqa: E731
+        T, H = self.T, c["hidden"]
+        self.scale = c["alpha"] / c["rank"]
+        self.p = c["dropout"]
+        self.proj = {}
+        for name, (K, N, bias) in proj_shapes(c).items():
+            b = 1.0 / K ** 0.5
+            self.proj[name] = dict(
+                K=K, N=N,
+                W=rn(N, K, std=0.02).to(dt),
+                bias=rn(N, std=0.02).to(dt) if bias else None,
+                A=(torch.rand(K, c["rank"], generator=g, device=dev) * 2 - 1) * b,
+                B=rn(c["rank"], N, std=0.02),
+                dy=rn(T, N, std=1e-2).to(dt),
+                mask=(mc.dropout_mask(1234 + len(self.proj), self.p, T, c["rank"]).to(dev) if self.p > 0 else None),
+            )
+        self.h_in = rn(T, H).to(dt)
+        self.h_mid = rn(T, H).to(dt)
+        self.attn = rn(T, c["heads"] * c["head_dim"]).to(dt)
+        self.act = rn(T, c["inter"]).to(dt) if c["inter"] else None
+        self.ln1 = (rn(H, std=0.1) + 1.0).to(dt)
+        self.ln2 = (rn(H, std=0.1) + 1.0).to(dt)
+        self.dy_ln = rn(T, H, std=1e-2).to(dt)
+        if c["softmax"]:
+            shape = (c["batch"], c["heads"], c["seq"], c["seq"])
+            self.scores = (rn(*shape, std=3.0)).to(dt)
+            self.dP = (rn(*shape, std=1e-2)).to(dt)
+        self.xn1 = rn(T, H).to(dt)
+        self.xn2 = rn(T, H).to(dt)
+
+    def _input_of(self, name):
+        if name in ("q", "k", "v"):
+            return self.xn1
+        if name == "o":
+            return self.attn
+        if name in ("gate", "up"):
+            return self.xn2
+        return self.act
+
+    def step(self):
+        mc, c = self.mc, self.c
+        saved = {}
+        if c["norm"]:
+            self.xn1, r1 = mc.rms_norm_forward(self.h_in, 1e-6, self.ln1)
+        order_f = [p for p in ("q", "k", "v") if p in self.proj]
+        for name in order_f:
+            saved[name] = self._lora_f(name)
+        P = mc.softmax_forward(self.scores, causal_rows=c["seq"]) if c["softmax"] else None
+        if "o" in self.proj:
+            saved["o"] = self._lora_f("o")
+        if c["norm"]:
+            self.xn2, r2 = mc.rms_norm_forward(self.h_mid, 1e-6, self.ln2)
+        for name in ("gate", "up", "down"):
+            if name in self.proj:
+                saved[name] = self._lora_f(name)
+        # backward
+        for name in ("down", "up", "gate"):
+            if name in self.proj:
+                self._lora_b(name, saved[name])
+        if c["norm"]:
+            mc.rms_norm_backward(self.h_mid, self.dy_ln, 1e-6, self.ln2, r2)
+        if "o" in self.proj:
+            self._lora_b("o", saved["o"])
+        if c["softmax"]:
+            mc.softmax_backward(P, self.dP, causal_rows=c["seq"])
+        for name in ("v", "k", "q"):
+            if name in self.proj:
+                self._lora_b(name, saved[name])
+        if c["norm"]:
+            mc.rms_norm_backward(self.h_in, self.dy_ln, 1e-6, self.ln1, r1)
+
+    def _lora_f(self, name):
+        pr = self.proj[name]
+        _, h = self.mc.lora_forward(self._input_of(name), pr["A"], pr["B"], self.scale, W=pr["W"],
+                                    bias=pr["bias"], mask=pr["mask"], dropout_p=self.p)
+        return h
+
+    def _lora_b(self, name, h):
+        pr = self.proj[name]
+        self.mc.lora_backward(self._input_of(name), pr["A"], pr["B"], pr["dy"], self.scale, W=pr["W"],
+                              mask=pr["mask"], dropout_p=self.p, h_save=h)
+
+    def flops_per_step(self):
+        base = sum(4.0 * self.T * p["K"] * p["N"] for p in self.proj.values())
+        low = sum(6.0 * self.T * self.c["rank"] * (p["K"] + p["N"]) for p in self.proj.values())
+        return base, low
+
+
+def cpu_baseline(c, tokens, threads):
+    """The oracle (C, fp64 accumulation, OpenMP) on a token sample of the
+    same layer: LoRA fwd+bwd of every projection, both RMSNorms fwd+bwd and
+    the softmax rows of the sampled tokens. Returns tokens / second."""
+    import numpy as np
+
+    import oracle
+
+    rng = np.random.default_rng(0)
+    T = tokens
+    f32 = lambda *s, std=1.0: (rng.standard_normal(s) * std).astype(np.float32)  # noqa: E731
+    work = []
+    for name, (K, N, bias) in proj_shapes(c).items():
+        b = 1.0 / K ** 0.5
+        work.append(dict(x=f32(T, K), W=f32(N, K, std=0.02), bias=f32(N, std=0.02) if bias else None,
+                         A=((rng.random((K, c["rank"])) * 2 - 1) * b).astype(np.float32),
+                         B=f32(c["rank"], N, std=0.02), dy=f32(T, N, std=1e-2),
+                         mask=oracle.dropout_mask(1234, c["dropout"], T, c["rank"]) if c["dropout"] > 0 else None))
+    H = c["hidden"]
+    xs, dys, w = f32(T, H), f32(T, H, std=1e-2), f32(H, std=0.1) + 1
+    S = c["seq"]
+    srows = T * c["heads"] if c["softmax"] else 0
+    scores = f32(srows, S, std=3.0) if srows else None
+    dP = f32(srows, S, std=1e-2) if srows else None
+    ids = (np.arange(srows) % S).astype(np.int64) if srows else None
+    s = c["alpha"] / c["rank"]
+    t0 = time.perf_counter()
+    for wk in work:
+        oracle.lora_fwd(wk["x"], wk["A"], wk["B"], s, W=wk["W"], bias=wk["bias"], mask=wk["mask"],
+                        p=c["dropout"], threads=threads)
+        oracle.lora_bwd(wk["x"], wk["A"], wk["B"], wk["dy"], s, W=wk["W"], mask=wk["mask"], p=c["dropout"],
+                        threads=threads)
+    if c["norm"]:
+        for _ in range(2):
+            oracle.rmsnorm_fwd(xs, 1e-6, w, threads=threads)
+            oracle.rmsnorm_bwd(xs, dys, 1e-6, w, threads=threads)
+    if srows:
+        P = oracle.softmax_fwd(scores, causal_rows=S, threads=threads, row_ids=ids)
+        oracle.softmax_bwd(P, dP, causal_rows=S, threads=threads, row_ids=ids)
+    dt = time.perf_counter() - t0
+    return T / dt, dt
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="c4", choices=sorted(CONFIGS))
+    ap.add_argument("--cpu-tokens", type=int, default=256, help="token sample of the CPU-oracle baseline")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (every box in this setup has one); --gpus {args.gpus} "
+              "is not supported", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import __graft_entry__
+
+    mc = __graft_entry__.load_package()
+    dev = torch.device("cuda:0")
+    c = CONFIGS[args.config]
+    layer = Layer(mc, c, dev)
+    for _ in range(args.warmup):
+        layer.step()
+    torch.cuda.synchronize()
+
+    mc._lib.check(mc._lib.lib().mc_profile_reset())
+    mc._lib.check(mc._lib.lib().mc_profile_enable(1))
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        layer.step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    mc._lib.check(mc._lib.lib().mc_profile_enable(0))
+    mc._lib.check(mc._lib.lib().mc_profile_collect())
+
+    ms_step = elapsed * 1e3 / args.steps
+    tokens_s = layer.T / (elapsed / args.steps)
+    kernels = {}
+    for kind in ("gemm", "lowrank", "rmsnorm", "softmax"):
+        ms, n, fl, by = mc._lib.profile_read(kind)
+        if n == 0:
+            continue
+        kernels[kind] = {
+            "launches_per_step": n / args.steps,
+            "ms_per_step": ms / args.steps,
+            "avg_launch_us": ms * 1e3 / n,
+            "TFLOP_s": fl / (ms * 1e-3) / 1e12 if fl else None,
+            "GB_s": by / (ms * 1e-3) / 1e9,
+            "hbm_frac": by / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        }
+
+    gemm_ms, gemm_n, gemm_fl, _ = mc._lib.profile_read("gemm")
+    achieved = gemm_fl / gemm_n / (gemm_ms / gemm_n * 1e-3) / 1e12
+    base_fl, low_fl = layer.flops_per_step()
+    line = {
+        "metric": "LoRA fwd+bwd tokens/s + MFMA util @1.5B shapes; RMSNorm/softmax HBM GB/s",
+        "value": tokens_s,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": c["dtype"],
+        "data": "synthetic (seeded normal / kaiming-uniform, resident in HBM)",
+        "config": {"workload": c["workload"], "config": args.config, "tokens": layer.T, "rank": c["rank"],
+                   "alpha": c["alpha"], "dropout": c["dropout"]},
+        "roofline": {
+            "kernel": "gemm_bf16_kernel (base GEMMs x.W^T and dY.W with the rank-r columns folded in)",
+            "bound": "mfma",
+            "achieved": achieved,
+            "peak": BF16_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": achieved / BF16_PEAK_TFLOPS,
+            "traffic": None,
+        },
+        "layer_TFLOP_s": (base_fl + low_fl) / (ms_step * 1e-3) / 1e12,
+        "kernels": kernels,
+    }
+    if not args.no_cpu_baseline:
+        threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
+        v, dt = cpu_baseline(c, args.cpu_tokens, threads)
+        line["cpu_baseline"] = {
+            "value": v, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"{args.cpu_tokens} tokens of the same layer (LoRA fwd+bwd x{len(c['projections'])}, "
+                      f"RMSNorm fwd+bwd x2, softmax rows of those tokens) through the C oracle, {dt:.1f} s",
+        }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,169 @@
+/*
+ * mc_hip.h - C ABI of the MI355X (gfx950) fused LoRA / RMSNorm / softmax path.
+ *
+ * This is the drop-in boundary for the fused custom ops of GarthDB/metal-candle
+ * v1.3.0. Each entry point replaces the Metal dispatch inside one candle
+ * CustomOp (or the candle autograd of the composite the op stands for):
+ *
+ *   mc_lora_fwd      FusedLoRAOp::metal_fwd / metal_fwd_impl
+ *                    (src/backend/custom_ops.rs:247-249, 359-430), extended
+ *                    with the frozen base linear of candle_nn::Linear
+ *                    (src/models/transformer.rs:189-192) and the dropout of
+ *                    LoRALayer::forward (src/training/lora.rs:320-339).
+ *   mc_lora_bwd      no reference kernel: candle autograd of lora.rs:323-339
+ *                    (dX, dA, dB with W frozen). FusedLoRAOp leaves
+ *                    CustomOp1::bwd at candle's default.
+ *   mc_rmsnorm_fwd   FusedRMSNormOp::metal_fwd (custom_ops.rs:534-631), plus
+ *                    the weight multiply of Qwen RMSNorm::forward
+ *                    (src/models/qwen.rs:314-325).
+ *   mc_rmsnorm_bwd   no reference kernel: autograd of tensor.rs:111-117 and
+ *                    qwen.rs:320-321.
+ *   mc_softmax_fwd   FusedSoftmaxOp::metal_fwd (custom_ops.rs:727-823), plus
+ *                    the causal -inf mask that Attention::forward adds before
+ *                    softmax_stable (src/models/transformer.rs:264-275).
+ *   mc_softmax_bwd   no reference kernel: autograd of tensor.rs:91-98.
+ *
+ * Conventions (all entry points):
+ *  - Device buffers are caller-owned, row-major and contiguous; inputs are
+ *    read-only; outputs are fully written. Pointers must be 16-byte aligned.
+ *  - All work is enqueued on `stream` (0 = the null stream); no call
+ *    synchronises the device. Workspace is passed in explicitly and its size
+ *    is given by the matching *_workspace_size() query.
+ *  - Return value 0 (MC_OK) on success, otherwise an mc_status code; the
+ *    message for the calling thread is in mc_last_error(). A caller that gets
+ *    a non-zero status uses its fallback, as LoRALayer::forward does on any
+ *    Err from the fused op (lora.rs:302-310).
+ *  - Argument validation runs on the host before anything is enqueued, so
+ *    every error path is testable without a GPU.
+ */
+#ifndef MC_HIP_H
+#define MC_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum mc_status {
+    MC_OK = 0,
+    MC_ERR_NULL = 1,        /* a required pointer is NULL */
+    MC_ERR_SHAPE = 2,       /* sizes inconsistent, zero where not allowed, or unsupported */
+    MC_ERR_DTYPE = 3,       /* dtype code not supported by this entry point */
+    MC_ERR_LAYOUT = 4,      /* misaligned pointer / row stride */
+    MC_ERR_VALUE = 5,       /* scalar argument out of range (eps, p, scale) */
+    MC_ERR_WORKSPACE = 6,   /* workspace missing or smaller than the query */
+    MC_ERR_HIP = 7,         /* HIP runtime error (launch failure, bad stream) */
+} mc_status;
+
+typedef enum mc_dtype {
+    MC_F32 = 0,
+    MC_BF16 = 1,
+} mc_dtype;
+
+/* LoRA linear, shapes in the reference's conventions:
+ *   x [T, K] (T = product of the leading dims of the input, as
+ *   FusedLoRAOp::extract_dimensions folds batch x seq, custom_ops.rs:254-270),
+ *   W [N, K] (candle Linear), bias [N], A [K, r] (lora.rs:233-239),
+ *   B [r, N] (lora.rs:241-247), y [T, N].
+ * x, W, bias, y, dY, dX use act_dtype; A, B, dA, dB, the saved hidden are fp32.
+ * dropout mask: uint8 [T, r], 1 = keep; required iff dropout_p > 0; kept
+ * values are scaled by 1/(1 - p) (candle_nn::ops::dropout semantics). */
+typedef struct mc_lora_desc {
+    int64_t tokens;        /* T >= 1 */
+    int64_t in_features;   /* K >= 1 */
+    int64_t out_features;  /* N >= 1 */
+    int32_t rank;          /* 1 <= r <= 128 */
+    float scale;           /* alpha / rank (LoRAConfig::scaling, lora.rs:84-87) */
+    float dropout_p;       /* 0 <= p < 1 (LoRAConfig::validate, lora.rs:97-120) */
+    int32_t act_dtype;     /* mc_dtype */
+} mc_lora_desc;
+
+/* Workspace bytes mc_lora_fwd / mc_lora_bwd need for this descriptor. */
+size_t mc_lora_fwd_workspace_size(const mc_lora_desc* d);
+size_t mc_lora_bwd_workspace_size(const mc_lora_desc* d);
+
+/* y = x W^T + bias + scale * ((x A) (.) mask / (1-p)) B.
+ * W == NULL: delta only (exactly what FusedLoRAOp computes); bias may be NULL.
+ * h_save [r, T] fp32 (may be NULL) receives Hd^T = ((x A) (.) mask/(1-p))^T,
+ * the saved activation mc_lora_bwd needs for dB. */
+mc_status mc_lora_fwd(const mc_lora_desc* d, const void* x, const void* W, const void* bias,
+                      const float* A, const float* B, const uint8_t* mask,
+                      void* y, float* h_save, void* workspace, size_t workspace_bytes,
+                      hipStream_t stream);
+
+/* Backward with W frozen:
+ *   G = scale dY B^T, Gd = G (.) mask/(1-p)
+ *   dX = dY W + Gd A^T   (dY W omitted when W == NULL)
+ *   dA = x^T Gd          [K, r]
+ *   dB = scale Hd^T dY   [r, N]  (Hd^T from h_save of mc_lora_fwd)
+ * dX, dA, dB may individually be NULL (not computed); h_save is required iff
+ * dB is requested. Reductions over T are split in a fixed partition and
+ * summed in a fixed order: results are bitwise reproducible run to run. */
+mc_status mc_lora_bwd(const mc_lora_desc* d, const void* x, const void* W, const float* A,
+                      const float* B, const uint8_t* mask, const float* h_save,
+                      const void* dY, void* dX, float* dA, float* dB,
+                      void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* RMSNorm over the last dim of x [rows, dim]:
+ *   y = x / sqrt(mean(x^2) + eps) * w     (w == NULL: no weight, as FusedRMSNormOp)
+ * x, w, y in dtype; rstd [rows] fp32 (may be NULL) receives 1/sqrt(mean + eps). */
+mc_status mc_rmsnorm_fwd(int64_t rows, int64_t dim, float eps, int32_t dtype, const void* x,
+                         const void* w, void* y, float* rstd, hipStream_t stream);
+
+size_t mc_rmsnorm_bwd_workspace_size(int64_t rows, int64_t dim);
+
+/* dx = r g - x r^3 mean(g x), g = dy (.) w ; dw = sum_rows dy x r (fp32 [dim]).
+ * rstd may be NULL (recomputed from x); dw may be NULL (not computed; then no
+ * workspace is needed). dw is reduced in a fixed order (reproducible). */
+mc_status mc_rmsnorm_bwd(int64_t rows, int64_t dim, float eps, int32_t dtype, const void* x,
+                         const void* w, const float* rstd, const void* dy, void* dx, float* dw,
+                         void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* Softmax over the last dim of s [rows, dim]. causal_rows = 0: no mask;
+ * causal_rows = S > 0 (S <= dim): row i is query q = i mod S and column j is
+ * masked (-inf before the softmax, so p = 0 exactly) iff j > q + (dim - S).
+ * Masked positions of s are not read. */
+mc_status mc_softmax_fwd(int64_t rows, int64_t dim, int64_t causal_rows, int32_t dtype,
+                         const void* s, void* p, hipStream_t stream);
+
+/* ds = p (.) (dp - sum_j dp_j p_j), same mask convention (masked ds = 0,
+ * masked p / dp not read). */
+mc_status mc_softmax_bwd(int64_t rows, int64_t dim, int64_t causal_rows, int32_t dtype,
+                         const void* p, const void* dp, void* ds, hipStream_t stream);
+
+/* Host-side dropout keep-mask [rows, rank] from a seed (Philox4x32-10; element
+ * i = t*rank + j uses counter block i/4, word i%4, key = seed; keep iff
+ * (word >> 8) * 2^-24 >= p). Both the GPU path and the CPU reference are fed
+ * the same bytes. Writes host memory; touches no device. */
+mc_status mc_dropout_mask(uint64_t seed, float p, int64_t rows, int32_t rank, uint8_t* mask_host);
+
+/* Kernel timing hook. No counterpart in the reference (its benches time whole
+ * candle calls); it is for callers that need per-kernel times on their own
+ * stream, such as the roofline report of bench.py.
+ * While enabled, every kernel launch of the entry points above is bracketed
+ * by a hipEvent pair recorded on the launch stream and tagged with its class
+ * and its algorithmic work (FLOPs, HBM bytes). mc_profile_collect() waits for
+ * the recorded events and adds them to per-class totals; mc_profile_read()
+ * returns the totals of one class. Classes: 0 = MFMA GEMM (FLOPs count the
+ * base x.W^T / dY.W product only), 1 = rank-r kernels, 2 = RMSNorm,
+ * 3 = softmax. Enabling allocates hipEvents (not for allocation-free use). */
+mc_status mc_profile_enable(int32_t on);
+mc_status mc_profile_collect(void);
+mc_status mc_profile_read(int32_t kind, double* elapsed_ms, int64_t* launches, double* flops, double* bytes);
+mc_status mc_profile_reset(void);
+
+/* Message for the last non-zero status returned on this thread. */
+const char* mc_last_error(void);
+
+/* Library version string. */
+const char* mc_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MC_HIP_H */

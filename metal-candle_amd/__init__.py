@@ -1,0 +1,18 @@
+"""metal-candle's fused LoRA / RMSNorm / softmax custom ops on MI355X (gfx950).
+
+The arithmetic lives in libmc_hip.so (HIP kernels behind the C ABI of
+include/mc_hip.h); this package is the Python host side over that ABI.
+The directory name is not an identifier: load it with
+__graft_entry__.load_package(), which registers it as `metal_candle_amd`.
+"""
+from . import _lib, ops  # noqa: F401
+from ._lib import McError  # noqa: F401
+from .ops import (  # noqa: F401
+    dropout_mask,
+    lora_backward,
+    lora_forward,
+    rms_norm_backward,
+    rms_norm_forward,
+    softmax_backward,
+    softmax_forward,
+)

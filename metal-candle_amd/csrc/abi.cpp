@@ -1,0 +1,284 @@
+// C ABI of libmc_hip.so: argument validation, error reporting, dispatch.
+//
+// Validation mirrors the checks of the reference's fused ops and LoRA config
+// (FusedLoRAOp::new, custom_ops.rs:118-148; compute_output_shape, 153-174;
+// FusedRMSNormOp / FusedSoftmaxOp metal_fwd, 534-560 / 727-752;
+// LoRAConfig::validate, lora.rs:97-120) and returns a status code instead of
+// a candle error, with the message kept per thread in mc_last_error(). It runs
+// on the host before anything is enqueued, so every error path can be
+// exercised without a GPU.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "kernels.hpp"
+#include "mc_hip.h"
+#include "profile.hpp"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+mc_status fail(mc_status code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    std::vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+mc_status ok() {
+    g_last_error.clear();
+    return MC_OK;
+}
+
+mc_status hip_status(hipError_t e, const char* what) {
+    if (e == hipSuccess) return ok();
+    return fail(MC_ERR_HIP, "%s: HIP error %d (%s)", what, (int)e, hipGetErrorString(e));
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+#define MC_CHECK(cond, code, ...)                     \
+    do {                                              \
+        if (!(cond)) return fail(code, __VA_ARGS__);  \
+    } while (0)
+
+mc_status check_dtype(int32_t dtype, const char* op) {
+    MC_CHECK(dtype == MC_F32 || dtype == MC_BF16, MC_ERR_DTYPE,
+             "%s: unsupported dtype code %d (supported: 0 = f32, 1 = bf16)", op, (int)dtype);
+    return MC_OK;
+}
+
+mc_status check_lora_desc(const mc_lora_desc* d) {
+    MC_CHECK(d != nullptr, MC_ERR_NULL, "LoRA: descriptor is NULL");
+    MC_CHECK(d->act_dtype == MC_F32 || d->act_dtype == MC_BF16, MC_ERR_DTYPE,
+             "LoRA: unsupported act_dtype code %d (supported: 0 = f32, 1 = bf16)", (int)d->act_dtype);
+    MC_CHECK(d->tokens >= 1 && d->in_features >= 1 && d->out_features >= 1, MC_ERR_SHAPE,
+             "LoRA: tokens, in_features and out_features must be >= 1, got %lld, %lld, %lld",
+             (long long)d->tokens, (long long)d->in_features, (long long)d->out_features);
+    // LoRAConfig::validate: "LoRA rank must be greater than 0" (lora.rs:99-104)
+    MC_CHECK(d->rank >= 1, MC_ERR_SHAPE, "LoRA rank must be greater than 0");
+    MC_CHECK(d->rank <= 128, MC_ERR_SHAPE, "LoRA: rank %d exceeds the supported maximum 128", (int)d->rank);
+    MC_CHECK(std::isfinite(d->scale), MC_ERR_VALUE, "LoRA: scale must be finite");
+    // LoRAConfig::validate: "LoRA dropout must be in [0, 1)" (lora.rs:113-118)
+    MC_CHECK(d->dropout_p >= 0.0f && d->dropout_p < 1.0f, MC_ERR_VALUE, "LoRA dropout must be in [0, 1)");
+    if (d->act_dtype == MC_BF16) {
+        MC_CHECK(d->in_features % 8 == 0 && d->out_features % 8 == 0, MC_ERR_SHAPE,
+                 "LoRA bf16: in_features (%lld) and out_features (%lld) must be multiples of 8",
+                 (long long)d->in_features, (long long)d->out_features);
+    }
+    return MC_OK;
+}
+
+mc_status check_rows(int64_t rows, int64_t dim, const char* op) {
+    MC_CHECK(rows >= 1 && dim >= 1, MC_ERR_SHAPE, "%s: rows and dim must be >= 1, got %lld x %lld", op,
+             (long long)rows, (long long)dim);
+    return MC_OK;
+}
+
+// Elements a causal softmax reads: row i (query q = i mod S) reads columns
+// 0 .. q + dim - S; summed over whole S-row blocks plus the partial block.
+double unmasked(int64_t rows, int64_t dim, int64_t S) {
+    if (S <= 0) return (double)rows * dim;
+    auto block = [&](int64_t n) {  // first n queries of a block
+        return (double)n * (dim - S) + (double)n * (n + 1) / 2.0;
+    };
+    return (double)(rows / S) * block(S) + block(rows % S);
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* mc_version(void) { return "mc_hip 0.1.0 (gfx950)"; }
+
+mc_status mc_profile_enable(int32_t on) {
+    mc::prof::set_enabled(on != 0);
+    return ok();
+}
+
+mc_status mc_profile_collect(void) { return hip_status(mc::prof::collect(), "profile collect"); }
+
+mc_status mc_profile_read(int32_t kind, double* elapsed_ms, int64_t* launches, double* flops, double* bytes) {
+    MC_CHECK(kind >= 0 && kind < mc::prof::kNumKinds, MC_ERR_VALUE, "profile: unknown kernel class %d", (int)kind);
+    long long n = 0;
+    mc::prof::read(kind, elapsed_ms, &n, flops, bytes);
+    if (launches) *launches = n;
+    return ok();
+}
+
+mc_status mc_profile_reset(void) {
+    mc::prof::reset();
+    return ok();
+}
+
+const char* mc_last_error(void) { return g_last_error.c_str(); }
+
+size_t mc_lora_fwd_workspace_size(const mc_lora_desc* d) {
+    if (check_lora_desc(d) != MC_OK) return 0;
+    return mc::lora_fwd_ws(*d).total;
+}
+
+size_t mc_lora_bwd_workspace_size(const mc_lora_desc* d) {
+    if (check_lora_desc(d) != MC_OK) return 0;
+    return mc::lora_bwd_ws(*d).total;
+}
+
+mc_status mc_lora_fwd(const mc_lora_desc* d, const void* x, const void* W, const void* bias,
+                      const float* A, const float* B, const uint8_t* mask, void* y, float* h_save,
+                      void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    mc_status s = check_lora_desc(d);
+    if (s != MC_OK) return s;
+    MC_CHECK(x && A && B && y, MC_ERR_NULL, "LoRA forward: x, A, B and y must not be NULL");
+    MC_CHECK(!bias || W, MC_ERR_NULL, "LoRA forward: bias given without W");
+    MC_CHECK(d->dropout_p == 0.0f || mask, MC_ERR_NULL, "LoRA forward: dropout_p > 0 requires a mask");
+    MC_CHECK(aligned16(x) && aligned16(y) && (!W || aligned16(W)) && (!h_save || aligned16(h_save)),
+             MC_ERR_LAYOUT, "LoRA forward: x, W, y and h_save must be 16-byte aligned");
+    const size_t need = mc::lora_fwd_ws(*d).total;
+    MC_CHECK(workspace_bytes >= need && (need == 0 || workspace), MC_ERR_WORKSPACE,
+             "LoRA forward: workspace of %zu bytes required, %zu given", need, workspace_bytes);
+    MC_CHECK(aligned16(workspace), MC_ERR_LAYOUT, "LoRA forward: workspace must be 16-byte aligned");
+    return hip_status(mc::launch_lora_fwd(*d, x, W, bias, A, B, mask, y, h_save, workspace, stream),
+                      "LoRA forward");
+}
+
+mc_status mc_lora_bwd(const mc_lora_desc* d, const void* x, const void* W, const float* A, const float* B,
+                      const uint8_t* mask, const float* h_save, const void* dY, void* dX, float* dA,
+                      float* dB, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    mc_status s = check_lora_desc(d);
+    if (s != MC_OK) return s;
+    MC_CHECK(dY && A && B, MC_ERR_NULL, "LoRA backward: dY, A and B must not be NULL");
+    MC_CHECK(!dA || x, MC_ERR_NULL, "LoRA backward: dA requires x");
+    MC_CHECK(!dB || h_save, MC_ERR_NULL, "LoRA backward: dB requires h_save from the forward");
+    MC_CHECK(d->dropout_p == 0.0f || mask, MC_ERR_NULL, "LoRA backward: dropout_p > 0 requires a mask");
+    MC_CHECK(aligned16(dY) && (!x || aligned16(x)) && (!W || aligned16(W)) && (!dX || aligned16(dX)) &&
+                 (!h_save || aligned16(h_save)),
+             MC_ERR_LAYOUT, "LoRA backward: x, W, dY, dX and h_save must be 16-byte aligned");
+    const size_t need = mc::lora_bwd_ws(*d).total;
+    MC_CHECK(workspace_bytes >= need && (need == 0 || workspace), MC_ERR_WORKSPACE,
+             "LoRA backward: workspace of %zu bytes required, %zu given", need, workspace_bytes);
+    MC_CHECK(aligned16(workspace), MC_ERR_LAYOUT, "LoRA backward: workspace must be 16-byte aligned");
+    if (!dX && !dA && !dB) return ok();
+    return hip_status(mc::launch_lora_bwd(*d, x, W, A, B, mask, h_save, dY, dX, dA, dB, workspace, stream),
+                      "LoRA backward");
+}
+
+mc_status mc_rmsnorm_fwd(int64_t rows, int64_t dim, float eps, int32_t dtype, const void* x, const void* w,
+                         void* y, float* rstd, hipStream_t stream) {
+    mc_status s = check_rows(rows, dim, "RMSNorm");
+    if (s != MC_OK) return s;
+    if ((s = check_dtype(dtype, "RMSNorm")) != MC_OK) return s;
+    MC_CHECK(eps >= 0.0f && std::isfinite(eps), MC_ERR_VALUE, "RMSNorm: eps must be finite and >= 0");
+    MC_CHECK(x && y, MC_ERR_NULL, "RMSNorm: x and y must not be NULL");
+    MC_CHECK(aligned16(x) && aligned16(y) && (!w || aligned16(w)), MC_ERR_LAYOUT,
+             "RMSNorm: x, w and y must be 16-byte aligned");
+    const double es = dtype == MC_F32 ? 4.0 : 2.0;
+    mc::prof::Scope sc(mc::prof::kRmsNorm, stream, 0.0,
+                       es * (2.0 * rows * dim + (w ? dim : 0)) + (rstd ? 4.0 * rows : 0.0));
+    return hip_status(mc::launch_rmsnorm_fwd(rows, dim, eps, dtype, x, w, y, rstd, stream), "RMSNorm forward");
+}
+
+size_t mc_rmsnorm_bwd_workspace_size(int64_t rows, int64_t dim) {
+    if (rows < 1 || dim < 1) return 0;
+    return (size_t)mc::rmsnorm_bwd_blocks(rows, dim) * (size_t)dim * sizeof(float);
+}
+
+mc_status mc_rmsnorm_bwd(int64_t rows, int64_t dim, float eps, int32_t dtype, const void* x, const void* w,
+                         const float* rstd, const void* dy, void* dx, float* dw, void* workspace,
+                         size_t workspace_bytes, hipStream_t stream) {
+    mc_status s = check_rows(rows, dim, "RMSNorm backward");
+    if (s != MC_OK) return s;
+    if ((s = check_dtype(dtype, "RMSNorm backward")) != MC_OK) return s;
+    MC_CHECK(eps >= 0.0f && std::isfinite(eps), MC_ERR_VALUE, "RMSNorm: eps must be finite and >= 0");
+    MC_CHECK(x && dy && dx, MC_ERR_NULL, "RMSNorm backward: x, dy and dx must not be NULL");
+    MC_CHECK(aligned16(x) && aligned16(dy) && aligned16(dx) && (!w || aligned16(w)), MC_ERR_LAYOUT,
+             "RMSNorm backward: x, w, dy and dx must be 16-byte aligned");
+    if (dw) {
+        const size_t need = mc_rmsnorm_bwd_workspace_size(rows, dim);
+        MC_CHECK(workspace && workspace_bytes >= need, MC_ERR_WORKSPACE,
+                 "RMSNorm backward: workspace of %zu bytes required for dw, %zu given", need, workspace_bytes);
+    }
+    const double es = dtype == MC_F32 ? 4.0 : 2.0;
+    mc::prof::Scope sc(mc::prof::kRmsNorm, stream, 0.0,
+                       es * (3.0 * rows * dim + (w ? dim : 0)) + (rstd ? 4.0 * rows : 0.0) + (dw ? 4.0 * dim : 0.0));
+    return hip_status(mc::launch_rmsnorm_bwd(rows, dim, eps, dtype, x, w, rstd, dy, dx, dw,
+                                             static_cast<float*>(workspace), stream),
+                      "RMSNorm backward");
+}
+
+mc_status mc_softmax_fwd(int64_t rows, int64_t dim, int64_t causal_rows, int32_t dtype, const void* sc,
+                         void* p, hipStream_t stream) {
+    mc_status s = check_rows(rows, dim, "Softmax");
+    if (s != MC_OK) return s;
+    if ((s = check_dtype(dtype, "Softmax")) != MC_OK) return s;
+    MC_CHECK(causal_rows >= 0 && causal_rows <= dim, MC_ERR_SHAPE,
+             "Softmax: causal_rows must be in [0, dim], got %lld for dim %lld", (long long)causal_rows,
+             (long long)dim);
+    MC_CHECK(sc && p, MC_ERR_NULL, "Softmax: input and output must not be NULL");
+    MC_CHECK(aligned16(sc) && aligned16(p), MC_ERR_LAYOUT, "Softmax: input and output must be 16-byte aligned");
+    const double es = dtype == MC_F32 ? 4.0 : 2.0;
+    mc::prof::Scope scope(mc::prof::kSoftmax, stream, 0.0, es * (unmasked(rows, dim, causal_rows) + (double)rows * dim));
+    return hip_status(mc::launch_softmax_fwd(rows, dim, causal_rows, dtype, sc, p, stream), "Softmax forward");
+}
+
+mc_status mc_softmax_bwd(int64_t rows, int64_t dim, int64_t causal_rows, int32_t dtype, const void* p,
+                         const void* dp, void* ds, hipStream_t stream) {
+    mc_status s = check_rows(rows, dim, "Softmax backward");
+    if (s != MC_OK) return s;
+    if ((s = check_dtype(dtype, "Softmax backward")) != MC_OK) return s;
+    MC_CHECK(causal_rows >= 0 && causal_rows <= dim, MC_ERR_SHAPE,
+             "Softmax: causal_rows must be in [0, dim], got %lld for dim %lld", (long long)causal_rows,
+             (long long)dim);
+    MC_CHECK(p && dp && ds, MC_ERR_NULL, "Softmax backward: p, dp and ds must not be NULL");
+    MC_CHECK(aligned16(p) && aligned16(dp) && aligned16(ds), MC_ERR_LAYOUT,
+             "Softmax backward: p, dp and ds must be 16-byte aligned");
+    const double es = dtype == MC_F32 ? 4.0 : 2.0;
+    mc::prof::Scope scope(mc::prof::kSoftmax, stream, 0.0,
+                          es * (2.0 * unmasked(rows, dim, causal_rows) + (double)rows * dim));
+    return hip_status(mc::launch_softmax_bwd(rows, dim, causal_rows, dtype, p, dp, ds, stream),
+                      "Softmax backward");
+}
+
+// Philox4x32-10 (Salmon et al., SC'11), 10 rounds of the two 32x32->64
+// multiplies 0xD2511F53 / 0xCD9E8D57 with Weyl key steps 0x9E3779B9 /
+// 0xBB67AE85.
+static void philox_block(uint64_t blk, uint64_t seed, uint32_t out[4]) {
+    uint32_t c0 = (uint32_t)blk, c1 = (uint32_t)(blk >> 32), c2 = 0, c3 = 0;
+    uint32_t k0 = (uint32_t)seed, k1 = (uint32_t)(seed >> 32);
+    for (int i = 0; i < 10; ++i) {
+        const uint64_t a = (uint64_t)0xD2511F53u * c0;
+        const uint64_t b = (uint64_t)0xCD9E8D57u * c2;
+        const uint32_t n0 = (uint32_t)(b >> 32) ^ c1 ^ k0;
+        const uint32_t n2 = (uint32_t)(a >> 32) ^ c3 ^ k1;
+        c1 = (uint32_t)b;
+        c3 = (uint32_t)a;
+        c0 = n0;
+        c2 = n2;
+        k0 += 0x9E3779B9u;
+        k1 += 0xBB67AE85u;
+    }
+    out[0] = c0; out[1] = c1; out[2] = c2; out[3] = c3;
+}
+
+mc_status mc_dropout_mask(uint64_t seed, float p, int64_t rows, int32_t rank, uint8_t* mask_host) {
+    MC_CHECK(rows >= 1 && rank >= 1, MC_ERR_SHAPE, "dropout mask: rows and rank must be >= 1");
+    MC_CHECK(p >= 0.0f && p < 1.0f, MC_ERR_VALUE, "LoRA dropout must be in [0, 1)");
+    MC_CHECK(mask_host != nullptr, MC_ERR_NULL, "dropout mask: output must not be NULL");
+    const int64_t n = rows * (int64_t)rank;
+    uint32_t w[4];
+    for (int64_t i = 0; i < n; ++i) {
+        if ((i & 3) == 0) philox_block((uint64_t)(i >> 2), seed, w);
+        const float u = (float)(w[i & 3] >> 8) * (1.0f / 16777216.0f);
+        mask_host[i] = (uint8_t)(u >= p);
+    }
+    return ok();
+}
+
+}  // extern "C"

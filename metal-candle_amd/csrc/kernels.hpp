@@ -1,0 +1,58 @@
+// Host-side launchers of the gfx950 kernels. Arguments are validated by the
+// C ABI layer (abi.cpp) before any of these is called; the launchers assume
+// consistent shapes, 16-byte aligned pointers and non-null required buffers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "mc_hip.h"
+
+namespace mc {
+
+// ------------------------------------------------------------- RMSNorm
+hipError_t launch_rmsnorm_fwd(int64_t rows, int64_t dim, float eps, int dtype, const void* x,
+                              const void* w, void* y, float* rstd, hipStream_t stream);
+// Number of row blocks the dw reduction is split into (fixed for a shape).
+int rmsnorm_bwd_blocks(int64_t rows, int64_t dim);
+hipError_t launch_rmsnorm_bwd(int64_t rows, int64_t dim, float eps, int dtype, const void* x,
+                              const void* w, const float* rstd, const void* dy, void* dx, float* dw,
+                              float* partial, hipStream_t stream);
+
+// ------------------------------------------------------------- softmax
+hipError_t launch_softmax_fwd(int64_t rows, int64_t dim, int64_t causal_rows, int dtype,
+                              const void* s, void* p, hipStream_t stream);
+hipError_t launch_softmax_bwd(int64_t rows, int64_t dim, int64_t causal_rows, int dtype,
+                              const void* p, const void* dp, void* ds, hipStream_t stream);
+
+// ---------------------------------------------------------------- LoRA
+// Workspace layout of the LoRA entry points (byte offsets into workspace).
+struct LoraFwdWs {
+    size_t at_hilo;   // bf16 [2][r16][K]  A^T split into hi/lo (bf16 path)
+    size_t bt_ext;    // bf16 [N][rext]    B^T, zero padded (GEMM extension operand)
+    size_t hs_ext;    // bf16 [T][rext]    s*Hd, zero padded (GEMM extension operand)
+    size_t hd_t;      // f32  [r][T]       Hd^T when the caller passes no h_save
+    size_t total;
+};
+struct LoraBwdWs {
+    size_t b_hilo;    // bf16 [2][r16][N]  B split into hi/lo
+    size_t at_ext;    // bf16 [rext][K]    A^T, zero padded rows (dX extension operand)
+    size_t gd_ext;    // bf16 [T][rext]    Gd, zero padded (dX extension operand)
+    size_t gd_t;      // f32  [r][T]       Gd^T
+    size_t part_a;    // f32  [S_a][r16][K] split-T partials of dA
+    size_t part_b;    // f32  [S_b][r16][N] split-T partials of dB
+    size_t total;
+};
+LoraFwdWs lora_fwd_ws(const mc_lora_desc& d);
+LoraBwdWs lora_bwd_ws(const mc_lora_desc& d);
+
+hipError_t launch_lora_fwd(const mc_lora_desc& d, const void* x, const void* W, const void* bias,
+                           const float* A, const float* B, const uint8_t* mask, void* y,
+                           float* h_save, void* ws, hipStream_t stream);
+hipError_t launch_lora_bwd(const mc_lora_desc& d, const void* x, const void* W, const float* A,
+                           const float* B, const uint8_t* mask, const float* h_save,
+                           const void* dY, void* dX, float* dA, float* dB, void* ws,
+                           hipStream_t stream);
+
+}  // namespace mc

@@ -1,0 +1,80 @@
+// Internal launch wrappers of the LoRA kernels (lora_lowrank.hip,
+// lora_gemm.hip), orchestrated by lora.hip. Shapes are validated by abi.cpp.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mc {
+
+inline int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
+
+// ------------------------------------------------------ operand preparation
+// out[i][j] (bf16, rows_out x cols_out, ld = cols_out) = src element
+// (transpose ? src[j*ld_src + i] : src[i*ld_src + j]) for i < valid_rows,
+// j < valid_cols, else 0. With lo != nullptr the fp32 value v is split as
+// hi = bf16(v), lo = bf16(v - hi).
+hipError_t launch_prep_bf16(const float* src, int64_t ld_src, int64_t valid_rows, int64_t valid_cols,
+                            bool transpose, uint16_t* hi, uint16_t* lo, int64_t rows_out,
+                            int64_t cols_out, hipStream_t stream);
+
+// ------------------------------------------------------- row projection
+// For t < T, j < r:  v = scale * sum_c X[t][c] * P[j][c]   (P = P_hi + P_lo)
+//                    v = mask ? (mask[t*r+j] ? v*keep : 0) : v
+//   out_t[j*T + t] = v                       (fp32, may be null)
+//   out_ext[t*rext + j] = bf16(ext_scale*v)  (j < r; zero for r <= j < rext; may be null)
+// X bf16 [T][C] (C % 8 == 0), P_hi / P_lo bf16 [r16][C] with r16 = 16, 32,
+// 64 or 128 (the smallest >= r), rows past r zero.
+hipError_t launch_rowproj_bf16(const uint16_t* X, int64_t T, int64_t C, const uint16_t* P_hi,
+                               const uint16_t* P_lo, int r, float scale, const uint8_t* mask,
+                               float keep, float* out_t, uint16_t* out_ext, int rext, float ext_scale,
+                               hipStream_t stream);
+
+// ------------------------------------------------- column reduction (split T)
+// partial[s][j][c] = sum_{t in split s} Pt[j*T + t] * X[t][c] for j < r16, c < C
+// (j >= r contributes 0; r16 as for rowproj). X bf16 [T][C] (C % 8 == 0),
+// Pt fp32 [r][T].
+int colreduce_splits(int64_t T, int64_t C);
+hipError_t launch_colreduce_bf16(const uint16_t* X, int64_t T, int64_t C, const float* Pt, int r,
+                                 int splits, float* partial, hipStream_t stream);
+// out = scale * sum_s partial[s][j][c] (s ascending) for j < r, c < C, written
+// to out[c*r + j] when transpose_out (dA [K][r]) else out[j*C + c] (dB [r][N]).
+hipError_t launch_split_sum(const float* partial, int splits, int r16, int r, int64_t C, float scale,
+                            bool transpose_out, float* out, hipStream_t stream);
+
+// -------------------------------------------------------------- GEMM bf16
+// C[M][N] = sum over two reduction segments of A_s . B_s (+ bias[n]), bf16 out.
+// A_s bf16 [M][k_s] (row stride lda_s). B_s: NT mode [N][k_s] (stride ldb_s);
+// NN mode [k_s][N] (stride ldb_s). k_s % 8 == 0; k_s may be 0.
+struct GemmSeg {
+    const uint16_t* a;
+    int64_t lda;
+    const uint16_t* b;
+    int64_t ldb;
+    int64_t k;
+};
+hipError_t launch_gemm_bf16(bool nn, int64_t M, int64_t N, GemmSeg s0, GemmSeg s1,
+                            const uint16_t* bias, uint16_t* c, int64_t ldc, hipStream_t stream);
+
+// ------------------------------------------------------------- fp32 path
+// Same contracts as above with fp32 storage and plain FMA arithmetic; used
+// for act_dtype == MC_F32 (the fp32 parity configuration).
+struct GemmSegF32 {
+    const float* a;
+    int64_t lda;
+    const float* b;
+    int64_t ldb;
+    int64_t k;
+};
+hipError_t launch_gemm_f32(bool nn, int64_t M, int64_t N, GemmSegF32 s0, GemmSegF32 s1,
+                           const float* bias, float* c, int64_t ldc, hipStream_t stream);
+// v[t][j] = scale * sum_c X[t][c] * (transpose_p ? P[c*r + j] : P[j*C + c]),
+// masked as in launch_rowproj_bf16; out_t [r][T]; out_ext [T][r] = ext_scale*v.
+hipError_t launch_rowproj_f32(const float* X, int64_t T, int64_t C, const float* P, bool transpose_p,
+                              int r, float scale, const uint8_t* mask, float keep, float* out_t,
+                              float* out_ext, float ext_scale, hipStream_t stream);
+// out = scale * sum_t Pt[j*T + t] * X[t][c]; layout as launch_split_sum.
+hipError_t launch_colreduce_f32(const float* X, int64_t T, int64_t C, const float* Pt, int r,
+                                float scale, bool transpose_out, float* out, hipStream_t stream);
+
+}  // namespace mc

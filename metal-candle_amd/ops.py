@@ -1,0 +1,129 @@
+"""torch-tensor front end of the C ABI (device memory and streams come from
+torch; all arithmetic runs in libmc_hip.so's HIP kernels).
+
+Shapes follow the reference: x [..., K], W [N, K], A [K, r], B [r, N]; the
+leading dims of x are folded into T tokens as FusedLoRAOp::extract_dimensions
+does (src/backend/custom_ops.rs:254-270). Activations are float32 or bfloat16;
+A, B and their gradients are float32. Every call enqueues on torch's current
+stream of the tensors' device and does not synchronise.
+"""
+import ctypes
+
+import torch
+
+from . import _lib
+from ._lib import LoraDesc, McError, check, lib
+
+_DTYPES = {torch.float32: _lib.MC_F32, torch.bfloat16: _lib.MC_BF16}
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(t):
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _dtype_code(t):
+    try:
+        return _DTYPES[t.dtype]
+    except KeyError:
+        raise McError(_lib.MC_ERR_DTYPE, f"unsupported dtype {t.dtype} (float32 or bfloat16)")
+
+
+def _contig(t, name):
+    if t is None:
+        return None
+    if not t.is_contiguous():
+        raise McError(_lib.MC_ERR_LAYOUT, f"{name} must be contiguous")
+    return t
+
+
+def _workspace(nbytes, device):
+    if nbytes == 0:
+        return None
+    return torch.empty(nbytes, dtype=torch.uint8, device=device)
+
+
+def lora_desc(tokens, in_features, out_features, rank, scale, dropout_p=0.0, dtype=torch.bfloat16):
+    return LoraDesc(tokens, in_features, out_features, rank, scale, dropout_p, _DTYPES[dtype])
+
+
+def lora_forward(x, A, B, scale, W=None, bias=None, mask=None, dropout_p=0.0, save_hidden=True):
+    """y = x.W^T + bias + scale*((x.A) (.) mask/(1-p)).B ; returns (y, h_save)."""
+    _contig(x, "x"), _contig(W, "W"), _contig(A, "A"), _contig(B, "B")
+    K = x.shape[-1]
+    T = x.numel() // K
+    r, N = B.shape
+    d = LoraDesc(T, K, N, r, float(scale), float(dropout_p), _dtype_code(x))
+    y = torch.empty(*x.shape[:-1], N, dtype=x.dtype, device=x.device)
+    h = torch.empty(r, T, dtype=torch.float32, device=x.device) if save_hidden else None
+    ws_n = lib().mc_lora_fwd_workspace_size(ctypes.byref(d))  # 0 for an invalid descriptor
+    ws = _workspace(ws_n, x.device)
+    check(lib().mc_lora_fwd(ctypes.byref(d), _ptr(x), _ptr(W), _ptr(bias), _ptr(A), _ptr(B), _ptr(mask),
+                            _ptr(y), _ptr(h), _ptr(ws), ws_n, _stream(x)))
+    return y, h
+
+
+def lora_backward(x, A, B, dY, scale, W=None, mask=None, dropout_p=0.0, h_save=None,
+                  need_dx=True, need_dA=True, need_dB=True):
+    """(dX, dA, dB) with W frozen; entries not requested are None."""
+    K = A.shape[0]
+    r, N = B.shape
+    T = dY.numel() // N
+    d = LoraDesc(T, K, N, r, float(scale), float(dropout_p), _dtype_code(dY))
+    dX = torch.empty(*dY.shape[:-1], K, dtype=dY.dtype, device=dY.device) if need_dx else None
+    dA = torch.empty(K, r, dtype=torch.float32, device=dY.device) if need_dA else None
+    dB = torch.empty(r, N, dtype=torch.float32, device=dY.device) if need_dB else None
+    ws_n = lib().mc_lora_bwd_workspace_size(ctypes.byref(d))  # 0 for an invalid descriptor
+    ws = _workspace(ws_n, dY.device)
+    check(lib().mc_lora_bwd(ctypes.byref(d), _ptr(x), _ptr(W), _ptr(A), _ptr(B), _ptr(mask), _ptr(h_save),
+                            _ptr(dY), _ptr(dX), _ptr(dA), _ptr(dB), _ptr(ws), ws_n, _stream(dY)))
+    return dX, dA, dB
+
+
+def rms_norm_forward(x, eps, w=None, save_rstd=True):
+    D = x.shape[-1]
+    rows = x.numel() // D if D else 0
+    y = torch.empty_like(x)
+    rstd = torch.empty(rows, dtype=torch.float32, device=x.device) if save_rstd else None
+    check(lib().mc_rmsnorm_fwd(rows, D, float(eps), _dtype_code(x), _ptr(x), _ptr(w), _ptr(y), _ptr(rstd),
+                               _stream(x)))
+    return y, rstd
+
+
+def rms_norm_backward(x, dy, eps, w=None, rstd=None, need_dw=True):
+    D = x.shape[-1]
+    rows = x.numel() // D if D else 0
+    dx = torch.empty_like(x)
+    dw = torch.empty(D, dtype=torch.float32, device=x.device) if need_dw else None
+    ws_n = lib().mc_rmsnorm_bwd_workspace_size(rows, D) if need_dw else 0
+    ws = _workspace(ws_n, x.device)
+    check(lib().mc_rmsnorm_bwd(rows, D, float(eps), _dtype_code(x), _ptr(x), _ptr(w), _ptr(rstd), _ptr(dy),
+                               _ptr(dx), _ptr(dw), _ptr(ws), ws_n, _stream(x)))
+    return dx, dw
+
+
+def softmax_forward(s, causal_rows=0):
+    D = s.shape[-1]
+    rows = s.numel() // D if D else 0
+    p = torch.empty_like(s)
+    check(lib().mc_softmax_fwd(rows, D, int(causal_rows), _dtype_code(s), _ptr(s), _ptr(p), _stream(s)))
+    return p
+
+
+def softmax_backward(p, dp, causal_rows=0):
+    D = p.shape[-1]
+    rows = p.numel() // D if D else 0
+    ds = torch.empty_like(p)
+    check(lib().mc_softmax_bwd(rows, D, int(causal_rows), _dtype_code(p), _ptr(p), _ptr(dp), _ptr(ds),
+                               _stream(p)))
+    return ds
+
+
+def dropout_mask(seed, p, rows, rank):
+    """Host-generated keep-mask (uint8 [rows, rank]) as a CPU torch tensor."""
+    m = torch.empty(rows, rank, dtype=torch.uint8)
+    check(lib().mc_dropout_mask(int(seed), float(p), int(rows), int(rank), ctypes.c_void_p(m.data_ptr())))
+    return m

@@ -1,0 +1,319 @@
+/*
+ * CPU oracle (test infrastructure only; never linked into the product).
+ * Every function restates a reference composite; see oracle.h for the
+ * reference file:line each one follows and the checks that pin it.
+ *
+ * Accumulation is fp64 in the order of the composite's ops; results are
+ * stored as fp32. OpenMP parallelises over independent rows/columns only,
+ * so results do not depend on the thread count.
+ */
+#include "oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+static int nthreads(int threads) {
+#ifdef _OPENMP
+    return threads > 0 ? threads : omp_get_max_threads();
+#else
+    (void)threads;
+    return 1;
+#endif
+}
+
+/* ---------------------------------------------------------------- Philox */
+/* Philox4x32-10, Salmon, Moraes, Dror, Shaw, "Parallel random numbers: as
+ * easy as 1, 2, 3", SC'11: round multipliers 0xD2511F53 / 0xCD9E8D57, Weyl
+ * key increments 0x9E3779B9 / 0xBB67AE85. */
+void oracle_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]) {
+    uint32_t c0 = ctr[0], c1 = ctr[1], c2 = ctr[2], c3 = ctr[3];
+    uint32_t k0 = key[0], k1 = key[1];
+    for (int round = 0; round < 10; ++round) {
+        uint64_t p0 = (uint64_t)0xD2511F53u * c0;
+        uint64_t p1 = (uint64_t)0xCD9E8D57u * c2;
+        uint32_t hi0 = (uint32_t)(p0 >> 32), lo0 = (uint32_t)p0;
+        uint32_t hi1 = (uint32_t)(p1 >> 32), lo1 = (uint32_t)p1;
+        uint32_t n0 = hi1 ^ c1 ^ k0;
+        uint32_t n2 = hi0 ^ c3 ^ k1;
+        c0 = n0; c1 = lo1; c2 = n2; c3 = lo0;
+        k0 += 0x9E3779B9u;
+        k1 += 0xBB67AE85u;
+    }
+    out[0] = c0; out[1] = c1; out[2] = c2; out[3] = c3;
+}
+
+void oracle_dropout_mask(uint64_t seed, float p, int64_t rows, int32_t rank, uint8_t* mask) {
+    const int64_t n = rows * (int64_t)rank;
+    const uint32_t key[2] = {(uint32_t)seed, (uint32_t)(seed >> 32)};
+    for (int64_t blk = 0; blk * 4 < n; ++blk) {
+        uint32_t ctr[4] = {(uint32_t)blk, (uint32_t)((uint64_t)blk >> 32), 0u, 0u};
+        uint32_t w[4];
+        oracle_philox4x32_10(ctr, key, w);
+        for (int q = 0; q < 4 && blk * 4 + q < n; ++q) {
+            float u = (float)(w[q] >> 8) * (1.0f / 16777216.0f);
+            mask[blk * 4 + q] = (uint8_t)(u >= p);
+        }
+    }
+}
+
+/* ------------------------------------------------------------------ LoRA */
+/* Dropout scale as candle-nn computes it: kept values times 1/(1-p) in fp32. */
+static float keep_scale(float p) { return 1.0f / (1.0f - p); }
+
+void oracle_lora_fwd(int64_t T, int64_t K, int64_t N, int32_t r, float scale, float p,
+                     const float* x, const float* W, const float* bias,
+                     const float* A, const float* B, const uint8_t* mask,
+                     float* y, float* hd_out, int threads) {
+    const float ks = mask ? keep_scale(p) : 1.0f;
+#pragma omp parallel for schedule(static) num_threads(nthreads(threads))
+    for (int64_t t = 0; t < T; ++t) {
+        const float* xr = x + t * K;
+        double hd[512];
+        double* h = hd;
+        double* hbuf = NULL;
+        if (r > 512) { hbuf = (double*)malloc(sizeof(double) * (size_t)r); h = hbuf; }
+        /* lora.rs:323  hidden = input.broadcast_matmul(A) */
+        for (int32_t j = 0; j < r; ++j) {
+            double acc = 0.0;
+            for (int64_t k = 0; k < K; ++k) acc += (double)xr[k] * (double)A[k * r + j];
+            /* fp32 storage of the matmul result, as candle keeps it */
+            float hf = (float)acc;
+            /* lora.rs:326-330  dropout on the rank-r hidden */
+            if (mask) hf = mask[t * r + j] ? hf * ks : 0.0f;
+            h[j] = hf;
+            if (hd_out) hd_out[t * r + j] = hf;
+        }
+        for (int64_t n = 0; n < N; ++n) {
+            /* lora.rs:336-339  (hidden . B) then affine(scale) */
+            double d = 0.0;
+            for (int32_t j = 0; j < r; ++j) d += h[j] * (double)B[(int64_t)j * N + n];
+            double acc = (double)scale * d;
+            if (W) {
+                /* candle_nn::Linear: x . W^T (+ b) */
+                const float* wr = W + n * K;
+                double base = 0.0;
+                for (int64_t k = 0; k < K; ++k) base += (double)xr[k] * (double)wr[k];
+                acc += base;
+                if (bias) acc += (double)bias[n];
+            }
+            y[t * N + n] = (float)acc;
+        }
+        free(hbuf);
+    }
+}
+
+void oracle_lora_bwd(int64_t T, int64_t K, int64_t N, int32_t r, float scale, float p,
+                     const float* x, const float* W, const float* A, const float* B,
+                     const uint8_t* mask, const float* dy,
+                     float* dx, float* dA, float* dB, int threads) {
+    const float ks = mask ? keep_scale(p) : 1.0f;
+    const int nt = nthreads(threads);
+    /* Hd (forward hidden after dropout) and Gd (gradient of the hidden). */
+    double* hd = (double*)malloc(sizeof(double) * (size_t)(T * r));
+    double* gd = (double*)malloc(sizeof(double) * (size_t)(T * r));
+#pragma omp parallel for schedule(static) num_threads(nt)
+    for (int64_t t = 0; t < T; ++t) {
+        const float* xr = x + t * K;
+        const float* dyr = dy + t * N;
+        for (int32_t j = 0; j < r; ++j) {
+            double h = 0.0;
+            for (int64_t k = 0; k < K; ++k) h += (double)xr[k] * (double)A[k * r + j];
+            double g = 0.0;
+            for (int64_t n = 0; n < N; ++n) g += (double)dyr[n] * (double)B[(int64_t)j * N + n];
+            g *= (double)scale;
+            float hf = (float)h;
+            if (mask) {
+                int keep = mask[t * r + j];
+                hf = keep ? hf * ks : 0.0f;
+                g = keep ? g * (double)ks : 0.0;
+            }
+            hd[t * r + j] = (double)hf;
+            gd[t * r + j] = g;
+        }
+    }
+    if (dx) {
+#pragma omp parallel for schedule(static) num_threads(nt)
+        for (int64_t t = 0; t < T; ++t) {
+            const float* dyr = dy + t * N;
+            for (int64_t k = 0; k < K; ++k) {
+                double acc = 0.0;
+                if (W)
+                    for (int64_t n = 0; n < N; ++n) acc += (double)dyr[n] * (double)W[n * K + k];
+                for (int32_t j = 0; j < r; ++j) acc += gd[t * r + j] * (double)A[k * r + j];
+                dx[t * K + k] = (float)acc;
+            }
+        }
+    }
+    /* dA[k][j] = sum_t x[t][k] gd[t][j] and dB[j][n] = s sum_t hd[t][j] dy[t][n]:
+     * columns are processed in blocks of 64 so x / dy rows are read
+     * contiguously; each sum still runs over t in ascending order. */
+    if (dA) {
+#pragma omp parallel for schedule(dynamic) num_threads(nt)
+        for (int64_t k0 = 0; k0 < K; k0 += 64) {
+            const int64_t kn = K - k0 < 64 ? K - k0 : 64;
+            double* acc = (double*)calloc((size_t)(kn * r), sizeof(double));
+            for (int64_t t = 0; t < T; ++t)
+                for (int64_t k = 0; k < kn; ++k) {
+                    const double xv = (double)x[t * K + k0 + k];
+                    for (int32_t j = 0; j < r; ++j) acc[k * r + j] += xv * gd[t * r + j];
+                }
+            for (int64_t k = 0; k < kn; ++k)
+                for (int32_t j = 0; j < r; ++j) dA[(k0 + k) * r + j] = (float)acc[k * r + j];
+            free(acc);
+        }
+    }
+    if (dB) {
+#pragma omp parallel for schedule(dynamic) num_threads(nt)
+        for (int64_t n0 = 0; n0 < N; n0 += 64) {
+            const int64_t nn = N - n0 < 64 ? N - n0 : 64;
+            double* acc = (double*)calloc((size_t)(nn * r), sizeof(double));
+            for (int64_t t = 0; t < T; ++t)
+                for (int64_t n = 0; n < nn; ++n) {
+                    const double gv = (double)dy[t * N + n0 + n];
+                    for (int32_t j = 0; j < r; ++j) acc[n * r + j] += hd[t * r + j] * gv;
+                }
+            for (int64_t n = 0; n < nn; ++n)
+                for (int32_t j = 0; j < r; ++j)
+                    dB[(int64_t)j * N + n0 + n] = (float)((double)scale * acc[n * r + j]);
+            free(acc);
+        }
+    }
+    free(hd);
+    free(gd);
+}
+
+/* --------------------------------------------------------------- RMSNorm */
+void oracle_rmsnorm_fwd(int64_t rows, int64_t D, float eps, const float* x, const float* w,
+                        float* y, float* rstd_out, int threads) {
+#pragma omp parallel for schedule(static) num_threads(nthreads(threads))
+    for (int64_t i = 0; i < rows; ++i) {
+        const float* xr = x + i * D;
+        /* tensor.rs:113-115  sqr -> mean_keepdim -> (+eps) -> sqrt */
+        double ss = 0.0;
+        for (int64_t j = 0; j < D; ++j) ss += (double)xr[j] * (double)xr[j];
+        double rms = sqrt(ss / (double)D + (double)eps);
+        if (rstd_out) rstd_out[i] = (float)(1.0 / rms);
+        for (int64_t j = 0; j < D; ++j) {
+            /* tensor.rs:116 broadcast_div, then qwen.rs:321 broadcast_mul(weight) */
+            double v = (double)xr[j] / rms;
+            if (w) v *= (double)w[j];
+            y[i * D + j] = (float)v;
+        }
+    }
+}
+
+void oracle_rmsnorm_bwd(int64_t rows, int64_t D, float eps, const float* x, const float* w,
+                        const float* dy, float* dx, float* dw, int threads) {
+    const int nt = nthreads(threads);
+    double* rs = (double*)malloc(sizeof(double) * (size_t)(rows > 0 ? rows : 1));
+#pragma omp parallel for schedule(static) num_threads(nt)
+    for (int64_t i = 0; i < rows; ++i) {
+        const float* xr = x + i * D;
+        const float* dyr = dy + i * D;
+        double ss = 0.0;
+        for (int64_t j = 0; j < D; ++j) ss += (double)xr[j] * (double)xr[j];
+        double r = 1.0 / sqrt(ss / (double)D + (double)eps);
+        rs[i] = r;
+        if (dx) {
+            double gx = 0.0;
+            for (int64_t j = 0; j < D; ++j) {
+                double g = (double)dyr[j] * (w ? (double)w[j] : 1.0);
+                gx += g * (double)xr[j];
+            }
+            double c = r * r * r * gx / (double)D;
+            for (int64_t j = 0; j < D; ++j) {
+                double g = (double)dyr[j] * (w ? (double)w[j] : 1.0);
+                dx[i * D + j] = (float)(r * g - (double)xr[j] * c);
+            }
+        }
+    }
+    if (dw) {
+#pragma omp parallel for schedule(static) num_threads(nt)
+        for (int64_t j = 0; j < D; ++j) {
+            double acc = 0.0;
+            for (int64_t i = 0; i < rows; ++i) acc += (double)dy[i * D + j] * (double)x[i * D + j] * rs[i];
+            dw[j] = (float)acc;
+        }
+    }
+    free(rs);
+}
+
+/* --------------------------------------------------------------- softmax */
+static int64_t causal_limit(int64_t row, int64_t D, int64_t causal_rows) {
+    /* last unmasked column of this row (inclusive) */
+    if (causal_rows <= 0) return D - 1;
+    return row % causal_rows + (D - causal_rows);
+}
+
+static void softmax_fwd_impl(int64_t rows, int64_t D, int64_t causal_rows, const int64_t* row_ids,
+                             const float* s, float* p, int threads) {
+#pragma omp parallel for schedule(static) num_threads(nthreads(threads))
+    for (int64_t i = 0; i < rows; ++i) {
+        const float* sr = s + i * D;
+        float* pr = p + i * D;
+        int64_t lim = causal_limit(row_ids ? row_ids[i] : i, D, causal_rows);
+        /* tensor.rs:93 max_keepdim (masked entries are -inf and never the max) */
+        double m = -INFINITY;
+        for (int64_t j = 0; j <= lim; ++j) if ((double)sr[j] > m) m = (double)sr[j];
+        /* tensor.rs:94-96  sub, exp, sum_keepdim */
+        double sum = 0.0;
+        for (int64_t j = 0; j <= lim; ++j) sum += exp((double)sr[j] - m);
+        /* tensor.rs:97 broadcast_div; exp(-inf) = 0 exactly at masked entries */
+        for (int64_t j = 0; j < D; ++j)
+            pr[j] = j <= lim ? (float)(exp((double)sr[j] - m) / sum) : 0.0f;
+    }
+}
+
+static void softmax_bwd_impl(int64_t rows, int64_t D, int64_t causal_rows, const int64_t* row_ids,
+                             const float* p, const float* dp, float* ds, int threads) {
+#pragma omp parallel for schedule(static) num_threads(nthreads(threads))
+    for (int64_t i = 0; i < rows; ++i) {
+        const float* pr = p + i * D;
+        const float* dpr = dp + i * D;
+        int64_t lim = causal_limit(row_ids ? row_ids[i] : i, D, causal_rows);
+        double dot = 0.0;
+        for (int64_t j = 0; j <= lim; ++j) dot += (double)pr[j] * (double)dpr[j];
+        for (int64_t j = 0; j < D; ++j)
+            ds[i * D + j] = j <= lim ? (float)((double)pr[j] * ((double)dpr[j] - dot)) : 0.0f;
+    }
+}
+
+void oracle_softmax_fwd(int64_t rows, int64_t D, int64_t causal_rows, const float* s, float* p,
+                        int threads) {
+    softmax_fwd_impl(rows, D, causal_rows, NULL, s, p, threads);
+}
+
+void oracle_softmax_bwd(int64_t rows, int64_t D, int64_t causal_rows, const float* p,
+                        const float* dp, float* ds, int threads) {
+    softmax_bwd_impl(rows, D, causal_rows, NULL, p, dp, ds, threads);
+}
+
+void oracle_softmax_fwd_rows(int64_t n, int64_t D, int64_t causal_rows, const int64_t* row_ids,
+                             const float* s, float* p, int threads) {
+    softmax_fwd_impl(n, D, causal_rows, row_ids, s, p, threads);
+}
+
+void oracle_softmax_bwd_rows(int64_t n, int64_t D, int64_t causal_rows, const int64_t* row_ids,
+                             const float* p, const float* dp, float* ds, int threads) {
+    softmax_bwd_impl(n, D, causal_rows, row_ids, p, dp, ds, threads);
+}
+
+/* ------------------------------------------------------------------ bf16 */
+void oracle_round_bf16(const float* in, float* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) {
+        uint32_t u;
+        memcpy(&u, &in[i], 4);
+        if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) {
+            u |= 0x00400000u; /* quiet NaN */
+        } else {
+            u += 0x7fffu + ((u >> 16) & 1u);
+        }
+        u &= 0xffff0000u;
+        memcpy(&out[i], &u, 4);
+    }
+}

@@ -1,0 +1,113 @@
+/*
+ * CPU oracle for the fused LoRA / RMSNorm / softmax hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY. This library is the checker the parity tests,
+ * __graft_entry__.smoke() and bench.py's cpu_baseline leg compare against.
+ * The product (libmc_hip.so) never links, loads or calls it, and nothing on
+ * the product path may fall back to it.
+ *
+ * It restates the candle CPU composites of GarthDB/metal-candle v1.3.0 in
+ * their op order, with fp64 accumulation and fp32 storage:
+ *   LoRA delta   src/training/lora.rs:320-339  (H = x.A; dropout(H); H.B; *s)
+ *                src/graph/executor.rs:141-158  (same order, no dropout)
+ *   base linear  candle_nn::Linear as used at src/models/transformer.rs:189-192
+ *                (y = x.W^T + b, W stored [out, in])
+ *   RMSNorm      src/backend/tensor.rs:111-117  (sqr, mean, +eps, sqrt, divide)
+ *                src/models/qwen.rs:314-325     (then * weight)
+ *   softmax      src/backend/tensor.rs:91-98    (max, sub, exp, sum, divide)
+ *                src/models/transformer.rs:264-275 (causal -inf mask added first)
+ *   dropout      candle_nn::ops::dropout (candle-nn 0.9, not vendored): keep iff
+ *                U >= p, kept values scaled by 1/(1-p); the mask itself comes
+ *                from the Philox4x32-10 generator below, shared with the GPU path.
+ * The reference has no backward for any of these ops; the backward functions
+ * are the closed-form gradients of the composites above (candle autograd of
+ * lora.rs:323-339, tensor.rs:91-117, qwen.rs:320-321).
+ *
+ * How each function is pinned (tests/test_oracle.py):
+ *   oracle_lora_fwd      executor known answer (tests/executor_direct.rs:345-367),
+ *                        numpy fp64 brute force, B = 0 => delta = 0, p = 0 => W-only
+ *                        linearity, committed golden vectors.
+ *   oracle_lora_bwd      central finite differences of <y, dY> in fp64,
+ *                        shape contract of tests/gradient_verification.rs:57-62.
+ *   oracle_rmsnorm_fwd   known answers tensor.rs:185-199, 321-336, 382-420,
+ *                        executor_direct.rs:480-495, constant rows
+ *                        rmsnorm_correctness.rs:205-265 closed form.
+ *   oracle_rmsnorm_bwd   finite differences (dx and dw).
+ *   oracle_softmax_fwd   known answers tensor.rs:126-162, 262-276, 400-420,
+ *                        softmax_correctness.rs:200-243, shift invariance,
+ *                        exact zeros under the mask.
+ *   oracle_softmax_bwd   finite differences, rows of dS sum to 0, masked zeros.
+ *   oracle_philox4x32_10 Random123 known-answer vectors (Salmon et al., SC'11).
+ *   oracle_dropout_mask  fraction kept ~ 1-p, independence of (seed, element).
+ */
+#ifndef MC_ORACLE_H
+#define MC_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Philox4x32-10 block: ctr[4], key[2] -> out[4]. */
+void oracle_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]);
+
+/* Dropout keep-mask for a [rows, rank] hidden: mask[i] = (U_i >= p), with
+ * U_i = (philox word >> 8) * 2^-24 and element i = t*rank + j drawn from
+ * counter block i/4, word i%4, key = (seed lo, seed hi). */
+void oracle_dropout_mask(uint64_t seed, float p, int64_t rows, int32_t rank, uint8_t* mask);
+
+/* y[T,N] = x[T,K] . W[N,K]^T + bias[N] + scale * ((x.A) (.) mask / (1-p)) . B
+ * W and bias may be NULL (delta only, like FusedLoRAOp). mask may be NULL
+ * (no dropout). If hd_out is not NULL it receives Hd[T,r] (post-dropout,
+ * pre-scale hidden). threads <= 0 means all OpenMP threads. */
+void oracle_lora_fwd(int64_t T, int64_t K, int64_t N, int32_t r, float scale, float p,
+                     const float* x, const float* W, const float* bias,
+                     const float* A, const float* B, const uint8_t* mask,
+                     float* y, float* hd_out, int threads);
+
+/* Backward of oracle_lora_fwd with W frozen:
+ *   G = s dY B^T, Gd = G (.) M/(1-p)
+ *   dX = dY W + Gd A^T ; dA = x^T Gd ; dB = s Hd^T dY
+ * W may be NULL (delta-only op). Any of dx, dA, dB may be NULL (skipped). */
+void oracle_lora_bwd(int64_t T, int64_t K, int64_t N, int32_t r, float scale, float p,
+                     const float* x, const float* W, const float* A, const float* B,
+                     const uint8_t* mask, const float* dy,
+                     float* dx, float* dA, float* dB, int threads);
+
+/* y = x / sqrt(mean(x^2) + eps) * w ; w may be NULL (unweighted, as in
+ * FusedRMSNormOp). rstd_out (may be NULL) receives 1/sqrt(mean+eps) per row. */
+void oracle_rmsnorm_fwd(int64_t rows, int64_t D, float eps, const float* x, const float* w,
+                        float* y, float* rstd_out, int threads);
+
+/* dx_ij = r_i g_ij - x_ij r_i^3 (1/D) sum_k g_ik x_ik, g = dy (.) w ;
+ * dw_j = sum_i dy_ij x_ij r_i. w may be NULL (then g = dy); dx / dw may be NULL. */
+void oracle_rmsnorm_bwd(int64_t rows, int64_t D, float eps, const float* x, const float* w,
+                        const float* dy, float* dx, float* dw, int threads);
+
+/* Row softmax over the last dim. causal_rows = 0: no mask. causal_rows = S > 0:
+ * row i is query q = i mod S and column j is masked (-inf) iff j > q + (D - S),
+ * the bottom-right aligned causal mask (S = D gives the square causal mask). */
+void oracle_softmax_fwd(int64_t rows, int64_t D, int64_t causal_rows, const float* s, float* p,
+                        int threads);
+
+/* dS = P (.) (dP - sum_j dP_j P_j) ; masked positions give exactly 0. */
+void oracle_softmax_bwd(int64_t rows, int64_t D, int64_t causal_rows, const float* p,
+                        const float* dp, float* ds, int threads);
+
+/* Same as oracle_softmax_fwd / _bwd on n rows whose positions in the full
+ * tensor are row_ids[i] (the causal mask of row i uses row_ids[i] mod S), so a
+ * sample of rows of a large tensor can be checked on its own. */
+void oracle_softmax_fwd_rows(int64_t n, int64_t D, int64_t causal_rows, const int64_t* row_ids,
+                             const float* s, float* p, int threads);
+void oracle_softmax_bwd_rows(int64_t n, int64_t D, int64_t causal_rows, const int64_t* row_ids,
+                             const float* p, const float* dp, float* ds, int threads);
+
+/* Round-to-nearest-even fp32 -> bf16 -> fp32 (the rounding the bf16 inputs get). */
+void oracle_round_bf16(const float* in, float* out, int64_t n);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

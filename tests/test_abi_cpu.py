@@ -1,0 +1,92 @@
+"""C ABI checks that need no GPU: libmc_hip.so loads, exports every function
+include/mc_hip.h declares, and rejects bad arguments on the host with the
+reference's error conventions (validation runs before anything is enqueued,
+so these calls never touch a device)."""
+import ctypes
+
+import numpy as np
+import pytest
+
+
+def test_library_loads_and_exports_header(mc):
+    L = mc._lib.lib()
+    names = mc._lib.header_symbols()
+    assert len(names) >= 16
+    missing = [n for n in names if not hasattr(L, n)]
+    assert not missing, missing
+    assert b"gfx950" in L.mc_version()
+
+
+def _desc(mc, T=16, K=16, N=16, r=4, scale=2.0, p=0.0, dtype=1):
+    return mc._lib.LoraDesc(T, K, N, r, scale, p, dtype)
+
+
+@pytest.mark.parametrize("field,value,code,msg", [
+    ("rank", 0, 2, "LoRA rank must be greater than 0"),        # lora.rs:99-104
+    ("dropout_p", 1.0, 5, "LoRA dropout must be in [0, 1)"),    # lora.rs:113-118
+    ("dropout_p", -0.1, 5, "LoRA dropout must be in [0, 1)"),
+    ("rank", 129, 2, "exceeds the supported maximum 128"),
+    ("tokens", 0, 2, "must be >= 1"),
+    ("act_dtype", 7, 3, "unsupported act_dtype"),
+    ("in_features", 12, 2, "multiples of 8"),
+])
+def test_lora_desc_validation(mc, field, value, code, msg):
+    L = mc._lib.lib()
+    d = _desc(mc)
+    setattr(d, field, value)
+    assert L.mc_lora_fwd_workspace_size(ctypes.byref(d)) == 0
+    fake = ctypes.c_void_p(256)
+    st = L.mc_lora_fwd(ctypes.byref(d), fake, None, None, fake, fake, None, fake, None, None, 0, None)
+    assert st == code
+    assert msg in mc._lib.last_error()
+
+
+def test_lora_null_and_workspace_errors(mc):
+    L = mc._lib.lib()
+    d = _desc(mc)
+    fake = ctypes.c_void_p(256)
+    assert L.mc_lora_fwd(ctypes.byref(d), None, None, None, fake, fake, None, fake, None, None, 0, None) == 1
+    assert L.mc_lora_fwd(None, fake, None, None, fake, fake, None, fake, None, None, 0, None) == 1
+    # workspace too small
+    need = L.mc_lora_fwd_workspace_size(ctypes.byref(d))
+    assert need > 0
+    assert L.mc_lora_fwd(ctypes.byref(d), fake, None, None, fake, fake, None, fake, None, fake, need - 1,
+                         None) == 6
+    assert "workspace" in mc._lib.last_error()
+    # misaligned activations
+    assert L.mc_lora_fwd(ctypes.byref(d), ctypes.c_void_p(258), None, None, fake, fake, None, fake, None, fake,
+                         need, None) == 4
+    # dropout without a mask
+    d.dropout_p = 0.1
+    assert L.mc_lora_fwd(ctypes.byref(d), fake, None, None, fake, fake, None, fake, None, fake, need, None) == 1
+    assert "requires a mask" in mc._lib.last_error()
+    # backward: dB without the saved hidden
+    d.dropout_p = 0.0
+    nb = L.mc_lora_bwd_workspace_size(ctypes.byref(d))
+    assert L.mc_lora_bwd(ctypes.byref(d), fake, None, fake, fake, None, None, fake, None, None, fake, fake, nb,
+                         None) == 1
+    assert "h_save" in mc._lib.last_error()
+
+
+def test_rowop_validation(mc):
+    L = mc._lib.lib()
+    fake = ctypes.c_void_p(256)
+    assert L.mc_rmsnorm_fwd(0, 8, 1e-6, 0, fake, None, fake, None, None) == 2
+    assert L.mc_rmsnorm_fwd(4, 8, -1.0, 0, fake, None, fake, None, None) == 5
+    assert L.mc_rmsnorm_fwd(4, 8, 1e-6, 2, fake, None, fake, None, None) == 3
+    assert L.mc_rmsnorm_bwd(4, 8, 1e-6, 0, fake, None, None, fake, fake, fake, None, 0, None) == 6
+    assert L.mc_softmax_fwd(4, 8, 9, 0, fake, fake, None) == 2
+    assert "causal_rows" in mc._lib.last_error()
+    assert L.mc_softmax_bwd(4, 8, 0, 0, None, fake, fake, None) == 1
+    assert L.mc_profile_read(9, None, None, None, None) == 5
+
+
+def test_dropout_mask_matches_oracle(mc):
+    import oracle
+
+    for seed, p, rows, rank in [(1234, 0.1, 257, 64), (0, 0.5, 3, 5), (2**40 + 7, 0.25, 100, 8)]:
+        got = mc.dropout_mask(seed, p, rows, rank).numpy()
+        assert np.array_equal(got, oracle.dropout_mask(seed, p, rows, rank))
+    m = mc.dropout_mask(1234, 0.1, 16384, 64).numpy()
+    assert abs(m.mean() - 0.9) < 0.005
+    assert mc._lib.lib().mc_dropout_mask(1, 1.0, 4, 4, ctypes.c_void_p(256)) == 5

@@ -1,0 +1,150 @@
+"""GPU parity of the fused LoRA linear (fwd + bwd) against the CPU oracle.
+
+Cases: the executor known answer (tests/executor_direct.rs:345-367), the
+reference's fused-vs-candle LoRA shapes (tests/custom_ops_correctness.rs:
+15-170: [2,64,512] r8 s2, batches 1/4/8 at [b,32,256], ranks 4..32),
+BASELINE config 1 (fp32, 1e-5) and the bf16 projection shapes of configs 3-5
+(2e-2), with dropout masks from the shared host generator, bias, delta-only
+(W absent, as FusedLoRAOp) and ragged sizes. At full token counts the
+O(T.K.N) outputs y and dX are checked on a seeded sample of token rows (rows
+are independent), dA / dB (reductions over all tokens) in full.
+Tolerance: max|out-ref|/max|ref|.
+"""
+import zlib
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from conftest import rel_err
+from inputs import lora_case, np32
+
+pytestmark = pytest.mark.gpu
+
+F32_TOL, BF16_TOL = 1e-5, 2e-2
+
+
+def _run(mc, dev, c, scale, mask=None, p=0.0):
+    g = lambda t: None if t is None else t.to(dev)  # noqa: E731
+    md = None if mask is None else torch.from_numpy(mask).to(dev)
+    y, h = mc.lora_forward(g(c["x"]), g(c["A"]), g(c["B"]), scale, W=g(c["W"]), bias=g(c["bias"]), mask=md,
+                           dropout_p=p)
+    dX, dA, dB = mc.lora_backward(g(c["x"]), g(c["A"]), g(c["B"]), g(c["dy"]), scale, W=g(c["W"]), mask=md,
+                                  dropout_p=p, h_save=h)
+    torch.cuda.synchronize()
+    return y, h, dX, dA, dB
+
+
+def _check(mc, dev, c, scale, tol, mask=None, p=0.0, sample_rows=None):
+    y, h, dX, dA, dB = _run(mc, dev, c, scale, mask, p)
+    x, W, A, B, dy, bias = (np32(c[k]) for k in ("x", "W", "A", "B", "dy", "bias"))
+    T = x.shape[0]
+    rows = np.arange(T) if sample_rows is None else np.sort(
+        np.random.default_rng(0).choice(T, size=min(sample_rows, T), replace=False))
+    m = None if mask is None else mask[rows]
+    y_ref, hd_ref = oracle.lora_fwd(x[rows], A, B, scale, W=W, bias=bias, mask=m, p=p, return_hidden=True)
+    dx_ref, _, _ = oracle.lora_bwd(x[rows], A, B, dy[rows], scale, W=W, mask=m, p=p, need_dA=False, need_dB=False)
+    _, dA_ref, dB_ref = oracle.lora_bwd(x, A, B, dy, scale, W=W, mask=mask, p=p, need_dx=False)
+    ri = torch.from_numpy(rows).to(dev)
+    errs = {
+        "y": rel_err(y.index_select(0, ri), y_ref),
+        "h": rel_err(h.index_select(1, ri).t(), hd_ref),
+        "dX": rel_err(dX.index_select(0, ri), dx_ref),
+        "dA": rel_err(dA, dA_ref),
+        "dB": rel_err(dB, dB_ref),
+    }
+    bad = {k: v for k, v in errs.items() if not v <= tol}
+    assert not bad, f"rel-err above {tol}: {errs}"
+    return y, h, dX, dA, dB
+
+
+def test_executor_known_answer(mc, dev):
+    """executor_direct.rs:345-367 inputs; y hand-derived in the survey."""
+    x = torch.tensor([[1.0, 2, 3, 4], [5, 6, 7, 8]], device=dev)
+    A = torch.tensor([[0.1, 0.2], [0.3, 0.4], [0.5, 0.6], [0.7, 0.8]], device=dev)
+    B = torch.tensor([[1.0, 2, 3, 4], [5, 6, 7, 8]], device=dev)
+    y, _ = mc.lora_forward(x, A, B, 0.5)
+    expect = np.array([[17.5, 23, 28.5, 34], [40.7, 53.4, 66.1, 78.8]])
+    assert rel_err(y, expect) <= F32_TOL
+
+
+def test_config1_fp32(mc, dev):
+    """BASELINE c1: x [4,128,768] fp32, W 768x768, r8 a16, no dropout, seed 0."""
+    c = lora_case(0, 4 * 128, 768, 768, 8, dtype=torch.float32)
+    _check(mc, dev, c, 2.0, F32_TOL)
+
+
+@pytest.mark.parametrize("T,K,N,r", [(128, 512, 512, 8), (32, 256, 256, 4), (4 * 32, 256, 256, 16),
+                                     (8 * 32, 256, 256, 32), (100, 40, 24, 3), (1, 8, 8, 1), (65, 72, 136, 17)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_reference_shapes(mc, dev, T, K, N, r, dtype):
+    c = lora_case(T * 7 + r, T, K, N, r, dtype=dtype, bias=True)
+    _check(mc, dev, c, 2.0, F32_TOL if dtype == torch.float32 else BF16_TOL)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_delta_only(mc, dev, dtype):
+    """W absent: exactly FusedLoRAOp's delta (custom_ops.rs:53-66)."""
+    c = lora_case(5, 2 * 64, 512, 512, 8, dtype=dtype, w=False, x_std=1.0)
+    c["B"] = c["B"] * 50  # make the delta O(1)
+    _check(mc, dev, c, 2.0, F32_TOL if dtype == torch.float32 else BF16_TOL)
+
+
+def test_zero_B_gives_base(mc, dev):
+    """B = 0 => delta = 0 (lora.rs:244, lora.rs:656-659): y equals the base linear."""
+    c = lora_case(6, 256, 256, 384, 8)
+    c["B"] = torch.zeros_like(c["B"])
+    y, _, _, _, _ = _run(mc, dev, c, 2.0)
+    y0, _, _, _, _ = _run(mc, dev, dict(c, A=torch.zeros_like(c["A"])), 2.0)
+    assert torch.equal(y, y0)
+
+
+@pytest.mark.parametrize("name,T,K,N,r", [("c3 q_proj", 8192, 896, 896, 8), ("c3 v_proj", 8192, 896, 128, 8),
+                                          ("c4 q_proj", 16384, 1536, 1536, 16), ("c4 k_proj", 16384, 1536, 256, 16),
+                                          ("c4 down_proj", 16384, 8960, 1536, 16)])
+def test_config_projections_bf16(mc, dev, name, T, K, N, r):
+    c = lora_case(zlib.crc32(name.encode()), T, K, N, r)
+    _check(mc, dev, c, 2.0, BF16_TOL, sample_rows=256)
+
+
+def test_config5_dropout_bf16(mc, dev):
+    """c5-style: rank 64, alpha 128, dropout 0.1 with the seed-1234 host mask."""
+    T, K, N, r = 2048, 3584, 512, 64
+    c = lora_case(1234, T, K, N, r)
+    mask = mc.dropout_mask(1234, 0.1, T, r).numpy()
+    assert np.array_equal(mask, oracle.dropout_mask(1234, 0.1, T, r))
+    _check(mc, dev, c, 2.0, BF16_TOL, mask=mask, p=0.1, sample_rows=256)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_dropout_mask_semantics(mc, dev, dtype):
+    """Masked hidden entries are exactly zero; kept ones scaled by 1/(1-p)."""
+    T, K, N, r, p = 96, 64, 64, 8, 0.5
+    c = lora_case(3, T, K, N, r, dtype=dtype)
+    mask = oracle.dropout_mask(77, p, T, r)
+    _, h, _, _, _ = _check(mc, dev, c, 2.0, F32_TOL if dtype == torch.float32 else BF16_TOL, mask=mask, p=p)
+    hn = h.t().cpu().numpy()
+    assert (hn[mask == 0] == 0).all()
+
+
+def test_backward_deterministic(mc, dev):
+    c = lora_case(21, 4096, 1536, 256, 16)
+    a = _run(mc, dev, c, 2.0)
+    b = _run(mc, dev, c, 2.0)
+    for u, v in zip(a, b):
+        assert torch.equal(u, v)
+
+
+def test_partial_outputs(mc, dev):
+    """dX / dA / dB individually optional (NULL outputs are skipped)."""
+    c = lora_case(8, 256, 128, 64, 8)
+    g = lambda t: t.to(dev)  # noqa: E731
+    y, h = mc.lora_forward(g(c["x"]), g(c["A"]), g(c["B"]), 2.0, W=g(c["W"]))
+    full = mc.lora_backward(g(c["x"]), g(c["A"]), g(c["B"]), g(c["dy"]), 2.0, W=g(c["W"]), h_save=h)
+    only_b = mc.lora_backward(None, g(c["A"]), g(c["B"]), g(c["dy"]), 2.0, W=g(c["W"]), h_save=h,
+                              need_dx=False, need_dA=False)
+    only_x = mc.lora_backward(None, g(c["A"]), g(c["B"]), g(c["dy"]), 2.0, W=g(c["W"]), need_dA=False,
+                              need_dB=False)
+    assert only_b[0] is None and only_b[1] is None and torch.equal(only_b[2], full[2])
+    assert torch.equal(only_x[0], full[0])
