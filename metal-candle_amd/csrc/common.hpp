@@ -99,4 +99,15 @@ __device__ __forceinline__ float wave_max(float v) {
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & (kWave - 1); }
 
+// 16-byte load of base[off .. off+8) (bf16) or base[off .. off+4) (fp32) that
+// yields zeros when !ok. The load itself is unconditional from an in-bounds
+// address (base[0] when !ok) and the zero is a value select: a conditional
+// load written as `ok ? *p : zero` is lowered to a load through a selected
+// pointer to a stack copy of `zero`, i.e. flat loads and scratch traffic.
+template <typename T>
+__device__ __forceinline__ uint4 load16(const T* base, int64_t off, bool ok) {
+    const uint4 v = *reinterpret_cast<const uint4*>(base + (ok ? off : 0));
+    return ok ? v : make_uint4(0u, 0u, 0u, 0u);
+}
+
 }  // namespace mc

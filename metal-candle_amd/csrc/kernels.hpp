@@ -37,7 +37,9 @@ struct LoraFwdWs {
 };
 struct LoraBwdWs {
     size_t b_hilo;    // bf16 [2][r16][N]  B split into hi/lo
-    size_t at_ext;    // bf16 [rext][K]    A^T, zero padded rows (dX extension operand)
+    size_t wt;        // bf16 [K][N]       W^T (dX GEMM operand; bf16 path with W)
+    size_t at_ext;    // bf16 [K][rext]    A, zero padded columns (dX extension operand);
+                      // fp32 path: f32 [r][K] A^T
     size_t gd_ext;    // bf16 [T][rext]    Gd, zero padded (dX extension operand)
     size_t gd_t;      // f32  [r][T]       Gd^T
     size_t part_a;    // f32  [S_a][r16][K] split-T partials of dA

@@ -8,7 +8,7 @@
 //   4. y = [x | s*Hd] . [W | B^T]^T + b        (one MFMA GEMM)
 // Backward (W frozen; candle autograd of the same composite):
 //   1. B -> bf16 hi/lo ; G = s dY.B^T, Gd = dropout'(G) -> Gd^T fp32, Gd bf16
-//   2. dX = [dY | Gd] . [W ; A^T]              (one MFMA GEMM, NN)
+//   2. W -> W^T, A -> bf16 ; dX = [dY | Gd] . [W^T | A]^T   (one MFMA GEMM)
 //   3. dA = x^T.Gd  (split-T colreduce + fixed-order split sum)
 //   4. dB = s Hd^T.dY (same)
 // The fp32 path runs the same sequence with fp32 operands and FMA kernels.
@@ -105,7 +105,8 @@ LoraBwdWs lora_bwd_ws(const mc_lora_desc& d) {
     size_t off = 0;
     if (m.bf16) {
         w.b_hilo = off; off += align256((size_t)2 * m.r16 * m.N * 2);
-        w.at_ext = off; off += align256((size_t)m.rext * m.K * 2);
+        w.wt = off;     off += align256((size_t)m.K * m.N * 2);
+        w.at_ext = off; off += align256((size_t)m.K * m.rext * 2);
         w.gd_ext = off; off += align256((size_t)m.T * m.rext * 2);
         w.gd_t = off;   off += align256((size_t)m.r * m.T * 4);
         w.part_a = off; off += align256((size_t)colreduce_splits(m.T, m.K) * m.r16 * m.K * 4);
@@ -143,8 +144,8 @@ hipError_t launch_lora_fwd(const mc_lora_desc& d, const void* x, const void* W, 
         GemmSeg s0{xb, m.K, static_cast<const uint16_t*>(W), m.K, kbase};
         GemmSeg s1{hs, m.rext, bt, m.rext, m.rext};
         auto sc = gemm_scope(st, m.T, m.N, kbase, m.rext, m.r, 2);
-        return launch_gemm_bf16(false, m.T, m.N, s0, s1, static_cast<const uint16_t*>(bias),
-                                static_cast<uint16_t*>(y), m.N, st);
+        return launch_gemm_bf16(m.T, m.N, s0, s1, static_cast<const uint16_t*>(bias), static_cast<uint16_t*>(y),
+                                m.N, st);
     }
     float* bt = reinterpret_cast<float*>(base + w.bt_ext);
     float* hs = reinterpret_cast<float*>(base + w.hs_ext);
@@ -185,14 +186,16 @@ hipError_t launch_lora_bwd(const mc_lora_desc& d, const void* x, const void* W, 
                                        dX ? gd : nullptr, m.rext, 1.0f, st));
         }
         if (dX) {
+            uint16_t* wt = reinterpret_cast<uint16_t*>(base + w.wt);
             {
-                auto sc = prof::Scope(prof::kLowRank, st, 0.0, 6.0 * m.r * m.K);
-                MC_TRY(launch_prep_bf16(A, m.r, m.r, m.K, true, at, nullptr, m.rext, m.K, st));
+                auto sc = prof::Scope(prof::kLowRank, st, 0.0, 6.0 * m.r * m.K + (W ? 4.0 * m.N * m.K : 0.0));
+                MC_TRY(launch_prep_bf16(A, m.r, m.K, m.r, false, at, nullptr, m.K, m.rext, st));
+                if (W) MC_TRY(launch_transpose_bf16(static_cast<const uint16_t*>(W), m.N, m.K, wt, st));
             }
-            GemmSeg s0{dyb, m.N, static_cast<const uint16_t*>(W), m.K, kbase};
-            GemmSeg s1{gd, m.rext, at, m.K, m.rext};
+            GemmSeg s0{dyb, m.N, wt, m.N, kbase};
+            GemmSeg s1{gd, m.rext, at, m.rext, m.rext};
             auto sc = gemm_scope(st, m.T, m.K, kbase, m.rext, m.r, 2);
-            MC_TRY(launch_gemm_bf16(true, m.T, m.K, s0, s1, nullptr, static_cast<uint16_t*>(dX), m.K, st));
+            MC_TRY(launch_gemm_bf16(m.T, m.K, s0, s1, nullptr, static_cast<uint16_t*>(dX), m.K, st));
         }
         if (dA) {
             const int sa = colreduce_splits(m.T, m.K);

@@ -43,9 +43,9 @@ hipError_t launch_split_sum(const float* partial, int splits, int r16, int r, in
                             bool transpose_out, float* out, hipStream_t stream);
 
 // -------------------------------------------------------------- GEMM bf16
-// C[M][N] = sum over two reduction segments of A_s . B_s (+ bias[n]), bf16 out.
-// A_s bf16 [M][k_s] (row stride lda_s). B_s: NT mode [N][k_s] (stride ldb_s);
-// NN mode [k_s][N] (stride ldb_s). k_s % 8 == 0; k_s may be 0.
+// C[M][N] = sum over two reduction segments of A_s . B_s^T (+ bias[n]), bf16
+// out. A_s bf16 [M][k_s] (row stride lda_s), B_s bf16 [N][k_s] (row stride
+// ldb_s). Row strides and k_s are multiples of 8; k_s may be 0.
 struct GemmSeg {
     const uint16_t* a;
     int64_t lda;
@@ -53,8 +53,11 @@ struct GemmSeg {
     int64_t ldb;
     int64_t k;
 };
-hipError_t launch_gemm_bf16(bool nn, int64_t M, int64_t N, GemmSeg s0, GemmSeg s1,
-                            const uint16_t* bias, uint16_t* c, int64_t ldc, hipStream_t stream);
+hipError_t launch_gemm_bf16(int64_t M, int64_t N, GemmSeg s0, GemmSeg s1, const uint16_t* bias, uint16_t* c,
+                            int64_t ldc, hipStream_t stream);
+// out[c][r] = in[r][c] for a bf16 rows x cols matrix (cols, rows % 8 == 0).
+hipError_t launch_transpose_bf16(const uint16_t* in, int64_t rows, int64_t cols, uint16_t* out,
+                                 hipStream_t stream);
 
 // ------------------------------------------------------------- fp32 path
 // Same contracts as above with fp32 storage and plain FMA arithmetic; used

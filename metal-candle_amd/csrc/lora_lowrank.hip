@@ -108,8 +108,7 @@ __global__ __launch_bounds__(256) void rowproj_bf16(const uint16_t* __restrict__
         for (int u = 0; u < U; ++u) {
             const int64_t s = s0 + 4 * u;
             const int64_t c = s * 32 + kgrp;
-            xa[u] = (row_ok && s < nsteps && c < C) ? *reinterpret_cast<const uint4*>(xrow + s * 32)
-                                                     : make_uint4(0, 0, 0, 0);
+            xa[u] = load16(xrow, s * 32, row_ok && s < nsteps && c < C);
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
@@ -120,8 +119,8 @@ __global__ __launch_bounds__(256) void rowproj_bf16(const uint16_t* __restrict__
 #pragma unroll
                 for (int rc = 0; rc < RC; ++rc) {
                     const int64_t prow = (int64_t)(rc * 16 + (lane & 15)) * C + c;
-                    const uint4 ph = c_ok ? *reinterpret_cast<const uint4*>(Phi + prow) : make_uint4(0, 0, 0, 0);
-                    const uint4 pl = c_ok ? *reinterpret_cast<const uint4*>(Plo + prow) : make_uint4(0, 0, 0, 0);
+                    const uint4 ph = load16(Phi, prow, c_ok);
+                    const uint4 pl = load16(Plo, prow, c_ok);
                     acc[rc] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(xa[u]), as_bf16x8(ph), acc[rc], 0, 0, 0);
                     acc[rc] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(xa[u]), as_bf16x8(pl), acc[rc], 0, 0, 0);
                 }
@@ -185,7 +184,7 @@ __global__ __launch_bounds__(256) void colreduce_bf16(const uint16_t* __restrict
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const int64_t t = t0 + g8 + i;
-            R[i] = (col_ok && t < te) ? *reinterpret_cast<const uint4*>(X + t * C + col) : make_uint4(0, 0, 0, 0);
+            R[i] = load16(X, t * C + col, col_ok && t < te);
         }
         uint4 ahi[RC], alo[RC];
 #pragma unroll
@@ -265,6 +264,36 @@ __global__ __launch_bounds__(256) void split_sum(const float* __restrict__ parti
         s *= scale;
         if (transpose_out) out[c * r + j] = s;
         else out[j * C + c] = s;
+    }
+}
+
+// -------------------------------------------------------- bf16 transpose
+// 64 x 64 tiles through LDS: 16-byte row chunks in, 16-byte column chunks
+// out (the frozen W of the backward GEMM, read and written once per call).
+__global__ __launch_bounds__(256) void transpose_bf16(const uint16_t* __restrict__ in, int64_t rows, int64_t cols,
+                                                      uint16_t* __restrict__ out) {
+    __shared__ uint16_t tile[64][64 + 2];
+    const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
+    for (int i = threadIdx.x; i < 512; i += 256) {
+        const int r = i >> 3, c = (i & 7) * 8;
+        uint4 v = make_uint4(0, 0, 0, 0);
+        if (r0 + r < rows && c0 + c < cols) v = *reinterpret_cast<const uint4*>(in + (r0 + r) * cols + c0 + c);
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            tile[r][c + 2 * e] = (uint16_t)w[e];
+            tile[r][c + 2 * e + 1] = (uint16_t)(w[e] >> 16);
+        }
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < 512; i += 256) {
+        const int c = i >> 3, r = (i & 7) * 8;  // output row c (input column), 8 input rows r..r+7
+        if (c0 + c < cols && r0 + r < rows) {
+            uint32_t w[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) w[e] = (uint32_t)tile[r + 2 * e][c] | ((uint32_t)tile[r + 2 * e + 1][c] << 16);
+            *reinterpret_cast<uint4*>(out + (c0 + c) * rows + r0 + r) = make_uint4(w[0], w[1], w[2], w[3]);
+        }
     }
 }
 
@@ -375,6 +404,13 @@ hipError_t launch_split_sum(const float* partial, int splits, int r16, int r, in
     if (blocks > 4096) blocks = 4096;
     split_sum<<<dim3((unsigned)blocks), 256, 0, stream>>>(partial, splits, r16, r, C, scale,
                                                           transpose_out ? 1 : 0, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_transpose_bf16(const uint16_t* in, int64_t rows, int64_t cols, uint16_t* out,
+                                 hipStream_t stream) {
+    transpose_bf16<<<dim3((unsigned)((cols + 63) / 64), (unsigned)((rows + 63) / 64)), 256, 0, stream>>>(in, rows, cols,
+                                                                                                      out);
     return hipGetLastError();
 }
 

@@ -294,8 +294,7 @@ void bwd_vec_launch(int vpl, dim3 grid, size_t lds, hipStream_t s, int64_t rows,
         case 1: rmsnorm_bwd_vec<T, 1, DW><<<grid, 256, lds, s>>>(rows, d, eps, chunk, x, w, rstd, dy, dx, part); break;
         case 2: rmsnorm_bwd_vec<T, 2, DW><<<grid, 256, lds, s>>>(rows, d, eps, chunk, x, w, rstd, dy, dx, part); break;
         case 4: rmsnorm_bwd_vec<T, 4, DW><<<grid, 256, lds, s>>>(rows, d, eps, chunk, x, w, rstd, dy, dx, part); break;
-        case 8: rmsnorm_bwd_vec<T, 8, DW><<<grid, 256, lds, s>>>(rows, d, eps, chunk, x, w, rstd, dy, dx, part); break;
-        default: rmsnorm_bwd_vec<T, 16, DW><<<grid, 256, lds, s>>>(rows, d, eps, chunk, x, w, rstd, dy, dx, part); break;
+        default: rmsnorm_bwd_vec<T, 8, DW><<<grid, 256, lds, s>>>(rows, d, eps, chunk, x, w, rstd, dy, dx, part); break;
     }
 }
 
@@ -310,7 +309,9 @@ hipError_t bwd_impl(int64_t rows, int64_t dim, float eps, const void* x, const v
     const T* wp = static_cast<const T*>(w);
     const T* gp = static_cast<const T*>(dy);
     T* dxp = static_cast<T*>(dx);
-    if (vec_ok<T>(dim) && (!dw || dim * kRowsPerBlock * sizeof(float) <= 64 * 1024)) {
+    // The backward keeps x, dy, w (and the dw partials) of a row in registers:
+    // up to 8 vectors per lane (4096 bf16 / 2048 fp32 columns).
+    if (vec_ok<T>(dim) && vpl_for<T>(dim) <= 8 && (!dw || dim * kRowsPerBlock * sizeof(float) <= 64 * 1024)) {
         const int vpl = vpl_for<T>(dim);
         if (dw)
             bwd_vec_launch<T, true>(vpl, grid, dim * kRowsPerBlock * sizeof(float), stream, rows, (int)dim,

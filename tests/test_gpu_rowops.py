@@ -80,7 +80,12 @@ def test_rmsnorm_bwd(mc, dev, dtype, shape, use_rstd):
     dx, dw = mc.rms_norm_backward(xd, dyd, 1e-6, wd, rstd if use_rstd else None)
     dx_ref, dw_ref = oracle.rmsnorm_bwd(x.float().numpy(), dy.float().numpy(), 1e-6, w.float().numpy())
     tol = _tol(dtype)
-    assert rel_err(dx, dx_ref) <= tol
+    # dx = r*g - x*r^3*mean(g*x) cancels to ~eps for dim = 1; measure the error
+    # against the size of its terms (r*g) where that exceeds the result
+    _, r_ref = oracle.rmsnorm_fwd(x.float().numpy(), 1e-6, w.float().numpy())
+    terms = np.abs(dy.float().numpy() * w.float().numpy() * r_ref.reshape(x.shape[:-1] + (1,))).max()
+    err = np.abs(to_np(dx).astype(np.float64) - dx_ref).max() / max(np.abs(dx_ref).max(), terms)
+    assert err <= tol
     assert rel_err(dw, dw_ref) <= (1e-5 if dtype == torch.float32 else 1e-4)  # dw accumulates in fp32
     # fixed-order split reduction: bitwise reproducible
     dx2, dw2 = mc.rms_norm_backward(xd, dyd, 1e-6, wd, rstd if use_rstd else None)
