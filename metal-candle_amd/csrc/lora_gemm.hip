@@ -114,15 +114,17 @@ __device__ __forceinline__ i32x4 rsrc_words(const void* base, int64_t bytes) {
 // wave issues ROWS/RPI/waves of them; lane l fetches the global chunk that
 // the swizzle places at row RPI i + l / CPR, slot l % CPR. Chunks at k >= ks
 // load as zeros.
-template <int ROWS, int NT, int BK>
+template <int ROWS, int NT, int BK, int PARTS = 1>
 __device__ __forceinline__ void dma_tile(i32x4 r, uint32_t lds_byte, uint32_t ld, uint32_t kb, uint32_t ks,
-                                         int tid) {
+                                         int tid, int part = 0) {
     constexpr int CPR = BK / 8, RPI = 64 / CPR;
     static_assert(ROWS % (RPI * (NT / 64)) == 0, "rows per wave");
     constexpr int PER_WAVE = ROWS / RPI / (NT / 64);
+    static_assert(PER_WAVE % PARTS == 0, "loads per part");
     const int wave = tid >> 6, lane = tid & 63;
 #pragma unroll
-    for (int j = 0; j < PER_WAVE; ++j) {
+    for (int jj = 0; jj < PER_WAVE / PARTS; ++jj) {
+        const int j = part * (PER_WAVE / PARTS) + jj;
         const int blk = wave * PER_WAVE + j;
         const int row = blk * RPI + lane / CPR;
         const uint32_t k = kb + 8u * (uint32_t)swz<BK>(row, lane % CPR);
@@ -151,122 +153,18 @@ __device__ __forceinline__ void wait_tiles(int remaining) {
     }
 }
 
-template <int BM, int BN, int WM, int WN, int BK, int STAGES>
-__global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, 1)
-__attribute__((amdgpu_waves_per_eu(1, 2))) void gemm_bf16_kernel(GemmArgs g) {
-    constexpr int NWN = BN / WN;
-    constexpr int NT = (BM / WM) * NWN * 64;
-    constexpr int TM = WM / 32, TN = WN / 32;
-    constexpr int KS = BK / 16;                          // MFMA k-substeps per tile
-    constexpr int CPR = BK / 8;                          // 16-byte chunks per LDS row
-    constexpr int STAGE = (BM + BN) * BK;                // bf16 elements per stage (A tile, then B tile)
-    constexpr int LOADS = (BM + BN) / (512 / BK) / (NT / 64);  // loads per wave per tile
-    static_assert(STAGES >= 2 && STAGES <= 5 && (STAGES - 2) * LOADS < 64, "pipeline depth");
-    static_assert(NT / 64 * 4096 <= STAGES * STAGE * 2, "epilogue staging fits in the stage buffers");
-
-    __shared__ __attribute__((aligned(1024))) uint16_t smem[STAGES * STAGE];
-    const uint32_t smem_byte = (uint32_t)reinterpret_cast<uintptr_t>(smem);
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
-    const int wm = wave / NWN, wn = wave % NWN;
-    int tm, tn;
-    tile_of(blockIdx.x, g.tiles_m, g.tiles_n, g.group_m, tm, tn);
-    const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
-    const int nk0 = (int)((g.k0 + BK - 1) / BK);
-    const int nk = nk0 + (int)((g.k1 + BK - 1) / BK);
-
-    // Per-segment buffer resources over the workgroup's rows of A and B:
-    // rows past M / N fall outside num_records and load as zero.
-    const i32x4 ra0 = rsrc_words(g.a0 + m0 * g.lda0, (g.M - m0) * g.lda0 * 2);
-    const i32x4 ra1 = rsrc_words(g.a1 + m0 * g.lda1, (g.M - m0) * g.lda1 * 2);
-    const i32x4 rb0 = rsrc_words(g.b0 + n0 * g.ldb0, (g.N - n0) * g.ldb0 * 2);
-    const i32x4 rb1 = rsrc_words(g.b1 + n0 * g.ldb1, (g.N - n0) * g.ldb1 * 2);
-
-    auto issue = [&](int kt, int stage) {
-        const bool second = kt >= nk0;
-        const uint32_t kb = (uint32_t)(second ? kt - nk0 : kt) * BK;
-        const uint32_t ks = (uint32_t)(second ? g.k1 : g.k0);
-        const uint32_t base = smem_byte + (uint32_t)(stage * STAGE * 2);
-        dma_tile<BM, NT, BK>(second ? ra1 : ra0, base, (uint32_t)(second ? g.lda1 : g.lda0), kb, ks, tid);
-        dma_tile<BN, NT, BK>(second ? rb1 : rb0, base + BM * BK * 2, (uint32_t)(second ? g.ldb1 : g.ldb0), kb, ks,
-                             tid);
-    };
-
-    f32x16 acc[TM][TN];
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
-#pragma unroll
-            for (int q = 0; q < 16; ++q) acc[i][j][q] = 0.f;
-
-    // MFMA 32x32x16 fragments: lane l supplies row l % 32 and k-chunk
-    // 2 ks + l / 32 of the tile. The fragment rows of a lane differ by
-    // multiples of 32, so the swizzle term is the same for all of them: the
-    // slot is (2 ks + l / 32) ^ sw with a per-lane sw, and the row offsets are
-    // immediates of the ds_read.
+// Epilogue shared by the GEMM kernels, one 32 x 32 block at a time through
+// a per-wave 4 KB LDS patch (the stage buffers are free once the main loop
+// has finished and a barrier has passed): accumulator q of lane l is row
+// 8*(q/4) + 4*(l/32) + q%4, column l%32 of the block; it is written to the
+// patch row-major, read back as lane l -> row l/2, columns 16*(l%2) .. +15,
+// and stored as two 16-byte bf16 chunks with the bias added. Rows past M and
+// columns past N are dropped by the buffer bounds / the column check.
+template <int TM, int TN, int WM, int WN>
+__device__ __forceinline__ void store_c(const f32x16 (&acc)[TM][TN], uint16_t* smem, const GemmArgs& g, int64_t m0,
+                                        int64_t n0, int wm, int wn) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int frag_row = lane & 31;
-    const int sw = (frag_row / (128 / BK)) % CPR;
-    const int a_row0 = (wm * WM + frag_row) * BK;
-    const int b_row0 = BM * BK + (wn * WN + frag_row) * BK;
-    bf16x8 fa[2][TM], fb[2][TN];
-    auto load_frags = [&](const uint16_t* st, int ks, int slot) {
-        const int col = 8 * ((2 * ks + (lane >> 5)) ^ sw);
-#pragma unroll
-        for (int t = 0; t < TM; ++t)
-            fa[slot][t] = *reinterpret_cast<const bf16x8*>(&st[a_row0 + t * 32 * BK + col]);
-#pragma unroll
-        for (int t = 0; t < TN; ++t)
-            fb[slot][t] = *reinterpret_cast<const bf16x8*>(&st[b_row0 + t * 32 * BK + col]);
-    };
-
-    // Pipeline over STAGES LDS stages: tile kt lives in stage kt % STAGES and
-    // its loads are issued STAGES-1 tiles ahead. Each tile starts with every
-    // wave waiting until its own loads of the tile are done (the loads of the
-    // later tiles may stay in flight) and a barrier (all loads visible, every
-    // wave done with the previous tile); then the loads of tile
-    // kt + STAGES - 1 go out into the stage the previous tile used.
-#pragma unroll
-    for (int s0 = 0; s0 < STAGES - 1; ++s0)
-        if (s0 < nk) issue(s0, s0);
-    for (int kt = 0; kt < nk; ++kt) {
-        const int ahead = nk - 1 - kt;
-        wait_tiles<LOADS>(ahead < STAGES - 2 ? ahead : STAGES - 2);
-        __syncthreads();
-        if (kt + STAGES - 1 < nk) issue(kt + STAGES - 1, (kt + STAGES - 1) % STAGES);
-        const uint16_t* st = smem + (kt % STAGES) * STAGE;
-        load_frags(st, 0, 0);
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-            const int cur = ks & 1;
-            if (ks + 1 < KS) load_frags(st, ks + 1, cur ^ 1);
-#pragma unroll
-            for (int i = 0; i < TM; ++i)
-#pragma unroll
-                for (int j = 0; j < TN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[cur][i], fb[cur][j], acc[i][j], 0, 0, 0);
-        }
-        // Schedule: the first substep's fragment reads, then per substep the
-        // next substep's reads placed one after each of its first MFMAs.
-        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, TM + TN, 0);
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-#pragma unroll
-            for (int u = 0; u < TM * TN; ++u) {
-                __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-                if (ks + 1 < KS && u < TM + TN) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
-            }
-        }
-    }
-
-    // Epilogue, one 32 x 32 block at a time through a per-wave 4 KB LDS
-    // patch: accumulator q of lane l is row 8*(q/4) + 4*(l/32) + q%4, column
-    // l%32 of the block; it is written to the patch row-major, read back as
-    // lane l -> row l/2, columns 16*(l%2) .. +15, and stored as two 16-byte
-    // bf16 chunks with the bias added. Rows past M and columns past N are
-    // dropped by the buffer bounds / the column check.
-    __syncthreads();
     float* patch = reinterpret_cast<float*>(smem) + wave * 1024;
     const __amdgpu_buffer_rsrc_t rc = make_rsrc(g.c + m0 * g.ldc, (g.M - m0) * g.ldc * 2);
     const __amdgpu_buffer_rsrc_t rbias = make_rsrc(g.bias, g.bias ? g.N * 2 : 0);
@@ -303,6 +201,149 @@ __attribute__((amdgpu_waves_per_eu(1, 2))) void gemm_bf16_kernel(GemmArgs g) {
             }
             __builtin_amdgcn_s_waitcnt(0xc07f);  // patch reads done before it is rewritten
         }
+}
+
+template <int BM, int BN, int WM, int WN, int BK, int STAGES>
+__global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, 1)
+__attribute__((amdgpu_waves_per_eu(1, 2))) void gemm_bf16_kernel(GemmArgs g) {
+    constexpr int NWN = BN / WN;
+    constexpr int NT = (BM / WM) * NWN * 64;
+    constexpr int TM = WM / 32, TN = WN / 32;
+    constexpr int KS = BK / 16;                          // MFMA k-substeps per tile
+    constexpr int CPR = BK / 8;                          // 16-byte chunks per LDS row
+    constexpr int STAGE = (BM + BN) * BK;                // bf16 elements per stage (A tile, then B tile)
+    constexpr int LOADS = (BM + BN) / (512 / BK) / (NT / 64);  // loads per wave per tile
+    static_assert(STAGES >= 2 && STAGES <= 5 && (STAGES - 2) * LOADS < 64 && KS % 2 == 0, "pipeline depth");
+    static_assert(NT / 64 * 4096 <= STAGES * STAGE * 2, "epilogue staging fits in the stage buffers");
+
+    __shared__ __attribute__((aligned(1024))) uint16_t smem[STAGES * STAGE];
+    const uint32_t smem_byte = (uint32_t)reinterpret_cast<uintptr_t>(smem);
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / NWN, wn = wave % NWN;
+    int tm, tn;
+    tile_of(blockIdx.x, g.tiles_m, g.tiles_n, g.group_m, tm, tn);
+    const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+    const int nk0 = (int)((g.k0 + BK - 1) / BK);
+    const int nk = nk0 + (int)((g.k1 + BK - 1) / BK);
+
+    // Per-segment buffer resources over the workgroup's rows of A and B:
+    // rows past M / N fall outside num_records and load as zero.
+    const i32x4 ra0 = rsrc_words(g.a0 + m0 * g.lda0, (g.M - m0) * g.lda0 * 2);
+    const i32x4 ra1 = rsrc_words(g.a1 + m0 * g.lda1, (g.M - m0) * g.lda1 * 2);
+    const i32x4 rb0 = rsrc_words(g.b0 + n0 * g.ldb0, (g.N - n0) * g.ldb0 * 2);
+    const i32x4 rb1 = rsrc_words(g.b1 + n0 * g.ldb1, (g.N - n0) * g.ldb1 * 2);
+
+    // Loads of tile kt into a stage, in KS parts.
+    auto issue = [&](int kt, int stage, int part) {
+        const bool second = kt >= nk0;
+        const uint32_t kb = (uint32_t)(second ? kt - nk0 : kt) * BK;
+        const uint32_t ks = kt < nk ? (uint32_t)(second ? g.k1 : g.k0) : 0u;
+        const uint32_t base = smem_byte + (uint32_t)(stage * STAGE * 2);
+        dma_tile<BM, NT, BK, KS>(second ? ra1 : ra0, base, (uint32_t)(second ? g.lda1 : g.lda0), kb, ks, tid, part);
+        dma_tile<BN, NT, BK, KS>(second ? rb1 : rb0, base + BM * BK * 2, (uint32_t)(second ? g.ldb1 : g.ldb0), kb,
+                                 ks, tid, part);
+    };
+
+    f32x16 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int q = 0; q < 16; ++q) acc[i][j][q] = 0.f;
+
+    // MFMA 32x32x16 fragments: lane l supplies row l % 32 and k-chunk
+    // 2 ks + l / 32 of the tile. The fragment rows of a lane differ by
+    // multiples of 32, so the swizzle term is the same for all of them: the
+    // slot is (2 ks + l / 32) ^ sw with a per-lane sw, and the row offsets are
+    // immediates of the ds_read.
+    const int frag_row = lane & 31;
+    const int sw = (frag_row / (128 / BK)) % CPR;
+    const int a_row0 = (wm * WM + frag_row) * BK;
+    const int b_row0 = BM * BK + (wn * WN + frag_row) * BK;
+    bf16x8 fa[2][TM], fb[2][TN];
+    auto load_frags = [&](const uint16_t* st, int ks, int slot) {
+        const int col = 8 * ((2 * ks + (lane >> 5)) ^ sw);
+#pragma unroll
+        for (int t = 0; t < TM; ++t)
+            fa[slot][t] = *reinterpret_cast<const bf16x8*>(&st[a_row0 + t * 32 * BK + col]);
+#pragma unroll
+        for (int t = 0; t < TN; ++t)
+            fb[slot][t] = *reinterpret_cast<const bf16x8*>(&st[b_row0 + t * 32 * BK + col]);
+    };
+
+    auto issue_all = [&](int t) {
+#pragma unroll
+        for (int p = 0; p < KS; ++p) issue(t, t % STAGES, p);
+    };
+    if constexpr (STAGES == 2) {
+        // Two stages: each tile starts with every wave waiting for its own
+        // loads of the tile and a barrier (all loads visible, every wave done
+        // with the previous tile); the next tile's loads then go out into the
+        // other stage, a part between each pair of MFMA substeps.
+        if (nk > 0) issue_all(0);
+        for (int kt = 0; kt < nk; ++kt) {
+            wait_vmcnt<0>();
+            __syncthreads();
+            const uint16_t* st = smem + (kt & 1) * STAGE;
+            load_frags(st, 0, 0);
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                const int cur = ks & 1;
+                if (ks + 1 < KS) load_frags(st, ks + 1, cur ^ 1);
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[cur][i], fb[cur][j], acc[i][j], 0, 0, 0);
+                if (kt + 1 < nk) issue(kt + 1, (kt + 1) & 1, ks);
+            }
+        }
+    } else {
+        // Three or more stages: tile kt lives in stage kt % STAGES, its loads
+        // issued STAGES-1 tiles ahead. The barrier that publishes tile kt+1
+        // sits before the last substep of tile kt: each wave first waits
+        // until its own loads of tile kt+1 are done (later tiles may stay in
+        // flight); after the barrier every wave has finished tile kt-1, so the
+        // loads of tile kt+STAGES-1 go into its stage, and the fragments of
+        // tile kt+1's first substep are read while the last MFMAs of tile kt
+        // run.
+#pragma unroll
+        for (int s0 = 0; s0 < STAGES - 1; ++s0)
+            if (s0 < nk) issue_all(s0);
+        {
+            const int ahead = nk - 1;
+            wait_tiles<LOADS>(ahead < STAGES - 2 ? ahead : STAGES - 2);
+        }
+        __syncthreads();
+        if (nk > 0) load_frags(smem, 0, 0);
+        for (int kt = 0; kt < nk; ++kt) {
+            const uint16_t* st = smem + (kt % STAGES) * STAGE;
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                const int cur = ks & 1;
+                if (ks + 1 < KS) {
+                    load_frags(st, ks + 1, cur ^ 1);
+                } else if (kt + 1 < nk) {
+                    const int ahead = nk - 2 - kt;  // tiles after kt+1 that were issued
+                    wait_tiles<LOADS>(ahead < STAGES - 3 ? ahead : STAGES - 3);
+                    __syncthreads();
+                    if (kt + STAGES - 1 < nk) issue_all(kt + STAGES - 1);
+                    load_frags(smem + ((kt + 1) % STAGES) * STAGE, 0, cur ^ 1);
+                }
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[cur][i], fb[cur][j], acc[i][j], 0, 0, 0);
+            }
+        }
+    }
+
+    __syncthreads();
+    store_c<TM, TN, WM, WN>(acc, smem, g, m0, n0, wm, wn);
 }
 
 // ------------------------------------------------------------- fp32 GEMM
