@@ -215,7 +215,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="c4", choices=sorted(CONFIGS))
-    ap.add_argument("--cpu-tokens", type=int, default=256, help="token sample of the CPU-oracle baseline")
+    ap.add_argument("--cpu-tokens", type=int, default=2048, help="token sample of the CPU-oracle baseline")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
