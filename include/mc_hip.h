@@ -126,12 +126,12 @@ mc_status mc_rmsnorm_bwd(int64_t rows, int64_t dim, float eps, int32_t dtype, co
 /* Softmax over the last dim of s [rows, dim]. causal_rows = 0: no mask;
  * causal_rows = S > 0 (S <= dim): row i is query q = i mod S and column j is
  * masked (-inf before the softmax, so p = 0 exactly) iff j > q + (dim - S).
- * Masked positions of s are not read. */
+ * 16-byte vectors of s lying wholly in the masked region are not read. */
 mc_status mc_softmax_fwd(int64_t rows, int64_t dim, int64_t causal_rows, int32_t dtype,
                          const void* s, void* p, hipStream_t stream);
 
-/* ds = p (.) (dp - sum_j dp_j p_j), same mask convention (masked ds = 0,
- * masked p / dp not read). */
+/* ds = p (.) (dp - sum_j dp_j p_j), same mask convention (masked ds = 0;
+ * 16-byte vectors of p / dp lying wholly in the masked region are not read). */
 mc_status mc_softmax_bwd(int64_t rows, int64_t dim, int64_t causal_rows, int32_t dtype,
                          const void* p, const void* dp, void* ds, hipStream_t stream);
 
