@@ -62,9 +62,6 @@ __device__ __forceinline__ void tile_of(int pid, int tiles_m, int tiles_n, int g
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
-// Scheduling-group masks of __builtin_amdgcn_sched_group_barrier.
-constexpr int kSchedMfma = 0x008, kSchedDsRead = 0x100;
-
 // Buffer resource (gfx9 raw buffer, stride 0): loads at byte offsets
 // >= num_records return zeros (for loads into LDS, zeros are written), which
 // gives branch-free bounds handling. kOOB is always out of range.

@@ -1,0 +1,754 @@
+// mc_candle.cpp - implementation of the C++ host interface (mc_candle.hpp)
+// over the C ABI of libmc_hip.so. No arithmetic on tensor data happens here
+// (apart from dtype conversion of host copies): every op is one or more
+// mc_* calls, and an mc_* error becomes the op's error.
+#include "mc_candle.hpp"
+
+#include <hip/hip_runtime_api.h>
+#include <math.h>
+#include <string.h>
+
+#include <random>
+#include <sstream>
+
+#include "mc_hip.h"
+
+namespace mc_candle {
+
+// ------------------------------------------------------------------ errors
+std::string TrainingError::to_string() const {
+    switch (kind) {  // src/error.rs:97-114
+        case Kind::InvalidLoRAConfig: return "invalid LoRA configuration: " + reason;
+        case Kind::InvalidConfig: return "invalid training configuration: " + reason;
+        default: return "training failed: " + reason;
+    }
+}
+
+std::string Error::to_string() const {
+    // src/error.rs:18-44: "training error: {0}", "candle error: {0}".
+    return kind == Kind::Training ? "training error: " + training.to_string() : "candle error: " + candle.to_string();
+}
+
+namespace {
+
+CandleError bail(std::string msg) { return CandleError{std::move(msg)}; }
+
+CandleError mc_error(const char* what, mc_status st) {
+    std::ostringstream s;
+    s << what << " failed (status " << (int)st << "): " << mc_last_error();
+    return bail(s.str());
+}
+
+CandleError hip_error(const char* what, hipError_t e) {
+    std::ostringstream s;
+    s << what << ": " << hipGetErrorString(e);
+    return bail(s.str());
+}
+
+size_t dtype_size(DType d) { return d == DType::F32 ? 4 : d == DType::BF16 ? 2 : 1; }
+
+int32_t mc_dtype_of(DType d) { return d == DType::BF16 ? MC_BF16 : MC_F32; }
+
+uint16_t f32_to_bf16(float f) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);  // quiet NaN
+    u += 0x7fffu + ((u >> 16) & 1u);                                             // round to nearest even
+    return (uint16_t)(u >> 16);
+}
+
+float bf16_to_f32(uint16_t h) {
+    const uint32_t u = (uint32_t)h << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+int64_t product(const std::vector<int64_t>& d, size_t from, size_t to) {
+    int64_t p = 1;
+    for (size_t i = from; i < to; ++i) p *= d[i];
+    return p;
+}
+
+// Device-resident workspace for one call.
+struct Workspace {
+    void* p = nullptr;
+    ~Workspace() {
+        if (p) (void)hipFree(p);
+    }
+};
+
+Result<void, CandleError> alloc_ws(Workspace& ws, size_t bytes) {
+    if (bytes == 0) return {};
+    hipError_t e = hipMalloc(&ws.p, bytes);
+    if (e != hipSuccess) return hip_error("workspace allocation", e);
+    return {};
+}
+
+bool same_device(const Tensor& a, const Tensor& b) {
+    return a.device().kind == b.device().kind && a.device().ordinal == b.device().ordinal;
+}
+
+}  // namespace
+
+std::string dims_to_string(const std::vector<int64_t>& dims) {
+    std::ostringstream s;
+    s << "[";
+    for (size_t i = 0; i < dims.size(); ++i) s << (i ? ", " : "") << dims[i];
+    s << "]";
+    return s.str();
+}
+
+// ------------------------------------------------------------------ tensors
+int64_t Tensor::elem_count() const { return product(dims_, 0, dims_.size()); }
+
+size_t Tensor::size_bytes() const { return (size_t)elem_count() * dtype_size(dtype_); }
+
+Result<int64_t, CandleError> Tensor::dim(int64_t i) const {
+    const int64_t r = (int64_t)dims_.size();
+    const int64_t j = i < 0 ? r + i : i;
+    if (j < 0 || j >= r) return bail("DimOutOfRange: dim " + std::to_string(i) + " of shape " + dims_to_string(dims_));
+    return dims_[(size_t)j];
+}
+
+Result<Tensor, CandleError> Tensor::empty(std::vector<int64_t> dims, DType dtype, const Device& device) {
+    for (int64_t d : dims)
+        if (d < 0) return bail("negative dimension in shape " + dims_to_string(dims));
+    Tensor t;
+    t.dims_ = std::move(dims);
+    t.dtype_ = dtype;
+    t.device_ = device;
+    const size_t bytes = t.size_bytes();
+    if (bytes == 0) return t;
+    if (device.is_cpu()) {
+        void* p = ::operator new(bytes);
+        t.storage_ = std::shared_ptr<void>(p, [](void* q) { ::operator delete(q); });
+    } else {
+        hipError_t e = hipSetDevice(device.ordinal);
+        if (e != hipSuccess) return hip_error("hipSetDevice", e);
+        void* p = nullptr;
+        e = hipMalloc(&p, bytes);
+        if (e != hipSuccess) return hip_error("hipMalloc", e);
+        t.storage_ = std::shared_ptr<void>(p, [](void* q) { (void)hipFree(q); });
+    }
+    return t;
+}
+
+Result<Tensor, CandleError> Tensor::zeros(std::vector<int64_t> dims, DType dtype, const Device& device) {
+    auto r = empty(std::move(dims), dtype, device);
+    if (r.is_err() || r.value().size_bytes() == 0) return r;
+    Tensor& t = r.value();
+    if (device.is_cpu()) {
+        memset(t.data(), 0, t.size_bytes());
+    } else {
+        hipError_t e = hipMemset(t.data(), 0, t.size_bytes());
+        if (e != hipSuccess) return hip_error("hipMemset", e);
+    }
+    return r;
+}
+
+Result<Tensor, CandleError> Tensor::from_slice(const std::vector<float>& data, std::vector<int64_t> dims,
+                                               const Device& device, DType dtype) {
+    if ((int64_t)data.size() != product(dims, 0, dims.size()))
+        return bail("shape mismatch in from_slice, got buffer of size " + std::to_string(data.size()) +
+                    " which is incompatible with shape " + dims_to_string(dims));
+    std::vector<uint8_t> host(data.size() * dtype_size(dtype));
+    for (size_t i = 0; i < data.size(); ++i) {
+        if (dtype == DType::F32) {
+            memcpy(&host[i * 4], &data[i], 4);
+        } else if (dtype == DType::BF16) {
+            const uint16_t h = f32_to_bf16(data[i]);
+            memcpy(&host[i * 2], &h, 2);
+        } else {
+            host[i] = (uint8_t)data[i];
+        }
+    }
+    auto r = empty(std::move(dims), dtype, device);
+    if (r.is_err() || host.empty()) return r;
+    Tensor& t = r.value();
+    if (device.is_cpu()) {
+        memcpy(t.data(), host.data(), host.size());
+    } else {
+        hipError_t e = hipMemcpy(t.data(), host.data(), host.size(), hipMemcpyHostToDevice);
+        if (e != hipSuccess) return hip_error("hipMemcpy H2D", e);
+    }
+    return r;
+}
+
+Result<Tensor, CandleError> Tensor::from_bytes(const std::vector<uint8_t>& data, std::vector<int64_t> dims,
+                                               const Device& device) {
+    if ((int64_t)data.size() != product(dims, 0, dims.size()))
+        return bail("shape mismatch in from_bytes for shape " + dims_to_string(dims));
+    auto r = empty(std::move(dims), DType::U8, device);
+    if (r.is_err() || data.empty()) return r;
+    Tensor& t = r.value();
+    if (device.is_cpu()) {
+        memcpy(t.data(), data.data(), data.size());
+    } else {
+        hipError_t e = hipMemcpy(t.data(), data.data(), data.size(), hipMemcpyHostToDevice);
+        if (e != hipSuccess) return hip_error("hipMemcpy H2D", e);
+    }
+    return r;
+}
+
+Result<Tensor, CandleError> Tensor::to_device(const Device& device) const {
+    auto r = empty(dims_, dtype_, device);
+    if (r.is_err() || size_bytes() == 0) return r;
+    Tensor& t = r.value();
+    hipMemcpyKind kind = device_.is_cpu() ? (device.is_cpu() ? hipMemcpyHostToHost : hipMemcpyHostToDevice)
+                                          : (device.is_cpu() ? hipMemcpyDeviceToHost : hipMemcpyDeviceToDevice);
+    if (kind == hipMemcpyHostToHost) {
+        memcpy(t.data(), data(), size_bytes());
+        return r;
+    }
+    hipError_t e = hipMemcpy(t.data(), data(), size_bytes(), kind);
+    if (e != hipSuccess) return hip_error("hipMemcpy", e);
+    return r;
+}
+
+Result<std::vector<float>, CandleError> Tensor::to_vec_f32() const {
+    std::vector<uint8_t> host(size_bytes());
+    if (!host.empty()) {
+        if (device_.is_cpu()) {
+            memcpy(host.data(), data(), host.size());
+        } else {
+            hipError_t e = hipMemcpy(host.data(), data(), host.size(), hipMemcpyDeviceToHost);
+            if (e != hipSuccess) return hip_error("hipMemcpy D2H", e);
+        }
+    }
+    std::vector<float> out((size_t)elem_count());
+    for (size_t i = 0; i < out.size(); ++i) {
+        if (dtype_ == DType::F32) {
+            memcpy(&out[i], &host[i * 4], 4);
+        } else if (dtype_ == DType::BF16) {
+            uint16_t h;
+            memcpy(&h, &host[i * 2], 2);
+            out[i] = bf16_to_f32(h);
+        } else {
+            out[i] = (float)host[i];
+        }
+    }
+    return out;
+}
+
+// ------------------------------------------------------------------ FusedLoRAOp
+Result<FusedLoRAOp, CandleError> FusedLoRAOp::create(Tensor lora_a, Tensor lora_b, float scaling) {
+    // custom_ops.rs:118-150
+    if (lora_a.rank() != 2 || lora_b.rank() != 2)
+        return bail("LoRA matrices must be 2D, got shapes " + dims_to_string(lora_a.dims()) + " and " +
+                    dims_to_string(lora_b.dims()));
+    if (lora_a.dims()[1] != lora_b.dims()[0]) {
+        std::ostringstream s;
+        s << "Incompatible LoRA matrix dimensions: " << lora_a.dims()[0] << "×" << lora_a.dims()[1] << " and "
+          << lora_b.dims()[0] << "×" << lora_b.dims()[1];
+        return bail(s.str());
+    }
+    FusedLoRAOp op;
+    op.lora_a_ = std::move(lora_a);
+    op.lora_b_ = std::move(lora_b);
+    op.scaling_ = scaling;
+    return op;
+}
+
+Result<std::vector<int64_t>, CandleError> FusedLoRAOp::compute_output_shape(const std::vector<int64_t>& dims) const {
+    if (dims.empty()) return bail("Input must have at least 1 dimension");
+    const int64_t in_features = dims.back();
+    const int64_t expected_in = lora_a_.dims()[0];
+    if (in_features != expected_in)
+        return bail("Input feature dimension mismatch: expected " + std::to_string(expected_in) + ", got " +
+                    std::to_string(in_features));
+    std::vector<int64_t> out = dims;
+    out.back() = lora_b_.dims()[1];
+    return out;
+}
+
+Result<Tensor, CandleError> FusedLoRAOp::apply(const Tensor& input) const {
+    return input.device().is_hip() ? hip_fwd(input) : cpu_fwd(input);
+}
+
+Result<Tensor, CandleError> FusedLoRAOp::cpu_fwd(const Tensor&) const {
+    // custom_ops.rs:235-245
+    return bail("FusedLoRAOp is HIP-only. Use standard LoRA operations on CPU or move tensors to a HIP device.");
+}
+
+Result<Tensor, CandleError> FusedLoRAOp::hip_fwd(const Tensor& input) const {
+    auto r = forward_with_base(input, nullptr, nullptr, nullptr, 0.f);
+    if (r.is_err()) return r.error();
+    return std::move(r.value().first);
+}
+
+Result<std::pair<Tensor, LoRASaved>, CandleError> FusedLoRAOp::forward_with_base(const Tensor& input,
+                                                                                 const Tensor* weight,
+                                                                                 const Tensor* bias,
+                                                                                 const Tensor* mask,
+                                                                                 float dropout_p) const {
+    if (!input.device().is_hip()) return cpu_fwd(input).error();
+    auto shape = compute_output_shape(input.dims());
+    if (shape.is_err()) return shape.error();
+    if (!lora_a_.device().is_hip() || !same_device(lora_a_, input)) return bail("LoRA_A must be on HIP device");
+    if (!lora_b_.device().is_hip() || !same_device(lora_b_, input)) return bail("LoRA_B must be on HIP device");
+    if (lora_a_.dtype() != DType::F32 || lora_b_.dtype() != DType::F32)
+        return bail("LoRA_A and LoRA_B must be F32");
+    if (input.dtype() == DType::U8) return bail("fused_lora: input must be F32 or BF16");
+    const int64_t K = lora_a_.dims()[0], r = lora_a_.dims()[1], N = lora_b_.dims()[1];
+    const int64_t T = input.elem_count() / (K ? K : 1);
+    if (weight && (weight->dims() != std::vector<int64_t>{N, K} || weight->dtype() != input.dtype() ||
+                   !same_device(*weight, input)))
+        return bail("fused_lora: weight must be [" + std::to_string(N) + ", " + std::to_string(K) +
+                    "] in the input's dtype on its device, got " + dims_to_string(weight->dims()));
+    if (bias && (bias->dims() != std::vector<int64_t>{N} || bias->dtype() != input.dtype() ||
+                 !same_device(*bias, input)))
+        return bail("fused_lora: bias must be [" + std::to_string(N) + "] in the input's dtype on its device");
+    if (mask && (mask->dims() != std::vector<int64_t>{T, r} || mask->dtype() != DType::U8 ||
+                 !same_device(*mask, input)))
+        return bail("fused_lora: dropout mask must be U8 [" + std::to_string(T) + ", " + std::to_string(r) + "]");
+
+    auto y = Tensor::empty(shape.value(), input.dtype(), input.device());
+    if (y.is_err()) return y.error();
+    auto h = Tensor::empty({r, T}, DType::F32, input.device());
+    if (h.is_err()) return h.error();
+    mc_lora_desc d{T, K, N, (int32_t)r, scaling_, dropout_p, mc_dtype_of(input.dtype())};
+    Workspace ws;
+    const size_t ws_bytes = mc_lora_fwd_workspace_size(&d);
+    auto a = alloc_ws(ws, ws_bytes);
+    if (a.is_err()) return a.error();
+    const mc_status st = mc_lora_fwd(&d, input.data(), weight ? weight->data() : nullptr,
+                                     bias ? bias->data() : nullptr, static_cast<const float*>(lora_a_.data()),
+                                     static_cast<const float*>(lora_b_.data()),
+                                     mask ? static_cast<const uint8_t*>(mask->data()) : nullptr, y.value().data(),
+                                     static_cast<float*>(h.value().data()), ws.p, ws_bytes, nullptr);
+    if (st != MC_OK) return mc_error("fused_lora_forward", st);
+    if (ws.p) {
+        // The workspace is freed at scope exit; hipFree waits for the device.
+    }
+    return std::make_pair(std::move(y.value()), LoRASaved{std::move(h.value())});
+}
+
+Result<LoRAGrads, CandleError> FusedLoRAOp::backward(const Tensor& input, const Tensor* weight,
+                                                     const LoRASaved& saved, const Tensor& grad_output,
+                                                     const Tensor* mask, float dropout_p) const {
+    if (!input.device().is_hip()) return cpu_fwd(input).error();
+    auto shape = compute_output_shape(input.dims());
+    if (shape.is_err()) return shape.error();
+    if (grad_output.dims() != shape.value() || grad_output.dtype() != input.dtype())
+        return bail("fused_lora backward: grad_output must have shape " + dims_to_string(shape.value()) +
+                    " and the input's dtype, got " + dims_to_string(grad_output.dims()));
+    const int64_t K = lora_a_.dims()[0], r = lora_a_.dims()[1], N = lora_b_.dims()[1];
+    const int64_t T = input.elem_count() / (K ? K : 1);
+    if (saved.hidden_t.dims() != std::vector<int64_t>{r, T} || saved.hidden_t.dtype() != DType::F32)
+        return bail("fused_lora backward: saved hidden must be F32 [" + std::to_string(r) + ", " +
+                    std::to_string(T) + "]");
+    if (weight && (weight->dims() != std::vector<int64_t>{N, K} || weight->dtype() != input.dtype()))
+        return bail("fused_lora backward: weight must be [" + std::to_string(N) + ", " + std::to_string(K) + "]");
+    if (mask && (mask->dims() != std::vector<int64_t>{T, r} || mask->dtype() != DType::U8))
+        return bail("fused_lora backward: dropout mask must be U8 [" + std::to_string(T) + ", " +
+                    std::to_string(r) + "]");
+    auto dx = Tensor::empty(input.dims(), input.dtype(), input.device());
+    auto da = Tensor::empty({K, r}, DType::F32, input.device());
+    auto db = Tensor::empty({r, N}, DType::F32, input.device());
+    if (dx.is_err()) return dx.error();
+    if (da.is_err()) return da.error();
+    if (db.is_err()) return db.error();
+    mc_lora_desc d{T, K, N, (int32_t)r, scaling_, dropout_p, mc_dtype_of(input.dtype())};
+    Workspace ws;
+    const size_t ws_bytes = mc_lora_bwd_workspace_size(&d);
+    auto a = alloc_ws(ws, ws_bytes);
+    if (a.is_err()) return a.error();
+    const mc_status st = mc_lora_bwd(
+        &d, input.data(), weight ? weight->data() : nullptr, static_cast<const float*>(lora_a_.data()),
+        static_cast<const float*>(lora_b_.data()), mask ? static_cast<const uint8_t*>(mask->data()) : nullptr,
+        static_cast<const float*>(saved.hidden_t.data()), grad_output.data(), dx.value().data(),
+        static_cast<float*>(da.value().data()), static_cast<float*>(db.value().data()), ws.p, ws_bytes, nullptr);
+    if (st != MC_OK) return mc_error("fused_lora_backward", st);
+    return LoRAGrads{std::move(dx.value()), std::move(da.value()), std::move(db.value())};
+}
+
+// ------------------------------------------------------------------ FusedRMSNormOp
+Result<FusedRMSNormOp, CandleError> FusedRMSNormOp::create(float eps) {
+    FusedRMSNormOp op;
+    op.eps_ = eps;
+    return op;
+}
+
+Result<Tensor, CandleError> FusedRMSNormOp::apply(const Tensor& input) const {
+    return input.device().is_hip() ? hip_fwd(input) : cpu_fwd(input);
+}
+
+Result<Tensor, CandleError> FusedRMSNormOp::cpu_fwd(const Tensor&) const {
+    // custom_ops.rs:526-532
+    return bail("Fused RMS Norm kernel not implemented for CPU. Use a HIP device.");
+}
+
+Result<Tensor, CandleError> FusedRMSNormOp::hip_fwd(const Tensor& input) const {
+    auto r = forward_weighted(input, nullptr);
+    if (r.is_err()) return r.error();
+    return std::move(r.value().first);
+}
+
+Result<std::pair<Tensor, Tensor>, CandleError> FusedRMSNormOp::forward_weighted(const Tensor& input,
+                                                                                const Tensor* weight) const {
+    if (!input.device().is_hip()) return cpu_fwd(input).error();
+    if (input.rank() == 0)
+        return bail("Input tensor for FusedRMSNormOp must have at least 1 dimension, got " +
+                    dims_to_string(input.dims()));
+    if (input.dtype() == DType::U8) return bail("fused-rms-norm: input must be F32 or BF16");
+    const int64_t dim = input.dims().back();
+    const int64_t rows = dim ? input.elem_count() / dim : 0;
+    if (weight && (weight->dims() != std::vector<int64_t>{dim} || weight->dtype() != input.dtype() ||
+                   !same_device(*weight, input)))
+        return bail("fused-rms-norm: weight must be [" + std::to_string(dim) + "] in the input's dtype");
+    auto y = Tensor::empty(input.dims(), input.dtype(), input.device());
+    auto rstd = Tensor::empty({rows}, DType::F32, input.device());
+    if (y.is_err()) return y.error();
+    if (rstd.is_err()) return rstd.error();
+    const mc_status st = mc_rmsnorm_fwd(rows, dim, eps_, mc_dtype_of(input.dtype()), input.data(),
+                                        weight ? weight->data() : nullptr, y.value().data(),
+                                        static_cast<float*>(rstd.value().data()), nullptr);
+    if (st != MC_OK) return mc_error("fused-rms-norm", st);
+    return std::make_pair(std::move(y.value()), std::move(rstd.value()));
+}
+
+Result<std::pair<Tensor, Tensor>, CandleError> FusedRMSNormOp::backward(const Tensor& input, const Tensor* weight,
+                                                                        const Tensor& rstd,
+                                                                        const Tensor& grad_output) const {
+    if (!input.device().is_hip()) return cpu_fwd(input).error();
+    if (input.rank() == 0)
+        return bail("Input tensor for FusedRMSNormOp must have at least 1 dimension, got " +
+                    dims_to_string(input.dims()));
+    const int64_t dim = input.dims().back();
+    const int64_t rows = dim ? input.elem_count() / dim : 0;
+    if (grad_output.dims() != input.dims() || grad_output.dtype() != input.dtype())
+        return bail("fused-rms-norm backward: grad_output must match the input, got " +
+                    dims_to_string(grad_output.dims()));
+    if (rstd.defined() && rstd.rank() && (rstd.dims() != std::vector<int64_t>{rows} || rstd.dtype() != DType::F32))
+        return bail("fused-rms-norm backward: rstd must be F32 [" + std::to_string(rows) + "]");
+    if (weight && (weight->dims() != std::vector<int64_t>{dim} || weight->dtype() != input.dtype()))
+        return bail("fused-rms-norm backward: weight must be [" + std::to_string(dim) + "]");
+    auto dx = Tensor::empty(input.dims(), input.dtype(), input.device());
+    auto dw = Tensor::empty({dim}, DType::F32, input.device());
+    if (dx.is_err()) return dx.error();
+    if (dw.is_err()) return dw.error();
+    Workspace ws;
+    const size_t ws_bytes = mc_rmsnorm_bwd_workspace_size(rows, dim);
+    auto a = alloc_ws(ws, ws_bytes);
+    if (a.is_err()) return a.error();
+    const mc_status st = mc_rmsnorm_bwd(rows, dim, eps_, mc_dtype_of(input.dtype()), input.data(),
+                                        weight ? weight->data() : nullptr,
+                                        rstd.rank() ? static_cast<const float*>(rstd.data()) : nullptr,
+                                        grad_output.data(), dx.value().data(), static_cast<float*>(dw.value().data()),
+                                        ws.p, ws_bytes, nullptr);
+    if (st != MC_OK) return mc_error("fused-rms-norm backward", st);
+    return std::make_pair(std::move(dx.value()), std::move(dw.value()));
+}
+
+// ------------------------------------------------------------------ FusedSoftmaxOp
+Result<FusedSoftmaxOp, CandleError> FusedSoftmaxOp::create() { return FusedSoftmaxOp{}; }
+
+Result<Tensor, CandleError> FusedSoftmaxOp::apply(const Tensor& input) const {
+    return input.device().is_hip() ? hip_fwd(input) : cpu_fwd(input);
+}
+
+Result<Tensor, CandleError> FusedSoftmaxOp::cpu_fwd(const Tensor&) const {
+    // custom_ops.rs:719-725
+    return bail("Fused Softmax kernel not implemented for CPU. Use a HIP device.");
+}
+
+Result<Tensor, CandleError> FusedSoftmaxOp::hip_fwd(const Tensor& input) const { return forward_causal(input, false); }
+
+namespace {
+Result<int64_t, CandleError> causal_rows_of(const Tensor& t, bool causal) {
+    if (!causal) return (int64_t)0;
+    if (t.rank() < 2) return bail("fused-softmax: a causal mask needs at least 2 dimensions, got " +
+                                  dims_to_string(t.dims()));
+    const int64_t S = t.dims()[t.rank() - 2], D = t.dims().back();
+    if (S > D) return bail("fused-softmax: causal mask needs dims[-2] <= dims[-1], got " + dims_to_string(t.dims()));
+    return S;
+}
+}  // namespace
+
+Result<Tensor, CandleError> FusedSoftmaxOp::forward_causal(const Tensor& input, bool causal) const {
+    if (!input.device().is_hip()) return cpu_fwd(input).error();
+    if (input.rank() == 0)
+        return bail("Input tensor for FusedSoftmaxOp must have at least 1 dimension, got " +
+                    dims_to_string(input.dims()));
+    if (input.dtype() == DType::U8) return bail("fused-softmax: input must be F32 or BF16");
+    auto S = causal_rows_of(input, causal);
+    if (S.is_err()) return S.error();
+    const int64_t dim = input.dims().back();
+    const int64_t rows = dim ? input.elem_count() / dim : 0;
+    auto p = Tensor::empty(input.dims(), input.dtype(), input.device());
+    if (p.is_err()) return p.error();
+    const mc_status st = mc_softmax_fwd(rows, dim, S.value(), mc_dtype_of(input.dtype()), input.data(),
+                                        p.value().data(), nullptr);
+    if (st != MC_OK) return mc_error("fused-softmax", st);
+    return p;
+}
+
+Result<Tensor, CandleError> FusedSoftmaxOp::backward(const Tensor& probs, const Tensor& grad_output,
+                                                     bool causal) const {
+    if (!probs.device().is_hip()) return cpu_fwd(probs).error();
+    if (probs.rank() == 0)
+        return bail("Input tensor for FusedSoftmaxOp must have at least 1 dimension, got " +
+                    dims_to_string(probs.dims()));
+    if (grad_output.dims() != probs.dims() || grad_output.dtype() != probs.dtype())
+        return bail("fused-softmax backward: grad_output must match the probabilities, got " +
+                    dims_to_string(grad_output.dims()));
+    auto S = causal_rows_of(probs, causal);
+    if (S.is_err()) return S.error();
+    const int64_t dim = probs.dims().back();
+    const int64_t rows = dim ? probs.elem_count() / dim : 0;
+    auto ds = Tensor::empty(probs.dims(), probs.dtype(), probs.device());
+    if (ds.is_err()) return ds.error();
+    const mc_status st = mc_softmax_bwd(rows, dim, S.value(), mc_dtype_of(probs.dtype()), probs.data(),
+                                        grad_output.data(), ds.value().data(), nullptr);
+    if (st != MC_OK) return mc_error("fused-softmax backward", st);
+    return ds;
+}
+
+// ------------------------------------------------------------------ CustomMetalOps mirror
+Result<Tensor, TrainingError> lora_forward_fused(const Tensor& input, const Tensor& lora_a, const Tensor& lora_b,
+                                                 float scaling) {
+    // metal_ops.rs:127-144
+    auto op = FusedLoRAOp::create(lora_a, lora_b, scaling);
+    if (op.is_err()) return TrainingError::failed("Failed to create FusedLoRAOp: " + op.error().to_string());
+    auto y = op.value().apply(input);
+    if (y.is_err()) return TrainingError::failed("Failed to apply fused LoRA op: " + y.error().to_string());
+    return std::move(y.value());
+}
+
+Result<Tensor, TrainingError> softmax_fused(const Tensor& input) {
+    // metal_ops.rs:146-157
+    auto op = FusedSoftmaxOp::create();
+    if (op.is_err()) return TrainingError::failed("Failed to create FusedSoftmaxOp: " + op.error().to_string());
+    auto y = op.value().apply(input);
+    if (y.is_err()) return TrainingError::failed("Fused Softmax kernel execution failed: " + y.error().to_string());
+    return std::move(y.value());
+}
+
+Result<Tensor, TrainingError> rms_norm_fused(const Tensor& input, float eps) {
+    // metal_ops.rs:159-170
+    auto op = FusedRMSNormOp::create(eps);
+    if (op.is_err()) return TrainingError::failed("Failed to create FusedRMSNormOp: " + op.error().to_string());
+    auto y = op.value().apply(input);
+    if (y.is_err()) return TrainingError::failed("Fused RMS Norm kernel execution failed: " + y.error().to_string());
+    return std::move(y.value());
+}
+
+// ------------------------------------------------------------------ LoRAConfig / LoRALayer
+Result<void, Error> LoRAConfig::validate() const {
+    // lora.rs:97-120
+    if (rank == 0) return Error::from(TrainingError::invalid_config("LoRA rank must be greater than 0"));
+    if (!(alpha > 0.f)) return Error::from(TrainingError::invalid_config("LoRA alpha must be positive"));
+    if (!(dropout >= 0.f && dropout < 1.f))
+        return Error::from(TrainingError::invalid_config("LoRA dropout must be in [0, 1)"));
+    return {};
+}
+
+Result<LoRALayer, Error> LoRALayer::create(size_t in_features, size_t out_features, const LoRAConfig& config,
+                                           const Device& device, uint64_t seed) {
+    auto v = config.validate();
+    if (v.is_err()) return v.error();
+    const size_t max_rank = in_features < out_features ? in_features : out_features;
+    if (config.rank > max_rank) {
+        std::ostringstream s;  // lora.rs:219-228
+        s << "LoRA rank " << config.rank << " exceeds maximum rank " << max_rank << " (min of in_features="
+          << in_features << ", out_features=" << out_features << ")";
+        return Error::from(TrainingError::invalid_config(s.str()));
+    }
+    // A ~ N(0, 1/sqrt(rank)), B = 0 (lora.rs:233-247). Host initialisation.
+    std::mt19937_64 gen(seed);
+    std::normal_distribution<float> nd(0.f, 1.f / sqrtf((float)config.rank));
+    std::vector<float> a(in_features * config.rank);
+    for (float& x : a) x = nd(gen);
+    auto ta = Tensor::from_slice(a, {(int64_t)in_features, (int64_t)config.rank}, device);
+    if (ta.is_err()) return Error::from(ta.error());
+    auto tb = Tensor::zeros({(int64_t)config.rank, (int64_t)out_features}, DType::F32, device);
+    if (tb.is_err()) return Error::from(tb.error());
+    LoRALayer l;
+    l.lora_a_ = std::move(ta.value());
+    l.lora_b_ = std::move(tb.value());
+    l.config_ = config;
+    l.in_features_ = in_features;
+    l.out_features_ = out_features;
+    l.seed_ = seed;
+    return l;
+}
+
+Result<void, Error> LoRALayer::set_lora_a(Tensor a) {
+    if (a.dims() != lora_a_.dims() || a.dtype() != DType::F32)
+        return Error::from(bail("set_lora_a: expected F32 " + dims_to_string(lora_a_.dims()) + ", got " +
+                                dims_to_string(a.dims())));
+    lora_a_ = std::move(a);
+    have_saved_ = false;
+    return {};
+}
+
+Result<void, Error> LoRALayer::set_lora_b(Tensor b) {
+    if (b.dims() != lora_b_.dims() || b.dtype() != DType::F32)
+        return Error::from(bail("set_lora_b: expected F32 " + dims_to_string(lora_b_.dims()) + ", got " +
+                                dims_to_string(b.dims())));
+    lora_b_ = std::move(b);
+    have_saved_ = false;
+    return {};
+}
+
+Result<Tensor, Error> LoRALayer::forward(const Tensor& input) {
+    auto op = FusedLoRAOp::create(lora_a_, lora_b_, config_.scaling());
+    if (op.is_err()) return Error::from(op.error());
+    const bool drop = training_ && config_.dropout > 0.f;
+    mask_ = Tensor();
+    if (drop) {
+        if (input.rank() == 0) return Error::from(bail("Input must have at least 1 dimension"));
+        const int64_t T = input.dims().back() ? input.elem_count() / input.dims().back() : 0;
+        std::vector<uint8_t> m((size_t)T * config_.rank);
+        const mc_status st = mc_dropout_mask(seed_ + step_, config_.dropout, T, (int32_t)config_.rank, m.data());
+        if (st != MC_OK) return Error::from(mc_error("dropout mask", st));
+        ++step_;
+        auto tm = Tensor::from_bytes(m, {T, (int64_t)config_.rank}, input.device());
+        if (tm.is_err()) return Error::from(tm.error());
+        mask_ = std::move(tm.value());
+    }
+    auto r = op.value().forward_with_base(input, nullptr, nullptr, drop ? &mask_ : nullptr,
+                                          drop ? config_.dropout : 0.f);
+    if (r.is_err()) return Error::from(r.error());
+    saved_ = std::move(r.value().second);
+    have_saved_ = true;
+    return std::move(r.value().first);
+}
+
+Result<LoRAGrads, Error> LoRALayer::backward(const Tensor& input, const Tensor& grad_output) {
+    if (!have_saved_) return Error::from(TrainingError::failed("LoRALayer::backward needs a forward first"));
+    auto op = FusedLoRAOp::create(lora_a_, lora_b_, config_.scaling());
+    if (op.is_err()) return Error::from(op.error());
+    const bool drop = mask_.rank() != 0;
+    auto g = op.value().backward(input, nullptr, saved_, grad_output, drop ? &mask_ : nullptr,
+                                 drop ? config_.dropout : 0.f);
+    if (g.is_err()) return Error::from(g.error());
+    return std::move(g.value());
+}
+
+// ------------------------------------------------------------------ Operation
+const char* Operation::name() const {
+    switch (kind) {  // operation.rs:49-63
+        case Kind::Input: return "input";
+        case Kind::Matmul: return "matmul";
+        case Kind::Add: return "add";
+        case Kind::Mul: return "mul";
+        case Kind::MulScalar: return "mul_scalar";
+        case Kind::LoRA: return "lora";
+        case Kind::Softmax: return "softmax";
+        case Kind::RMSNorm: return "rms_norm";
+    }
+    return "unknown";
+}
+
+Result<std::vector<int64_t>, std::string> Operation::output_shape(
+    const std::vector<std::vector<int64_t>>& in) const {
+    // operation.rs:66-160
+    switch (kind) {
+        case Kind::Input:
+            if (in.empty()) return std::string("Input operation requires shape");
+            return in[0];
+        case Kind::Matmul: {
+            if (in.size() != 2) return "Matmul requires 2 inputs, got " + std::to_string(in.size());
+            const auto &a = in[0], &b = in[1];
+            if (a.size() < 2 || b.size() < 2) return std::string("Matmul requires at least 2D tensors");
+            const int64_t ar = a[a.size() - 2], ac = a.back(), br = b[b.size() - 2], bc = b.back();
+            if (ac != br) {
+                std::ostringstream s;
+                s << "Matmul dimension mismatch: " << ar << "×" << ac << " @ " << br << "×" << bc;
+                return s.str();
+            }
+            std::vector<int64_t> out(a.begin(), a.end() - 2);
+            out.push_back(ar);
+            out.push_back(bc);
+            return out;
+        }
+        case Kind::Add:
+        case Kind::Mul:
+            if (in.size() != 2) return std::string(name()) + " requires 2 inputs, got " + std::to_string(in.size());
+            if (in[0] != in[1])
+                return "Shape mismatch: " + dims_to_string(in[0]) + " vs " + dims_to_string(in[1]);
+            return in[0];
+        case Kind::MulScalar:
+            if (in.size() != 1) return "MulScalar requires 1 input, got " + std::to_string(in.size());
+            return in[0];
+        case Kind::LoRA: {
+            if (in.size() != 3) return "LoRA requires 3 inputs (input, a, b), got " + std::to_string(in.size());
+            std::vector<int64_t> out = in[0];
+            if (!out.empty() && !in[2].empty()) out.back() = in[2].back();
+            return out;
+        }
+        case Kind::Softmax:
+        case Kind::RMSNorm:
+            if (in.size() != 1) return std::string(name()) + " requires 1 input, got " + std::to_string(in.size());
+            return in[0];
+    }
+    return std::string("unknown operation");
+}
+
+// ------------------------------------------------------------------ AsyncExecutor
+Result<AsyncExecutor, TrainingError> AsyncExecutor::create(const Device& device) {
+    AsyncExecutor e;
+    e.device_ = device;
+    return e;
+}
+
+Result<Tensor, TrainingError> AsyncExecutor::execute_operation(const Operation& op,
+                                                               const std::vector<Tensor>& inputs) {
+    using K = Operation::Kind;
+    const std::string n = std::to_string(inputs.size());
+    auto candle_only = [&](const char* what) {
+        return TrainingError::failed(std::string(what) +
+                                     " is a generic candle op; libmc_hip.so only provides the fused ops");
+    };
+    switch (op.kind) {  // executor.rs:48-66
+        case K::Input: return TrainingError::failed("Cannot execute Input operation");
+        case K::Matmul:
+            if (inputs.size() != 2) return TrainingError::failed("Matmul requires 2 inputs, got " + n);
+            return candle_only("Matmul");
+        case K::Add:
+            if (inputs.size() != 2) return TrainingError::failed("Add requires 2 inputs, got " + n);
+            return candle_only("Add");
+        case K::Mul:
+            if (inputs.size() != 2) return TrainingError::failed("Mul requires 2 inputs, got " + n);
+            return candle_only("Mul");
+        case K::MulScalar:
+            if (inputs.size() != 1) return TrainingError::failed("MulScalar requires 1 input, got " + n);
+            return candle_only("MulScalar");
+        case K::LoRA:
+            // executor.rs:123-159 (fused path; the candle composite fallback belongs to the caller)
+            if (inputs.size() != 3) return TrainingError::failed("LoRA requires 3 inputs (input, a, b), got " + n);
+            return lora_forward_fused(inputs[0], inputs[1], inputs[2], op.scale);
+        case K::Softmax:
+            // executor.rs:162-185: the fused kernel is for the last dim only
+            if (inputs.size() != 1) return TrainingError::failed("Softmax requires 1 input, got " + n);
+            if (inputs[0].rank() == 0 || op.dim != inputs[0].rank() - 1)
+                return TrainingError::failed("Softmax failed: only the last dimension has a fused kernel, got dim " +
+                                             std::to_string(op.dim) + " of shape " +
+                                             dims_to_string(inputs[0].dims()));
+            return softmax_fused(inputs[0]);
+        case K::RMSNorm:
+            // executor.rs:188-215
+            if (inputs.size() != 1) return TrainingError::failed("RMSNorm requires 1 input, got " + n);
+            return rms_norm_fused(inputs[0], op.eps);
+    }
+    return TrainingError::failed("unknown operation");
+}
+
+Result<void, TrainingError> AsyncExecutor::synchronize() {
+    if (device_.is_cpu()) return {};
+    hipError_t e = hipDeviceSynchronize();
+    if (e != hipSuccess) return TrainingError::failed(std::string("synchronize: ") + hipGetErrorString(e));
+    return {};
+}
+
+std::string AsyncExecutor::debug_string() const {
+    std::ostringstream s;
+    s << "AsyncExecutor { device: " << (device_.is_cpu() ? "Cpu" : "Hip(") ;
+    if (device_.is_hip()) s << device_.ordinal << ")";
+    s << " }";
+    return s.str();
+}
+
+}  // namespace mc_candle

@@ -1,0 +1,333 @@
+// mc_candle.hpp - C++ host side of the MI355X fused-op path, mirroring the
+// operator / layer / executor interface of GarthDB/metal-candle v1.3.0 above
+// the C ABI of libmc_hip.so (include/mc_hip.h).
+//
+// The reference is Rust over candle; this is the same interface in C++, so a
+// caller (and the parity tests) use the names, argument meanings and error
+// strings of the reference:
+//
+//   FusedLoRAOp, FusedRMSNormOp, FusedSoftmaxOp  src/backend/custom_ops.rs:73-824
+//   lora_forward_fused / softmax_fused /
+//   rms_norm_fused (CustomMetalOps)              src/backend/metal_ops.rs:33-171
+//   LoRAConfig, LoRALayer                        src/training/lora.rs:49-560
+//   Operation                                    src/graph/operation.rs:5-181
+//   AsyncExecutor::execute_operation             src/graph/executor.rs:40-226
+//   TrainingError / Error display strings        src/error.rs:10-117
+//
+// Differences from the reference, all additive:
+//   * ops run on HIP device tensors; a CPU tensor gets the reference's
+//     "not implemented for CPU" error (there is no CPU compute here: on any
+//     error the caller's own fallback applies, as in lora.rs:302-310);
+//   * FusedLoRAOp also takes the frozen base weight, bias and a dropout mask,
+//     and has a backward (dX, dA, dB); RMSNorm takes a weight and has a
+//     backward; softmax takes a causal mask and has a backward;
+//   * RMSNorm and softmax accept any rank >= 1 (leading dims are folded into
+//     rows); the Metal kernels stop at rank 3 (custom_ops.rs:548-556, 741-749);
+//   * Operation::output_shape of LoRA returns [..., out_features] (the
+//     reference returns the input shape, operation.rs:139-150).
+//
+// All device work is enqueued on the null stream and every call that returns
+// a host value synchronises through hipMemcpy. Output tensors are allocated
+// here with hipMalloc (like the reference's op allocates its output buffer,
+// custom_ops.rs:395-397); the C ABI underneath allocates nothing.
+#pragma once
+
+#include <stdint.h>
+
+#include <memory>
+#include <optional>
+#include <string>
+#include <utility>
+#include <vector>
+
+namespace mc_candle {
+
+// ------------------------------------------------------------------ errors
+// candle_core::Error::Msg: the op-level error.
+struct CandleError {
+    std::string msg;
+    std::string to_string() const { return msg; }
+};
+
+// crate::error::TrainingError (src/error.rs:94-117).
+struct TrainingError {
+    enum class Kind { InvalidLoRAConfig, InvalidConfig, Failed };
+    Kind kind = Kind::Failed;
+    std::string reason;
+    static TrainingError failed(std::string r) { return {Kind::Failed, std::move(r)}; }
+    static TrainingError invalid_config(std::string r) { return {Kind::InvalidConfig, std::move(r)}; }
+    std::string to_string() const;
+};
+
+// crate::error::Error: a candle error or a training error (src/error.rs:10-50).
+struct Error {
+    enum class Kind { Candle, Training };
+    Kind kind = Kind::Candle;
+    CandleError candle;
+    TrainingError training;
+    static Error from(CandleError e) { Error x; x.kind = Kind::Candle; x.candle = std::move(e); return x; }
+    static Error from(TrainingError e) { Error x; x.kind = Kind::Training; x.training = std::move(e); return x; }
+    std::string to_string() const;
+};
+
+// Rust's Result<T, E>.
+template <class T, class E>
+class Result {
+public:
+    Result(T v) : v_(std::move(v)) {}                      // NOLINT: implicit like Ok(v)
+    Result(E e) : e_(std::move(e)) {}                      // NOLINT: implicit like Err(e)
+    bool is_ok() const { return v_.has_value(); }
+    bool is_err() const { return !v_.has_value(); }
+    T& value() { return *v_; }
+    const T& value() const { return *v_; }
+    const E& error() const { return *e_; }
+    T unwrap() && { return std::move(*v_); }
+private:
+    std::optional<T> v_;
+    std::optional<E> e_;
+};
+
+template <class E>
+class Result<void, E> {
+public:
+    Result() = default;
+    Result(E e) : e_(std::move(e)) {}                      // NOLINT
+    bool is_ok() const { return !e_.has_value(); }
+    bool is_err() const { return e_.has_value(); }
+    const E& error() const { return *e_; }
+private:
+    std::optional<E> e_;
+};
+
+// ------------------------------------------------------------------ tensors
+enum class DType { F32, BF16, U8 };
+
+struct Device {
+    enum class Kind { Cpu, Hip };
+    Kind kind = Kind::Cpu;
+    int ordinal = 0;
+    static Device cpu() { return {Kind::Cpu, 0}; }
+    static Device hip(int ordinal = 0) { return {Kind::Hip, ordinal}; }
+    bool is_cpu() const { return kind == Kind::Cpu; }
+    bool is_hip() const { return kind == Kind::Hip; }
+};
+
+std::string dims_to_string(const std::vector<int64_t>& dims);  // "[2, 3]", as {:?} of a dims slice
+
+// A contiguous row-major tensor in host memory (Device::cpu) or HIP device
+// memory (Device::hip). Copies share storage, like candle's Arc'd storage.
+class Tensor {
+public:
+    Tensor() = default;
+    // Tensor::from_slice: values given as fp32, stored as `dtype` (bf16 is
+    // rounded to nearest even; U8 truncates).
+    static Result<Tensor, CandleError> from_slice(const std::vector<float>& data, std::vector<int64_t> dims,
+                                                  const Device& device, DType dtype = DType::F32);
+    static Result<Tensor, CandleError> from_bytes(const std::vector<uint8_t>& data, std::vector<int64_t> dims,
+                                                  const Device& device);
+    static Result<Tensor, CandleError> zeros(std::vector<int64_t> dims, DType dtype, const Device& device);
+    // Uninitialised storage (for outputs).
+    static Result<Tensor, CandleError> empty(std::vector<int64_t> dims, DType dtype, const Device& device);
+
+    Result<Tensor, CandleError> to_device(const Device& device) const;
+    // Host copy as fp32 (the to_vec1 / flatten_all().to_vec1() of candle).
+    Result<std::vector<float>, CandleError> to_vec_f32() const;
+
+    const std::vector<int64_t>& dims() const { return dims_; }
+    Result<int64_t, CandleError> dim(int64_t i) const;  // negative i counts from the end
+    size_t rank() const { return dims_.size(); }
+    int64_t elem_count() const;
+    DType dtype() const { return dtype_; }
+    const Device& device() const { return device_; }
+    size_t size_bytes() const;
+    void* data() const { return storage_.get(); }
+    bool defined() const { return storage_ != nullptr || elem_count() == 0; }
+
+private:
+    std::vector<int64_t> dims_;
+    DType dtype_ = DType::F32;
+    Device device_;
+    std::shared_ptr<void> storage_;
+};
+
+// ------------------------------------------------------------------ ops
+// Saved state of a LoRA forward that the backward needs.
+struct LoRASaved {
+    Tensor hidden_t;   // Hd^T [r, T] fp32 (post-dropout, pre-scale hidden)
+};
+
+struct LoRAGrads {
+    Tensor dx;         // like the input
+    Tensor da;         // [K, r] fp32
+    Tensor db;         // [r, N] fp32
+};
+
+// FusedLoRAOp (custom_ops.rs:73-431): y = scaling * (x A) B, extended with
+// an optional frozen base linear (x W^T + b) and a dropout keep-mask.
+class FusedLoRAOp {
+public:
+    // FusedLoRAOp::new (custom_ops.rs:118-150): A [K, r], B [r, N].
+    static Result<FusedLoRAOp, CandleError> create(Tensor lora_a, Tensor lora_b, float scaling);
+    const char* name() const { return "fused_lora_forward"; }
+
+    // candle's apply_op1: dispatch on the input's device.
+    Result<Tensor, CandleError> apply(const Tensor& input) const;
+    Result<Tensor, CandleError> cpu_fwd(const Tensor& input) const;
+    Result<Tensor, CandleError> hip_fwd(const Tensor& input) const;
+
+    // Extensions. W [N, K] and bias [N] in the input's dtype (may be
+    // undefined Tensors); mask [T, r] uint8 (1 = keep) with dropout_p > 0.
+    Result<std::pair<Tensor, LoRASaved>, CandleError> forward_with_base(const Tensor& input, const Tensor* weight,
+                                                                        const Tensor* bias, const Tensor* mask,
+                                                                        float dropout_p) const;
+    Result<LoRAGrads, CandleError> backward(const Tensor& input, const Tensor* weight, const LoRASaved& saved,
+                                            const Tensor& grad_output, const Tensor* mask,
+                                            float dropout_p) const;
+
+    const Tensor& lora_a() const { return lora_a_; }
+    const Tensor& lora_b() const { return lora_b_; }
+    float scaling() const { return scaling_; }
+
+private:
+    // compute_output_shape (custom_ops.rs:153-174).
+    Result<std::vector<int64_t>, CandleError> compute_output_shape(const std::vector<int64_t>& dims) const;
+    Tensor lora_a_, lora_b_;
+    float scaling_ = 1.f;
+};
+
+// FusedRMSNormOp (custom_ops.rs:443-632): y = x / sqrt(mean(x^2) + eps) [* w].
+class FusedRMSNormOp {
+public:
+    static Result<FusedRMSNormOp, CandleError> create(float eps);
+    const char* name() const { return "fused-rms-norm"; }
+    Result<Tensor, CandleError> apply(const Tensor& input) const;
+    Result<Tensor, CandleError> cpu_fwd(const Tensor& input) const;
+    Result<Tensor, CandleError> hip_fwd(const Tensor& input) const;
+    // Extensions: weight [dim] (Qwen RMSNorm, qwen.rs:314-325), saved rstd,
+    // backward (dx, dw).
+    Result<std::pair<Tensor, Tensor>, CandleError> forward_weighted(const Tensor& input, const Tensor* weight) const;
+    Result<std::pair<Tensor, Tensor>, CandleError> backward(const Tensor& input, const Tensor* weight,
+                                                            const Tensor& rstd, const Tensor& grad_output) const;
+    float eps() const { return eps_; }
+
+private:
+    float eps_ = 1e-6f;
+};
+
+// FusedSoftmaxOp (custom_ops.rs:644-824): last-dim softmax.
+class FusedSoftmaxOp {
+public:
+    static Result<FusedSoftmaxOp, CandleError> create();
+    const char* name() const { return "fused-softmax"; }
+    Result<Tensor, CandleError> apply(const Tensor& input) const;
+    Result<Tensor, CandleError> cpu_fwd(const Tensor& input) const;
+    Result<Tensor, CandleError> hip_fwd(const Tensor& input) const;
+    // Extensions: causal mask over the last two dims (S = dims[-2]; the mask
+    // of Attention::forward, transformer.rs:264-275) and the backward.
+    Result<Tensor, CandleError> forward_causal(const Tensor& input, bool causal) const;
+    Result<Tensor, CandleError> backward(const Tensor& probs, const Tensor& grad_output, bool causal) const;
+};
+
+// CustomMetalOps (metal_ops.rs:33-171), as free functions over HIP tensors.
+Result<Tensor, TrainingError> lora_forward_fused(const Tensor& input, const Tensor& lora_a, const Tensor& lora_b,
+                                                 float scaling);
+Result<Tensor, TrainingError> softmax_fused(const Tensor& input);
+Result<Tensor, TrainingError> rms_norm_fused(const Tensor& input, float eps);
+
+// ------------------------------------------------------------------ LoRA layer
+// LoRAConfig (lora.rs:49-121).
+struct LoRAConfig {
+    size_t rank = 8;
+    float alpha = 16.f;
+    float dropout = 0.f;
+    float scaling() const { return alpha / (float)rank; }
+    Result<void, Error> validate() const;
+};
+
+// LoRALayer (lora.rs:123-560). A is initialised N(0, 1/sqrt(rank)) from a
+// seeded host generator, B with zeros (lora.rs:233-247). In training mode with
+// dropout > 0 the keep-mask of each forward is drawn with mc_dropout_mask from
+// (seed, forward counter), so a CPU reference fed the same bytes reproduces it.
+class LoRALayer {
+public:
+    static Result<LoRALayer, Error> create(size_t in_features, size_t out_features, const LoRAConfig& config,
+                                           const Device& device, uint64_t seed = 0);
+    // forward (lora.rs:292-342): scaling * (input A) B, dropout in training mode.
+    Result<Tensor, Error> forward(const Tensor& input);
+    // Gradients of the most recent forward for grad_output = dL/dy (the candle
+    // autograd of lora.rs:323-339): dX, dA, dB.
+    Result<LoRAGrads, Error> backward(const Tensor& input, const Tensor& grad_output);
+
+    size_t num_parameters() const { return config_.rank * (in_features_ + out_features_); }
+    void set_training(bool training) { training_ = training; }
+    void eval() { training_ = false; }
+    bool is_training() const { return training_; }
+    const Tensor& lora_a_tensor() const { return lora_a_; }
+    const Tensor& lora_b_tensor() const { return lora_b_; }
+    // Replaces A or B (same shape), e.g. after an optimizer step or a load.
+    Result<void, Error> set_lora_a(Tensor a);
+    Result<void, Error> set_lora_b(Tensor b);
+    const LoRAConfig& config() const { return config_; }
+    size_t in_features() const { return in_features_; }
+    size_t out_features() const { return out_features_; }
+    // Keep-mask [T, rank] of the most recent training-mode forward (undefined otherwise).
+    const Tensor& last_mask() const { return mask_; }
+
+private:
+    Tensor lora_a_, lora_b_;
+    LoRAConfig config_;
+    size_t in_features_ = 0, out_features_ = 0;
+    bool training_ = true;
+    uint64_t seed_ = 0, step_ = 0;
+    LoRASaved saved_;
+    Tensor mask_;
+    bool have_saved_ = false;
+};
+
+// ------------------------------------------------------------------ graph
+struct NodeId {
+    size_t id = 0;
+};
+
+// Operation (operation.rs:5-181).
+struct Operation {
+    enum class Kind { Input, Matmul, Add, Mul, MulScalar, LoRA, Softmax, RMSNorm };
+    Kind kind = Kind::Input;
+    float value = 0.f;      // MulScalar
+    NodeId a, b;            // LoRA
+    float scale = 1.f;      // LoRA
+    size_t dim = 0;         // Softmax
+    float eps = 1e-5f;      // RMSNorm
+
+    static Operation input() { return {}; }
+    static Operation matmul() { Operation o; o.kind = Kind::Matmul; return o; }
+    static Operation add() { Operation o; o.kind = Kind::Add; return o; }
+    static Operation mul() { Operation o; o.kind = Kind::Mul; return o; }
+    static Operation mul_scalar(float v) { Operation o; o.kind = Kind::MulScalar; o.value = v; return o; }
+    static Operation lora(NodeId a, NodeId b, float scale) {
+        Operation o; o.kind = Kind::LoRA; o.a = a; o.b = b; o.scale = scale; return o;
+    }
+    static Operation softmax(size_t dim) { Operation o; o.kind = Kind::Softmax; o.dim = dim; return o; }
+    static Operation rms_norm(float eps) { Operation o; o.kind = Kind::RMSNorm; o.eps = eps; return o; }
+
+    const char* name() const;
+    Result<std::vector<int64_t>, std::string> output_shape(const std::vector<std::vector<int64_t>>& input_shapes) const;
+};
+
+// AsyncExecutor (executor.rs:20-226). The fused ops (LoRA, Softmax, RMSNorm)
+// run on HIP tensors through libmc_hip.so; the generic ops (Matmul, Add, Mul,
+// MulScalar) are candle's and return an error here after the reference's
+// input-count checks.
+class AsyncExecutor {
+public:
+    static Result<AsyncExecutor, TrainingError> create(const Device& device);
+    Result<Tensor, TrainingError> execute_operation(const Operation& op, const std::vector<Tensor>& inputs);
+    Result<void, TrainingError> synchronize();
+    const Device& device() const { return device_; }
+    std::string debug_string() const;
+
+private:
+    Device device_;
+};
+
+}  // namespace mc_candle

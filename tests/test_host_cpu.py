@@ -1,0 +1,10 @@
+"""C++ host interface (metal-candle_amd/host/mc_candle.hpp): the cases that
+need no GPU — LoRAConfig / LoRALayer validation, FusedLoRAOp::new checks, op
+names, the CPU-forward errors, AsyncExecutor input-count errors, Operation
+shapes and the dropout-mask generator — with the reference's messages."""
+import host_runner
+
+
+def test_host_interface_cpu_cases():
+    out = host_runner.run("--cpu", timeout=120)
+    assert "0 failed" in out
