@@ -23,6 +23,8 @@
 //    multiplied; MFMA fragments are double-buffered across the 4 substeps.
 //  - The epilogue goes through a per-wave LDS patch so C is written with
 //    16-byte stores and the bias is added on the way.
+#include <atomic>
+
 #include "common.hpp"
 #include "lora_kernels.hpp"
 
@@ -108,20 +110,21 @@ __device__ __forceinline__ i32x4 rsrc_words(const void* base, int64_t bytes) {
 
 // Loads rows [0, ROWS) x BK columns (k = kb .. kb+BK-1) of one operand tile
 // into the swizzled layout at lds_byte: a load moves RPI = 512/BK rows; each
-// wave issues ROWS/RPI/waves of them; lane l fetches the global chunk that
-// the swizzle places at row RPI i + l / CPR, slot l % CPR. Chunks at k >= ks
-// load as zeros.
+// wave issues ROWS/RPI/waves of them, split over PARTS calls (part p issues
+// loads p, p + PARTS, ...); lane l fetches the global chunk that the swizzle
+// places at row RPI i + l / CPR, slot l % CPR. Chunks at k >= ks load as
+// zeros.
 template <int ROWS, int NT, int BK, int PARTS = 1>
 __device__ __forceinline__ void dma_tile(i32x4 r, uint32_t lds_byte, uint32_t ld, uint32_t kb, uint32_t ks,
                                          int tid, int part = 0) {
     constexpr int CPR = BK / 8, RPI = 64 / CPR;
     static_assert(ROWS % (RPI * (NT / 64)) == 0, "rows per wave");
     constexpr int PER_WAVE = ROWS / RPI / (NT / 64);
-    static_assert(PER_WAVE % PARTS == 0, "loads per part");
+    static_assert(PER_WAVE >= 1, "rows per wave");
     const int wave = tid >> 6, lane = tid & 63;
 #pragma unroll
-    for (int jj = 0; jj < PER_WAVE / PARTS; ++jj) {
-        const int j = part * (PER_WAVE / PARTS) + jj;
+    for (int j = 0; j < PER_WAVE; ++j) {
+        if (j % PARTS != part) continue;  // part p issues loads p, p + PARTS, ...
         const int blk = wave * PER_WAVE + j;
         const int row = blk * RPI + lane / CPR;
         const uint32_t k = kb + 8u * (uint32_t)swz<BK>(row, lane % CPR);
@@ -299,42 +302,31 @@ __attribute__((amdgpu_waves_per_eu(1, 2))) void gemm_bf16_kernel(GemmArgs g) {
             }
         }
     } else {
-        // Three or more stages: tile kt lives in stage kt % STAGES, its loads
-        // issued STAGES-1 tiles ahead. The barrier that publishes tile kt+1
-        // sits before the last substep of tile kt: each wave first waits
-        // until its own loads of tile kt+1 are done (later tiles may stay in
-        // flight); after the barrier every wave has finished tile kt-1, so the
-        // loads of tile kt+STAGES-1 go into its stage, and the fragments of
-        // tile kt+1's first substep are read while the last MFMAs of tile kt
-        // run.
+        // Ring of STAGES stages: tiles 0 .. STAGES-2 are issued up front;
+        // tile kt waits for its own loads (later tiles stay in flight), a
+        // barrier publishes it to every wave and frees stage (kt-1) % STAGES
+        // (every wave has finished tile kt-1), into which the loads of tile
+        // kt+STAGES-1 go, one part after each MFMA substep.
 #pragma unroll
         for (int s0 = 0; s0 < STAGES - 1; ++s0)
             if (s0 < nk) issue_all(s0);
-        {
-            const int ahead = nk - 1;
-            wait_tiles<LOADS>(ahead < STAGES - 2 ? ahead : STAGES - 2);
-        }
-        __syncthreads();
-        if (nk > 0) load_frags(smem, 0, 0);
         for (int kt = 0; kt < nk; ++kt) {
+            const int ahead = nk - 1 - kt;  // tiles after kt already issued, at most STAGES-2
+            wait_tiles<LOADS>(ahead < STAGES - 2 ? ahead : STAGES - 2);
+            __syncthreads();
             const uint16_t* st = smem + (kt % STAGES) * STAGE;
+            load_frags(st, 0, 0);
+            const int nt = kt + STAGES - 1;
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
                 const int cur = ks & 1;
-                if (ks + 1 < KS) {
-                    load_frags(st, ks + 1, cur ^ 1);
-                } else if (kt + 1 < nk) {
-                    const int ahead = nk - 2 - kt;  // tiles after kt+1 that were issued
-                    wait_tiles<LOADS>(ahead < STAGES - 3 ? ahead : STAGES - 3);
-                    __syncthreads();
-                    if (kt + STAGES - 1 < nk) issue_all(kt + STAGES - 1);
-                    load_frags(smem + ((kt + 1) % STAGES) * STAGE, 0, cur ^ 1);
-                }
+                if (ks + 1 < KS) load_frags(st, ks + 1, cur ^ 1);
 #pragma unroll
                 for (int i = 0; i < TM; ++i)
 #pragma unroll
                     for (int j = 0; j < TN; ++j)
                         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[cur][i], fb[cur][j], acc[i][j], 0, 0, 0);
+                if (nt < nk) issue(nt, nt % STAGES, ks);
             }
         }
     }
@@ -406,7 +398,7 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(int64_t M, int64_t N, Gem
 
 template <int BM, int BN, int WM, int WN, int BK, int STAGES>
 hipError_t launch_cfg(int64_t M, int64_t N, GemmSeg s0, GemmSeg s1, const uint16_t* bias, uint16_t* c, int64_t ldc,
-                      hipStream_t stream) {
+                      hipStream_t stream, int group_m) {
     GemmArgs g;
     g.M = M; g.N = N;
     g.a0 = s0.a; g.b0 = s0.b; g.lda0 = s0.lda; g.ldb0 = s0.ldb; g.k0 = s0.k;
@@ -414,19 +406,59 @@ hipError_t launch_cfg(int64_t M, int64_t N, GemmSeg s0, GemmSeg s1, const uint16
     g.bias = bias; g.c = c; g.ldc = ldc;
     g.tiles_m = (int)((M + BM - 1) / BM);
     g.tiles_n = (int)((N + BN - 1) / BN);
-    g.group_m = 8;
+    g.group_m = group_m;
     constexpr int NT = (BM / WM) * (BN / WN) * 64;
     gemm_bf16_kernel<BM, BN, WM, WN, BK, STAGES><<<dim3((unsigned)(g.tiles_m * g.tiles_n)), NT, 0, stream>>>(g);
     return hipGetLastError();
 }
 
+namespace {
+// Compute units of the current device (the number of workgroups one round
+// of the 1-workgroup-per-CU tiles runs at once), cached per device.
+int cu_count() {
+    static std::atomic<int> cache[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    int v = cache[dev].load(std::memory_order_relaxed);
+    if (v > 0) return v;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+    cache[dev].store(v, std::memory_order_relaxed);
+    return v;
+}
+}  // namespace
+
+GemmTile choose_gemm_tile(int64_t M, int64_t N, int cus) {
+    // Estimated time = rounds of one-workgroup-per-CU tiles x work per tile
+    // / relative per-tile throughput (measured on MI355X at the Qwen2.5 layer
+    // shapes): 256 x 256 with 8 waves is the fastest per FLOP, 256 x 192
+    // fills two rounds exactly where N = 1536 (384 tiles of 256 x 256 would
+    // take two rounds at 75%), 128 x 128 keeps small problems spread over
+    // every CU.
+    struct Cand { GemmTile t; int bm, bn; double speed; };
+    const Cand cands[] = {{GemmTile::k256x256, 256, 256, 1.0},
+                          {GemmTile::k256x192, 256, 192, 0.95},
+                          {GemmTile::k128x128, 128, 128, 0.8}};
+    GemmTile best = GemmTile::k128x128;
+    double best_t = 1e300;
+    for (const Cand& c : cands) {
+        const int64_t tiles = ((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn);
+        const int64_t rounds = (tiles + cus - 1) / cus;
+        const double t = (double)rounds * c.bm * c.bn / c.speed;
+        if (t < best_t) { best_t = t; best = c.t; }
+    }
+    return best;
+}
+
 hipError_t launch_gemm_bf16(int64_t M, int64_t N, GemmSeg s0, GemmSeg s1, const uint16_t* bias, uint16_t* c,
                             int64_t ldc, hipStream_t stream) {
-    // 128 x 128 tiles, k-steps of 64, two stages (64 KB of LDS, two
-    // workgroups per CU): the fastest measured configuration on every layer
-    // shape of the 1.5B / 7B configurations (256 x 256 tiles with deeper
-    // pipelines measured slower).
-    return launch_cfg<128, 128, 64, 64, 64, 2>(M, N, s0, s1, bias, c, ldc, stream);
+    switch (choose_gemm_tile(M, N, cu_count())) {
+        case GemmTile::k256x256:  // 8 waves of 128 x 64, k-steps of 64, 2 stages (128 KB LDS)
+            return launch_cfg<256, 256, 128, 64, 64, 2>(M, N, s0, s1, bias, c, ldc, stream, 4);
+        case GemmTile::k256x192:  // 8 waves of 64 x 96, 2 stages (112 KB LDS)
+            return launch_cfg<256, 192, 64, 96, 64, 2>(M, N, s0, s1, bias, c, ldc, stream, 4);
+        default:                  // 4 waves of 64 x 64, k-steps of 32, 4 stages (64 KB LDS)
+            return launch_cfg<128, 128, 64, 64, 32, 4>(M, N, s0, s1, bias, c, ldc, stream, 4);
+    }
 }
 
 hipError_t launch_gemm_f32(bool nn, int64_t M, int64_t N, GemmSegF32 s0, GemmSegF32 s1, const float* bias,
