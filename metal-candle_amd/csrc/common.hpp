@@ -13,6 +13,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
 
 // ---------------------------------------------------------------- bf16
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
@@ -98,6 +99,22 @@ __device__ __forceinline__ float wave_max(float v) {
 }
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & (kWave - 1); }
+
+// ---------------------------------------------------- buffer resources
+// Raw buffer resource (gfx9 layout, stride 0) over [base, base + bytes):
+// loads at byte offsets >= num_records return zeros (loads into LDS write
+// zeros) and stores there are dropped, which gives branch-free bounds
+// handling. kOOB is an offset that is always out of range. num_records is
+// 32-bit: callers keep every offset below 2^31 by basing the resource at
+// the block of rows a workgroup touches.
+constexpr uint32_t kOOB = 0x80000000u;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
+    const int n = bytes <= 0 ? 0 : bytes >= 0x7fffffff ? 0x7fffffff : (int)bytes;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, 0x00020000);
+}
+__device__ __forceinline__ i32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+}
 
 // 16-byte load of base[off .. off+8) (bf16) or base[off .. off+4) (fp32) that
 // yields zeros when !ok. The load itself is unconditional from an in-bounds

@@ -1,16 +1,16 @@
 // LoRA linear forward / backward: workspace layout and launch sequence.
 //
 // Forward (bf16 activations), reference order lora.rs:320-339 plus the base
-// candle Linear (transformer.rs:189-192):
-//   1. A^T -> bf16 hi/lo                       (prep)
+// candle Linear (transformer.rs:189-192), three launches:
+//   1. A^T -> bf16 hi/lo, B^T -> bf16 ext operand          (one prep launch)
 //   2. Hd = dropout(x.A) -> h_save (fp32 [r][T]) and s*Hd (bf16 ext operand)
-//   3. B^T -> bf16 ext operand                 (prep)
-//   4. y = [x | s*Hd] . [W | B^T]^T + b        (one MFMA GEMM)
+//   3. y = [x | s*Hd] . [W | B^T]^T + b                    (one MFMA GEMM)
 // Backward (W frozen; candle autograd of the same composite):
-//   1. B -> bf16 hi/lo ; G = s dY.B^T, Gd = dropout'(G) -> Gd^T fp32, Gd bf16
-//   2. W -> W^T, A -> bf16 ; dX = [dY | Gd] . [W^T | A]^T   (one MFMA GEMM)
-//   3. dA = x^T.Gd  (split-T colreduce + fixed-order split sum)
-//   4. dB = s Hd^T.dY (same)
+//   1. B -> bf16 hi/lo, A -> bf16 ext operand              (one prep launch)
+//   2. G = s dY.B^T, Gd = dropout'(G) -> Gd^T fp32, Gd bf16
+//   3. W -> W^T ; dX = [dY | Gd] . [W^T | A]^T             (one MFMA GEMM)
+//   4. dA = x^T.Gd and dB = s Hd^T.dY: split-T column reductions (one
+//      launch) and their fixed-order split sums (one launch)
 // The fp32 path runs the same sequence with fp32 operands and FMA kernels.
 #include "common.hpp"
 #include "kernels.hpp"
@@ -136,10 +136,11 @@ hipError_t launch_lora_fwd(const mc_lora_desc& d, const void* x, const void* W, 
         const uint16_t* xb = static_cast<const uint16_t*>(x);
         {
             auto sc = lowrank_scope(st, m.T, m.K, m.r, 2);
-            MC_TRY(launch_prep_bf16(A, m.r, m.r, m.K, true, at_hi, at_lo, m.r16, m.K, st));
+            const PrepJob ja{A, m.r, m.r, m.K, true, at_hi, at_lo, m.r16, m.K};   // A^T hi / lo
+            const PrepJob jb{B, m.N, m.N, m.r, true, bt, nullptr, m.N, m.rext};   // B^T, zero-padded
+            MC_TRY(launch_prep_bf16(ja, jb, st));
             MC_TRY(launch_rowproj_bf16(xb, m.T, m.K, at_hi, at_lo, m.r, 1.0f, mask, keep, h_save, hs, m.rext,
                                        d.scale, st));
-            MC_TRY(launch_prep_bf16(B, m.N, m.N, m.r, true, bt, nullptr, m.N, m.rext, st));
         }
         GemmSeg s0{xb, m.K, static_cast<const uint16_t*>(W), m.K, kbase};
         GemmSeg s1{hs, m.rext, bt, m.rext, m.rext};
@@ -179,37 +180,45 @@ hipError_t launch_lora_bwd(const mc_lora_desc& d, const void* x, const void* W, 
         uint16_t* at = reinterpret_cast<uint16_t*>(base + w.at_ext);
         uint16_t* gd = reinterpret_cast<uint16_t*>(base + w.gd_ext);
         float* gdt = reinterpret_cast<float*>(base + w.gd_t);
+        {
+            // B hi / lo for G; A zero-padded for the dX extension columns
+            const PrepJob jb{B, m.N, m.r, m.N, false, need_g ? b_hi : nullptr, b_lo, m.r16, m.N};
+            const PrepJob ja{A, m.r, m.K, m.r, false, dX ? at : nullptr, nullptr, m.K, m.rext};
+            auto sc = prof::Scope(prof::kLowRank, st, 0.0, need_g ? 6.0 * m.r * m.N : 0.0);
+            MC_TRY(launch_prep_bf16(jb, ja, st));
+        }
         if (need_g) {
             auto sc = lowrank_scope(st, m.T, m.N, m.r, 2);
-            MC_TRY(launch_prep_bf16(B, m.N, m.r, m.N, false, b_hi, b_lo, m.r16, m.N, st));
             MC_TRY(launch_rowproj_bf16(dyb, m.T, m.N, b_hi, b_lo, m.r, d.scale, mask, keep, dA ? gdt : nullptr,
                                        dX ? gd : nullptr, m.rext, 1.0f, st));
         }
         if (dX) {
             uint16_t* wt = reinterpret_cast<uint16_t*>(base + w.wt);
-            {
-                auto sc = prof::Scope(prof::kLowRank, st, 0.0, 6.0 * m.r * m.K + (W ? 4.0 * m.N * m.K : 0.0));
-                MC_TRY(launch_prep_bf16(A, m.r, m.K, m.r, false, at, nullptr, m.K, m.rext, st));
-                if (W) MC_TRY(launch_transpose_bf16(static_cast<const uint16_t*>(W), m.N, m.K, wt, st));
+            if (W) {
+                auto sc = prof::Scope(prof::kLowRank, st, 0.0, 4.0 * m.N * m.K);
+                MC_TRY(launch_transpose_bf16(static_cast<const uint16_t*>(W), m.N, m.K, wt, st));
             }
             GemmSeg s0{dyb, m.N, wt, m.N, kbase};
             GemmSeg s1{gd, m.rext, at, m.rext, m.rext};
             auto sc = gemm_scope(st, m.T, m.K, kbase, m.rext, m.r, 2);
             MC_TRY(launch_gemm_bf16(m.T, m.K, s0, s1, nullptr, static_cast<uint16_t*>(dX), m.K, st));
         }
-        if (dA) {
-            const int sa = colreduce_splits(m.T, m.K);
+        if (dA || dB) {
+            // dA = x^T.Gd and dB = s Hd^T.dY: split-T column reductions in one
+            // launch, then both fixed-order split sums in one launch
+            const int sa = colreduce_splits(m.T, m.K), sb = colreduce_splits(m.T, m.N);
             float* pa = reinterpret_cast<float*>(base + w.part_a);
-            auto sc = lowrank_scope(st, m.T, m.K, m.r, 2);
-            MC_TRY(launch_colreduce_bf16(static_cast<const uint16_t*>(x), m.T, m.K, gdt, m.r, sa, pa, st));
-            MC_TRY(launch_split_sum(pa, sa, m.r16, m.r, m.K, 1.0f, true, dA, st));
-        }
-        if (dB) {
-            const int sb = colreduce_splits(m.T, m.N);
             float* pb = reinterpret_cast<float*>(base + w.part_b);
-            auto sc = lowrank_scope(st, m.T, m.N, m.r, 2);
-            MC_TRY(launch_colreduce_bf16(dyb, m.T, m.N, h_save, m.r, sb, pb, st));
-            MC_TRY(launch_split_sum(pb, sb, m.r16, m.r, m.N, d.scale, false, dB, st));
+            const ColJob ca{dA ? static_cast<const uint16_t*>(x) : nullptr, m.K, gdt, sa, pa};
+            const ColJob cb{dB ? dyb : nullptr, m.N, h_save, sb, pb};
+            const SumJob ua{pa, sa, m.K, (int64_t)m.r16 * m.K, 1.0f, true, dA};
+            const SumJob ub{pb, sb, m.N, (int64_t)m.r16 * m.N, d.scale, false, dB};
+            const double bytes = (dA ? 2.0 * m.T * m.K + 4.0 * m.T * m.r : 0.0) +
+                                 (dB ? 2.0 * m.T * m.N + 4.0 * m.T * m.r : 0.0);
+            const double flops = (dA ? 2.0 * m.T * m.K * m.r : 0.0) + (dB ? 2.0 * m.T * m.N * m.r : 0.0);
+            auto sc = prof::Scope(prof::kLowRank, st, flops, bytes);
+            MC_TRY(launch_colreduce_bf16(m.T, m.r, ca, cb, st));
+            MC_TRY(launch_split_sum(m.r, ua, ub, st));
         }
         return hipSuccess;
     }

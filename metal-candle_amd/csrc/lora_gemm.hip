@@ -13,14 +13,20 @@
 //
 // bf16 kernel: a workgroup computes a BM x BN tile with (BM/WM) x (BN/WN)
 // waves, each a WM x WN block of MFMA 32x32x16 bf16 tiles with fp32
-// accumulators (AGPRs for the 128 x 128 wave tile), k-steps of 64.
+// accumulators. The tile is chosen per shape (choose_gemm_tile): 256 x 256
+// or 256 x 192 with 8 waves and one workgroup per CU for the large layer
+// products, 128 x 128 with 4 waves where there are too few large tiles to
+// fill the 256 CUs.
 //  - Operands go straight from HBM/L2 into LDS with buffer_load ... lds
 //    (no VGPR staging, no ds_write), bounds handled by the buffer descriptor
 //    (out-of-range chunks load as zeros).
-//  - LDS rows are 128 B with an XOR swizzle of the 16-byte chunks, so both
-//    the loads and the MFMA fragment reads are bank-conflict free.
-//  - Two LDS stages: the loads of k-step k+1 run while k-step k is
-//    multiplied; MFMA fragments are double-buffered across the 4 substeps.
+//  - LDS rows are XOR-swizzled 16-byte chunks, so both the loads and the
+//    MFMA fragment reads are bank-conflict free without padding.
+//  - k-steps of 64 through two LDS stages (the loads of k-step k+1 run
+//    while k-step k is multiplied), or of 32 through a ring of four;
+//    MFMA fragments are double-buffered across the substeps.
+//  - Workgroup ids are remapped per XCD and grouped by 4 tile-rows for L2
+//    reuse (tile_of).
 //  - The epilogue goes through a per-wave LDS patch so C is written with
 //    16-byte stores and the bias is added on the way.
 #include <atomic>
@@ -61,17 +67,7 @@ __device__ __forceinline__ void tile_of(int pid, int tiles_m, int tiles_n, int g
     tn = r / gm;
 }
 
-typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
-
-// Buffer resource (gfx9 raw buffer, stride 0): loads at byte offsets
-// >= num_records return zeros (for loads into LDS, zeros are written), which
-// gives branch-free bounds handling. kOOB is always out of range.
-constexpr uint32_t kOOB = 0x80000000u;
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
-    const int n = bytes <= 0 ? 0 : bytes >= 0x7fffffff ? 0x7fffffff : (int)bytes;
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, 0x00020000);
-}
 
 // LDS tile layout: rows of BK bf16 (2 BK bytes, no padding), CPR = BK/8
 // 16-byte chunks per row; chunk c of row r sits in slot
@@ -282,12 +278,20 @@ __attribute__((amdgpu_waves_per_eu(1, 2))) void gemm_bf16_kernel(GemmArgs g) {
         // Two stages: each tile starts with every wave waiting for its own
         // loads of the tile and a barrier (all loads visible, every wave done
         // with the previous tile); the next tile's loads then go out into the
-        // other stage, a part between each pair of MFMA substeps.
+        // other stage, front-loaded so that they have most of the tile to
+        // land: half of them before the first MFMA substep, a quarter after
+        // each of the first two substeps (issuing a part after every substep
+        // left the last part only one substep to land before the wait).
+        static_assert(KS == 4, "the two-stage schedule assumes four substeps per tile");
         if (nk > 0) issue_all(0);
         for (int kt = 0; kt < nk; ++kt) {
             wait_vmcnt<0>();
             __syncthreads();
             const uint16_t* st = smem + (kt & 1) * STAGE;
+            if (kt + 1 < nk) {
+                issue(kt + 1, (kt + 1) & 1, 0);
+                issue(kt + 1, (kt + 1) & 1, 1);
+            }
             load_frags(st, 0, 0);
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
@@ -298,7 +302,7 @@ __attribute__((amdgpu_waves_per_eu(1, 2))) void gemm_bf16_kernel(GemmArgs g) {
 #pragma unroll
                     for (int j = 0; j < TN; ++j)
                         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[cur][i], fb[cur][j], acc[i][j], 0, 0, 0);
-                if (kt + 1 < nk) issue(kt + 1, (kt + 1) & 1, ks);
+                if (ks < 2 && kt + 1 < nk) issue(kt + 1, (kt + 1) & 1, ks + 2);
             }
         }
     } else {

@@ -10,13 +10,20 @@ namespace mc {
 inline int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
 
 // ------------------------------------------------------ operand preparation
-// out[i][j] (bf16, rows_out x cols_out, ld = cols_out) = src element
+// One job: out[i][j] (bf16, rows_out x cols_out, ld = cols_out) = src element
 // (transpose ? src[j*ld_src + i] : src[i*ld_src + j]) for i < valid_rows,
 // j < valid_cols, else 0. With lo != nullptr the fp32 value v is split as
-// hi = bf16(v), lo = bf16(v - hi).
-hipError_t launch_prep_bf16(const float* src, int64_t ld_src, int64_t valid_rows, int64_t valid_cols,
-                            bool transpose, uint16_t* hi, uint16_t* lo, int64_t rows_out,
-                            int64_t cols_out, hipStream_t stream);
+// hi = bf16(v), lo = bf16(v - hi). A job with hi == nullptr is skipped.
+struct PrepJob {
+    const float* src;
+    int64_t ld_src, valid_rows, valid_cols;
+    bool transpose;
+    uint16_t* hi;
+    uint16_t* lo;
+    int64_t rows_out, cols_out;
+};
+// Both jobs in one launch.
+hipError_t launch_prep_bf16(const PrepJob& j0, const PrepJob& j1, hipStream_t stream);
 
 // ------------------------------------------------------- row projection
 // For t < T, j < r:  v = scale * sum_c X[t][c] * P[j][c]   (P = P_hi + P_lo)
@@ -31,16 +38,33 @@ hipError_t launch_rowproj_bf16(const uint16_t* X, int64_t T, int64_t C, const ui
                                hipStream_t stream);
 
 // ------------------------------------------------- column reduction (split T)
-// partial[s][j][c] = sum_{t in split s} Pt[j*T + t] * X[t][c] for j < r16, c < C
-// (j >= r contributes 0; r16 as for rowproj). X bf16 [T][C] (C % 8 == 0),
-// Pt fp32 [r][T].
+// One job: partial[s][j][c] = sum_{t in split s} Pt[j*T + t] * X[t][c] for
+// j < r16, c < C (j >= r contributes 0; r16 as for rowproj). X bf16 [T][C]
+// (C % 8 == 0), Pt fp32 [r][T]. A job with X == nullptr is skipped; both
+// jobs run in one launch per group of 32 ranks.
+struct ColJob {
+    const uint16_t* X;
+    int64_t C;
+    const float* Pt;
+    int splits;
+    float* partial;
+};
 int colreduce_splits(int64_t T, int64_t C);
-hipError_t launch_colreduce_bf16(const uint16_t* X, int64_t T, int64_t C, const float* Pt, int r,
-                                 int splits, float* partial, hipStream_t stream);
-// out = scale * sum_s partial[s][j][c] (s ascending) for j < r, c < C, written
-// to out[c*r + j] when transpose_out (dA [K][r]) else out[j*C + c] (dB [r][N]).
-hipError_t launch_split_sum(const float* partial, int splits, int r16, int r, int64_t C, float scale,
-                            bool transpose_out, float* out, hipStream_t stream);
+hipError_t launch_colreduce_bf16(int64_t T, int r, const ColJob& j0, const ColJob& j1, hipStream_t stream);
+// One job: out = scale * sum_s partial[s][j][c] (s ascending) for j < r,
+// c < C, written to out[c*r + j] when transpose_out (dA [K][r]) else
+// out[j*C + c] (dB [r][N]); part_stride = r16 * C. A job with out == nullptr
+// is skipped; both jobs run in one launch.
+struct SumJob {
+    const float* partial;
+    int splits;
+    int64_t C;
+    int64_t part_stride;
+    float scale;
+    bool transpose_out;
+    float* out;
+};
+hipError_t launch_split_sum(int r, const SumJob& j0, const SumJob& j1, hipStream_t stream);
 
 // -------------------------------------------------------------- GEMM bf16
 // C[M][N] = sum over two reduction segments of A_s . B_s^T (+ bias[n]), bf16

@@ -19,6 +19,9 @@
 //             groups. The fp32 Gd^T / Hd^T operand is split hi + lo as above.
 //             Tokens are split in a fixed partition; the partials are summed
 //             in split order by split_sum (deterministic, no atomics).
+//  All bf16 kernels load through buffer resources whose range checks zero
+//  the out-of-range rows and columns, so their loops have no branches and
+//  issue every load of an unrolled block before its MFMAs.
 //
 // fp32 variants (plain FMA) serve act_dtype == MC_F32.
 #include "common.hpp"
@@ -28,6 +31,9 @@ namespace mc {
 namespace {
 
 __device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+// Instruction classes of __builtin_amdgcn_sched_group_barrier.
+constexpr int kSchedMfma = 0x008, kSchedVmemRead = 0x020;
 
 __device__ __forceinline__ void split_hilo8(const float (&v)[8], uint4& hi, uint4& lo) {
     uint32_t h[4], l[4];
@@ -61,88 +67,118 @@ __device__ __forceinline__ void transpose8x8(const uint4 (&R)[8], uint4 (&O)[8])
 }
 
 // ------------------------------------------------------------------ prep
-__global__ __launch_bounds__(256) void prep_bf16(const float* __restrict__ src, int64_t ld_src,
-                                                 int64_t valid_rows, int64_t valid_cols, int transpose,
-                                                 uint16_t* __restrict__ hi, uint16_t* __restrict__ lo,
-                                                 int64_t rows_out, int64_t cols_out) {
-    const int64_t n = rows_out * cols_out;
+// Up to two operand-preparation jobs in one launch: threads [0, n0) do job 0,
+// the rest job 1.
+__device__ __forceinline__ void prep_one(const PrepJob& j, int64_t idx) {
+    const int64_t i = idx / j.cols_out, c = idx % j.cols_out;
+    float v = 0.f;
+    if (i < j.valid_rows && c < j.valid_cols) v = j.transpose ? j.src[c * j.ld_src + i] : j.src[i * j.ld_src + c];
+    const uint16_t h = f32_to_bf16(v);
+    j.hi[idx] = h;
+    if (j.lo) j.lo[idx] = f32_to_bf16(v - bf16_to_f32(h));
+}
+
+__global__ __launch_bounds__(256) void prep_bf16(PrepJob j0, PrepJob j1, int64_t n0, int64_t n) {
     for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < n;
          idx += (int64_t)gridDim.x * blockDim.x) {
-        const int64_t i = idx / cols_out, j = idx % cols_out;
-        float v = 0.f;
-        if (i < valid_rows && j < valid_cols) v = transpose ? src[j * ld_src + i] : src[i * ld_src + j];
-        const uint16_t h = f32_to_bf16(v);
-        hi[idx] = h;
-        if (lo) lo[idx] = f32_to_bf16(v - bf16_to_f32(h));
+        if (idx < n0) prep_one(j0, idx);
+        else prep_one(j1, idx - n0);
     }
 }
 
 // --------------------------------------------------------------- rowproj
-// Workgroup: 4 waves, 16 token rows. Wave w takes 32-column steps w, w+4, ...
-// (so the 4 waves read 4 adjacent 64-byte pieces of each row at once); their
-// accumulators are combined in wave order through LDS.
-template <int RC>
+// Workgroup: 4 waves, 16 RT token rows (RT MFMA row tiles). Wave w takes the
+// 64-column steps w, w+4, ...; in a step, lane l (row l % 16 of each row
+// tile, group g = l / 16) loads the 16 contiguous columns 64 s + 16 g .. +15
+// of x and of the parameter rows (32 bytes per lane, whole 128-byte lines per
+// wave) and feeds them to two MFMA 16x16x32 as k-chunks (columns 0-7, then
+// 8-15 of its 16): the k order inside a step is permuted identically for x
+// and P, so the sum over columns is unchanged. The parameter fragments are
+// shared by the RT row tiles. All loads of U steps are issued before their
+// MFMAs, through buffer loads whose range check zeroes rows past T and
+// columns past C (no branches). The 4 waves' partial sums are combined in
+// wave order through LDS.
+template <int RC, int RT, int U>
 __global__ __launch_bounds__(256) void rowproj_bf16(const uint16_t* __restrict__ X, int64_t T, int64_t C,
                                                     const uint16_t* __restrict__ Phi,
                                                     const uint16_t* __restrict__ Plo, int r, float scale,
                                                     const uint8_t* __restrict__ mask, float keep,
                                                     float* __restrict__ out_t, uint16_t* __restrict__ out_ext,
                                                     int rext, float ext_scale) {
+    constexpr int ROWS = 16 * RT;
     const int lane = lane_id();
     const int wave = threadIdx.x >> 6;
-    const int64_t t0 = (int64_t)blockIdx.x * 16;
-    const int64_t trow = t0 + (lane & 15);
-    const bool row_ok = trow < T;
-    const int kgrp = (lane >> 4) * 8;
-    const uint16_t* xrow = X + (row_ok ? trow : 0) * C + kgrp;
-    const int64_t nsteps = (C + 31) / 32;
+    const int64_t t0 = (int64_t)blockIdx.x * ROWS;
+    const int64_t nrows = T - t0 < ROWS ? T - t0 : ROWS;
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(X + t0 * C, nrows * C * 2);
+    const __amdgpu_buffer_rsrc_t rhi = make_rsrc(Phi, (int64_t)16 * RC * C * 2);
+    const __amdgpu_buffer_rsrc_t rlo = make_rsrc(Plo, (int64_t)16 * RC * C * 2);
+    const int row = lane & 15, grp = lane >> 4;
+    const int64_t nsteps = (C + 63) / 64;
 
-    f32x4 acc[RC];
+    f32x4 acc[RT][RC];
 #pragma unroll
-    for (int rc = 0; rc < RC; ++rc) acc[rc] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int rc = 0; rc < RC; ++rc) acc[rt][rc] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    constexpr int U = 4;
     for (int64_t s0 = wave; s0 < nsteps; s0 += 4 * U) {
-        uint4 xa[U];
+        i32x4 xv[U][RT][2], ph[U][RC][2], pl[U][RC][2];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int64_t s = s0 + 4 * u;
-            const int64_t c = s * 32 + kgrp;
-            xa[u] = load16(xrow, s * 32, row_ok && s < nsteps && c < C);
-        }
+            const int64_t c = (s0 + 4 * u) * 64 + grp * 16;
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int64_t s = s0 + 4 * u;
-            if (s < nsteps) {
-                const int64_t c = s * 32 + kgrp;
-                const bool c_ok = c < C;
+            for (int h = 0; h < 2; ++h) {
+                const bool ok = c + 8 * h < C;
+#pragma unroll
+                for (int rt = 0; rt < RT; ++rt)
+                    xv[u][rt][h] = buf_load16(rx, ok ? (uint32_t)(((int64_t)(rt * 16 + row) * C + c + 8 * h) * 2) : kOOB);
 #pragma unroll
                 for (int rc = 0; rc < RC; ++rc) {
-                    const int64_t prow = (int64_t)(rc * 16 + (lane & 15)) * C + c;
-                    const uint4 ph = load16(Phi, prow, c_ok);
-                    const uint4 pl = load16(Plo, prow, c_ok);
-                    acc[rc] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(xa[u]), as_bf16x8(ph), acc[rc], 0, 0, 0);
-                    acc[rc] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(xa[u]), as_bf16x8(pl), acc[rc], 0, 0, 0);
+                    const uint32_t off = ok ? (uint32_t)(((int64_t)(rc * 16 + row) * C + c + 8 * h) * 2) : kOOB;
+                    ph[u][rc][h] = buf_load16(rhi, off);
+                    pl[u][rc][h] = buf_load16(rlo, off);
                 }
             }
         }
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+                    for (int rc = 0; rc < RC; ++rc) {
+                        const bf16x8 xa = __builtin_bit_cast(bf16x8, xv[u][rt][h]);
+                        acc[rt][rc] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                            xa, __builtin_bit_cast(bf16x8, ph[u][rc][h]), acc[rt][rc], 0, 0, 0);
+                        acc[rt][rc] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                            xa, __builtin_bit_cast(bf16x8, pl[u][rc][h]), acc[rt][rc], 0, 0, 0);
+                    }
+        // keep every load of the block ahead of its MFMAs (the scheduler
+        // would otherwise sink each load next to its use to save registers,
+        // exposing one memory latency per MFMA pair)
+        __builtin_amdgcn_sched_group_barrier(kSchedVmemRead, U * 2 * (RT + 2 * RC), 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, U * 4 * RT * RC, 0);
     }
 
-    // combine the 4 waves: [wave][rc][q][lane]
-    __shared__ float red[4][RC][4][64];
+    // combine the 4 waves: [wave][rt][rc][q][lane]; accumulator q of lane l
+    // is token 4 (l / 16) + q of its row tile, rank index l % 16.
+    __shared__ float red[4][RT][RC][4][64];
 #pragma unroll
-    for (int rc = 0; rc < RC; ++rc)
+    for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) red[wave][rc][q][lane] = acc[rc][q];
+        for (int rc = 0; rc < RC; ++rc)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) red[wave][rt][rc][q][lane] = acc[rt][rc][q];
     __syncthreads();
-    // every thread finalises (rc, q) entries: 64*4*RC values over 256 threads
-    for (int idx = threadIdx.x; idx < RC * 4 * 64; idx += 256) {
-        const int l = idx & 63, q = (idx >> 6) & 3, rc = idx >> 8;
-        float v = red[0][rc][q][l];
+    for (int idx = threadIdx.x; idx < RT * RC * 4 * 64; idx += 256) {
+        const int l = idx & 63, q = (idx >> 6) & 3, rc = (idx >> 8) % RC, rt = (idx >> 8) / RC;
+        float v = red[0][rt][rc][q][l];
 #pragma unroll
-        for (int w = 1; w < 4; ++w) v += red[w][rc][q][l];
+        for (int w = 1; w < 4; ++w) v += red[w][rt][rc][q][l];
         const int j = rc * 16 + (l & 15);
-        const int64_t t = t0 + (l >> 4) * 4 + q;
+        const int64_t t = t0 + rt * 16 + (l >> 4) * 4 + q;
         if (t >= T) continue;
         if (j < r) {
             v *= scale;
@@ -156,22 +192,43 @@ __global__ __launch_bounds__(256) void rowproj_bf16(const uint16_t* __restrict__
 }
 
 // ------------------------------------------------------------- colreduce
-// Workgroup: 4 waves, 128 columns, token range of split blockIdx.y. Wave w
-// takes 32-row steps w, w+4, ... of the range. Lane l loads rows
-// t0 + 8*(l/16) + 0..7 at columns c0 + 8*(l%16) + 0..7.
-template <int RC>
-__global__ __launch_bounds__(256) void colreduce_bf16(const uint16_t* __restrict__ X, int64_t T, int64_t C,
-                                                      const float* __restrict__ Pt, int r, int64_t chunk,
-                                                      float* __restrict__ partial, int64_t part_stride) {
+// Up to two column-reduction jobs in one launch (blocks [0, nblk0) job 0).
+// Workgroup: 4 waves, 128 columns, the token range of one split. Wave w takes
+// 32-row steps w, w+4, ... of the range; lane l loads rows t0 + 8 (l/16) + i
+// (i < 8) at columns c0 + 8 (l%16) .. +7 (256 contiguous bytes per row and
+// wave), transposes the 8 x 8 block in registers and feeds the 8 columns to
+// 8 MFMAs whose 16 output columns are the lanes' 16 column groups. Loads of
+// U steps are issued ahead of their MFMAs; buffer range checks zero rows
+// past the split and columns past C.
+struct ColJobDev {
+    const uint16_t* X;
+    int64_t C;
+    const float* Pt;
+    int64_t chunk;
+    float* partial;
+    int64_t part_stride;
+    int ctiles;
+};
+
+template <int RC, int U, bool PTV>
+__global__ __launch_bounds__(256) void colreduce_bf16(int64_t T, int r, ColJobDev j0, ColJobDev j1, int nblk0) {
+    const bool second = (int)blockIdx.x >= nblk0;
+    const int b = second ? (int)blockIdx.x - nblk0 : (int)blockIdx.x;
+    const uint16_t* X = second ? j1.X : j0.X;
+    const int64_t C = second ? j1.C : j0.C;
+    const float* Pt = second ? j1.Pt : j0.Pt;
+    const int64_t chunk = second ? j1.chunk : j0.chunk;
+    const int ctiles = second ? j1.ctiles : j0.ctiles;
     const int lane = lane_id();
     const int wave = threadIdx.x >> 6;
-    const int64_t c0 = (int64_t)blockIdx.x * 128;
-    const int64_t tb = (int64_t)blockIdx.y * chunk;
+    const int64_t c0 = (int64_t)(b % ctiles) * 128;
+    const int64_t tb = (int64_t)(b / ctiles) * chunk;
     const int64_t te = tb + chunk < T ? tb + chunk : T;
     const int64_t col = c0 + 8 * (lane & 15);
     const bool col_ok = col < C;
     const int g8 = 8 * (lane >> 4);
-    const bool pt_vec = (T & 3) == 0;
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(X + tb * C, (te - tb) * C * 2);
+    const __amdgpu_buffer_rsrc_t rp = make_rsrc(Pt, (int64_t)r * T * 4);
 
     f32x4 acc[8][RC];
 #pragma unroll
@@ -179,38 +236,62 @@ __global__ __launch_bounds__(256) void colreduce_bf16(const uint16_t* __restrict
 #pragma unroll
         for (int rc = 0; rc < RC; ++rc) acc[e][rc] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    for (int64_t t0 = tb + 32 * wave; t0 < te; t0 += 128) {
-        uint4 R[8];
+    for (int64_t s0 = tb + 32 * wave; s0 < te; s0 += 128 * U) {
+        uint4 R[U][8];
+        float pv[U][RC][8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int64_t t = t0 + g8 + i;
-            R[i] = load16(X, t * C + col, col_ok && t < te);
-        }
-        uint4 ahi[RC], alo[RC];
+        for (int u = 0; u < U; ++u) {
+            const int64_t t0 = s0 + 128 * u;
 #pragma unroll
-        for (int rc = 0; rc < RC; ++rc) {
-            const int j = rc * 16 + (lane & 15);
-            float v[8];
-            const int64_t t = t0 + g8;
-            if (j < r && t + 8 <= te && pt_vec) {
-                const float4 a = *reinterpret_cast<const float4*>(Pt + (int64_t)j * T + t);
-                const float4 b = *reinterpret_cast<const float4*>(Pt + (int64_t)j * T + t + 4);
-                v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-            } else {
-#pragma unroll
-                for (int e = 0; e < 8; ++e) v[e] = (j < r && t + e < te) ? Pt[(int64_t)j * T + t + e] : 0.f;
+            for (int i = 0; i < 8; ++i) {
+                const int64_t t = t0 + g8 + i - tb;
+                const i32x4 v = buf_load16(rx, col_ok ? (uint32_t)((t * C + col) * 2) : kOOB);
+                R[u][i] = __builtin_bit_cast(uint4, v);
             }
-            split_hilo8(v, ahi[rc], alo[rc]);
-        }
-        uint4 Bt[8];
-        transpose8x8(R, Bt);
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
 #pragma unroll
             for (int rc = 0; rc < RC; ++rc) {
-                acc[e][rc] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ahi[rc]), as_bf16x8(Bt[e]), acc[e][rc], 0, 0, 0);
-                acc[e][rc] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(alo[rc]), as_bf16x8(Bt[e]), acc[e][rc], 0, 0, 0);
+                const int j = rc * 16 + (lane & 15);
+                const int64_t t = t0 + g8;
+                if constexpr (PTV) {  // T % 4 == 0: 16-byte aligned rows of Pt
+                    const uint32_t off = (uint32_t)(((int64_t)j * T + t) * 4);
+                    const i32x4 a = buf_load16(rp, off), bq = buf_load16(rp, off + 16);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        pv[u][rc][e] = __int_as_float(a[e]);
+                        pv[u][rc][4 + e] = __int_as_float(bq[e]);
+                    }
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e)
+                        pv[u][rc][e] = __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+                            rp, (int)(((int64_t)j * T + t + e) * 4), 0, 0));
+                }
             }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            uint4 ahi[RC], alo[RC];
+#pragma unroll
+            for (int rc = 0; rc < RC; ++rc) {
+                // tokens past the range: x is zero there, and Pt is zeroed so
+                // that a non-finite value of another token cannot leak in
+                float v[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[e] = (s0 + 128 * u + g8 + e < te) ? pv[u][rc][e] : 0.f;
+                split_hilo8(v, ahi[rc], alo[rc]);
+            }
+            uint4 Bt[8];
+            transpose8x8(R[u], Bt);
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+#pragma unroll
+                for (int rc = 0; rc < RC; ++rc) {
+                    acc[e][rc] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ahi[rc]), as_bf16x8(Bt[e]), acc[e][rc], 0, 0, 0);
+                    acc[e][rc] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(alo[rc]), as_bf16x8(Bt[e]), acc[e][rc], 0, 0, 0);
+                }
+        }
+        // every load of the block first (see rowproj_bf16)
+        __builtin_amdgcn_sched_group_barrier(kSchedVmemRead, U * (8 + (PTV ? 2 : 8) * RC), 0);
     }
 
     // combine waves in order 0,1,2,3 through one LDS staging buffer
@@ -235,12 +316,11 @@ __global__ __launch_bounds__(256) void colreduce_bf16(const uint16_t* __restrict
         }
         __syncthreads();
     }
-    if (wave == 0) {
-        float* out = partial + (int64_t)blockIdx.y * part_stride;
+    if (wave == 0 && col_ok) {
+        float* out = (second ? j1.partial : j0.partial) + (int64_t)(b / ctiles) * (second ? j1.part_stride : j0.part_stride);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             const int64_t c = col + e;
-            if (!col_ok) continue;
 #pragma unroll
             for (int rc = 0; rc < RC; ++rc)
 #pragma unroll
@@ -252,18 +332,33 @@ __global__ __launch_bounds__(256) void colreduce_bf16(const uint16_t* __restrict
     }
 }
 
-__global__ __launch_bounds__(256) void split_sum(const float* __restrict__ partial, int splits, int r16, int r,
-                                                 int64_t C, float scale, int transpose_out,
-                                                 float* __restrict__ out) {
-    const int64_t n = (int64_t)r * C;
+// out = scale * sum_s partial[s][j][c] (s ascending) for up to two jobs
+// (threads [0, n0) job 0). Splits are unrolled by 8 so that their loads are
+// in flight together; the adds stay in split order.
+__device__ __forceinline__ void split_sum_one(const SumJob& J, int r, int64_t idx) {
+    const int64_t j = idx / J.C, c = idx % J.C;
+    const float* p = J.partial + j * J.C + c;
+    const int64_t stride = J.part_stride;
+    float s = 0.f;
+    int k = 0;
+    for (; k + 8 <= J.splits; k += 8) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = p[(int64_t)(k + u) * stride];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) s += v[u];
+    }
+    for (; k < J.splits; ++k) s += p[(int64_t)k * stride];
+    s *= J.scale;
+    if (J.transpose_out) J.out[c * r + j] = s;
+    else J.out[j * J.C + c] = s;
+}
+
+__global__ __launch_bounds__(256) void split_sum(int r, SumJob j0, SumJob j1, int64_t n0, int64_t n) {
     for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < n;
          idx += (int64_t)gridDim.x * blockDim.x) {
-        const int64_t j = idx / C, c = idx % C;
-        float s = 0.f;
-        for (int k = 0; k < splits; ++k) s += partial[((int64_t)k * r16 + j) * C + c];
-        s *= scale;
-        if (transpose_out) out[c * r + j] = s;
-        else out[j * C + c] = s;
+        if (idx < n0) split_sum_one(j0, r, idx);
+        else split_sum_one(j1, r, idx - n0);
     }
 }
 
@@ -337,15 +432,13 @@ __global__ __launch_bounds__(256) void colreduce_f32(const float* __restrict__ X
 
 }  // namespace
 
-hipError_t launch_prep_bf16(const float* src, int64_t ld_src, int64_t valid_rows, int64_t valid_cols,
-                            bool transpose, uint16_t* hi, uint16_t* lo, int64_t rows_out,
-                            int64_t cols_out, hipStream_t stream) {
-    const int64_t n = rows_out * cols_out;
+hipError_t launch_prep_bf16(const PrepJob& j0, const PrepJob& j1, hipStream_t stream) {
+    const int64_t n0 = j0.hi ? j0.rows_out * j0.cols_out : 0;
+    const int64_t n = n0 + (j1.hi ? j1.rows_out * j1.cols_out : 0);
+    if (n == 0) return hipSuccess;
     int64_t blocks = (n + 255) / 256;
     if (blocks > 4096) blocks = 4096;
-    if (blocks < 1) blocks = 1;
-    prep_bf16<<<dim3((unsigned)blocks), 256, 0, stream>>>(src, ld_src, valid_rows, valid_cols, transpose ? 1 : 0,
-                                                          hi, lo, rows_out, cols_out);
+    prep_bf16<<<dim3((unsigned)blocks), 256, 0, stream>>>(j0, j1, n0, n);
     return hipGetLastError();
 }
 
@@ -353,14 +446,15 @@ hipError_t launch_rowproj_bf16(const uint16_t* X, int64_t T, int64_t C, const ui
                                const uint16_t* P_lo, int r, float scale, const uint8_t* mask,
                                float keep, float* out_t, uint16_t* out_ext, int rext, float ext_scale,
                                hipStream_t stream) {
-    const dim3 grid((unsigned)((T + 15) / 16));
-    // P_hi / P_lo hold r16 = 16, 32, 64 or 128 rows (zero past r)
+    // 32 token rows per workgroup (two MFMA row tiles share each parameter
+    // fragment); P_hi / P_lo hold r16 = 16, 32, 64 or 128 rows (zero past r).
+    const dim3 grid((unsigned)((T + 31) / 32));
     const int rc = r <= 16 ? 1 : r <= 32 ? 2 : r <= 64 ? 4 : 8;
     switch (rc) {
-        case 1: rowproj_bf16<1><<<grid, 256, 0, stream>>>(X, T, C, P_hi, P_lo, r, scale, mask, keep, out_t, out_ext, rext, ext_scale); break;
-        case 2: rowproj_bf16<2><<<grid, 256, 0, stream>>>(X, T, C, P_hi, P_lo, r, scale, mask, keep, out_t, out_ext, rext, ext_scale); break;
-        case 4: rowproj_bf16<4><<<grid, 256, 0, stream>>>(X, T, C, P_hi, P_lo, r, scale, mask, keep, out_t, out_ext, rext, ext_scale); break;
-        default: rowproj_bf16<8><<<grid, 256, 0, stream>>>(X, T, C, P_hi, P_lo, r, scale, mask, keep, out_t, out_ext, rext, ext_scale); break;
+        case 1: rowproj_bf16<1, 2, 2><<<grid, 256, 0, stream>>>(X, T, C, P_hi, P_lo, r, scale, mask, keep, out_t, out_ext, rext, ext_scale); break;
+        case 2: rowproj_bf16<2, 2, 1><<<grid, 256, 0, stream>>>(X, T, C, P_hi, P_lo, r, scale, mask, keep, out_t, out_ext, rext, ext_scale); break;
+        case 4: rowproj_bf16<4, 2, 1><<<grid, 256, 0, stream>>>(X, T, C, P_hi, P_lo, r, scale, mask, keep, out_t, out_ext, rext, ext_scale); break;
+        default: rowproj_bf16<8, 2, 1><<<grid, 256, 0, stream>>>(X, T, C, P_hi, P_lo, r, scale, mask, keep, out_t, out_ext, rext, ext_scale); break;
     }
     return hipGetLastError();
 }
@@ -376,34 +470,50 @@ int colreduce_splits(int64_t T, int64_t C) {
     return (int)s;
 }
 
-hipError_t launch_colreduce_bf16(const uint16_t* X, int64_t T, int64_t C, const float* Pt, int r,
-                                 int splits, float* partial, hipStream_t stream) {
+hipError_t launch_colreduce_bf16(int64_t T, int r, const ColJob& a, const ColJob& b, hipStream_t stream) {
     // Rank tiles are processed 32 at a time (accumulators and the LDS combine
     // buffer are sized for two 16-row MFMA tiles); each group re-reads X.
-    const int64_t chunk = round_up((T + splits - 1) / splits, 32);
-    const dim3 grid((unsigned)((C + 127) / 128), (unsigned)splits);
-    const int64_t part_stride = (int64_t)(r <= 16 ? 16 : r <= 32 ? 32 : r <= 64 ? 64 : 128) * C;
+    const int r16 = r <= 16 ? 16 : r <= 32 ? 32 : r <= 64 ? 64 : 128;
     for (int g = 0; g * 32 < r; ++g) {
         const int rs = r - 32 * g < 32 ? r - 32 * g : 32;
-        const float* pt = Pt + (int64_t)32 * g * T;
-        float* part = partial + (int64_t)32 * g * C;
-        if (rs <= 16)
-            colreduce_bf16<1><<<grid, 256, 0, stream>>>(X, T, C, pt, rs, chunk, part, part_stride);
-        else
-            colreduce_bf16<2><<<grid, 256, 0, stream>>>(X, T, C, pt, rs, chunk, part, part_stride);
+        ColJobDev d[2];
+        int nblk[2] = {0, 0};
+        const ColJob* jobs[2] = {&a, &b};
+        for (int i = 0; i < 2; ++i) {
+            const ColJob& J = *jobs[i];
+            d[i] = ColJobDev{J.X, J.C, J.Pt ? J.Pt + (int64_t)32 * g * T : nullptr, 0,
+                             J.partial ? J.partial + (int64_t)32 * g * J.C : nullptr, (int64_t)r16 * J.C,
+                             (int)((J.C + 127) / 128)};
+            if (!J.X) continue;
+            d[i].chunk = round_up((T + J.splits - 1) / J.splits, 32);
+            nblk[i] = d[i].ctiles * J.splits;
+        }
+        if (nblk[0] + nblk[1] == 0) return hipSuccess;
+        if (nblk[0] == 0) { d[0] = d[1]; nblk[0] = nblk[1]; nblk[1] = 0; }
+        const dim3 grid((unsigned)(nblk[0] + nblk[1]));
+        const bool ptv = (T & 3) == 0;
+        if (rs <= 16) {
+            if (ptv) colreduce_bf16<1, 2, true><<<grid, 256, 0, stream>>>(T, rs, d[0], d[1], nblk[0]);
+            else colreduce_bf16<1, 2, false><<<grid, 256, 0, stream>>>(T, rs, d[0], d[1], nblk[0]);
+        } else {
+            if (ptv) colreduce_bf16<2, 1, true><<<grid, 256, 0, stream>>>(T, rs, d[0], d[1], nblk[0]);
+            else colreduce_bf16<2, 1, false><<<grid, 256, 0, stream>>>(T, rs, d[0], d[1], nblk[0]);
+        }
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
     return hipSuccess;
 }
 
-hipError_t launch_split_sum(const float* partial, int splits, int r16, int r, int64_t C, float scale,
-                            bool transpose_out, float* out, hipStream_t stream) {
-    const int64_t n = (int64_t)r * C;
+hipError_t launch_split_sum(int r, const SumJob& a, const SumJob& b, hipStream_t stream) {
+    SumJob j0 = a, j1 = b;
+    if (!j0.out) { j0 = j1; j1.out = nullptr; }
+    const int64_t n0 = j0.out ? (int64_t)r * j0.C : 0;
+    const int64_t n = n0 + (j1.out ? (int64_t)r * j1.C : 0);
+    if (n == 0) return hipSuccess;
     int64_t blocks = (n + 255) / 256;
     if (blocks > 4096) blocks = 4096;
-    split_sum<<<dim3((unsigned)blocks), 256, 0, stream>>>(partial, splits, r16, r, C, scale,
-                                                          transpose_out ? 1 : 0, out);
+    split_sum<<<dim3((unsigned)blocks), 256, 0, stream>>>(r, j0, j1, n0, n);
     return hipGetLastError();
 }
 
