@@ -126,7 +126,7 @@ __global__ __launch_bounds__(256) void rowproj_bf16(const uint16_t* __restrict__
         i32x4 xv[U][RT][2], ph[U][RC][2], pl[U][RC][2];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int64_t c = (s0 + 4 * u) * 64 + grp * 16;
+            const int64_t c = (s0 + 4 * u) * 64 + grp * 16;  // steps past the end load zeros
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
                 const bool ok = c + 8 * h < C;
@@ -446,15 +446,19 @@ hipError_t launch_rowproj_bf16(const uint16_t* X, int64_t T, int64_t C, const ui
                                const uint16_t* P_lo, int r, float scale, const uint8_t* mask,
                                float keep, float* out_t, uint16_t* out_ext, int rext, float ext_scale,
                                hipStream_t stream) {
-    // 32 token rows per workgroup (two MFMA row tiles share each parameter
-    // fragment); P_hi / P_lo hold r16 = 16, 32, 64 or 128 rows (zero past r).
-    const dim3 grid((unsigned)((T + 31) / 32));
+    // 64 token rows per workgroup: four MFMA row tiles share each parameter
+    // fragment (measured at the c4 shapes, loading the fragments costs as
+    // much per byte as streaming x, so the rows per fragment set the speed;
+    // 16 or 32 rows per workgroup ran at 2.7 / 3.6 TB/s, 64 at 4.9 TB/s for
+    // x [16384, 8960]). Rank 128 keeps 32 rows (register budget).
+    // P_hi / P_lo hold r16 = 16, 32, 64 or 128 rows (zero past r).
     const int rc = r <= 16 ? 1 : r <= 32 ? 2 : r <= 64 ? 4 : 8;
+    const dim3 g64((unsigned)((T + 63) / 64)), g32((unsigned)((T + 31) / 32));
     switch (rc) {
-        case 1: rowproj_bf16<1, 2, 2><<<grid, 256, 0, stream>>>(X, T, C, P_hi, P_lo, r, scale, mask, keep, out_t, out_ext, rext, ext_scale); break;
-        case 2: rowproj_bf16<2, 2, 1><<<grid, 256, 0, stream>>>(X, T, C, P_hi, P_lo, r, scale, mask, keep, out_t, out_ext, rext, ext_scale); break;
-        case 4: rowproj_bf16<4, 2, 1><<<grid, 256, 0, stream>>>(X, T, C, P_hi, P_lo, r, scale, mask, keep, out_t, out_ext, rext, ext_scale); break;
-        default: rowproj_bf16<8, 2, 1><<<grid, 256, 0, stream>>>(X, T, C, P_hi, P_lo, r, scale, mask, keep, out_t, out_ext, rext, ext_scale); break;
+        case 1: rowproj_bf16<1, 4, 1><<<g64, 256, 0, stream>>>(X, T, C, P_hi, P_lo, r, scale, mask, keep, out_t, out_ext, rext, ext_scale); break;
+        case 2: rowproj_bf16<2, 4, 1><<<g64, 256, 0, stream>>>(X, T, C, P_hi, P_lo, r, scale, mask, keep, out_t, out_ext, rext, ext_scale); break;
+        case 4: rowproj_bf16<4, 4, 1><<<g64, 256, 0, stream>>>(X, T, C, P_hi, P_lo, r, scale, mask, keep, out_t, out_ext, rext, ext_scale); break;
+        default: rowproj_bf16<8, 2, 1><<<g32, 256, 0, stream>>>(X, T, C, P_hi, P_lo, r, scale, mask, keep, out_t, out_ext, rext, ext_scale); break;
     }
     return hipGetLastError();
 }
