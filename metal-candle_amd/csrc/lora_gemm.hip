@@ -23,8 +23,8 @@
 //  - LDS rows are XOR-swizzled 16-byte chunks, so both the loads and the
 //    MFMA fragment reads are bank-conflict free without padding.
 //  - k-steps of 64 through two LDS stages (the loads of k-step k+1 run
-//    while k-step k is multiplied), or of 32 through a ring of four;
-//    MFMA fragments are double-buffered across the substeps.
+//    while k-step k is multiplied) or a ring of three; MFMA fragments are
+//    double-buffered across the substeps.
 //  - Workgroup ids are remapped per XCD and grouped by 4 tile-rows for L2
 //    reuse (tile_of).
 //  - The epilogue goes through a per-wave LDS patch so C is written with
@@ -431,16 +431,21 @@ int cu_count() {
 }
 }  // namespace
 
-GemmTile choose_gemm_tile(int64_t M, int64_t N, int cus) {
+GemmTile choose_gemm_tile(int64_t M, int64_t N, int64_t K, int cus) {
     // Estimated time = rounds of one-workgroup-per-CU tiles x work per tile
-    // / relative per-tile throughput (measured on MI355X at the Qwen2.5 layer
-    // shapes): 256 x 256 with 8 waves is the fastest per FLOP, 256 x 192
-    // fills two rounds exactly where N = 1536 (384 tiles of 256 x 256 would
-    // take two rounds at 75%), 128 x 128 keeps small problems spread over
-    // every CU.
+    // / relative per-tile throughput, measured on MI355X at the Qwen2.5
+    // layer shapes:
+    //  - 256 x 256 (8 waves, 2 stages) is the fastest per FLOP at K ~ 1.5k;
+    //  - 256 x 192 fills two rounds exactly where N = 1536 (384 tiles of
+    //    256 x 256 would take two rounds at 75%);
+    //  - 256 x 128 with a 3-stage ring is fastest on long reductions
+    //    (K = 8960: 1050 vs 1010 / 950 TFLOP/s), slower at K ~ 1.5k;
+    //  - 128 x 128 (4 waves, 3 stages) keeps small problems on every CU.
+    const double s128 = K >= 4096 ? 1.08 : 0.9;
     struct Cand { GemmTile t; int bm, bn; double speed; };
     const Cand cands[] = {{GemmTile::k256x256, 256, 256, 1.0},
                           {GemmTile::k256x192, 256, 192, 0.95},
+                          {GemmTile::k256x128, 256, 128, s128},
                           {GemmTile::k128x128, 128, 128, 0.8}};
     GemmTile best = GemmTile::k128x128;
     double best_t = 1e300;
@@ -455,13 +460,15 @@ GemmTile choose_gemm_tile(int64_t M, int64_t N, int cus) {
 
 hipError_t launch_gemm_bf16(int64_t M, int64_t N, GemmSeg s0, GemmSeg s1, const uint16_t* bias, uint16_t* c,
                             int64_t ldc, hipStream_t stream) {
-    switch (choose_gemm_tile(M, N, cu_count())) {
+    switch (choose_gemm_tile(M, N, s0.k + s1.k, cu_count())) {
         case GemmTile::k256x256:  // 8 waves of 128 x 64, k-steps of 64, 2 stages (128 KB LDS)
             return launch_cfg<256, 256, 128, 64, 64, 2>(M, N, s0, s1, bias, c, ldc, stream, 4);
         case GemmTile::k256x192:  // 8 waves of 64 x 96, 2 stages (112 KB LDS)
             return launch_cfg<256, 192, 64, 96, 64, 2>(M, N, s0, s1, bias, c, ldc, stream, 4);
-        default:                  // 4 waves of 64 x 64, k-steps of 32, 4 stages (64 KB LDS)
-            return launch_cfg<128, 128, 64, 64, 32, 4>(M, N, s0, s1, bias, c, ldc, stream, 4);
+        case GemmTile::k256x128:  // 8 waves of 64 x 64, 3 stages (144 KB LDS)
+            return launch_cfg<256, 128, 64, 64, 64, 3>(M, N, s0, s1, bias, c, ldc, stream, 4);
+        default:                  // 4 waves of 64 x 64, 3 stages (96 KB LDS)
+            return launch_cfg<128, 128, 64, 64, 64, 3>(M, N, s0, s1, bias, c, ldc, stream, 4);
     }
 }
 

@@ -79,9 +79,10 @@ struct GemmSeg {
 };
 hipError_t launch_gemm_bf16(int64_t M, int64_t N, GemmSeg s0, GemmSeg s1, const uint16_t* bias, uint16_t* c,
                             int64_t ldc, hipStream_t stream);
-// Workgroup tile the bf16 GEMM uses for an M x N output on `cus` compute units.
-enum class GemmTile { k256x256, k256x192, k128x128 };
-GemmTile choose_gemm_tile(int64_t M, int64_t N, int cus);
+// Workgroup tile the bf16 GEMM uses for an M x N output with reduction
+// length K on `cus` compute units.
+enum class GemmTile { k256x256, k256x192, k256x128, k128x128 };
+GemmTile choose_gemm_tile(int64_t M, int64_t N, int64_t K, int cus);
 // out[c][r] = in[r][c] for a bf16 rows x cols matrix (cols, rows % 8 == 0).
 hipError_t launch_transpose_bf16(const uint16_t* in, int64_t rows, int64_t cols, uint16_t* out,
                                  hipStream_t stream);
