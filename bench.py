@@ -32,6 +32,12 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+# HBM bytes per gemm_bf16_kernel launch (average over a step's launches),
+# measured with two rocprofv3 --pmc passes (FETCH_SIZE, then WRITE_SIZE)
+# scaled by the same counters on a 256 MiB copy (--copy-calibration); the
+# summary and commands are in profiles/gemm_bf16_kernel_c4_hbm_traffic.md.
+# Re-measured whenever the GEMM's tiling changes; None for unmeasured configs.
+GEMM_TRAFFIC_BYTES = {"c4": 515.5e6}
 BF16_PEAK_TFLOPS = 2500.0
 FP32_PEAK_TFLOPS = 157.3
 
@@ -217,6 +223,9 @@ def main():
     ap.add_argument("--config", default="c4", choices=sorted(CONFIGS))
     ap.add_argument("--cpu-tokens", type=int, default=2048, help="token sample of the CPU-oracle baseline")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
+                    help="run one plain device copy of BYTES before the steps (a kernel of known HBM traffic "
+                         "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (every box in this setup has one); --gpus {args.gpus} "
@@ -231,6 +240,13 @@ def main():
     dev = torch.device("cuda:0")
     c = CONFIGS[args.config]
     layer = Layer(mc, c, dev)
+    if args.copy_calibration > 0:
+        src = torch.empty(args.copy_calibration // 2, dtype=torch.bfloat16, device=dev).fill_(1.0)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     for _ in range(args.warmup):
         layer.step()
     torch.cuda.synchronize()
@@ -287,7 +303,7 @@ def main():
             "peak": BF16_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": achieved / BF16_PEAK_TFLOPS,
-            "traffic": None,
+            "traffic": GEMM_TRAFFIC_BYTES.get(args.config),
         },
         "layer_TFLOP_s": (base_fl + low_fl) / (ms_step * 1e-3) / 1e12,
         "kernels": kernels,
