@@ -116,6 +116,46 @@ __device__ __forceinline__ i32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t o
     return __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
 }
 
+// 16-byte vectors of T (4 floats or 8 bf16) at a byte offset of a buffer
+// resource, converted to / from fp32. Out-of-range offsets load zeros and
+// drop the store, so callers select offsets instead of branching.
+template <typename T> struct BVec;
+template <> struct BVec<float> {
+    static constexpr int N = 4;
+    static __device__ __forceinline__ void unpack(const i32x4& q, float (&v)[4]) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = __int_as_float(q[e]);
+    }
+    static __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t r, uint32_t off, float (&v)[4]) {
+        unpack(buf_load16(r, off), v);
+    }
+    static __device__ __forceinline__ void store(__amdgpu_buffer_rsrc_t r, uint32_t off, const float (&v)[4]) {
+        const i32x4 q = {__float_as_int(v[0]), __float_as_int(v[1]), __float_as_int(v[2]), __float_as_int(v[3])};
+        __builtin_amdgcn_raw_buffer_store_b128(q, r, (int)off, 0, 0);
+    }
+};
+template <> struct BVec<uint16_t> {
+    static constexpr int N = 8;
+    static __device__ __forceinline__ void unpack(const i32x4& q, float (&v)[8]) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            v[2 * e] = bf16_lo((uint32_t)q[e]);
+            v[2 * e + 1] = bf16_hi((uint32_t)q[e]);
+        }
+    }
+    static __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t r, uint32_t off, float (&v)[8]) {
+        unpack(buf_load16(r, off), v);
+    }
+    static __device__ __forceinline__ void store(__amdgpu_buffer_rsrc_t r, uint32_t off, const float (&v)[8]) {
+        const i32x4 q = {(int)pack_bf16x2(v[0], v[1]), (int)pack_bf16x2(v[2], v[3]), (int)pack_bf16x2(v[4], v[5]),
+                         (int)pack_bf16x2(v[6], v[7])};
+        __builtin_amdgcn_raw_buffer_store_b128(q, r, (int)off, 0, 0);
+    }
+};
+
+// Wave index within the workgroup as a scalar (wave-uniform) value.
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
+
 // 16-byte load of base[off .. off+8) (bf16) or base[off .. off+4) (fp32) that
 // yields zeros when !ok. The load itself is unconditional from an in-bounds
 // address (base[0] when !ok) and the zero is a value select: a conditional

@@ -23,49 +23,53 @@ namespace {
 constexpr int kRowsPerBlock = 4;  // waves (rows) per 256-thread workgroup
 
 // ------------------------------------------------------------- forward
+// Vector path: the workgroup's 4 rows through one buffer resource (a wave's
+// row at a scalar byte offset); the row and the weight are loaded before any
+// use, vectors past the row through out-of-range offsets (zeros, stores
+// dropped) instead of branches.
 template <typename T, int VPL>
 __global__ __launch_bounds__(256) void rmsnorm_fwd_vec(int64_t rows, int dim, float eps,
                                                        const T* __restrict__ x,
                                                        const T* __restrict__ w,
                                                        T* __restrict__ y,
                                                        float* __restrict__ rstd) {
-    constexpr int N = Vec16<T>::N;
+    constexpr int N = BVec<T>::N;
+    constexpr int ES = (int)sizeof(T);
     const int lane = lane_id();
-    const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+    const int wave = wave_id();
+    const int64_t r0 = (int64_t)blockIdx.x * kRowsPerBlock;
+    const int64_t row = r0 + wave;
     if (row >= rows) return;
+    const int64_t nrows = rows - r0 < kRowsPerBlock ? rows - r0 : kRowsPerBlock;
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + r0 * dim, nrows * dim * ES);
+    const __amdgpu_buffer_rsrc_t ry = make_rsrc(y + r0 * dim, nrows * dim * ES);
+    const bool hw = w != nullptr;
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, hw ? (int64_t)dim * ES : 0);
     const int nvec = dim / N;
-    const T* xr = x + row * dim;
-    float v[VPL][N];
-    float ss = 0.f;
+    const uint32_t rowoff = (uint32_t)(wave * dim * ES);
+    float v[VPL][N], wv[VPL][N];
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
         const int vi = lane + i * kWave;
-        if (vi < nvec) {
-            Vec16<T>::load(xr + vi * N, v[i]);
-#pragma unroll
-            for (int e = 0; e < N; ++e) ss += v[i][e] * v[i][e];
-        }
+        const uint32_t off = vi < nvec ? (uint32_t)(vi * N * ES) : kOOB;
+        BVec<T>::load(rx, off == kOOB ? kOOB : rowoff + off, v[i]);
+        BVec<T>::load(rw, off, wv[i]);
     }
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i)
+#pragma unroll
+        for (int e = 0; e < N; ++e) ss += v[i][e] * v[i][e];
     ss = wave_sum(ss);
     const float r = 1.0f / sqrtf(ss / (float)dim + eps);
     if (rstd && lane == 0) rstd[row] = r;
-    T* yr = y + row * dim;
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
         const int vi = lane + i * kWave;
-        if (vi < nvec) {
-            float o[N];
-            if (w) {
-                float wv[N];
-                Vec16<T>::load(w + vi * N, wv);
+        float o[N];
 #pragma unroll
-                for (int e = 0; e < N; ++e) o[e] = v[i][e] * r * wv[e];
-            } else {
-#pragma unroll
-                for (int e = 0; e < N; ++e) o[e] = v[i][e] * r;
-            }
-            Vec16<T>::store(yr + vi * N, o);
-        }
+        for (int e = 0; e < N; ++e) o[e] = v[i][e] * r * (hw ? wv[i][e] : 1.f);
+        BVec<T>::store(ry, vi < nvec ? rowoff + (uint32_t)(vi * N * ES) : kOOB, o);
     }
 }
 
@@ -96,9 +100,10 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_scalar(int64_t rows, int64_t 
 
 // ------------------------------------------------------------ backward
 // Block b owns rows [b*chunk, min(rows, (b+1)*chunk)); wave k of the block
-// takes rows k, k+4, ... of that range. dw partials: per lane in registers,
-// then summed over the 4 waves in LDS in wave order, written to
-// partial[b][dim].
+// takes rows k, k+4, ... of that range, two at a time (the loads of both
+// rows issued before either is used). dw partials: per lane in registers,
+// accumulated in row order, then summed over the 4 waves in LDS in wave
+// order, written to partial[b][dim].
 template <typename T, int VPL, bool DW>
 __global__ __launch_bounds__(256) void rmsnorm_bwd_vec(int64_t rows, int dim, float eps, int64_t chunk,
                                                        const T* __restrict__ x,
@@ -107,19 +112,26 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_vec(int64_t rows, int dim, fl
                                                        const T* __restrict__ dy,
                                                        T* __restrict__ dx,
                                                        float* __restrict__ partial) {
-    constexpr int N = Vec16<T>::N;
+    constexpr int N = BVec<T>::N;
+    constexpr int ES = (int)sizeof(T);
     const int lane = lane_id();
-    const int wave = threadIdx.x >> 6;
+    const int wave = wave_id();
     const int nvec = dim / N;
     const int64_t r0 = (int64_t)blockIdx.x * chunk;
     const int64_t r1 = r0 + chunk < rows ? r0 + chunk : rows;
+    const int64_t nr = r1 > r0 ? r1 - r0 : 0;
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + r0 * dim, nr * dim * ES);
+    const __amdgpu_buffer_rsrc_t rg = make_rsrc(dy + r0 * dim, nr * dim * ES);
+    const __amdgpu_buffer_rsrc_t rd = make_rsrc(dx + r0 * dim, nr * dim * ES);
+    const bool hw = w != nullptr;
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, hw ? (int64_t)dim * ES : 0);
     float wv[VPL][N];
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
         const int vi = lane + i * kWave;
+        BVec<T>::load(rw, vi < nvec ? (uint32_t)(vi * N * ES) : kOOB, wv[i]);
 #pragma unroll
-        for (int e = 0; e < N; ++e) wv[i][e] = 1.f;
-        if (w && vi < nvec) Vec16<T>::load(w + vi * N, wv[i]);
+        for (int e = 0; e < N; ++e) wv[i][e] = hw ? wv[i][e] : 1.f;
     }
     float acc[DW ? VPL : 1][N];
 #pragma unroll
@@ -127,46 +139,59 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_vec(int64_t rows, int dim, fl
 #pragma unroll
         for (int e = 0; e < N; ++e) acc[i][e] = 0.f;
 
-    for (int64_t row = r0 + wave; row < r1; row += kRowsPerBlock) {
-        const T* xr = x + row * dim;
-        const T* gr = dy + row * dim;
-        float xv[VPL][N], gv[VPL][N];
-        float ss = 0.f, gx = 0.f;
+    for (int64_t rr = wave; rr < nr; rr += 2 * kRowsPerBlock) {
+        // raw 16-byte vectors of both rows (converted on use: bf16 rows stay
+        // packed, which halves the registers they hold)
+        i32x4 xq[2][VPL], gq[2][VPL];
 #pragma unroll
-        for (int i = 0; i < VPL; ++i) {
-            const int vi = lane + i * kWave;
-            if (vi < nvec) {
-                Vec16<T>::load(xr + vi * N, xv[i]);
-                Vec16<T>::load(gr + vi * N, gv[i]);
+        for (int h = 0; h < 2; ++h) {
+            const int64_t q = rr + h * kRowsPerBlock;  // rows past the range load zeros
 #pragma unroll
-                for (int e = 0; e < N; ++e) {
-                    ss += xv[i][e] * xv[i][e];
-                    gx += gv[i][e] * wv[i][e] * xv[i][e];
-                }
+            for (int i = 0; i < VPL; ++i) {
+                const int vi = lane + i * kWave;
+                const uint32_t off = vi < nvec ? (uint32_t)((q * dim + vi * N) * ES) : kOOB;
+                xq[h][i] = buf_load16(rx, off);
+                gq[h][i] = buf_load16(rg, off);
             }
         }
-        float r;
-        if (rstd) {
-            r = rstd[row];
-            gx = wave_sum(gx);
-        } else {
-            ss = wave_sum(ss);
-            gx = wave_sum(gx);
-            r = 1.0f / sqrtf(ss / (float)dim + eps);
-        }
-        const float c = r * r * r * gx / (float)dim;
-        T* dxr = dx + row * dim;
 #pragma unroll
-        for (int i = 0; i < VPL; ++i) {
-            const int vi = lane + i * kWave;
-            if (vi < nvec) {
-                float o[N];
+        for (int h = 0; h < 2; ++h) {
+            const int64_t q = rr + h * kRowsPerBlock;
+            if (q >= nr) break;  // wave-uniform
+            float ss = 0.f, gx = 0.f;
 #pragma unroll
-                for (int e = 0; e < N; ++e) o[e] = r * gv[i][e] * wv[i][e] - xv[i][e] * c;
-                Vec16<T>::store(dxr + vi * N, o);
+            for (int i = 0; i < VPL; ++i) {
+                float xv[N], gv[N];
+                BVec<T>::unpack(xq[h][i], xv);
+                BVec<T>::unpack(gq[h][i], gv);
+#pragma unroll
+                for (int e = 0; e < N; ++e) {
+                    ss += xv[e] * xv[e];
+                    gx += gv[e] * wv[i][e] * xv[e];
+                }
+            }
+            float r;
+            if (rstd) {
+                r = rstd[r0 + q];
+                gx = wave_sum(gx);
+            } else {
+                ss = wave_sum(ss);
+                gx = wave_sum(gx);
+                r = 1.0f / sqrtf(ss / (float)dim + eps);
+            }
+            const float c = r * r * r * gx / (float)dim;
+#pragma unroll
+            for (int i = 0; i < VPL; ++i) {
+                const int vi = lane + i * kWave;
+                float xv[N], gv[N], o[N];
+                BVec<T>::unpack(xq[h][i], xv);
+                BVec<T>::unpack(gq[h][i], gv);
+#pragma unroll
+                for (int e = 0; e < N; ++e) o[e] = r * gv[e] * wv[i][e] - xv[e] * c;
+                BVec<T>::store(rd, vi < nvec ? (uint32_t)((q * dim + vi * N) * ES) : kOOB, o);
                 if constexpr (DW) {
 #pragma unroll
-                    for (int e = 0; e < N; ++e) acc[i][e] += gv[i][e] * xv[i][e] * r;
+                    for (int e = 0; e < N; ++e) acc[i][e] += gv[e] * xv[e] * r;
                 }
             }
         }

@@ -29,61 +29,64 @@ __device__ __forceinline__ int64_t row_limit(int64_t row, int64_t dim, int64_t c
     return causal_rows > 0 ? row % causal_rows + (dim - causal_rows) : dim - 1;
 }
 
+// Vector path: the 4 rows of a workgroup through one buffer resource (a
+// wave's row at a scalar byte offset); every load of the row is issued
+// before any use, with wholly masked vectors and vectors past the row given
+// out-of-range offsets (no memory traffic, zeros), and the masks applied as
+// value selects.
 template <typename T, int VPL>
 __global__ __launch_bounds__(256) void softmax_fwd_vec(int64_t rows, int dim, int64_t causal_rows,
                                                        const T* __restrict__ s, T* __restrict__ p) {
-    constexpr int N = Vec16<T>::N;
+    constexpr int N = BVec<T>::N;
+    constexpr int ES = (int)sizeof(T);
     const int lane = lane_id();
-    const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+    const int wave = wave_id();
+    const int64_t r0 = (int64_t)blockIdx.x * kRowsPerBlock;
+    const int64_t row = r0 + wave;
     if (row >= rows) return;
+    const int64_t nrows = rows - r0 < kRowsPerBlock ? rows - r0 : kRowsPerBlock;
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(s + r0 * dim, nrows * dim * ES);
+    const __amdgpu_buffer_rsrc_t rp = make_rsrc(p + r0 * dim, nrows * dim * ES);
     const int nvec = dim / N;
     const int lim = (int)row_limit(row, dim, causal_rows);
-    const T* sr = s + row * (int64_t)dim;
+    const uint32_t rowoff = (uint32_t)(wave * dim * ES);
     float v[VPL][N];
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+        const int vi = lane + i * kWave;
+        const bool ok = vi < nvec && vi * N <= lim;
+        BVec<T>::load(rs, ok ? rowoff + (uint32_t)(vi * N * ES) : kOOB, v[i]);
+    }
     float m = -INFINITY;
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
         const int vi = lane + i * kWave;
-        if (vi < nvec && vi * N <= lim) {
-            Vec16<T>::load(sr + vi * N, v[i]);
 #pragma unroll
-            for (int e = 0; e < N; ++e) {
-                if (vi * N + e > lim) v[i][e] = -INFINITY;
-                m = fmaxf(m, v[i][e]);
-            }
+        for (int e = 0; e < N; ++e) {
+            const bool valid = vi < nvec && vi * N + e <= lim;
+            v[i][e] = valid ? v[i][e] : -INFINITY;
+            m = fmaxf(m, v[i][e]);
         }
     }
     m = wave_max(m);
     float sum = 0.f;
 #pragma unroll
-    for (int i = 0; i < VPL; ++i) {
-        const int vi = lane + i * kWave;
-        if (vi < nvec && vi * N <= lim) {
+    for (int i = 0; i < VPL; ++i)
 #pragma unroll
-            for (int e = 0; e < N; ++e) {
-                float ex = fast_exp2((v[i][e] - m) * kLog2e);
-                v[i][e] = ex;
-                sum += ex;
-            }
+        for (int e = 0; e < N; ++e) {
+            const float ex = fast_exp2((v[i][e] - m) * kLog2e);  // masked: exp2(-inf) = 0
+            v[i][e] = ex;
+            sum += ex;
         }
-    }
     sum = wave_sum(sum);
     const float inv = 1.0f / sum;
-    T* pr = p + row * (int64_t)dim;
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
         const int vi = lane + i * kWave;
-        if (vi < nvec) {
-            float o[N];
-            if (vi * N <= lim) {
+        float o[N];
 #pragma unroll
-                for (int e = 0; e < N; ++e) o[e] = v[i][e] * inv;
-            } else {
-#pragma unroll
-                for (int e = 0; e < N; ++e) o[e] = 0.f;
-            }
-            Vec16<T>::store(pr + vi * N, o);
-        }
+        for (int e = 0; e < N; ++e) o[e] = v[i][e] * inv;
+        BVec<T>::store(rp, vi < nvec ? rowoff + (uint32_t)(vi * N * ES) : kOOB, o);
     }
 }
 
@@ -112,45 +115,47 @@ template <typename T, int VPL>
 __global__ __launch_bounds__(256) void softmax_bwd_vec(int64_t rows, int dim, int64_t causal_rows,
                                                        const T* __restrict__ p, const T* __restrict__ dp,
                                                        T* __restrict__ ds) {
-    constexpr int N = Vec16<T>::N;
+    constexpr int N = BVec<T>::N;
+    constexpr int ES = (int)sizeof(T);
     const int lane = lane_id();
-    const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+    const int wave = wave_id();
+    const int64_t r0 = (int64_t)blockIdx.x * kRowsPerBlock;
+    const int64_t row = r0 + wave;
     if (row >= rows) return;
+    const int64_t nrows = rows - r0 < kRowsPerBlock ? rows - r0 : kRowsPerBlock;
+    const __amdgpu_buffer_rsrc_t rp = make_rsrc(p + r0 * dim, nrows * dim * ES);
+    const __amdgpu_buffer_rsrc_t rg = make_rsrc(dp + r0 * dim, nrows * dim * ES);
+    const __amdgpu_buffer_rsrc_t rd = make_rsrc(ds + r0 * dim, nrows * dim * ES);
     const int nvec = dim / N;
     const int lim = (int)row_limit(row, dim, causal_rows);
-    const T* pr = p + row * (int64_t)dim;
-    const T* gr = dp + row * (int64_t)dim;
+    const uint32_t rowoff = (uint32_t)(wave * dim * ES);
     float pv[VPL][N], gv[VPL][N];
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+        const int vi = lane + i * kWave;
+        const uint32_t off = (vi < nvec && vi * N <= lim) ? rowoff + (uint32_t)(vi * N * ES) : kOOB;
+        BVec<T>::load(rp, off, pv[i]);
+        BVec<T>::load(rg, off, gv[i]);
+    }
     float dot = 0.f;
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
         const int vi = lane + i * kWave;
-        if (vi < nvec && vi * N <= lim) {
-            Vec16<T>::load(pr + vi * N, pv[i]);
-            Vec16<T>::load(gr + vi * N, gv[i]);
 #pragma unroll
-            for (int e = 0; e < N; ++e) {
-                if (vi * N + e > lim) pv[i][e] = 0.f;  // masked: p = 0 by definition
-                dot += pv[i][e] * gv[i][e];
-            }
+        for (int e = 0; e < N; ++e) {
+            // masked: p = 0 by definition (and dp is not read there)
+            pv[i][e] = (vi < nvec && vi * N + e <= lim) ? pv[i][e] : 0.f;
+            dot += pv[i][e] * gv[i][e];
         }
     }
     dot = wave_sum(dot);
-    T* dr = ds + row * (int64_t)dim;
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
         const int vi = lane + i * kWave;
-        if (vi < nvec) {
-            float o[N];
-            if (vi * N <= lim) {
+        float o[N];
 #pragma unroll
-                for (int e = 0; e < N; ++e) o[e] = pv[i][e] * (gv[i][e] - dot);
-            } else {
-#pragma unroll
-                for (int e = 0; e < N; ++e) o[e] = 0.f;
-            }
-            Vec16<T>::store(dr + vi * N, o);
-        }
+        for (int e = 0; e < N; ++e) o[e] = pv[i][e] * (gv[i][e] - dot);
+        BVec<T>::store(rd, vi < nvec ? rowoff + (uint32_t)(vi * N * ES) : kOOB, o);
     }
 }
 
