@@ -17,10 +17,15 @@ are not part of the step; their outputs are synthetic tensors of the right
 shape. Inputs are synthetic (seeded normal / kaiming-uniform draws) and
 resident in HBM before timing starts.
 
-value = tokens / second of the timed steps. The roofline object is for the
-dominant kernel, the MFMA GEMM (base x.W^T / dY.W with the rank-r columns
-folded in), timed per launch with hipEvents on its stream by the library's
-profiling hook; achieved counts the base-product FLOPs only.
+value = tokens / second of the timed steps (plain eager calls; with --graph
+the step is captured once into a HIP graph, torch.cuda.CUDAGraph, and the
+timed steps are replays: the entry points allocate nothing, never
+synchronise and record no memset, so they capture). The roofline object is
+for the dominant kernel, the MFMA GEMM (base x.W^T / dY.W with the rank-r
+columns folded in), timed per launch with hipEvents on its stream by the
+library's profiling hook in a separate pass after the timed steps (the
+hook's events are not in the timed region); achieved counts the
+base-product FLOPs only.
 """
 import argparse
 import json
@@ -223,6 +228,7 @@ def main():
     ap.add_argument("--config", default="c4", choices=sorted(CONFIGS))
     ap.add_argument("--cpu-tokens", type=int, default=2048, help="token sample of the CPU-oracle baseline")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--graph", action="store_true", help="time HIP graph replays of one captured step")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="run one plain device copy of BYTES before the steps (a kernel of known HBM traffic "
                          "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
@@ -251,14 +257,35 @@ def main():
         layer.step()
     torch.cuda.synchronize()
 
-    mc._lib.check(mc._lib.lib().mc_profile_reset())
-    mc._lib.check(mc._lib.lib().mc_profile_enable(1))
+    if args.graph:
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            layer.step()
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            layer.step()
+        torch.cuda.synchronize()
+        graph.replay()  # one untimed replay
+        run = graph.replay
+    else:
+        run = layer.step
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        layer.step()
+        run()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
+
+    # per-kernel event timing of eager steps (the library's profiling hook),
+    # after and outside the timed region
+    prof_steps = max(1, min(args.steps, 20))
+    mc._lib.check(mc._lib.lib().mc_profile_reset())
+    mc._lib.check(mc._lib.lib().mc_profile_enable(1))
+    for _ in range(prof_steps):
+        layer.step()
+    torch.cuda.synchronize()
     mc._lib.check(mc._lib.lib().mc_profile_enable(0))
     mc._lib.check(mc._lib.lib().mc_profile_collect())
 
@@ -270,8 +297,8 @@ def main():
         if n == 0:
             continue
         kernels[kind] = {
-            "launches_per_step": n / args.steps,
-            "ms_per_step": ms / args.steps,
+            "launches_per_step": n / prof_steps,
+            "ms_per_step": ms / prof_steps,
             "avg_launch_us": ms * 1e3 / n,
             "TFLOP_s": fl / (ms * 1e-3) / 1e12 if fl else None,
             "GB_s": by / (ms * 1e-3) / 1e9,
@@ -306,6 +333,7 @@ def main():
             "traffic": GEMM_TRAFFIC_BYTES.get(args.config),
         },
         "layer_TFLOP_s": (base_fl + low_fl) / (ms_step * 1e-3) / 1e12,
+        "launch": "hip_graph" if args.graph else "eager",
         "kernels": kernels,
     }
     if not args.no_cpu_baseline:
