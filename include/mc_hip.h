@@ -22,6 +22,9 @@
  *                    the causal -inf mask that Attention::forward adds before
  *                    softmax_stable (src/models/transformer.rs:264-275).
  *   mc_softmax_bwd   no reference kernel: autograd of tensor.rs:91-98.
+ *   mc_attention_fwd the attention core of Attention::forward
+ *                    (src/models/transformer.rs:258-283) with repeat_kv
+ *                    (295-319), without materialising the score matrix.
  *
  * Conventions (all entry points):
  *  - Device buffers are caller-owned, row-major and contiguous; inputs are
@@ -135,6 +138,40 @@ mc_status mc_softmax_fwd(int64_t rows, int64_t dim, int64_t causal_rows, int32_t
 mc_status mc_softmax_bwd(int64_t rows, int64_t dim, int64_t causal_rows, int32_t dtype,
                          const void* p, const void* dp, void* ds, hipStream_t stream);
 
+/* Attention core: the part of Attention::forward between the rotary
+ * embedding and o_proj (src/models/transformer.rs:258-283), with the K/V head
+ * repetition of repeat_kv (transformer.rs:295-319) done by indexing:
+ *   q [B, H, S, D], k, v [B, Hkv, S, D]   (after RoPE and transpose(1, 2))
+ *   query head h reads K/V head h / (H / Hkv)
+ *   scores = scale q.k^T  (+ mask[i, j])  (-inf where key j > query i if causal)
+ *   o [B, S, H * D] = softmax_stable(scores) . v   (the reference's
+ *                     transpose(1, 2) + reshape, transformer.rs:280-282)
+ * scale is 1/sqrt(D) in the reference (transformer.rs:266). mask is an
+ * optional fp32 [S, S] additive mask broadcast over B and H (the reference's
+ * attention_mask of shape [1, 1, S, S]); S * S * 4 must stay below 2^31. A
+ * row whose scores are all -inf gives NaN, as softmax_stable does. lse
+ * [B, H, S] fp32 (may be NULL) receives the natural log-sum-exp of each score
+ * row, which mc_attention_bwd takes.
+ * bf16 with D = 64 or 128 runs the MFMA (flash) kernel and needs the
+ * workspace of mc_attention_fwd_workspace_size(); other D (<= 256) and fp32
+ * run a one-wave-per-row kernel with no workspace. */
+typedef struct mc_attn_desc {
+    int64_t batch;     /* B >= 1 */
+    int64_t seq;       /* S >= 1: queries and keys (self-attention, no KV cache) */
+    int32_t heads;     /* H >= 1 */
+    int32_t kv_heads;  /* Hkv >= 1, H % Hkv == 0 */
+    int32_t head_dim;  /* 1 <= D <= 256; bf16: D % 8 == 0 */
+    int32_t causal;    /* 0 or 1 */
+    float scale;       /* finite */
+    int32_t dtype;     /* mc_dtype of q, k, v, o, dq, dk, dv, do */
+} mc_attn_desc;
+
+size_t mc_attention_fwd_workspace_size(const mc_attn_desc* d);
+
+mc_status mc_attention_fwd(const mc_attn_desc* d, const void* q, const void* k, const void* v,
+                           const float* mask, void* o, float* lse, void* workspace,
+                           size_t workspace_bytes, hipStream_t stream);
+
 /* Host-side dropout keep-mask [rows, rank] from a seed (Philox4x32-10; element
  * i = t*rank + j uses counter block i/4, word i%4, key = seed; keep iff
  * (word >> 8) * 2^-24 >= p). Both the GPU path and the CPU reference are fed
@@ -150,7 +187,8 @@ mc_status mc_dropout_mask(uint64_t seed, float p, int64_t rows, int32_t rank, ui
  * the recorded events and adds them to per-class totals; mc_profile_read()
  * returns the totals of one class. Classes: 0 = MFMA GEMM (FLOPs count the
  * base x.W^T / dY.W product only), 1 = rank-r kernels, 2 = RMSNorm,
- * 3 = softmax. Enabling allocates hipEvents (not for allocation-free use). */
+ * 3 = softmax, 4 = attention (FLOPs of the unmasked score and P.V products).
+ * Enabling allocates hipEvents (not for allocation-free use). */
 mc_status mc_profile_enable(int32_t on);
 mc_status mc_profile_collect(void);
 mc_status mc_profile_read(int32_t kind, double* elapsed_ms, int64_t* launches, double* flops, double* bytes);

@@ -1,4 +1,5 @@
-"""metal-candle's fused LoRA / RMSNorm / softmax custom ops on MI355X (gfx950).
+"""metal-candle's fused LoRA / RMSNorm / softmax custom ops and the attention
+core on MI355X (gfx950).
 
 The arithmetic lives in libmc_hip.so (HIP kernels behind the C ABI of
 include/mc_hip.h); this package is the Python host side over that ABI.
@@ -8,6 +9,7 @@ __graft_entry__.load_package(), which registers it as `metal_candle_amd`.
 from . import _lib, ops  # noqa: F401
 from ._lib import McError  # noqa: F401
 from .ops import (  # noqa: F401
+    attention_forward,
     dropout_mask,
     lora_backward,
     lora_forward,

@@ -50,12 +50,26 @@ class LoraDesc(ctypes.Structure):
     ]
 
 
+class AttnDesc(ctypes.Structure):
+    _fields_ = [
+        ("batch", ctypes.c_int64),
+        ("seq", ctypes.c_int64),
+        ("heads", ctypes.c_int32),
+        ("kv_heads", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("causal", ctypes.c_int32),
+        ("scale", ctypes.c_float),
+        ("dtype", ctypes.c_int32),
+    ]
+
+
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int32
 _f32 = ctypes.c_float
 _sz = ctypes.c_size_t
 _dp = ctypes.POINTER(LoraDesc)
+_ap = ctypes.POINTER(AttnDesc)
 
 _SIGNATURES = {
     "mc_version": (ctypes.c_char_p, []),
@@ -69,6 +83,8 @@ _SIGNATURES = {
     "mc_rmsnorm_bwd": (ctypes.c_int, [_i64, _i64, _f32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "mc_softmax_fwd": (ctypes.c_int, [_i64, _i64, _i64, _i32, _vp, _vp, _vp]),
     "mc_softmax_bwd": (ctypes.c_int, [_i64, _i64, _i64, _i32, _vp, _vp, _vp, _vp]),
+    "mc_attention_fwd_workspace_size": (_sz, [_ap]),
+    "mc_attention_fwd": (ctypes.c_int, [_ap, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "mc_dropout_mask": (ctypes.c_int, [ctypes.c_uint64, _f32, _i64, _i32, _vp]),
     "mc_profile_enable": (ctypes.c_int, [_i32]),
     "mc_profile_collect": (ctypes.c_int, []),
@@ -77,7 +93,7 @@ _SIGNATURES = {
     "mc_profile_reset": (ctypes.c_int, []),
 }
 
-PROFILE_KINDS = {"gemm": 0, "lowrank": 1, "rmsnorm": 2, "softmax": 3}
+PROFILE_KINDS = {"gemm": 0, "lowrank": 1, "rmsnorm": 2, "softmax": 3, "attention": 4}
 
 _lib = None
 

@@ -93,6 +93,34 @@ double unmasked(int64_t rows, int64_t dim, int64_t S) {
     return (double)(rows / S) * block(S) + block(rows % S);
 }
 
+mc_status check_attn_desc(const mc_attn_desc* d, const char* op) {
+    MC_CHECK(d != nullptr, MC_ERR_NULL, "%s: descriptor is NULL", op);
+    mc_status s = check_dtype(d->dtype, op);
+    if (s != MC_OK) return s;
+    MC_CHECK(d->batch >= 1 && d->seq >= 1 && d->heads >= 1 && d->kv_heads >= 1, MC_ERR_SHAPE,
+             "%s: batch, seq, heads and kv_heads must be >= 1, got %lld, %lld, %d, %d", op, (long long)d->batch,
+             (long long)d->seq, (int)d->heads, (int)d->kv_heads);
+    // repeat_kv repeats each K/V head num_heads / num_kv_heads times (transformer.rs:258-259, 300-318)
+    MC_CHECK(d->heads % d->kv_heads == 0, MC_ERR_SHAPE, "%s: heads (%d) must be a multiple of kv_heads (%d)", op,
+             (int)d->heads, (int)d->kv_heads);
+    MC_CHECK(d->head_dim >= 1 && d->head_dim <= 256, MC_ERR_SHAPE, "%s: head_dim must be in [1, 256], got %d", op,
+             (int)d->head_dim);
+    MC_CHECK(d->dtype != MC_BF16 || d->head_dim % 8 == 0, MC_ERR_SHAPE,
+             "%s: bf16 head_dim must be a multiple of 8, got %d", op, (int)d->head_dim);
+    MC_CHECK(d->causal == 0 || d->causal == 1, MC_ERR_VALUE, "%s: causal must be 0 or 1", op);
+    MC_CHECK(std::isfinite(d->scale), MC_ERR_VALUE, "%s: scale must be finite", op);
+    const double elems = (double)d->batch * d->heads * d->seq * d->head_dim;
+    MC_CHECK(elems < 9.0e15 && (double)d->batch * d->heads * d->seq < 2.0e9, MC_ERR_SHAPE,
+             "%s: problem too large (B * H * S must stay below 2^31)", op);
+    return MC_OK;
+}
+
+// Score-matrix entries an attention pass computes (causal: the lower triangle).
+double attn_pairs(const mc_attn_desc* d) {
+    const double S = (double)d->seq;
+    return (double)d->batch * d->heads * (d->causal ? S * (S + 1) / 2 : S * S);
+}
+
 }  // namespace
 
 extern "C" {
@@ -244,6 +272,32 @@ mc_status mc_softmax_bwd(int64_t rows, int64_t dim, int64_t causal_rows, int32_t
                           es * (2.0 * unmasked(rows, dim, causal_rows) + (double)rows * dim));
     return hip_status(mc::launch_softmax_bwd(rows, dim, causal_rows, dtype, p, dp, ds, stream),
                       "Softmax backward");
+}
+
+size_t mc_attention_fwd_workspace_size(const mc_attn_desc* d) {
+    if (check_attn_desc(d, "Attention") != MC_OK) return 0;
+    return mc::attention_fwd_ws(*d).total;
+}
+
+mc_status mc_attention_fwd(const mc_attn_desc* d, const void* q, const void* k, const void* v, const float* mask,
+                           void* o, float* lse, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    mc_status s = check_attn_desc(d, "Attention");
+    if (s != MC_OK) return s;
+    MC_CHECK(q && k && v && o, MC_ERR_NULL, "Attention: q, k, v and o must not be NULL");
+    MC_CHECK(!mask || (double)d->seq * d->seq * 4.0 < 2147483647.0, MC_ERR_SHAPE,
+             "Attention: an explicit mask needs S * S * 4 < 2^31 bytes (S = %lld)", (long long)d->seq);
+    MC_CHECK(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o), MC_ERR_LAYOUT,
+             "Attention: q, k, v and o must be 16-byte aligned");
+    const size_t need = mc::attention_fwd_ws(*d).total;
+    MC_CHECK(workspace_bytes >= need && (need == 0 || workspace), MC_ERR_WORKSPACE,
+             "Attention: workspace of %zu bytes required, %zu given", need, workspace_bytes);
+    MC_CHECK(aligned16(workspace), MC_ERR_LAYOUT, "Attention: workspace must be 16-byte aligned");
+    const double es = d->dtype == MC_F32 ? 4.0 : 2.0;
+    const double qo = (double)d->batch * d->heads * d->seq * d->head_dim;
+    const double kv = (double)d->batch * d->kv_heads * d->seq * d->head_dim;
+    mc::prof::Scope sc(mc::prof::kAttention, stream, 4.0 * attn_pairs(d) * d->head_dim,
+                       es * (2.0 * qo + 2.0 * kv) + (lse ? 4.0 * d->batch * d->heads * d->seq : 0.0));
+    return hip_status(mc::launch_attention_fwd(*d, q, k, v, mask, o, lse, workspace, stream), "Attention forward");
 }
 
 // Philox4x32-10 (Salmon et al., SC'11), 10 rounds of the two 32x32->64

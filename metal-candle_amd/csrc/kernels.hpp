@@ -57,4 +57,16 @@ hipError_t launch_lora_bwd(const mc_lora_desc& d, const void* x, const void* W, 
                            const void* dY, void* dX, float* dA, float* dB, void* ws,
                            hipStream_t stream);
 
+// ----------------------------------------------------------- attention
+// Workspace of mc_attention_fwd: V^T [B, Hkv, D, Sp] bf16 for the MFMA path
+// (Sp = S rounded up to 64), nothing for the generic path.
+struct AttnWs {
+    size_t vt;
+    size_t total;
+};
+bool attention_uses_mfma(const mc_attn_desc& d);
+AttnWs attention_fwd_ws(const mc_attn_desc& d);
+hipError_t launch_attention_fwd(const mc_attn_desc& d, const void* q, const void* k, const void* v,
+                                const float* mask, void* o, float* lse, void* ws, hipStream_t stream);
+
 }  // namespace mc

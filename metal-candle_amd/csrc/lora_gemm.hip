@@ -67,43 +67,6 @@ __device__ __forceinline__ void tile_of(int pid, int tiles_m, int tiles_n, int g
     tn = r / gm;
 }
 
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
-
-// LDS tile layout: rows of BK bf16 (2 BK bytes, no padding), CPR = BK/8
-// 16-byte chunks per row; chunk c of row r sits in slot
-// c ^ ((r / (128/BK)) % CPR). A 256-byte bank window holds 128/BK rows, so a
-// 16-lane group touches 16 distinct 16-byte bank groups both when the loads
-// write whole rows and when the MFMA fragment reads walk down 16 rows of one
-// chunk column.
-template <int BK>
-__device__ __forceinline__ int swz(int r, int c) {
-    return c ^ ((r / (128 / BK)) % (BK / 8));
-}
-
-// One buffer_load_dwordx4 ... lds: 64 lanes x 16 B to LDS bytes
-// [lds_byte, lds_byte + 1 KB), lane l -> lds_byte + 16 l (M0 holds the LDS
-// base). Issued from inline asm so that the compiler's wait-count pass does
-// not see an LDS write it cannot place, which makes it wait for every such
-// load before any LDS read; the kernel waits for these loads itself
-// (wait_vmcnt + barrier) before the stage they fill is read.
-__device__ __forceinline__ void dma16(i32x4 rsrc, uint32_t lds_byte, uint32_t voff) {
-    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-                 :
-                 : "s"(lds_byte), "v"(voff), "s"(rsrc)
-                 : "memory", "m0");
-}
-
-__device__ __forceinline__ i32x4 rsrc_words(const void* base, int64_t bytes) {
-    const int n = bytes <= 0 ? 0 : bytes >= 0x7fffffff ? 0x7fffffff : (int)bytes;
-    const uint64_t a = reinterpret_cast<uint64_t>(base);
-    i32x4 r;
-    r[0] = (int)(uint32_t)a;
-    r[1] = (int)(uint32_t)(a >> 32) & 0xffff;  // stride 0
-    r[2] = n;
-    r[3] = 0x00020000;
-    return r;
-}
-
 // Loads rows [0, ROWS) x BK columns (k = kb .. kb+BK-1) of one operand tile
 // into the swizzled layout at lds_byte: a load moves RPI = 512/BK rows; each
 // wave issues ROWS/RPI/waves of them, split over PARTS calls (part p issues
@@ -128,14 +91,6 @@ __device__ __forceinline__ void dma_tile(i32x4 r, uint32_t lds_byte, uint32_t ld
         // the LDS address is wave-uniform: make it scalar for M0
         dma16(r, __builtin_amdgcn_readfirstlane(lds_byte + (uint32_t)blk * 1024u), off);
     }
-}
-
-// s_waitcnt vmcnt(n) with the other counters left alone (gfx9 encoding:
-// vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] at [15:14]).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
 template <int N>

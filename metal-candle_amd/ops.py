@@ -12,7 +12,7 @@ import ctypes
 import torch
 
 from . import _lib
-from ._lib import LoraDesc, McError, check, lib
+from ._lib import AttnDesc, LoraDesc, McError, check, lib
 
 _DTYPES = {torch.float32: _lib.MC_F32, torch.bfloat16: _lib.MC_BF16}
 
@@ -120,6 +120,29 @@ def softmax_backward(p, dp, causal_rows=0):
     check(lib().mc_softmax_bwd(rows, D, int(causal_rows), _dtype_code(p), _ptr(p), _ptr(dp), _ptr(ds),
                                _stream(p)))
     return ds
+
+
+def attention_desc(q, k, causal, scale):
+    B, H, S, D = q.shape
+    return AttnDesc(B, S, H, k.shape[1], D, int(bool(causal)), float(scale), _dtype_code(q))
+
+
+def attention_forward(q, k, v, causal=False, scale=None, mask=None, save_lse=True):
+    """Attention core of Attention::forward (src/models/transformer.rs:258-283):
+    q [B, H, S, D], k, v [B, Hkv, S, D] -> (o [B, S, H*D], lse [B, H, S])."""
+    for t, n in ((q, "q"), (k, "k"), (v, "v"), (mask, "mask")):
+        _contig(t, n)
+    B, H, S, D = q.shape
+    if scale is None:
+        scale = D ** -0.5
+    d = attention_desc(q, k, causal, scale)
+    o = torch.empty(B, S, H * D, dtype=q.dtype, device=q.device)
+    lse = torch.empty(B, H, S, dtype=torch.float32, device=q.device) if save_lse else None
+    ws_n = lib().mc_attention_fwd_workspace_size(ctypes.byref(d))
+    ws = _workspace(ws_n, q.device)
+    check(lib().mc_attention_fwd(ctypes.byref(d), _ptr(q), _ptr(k), _ptr(v), _ptr(mask), _ptr(o), _ptr(lse),
+                                 _ptr(ws), ws_n, _stream(q)))
+    return o, lse
 
 
 def dropout_mask(seed, p, rows, rank):

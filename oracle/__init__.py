@@ -46,6 +46,12 @@ def lib():
         L.oracle_softmax_fwd.argtypes = [_i64, _i64, _i64, _f32p, _f32p, ctypes.c_int]
         L.oracle_softmax_bwd.argtypes = [_i64, _i64, _i64, _f32p, _f32p, _f32p, ctypes.c_int]
         L.oracle_round_bf16.argtypes = [_f32p, _f32p, _i64]
+        _i32 = ctypes.c_int32
+        L.oracle_attention_fwd.argtypes = [_i64, _i32, _i32, _i64, _i32, ctypes.c_float, ctypes.c_int,
+                                           _f32p, _f32p, _f32p, _f32p, _f32p, _f32p, ctypes.c_int]
+        L.oracle_attention_bwd.argtypes = [_i64, _i32, _i32, _i64, _i32, ctypes.c_float, ctypes.c_int,
+                                           _f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p,
+                                           ctypes.c_int]
         _i64p = ctypes.POINTER(ctypes.c_int64)
         L.oracle_softmax_fwd_rows.argtypes = [_i64, _i64, _i64, _i64p, _f32p, _f32p, ctypes.c_int]
         L.oracle_softmax_bwd_rows.argtypes = [_i64, _i64, _i64, _i64p, _f32p, _f32p, _f32p, ctypes.c_int]
@@ -170,3 +176,26 @@ def softmax_bwd(p, dp, causal_rows=0, threads=0, row_ids=None):
         assert ids.size == rows
         lib().oracle_softmax_bwd_rows(rows, D, causal_rows, ip, _f(p), _f(dp), _f(ds), threads)
     return ds
+
+
+def attention_fwd(q, k, v, scale, causal=False, mask=None, threads=0):
+    """(o [B, S, H*D], lse [B, H, S]) for q [B, H, S, D], k, v [B, Hkv, S, D]."""
+    q, k, v, mask = _c32(q), _c32(k), _c32(v), _c32(mask)
+    B, H, S, D = q.shape
+    Hkv = k.shape[1]
+    o = np.empty((B, S, H * D), dtype=np.float32)
+    lse = np.empty((B, H, S), dtype=np.float32)
+    lib().oracle_attention_fwd(B, H, Hkv, S, D, scale, int(causal), _f(q), _f(k), _f(v), _f(mask), _f(o),
+                               _f(lse), threads)
+    return o, lse
+
+
+def attention_bwd(q, k, v, dout, scale, causal=False, mask=None, threads=0):
+    """(dq, dk, dv) of attention_fwd for dout [B, S, H*D]."""
+    q, k, v, mask, dout = _c32(q), _c32(k), _c32(v), _c32(mask), _c32(dout)
+    B, H, S, D = q.shape
+    Hkv = k.shape[1]
+    dq, dk, dv = np.empty_like(q), np.empty_like(k), np.empty_like(v)
+    lib().oracle_attention_bwd(B, H, Hkv, S, D, scale, int(causal), _f(q), _f(k), _f(v), _f(mask), _f(dout),
+                               _f(dq), _f(dk), _f(dv), threads)
+    return dq, dk, dv

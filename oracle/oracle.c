@@ -303,6 +303,139 @@ void oracle_softmax_bwd_rows(int64_t n, int64_t D, int64_t causal_rows, const in
     softmax_bwd_impl(n, D, causal_rows, row_ids, p, dp, ds, threads);
 }
 
+/* ------------------------------------------------------------- attention */
+/* Attention::forward (src/models/transformer.rs:258-283) for one (b, h, i)
+ * score row, in the reference's op order: q.k^T (matmul, 264), scaled (266;
+ * the reference divides by sqrt(d), callers pass scale = 1/sqrt(d)), the
+ * broadcast mask added (268-272), softmax_stable (tensor.rs:91-98: max, sub,
+ * exp, sum, divide). The causal mask is -inf where key j > query i. K/V head
+ * of query head h: h / (H / Hkv), the order repeat_kv builds (295-319).
+ * Returns the row max; *sum receives the exp sum; p[j] the probabilities. */
+static double attn_row(int64_t S, int D, double scale, int causal, const float* qi, const float* kh,
+                       const float* mrow, int64_t i, double* p, double* sum) {
+    double m = -INFINITY;
+    for (int64_t j = 0; j < S; ++j) {
+        double s = 0.0;
+        const float* kj = kh + j * D;
+        for (int d = 0; d < D; ++d) s += (double)qi[d] * (double)kj[d];
+        s *= scale;
+        if (mrow) s += (double)mrow[j];
+        if (causal && j > i) s = -INFINITY;
+        p[j] = s;
+        if (s > m) m = s;
+    }
+    double z = 0.0;
+    for (int64_t j = 0; j < S; ++j) {
+        p[j] = exp(p[j] - m); /* all -inf: exp(nan) = nan, as the reference */
+        z += p[j];
+    }
+    for (int64_t j = 0; j < S; ++j) p[j] /= z;
+    *sum = z;
+    return m;
+}
+
+void oracle_attention_fwd(int64_t B, int32_t H, int32_t Hkv, int64_t S, int32_t D, float scale, int causal,
+                          const float* q, const float* k, const float* v, const float* mask, float* o,
+                          float* lse, int threads) {
+    const int rep = H / Hkv;
+#pragma omp parallel num_threads(nthreads(threads))
+    {
+        double* p = (double*)malloc(sizeof(double) * (size_t)S);
+        double* acc = (double*)malloc(sizeof(double) * (size_t)D);
+#pragma omp for schedule(dynamic, 16)
+        for (int64_t row = 0; row < B * H * S; ++row) {
+            const int64_t bh = row / S, i = row % S;
+            const int64_t b = bh / H, h = bh % H;
+            const int64_t bhk = b * Hkv + h / rep;
+            const float* kh = k + bhk * S * D;
+            const float* vh = v + bhk * S * D;
+            double z;
+            const double m = attn_row(S, D, scale, causal, q + (bh * S + i) * D, kh, mask ? mask + i * S : NULL,
+                                      i, p, &z);
+            for (int d = 0; d < D; ++d) acc[d] = 0.0;
+            for (int64_t j = 0; j < S; ++j) {
+                if (p[j] == 0.0) continue;
+                const float* vj = vh + j * D;
+                for (int d = 0; d < D; ++d) acc[d] += p[j] * (double)vj[d];
+            }
+            /* transpose(1, 2) + reshape to [B, S, H * D] (transformer.rs:280-282) */
+            float* orow = o + ((b * S + i) * H + h) * D;
+            for (int d = 0; d < D; ++d) orow[d] = (float)acc[d];
+            if (lse) lse[bh * S + i] = (float)(m + log(z));
+        }
+        free(p);
+        free(acc);
+    }
+}
+
+/* Gradients of the forward above (candle autograd of transformer.rs:264-278,
+ * no reference kernel): with P the probabilities and dO [B, S, H * D],
+ *   dV_j = sum_i P_ij dO_i            dP_ij = dO_i . v_j
+ *   dS_ij = P_ij (dP_ij - sum_k P_ik dP_ik)
+ *   dQ_i = scale sum_j dS_ij k_j      dK_j = scale sum_i dS_ij q_i
+ * dK and dV of a K/V head sum over the H / Hkv query heads that read it (the
+ * backward of repeat_kv's concatenation). dq [B, H, S, D], dk, dv
+ * [B, Hkv, S, D]. */
+void oracle_attention_bwd(int64_t B, int32_t H, int32_t Hkv, int64_t S, int32_t D, float scale, int causal,
+                          const float* q, const float* k, const float* v, const float* mask, const float* dout,
+                          float* dq, float* dk, float* dv, int threads) {
+    const int rep = H / Hkv;
+#pragma omp parallel num_threads(nthreads(threads))
+    {
+        double* p = (double*)malloc(sizeof(double) * (size_t)S);
+        double* dp = (double*)malloc(sizeof(double) * (size_t)S);
+        double* gk = (double*)malloc(sizeof(double) * (size_t)S * D);
+        double* gv = (double*)malloc(sizeof(double) * (size_t)S * D);
+        double* gq = (double*)malloc(sizeof(double) * (size_t)D);
+#pragma omp for schedule(dynamic, 1)
+        for (int64_t bhk = 0; bhk < B * Hkv; ++bhk) {
+            const int64_t b = bhk / Hkv, hk = bhk % Hkv;
+            const float* kh = k + bhk * S * D;
+            const float* vh = v + bhk * S * D;
+            for (int64_t e = 0; e < S * D; ++e) gk[e] = gv[e] = 0.0;
+            for (int64_t h = hk * rep; h < (hk + 1) * rep; ++h) {
+                const int64_t bh = b * H + h;
+                for (int64_t i = 0; i < S; ++i) {
+                    const float* qi = q + (bh * S + i) * D;
+                    const float* doi = dout + ((b * S + i) * H + h) * D;
+                    double z;
+                    attn_row(S, D, scale, causal, qi, kh, mask ? mask + i * S : NULL, i, p, &z);
+                    double dot = 0.0;
+                    for (int64_t j = 0; j < S; ++j) {
+                        double s = 0.0;
+                        const float* vj = vh + j * D;
+                        for (int d = 0; d < D; ++d) s += (double)doi[d] * (double)vj[d];
+                        dp[j] = s;
+                        dot += p[j] * s;
+                    }
+                    for (int d = 0; d < D; ++d) gq[d] = 0.0;
+                    for (int64_t j = 0; j < S; ++j) {
+                        if (p[j] == 0.0) continue;
+                        const double ds = p[j] * (dp[j] - dot) * (double)scale;
+                        const float* kj = kh + j * D;
+                        for (int d = 0; d < D; ++d) {
+                            gq[d] += ds * (double)kj[d];
+                            gk[j * D + d] += ds * (double)qi[d];
+                            gv[j * D + d] += p[j] * (double)doi[d];
+                        }
+                    }
+                    float* dqi = dq + (bh * S + i) * D;
+                    for (int d = 0; d < D; ++d) dqi[d] = (float)gq[d];
+                }
+            }
+            for (int64_t e = 0; e < S * D; ++e) {
+                dk[bhk * S * D + e] = (float)gk[e];
+                dv[bhk * S * D + e] = (float)gv[e];
+            }
+        }
+        free(p);
+        free(dp);
+        free(gk);
+        free(gv);
+        free(gq);
+    }
+}
+
 /* ------------------------------------------------------------------ bf16 */
 void oracle_round_bf16(const float* in, float* out, int64_t n) {
     for (int64_t i = 0; i < n; ++i) {

@@ -39,6 +39,18 @@
  *   oracle_softmax_bwd   finite differences, rows of dS sum to 0, masked zeros.
  *   oracle_philox4x32_10 Random123 known-answer vectors (Salmon et al., SC'11).
  *   oracle_dropout_mask  fraction kept ~ 1-p, independence of (seed, element).
+ *   oracle_attention_fwd closed forms (q = 0: uniform / prefix-mean rows of v;
+ *                        S = 1: o = v; a dominant key: o = its v row), an
+ *                        all-zero mask equals no mask (transformer.rs:469-480),
+ *                        torch.nn.functional.scaled_dot_product_attention on
+ *                        the CPU in fp64 as a library cross-check, GQA equal to
+ *                        explicitly repeated K/V heads.
+ *   oracle_attention_bwd central finite differences of <o, dO> in fp64 for
+ *                        q, k and v, torch autograd of the fp64 composite.
+ *
+ * Attention (src/models/transformer.rs:258-283, repeat_kv 295-319) is the
+ * first of the rows next to the hot path: the score row of the reference's
+ * q.k^T / sqrt(d) + mask, softmax_stable, .v sequence.
  */
 #ifndef MC_ORACLE_H
 #define MC_ORACLE_H
@@ -104,6 +116,16 @@ void oracle_softmax_bwd_rows(int64_t n, int64_t D, int64_t causal_rows, const in
                              const float* p, const float* dp, float* ds, int threads);
 
 /* Round-to-nearest-even fp32 -> bf16 -> fp32 (the rounding the bf16 inputs get). */
+/* Attention core: q [B, H, S, D], k, v [B, Hkv, S, D], mask [S, S] or NULL,
+ * o [B, S, H * D], lse [B, H, S] or NULL (natural log-sum-exp of each row). */
+void oracle_attention_fwd(int64_t B, int32_t H, int32_t Hkv, int64_t S, int32_t D, float scale, int causal,
+                          const float* q, const float* k, const float* v, const float* mask, float* o,
+                          float* lse, int threads);
+/* dq [B, H, S, D], dk, dv [B, Hkv, S, D] from dout [B, S, H * D]. */
+void oracle_attention_bwd(int64_t B, int32_t H, int32_t Hkv, int64_t S, int32_t D, float scale, int causal,
+                          const float* q, const float* k, const float* v, const float* mask, const float* dout,
+                          float* dq, float* dk, float* dv, int threads);
+
 void oracle_round_bf16(const float* in, float* out, int64_t n);
 
 #ifdef __cplusplus

@@ -90,3 +90,47 @@ def test_dropout_mask_matches_oracle(mc):
     m = mc.dropout_mask(1234, 0.1, 16384, 64).numpy()
     assert abs(m.mean() - 0.9) < 0.005
     assert mc._lib.lib().mc_dropout_mask(1, 1.0, 4, 4, ctypes.c_void_p(256)) == 5
+
+
+def _attn(mc, B=1, S=64, H=4, Hkv=2, D=64, causal=1, scale=0.125, dtype=1):
+    return mc._lib.AttnDesc(B, S, H, Hkv, D, causal, scale, dtype)
+
+
+@pytest.mark.parametrize("field,value,code,msg", [
+    ("kv_heads", 3, 2, "must be a multiple of kv_heads"),   # repeat_kv, transformer.rs:258-259
+    ("heads", 0, 2, "must be >= 1"),
+    ("seq", 0, 2, "must be >= 1"),
+    ("head_dim", 257, 2, "head_dim must be in [1, 256]"),
+    ("head_dim", 36, 2, "multiple of 8"),
+    ("causal", 2, 5, "causal must be 0 or 1"),
+    ("scale", float("nan"), 5, "scale must be finite"),
+    ("dtype", 9, 3, "unsupported dtype"),
+])
+def test_attention_desc_validation(mc, field, value, code, msg):
+    L = mc._lib.lib()
+    d = _attn(mc)
+    setattr(d, field, value)
+    assert L.mc_attention_fwd_workspace_size(ctypes.byref(d)) == 0
+    fake = ctypes.c_void_p(256)
+    st = L.mc_attention_fwd(ctypes.byref(d), fake, fake, fake, None, fake, None, fake, 1 << 30, None)
+    assert st == code
+    assert msg in mc._lib.last_error()
+
+
+def test_attention_null_workspace_and_layout_errors(mc):
+    L = mc._lib.lib()
+    d = _attn(mc)
+    fake = ctypes.c_void_p(256)
+    need = L.mc_attention_fwd_workspace_size(ctypes.byref(d))
+    assert need == 1 * 2 * 64 * 64 * 2  # V^T [B, Hkv, D, Sp] bf16
+    assert L.mc_attention_fwd(ctypes.byref(d), None, fake, fake, None, fake, None, fake, need, None) == 1
+    assert L.mc_attention_fwd(ctypes.byref(d), fake, fake, fake, None, fake, None, fake, need - 1, None) == 6
+    assert L.mc_attention_fwd(ctypes.byref(d), fake, ctypes.c_void_p(264), fake, None, fake, None, fake, need,
+                              None) == 4
+    # a mask of S * S fp32 beyond 2^31 bytes
+    big = _attn(mc, S=30000)
+    st = L.mc_attention_fwd(ctypes.byref(big), fake, fake, fake, fake, fake, None, fake, 1 << 40, None)
+    assert st == 2 and "explicit mask" in mc._lib.last_error()
+    # fp32 and other bf16 head dims take the workspace-free kernel
+    assert L.mc_attention_fwd_workspace_size(ctypes.byref(_attn(mc, dtype=0))) == 0
+    assert L.mc_attention_fwd_workspace_size(ctypes.byref(_attn(mc, D=32))) == 0

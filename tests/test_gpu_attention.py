@@ -1,0 +1,170 @@
+"""GPU parity of the attention core (mc_attention_fwd) against the CPU oracle
+(oracle_attention_fwd, pinned in tests/test_oracle_attention.py).
+
+Cases: the reference's attention test geometries (src/models/transformer.rs:
+443-480: H = 4 with 2 or 4 K/V heads, S = 8, D = 32, fp32, zero mask),
+sequence lengths around the 64-key / 128-query block edges for both head dims
+of the MFMA kernel (64, 128), GQA ratios 1, 2 and 6, causal / additive mask /
+both, -inf mask entries and a fully masked row, the workspace-free kernel
+(fp32, other bf16 head dims), and BASELINE c4's attention [8, 12, 2048, 128]
+with 2 K/V heads: there the oracle checks two whole K/V groups (6 heads, every
+query) and every output row is checked to lie within the range of the v rows
+it averages. Tolerance max|out-ref|/max|ref|: 1e-5 (fp32), 2e-2 (bf16); the
+log-sum-exp, computed from fp32 scores: 1e-4 (bf16), 1e-5 (fp32).
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from conftest import rel_err, to_np
+from inputs import gen
+
+pytestmark = pytest.mark.gpu
+
+F32_TOL, BF16_TOL = 1e-5, 2e-2
+
+
+def case(seed, B, H, Hkv, S, D, dtype, masked=False):
+    g = gen(seed)
+    q = torch.randn(B, H, S, D, generator=g).to(dtype)
+    k = torch.randn(B, Hkv, S, D, generator=g).to(dtype)
+    v = torch.randn(B, Hkv, S, D, generator=g).to(dtype)
+    mask = torch.randn(S, S, generator=g) if masked else None
+    return q, k, v, mask
+
+
+def run(mc, dev, q, k, v, mask, causal, scale=None):
+    o, lse = mc.attention_forward(q.to(dev), k.to(dev), v.to(dev), causal=causal, scale=scale,
+                                  mask=None if mask is None else mask.to(dev))
+    torch.cuda.synchronize()
+    return o, lse
+
+
+def ref(q, k, v, mask, causal, scale=None):
+    D = q.shape[-1]
+    return oracle.attention_fwd(q.float().numpy(), k.float().numpy(), v.float().numpy(),
+                                D ** -0.5 if scale is None else scale, causal=causal,
+                                mask=None if mask is None else mask.numpy())
+
+
+def check(o, lse, o_ref, lse_ref, dtype):
+    tol = F32_TOL if dtype == torch.float32 else BF16_TOL
+    assert rel_err(o, o_ref) <= tol
+    assert rel_err(lse, lse_ref) <= (F32_TOL if dtype == torch.float32 else 1e-4)
+
+
+@pytest.mark.parametrize("B,H,Hkv,S,D,causal,masked", [
+    (1, 4, 2, 8, 32, False, False),   # test_attention_forward (transformer.rs:456-466)
+    (1, 4, 4, 8, 32, False, True),    # test_attention_with_mask (transformer.rs:469-480)
+    (2, 6, 2, 37, 16, True, False),
+    (1, 4, 1, 64, 128, True, True),
+    (2, 2, 2, 130, 64, False, False),
+    (1, 3, 3, 5, 200, True, False),
+])
+def test_attention_fwd_f32(mc, dev, B, H, Hkv, S, D, causal, masked):
+    q, k, v, mask = case(B * 1000 + S, B, H, Hkv, S, D, torch.float32, masked)
+    o, lse = run(mc, dev, q, k, v, mask, causal)
+    o_ref, lse_ref = ref(q, k, v, mask, causal)
+    check(o, lse, o_ref, lse_ref, torch.float32)
+
+
+def test_attention_reference_zero_mask_f32(mc, dev):
+    # test_attention_with_mask passes a [1, 1, 8, 8] zero mask: same result as none
+    q, k, v, _ = case(1, 1, 4, 4, 8, 32, torch.float32)
+    a, la = run(mc, dev, q, k, v, None, False)
+    b, lb = run(mc, dev, q, k, v, torch.zeros(8, 8), False)
+    assert torch.equal(a, b) and torch.equal(la, lb)
+
+
+MFMA_CASES = [
+    # B, H, Hkv, S, D, causal
+    (1, 4, 4, 1, 64, False), (1, 4, 4, 1, 128, True),
+    (1, 4, 2, 7, 128, True), (2, 4, 2, 63, 64, True),
+    (1, 4, 2, 64, 128, False), (1, 4, 2, 64, 128, True),
+    (1, 2, 1, 65, 64, True), (2, 12, 2, 127, 128, True),
+    (1, 12, 2, 128, 128, True), (1, 12, 2, 129, 128, False),
+    (1, 12, 2, 129, 64, True), (2, 6, 6, 200, 128, True),
+    (1, 4, 2, 256, 64, False), (1, 12, 2, 333, 128, True),
+    (1, 14, 2, 300, 64, True), (2, 28, 4, 192, 128, True),
+]
+
+
+@pytest.mark.parametrize("B,H,Hkv,S,D,causal", MFMA_CASES)
+def test_attention_fwd_bf16(mc, dev, B, H, Hkv, S, D, causal):
+    q, k, v, _ = case(7 * S + D + H, B, H, Hkv, S, D, torch.bfloat16)
+    o, lse = run(mc, dev, q, k, v, None, causal)
+    o_ref, lse_ref = ref(q, k, v, None, causal)
+    check(o, lse, o_ref, lse_ref, torch.bfloat16)
+
+
+@pytest.mark.parametrize("S,D,causal", [(100, 128, False), (256, 128, True), (77, 64, True), (130, 64, False)])
+def test_attention_fwd_bf16_mask(mc, dev, S, D, causal):
+    q, k, v, mask = case(S + D, 2, 4, 2, S, D, torch.bfloat16, masked=True)
+    mask[:, S - 3:] = float("-inf")  # padded keys, as an attention_mask would mark them
+    o, lse = run(mc, dev, q, k, v, mask, causal)
+    o_ref, lse_ref = ref(q, k, v, mask, causal)
+    check(o, lse, o_ref, lse_ref, torch.bfloat16)
+
+
+@pytest.mark.parametrize("D", [32, 96, 8])
+def test_attention_fwd_bf16_generic_head_dims(mc, dev, D):
+    q, k, v, mask = case(D, 2, 4, 2, 45, D, torch.bfloat16, masked=True)
+    o, lse = run(mc, dev, q, k, v, mask, True)
+    o_ref, lse_ref = ref(q, k, v, mask, True)
+    check(o, lse, o_ref, lse_ref, torch.bfloat16)
+
+
+@pytest.mark.parametrize("dtype,D", [(torch.bfloat16, 128), (torch.bfloat16, 64), (torch.float32, 32)])
+def test_attention_fully_masked_row_is_nan(mc, dev, dtype, D):
+    q, k, v, _ = case(3, 1, 2, 1, 70, D, dtype)
+    mask = torch.zeros(70, 70)
+    mask[5, :] = float("-inf")
+    o, lse = run(mc, dev, q, k, v, mask, False)
+    o = to_np(o)
+    assert np.isnan(o[0, 5]).all()
+    assert np.isfinite(np.delete(o[0], 5, axis=0)).all()
+    assert to_np(lse)[0, :, 5].tolist() == [float("-inf")] * 2
+
+
+def test_attention_scale_argument(mc, dev):
+    q, k, v, _ = case(11, 1, 4, 2, 96, 128, torch.bfloat16)
+    o, lse = run(mc, dev, q, k, v, None, True, scale=0.05)
+    o_ref, lse_ref = ref(q, k, v, None, True, scale=0.05)
+    check(o, lse, o_ref, lse_ref, torch.bfloat16)
+
+
+def test_attention_deterministic(mc, dev):
+    q, k, v, _ = case(12, 2, 12, 2, 300, 128, torch.bfloat16)
+    a, la = run(mc, dev, q, k, v, None, True)
+    b, lb = run(mc, dev, q, k, v, None, True)
+    assert torch.equal(a, b) and torch.equal(la, lb)
+
+
+def test_attention_c4_shape(mc, dev):
+    """BASELINE c4's attention: [8, 12, 2048, 128], 2 K/V heads, causal."""
+    B, H, Hkv, S, D = 8, 12, 2, 2048, 128
+    g = gen(2048)
+    q = torch.randn(B, H, S, D, generator=g).to(torch.bfloat16)
+    k = torch.randn(B, Hkv, S, D, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, Hkv, S, D, generator=g).to(torch.bfloat16)
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    o, lse = mc.attention_forward(qd, kd, vd, causal=True)
+    torch.cuda.synchronize()
+    # two whole K/V groups against the oracle (all 6 heads, every query)
+    rep = H // Hkv
+    for b, hk in ((0, 0), (7, 1)):
+        hs = slice(hk * rep, (hk + 1) * rep)
+        o_ref, lse_ref = oracle.attention_fwd(q[b:b + 1, hs].float().numpy(), k[b:b + 1, hk:hk + 1].float().numpy(),
+                                              v[b:b + 1, hk:hk + 1].float().numpy(), D ** -0.5, causal=True)
+        assert rel_err(o[b:b + 1, :, hs.start * D:hs.stop * D], o_ref) <= BF16_TOL
+        assert rel_err(lse[b:b + 1, hs], lse_ref) <= 1e-4
+    # every row: a convex combination of the v rows of its causal prefix
+    vf = vd.float()
+    lo = torch.cummin(vf, dim=2).values.repeat_interleave(rep, dim=1)  # [B, H, S, D]
+    hi = torch.cummax(vf, dim=2).values.repeat_interleave(rep, dim=1)
+    of = o.float().view(B, S, H, D).transpose(1, 2)
+    assert torch.isfinite(of).all()
+    slack = 1e-2 * (hi - lo).abs() + 1e-2
+    assert bool(((of >= lo - slack) & (of <= hi + slack)).all())
+    assert torch.isfinite(lse).all()
