@@ -25,6 +25,7 @@
  *   mc_attention_fwd the attention core of Attention::forward
  *                    (src/models/transformer.rs:258-283) with repeat_kv
  *                    (295-319), without materialising the score matrix.
+ *   mc_attention_bwd no reference kernel: autograd of the same composite.
  *
  * Conventions (all entry points):
  *  - Device buffers are caller-owned, row-major and contiguous; inputs are
@@ -171,6 +172,21 @@ size_t mc_attention_fwd_workspace_size(const mc_attn_desc* d);
 mc_status mc_attention_fwd(const mc_attn_desc* d, const void* q, const void* k, const void* v,
                            const float* mask, void* o, float* lse, void* workspace,
                            size_t workspace_bytes, hipStream_t stream);
+
+size_t mc_attention_bwd_workspace_size(const mc_attn_desc* d);
+
+/* Backward of mc_attention_fwd (no reference kernel: candle autograd of
+ * transformer.rs:264-283): from o and lse of the forward and the output
+ * gradient dout [B, S, H * D],
+ *   P = exp(scores - lse), dP = dout.v^T, dS = P (.) (dP - rowsum(dout (.) o))
+ *   dq = scale dS.k   [B, H, S, D]
+ *   dk = scale dS^T.q, dv = P^T.dout   [B, Hkv, S, D], each summed over the
+ *        H / Hkv query heads that read the K/V head (backward of repeat_kv)
+ * Every reduction runs in a fixed order: results are bitwise reproducible. */
+mc_status mc_attention_bwd(const mc_attn_desc* d, const void* q, const void* k, const void* v,
+                           const float* mask, const void* o, const float* lse, const void* dout,
+                           void* dq, void* dk, void* dv, void* workspace, size_t workspace_bytes,
+                           hipStream_t stream);
 
 /* Host-side dropout keep-mask [rows, rank] from a seed (Philox4x32-10; element
  * i = t*rank + j uses counter block i/4, word i%4, key = seed; keep iff

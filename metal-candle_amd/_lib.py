@@ -85,6 +85,8 @@ _SIGNATURES = {
     "mc_softmax_bwd": (ctypes.c_int, [_i64, _i64, _i64, _i32, _vp, _vp, _vp, _vp]),
     "mc_attention_fwd_workspace_size": (_sz, [_ap]),
     "mc_attention_fwd": (ctypes.c_int, [_ap, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "mc_attention_bwd_workspace_size": (_sz, [_ap]),
+    "mc_attention_bwd": (ctypes.c_int, [_ap, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "mc_dropout_mask": (ctypes.c_int, [ctypes.c_uint64, _f32, _i64, _i32, _vp]),
     "mc_profile_enable": (ctypes.c_int, [_i32]),
     "mc_profile_collect": (ctypes.c_int, []),

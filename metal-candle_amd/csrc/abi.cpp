@@ -109,6 +109,10 @@ mc_status check_attn_desc(const mc_attn_desc* d, const char* op) {
              "%s: bf16 head_dim must be a multiple of 8, got %d", op, (int)d->head_dim);
     MC_CHECK(d->causal == 0 || d->causal == 1, MC_ERR_VALUE, "%s: causal must be 0 or 1", op);
     MC_CHECK(std::isfinite(d->scale), MC_ERR_VALUE, "%s: scale must be finite", op);
+    // buffer offsets inside one batch slice of [S, H, D] stay below 2^31 bytes
+    MC_CHECK((double)d->seq * d->heads * d->head_dim * 4.0 < 2147483647.0, MC_ERR_SHAPE,
+             "%s: S * H * D (%lld x %d x %d) too large for one batch slice", op, (long long)d->seq, (int)d->heads,
+             (int)d->head_dim);
     const double elems = (double)d->batch * d->heads * d->seq * d->head_dim;
     MC_CHECK(elems < 9.0e15 && (double)d->batch * d->heads * d->seq < 2.0e9, MC_ERR_SHAPE,
              "%s: problem too large (B * H * S must stay below 2^31)", op);
@@ -298,6 +302,37 @@ mc_status mc_attention_fwd(const mc_attn_desc* d, const void* q, const void* k, 
     mc::prof::Scope sc(mc::prof::kAttention, stream, 4.0 * attn_pairs(d) * d->head_dim,
                        es * (2.0 * qo + 2.0 * kv) + (lse ? 4.0 * d->batch * d->heads * d->seq : 0.0));
     return hip_status(mc::launch_attention_fwd(*d, q, k, v, mask, o, lse, workspace, stream), "Attention forward");
+}
+
+size_t mc_attention_bwd_workspace_size(const mc_attn_desc* d) {
+    if (check_attn_desc(d, "Attention backward") != MC_OK) return 0;
+    return mc::attention_bwd_ws(*d).total;
+}
+
+mc_status mc_attention_bwd(const mc_attn_desc* d, const void* q, const void* k, const void* v, const float* mask,
+                           const void* o, const float* lse, const void* dout, void* dq, void* dk, void* dv,
+                           void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    mc_status s = check_attn_desc(d, "Attention backward");
+    if (s != MC_OK) return s;
+    MC_CHECK(q && k && v && o && lse && dout && dq && dk && dv, MC_ERR_NULL,
+             "Attention backward: q, k, v, o, lse, dout, dq, dk and dv must not be NULL");
+    MC_CHECK(!mask || (double)d->seq * d->seq * 4.0 < 2147483647.0, MC_ERR_SHAPE,
+             "Attention backward: an explicit mask needs S * S * 4 < 2^31 bytes (S = %lld)", (long long)d->seq);
+    MC_CHECK(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o) && aligned16(dout) && aligned16(dq) &&
+                 aligned16(dk) && aligned16(dv),
+             MC_ERR_LAYOUT, "Attention backward: q, k, v, o, dout, dq, dk and dv must be 16-byte aligned");
+    const size_t need = mc::attention_bwd_ws(*d).total;
+    MC_CHECK(workspace_bytes >= need && (need == 0 || workspace), MC_ERR_WORKSPACE,
+             "Attention backward: workspace of %zu bytes required, %zu given", need, workspace_bytes);
+    MC_CHECK(aligned16(workspace), MC_ERR_LAYOUT, "Attention backward: workspace must be 16-byte aligned");
+    const double es = d->dtype == MC_F32 ? 4.0 : 2.0;
+    const double qo = (double)d->batch * d->heads * d->seq * d->head_dim;
+    const double kv = (double)d->batch * d->kv_heads * d->seq * d->head_dim;
+    // dS.K, dS^T.Q, P^T.dO and dO.V^T: four products over the computed score pairs
+    mc::prof::Scope sc(mc::prof::kAttention, stream, 8.0 * attn_pairs(d) * d->head_dim,
+                       es * (4.0 * qo + 4.0 * kv) + 4.0 * d->batch * d->heads * d->seq);
+    return hip_status(mc::launch_attention_bwd(*d, q, k, v, mask, o, lse, dout, dq, dk, dv, workspace, stream),
+                      "Attention backward");
 }
 
 // Philox4x32-10 (Salmon et al., SC'11), 10 rounds of the two 32x32->64

@@ -32,6 +32,8 @@
 //
 // Other head dims and fp32: attn_fwd_generic, one wave per query row (lanes
 // over the head dim), online softmax in fp32.
+#include <algorithm>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -364,6 +366,628 @@ __global__ __launch_bounds__(256) void attn_fwd_generic(const T* __restrict__ q,
     if (lse && lane == 0) lse[bh * S + qi] = m + __logf(l);
 }
 
+// ================================================================ backward
+// Gradients of the forward (candle autograd of transformer.rs:264-278; the
+// reference has no kernel): with P = softmax(scores), dO the output gradient
+// [B, S, H, D], Delta_i = sum_d dO_id O_id and lse_i the forward's
+// log-sum-exp,
+//   P_ij = exp(scale q_i.k_j + mask_ij - lse_i)      (recomputed)
+//   dP_ij = dO_i . v_j,   dS_ij = P_ij (dP_ij - Delta_i)
+//   dV_j = sum_i P_ij dO_i,   dK_j = scale sum_i dS_ij q_i,   dQ_i = scale sum_j dS_ij k_j
+// and dK / dV of a K/V head sum over the H / Hkv query heads that read it.
+// Every sum runs in a fixed order: results are bitwise reproducible.
+//
+// bf16, D = 64 or 128:
+//  attn_bwd_prep_bf16  per (b, h, 64 queries): Delta, lse * log2 e (both
+//                      into one [2][64] fp32 block per query block), and Q^T,
+//                      dO^T [D, Sp] with the perm16 position order.
+//  attn_vt_bf16        K^T (the V^T prepass of the forward, applied to K).
+//  attn_bwd_dkdv_bf16  one workgroup per (b, h, 128 keys), 4 waves of 32 keys;
+//                      per block of 64 queries (Q, dO, Q^T, dO^T and the
+//                      lse/Delta block through LDS, two stages):
+//                        S = Q.K^T, dP = dO.V^T    (lane = key: K, V held in
+//                                                   registers as B operands)
+//                        dV^T += dO^T.P,  dK^T += Q^T.dS   (P, dS straight from
+//                                                   the accumulators as the
+//                                                   B operand)
+//                      dK, dV per query head: written directly when H = Hkv,
+//                      else as fp32 partials summed by attn_bwd_sum.
+//  attn_bwd_dq_bf16    one workgroup per (b, h, 128 queries) as the forward:
+//                        S^T = K.Q^T, dP^T = V.dO^T (lane = query: Q, dO held
+//                                                   in registers)
+//                        dQ^T += K^T.dS^T         (K^T from the prepass)
+struct AttnBwdArgs {
+    const uint16_t* q;     // [B, H, S, D]
+    const uint16_t* k;     // [B, Hkv, S, D]
+    const uint16_t* v;     // [B, Hkv, S, D]
+    const uint16_t* dout;  // [B, S, H, D]
+    const uint16_t* qt;    // [B, H, D, Sp]
+    const uint16_t* dot;   // [B, H, D, Sp]
+    const uint16_t* kt;    // [B, Hkv, D, Sp]
+    const float* mask;     // [S, S] or null
+    const float* lsd;      // [B, H, Sp / 64, 2, 64]: lse * log2 e, Delta
+    uint16_t* dq;          // [B, H, S, D]
+    uint16_t* dk;          // [B, Hkv, S, D] (H == Hkv)
+    uint16_t* dv;
+    float* dk_part;        // [B, H, S, D] fp32 (H > Hkv)
+    float* dv_part;
+    int64_t S, Sp;
+    int B, H, Hkv, causal, nblk;
+    float scale, scale_log2;
+};
+
+// [64 rows][D] tile into the swizzled LDS layout from rows row0 .. row0+63 of
+// a buffer with row stride ld (elements); rows past the buffer load zeros.
+template <int D>
+__device__ __forceinline__ void dma_rows(i32x4 r, uint32_t lds_byte, uint32_t row0, uint32_t ld, int wave,
+                                         int lane) {
+    constexpr int CPR = D / 8, RPI = 64 / CPR, LOADS = 64 / RPI / 4;
+#pragma unroll
+    for (int j = 0; j < LOADS; ++j) {
+        const int blk = wave * LOADS + j;
+        const int row = blk * RPI + lane / CPR;
+        const uint32_t chunk = (uint32_t)swz<D>(row, lane % CPR);
+        const uint32_t off = ((row0 + (uint32_t)row) * ld + 8u * chunk) * 2u;
+        dma16(r, __builtin_amdgcn_readfirstlane(lds_byte + (uint32_t)blk * 1024u), off);
+    }
+}
+
+// [D rows][64 positions] tile (positions pos0 .. pos0+63 of a transposed
+// buffer with row stride Sp) into the swizzled LDS layout.
+template <int D>
+__device__ __forceinline__ void dma_cols(i32x4 r, uint32_t lds_byte, uint32_t pos0, uint32_t Sp, int wave,
+                                         int lane) {
+    constexpr int LOADS = D / 8 / 4;
+#pragma unroll
+    for (int j = 0; j < LOADS; ++j) {
+        const int blk = wave * LOADS + j;
+        const int row = blk * 8 + lane / 8;
+        const uint32_t chunk = (uint32_t)swz<64>(row, lane % 8);
+        const uint32_t off = ((uint32_t)row * Sp + pos0 + 8u * chunk) * 2u;
+        dma16(r, __builtin_amdgcn_readfirstlane(lds_byte + (uint32_t)blk * 1024u), off);
+    }
+}
+
+template <int D>
+__device__ __forceinline__ bf16x8 frag_rows(const uint16_t* t, int row, int c) {
+    return *reinterpret_cast<const bf16x8*>(&t[row * D + 8 * swz<D>(row, c)]);
+}
+__device__ __forceinline__ bf16x8 frag_cols(const uint16_t* t, int row, int c) {
+    return *reinterpret_cast<const bf16x8*>(&t[row * 64 + 8 * swz<64>(row, c)]);
+}
+
+// Rows of a wave's transposed accumulators (acc[dt] element j = dim
+// 32 dt + 8 (j/4) + 4 half + j%4 of row `col`) through a per-wave LDS patch
+// to 16-byte stores of rows row0 + r (r < 32, row0 + r < nrows) of dst
+// (row stride ld elements). OutT: uint16_t (bf16) or float.
+template <int D, typename OutT>
+__device__ __forceinline__ void store_rows(const f32x16 (&acc)[D / 32], float scale, void* patch_mem, OutT* dst,
+                                           int64_t ld, int64_t row0, int64_t nrows, int lane) {
+    constexpr int EPC = 16 / sizeof(OutT);    // elements per 16-byte chunk
+    constexpr int PROW = D + 16 / sizeof(OutT);  // padded patch row (elements)
+    constexpr int CPR = D / EPC;
+    OutT* patch = static_cast<OutT*>(patch_mem);
+    const int col = lane & 31, half = lane >> 5;
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+        for (int jq = 0; jq < 4; ++jq) {
+            const int d = 32 * dt + 8 * jq + 4 * half;
+            if constexpr (sizeof(OutT) == 2) {
+                const uint32_t lo = pack_bf16x2(acc[dt][4 * jq] * scale, acc[dt][4 * jq + 1] * scale);
+                const uint32_t hi = pack_bf16x2(acc[dt][4 * jq + 2] * scale, acc[dt][4 * jq + 3] * scale);
+                *reinterpret_cast<uint2*>(&patch[col * PROW + d]) = make_uint2(lo, hi);
+            } else {
+                *reinterpret_cast<float4*>(&patch[col * PROW + d]) =
+                    make_float4(acc[dt][4 * jq] * scale, acc[dt][4 * jq + 1] * scale, acc[dt][4 * jq + 2] * scale,
+                                acc[dt][4 * jq + 3] * scale);
+            }
+        }
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the wave's patch is written
+#pragma unroll
+    for (int it = 0; it < 32 * CPR / 64; ++it) {
+        const int i = it * 64 + lane;
+        const int r = i / CPR, c = i % CPR;
+        if (row0 + r < nrows) {
+            const uint4 v = *reinterpret_cast<const uint4*>(&patch[r * PROW + EPC * c]);
+            *reinterpret_cast<uint4*>(dst + (row0 + r) * ld + EPC * c) = v;
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // patch reads done before it is rewritten
+}
+
+// --------------------------------------------------------- backward prep
+template <int D>
+__global__ __launch_bounds__(256) void attn_bwd_prep_bf16(const uint16_t* __restrict__ q,
+                                                          const uint16_t* __restrict__ o,
+                                                          const uint16_t* __restrict__ dout,
+                                                          const float* __restrict__ lse, int H, int64_t S,
+                                                          int64_t Sp, float* __restrict__ lsd,
+                                                          uint16_t* __restrict__ qt, uint16_t* __restrict__ dot) {
+    constexpr int CPR = D / 8;
+    __shared__ __attribute__((aligned(16))) uint16_t tile[2][64][D + 8];
+    const int64_t bh = blockIdx.y;
+    const int64_t b = bh / H, h = bh % H;
+    const int64_t q0 = (int64_t)blockIdx.x * 64;
+    const int64_t ldo = (int64_t)H * D;
+    const __amdgpu_buffer_rsrc_t rq = make_rsrc(q + bh * S * D, S * D * 2);
+    const __amdgpu_buffer_rsrc_t ro = make_rsrc(o + (b * S * H + h) * D, (S * H - h) * D * 2);
+    const __amdgpu_buffer_rsrc_t rd = make_rsrc(dout + (b * S * H + h) * D, (S * H - h) * D * 2);
+    for (int i = threadIdx.x; i < 64 * CPR; i += 256) {
+        const int row = i / CPR, c = i % CPR;
+        const bool ok = q0 + row < S;
+        const uint32_t oq = ok ? (uint32_t)(((q0 + row) * D + 8 * c) * 2) : kOOB;
+        const uint32_t od = ok ? (uint32_t)(((q0 + row) * ldo + 8 * c) * 2) : kOOB;
+        *reinterpret_cast<i32x4*>(&tile[0][row][8 * c]) = buf_load16(rq, oq);
+        *reinterpret_cast<i32x4*>(&tile[1][row][8 * c]) = buf_load16(rd, od);
+    }
+    // Delta = rowsum(dO * O): 4 threads per query row, D / 4 dims each
+    {
+        const int row = threadIdx.x >> 2, part = threadIdx.x & 3;
+        const bool ok = q0 + row < S;
+        float acc = 0.f;
+#pragma unroll
+        for (int c = 0; c < CPR / 4; ++c) {
+            const uint32_t off = ok ? (uint32_t)(((q0 + row) * ldo + 8 * (part * (CPR / 4) + c)) * 2) : kOOB;
+            float a[8], g[8];
+            BVec<uint16_t>::unpack(buf_load16(ro, off), a);
+            BVec<uint16_t>::unpack(buf_load16(rd, off), g);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc += a[e] * g[e];
+        }
+        acc += __shfl_xor(acc, 1, kWave);
+        acc += __shfl_xor(acc, 2, kWave);
+        if (part == 0) {
+            float* blk = lsd + (bh * (Sp / 64) + blockIdx.x) * 128;
+            // padded queries: lse = +inf makes their P exactly 0
+            blk[row] = ok ? lse[bh * S + q0 + row] * kLog2e : __builtin_inff();
+            blk[64 + row] = ok ? acc : 0.f;
+        }
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < 2 * D * 8; i += 256) {
+        const int which = i / (D * 8), d = (i >> 3) % D, c = i & 7;
+        uint32_t w[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int p0 = 8 * c + 2 * e, p1 = p0 + 1;
+            const int r0 = (p0 & ~15) | perm16(p0 & 15), r1 = (p1 & ~15) | perm16(p1 & 15);
+            w[e] = (uint32_t)tile[which][r0][d] | ((uint32_t)tile[which][r1][d] << 16);
+        }
+        uint16_t* dst = (which ? dot : qt) + bh * D * Sp + q0;
+        *reinterpret_cast<uint4*>(dst + (int64_t)d * Sp + 8 * c) = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+}
+
+// ------------------------------------------------------------ dK and dV
+template <int D>
+__global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_bf16(AttnBwdArgs a) {
+    constexpr int KS = D / 16, DT = D / 32;
+    constexpr int TILE = 64 * D;                 // one [64][D] or [D][64] tile
+    constexpr int STAGE = 4 * TILE + 512;        // Q, dO, Q^T, dO^T, lse/Delta (1 KB)
+    __shared__ __attribute__((aligned(1024))) uint16_t smem[2 * STAGE];
+    const uint32_t smem_byte = (uint32_t)reinterpret_cast<uintptr_t>(smem);
+    const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+    const int col = lane & 31, half = lane >> 5;
+    const int nbh = a.B * a.H;
+    const int kb = (int)(blockIdx.x / nbh);      // key block 0 sees the most queries: dispatched first
+    const int bh = (int)(blockIdx.x % nbh);
+    const int b = bh / a.H, h = bh % a.H;
+    const int rep = a.H / a.Hkv;
+    const int64_t bhk = (int64_t)b * a.Hkv + h / rep;
+    const int64_t S = a.S;
+    const int64_t key0 = (int64_t)kb * 128;
+    const int64_t kw = key0 + 32 * wave;         // first key of this wave
+    const int64_t my_key = kw + col;
+
+    // K and V fragments (B operands of S = Q.K^T and dP = dO.V^T): key my_key, dims 16 s + 8 half .. +7
+    const __amdgpu_buffer_rsrc_t rk = make_rsrc(a.k + bhk * S * D, S * D * 2);
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(a.v + bhk * S * D, S * D * 2);
+    bf16x8 kf[KS], vf[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+        const uint32_t off = my_key < S ? (uint32_t)((my_key * D + 16 * s + 8 * half) * 2) : kOOB;
+        kf[s] = __builtin_bit_cast(bf16x8, buf_load16(rk, off));
+        vf[s] = __builtin_bit_cast(bf16x8, buf_load16(rv, off));
+    }
+
+    const i32x4 rq = rsrc_words(a.q + (int64_t)bh * S * D, S * D * 2);
+    const i32x4 rdo = rsrc_words(a.dout + ((int64_t)b * S * a.H + h) * D, (S * a.H - h) * D * 2);
+    const i32x4 rqt = rsrc_words(a.qt + (int64_t)bh * D * a.Sp, (int64_t)D * a.Sp * 2);
+    const i32x4 rdot = rsrc_words(a.dot + (int64_t)bh * D * a.Sp, (int64_t)D * a.Sp * 2);
+    const i32x4 rl = rsrc_words(a.lsd + (int64_t)bh * (a.Sp / 64) * 128, (a.Sp / 64) * 128 * 4);
+    const __amdgpu_buffer_rsrc_t rm = make_rsrc(a.mask, a.mask ? S * S * 4 : 0);
+
+    const int nqb = (int)((S + 63) / 64);
+    const int qstart = a.causal ? (int)(key0 / 64) : 0;  // earlier query blocks see none of these keys
+    // this wave: query blocks whose last query reaches its first key
+    const int wstart = a.causal ? (int)(kw / 64) : 0;
+    const bool active = kw < S;
+
+    auto issue = [&](int qb, int stage) {
+        const uint32_t base = smem_byte + (uint32_t)(stage * STAGE * 2);
+        const uint32_t q0 = (uint32_t)qb * 64;
+        dma_rows<D>(rq, base, q0, D, wave, lane);
+        dma_rows<D>(rdo, base + TILE * 2, q0, (uint32_t)(a.H * D), wave, lane);
+        dma_cols<D>(rqt, base + 2 * TILE * 2, q0, (uint32_t)a.Sp, wave, lane);
+        dma_cols<D>(rdot, base + 3 * TILE * 2, q0, (uint32_t)a.Sp, wave, lane);
+        if (wave == 0)  // the [2][64] fp32 lse/Delta block (512 B; lanes 32-63 fall outside and write zeros)
+            dma16(rl, __builtin_amdgcn_readfirstlane(base + 4 * TILE * 2),
+                  lane < 32 ? (uint32_t)(qb * 512 + lane * 16) : kOOB);
+    };
+
+    f32x16 dvacc[DT], dkacc[DT];
+#pragma unroll
+    for (int t = 0; t < DT; ++t)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) dvacc[t][j] = dkacc[t][j] = 0.f;
+
+    if (qstart < nqb) issue(qstart, 0);
+    for (int qb = qstart; qb < nqb; ++qb) {
+        wait_vmcnt<0>();
+        __syncthreads();
+        if (qb + 1 < nqb) issue(qb + 1, (qb + 1 - qstart) & 1);
+        if (!active || qb < wstart) continue;  // wave-uniform
+        const uint16_t* sq = smem + ((qb - qstart) & 1) * STAGE;
+        const uint16_t* sdo = sq + TILE;
+        const uint16_t* sqt = sq + 2 * TILE;
+        const uint16_t* sdot = sq + 3 * TILE;
+        const float* sl = reinterpret_cast<const float*>(sq + 4 * TILE);
+        const int64_t q0 = (int64_t)qb * 64;
+
+        f32x16 sacc[2], dpacc[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) sacc[t][j] = dpacc[t][j] = 0.f;
+#pragma unroll
+        for (int s = 0; s < KS; ++s)
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                sacc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_rows<D>(sq, 32 * t + col, 2 * s + half),
+                                                                 kf[s], sacc[t], 0, 0, 0);
+                dpacc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_rows<D>(sdo, 32 * t + col, 2 * s + half),
+                                                                  vf[s], dpacc[t], 0, 0, 0);
+            }
+
+        // accumulator j of tile t: query q0 + 32 t + 8 (j/4) + 4 half + j%4, key my_key
+        const bool edge = a.causal && q0 < kw + 31;
+        bf16x8 pb[2][2], db[2][2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int jq = 0; jq < 4; ++jq) {
+                const int qi = 32 * t + 8 * jq + 4 * half;  // first of 4 consecutive queries
+                const float4 l2 = *reinterpret_cast<const float4*>(&sl[qi]);
+                const float4 dl = *reinterpret_cast<const float4*>(&sl[64 + qi]);
+                const float lv[4] = {l2.x, l2.y, l2.z, l2.w}, dv4[4] = {dl.x, dl.y, dl.z, dl.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int j = 4 * jq + e;
+                    const int64_t qq = q0 + qi + e;
+                    float x = sacc[t][j] * a.scale_log2;
+                    if (a.mask) {
+                        const uint32_t off = (qq < S && my_key < S) ? (uint32_t)((qq * S + my_key) * 4) : kOOB;
+                        x += __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(rm, (int)off, 0, 0)) * kLog2e;
+                    }
+                    if (edge && my_key > qq) x = kNegInf;
+                    const float p = exp2f(x - lv[e]);
+                    const float ds = p * (dpacc[t][j] - dv4[e]);
+                    pb[t][j >> 3][j & 7] = static_cast<__bf16>(p);
+                    db[t][j >> 3][j & 7] = static_cast<__bf16>(ds);
+                }
+            }
+
+        // dV^T (d x key) += dO^T . P ; dK^T += Q^T . dS ; query positions 16 (2t + kk) + 8 half .. +7
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+            const int row = 32 * dt + col;
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int kk = 0; kk < 2; ++kk) {
+                    const int chunk = 4 * t + 2 * kk + half;
+                    dvacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_cols(sdot, row, chunk), pb[t][kk],
+                                                                       dvacc[dt], 0, 0, 0);
+                    dkacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_cols(sqt, row, chunk), db[t][kk],
+                                                                       dkacc[dt], 0, 0, 0);
+                }
+        }
+    }
+
+    __syncthreads();
+    void* patch = smem + wave * 32 * (D + 8) * 2;  // 32 rows of up to D + 4 floats per wave
+    if (rep == 1) {
+        store_rows<D, uint16_t>(dvacc, 1.f, patch, a.dv + bhk * S * D, D, kw, S, lane);
+        store_rows<D, uint16_t>(dkacc, a.scale, patch, a.dk + bhk * S * D, D, kw, S, lane);
+    } else {
+        store_rows<D, float>(dvacc, 1.f, patch, a.dv_part + (int64_t)bh * S * D, D, kw, S, lane);
+        store_rows<D, float>(dkacc, a.scale, patch, a.dk_part + (int64_t)bh * S * D, D, kw, S, lane);
+    }
+}
+
+// dk / dv [B, Hkv, S, D] = sum over the rep query heads of each K/V head of
+// the fp32 partials, in head order; 8 elements per thread.
+__global__ __launch_bounds__(256) void attn_bwd_sum(const float* __restrict__ dk_part,
+                                                    const float* __restrict__ dv_part, uint16_t* __restrict__ dk,
+                                                    uint16_t* __restrict__ dv, int rep, int64_t per_head,
+                                                    int64_t n8) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < 2 * n8;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const bool second = i >= n8;
+        const int64_t e = (second ? i - n8 : i) * 8;  // element of [B, Hkv, S, D]
+        const int64_t bhk = e / per_head, off = e % per_head;
+        const float* src = (second ? dv_part : dk_part) + bhk * rep * per_head + off;
+        float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        for (int r = 0; r < rep; ++r) {
+            const float4 x0 = *reinterpret_cast<const float4*>(src + r * per_head);
+            const float4 x1 = *reinterpret_cast<const float4*>(src + r * per_head + 4);
+            acc[0] += x0.x; acc[1] += x0.y; acc[2] += x0.z; acc[3] += x0.w;
+            acc[4] += x1.x; acc[5] += x1.y; acc[6] += x1.z; acc[7] += x1.w;
+        }
+        uint16_t* dst = (second ? dv : dk) + e;
+        *reinterpret_cast<uint4*>(dst) = make_uint4(pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3]),
+                                                    pack_bf16x2(acc[4], acc[5]), pack_bf16x2(acc[6], acc[7]));
+    }
+}
+
+// ------------------------------------------------------------------- dQ
+template <int D>
+__global__ __launch_bounds__(256, 1) void attn_bwd_dq_bf16(AttnBwdArgs a) {
+    constexpr int KB = 64, QB = 128, KS = D / 16, DT = D / 32;
+    constexpr int TILE = 64 * D;
+    constexpr int STAGE = 3 * TILE;  // K, V [64][D], K^T [D][64]
+    __shared__ __attribute__((aligned(1024))) uint16_t smem[2 * STAGE];
+    const uint32_t smem_byte = (uint32_t)reinterpret_cast<uintptr_t>(smem);
+    const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+    const int col = lane & 31, half = lane >> 5;
+    const int nbh = a.B * a.H;
+    const int nqb = (int)((a.S + QB - 1) / QB);
+    const int qb = nqb - 1 - (int)(blockIdx.x / nbh);  // heaviest query blocks first
+    const int bh = (int)(blockIdx.x % nbh);
+    const int b = bh / a.H, h = bh % a.H;
+    const int64_t bhk = (int64_t)b * a.Hkv + h / (a.H / a.Hkv);
+    const int64_t S = a.S;
+    const int64_t q0 = (int64_t)qb * QB;
+    const int64_t qw = q0 + 32 * wave;
+    const int64_t my_q = qw + col;
+
+    // Q and dO fragments (B operands of S^T = K.Q^T and dP^T = V.dO^T)
+    const __amdgpu_buffer_rsrc_t rq = make_rsrc(a.q + (int64_t)bh * S * D, S * D * 2);
+    const __amdgpu_buffer_rsrc_t rdo = make_rsrc(a.dout + ((int64_t)b * S * a.H + h) * D, (S * a.H - h) * D * 2);
+    bf16x8 qf[KS], dof[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+        const bool ok = my_q < S;
+        qf[s] = __builtin_bit_cast(bf16x8, buf_load16(rq, ok ? (uint32_t)((my_q * D + 16 * s + 8 * half) * 2) : kOOB));
+        dof[s] = __builtin_bit_cast(
+            bf16x8, buf_load16(rdo, ok ? (uint32_t)((my_q * a.H * D + 16 * s + 8 * half) * 2) : kOOB));
+    }
+    float lse2 = __builtin_inff(), delta = 0.f;
+    if (my_q < S) {
+        const float* blk = a.lsd + ((int64_t)bh * (a.Sp / 64) + my_q / 64) * 128;
+        lse2 = blk[my_q % 64];
+        delta = blk[64 + my_q % 64];
+    }
+
+    const i32x4 rk = rsrc_words(a.k + bhk * S * D, S * D * 2);
+    const i32x4 rv = rsrc_words(a.v + bhk * S * D, S * D * 2);
+    const i32x4 rkt = rsrc_words(a.kt + bhk * D * a.Sp, (int64_t)D * a.Sp * 2);
+    const __amdgpu_buffer_rsrc_t rm = make_rsrc(a.mask, a.mask ? S * S * 4 : 0);
+
+    const int nkb_all = (int)((S + KB - 1) / KB);
+    int nkb = nkb_all, wkb = nkb_all;
+    if (a.causal) {
+        nkb = min(nkb_all, (int)((min(q0 + QB, S) - 1) / KB) + 1);
+        wkb = min(nkb, (int)(min(qw + 31, S - 1) / KB) + 1);
+    }
+    if (qw >= S) wkb = 0;
+
+    auto issue = [&](int kb, int stage) {
+        const uint32_t base = smem_byte + (uint32_t)(stage * STAGE * 2);
+        const uint32_t key0 = (uint32_t)kb * KB;
+        dma_rows<D>(rk, base, key0, D, wave, lane);
+        dma_rows<D>(rv, base + TILE * 2, key0, D, wave, lane);
+        dma_cols<D>(rkt, base + 2 * TILE * 2, key0, (uint32_t)a.Sp, wave, lane);
+    };
+
+    f32x16 dqacc[DT];
+#pragma unroll
+    for (int t = 0; t < DT; ++t)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) dqacc[t][j] = 0.f;
+
+    if (nkb > 0) issue(0, 0);
+    for (int kb = 0; kb < nkb; ++kb) {
+        wait_vmcnt<0>();
+        __syncthreads();
+        if (kb + 1 < nkb) issue(kb + 1, (kb + 1) & 1);
+        if (kb >= wkb) continue;
+        const uint16_t* sk = smem + (kb & 1) * STAGE;
+        const uint16_t* sv = sk + TILE;
+        const uint16_t* skt = sk + 2 * TILE;
+
+        f32x16 sacc[2], dpacc[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) sacc[t][j] = dpacc[t][j] = 0.f;
+#pragma unroll
+        for (int s = 0; s < KS; ++s)
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                sacc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_rows<D>(sk, 32 * t + col, 2 * s + half),
+                                                                 qf[s], sacc[t], 0, 0, 0);
+                dpacc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_rows<D>(sv, 32 * t + col, 2 * s + half),
+                                                                  dof[s], dpacc[t], 0, 0, 0);
+            }
+
+        // accumulator j of tile t: key key0 + 32 t + 8 (j/4) + 4 half + j%4, query my_q
+        const int64_t key0 = (int64_t)kb * KB;
+        const bool edge = key0 + KB > S || (a.causal && key0 + KB - 1 > qw);
+        bf16x8 db[2][2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const int64_t key = key0 + 32 * t + 8 * (j >> 2) + 4 * half + (j & 3);
+                float x = sacc[t][j] * a.scale_log2;
+                if (a.mask) {
+                    const uint32_t off = (my_q < S && key < S) ? (uint32_t)((my_q * S + key) * 4) : kOOB;
+                    x += __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(rm, (int)off, 0, 0)) * kLog2e;
+                }
+                if (edge && (key >= S || (a.causal && key > my_q))) x = kNegInf;
+                const float p = exp2f(x - lse2);
+                db[t][j >> 3][j & 7] = static_cast<__bf16>(p * (dpacc[t][j] - delta));
+            }
+
+        // dQ^T (d x query) += K^T . dS^T ; key positions 16 (2t + kk) + 8 half .. +7
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+            const int row = 32 * dt + col;
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int kk = 0; kk < 2; ++kk)
+                    dqacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_cols(skt, row, 4 * t + 2 * kk + half),
+                                                                       db[t][kk], dqacc[dt], 0, 0, 0);
+        }
+    }
+
+    __syncthreads();
+    store_rows<D, uint16_t>(dqacc, a.scale, smem + wave * 32 * (D + 8), a.dq + (int64_t)bh * S * D, D, qw, S, lane);
+}
+
+// ------------------------------------------------------ generic backward
+// One wave per row; lanes over the head dim (dims l, l + 64, l + 128, l + 192).
+template <typename T>
+__global__ __launch_bounds__(256) void attn_bwd_delta_generic(const T* __restrict__ o, const T* __restrict__ dout,
+                                                              float* __restrict__ delta, int B, int H, int64_t S,
+                                                              int D) {
+    const int lane = lane_id();
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);  // (b, h, i)
+    if (row >= (int64_t)B * H * S) return;
+    const int64_t bh = row / S, i = row % S, b = bh / H, h = bh % H;
+    const int64_t base = ((b * S + i) * H + h) * D;
+    float acc = 0.f;
+    for (int d = lane; d < D; d += 64) acc += Elem<T>::load(o, base + d) * Elem<T>::load(dout, base + d);
+    acc = wave_sum(acc);
+    if (lane == 0) delta[row] = acc;
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void attn_bwd_dq_generic(const T* __restrict__ q, const T* __restrict__ k,
+                                                           const T* __restrict__ v, const float* __restrict__ mask,
+                                                           const float* __restrict__ lse,
+                                                           const float* __restrict__ delta,
+                                                           const T* __restrict__ dout, T* __restrict__ dq, int B,
+                                                           int H, int Hkv, int64_t S, int D, float scale,
+                                                           int causal) {
+    const int lane = lane_id();
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= (int64_t)B * H * S) return;
+    const int64_t bh = row / S, i = row % S;
+    const int b = (int)(bh / H), h = (int)(bh % H);
+    const int64_t bhk = (int64_t)b * Hkv + h / (H / Hkv);
+    float qv[4], gv[4], acc[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int d = lane + 64 * u;
+        qv[u] = d < D ? Elem<T>::load(q, (bh * S + i) * D + d) : 0.f;
+        gv[u] = d < D ? Elem<T>::load(dout, (((int64_t)b * S + i) * H + h) * D + d) : 0.f;
+        acc[u] = 0.f;
+    }
+    const float li = lse[row], di = delta[row];
+    const int64_t kend = causal ? i + 1 : S;
+    for (int64_t j = 0; j < kend; ++j) {
+        const int64_t kr = (bhk * S + j) * D;
+        float s = 0.f, dp = 0.f;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int d = lane + 64 * u;
+            if (d < D) {
+                s += qv[u] * Elem<T>::load(k, kr + d);
+                dp += gv[u] * Elem<T>::load(v, kr + d);
+            }
+        }
+        s = wave_sum(s) * scale;
+        dp = wave_sum(dp);
+        if (mask) s += mask[i * S + j];
+        const float ds = __expf(s - li) * (dp - di);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int d = lane + 64 * u;
+            if (d < D) acc[u] += ds * Elem<T>::load(k, kr + d);
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int d = lane + 64 * u;
+        if (d < D) Elem<T>::store(dq, (bh * S + i) * D + d, acc[u] * scale);
+    }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void attn_bwd_dkdv_generic(const T* __restrict__ q, const T* __restrict__ k,
+                                                             const T* __restrict__ v,
+                                                             const float* __restrict__ mask,
+                                                             const float* __restrict__ lse,
+                                                             const float* __restrict__ delta,
+                                                             const T* __restrict__ dout, T* __restrict__ dk,
+                                                             T* __restrict__ dv, int B, int H, int Hkv, int64_t S,
+                                                             int D, float scale, int causal) {
+    const int lane = lane_id();
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);  // (b, hk, j)
+    if (row >= (int64_t)B * Hkv * S) return;
+    const int64_t bhk = row / S, j = row % S;
+    const int b = (int)(bhk / Hkv), hk = (int)(bhk % Hkv);
+    const int rep = H / Hkv;
+    float kv[4], vv[4], gk[4], gvv[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int d = lane + 64 * u;
+        kv[u] = d < D ? Elem<T>::load(k, row * D + d) : 0.f;
+        vv[u] = d < D ? Elem<T>::load(v, row * D + d) : 0.f;
+        gk[u] = gvv[u] = 0.f;
+    }
+    for (int h = hk * rep; h < (hk + 1) * rep; ++h) {
+        const int64_t bh = (int64_t)b * H + h;
+        for (int64_t i = causal ? j : 0; i < S; ++i) {
+            const int64_t qr = (bh * S + i) * D, gr = (((int64_t)b * S + i) * H + h) * D;
+            float s = 0.f, dp = 0.f;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int d = lane + 64 * u;
+                if (d < D) {
+                    s += Elem<T>::load(q, qr + d) * kv[u];
+                    dp += Elem<T>::load(dout, gr + d) * vv[u];
+                }
+            }
+            s = wave_sum(s) * scale;
+            dp = wave_sum(dp);
+            if (mask) s += mask[i * S + j];
+            const float p = __expf(s - lse[bh * S + i]);
+            const float ds = p * (dp - delta[bh * S + i]);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int d = lane + 64 * u;
+                if (d < D) {
+                    gk[u] += ds * Elem<T>::load(q, qr + d);
+                    gvv[u] += p * Elem<T>::load(dout, gr + d);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int d = lane + 64 * u;
+        if (d < D) {
+            Elem<T>::store(dk, row * D + d, gk[u] * scale);
+            Elem<T>::store(dv, row * D + d, gvv[u]);
+        }
+    }
+}
+
 }  // namespace
 
 AttnWs attention_fwd_ws(const mc_attn_desc& d) {
@@ -420,6 +1044,122 @@ hipError_t launch_attention_fwd(const mc_attn_desc& d, const void* q, const void
         attn_fwd_generic<uint16_t><<<grid, 256, 0, stream>>>(
             static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v), mask,
             static_cast<uint16_t*>(o), lse, B, H, Hkv, S, D, d.scale, d.causal);
+    return hipGetLastError();
+}
+
+namespace {
+size_t align256(size_t n) { return (n + 255) / 256 * 256; }
+}  // namespace
+
+AttnBwdWs attention_bwd_ws(const mc_attn_desc& d) {
+    AttnBwdWs w{};
+    const size_t B = (size_t)d.batch, H = (size_t)d.heads, Hkv = (size_t)d.kv_heads, D = (size_t)d.head_dim;
+    const size_t S = (size_t)d.seq;
+    size_t off = 0;
+    if (attention_uses_mfma(d)) {
+        const size_t Sp = (S + 63) / 64 * 64;
+        w.lsd = off;  off += align256(B * H * (Sp / 64) * 128 * 4);
+        w.qt = off;   off += align256(B * H * D * Sp * 2);
+        w.dot = off;  off += align256(B * H * D * Sp * 2);
+        w.kt = off;   off += align256(B * Hkv * D * Sp * 2);
+        if (H != Hkv) {
+            w.dk_part = off;  off += align256(B * H * S * D * 4);
+            w.dv_part = off;  off += align256(B * H * S * D * 4);
+        }
+    } else {
+        w.lsd = off;  off += align256(B * H * S * 4);  // Delta
+    }
+    w.total = off;
+    return w;
+}
+
+hipError_t launch_attention_bwd(const mc_attn_desc& d, const void* q, const void* k, const void* v,
+                                const float* mask, const void* o, const float* lse, const void* dout, void* dq,
+                                void* dk, void* dv, void* ws, hipStream_t stream) {
+    const int B = (int)d.batch, H = d.heads, Hkv = d.kv_heads, D = d.head_dim;
+    const int64_t S = d.seq;
+    const AttnBwdWs w = attention_bwd_ws(d);
+    char* base = static_cast<char*>(ws);
+    if (attention_uses_mfma(d)) {
+        const int64_t Sp = (S + 63) / 64 * 64;
+        AttnBwdArgs a;
+        a.q = static_cast<const uint16_t*>(q);
+        a.k = static_cast<const uint16_t*>(k);
+        a.v = static_cast<const uint16_t*>(v);
+        a.dout = static_cast<const uint16_t*>(dout);
+        a.qt = reinterpret_cast<const uint16_t*>(base + w.qt);
+        a.dot = reinterpret_cast<const uint16_t*>(base + w.dot);
+        a.kt = reinterpret_cast<const uint16_t*>(base + w.kt);
+        a.mask = mask;
+        a.lsd = reinterpret_cast<const float*>(base + w.lsd);
+        a.dq = static_cast<uint16_t*>(dq);
+        a.dk = static_cast<uint16_t*>(dk);
+        a.dv = static_cast<uint16_t*>(dv);
+        a.dk_part = H != Hkv ? reinterpret_cast<float*>(base + w.dk_part) : nullptr;
+        a.dv_part = H != Hkv ? reinterpret_cast<float*>(base + w.dv_part) : nullptr;
+        a.S = S;
+        a.Sp = Sp;
+        a.B = B; a.H = H; a.Hkv = Hkv;
+        a.causal = d.causal ? 1 : 0;
+        a.nblk = (int)((S + 127) / 128);
+        a.scale = d.scale;
+        a.scale_log2 = d.scale * kLog2e;
+        const dim3 gprep((unsigned)(Sp / 64), (unsigned)(B * H));
+        const dim3 gkt((unsigned)(Sp / 64), (unsigned)(B * Hkv));
+        const dim3 grid((unsigned)((int64_t)a.nblk * B * H));
+        float* lsd = reinterpret_cast<float*>(base + w.lsd);
+        uint16_t* qt = reinterpret_cast<uint16_t*>(base + w.qt);
+        uint16_t* dot = reinterpret_cast<uint16_t*>(base + w.dot);
+        uint16_t* kt = reinterpret_cast<uint16_t*>(base + w.kt);
+        const uint16_t* q16 = static_cast<const uint16_t*>(q);
+        const uint16_t* o16 = static_cast<const uint16_t*>(o);
+        const uint16_t* do16 = static_cast<const uint16_t*>(dout);
+        if (D == 64) {
+            attn_bwd_prep_bf16<64><<<gprep, 256, 0, stream>>>(q16, o16, do16, lse, H, S, Sp, lsd, qt, dot);
+            attn_vt_bf16<64><<<gkt, 256, 0, stream>>>(a.k, S, Sp, kt);
+            attn_bwd_dkdv_bf16<64><<<grid, 256, 0, stream>>>(a);
+        } else {
+            attn_bwd_prep_bf16<128><<<gprep, 256, 0, stream>>>(q16, o16, do16, lse, H, S, Sp, lsd, qt, dot);
+            attn_vt_bf16<128><<<gkt, 256, 0, stream>>>(a.k, S, Sp, kt);
+            attn_bwd_dkdv_bf16<128><<<grid, 256, 0, stream>>>(a);
+        }
+        if (H != Hkv) {
+            const int64_t n8 = (int64_t)B * Hkv * S * D / 8;
+            const int64_t blocks = std::min<int64_t>((2 * n8 + 255) / 256, 4096);
+            attn_bwd_sum<<<dim3((unsigned)blocks), 256, 0, stream>>>(a.dk_part, a.dv_part, a.dk, a.dv, H / Hkv,
+                                                                     S * D, n8);
+        }
+        if (D == 64) attn_bwd_dq_bf16<64><<<grid, 256, 0, stream>>>(a);
+        else attn_bwd_dq_bf16<128><<<grid, 256, 0, stream>>>(a);
+        return hipGetLastError();
+    }
+    float* delta = reinterpret_cast<float*>(base + w.lsd);
+    const dim3 gq((unsigned)(((int64_t)B * H * S + 3) / 4));
+    const dim3 gk((unsigned)(((int64_t)B * Hkv * S + 3) / 4));
+    if (d.dtype == MC_F32) {
+        const float *qf = static_cast<const float*>(q), *kf = static_cast<const float*>(k),
+                    *vf = static_cast<const float*>(v), *of = static_cast<const float*>(o),
+                    *gf = static_cast<const float*>(dout);
+        attn_bwd_delta_generic<float><<<gq, 256, 0, stream>>>(of, gf, delta, B, H, S, D);
+        attn_bwd_dq_generic<float><<<gq, 256, 0, stream>>>(qf, kf, vf, mask, lse, delta, gf,
+                                                           static_cast<float*>(dq), B, H, Hkv, S, D, d.scale,
+                                                           d.causal);
+        attn_bwd_dkdv_generic<float><<<gk, 256, 0, stream>>>(qf, kf, vf, mask, lse, delta, gf,
+                                                             static_cast<float*>(dk), static_cast<float*>(dv), B, H,
+                                                             Hkv, S, D, d.scale, d.causal);
+    } else {
+        const uint16_t *qh = static_cast<const uint16_t*>(q), *kh = static_cast<const uint16_t*>(k),
+                       *vh = static_cast<const uint16_t*>(v), *oh = static_cast<const uint16_t*>(o),
+                       *gh = static_cast<const uint16_t*>(dout);
+        attn_bwd_delta_generic<uint16_t><<<gq, 256, 0, stream>>>(oh, gh, delta, B, H, S, D);
+        attn_bwd_dq_generic<uint16_t><<<gq, 256, 0, stream>>>(qh, kh, vh, mask, lse, delta, gh,
+                                                              static_cast<uint16_t*>(dq), B, H, Hkv, S, D, d.scale,
+                                                              d.causal);
+        attn_bwd_dkdv_generic<uint16_t><<<gk, 256, 0, stream>>>(qh, kh, vh, mask, lse, delta, gh,
+                                                                static_cast<uint16_t*>(dk),
+                                                                static_cast<uint16_t*>(dv), B, H, Hkv, S, D, d.scale,
+                                                                d.causal);
+    }
     return hipGetLastError();
 }
 

@@ -145,6 +145,22 @@ def attention_forward(q, k, v, causal=False, scale=None, mask=None, save_lse=Tru
     return o, lse
 
 
+def attention_backward(q, k, v, o, lse, dout, causal=False, scale=None, mask=None):
+    """(dq, dk, dv) of attention_forward; o and lse come from the forward."""
+    for t, n in ((q, "q"), (k, "k"), (v, "v"), (o, "o"), (lse, "lse"), (dout, "dout"), (mask, "mask")):
+        _contig(t, n)
+    D = q.shape[-1]
+    if scale is None:
+        scale = D ** -0.5
+    d = attention_desc(q, k, causal, scale)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    ws_n = lib().mc_attention_bwd_workspace_size(ctypes.byref(d))
+    ws = _workspace(ws_n, q.device)
+    check(lib().mc_attention_bwd(ctypes.byref(d), _ptr(q), _ptr(k), _ptr(v), _ptr(mask), _ptr(o), _ptr(lse),
+                                 _ptr(dout), _ptr(dq), _ptr(dk), _ptr(dv), _ptr(ws), ws_n, _stream(q)))
+    return dq, dk, dv
+
+
 def dropout_mask(seed, p, rows, rank):
     """Host-generated keep-mask (uint8 [rows, rank]) as a CPU torch tensor."""
     m = torch.empty(rows, rank, dtype=torch.uint8)

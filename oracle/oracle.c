@@ -379,61 +379,73 @@ void oracle_attention_fwd(int64_t B, int32_t H, int32_t Hkv, int64_t S, int32_t 
 void oracle_attention_bwd(int64_t B, int32_t H, int32_t Hkv, int64_t S, int32_t D, float scale, int causal,
                           const float* q, const float* k, const float* v, const float* mask, const float* dout,
                           float* dq, float* dk, float* dv, int threads) {
+    /* tasks: (b, h, chunk of 128 queries); each writes its dq rows and its own
+     * dK / dV partial [S, D], summed afterwards per K/V head in (h, chunk) order */
     const int rep = H / Hkv;
+    const int64_t CH = 128, nch = (S + CH - 1) / CH, ntask = B * H * nch;
+    double* part = (double*)calloc((size_t)ntask * 2 * (size_t)S * D, sizeof(double));
 #pragma omp parallel num_threads(nthreads(threads))
     {
         double* p = (double*)malloc(sizeof(double) * (size_t)S);
         double* dp = (double*)malloc(sizeof(double) * (size_t)S);
-        double* gk = (double*)malloc(sizeof(double) * (size_t)S * D);
-        double* gv = (double*)malloc(sizeof(double) * (size_t)S * D);
         double* gq = (double*)malloc(sizeof(double) * (size_t)D);
 #pragma omp for schedule(dynamic, 1)
-        for (int64_t bhk = 0; bhk < B * Hkv; ++bhk) {
-            const int64_t b = bhk / Hkv, hk = bhk % Hkv;
+        for (int64_t task = 0; task < ntask; ++task) {
+            const int64_t bh = task / nch, ch = task % nch;
+            const int64_t b = bh / H, h = bh % H;
+            const int64_t bhk = b * Hkv + h / rep;
             const float* kh = k + bhk * S * D;
             const float* vh = v + bhk * S * D;
-            for (int64_t e = 0; e < S * D; ++e) gk[e] = gv[e] = 0.0;
-            for (int64_t h = hk * rep; h < (hk + 1) * rep; ++h) {
-                const int64_t bh = b * H + h;
-                for (int64_t i = 0; i < S; ++i) {
-                    const float* qi = q + (bh * S + i) * D;
-                    const float* doi = dout + ((b * S + i) * H + h) * D;
-                    double z;
-                    attn_row(S, D, scale, causal, qi, kh, mask ? mask + i * S : NULL, i, p, &z);
-                    double dot = 0.0;
-                    for (int64_t j = 0; j < S; ++j) {
-                        double s = 0.0;
-                        const float* vj = vh + j * D;
-                        for (int d = 0; d < D; ++d) s += (double)doi[d] * (double)vj[d];
-                        dp[j] = s;
-                        dot += p[j] * s;
-                    }
-                    for (int d = 0; d < D; ++d) gq[d] = 0.0;
-                    for (int64_t j = 0; j < S; ++j) {
-                        if (p[j] == 0.0) continue;
-                        const double ds = p[j] * (dp[j] - dot) * (double)scale;
-                        const float* kj = kh + j * D;
-                        for (int d = 0; d < D; ++d) {
-                            gq[d] += ds * (double)kj[d];
-                            gk[j * D + d] += ds * (double)qi[d];
-                            gv[j * D + d] += p[j] * (double)doi[d];
-                        }
-                    }
-                    float* dqi = dq + (bh * S + i) * D;
-                    for (int d = 0; d < D; ++d) dqi[d] = (float)gq[d];
+            double* gk = part + (size_t)task * 2 * S * D;
+            double* gv = gk + (size_t)S * D;
+            for (int64_t i = ch * CH; i < S && i < (ch + 1) * CH; ++i) {
+                const float* qi = q + (bh * S + i) * D;
+                const float* doi = dout + ((b * S + i) * H + h) * D;
+                double z;
+                attn_row(S, D, scale, causal, qi, kh, mask ? mask + i * S : NULL, i, p, &z);
+                double dot = 0.0;
+                for (int64_t j = 0; j < S; ++j) {
+                    double sv = 0.0;
+                    const float* vj = vh + j * D;
+                    for (int d = 0; d < D; ++d) sv += (double)doi[d] * (double)vj[d];
+                    dp[j] = sv;
+                    dot += p[j] * sv;
                 }
-            }
-            for (int64_t e = 0; e < S * D; ++e) {
-                dk[bhk * S * D + e] = (float)gk[e];
-                dv[bhk * S * D + e] = (float)gv[e];
+                for (int d = 0; d < D; ++d) gq[d] = 0.0;
+                for (int64_t j = 0; j < S; ++j) {
+                    if (p[j] == 0.0) continue;
+                    const double ds = p[j] * (dp[j] - dot) * (double)scale;
+                    const float* kj = kh + j * D;
+                    for (int d = 0; d < D; ++d) {
+                        gq[d] += ds * (double)kj[d];
+                        gk[j * D + d] += ds * (double)qi[d];
+                        gv[j * D + d] += p[j] * (double)doi[d];
+                    }
+                }
+                float* dqi = dq + (bh * S + i) * D;
+                for (int d = 0; d < D; ++d) dqi[d] = (float)gq[d];
             }
         }
         free(p);
         free(dp);
-        free(gk);
-        free(gv);
         free(gq);
+#pragma omp for schedule(static)
+        for (int64_t bhk = 0; bhk < B * Hkv; ++bhk) {
+            const int64_t b = bhk / Hkv, hk = bhk % Hkv;
+            for (int64_t e = 0; e < S * D; ++e) {
+                double sk = 0.0, sv = 0.0;
+                for (int64_t h = hk * rep; h < (hk + 1) * rep; ++h)
+                    for (int64_t ch = 0; ch < nch; ++ch) {
+                        const double* gk = part + (size_t)((b * H + h) * nch + ch) * 2 * S * D;
+                        sk += gk[e];
+                        sv += gk[(size_t)S * D + e];
+                    }
+                dk[bhk * S * D + e] = (float)sk;
+                dv[bhk * S * D + e] = (float)sv;
+            }
+        }
     }
+    free(part);
 }
 
 /* ------------------------------------------------------------------ bf16 */

@@ -1,5 +1,6 @@
-"""GPU parity of the attention core (mc_attention_fwd) against the CPU oracle
-(oracle_attention_fwd, pinned in tests/test_oracle_attention.py).
+"""GPU parity of the attention core (mc_attention_fwd / mc_attention_bwd)
+against the CPU oracle (oracle_attention_fwd / _bwd, pinned in
+tests/test_oracle_attention.py).
 
 Cases: the reference's attention test geometries (src/models/transformer.rs:
 443-480: H = 4 with 2 or 4 K/V heads, S = 8, D = 32, fp32, zero mask),
@@ -168,3 +169,113 @@ def test_attention_c4_shape(mc, dev):
     slack = 1e-2 * (hi - lo).abs() + 1e-2
     assert bool(((of >= lo - slack) & (of <= hi + slack)).all())
     assert torch.isfinite(lse).all()
+
+
+# ------------------------------------------------------------------ backward
+def run_bwd(mc, dev, q, k, v, mask, causal, dout, scale=None):
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    md = None if mask is None else mask.to(dev)
+    o, lse = mc.attention_forward(qd, kd, vd, causal=causal, scale=scale, mask=md)
+    grads = mc.attention_backward(qd, kd, vd, o, lse, dout.to(dev), causal=causal, scale=scale, mask=md)
+    torch.cuda.synchronize()
+    return grads
+
+
+def ref_bwd(q, k, v, mask, causal, dout, scale=None):
+    D = q.shape[-1]
+    return oracle.attention_bwd(q.float().numpy(), k.float().numpy(), v.float().numpy(), dout.float().numpy(),
+                                D ** -0.5 if scale is None else scale, causal=causal,
+                                mask=None if mask is None else mask.numpy())
+
+
+def check_bwd(got, want, dtype):
+    tol = F32_TOL if dtype == torch.float32 else BF16_TOL
+    for name, g, w in zip(("dq", "dk", "dv"), got, want):
+        assert rel_err(g, w) <= tol, name
+
+
+@pytest.mark.parametrize("B,H,Hkv,S,D,causal,masked", [
+    (1, 4, 2, 8, 32, False, False),   # test_attention_forward's geometry
+    (1, 4, 4, 8, 32, False, True),    # test_attention_with_mask's geometry
+    (2, 6, 2, 37, 16, True, False),
+    (1, 4, 1, 64, 128, True, True),
+    (1, 3, 3, 21, 200, False, False),
+])
+def test_attention_bwd_f32(mc, dev, B, H, Hkv, S, D, causal, masked):
+    q, k, v, mask = case(B * 77 + S, B, H, Hkv, S, D, torch.float32, masked)
+    dout = torch.randn(B, S, H * D, generator=gen(S))
+    got = run_bwd(mc, dev, q, k, v, mask, causal, dout)
+    check_bwd(got, ref_bwd(q, k, v, mask, causal, dout), torch.float32)
+
+
+BWD_CASES = [
+    # B, H, Hkv, S, D, causal
+    (1, 4, 4, 1, 64, False), (1, 4, 4, 1, 128, True),
+    (1, 4, 2, 7, 128, True), (2, 4, 2, 63, 64, True),
+    (1, 4, 4, 64, 128, False), (1, 4, 2, 64, 128, True),
+    (1, 2, 1, 65, 64, True), (2, 12, 2, 127, 128, True),
+    (1, 12, 2, 129, 128, False), (1, 6, 6, 200, 128, True),
+    (1, 4, 2, 256, 64, False), (1, 12, 2, 333, 128, True),
+    (1, 14, 2, 300, 64, True),
+]
+
+
+@pytest.mark.parametrize("B,H,Hkv,S,D,causal", BWD_CASES)
+def test_attention_bwd_bf16(mc, dev, B, H, Hkv, S, D, causal):
+    q, k, v, _ = case(5 * S + D + H, B, H, Hkv, S, D, torch.bfloat16)
+    dout = torch.randn(B, S, H * D, generator=gen(S + 1)).to(torch.bfloat16)
+    got = run_bwd(mc, dev, q, k, v, None, causal, dout)
+    check_bwd(got, ref_bwd(q, k, v, None, causal, dout), torch.bfloat16)
+
+
+@pytest.mark.parametrize("S,D,causal", [(100, 128, False), (200, 128, True), (77, 64, True)])
+def test_attention_bwd_bf16_mask(mc, dev, S, D, causal):
+    q, k, v, mask = case(S * 3 + D, 2, 4, 2, S, D, torch.bfloat16, masked=True)
+    mask[:, S - 3:] = float("-inf")
+    dout = torch.randn(2, S, 4 * D, generator=gen(S + 2)).to(torch.bfloat16)
+    got = run_bwd(mc, dev, q, k, v, mask, causal, dout)
+    check_bwd(got, ref_bwd(q, k, v, mask, causal, dout), torch.bfloat16)
+
+
+@pytest.mark.parametrize("D", [32, 96])
+def test_attention_bwd_bf16_generic_head_dims(mc, dev, D):
+    q, k, v, mask = case(D + 5, 1, 4, 2, 40, D, torch.bfloat16, masked=True)
+    dout = torch.randn(1, 40, 4 * D, generator=gen(D)).to(torch.bfloat16)
+    got = run_bwd(mc, dev, q, k, v, mask, True, dout)
+    check_bwd(got, ref_bwd(q, k, v, mask, True, dout), torch.bfloat16)
+
+
+def test_attention_bwd_deterministic(mc, dev):
+    q, k, v, _ = case(13, 2, 12, 2, 300, 128, torch.bfloat16)
+    dout = torch.randn(2, 300, 12 * 128, generator=gen(14)).to(torch.bfloat16)
+    a = run_bwd(mc, dev, q, k, v, None, True, dout)
+    b = run_bwd(mc, dev, q, k, v, None, True, dout)
+    assert all(torch.equal(x, y) for x, y in zip(a, b))
+
+
+def test_attention_bwd_c4_shape(mc, dev):
+    """Backward at BASELINE c4's attention shape: one whole K/V group (6 query
+    heads, every query and key) against the oracle; on every head, the rows
+    of dS sum to 0, so sum_j dK_j = scale sum_i (sum_j dS_ij) q_i = 0."""
+    B, H, Hkv, S, D = 8, 12, 2, 2048, 128
+    g = gen(4096)
+    q = torch.randn(B, H, S, D, generator=g).to(torch.bfloat16)
+    k = torch.randn(B, Hkv, S, D, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, Hkv, S, D, generator=g).to(torch.bfloat16)
+    dout = torch.randn(B, S, H * D, generator=g).to(torch.bfloat16)
+    dq, dk, dv = run_bwd(mc, dev, q, k, v, None, True, dout)
+    rep = H // Hkv
+    b, hk = 3, 1
+    hs = slice(hk * rep, (hk + 1) * rep)
+    rq, rk, rv = oracle.attention_bwd(q[b:b + 1, hs].float().numpy(), k[b:b + 1, hk:hk + 1].float().numpy(),
+                                      v[b:b + 1, hk:hk + 1].float().numpy(),
+                                      dout[b:b + 1].view(1, S, H, D)[:, :, hs].reshape(1, S, rep * D).float().numpy(),
+                                      D ** -0.5, causal=True)
+    assert rel_err(dq[b:b + 1, hs], rq) <= BF16_TOL
+    assert rel_err(dk[b:b + 1, hk:hk + 1], rk) <= BF16_TOL
+    assert rel_err(dv[b:b + 1, hk:hk + 1], rv) <= BF16_TOL
+    # rows of dS sum to 0, so the keys' gradients sum to 0 over the keys of each head
+    ksum = dk.float().sum(dim=2)
+    assert float(ksum.abs().max()) <= 2e-2 * float(dk.float().abs().max()) * 8
+    for t in (dq, dk, dv):
+        assert torch.isfinite(t).all()
