@@ -26,6 +26,13 @@ columns folded in), timed per launch with hipEvents on its stream by the
 library's profiling hook in a separate pass after the timed steps (the
 hook's events are not in the timed region); achieved counts the
 base-product FLOPs only.
+
+The attention core next to the softmax (mc_attention_fwd / _bwd, flash
+kernels, the materialised score matrix never reaches HBM) is measured in the
+same run at the layer's attention shape, outside the step and outside value:
+the "attention" object gives its per-call times and MFMA rate (FLOPs of the
+score and P.V products over the causal lower triangle; the backward counts
+its four algorithmic products, not the recomputation).
 """
 import argparse
 import json
@@ -220,6 +227,38 @@ def cpu_baseline(c, tokens, threads):
     return T / dt, dt
 
 
+def attention_core(mc, c, dev, iters):
+    """fwd / bwd of the attention core at the layer's shape, timed per call by
+    the library's profiling hook (hipEvents on the launch stream)."""
+    import torch
+
+    B, H, Hkv, S, D = c["batch"], c["heads"], c["kv_heads"], c["seq"], c["head_dim"]
+    g = torch.Generator(device=dev).manual_seed(7)
+    q = torch.randn(B, H, S, D, device=dev, generator=g).to(torch.bfloat16)
+    k = torch.randn(B, Hkv, S, D, device=dev, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, Hkv, S, D, device=dev, generator=g).to(torch.bfloat16)
+    dout = torch.randn(B, S, H * D, device=dev, generator=g).to(torch.bfloat16)
+    o, lse = mc.attention_forward(q, k, v, causal=True)
+    mc.attention_backward(q, k, v, o, lse, dout, causal=True)
+    torch.cuda.synchronize()
+    out = {"shape": {"batch": B, "heads": H, "kv_heads": Hkv, "seq": S, "head_dim": D, "causal": True},
+           "iters": iters}
+    for name, fn in (("fwd", lambda: mc.attention_forward(q, k, v, causal=True)),
+                     ("bwd", lambda: mc.attention_backward(q, k, v, o, lse, dout, causal=True))):
+        mc._lib.check(mc._lib.lib().mc_profile_reset())
+        mc._lib.check(mc._lib.lib().mc_profile_enable(1))
+        for _ in range(iters):
+            fn()
+        torch.cuda.synchronize()
+        mc._lib.check(mc._lib.lib().mc_profile_enable(0))
+        mc._lib.check(mc._lib.lib().mc_profile_collect())
+        ms, n, fl, by = mc._lib.profile_read("attention")
+        tf = fl / (ms * 1e-3) / 1e12
+        out[name] = {"us_per_call": ms * 1e3 / n, "TFLOP_s": tf, "mfma_frac": tf / BF16_PEAK_TFLOPS,
+                     "GB_s": by / (ms * 1e-3) / 1e9}
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -229,6 +268,8 @@ def main():
     ap.add_argument("--cpu-tokens", type=int, default=2048, help="token sample of the CPU-oracle baseline")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--graph", action="store_true", help="time HIP graph replays of one captured step")
+    ap.add_argument("--attention-iters", type=int, default=5,
+                    help="calls of the attention core fwd / bwd timed after the step (0: skip)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="run one plain device copy of BYTES before the steps (a kernel of known HBM traffic "
                          "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
@@ -336,6 +377,8 @@ def main():
         "launch": "hip_graph" if args.graph else "eager",
         "kernels": kernels,
     }
+    if args.attention_iters > 0 and c["softmax"]:
+        line["attention"] = attention_core(mc, c, dev, args.attention_iters)
     if not args.no_cpu_baseline:
         threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
         v, dt = cpu_baseline(c, args.cpu_tokens, threads)
