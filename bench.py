@@ -32,7 +32,9 @@ kernels, the materialised score matrix never reaches HBM) is measured in the
 same run at the layer's attention shape, outside the step and outside value:
 the "attention" object gives its per-call times and MFMA rate (FLOPs of the
 score and P.V products over the causal lower triangle; the backward counts
-its four algorithmic products, not the recomputation).
+its four algorithmic products, not the recomputation). The "adamw" object
+times one AdamW step (mc_adamw_step) over the layer's LoRA parameters, also
+outside the step.
 """
 import argparse
 import json
@@ -259,6 +261,37 @@ def attention_core(mc, c, dev, iters):
     return out
 
 
+def adamw_update(mc, c, dev, iters):
+    """One AdamW step over the layer's LoRA parameters (A [K, r] and B [r, N]
+    of every projection) per call, timed by the library's profiling hook."""
+    import torch
+
+    g = torch.Generator(device=dev).manual_seed(11)
+    shapes = []
+    for name in c["projections"]:
+        K, N, _ = proj_shapes(c)[name]
+        shapes += [(K, c["rank"]), (c["rank"], N)]
+    ps = [torch.randn(*s, device=dev, generator=g) for s in shapes]
+    gs = [torch.randn(*s, device=dev, generator=g) for s in shapes]
+    ms = [torch.zeros(*s, device=dev) for s in shapes]
+    vs = [torch.zeros(*s, device=dev) for s in shapes]
+    n = sum(p.numel() for p in ps)
+    steps = list(range(1, len(ps) + 1))
+    mc.adamw_step(ps, gs, ms, vs, steps)
+    torch.cuda.synchronize()
+    mc._lib.check(mc._lib.lib().mc_profile_reset())
+    mc._lib.check(mc._lib.lib().mc_profile_enable(1))
+    for _ in range(iters):
+        mc.adamw_step(ps, gs, ms, vs, steps)
+    torch.cuda.synchronize()
+    mc._lib.check(mc._lib.lib().mc_profile_enable(0))
+    mc._lib.check(mc._lib.lib().mc_profile_collect())
+    ms_, calls, _, by = mc._lib.profile_read("adamw")
+    return {"tensors": len(ps), "elements": n, "iters": iters, "us_per_call": ms_ * 1e3 / calls,
+            "GB_s": by / (ms_ * 1e-3) / 1e9, "hbm_frac": by / (ms_ * 1e-3) / 1e9 / HBM_PEAK_GBS,
+            "bytes_per_call": by / calls}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -379,6 +412,8 @@ def main():
     }
     if args.attention_iters > 0 and c["softmax"]:
         line["attention"] = attention_core(mc, c, dev, args.attention_iters)
+    if args.attention_iters > 0:
+        line["adamw"] = adamw_update(mc, c, dev, 20)
     if not args.no_cpu_baseline:
         threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
         v, dt = cpu_baseline(c, args.cpu_tokens, threads)

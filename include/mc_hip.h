@@ -26,6 +26,8 @@
  *                    (src/models/transformer.rs:258-283) with repeat_kv
  *                    (295-319), without materialising the score matrix.
  *   mc_attention_bwd no reference kernel: autograd of the same composite.
+ *   mc_adamw_step    AdamW::step (src/training/optimizer.rs:227-281) for many
+ *                    parameter tensors per launch.
  *
  * Conventions (all entry points):
  *  - Device buffers are caller-owned, row-major and contiguous; inputs are
@@ -188,6 +190,37 @@ mc_status mc_attention_bwd(const mc_attn_desc* d, const void* q, const void* k, 
                            void* dq, void* dk, void* dv, void* workspace, size_t workspace_bytes,
                            hipStream_t stream);
 
+/* AdamW (src/training/optimizer.rs:33-48 config, 227-281 step) over fp32
+ * parameter tensors, typically the LoRA A and B of every projection. */
+typedef struct mc_adamw_config {
+    float learning_rate;  /* > 0 */
+    float beta1;          /* [0, 1) */
+    float beta2;          /* [0, 1) */
+    float epsilon;        /* > 0 */
+    float weight_decay;   /* >= 0 */
+} mc_adamw_config;
+
+typedef struct mc_adamw_tensor {
+    const float* param;   /* theta_{t-1} [numel] */
+    const float* grad;    /* g_t [numel] */
+    float* m;             /* first moment, updated in place */
+    float* v;             /* second moment, updated in place */
+    float* param_out;     /* theta_t [numel]; may equal param (in place) */
+    int64_t numel;        /* >= 0 */
+    int64_t step;         /* t in 1 .. 2^31-1: the optimizer's step count for this update */
+} mc_adamw_tensor;
+
+/* One AdamW::step per tensor, all in one or a few launches:
+ *   m = b1 m + (1-b1) g ;  v = b2 v + (1-b2) g^2
+ *   theta_t = theta - lr (m/(1-b1^t)) / (sqrt(v/(1-b2^t)) + eps) - (wd lr) theta
+ * in the reference's fp32 op order (each intermediate rounded to fp32, no
+ * fused multiply-add; b^t as Rust's f32::powi), so results equal a CPU
+ * evaluation of optimizer.rs:246-281 bit for bit. The tensor table is read
+ * on the host; pointers must be 16-byte aligned. Validation messages are
+ * AdamWConfig::validate's (optimizer.rs:67-103). */
+mc_status mc_adamw_step(const mc_adamw_config* cfg, const mc_adamw_tensor* tensors, int32_t count,
+                        hipStream_t stream);
+
 /* Host-side dropout keep-mask [rows, rank] from a seed (Philox4x32-10; element
  * i = t*rank + j uses counter block i/4, word i%4, key = seed; keep iff
  * (word >> 8) * 2^-24 >= p). Both the GPU path and the CPU reference are fed
@@ -203,7 +236,8 @@ mc_status mc_dropout_mask(uint64_t seed, float p, int64_t rows, int32_t rank, ui
  * the recorded events and adds them to per-class totals; mc_profile_read()
  * returns the totals of one class. Classes: 0 = MFMA GEMM (FLOPs count the
  * base x.W^T / dY.W product only), 1 = rank-r kernels, 2 = RMSNorm,
- * 3 = softmax, 4 = attention (FLOPs of the unmasked score and P.V products).
+ * 3 = softmax, 4 = attention (FLOPs of the unmasked score and P.V products),
+ * 5 = AdamW (bytes: 28 per element).
  * Enabling allocates hipEvents (not for allocation-free use). */
 mc_status mc_profile_enable(int32_t on);
 mc_status mc_profile_collect(void);

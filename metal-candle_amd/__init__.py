@@ -9,6 +9,7 @@ __graft_entry__.load_package(), which registers it as `metal_candle_amd`.
 from . import _lib, ops  # noqa: F401
 from ._lib import McError  # noqa: F401
 from .ops import (  # noqa: F401
+    adamw_step,
     attention_backward,
     attention_forward,
     dropout_mask,

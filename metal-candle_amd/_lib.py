@@ -63,6 +63,28 @@ class AttnDesc(ctypes.Structure):
     ]
 
 
+class AdamWConfig(ctypes.Structure):
+    _fields_ = [
+        ("learning_rate", ctypes.c_float),
+        ("beta1", ctypes.c_float),
+        ("beta2", ctypes.c_float),
+        ("epsilon", ctypes.c_float),
+        ("weight_decay", ctypes.c_float),
+    ]
+
+
+class AdamWTensor(ctypes.Structure):
+    _fields_ = [
+        ("param", ctypes.c_void_p),
+        ("grad", ctypes.c_void_p),
+        ("m", ctypes.c_void_p),
+        ("v", ctypes.c_void_p),
+        ("param_out", ctypes.c_void_p),
+        ("numel", ctypes.c_int64),
+        ("step", ctypes.c_int64),
+    ]
+
+
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int32
@@ -87,6 +109,7 @@ _SIGNATURES = {
     "mc_attention_fwd": (ctypes.c_int, [_ap, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "mc_attention_bwd_workspace_size": (_sz, [_ap]),
     "mc_attention_bwd": (ctypes.c_int, [_ap, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "mc_adamw_step": (ctypes.c_int, [ctypes.POINTER(AdamWConfig), ctypes.POINTER(AdamWTensor), _i32, _vp]),
     "mc_dropout_mask": (ctypes.c_int, [ctypes.c_uint64, _f32, _i64, _i32, _vp]),
     "mc_profile_enable": (ctypes.c_int, [_i32]),
     "mc_profile_collect": (ctypes.c_int, []),
@@ -95,7 +118,7 @@ _SIGNATURES = {
     "mc_profile_reset": (ctypes.c_int, []),
 }
 
-PROFILE_KINDS = {"gemm": 0, "lowrank": 1, "rmsnorm": 2, "softmax": 3, "attention": 4}
+PROFILE_KINDS = {"gemm": 0, "lowrank": 1, "rmsnorm": 2, "softmax": 3, "attention": 4, "adamw": 5}
 
 _lib = None
 

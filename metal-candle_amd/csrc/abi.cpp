@@ -335,6 +335,86 @@ mc_status mc_attention_bwd(const mc_attn_desc* d, const void* q, const void* k, 
                       "Attention backward");
 }
 
+// b^t as Rust's f32::powi lowers it for a run-time exponent: right-to-left
+// binary exponentiation in fp32 (square the base, multiply the result in at
+// every set bit of t).
+static float powi_f32(float base, int32_t t) {
+    float r = 1.0f;
+    for (;;) {
+        if (t & 1) r *= base;
+        t /= 2;
+        if (t == 0) break;
+        base *= base;
+    }
+    return r;
+}
+
+mc_status mc_adamw_step(const mc_adamw_config* cfg, const mc_adamw_tensor* tensors, int32_t count,
+                        hipStream_t stream) {
+    MC_CHECK(cfg != nullptr, MC_ERR_NULL, "AdamW: config is NULL");
+    // AdamWConfig::validate (optimizer.rs:67-103), with its comparisons
+    MC_CHECK(!(cfg->learning_rate <= 0.0f), MC_ERR_VALUE, "learning rate must be positive");
+    MC_CHECK(cfg->beta1 >= 0.0f && cfg->beta1 < 1.0f, MC_ERR_VALUE, "beta1 must be in [0, 1), got %g",
+             (double)cfg->beta1);
+    MC_CHECK(cfg->beta2 >= 0.0f && cfg->beta2 < 1.0f, MC_ERR_VALUE, "beta2 must be in [0, 1), got %g",
+             (double)cfg->beta2);
+    MC_CHECK(!(cfg->epsilon <= 0.0f), MC_ERR_VALUE, "epsilon must be positive");
+    MC_CHECK(!(cfg->weight_decay < 0.0f), MC_ERR_VALUE, "weight decay must be non-negative");
+    MC_CHECK(count >= 0, MC_ERR_SHAPE, "AdamW: tensor count must be >= 0, got %d", (int)count);
+    MC_CHECK(count == 0 || tensors, MC_ERR_NULL, "AdamW: tensor table is NULL");
+    double bytes = 0.0;
+    for (int32_t i = 0; i < count; ++i) {
+        const mc_adamw_tensor& t = tensors[i];
+        MC_CHECK(t.numel >= 0 && t.numel < ((int64_t)1 << 40), MC_ERR_SHAPE, "AdamW: tensor %d: numel %lld out of range",
+                 (int)i, (long long)t.numel);
+        MC_CHECK(t.step >= 1 && t.step <= 2147483647, MC_ERR_VALUE, "AdamW: tensor %d: step must be in [1, 2^31), got %lld",
+                 (int)i, (long long)t.step);
+        if (t.numel == 0) continue;
+        MC_CHECK(t.param && t.grad && t.m && t.v && t.param_out, MC_ERR_NULL,
+                 "AdamW: tensor %d: param, grad, m, v and param_out must not be NULL", (int)i);
+        MC_CHECK(aligned16(t.param) && aligned16(t.grad) && aligned16(t.m) && aligned16(t.v) && aligned16(t.param_out),
+                 MC_ERR_LAYOUT, "AdamW: tensor %d: pointers must be 16-byte aligned", (int)i);
+        bytes += 28.0 * (double)t.numel;
+    }
+    mc::prof::Scope sc(mc::prof::kAdamW, stream, 0.0, bytes);
+    mc::AdamWBatch b{};
+    b.b1 = cfg->beta1;
+    b.b2 = cfg->beta2;
+    b.omb1 = 1.0f - cfg->beta1;  // f64::from(1.0 - beta1): the difference is taken in fp32
+    b.omb2 = 1.0f - cfg->beta2;
+    b.eps = cfg->epsilon;
+    b.lr = cfg->learning_rate;
+    b.wdlr = cfg->weight_decay * cfg->learning_rate;
+    int blocks = 0;
+    for (int32_t i = 0; i < count; ++i) {
+        const mc_adamw_tensor& t = tensors[i];
+        if (t.numel == 0) continue;
+        mc::AdamWSlot& sl = b.slot[b.count++];
+        sl.p = t.param;
+        sl.g = t.grad;
+        sl.m = t.m;
+        sl.v = t.v;
+        sl.po = t.param_out;
+        sl.n = t.numel;
+        // m_hat = m / f64::from(1 - b1^t): affine(1 / x, 0) with the reciprocal in f64, applied in fp32
+        sl.c1 = (float)(1.0 / (double)(1.0f - powi_f32(cfg->beta1, (int32_t)t.step)));
+        sl.c2 = (float)(1.0 / (double)(1.0f - powi_f32(cfg->beta2, (int32_t)t.step)));
+        sl.blk0 = blocks;
+        blocks += mc::adamw_blocks(t.numel);
+        if (b.count == mc::kAdamWSlots || i == count - 1) {
+            hipError_t e = mc::launch_adamw(b, blocks, stream);
+            if (e != hipSuccess) return hip_status(e, "AdamW");
+            b.count = 0;
+            blocks = 0;
+        }
+    }
+    if (b.count > 0) {
+        hipError_t e = mc::launch_adamw(b, blocks, stream);
+        if (e != hipSuccess) return hip_status(e, "AdamW");
+    }
+    return ok();
+}
+
 // Philox4x32-10 (Salmon et al., SC'11), 10 rounds of the two 32x32->64
 // multiplies 0xD2511F53 / 0xCD9E8D57 with Weyl key steps 0x9E3779B9 /
 // 0xBB67AE85.

@@ -82,4 +82,28 @@ hipError_t launch_attention_bwd(const mc_attn_desc& d, const void* q, const void
                                 const float* mask, const void* o, const float* lse, const void* dout, void* dq,
                                 void* dk, void* dv, void* ws, hipStream_t stream);
 
+// --------------------------------------------------------------- AdamW
+// One launch of the AdamW kernel updates up to kAdamWSlots tensors; the
+// table travels by value as a kernel argument (no device allocation).
+// blk0: first workgroup of the slot; c1, c2: the bias-correction factors of
+// the slot's step, as fp32.
+constexpr int kAdamWSlots = 16;
+struct AdamWSlot {
+    const float* p;
+    const float* g;
+    float* m;
+    float* v;
+    float* po;
+    int64_t n;
+    float c1, c2;
+    int blk0, pad;
+};
+struct AdamWBatch {
+    AdamWSlot slot[kAdamWSlots];
+    int count;
+    float b1, b2, omb1, omb2, eps, lr, wdlr;
+};
+int adamw_blocks(int64_t n);  // workgroups one tensor of n elements takes
+hipError_t launch_adamw(const AdamWBatch& batch, int blocks, hipStream_t stream);
+
 }  // namespace mc

@@ -20,6 +20,7 @@ std::string TrainingError::to_string() const {
     switch (kind) {  // src/error.rs:97-114
         case Kind::InvalidLoRAConfig: return "invalid LoRA configuration: " + reason;
         case Kind::InvalidConfig: return "invalid training configuration: " + reason;
+        case Kind::StateError: return "training state error: " + reason;
         default: return "training failed: " + reason;
     }
 }
@@ -542,6 +543,83 @@ Result<void, Error> LoRAConfig::validate() const {
     if (!(dropout >= 0.f && dropout < 1.f))
         return Error::from(TrainingError::invalid_config("LoRA dropout must be in [0, 1)"));
     return {};
+}
+
+// ------------------------------------------------------------------ AdamW
+Result<void, Error> AdamWConfig::validate() const {
+    // optimizer.rs:67-103, with its comparisons (a NaN learning rate passes, as there)
+    if (learning_rate <= 0.f) return Error::from(TrainingError::invalid_config("learning rate must be positive"));
+    if (!(beta1 >= 0.f && beta1 < 1.f)) {
+        std::ostringstream m;
+        m << "beta1 must be in [0, 1), got " << beta1;
+        return Error::from(TrainingError::invalid_config(m.str()));
+    }
+    if (!(beta2 >= 0.f && beta2 < 1.f)) {
+        std::ostringstream m;
+        m << "beta2 must be in [0, 1), got " << beta2;
+        return Error::from(TrainingError::invalid_config(m.str()));
+    }
+    if (epsilon <= 0.f) return Error::from(TrainingError::invalid_config("epsilon must be positive"));
+    if (weight_decay < 0.f) return Error::from(TrainingError::invalid_config("weight decay must be non-negative"));
+    return {};
+}
+
+Result<AdamW, Error> AdamW::create(const AdamWConfig& config) {
+    auto v = config.validate();
+    if (v.is_err()) return v.error();
+    AdamW a;
+    a.config_ = config;
+    return a;
+}
+
+AdamW::State* AdamW::find(const std::string& name) {
+    for (auto& kv : state_)
+        if (kv.first == name) return &kv.second;
+    return nullptr;
+}
+
+Result<void, Error> AdamW::add_parameter(const std::string& name, const Tensor& param) {
+    auto m = Tensor::zeros(param.dims(), DType::F32, param.device());
+    if (m.is_err()) return Error::from(m.error());
+    auto v = Tensor::zeros(param.dims(), DType::F32, param.device());
+    if (v.is_err()) return Error::from(v.error());
+    State st{std::move(m.value()), std::move(v.value())};
+    if (State* old = find(name)) *old = std::move(st);  // HashMap::insert replaces
+    else state_.emplace_back(name, std::move(st));
+    return {};
+}
+
+Result<Tensor, Error> AdamW::step(const std::string& name, const Tensor& param, const Tensor& grad) {
+    State* st = find(name);
+    if (!st) return Error::from(TrainingError::state_error("parameter '" + name + "' not found in optimizer"));
+    ++step_count_;  // optimizer.rs:235-237: counted per call, before the update
+    if (!param.device().is_hip() || !grad.device().is_hip())
+        return Error::from(bail("AdamW step is implemented for HIP tensors only"));
+    if (param.dtype() != DType::F32 || grad.dtype() != DType::F32)
+        return Error::from(bail("AdamW step: parameters and gradients must be f32"));
+    if (param.elem_count() != grad.elem_count() || param.elem_count() != st->m.elem_count())
+        return Error::from(bail("shape mismatch in AdamW step: param " + dims_to_string(param.dims()) + ", grad " +
+                                dims_to_string(grad.dims()) + ", state " + dims_to_string(st->m.dims())));
+    auto out = Tensor::empty(param.dims(), DType::F32, param.device());
+    if (out.is_err()) return Error::from(out.error());
+    const mc_adamw_config cfg{config_.learning_rate, config_.beta1, config_.beta2, config_.epsilon,
+                              config_.weight_decay};
+    const mc_adamw_tensor t{static_cast<const float*>(param.data()), static_cast<const float*>(grad.data()),
+                            static_cast<float*>(st->m.data()), static_cast<float*>(st->v.data()),
+                            static_cast<float*>(out.value().data()), param.elem_count(), (int64_t)step_count_};
+    const mc_status rc = mc_adamw_step(&cfg, &t, 1, nullptr);
+    if (rc != MC_OK) return Error::from(mc_error("mc_adamw_step", rc));
+    return std::move(out.value());
+}
+
+void AdamW::reset_state() {
+    step_count_ = 0;
+    for (auto& kv : state_) {
+        auto m = Tensor::zeros(kv.second.m.dims(), DType::F32, kv.second.m.device());
+        auto v = Tensor::zeros(kv.second.v.dims(), DType::F32, kv.second.v.device());
+        if (m.is_ok()) kv.second.m = std::move(m.value());
+        if (v.is_ok()) kv.second.v = std::move(v.value());
+    }
 }
 
 Result<LoRALayer, Error> LoRALayer::create(size_t in_features, size_t out_features, const LoRAConfig& config,

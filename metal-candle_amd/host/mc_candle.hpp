@@ -51,11 +51,12 @@ struct CandleError {
 
 // crate::error::TrainingError (src/error.rs:94-117).
 struct TrainingError {
-    enum class Kind { InvalidLoRAConfig, InvalidConfig, Failed };
+    enum class Kind { InvalidLoRAConfig, InvalidConfig, Failed, StateError };
     Kind kind = Kind::Failed;
     std::string reason;
     static TrainingError failed(std::string r) { return {Kind::Failed, std::move(r)}; }
     static TrainingError invalid_config(std::string r) { return {Kind::InvalidConfig, std::move(r)}; }
+    static TrainingError state_error(std::string r) { return {Kind::StateError, std::move(r)}; }
     std::string to_string() const;
 };
 
@@ -282,6 +283,47 @@ private:
     LoRASaved saved_;
     Tensor mask_;
     bool have_saved_ = false;
+};
+
+// ------------------------------------------------------------------ AdamW
+// AdamWConfig (optimizer.rs:33-104): defaults and validate() with the
+// reference's messages.
+struct AdamWConfig {
+    float learning_rate = 1e-4f;
+    float beta1 = 0.9f;
+    float beta2 = 0.999f;
+    float epsilon = 1e-8f;
+    float weight_decay = 0.01f;
+    Result<void, Error> validate() const;
+};
+
+// AdamW (optimizer.rs:130-362) over fp32 HIP tensors. Like the reference,
+// step() returns the updated parameter as a new tensor, keeps the moments per
+// parameter name, and counts one step per step() call (the count is shared
+// by all parameters and drives the bias correction). The update itself is
+// one mc_adamw_step launch.
+class AdamW {
+public:
+    static Result<AdamW, Error> create(const AdamWConfig& config);
+    // add_parameter (optimizer.rs:196-205): zero moments of the param's shape.
+    Result<void, Error> add_parameter(const std::string& name, const Tensor& param);
+    // step (optimizer.rs:227-281).
+    Result<Tensor, Error> step(const std::string& name, const Tensor& param, const Tensor& grad);
+    void set_lr(float lr) { config_.learning_rate = lr; }
+    float learning_rate() const { return config_.learning_rate; }
+    size_t step_count() const { return step_count_; }
+    const AdamWConfig& config() const { return config_; }
+    // reset_state (optimizer.rs:333-349): step count 0, moments zeroed.
+    void reset_state();
+
+private:
+    struct State {
+        Tensor m, v;
+    };
+    AdamWConfig config_;
+    std::vector<std::pair<std::string, State>> state_;
+    size_t step_count_ = 0;
+    State* find(const std::string& name);
 };
 
 // ------------------------------------------------------------------ graph

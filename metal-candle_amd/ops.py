@@ -12,7 +12,7 @@ import ctypes
 import torch
 
 from . import _lib
-from ._lib import AttnDesc, LoraDesc, McError, check, lib
+from ._lib import AdamWConfig, AdamWTensor, AttnDesc, LoraDesc, McError, check, lib
 
 _DTYPES = {torch.float32: _lib.MC_F32, torch.bfloat16: _lib.MC_BF16}
 
@@ -159,6 +159,37 @@ def attention_backward(q, k, v, o, lse, dout, causal=False, scale=None, mask=Non
     check(lib().mc_attention_bwd(ctypes.byref(d), _ptr(q), _ptr(k), _ptr(v), _ptr(mask), _ptr(o), _ptr(lse),
                                  _ptr(dout), _ptr(dq), _ptr(dk), _ptr(dv), _ptr(ws), ws_n, _stream(q)))
     return dq, dk, dv
+
+
+def adamw_step(params, grads, ms, vs, steps, lr=1e-4, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=0.01,
+               outs=None):
+    """AdamW::step (src/training/optimizer.rs:227-281) for a list of fp32
+    tensors in one call: m and v are updated in place; the new parameters go
+    to outs (default: the params themselves, in place). steps: one step count
+    per tensor (or one int for all)."""
+    n = len(params)
+    if isinstance(steps, int):
+        steps = [steps] * n
+    outs = params if outs is None else outs
+    for group, name in ((params, "param"), (grads, "grad"), (ms, "m"), (vs, "v"), (outs, "param_out")):
+        if len(group) != n:
+            raise McError(_lib.MC_ERR_SHAPE, f"{name} list has {len(group)} entries, expected {n}")
+        for t in group:
+            _contig(t, name)
+            if t.dtype != torch.float32:
+                raise McError(_lib.MC_ERR_DTYPE, f"{name} must be float32")
+    table = (AdamWTensor * max(n, 1))()
+    for i in range(n):
+        numel = params[i].numel()
+        for t in (grads[i], ms[i], vs[i], outs[i]):
+            if t.numel() != numel:
+                raise McError(_lib.MC_ERR_SHAPE, f"tensor {i}: element counts differ")
+        table[i] = AdamWTensor(params[i].data_ptr(), grads[i].data_ptr(), ms[i].data_ptr(), vs[i].data_ptr(),
+                               outs[i].data_ptr(), numel, int(steps[i]))
+    cfg = AdamWConfig(lr, beta1, beta2, eps, weight_decay)
+    stream = _stream(params[0]) if n else None
+    check(lib().mc_adamw_step(ctypes.byref(cfg), table, n, stream))
+    return outs
 
 
 def dropout_mask(seed, p, rows, rank):

@@ -49,6 +49,8 @@ def lib():
         _i32 = ctypes.c_int32
         L.oracle_attention_fwd.argtypes = [_i64, _i32, _i32, _i64, _i32, ctypes.c_float, ctypes.c_int,
                                            _f32p, _f32p, _f32p, _f32p, _f32p, _f32p, ctypes.c_int]
+        L.oracle_adamw_step.argtypes = [_i64, ctypes.c_float, ctypes.c_float, ctypes.c_float, ctypes.c_float,
+                                        ctypes.c_float, _i64, _f32p, _f32p, _f32p, _f32p, _f32p]
         L.oracle_attention_bwd.argtypes = [_i64, _i32, _i32, _i64, _i32, ctypes.c_float, ctypes.c_int,
                                            _f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p,
                                            ctypes.c_int]
@@ -199,3 +201,12 @@ def attention_bwd(q, k, v, dout, scale, causal=False, mask=None, threads=0):
     lib().oracle_attention_bwd(B, H, Hkv, S, D, scale, int(causal), _f(q), _f(k), _f(v), _f(mask), _f(dout),
                                _f(dq), _f(dk), _f(dv), threads)
     return dq, dk, dv
+
+
+def adamw_step(param, grad, m, v, step, lr=1e-4, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=0.01):
+    """One AdamW::step: returns (param_new, m_new, v_new); the inputs are not modified."""
+    p, g = _c32(param).copy(), _c32(grad)
+    m, v = _c32(m).copy(), _c32(v).copy()
+    out = np.empty_like(p)
+    lib().oracle_adamw_step(p.size, lr, beta1, beta2, eps, weight_decay, step, _f(p), _f(g), _f(m), _f(v), _f(out))
+    return out, m, v

@@ -448,6 +448,56 @@ void oracle_attention_bwd(int64_t B, int32_t H, int32_t Hkv, int64_t S, int32_t 
     free(part);
 }
 
+/* ----------------------------------------------------------------- AdamW */
+/* AdamW::step (src/training/optimizer.rs:227-281) as the reference evaluates
+ * it: candle fp32 tensor ops, one rounding each, in this order. `tensor * f64`
+ * and `tensor + f64` are candle's affine(mul, add) = v * mul + add in fp32
+ * (candle-core 0.9 CPU backend, not vendored), `tensor / f64` is
+ * affine(1 / x, 0) with the reciprocal taken in f64. beta^t is f32::powi
+ * (optimizer.rs:257-258), which a run-time exponent lowers to right-to-left
+ * binary exponentiation in fp32. The Makefile builds with -ffp-contract=off,
+ * so no multiply-add is fused. */
+static float powi_f32(float base, int32_t t) {
+    float r = 1.0f;
+    for (;;) {
+        if (t & 1) r *= base;
+        t /= 2;
+        if (t == 0) break;
+        base *= base;
+    }
+    return r;
+}
+
+static float affine0(float x, float mul) {
+    const float y = x * mul;
+    return y + 0.0f;
+}
+
+void oracle_adamw_step(int64_t n, float lr, float beta1, float beta2, float eps, float wd, int64_t step,
+                       const float* param, const float* grad, float* m, float* v, float* param_out) {
+    const float omb1 = 1.0f - beta1, omb2 = 1.0f - beta2;                   /* 243, 248 */
+    const float c1 = (float)(1.0 / (double)(1.0f - powi_f32(beta1, (int32_t)step)));  /* 260 */
+    const float c2 = (float)(1.0 / (double)(1.0f - powi_f32(beta2, (int32_t)step)));  /* 261 */
+    const float wdlr = wd * lr;                                              /* 272 */
+    for (int64_t i = 0; i < n; ++i) {
+        const float g = grad[i], p = param[i];
+        const float m1 = affine0(m[i], beta1) + affine0(g, omb1);           /* 242-243 */
+        const float g2 = g * g;                                              /* 246 */
+        const float v1 = affine0(v[i], beta2) + affine0(g2, omb2);          /* 247-248 */
+        const float mh = affine0(m1, c1);                                    /* 260 */
+        const float vh = affine0(v1, c2);                                    /* 261 */
+        const float sq = sqrtf(vh);                                          /* 264 */
+        const float den = sq * 1.0f + eps;                                   /* 265 */
+        const float u = mh / den;                                            /* 266 */
+        const float lru = affine0(u, lr);                                    /* 269 */
+        const float wdu = affine0(p, wdlr);                                  /* 272 */
+        const float p1 = p - lru;                                            /* 275 */
+        param_out[i] = p1 - wdu;
+        m[i] = m1;                                                           /* 278-279 */
+        v[i] = v1;
+    }
+}
+
 /* ------------------------------------------------------------------ bf16 */
 void oracle_round_bf16(const float* in, float* out, int64_t n) {
     for (int64_t i = 0; i < n; ++i) {

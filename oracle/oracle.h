@@ -16,6 +16,7 @@
  *                src/models/qwen.rs:314-325     (then * weight)
  *   softmax      src/backend/tensor.rs:91-98    (max, sub, exp, sum, divide)
  *                src/models/transformer.rs:264-275 (causal -inf mask added first)
+ *   AdamW        src/training/optimizer.rs:227-281 (fp32 op order of the step)
  *   dropout      candle_nn::ops::dropout (candle-nn 0.9, not vendored): keep iff
  *                U >= p, kept values scaled by 1/(1-p); the mask itself comes
  *                from the Philox4x32-10 generator below, shared with the GPU path.
@@ -45,6 +46,11 @@
  *                        torch.nn.functional.scaled_dot_product_attention on
  *                        the CPU in fp64 as a library cross-check, GQA equal to
  *                        explicitly repeated K/V heads.
+ *   oracle_adamw_step    the reference's own AdamW tests (optimizer.rs:395-509:
+ *                        lr 0.1 on ones gives 0.899 after one step, five
+ *                        default steps lower the sum), the constant-gradient
+ *                        closed form (m_hat = g, v_hat = g^2 at every step),
+ *                        torch.optim.AdamW as a library cross-check.
  *   oracle_attention_bwd central finite differences of <o, dO> in fp64 for
  *                        q, k and v, torch autograd of the fp64 composite.
  *
@@ -125,6 +131,11 @@ void oracle_attention_fwd(int64_t B, int32_t H, int32_t Hkv, int64_t S, int32_t 
 void oracle_attention_bwd(int64_t B, int32_t H, int32_t Hkv, int64_t S, int32_t D, float scale, int causal,
                           const float* q, const float* k, const float* v, const float* mask, const float* dout,
                           float* dq, float* dk, float* dv, int threads);
+
+/* One AdamW::step over n fp32 values: m, v updated in place, the new
+ * parameter written to param_out (may equal param). */
+void oracle_adamw_step(int64_t n, float lr, float beta1, float beta2, float eps, float wd, int64_t step,
+                       const float* param, const float* grad, float* m, float* v, float* param_out);
 
 void oracle_round_bf16(const float* in, float* out, int64_t n);
 

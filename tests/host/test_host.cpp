@@ -716,6 +716,137 @@ CASE(fused_lora_with_base_bf16, true) {
     CHECK_LE(rel_err(vh, transpose(rh, T, r)), kTolF32 * 10);
 }
 
+// ================================================================== AdamW
+// optimizer.rs:367-375 test_adamw_config_default
+CASE(adamw_config_default, false) {
+    const AdamWConfig c;
+    CHECK(fabs((double)c.learning_rate - 1e-4) < 1e-7);
+    CHECK(fabs((double)c.beta1 - 0.9) < 1e-7);
+    CHECK(fabs((double)c.beta2 - 0.999) < 1e-7);
+    CHECK(fabs((double)c.epsilon - 1e-8) < 1e-7);
+    CHECK(fabs((double)c.weight_decay - 0.01) < 1e-7);
+}
+
+// optimizer.rs:377-399 test_adamw_config_validation, with the messages of 67-103
+CASE(adamw_config_validation, false) {
+    CHECK(AdamWConfig().validate().is_ok());
+    const char* prefix = "training error: invalid training configuration: ";
+    AdamWConfig c;
+    c.learning_rate = -1.f;
+    CHECK(c.validate().is_err() && c.validate().error().to_string() == std::string(prefix) + "learning rate must be positive");
+    c = AdamWConfig();
+    c.beta1 = 1.5f;
+    CHECK(c.validate().is_err() && c.validate().error().to_string() == std::string(prefix) + "beta1 must be in [0, 1), got 1.5");
+    c = AdamWConfig();
+    c.beta2 = -0.1f;
+    CHECK(c.validate().is_err() && c.validate().error().to_string() == std::string(prefix) + "beta2 must be in [0, 1), got -0.1");
+    c = AdamWConfig();
+    c.epsilon = 0.f;
+    CHECK(c.validate().is_err() && c.validate().error().to_string() == std::string(prefix) + "epsilon must be positive");
+    c = AdamWConfig();
+    c.weight_decay = -0.5f;
+    CHECK(c.validate().is_err() && c.validate().error().to_string() == std::string(prefix) + "weight decay must be non-negative");
+}
+
+// optimizer.rs:401-409 test_adamw_creation
+CASE(adamw_creation, false) {
+    TRY(opt, AdamW::create(AdamWConfig()));
+    CHECK(opt.step_count() == 0);
+    AdamWConfig bad;
+    bad.learning_rate = 0.f;
+    CHECK(AdamW::create(bad).is_err());
+}
+
+// optimizer.rs:411-420 test_adamw_add_parameter
+CASE(adamw_add_parameter, false) {
+    TRY(opt, AdamW::create(AdamWConfig()));
+    TRY(p, Tensor::zeros({10, 10}, DType::F32, kCpu));
+    CHECK(opt.add_parameter("test_param", p).is_ok());
+}
+
+// optimizer.rs:490-508 test_adamw_parameter_not_found
+CASE(adamw_parameter_not_found, false) {
+    TRY(opt, AdamW::create(AdamWConfig()));
+    TRY(p, Tensor::from_slice(std::vector<float>(9, 1.f), {3, 3}, kCpu));
+    auto r = opt.step("unknown", p, p);
+    CHECK(r.is_err());
+    if (r.is_err())
+        CHECK(r.error().to_string() == "training error: training state error: parameter 'unknown' not found in optimizer");
+}
+
+// Runs `steps` AdamW steps of the oracle on host copies; returns the last parameter.
+static std::vector<float> adamw_oracle(const AdamWConfig& c, std::vector<float> p, const std::vector<float>& g,
+                                       int first_step, int steps) {
+    std::vector<float> m(p.size(), 0.f), v(p.size(), 0.f), out(p.size());
+    for (int t = first_step; t < first_step + steps; ++t) {
+        oracle_adamw_step((int64_t)p.size(), c.learning_rate, c.beta1, c.beta2, c.epsilon, c.weight_decay, t, p.data(),
+                          g.data(), m.data(), v.data(), out.data());
+        p = out;
+    }
+    return p;
+}
+
+// optimizer.rs:422-446 test_adamw_step
+CASE(adamw_step, true) {
+    AdamWConfig c;
+    c.learning_rate = 0.1f;
+    TRY(opt, AdamW::create(c));
+    const std::vector<float> ones(25, 1.f);
+    TRY(p, Tensor::from_slice(ones, {5, 5}, kHip));
+    TRY(g, Tensor::from_slice(ones, {5, 5}, kHip));
+    CHECK(opt.add_parameter("param", p).is_ok());
+    TRY(p1, opt.step("param", p, g));
+    CHECK(p1.dims() == std::vector<int64_t>({5, 5}));
+    TRY(v1, p1.to_vec_f32());
+    double sum = 0;
+    for (float x : v1) sum += x;
+    CHECK(fabs(25.0 - sum) > 1e-6);
+    CHECK(opt.step_count() == 1);
+    CHECK(v1 == adamw_oracle(c, ones, ones, 1, 1));  // bit for bit
+}
+
+// optimizer.rs:448-470 test_adamw_multiple_steps
+CASE(adamw_multiple_steps, true) {
+    const AdamWConfig c;
+    TRY(opt, AdamW::create(c));
+    const std::vector<float> ones(9, 1.f);
+    TRY(p, Tensor::from_slice(ones, {3, 3}, kHip));
+    TRY(g, Tensor::from_slice(ones, {3, 3}, kHip));
+    CHECK(opt.add_parameter("param", p).is_ok());
+    Tensor cur = p;
+    for (int i = 0; i < 5; ++i) {
+        TRY(next, opt.step("param", cur, g));
+        cur = next;
+    }
+    CHECK(opt.step_count() == 5);
+    TRY(v, cur.to_vec_f32());
+    double sum = 0;
+    for (float x : v) sum += x;
+    CHECK(sum < 9.0);
+    CHECK(v == adamw_oracle(c, ones, ones, 1, 5));
+}
+
+// optimizer.rs:472-488 test_adamw_reset_state
+CASE(adamw_reset_state, true) {
+    const AdamWConfig c;
+    TRY(opt, AdamW::create(c));
+    const std::vector<float> ones(9, 1.f);
+    TRY(p, Tensor::from_slice(ones, {3, 3}, kHip));
+    TRY(g, Tensor::from_slice(ones, {3, 3}, kHip));
+    CHECK(opt.add_parameter("param", p).is_ok());
+    TRY(a, opt.step("param", p, g));
+    TRY(b, opt.step("param", p, g));
+    CHECK(opt.step_count() == 2);
+    opt.reset_state();
+    CHECK(opt.step_count() == 0);
+    // after the reset the next step is a first step from zero moments
+    TRY(c1, opt.step("param", p, g));
+    TRY(vc, c1.to_vec_f32());
+    CHECK(vc == adamw_oracle(c, ones, ones, 1, 1));
+    (void)a;
+    (void)b;
+}
+
 // ================================================================== main
 int main(int argc, char** argv) {
     bool gpu = false;

@@ -134,3 +134,36 @@ def test_attention_null_workspace_and_layout_errors(mc):
     # fp32 and other bf16 head dims take the workspace-free kernel
     assert L.mc_attention_fwd_workspace_size(ctypes.byref(_attn(mc, dtype=0))) == 0
     assert L.mc_attention_fwd_workspace_size(ctypes.byref(_attn(mc, D=32))) == 0
+
+
+@pytest.mark.parametrize("field,value,msg", [
+    ("learning_rate", 0.0, "learning rate must be positive"),          # optimizer.rs:68-73
+    ("learning_rate", -1.0, "learning rate must be positive"),
+    ("beta1", 1.5, "beta1 must be in [0, 1), got 1.5"),               # optimizer.rs:75-80
+    ("beta2", -0.1, "beta2 must be in [0, 1), got -0.1"),             # optimizer.rs:82-87
+    ("epsilon", 0.0, "epsilon must be positive"),                      # optimizer.rs:89-94
+    ("weight_decay", -0.01, "weight decay must be non-negative"),      # optimizer.rs:96-101
+])
+def test_adamw_config_validation(mc, field, value, msg):
+    L = mc._lib.lib()
+    cfg = mc._lib.AdamWConfig(1e-4, 0.9, 0.999, 1e-8, 0.01)
+    setattr(cfg, field, value)
+    assert L.mc_adamw_step(ctypes.byref(cfg), None, 0, None) == 5
+    assert mc._lib.last_error() == msg
+
+
+def test_adamw_table_errors(mc):
+    L = mc._lib.lib()
+    cfg = mc._lib.AdamWConfig(1e-4, 0.9, 0.999, 1e-8, 0.01)
+    assert L.mc_adamw_step(ctypes.byref(cfg), None, 0, None) == 0   # nothing to do
+    assert L.mc_adamw_step(None, None, 0, None) == 1
+    assert L.mc_adamw_step(ctypes.byref(cfg), None, 2, None) == 1
+    t = (mc._lib.AdamWTensor * 1)()
+    t[0] = mc._lib.AdamWTensor(256, 256, 256, 256, 256, 10, 0)
+    assert L.mc_adamw_step(ctypes.byref(cfg), t, 1, None) == 5 and "step" in mc._lib.last_error()
+    t[0] = mc._lib.AdamWTensor(256, 256, None, 256, 256, 10, 1)
+    assert L.mc_adamw_step(ctypes.byref(cfg), t, 1, None) == 1
+    t[0] = mc._lib.AdamWTensor(256, 260, 256, 256, 256, 10, 1)
+    assert L.mc_adamw_step(ctypes.byref(cfg), t, 1, None) == 4
+    t[0] = mc._lib.AdamWTensor(None, None, None, None, None, 0, 1)   # empty tensors need no pointers
+    assert L.mc_adamw_step(ctypes.byref(cfg), t, 1, None) == 0

@@ -1,7 +1,8 @@
 """C++ host interface (metal-candle_amd/host/mc_candle.hpp): the cases that
 need no GPU — LoRAConfig / LoRALayer validation, FusedLoRAOp::new checks, op
 names, the CPU-forward errors, AsyncExecutor input-count errors, Operation
-shapes and the dropout-mask generator — with the reference's messages."""
+shapes, the dropout-mask generator and AdamWConfig / AdamW state handling —
+with the reference's messages."""
 import host_runner
 
 
