@@ -33,8 +33,9 @@ same run at the layer's attention shape, outside the step and outside value:
 the "attention" object gives its per-call times and MFMA rate (FLOPs of the
 score and P.V products over the causal lower triangle; the backward counts
 its four algorithmic products, not the recomputation). The "adamw" object
-times one AdamW step (mc_adamw_step) over the layer's LoRA parameters, also
-outside the step.
+times one AdamW step (mc_adamw_step) over the layer's LoRA parameters, and
+"row_ops" the LayerNorm and cross-entropy row kernels (cross entropy over a
+Qwen2.5-sized vocabulary of 151936), also outside the step.
 """
 import argparse
 import json
@@ -292,6 +293,50 @@ def adamw_update(mc, c, dev, iters):
             "bytes_per_call": by / calls}
 
 
+QWEN_VOCAB = 151936  # Qwen2.5 vocabulary: the LM head's logits row
+
+
+def row_ops(mc, c, dev, iters):
+    """LayerNorm fwd / bwd at the layer's [tokens, hidden] (with weight and
+    bias, as the embeddings' MetalLayerNorm) and the cross-entropy loss fwd /
+    bwd over [tokens, vocabulary] logits, each timed per call by the library's
+    profiling hook; GB/s from the algorithmic bytes of each call."""
+    import torch
+
+    T, D = c["batch"] * c["seq"], c["hidden"]
+    g = torch.Generator(device=dev).manual_seed(13)
+    x = torch.randn(T, D, device=dev, generator=g).to(torch.bfloat16)
+    w = (torch.randn(D, device=dev, generator=g) * 0.1 + 1).to(torch.bfloat16)
+    b = (torch.randn(D, device=dev, generator=g) * 0.1).to(torch.bfloat16)
+    dy = torch.randn(T, D, device=dev, generator=g).to(torch.bfloat16)
+    logits = torch.randn(T, QWEN_VOCAB, device=dev, generator=g).to(torch.bfloat16)
+    targets = torch.randint(0, QWEN_VOCAB, (T,), device=dev, generator=g, dtype=torch.int32)
+    y, mean, rstd = mc.layer_norm_forward(x, 1e-5, w, b)
+    loss, stats = mc.cross_entropy_forward(logits, targets)
+    calls = {
+        "layernorm_fwd": lambda: mc.layer_norm_forward(x, 1e-5, w, b),
+        "layernorm_bwd": lambda: mc.layer_norm_backward(x, dy, 1e-5, w, mean, rstd),
+        "cross_entropy_fwd": lambda: mc.cross_entropy_forward(logits, targets),
+        "cross_entropy_bwd": lambda: mc.cross_entropy_backward(logits, targets, stats),
+    }
+    out = {"layernorm_shape": [T, D], "cross_entropy_shape": [T, QWEN_VOCAB], "dtype": "bf16", "iters": iters}
+    for name, fn in calls.items():
+        fn()
+        torch.cuda.synchronize()
+        mc._lib.check(mc._lib.lib().mc_profile_reset())
+        mc._lib.check(mc._lib.lib().mc_profile_enable(1))
+        for _ in range(iters):
+            fn()
+        torch.cuda.synchronize()
+        mc._lib.check(mc._lib.lib().mc_profile_enable(0))
+        mc._lib.check(mc._lib.lib().mc_profile_collect())
+        ms, n, _, by = mc._lib.profile_read("rowops")
+        out[name] = {"us_per_call": ms * 1e3 / n, "GB_s": by / (ms * 1e-3) / 1e9,
+                     "hbm_frac": by / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+    del logits
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -414,6 +459,7 @@ def main():
         line["attention"] = attention_core(mc, c, dev, args.attention_iters)
     if args.attention_iters > 0:
         line["adamw"] = adamw_update(mc, c, dev, 20)
+        line["row_ops"] = row_ops(mc, c, dev, args.attention_iters)
     if not args.no_cpu_baseline:
         threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
         v, dt = cpu_baseline(c, args.cpu_tokens, threads)

@@ -28,6 +28,10 @@
  *   mc_attention_bwd no reference kernel: autograd of the same composite.
  *   mc_adamw_step    AdamW::step (src/training/optimizer.rs:227-281) for many
  *                    parameter tensors per launch.
+ *   mc_layernorm_*   LayerNormOp (custom_ops.rs:826-1079) with the weight and
+ *                    bias of MetalLayerNorm (src/embeddings/metal_bert.rs).
+ *   mc_log_softmax_*, mc_cross_entropy_*  cross_entropy_loss and its label
+ *                    smoothing (src/training/loss.rs:58-245).
  *
  * Conventions (all entry points):
  *  - Device buffers are caller-owned, row-major and contiguous; inputs are
@@ -221,6 +225,66 @@ typedef struct mc_adamw_tensor {
 mc_status mc_adamw_step(const mc_adamw_config* cfg, const mc_adamw_tensor* tensors, int32_t count,
                         hipStream_t stream);
 
+/* LayerNorm over the last dim of x [rows, dim] (LayerNormOp,
+ * src/backend/custom_ops.rs:826-1079; its CPU path cpu_fwd and
+ * TensorExt::layer_norm, src/backend/tensor.rs:100-109; the weight and bias
+ * of MetalLayerNorm::forward, src/embeddings/metal_bert.rs:30-72):
+ *   mean = sum(x)/D, var = sum((x - mean)^2)/D, y = (x - mean)/sqrt(var + eps) * w + b
+ * w, b may be NULL (none, as LayerNormOp); mean, rstd [rows] fp32 may be NULL. */
+mc_status mc_layernorm_fwd(int64_t rows, int64_t dim, float eps, int32_t dtype, const void* x,
+                           const void* w, const void* b, void* y, float* mean, float* rstd,
+                           hipStream_t stream);
+
+size_t mc_layernorm_bwd_workspace_size(int64_t rows, int64_t dim);
+
+/* Backward (no reference kernel: autograd of the composite): with
+ * xh = (x - mean) rstd and g = dy w,
+ *   dx = rstd (g - mean(g) - xh mean(g xh)), dw = sum_rows dy xh, db = sum_rows dy
+ * mean and rstd may be NULL (recomputed, both or neither); dw, db (fp32 [dim])
+ * may be NULL; they are reduced in a fixed order (reproducible). */
+mc_status mc_layernorm_bwd(int64_t rows, int64_t dim, float eps, int32_t dtype, const void* x,
+                           const void* w, const float* mean, const float* rstd, const void* dy,
+                           void* dx, float* dw, float* db, void* workspace, size_t workspace_bytes,
+                           hipStream_t stream);
+
+/* log-softmax over the last dim (candle_nn::ops::log_softmax as
+ * cross_entropy_loss uses it, src/training/loss.rs:108):
+ *   y = (x - max) - log(sum(exp(x - max)));  backward dx = dy - exp(y) sum(dy). */
+mc_status mc_log_softmax_fwd(int64_t rows, int64_t dim, int32_t dtype, const void* x, void* y,
+                             hipStream_t stream);
+mc_status mc_log_softmax_bwd(int64_t rows, int64_t dim, int32_t dtype, const void* y,
+                             const void* dy, void* dx, hipStream_t stream);
+
+/* Cross-entropy loss (cross_entropy_loss, src/training/loss.rs:58-148, and
+ * cross_entropy_loss_with_smoothing, loss.rs:208-245) over logits
+ * [rows, vocab] (rows = batch * seq_len) and uint32 targets [rows]:
+ *   loss = -mean over counted rows of log_softmax(logits)[target]
+ *   counted rows: target != ignore_index (every row when ignore_index < 0)
+ *   smoothing s > 0: (1 - s) * loss + s * (-mean of every log-probability,
+ *   ignored rows included, as the reference's log_probs.mean_all())
+ * loss: fp32 [1], device. stats (fp32 [rows + 1], may be NULL): per-row
+ * log-sum-exp, then the count of counted rows; mc_cross_entropy_bwd needs it.
+ * Where the reference returns an error the loss is NaN instead (the count is
+ * only known on the device): every row ignored, or a counted target >= vocab. */
+typedef struct mc_xent_desc {
+    int64_t rows;          /* >= 1 */
+    int64_t vocab;         /* >= 1 */
+    int64_t ignore_index;  /* < 0: none (the reference's Option<u32> None) */
+    float smoothing;       /* [0, 1) */
+    int32_t dtype;         /* mc_dtype of logits and dlogits */
+} mc_xent_desc;
+
+size_t mc_cross_entropy_workspace_size(const mc_xent_desc* d);
+
+mc_status mc_cross_entropy_fwd(const mc_xent_desc* d, const void* logits, const uint32_t* targets,
+                               float* loss, float* stats, void* workspace, size_t workspace_bytes,
+                               hipStream_t stream);
+
+/* dlogits = dloss ((1 - s) [counted] (p - onehot(target)) / count + s (p - 1/vocab) / rows),
+ * p = softmax(logits); dloss: fp32 [1] device (the loss gradient, usually 1). */
+mc_status mc_cross_entropy_bwd(const mc_xent_desc* d, const void* logits, const uint32_t* targets,
+                               const float* stats, const float* dloss, void* dlogits, hipStream_t stream);
+
 /* Host-side dropout keep-mask [rows, rank] from a seed (Philox4x32-10; element
  * i = t*rank + j uses counter block i/4, word i%4, key = seed; keep iff
  * (word >> 8) * 2^-24 >= p). Both the GPU path and the CPU reference are fed
@@ -237,7 +301,8 @@ mc_status mc_dropout_mask(uint64_t seed, float p, int64_t rows, int32_t rank, ui
  * returns the totals of one class. Classes: 0 = MFMA GEMM (FLOPs count the
  * base x.W^T / dY.W product only), 1 = rank-r kernels, 2 = RMSNorm,
  * 3 = softmax, 4 = attention (FLOPs of the unmasked score and P.V products),
- * 5 = AdamW (bytes: 28 per element).
+ * 5 = AdamW (bytes: 28 per element), 6 = LayerNorm / log-softmax /
+ * cross-entropy.
  * Enabling allocates hipEvents (not for allocation-free use). */
 mc_status mc_profile_enable(int32_t on);
 mc_status mc_profile_collect(void);

@@ -12,7 +12,13 @@ from .ops import (  # noqa: F401
     adamw_step,
     attention_backward,
     attention_forward,
+    cross_entropy_backward,
+    cross_entropy_forward,
     dropout_mask,
+    layer_norm_backward,
+    layer_norm_forward,
+    log_softmax_backward,
+    log_softmax_forward,
     lora_backward,
     lora_forward,
     rms_norm_backward,

@@ -63,6 +63,16 @@ class AttnDesc(ctypes.Structure):
     ]
 
 
+class XentDesc(ctypes.Structure):
+    _fields_ = [
+        ("rows", ctypes.c_int64),
+        ("vocab", ctypes.c_int64),
+        ("ignore_index", ctypes.c_int64),
+        ("smoothing", ctypes.c_float),
+        ("dtype", ctypes.c_int32),
+    ]
+
+
 class AdamWConfig(ctypes.Structure):
     _fields_ = [
         ("learning_rate", ctypes.c_float),
@@ -109,6 +119,15 @@ _SIGNATURES = {
     "mc_attention_fwd": (ctypes.c_int, [_ap, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "mc_attention_bwd_workspace_size": (_sz, [_ap]),
     "mc_attention_bwd": (ctypes.c_int, [_ap, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "mc_layernorm_fwd": (ctypes.c_int, [_i64, _i64, _f32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "mc_layernorm_bwd_workspace_size": (_sz, [_i64, _i64]),
+    "mc_layernorm_bwd": (ctypes.c_int, [_i64, _i64, _f32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz,
+                                        _vp]),
+    "mc_log_softmax_fwd": (ctypes.c_int, [_i64, _i64, _i32, _vp, _vp, _vp]),
+    "mc_log_softmax_bwd": (ctypes.c_int, [_i64, _i64, _i32, _vp, _vp, _vp, _vp]),
+    "mc_cross_entropy_workspace_size": (_sz, [ctypes.POINTER(XentDesc)]),
+    "mc_cross_entropy_fwd": (ctypes.c_int, [ctypes.POINTER(XentDesc), _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "mc_cross_entropy_bwd": (ctypes.c_int, [ctypes.POINTER(XentDesc), _vp, _vp, _vp, _vp, _vp, _vp]),
     "mc_adamw_step": (ctypes.c_int, [ctypes.POINTER(AdamWConfig), ctypes.POINTER(AdamWTensor), _i32, _vp]),
     "mc_dropout_mask": (ctypes.c_int, [ctypes.c_uint64, _f32, _i64, _i32, _vp]),
     "mc_profile_enable": (ctypes.c_int, [_i32]),
@@ -118,7 +137,7 @@ _SIGNATURES = {
     "mc_profile_reset": (ctypes.c_int, []),
 }
 
-PROFILE_KINDS = {"gemm": 0, "lowrank": 1, "rmsnorm": 2, "softmax": 3, "attention": 4, "adamw": 5}
+PROFILE_KINDS = {"gemm": 0, "lowrank": 1, "rmsnorm": 2, "softmax": 3, "attention": 4, "adamw": 5, "rowops": 6}
 
 _lib = None
 

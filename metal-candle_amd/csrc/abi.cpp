@@ -415,6 +415,120 @@ mc_status mc_adamw_step(const mc_adamw_config* cfg, const mc_adamw_tensor* tenso
     return ok();
 }
 
+size_t mc_layernorm_bwd_workspace_size(int64_t rows, int64_t dim) {
+    if (rows < 1 || dim < 1) return 0;
+    return 2 * (size_t)mc::layernorm_bwd_blocks(rows) * (size_t)dim * sizeof(float);
+}
+
+mc_status mc_layernorm_fwd(int64_t rows, int64_t dim, float eps, int32_t dtype, const void* x, const void* w,
+                           const void* b, void* y, float* mean, float* rstd, hipStream_t stream) {
+    mc_status s = check_rows(rows, dim, "LayerNorm");
+    if (s != MC_OK) return s;
+    if ((s = check_dtype(dtype, "LayerNorm")) != MC_OK) return s;
+    MC_CHECK(eps >= 0.0f && std::isfinite(eps), MC_ERR_VALUE, "LayerNorm: eps must be finite and >= 0");
+    MC_CHECK(x && y, MC_ERR_NULL, "LayerNorm: x and y must not be NULL");
+    MC_CHECK(aligned16(x) && aligned16(y) && (!w || aligned16(w)) && (!b || aligned16(b)), MC_ERR_LAYOUT,
+             "LayerNorm: x, w, b and y must be 16-byte aligned");
+    const double es = dtype == MC_F32 ? 4.0 : 2.0;
+    mc::prof::Scope sc(mc::prof::kRowOps, stream, 0.0,
+                       es * (2.0 * rows * dim) + (mean ? 4.0 * rows : 0.0) + (rstd ? 4.0 * rows : 0.0));
+    return hip_status(mc::launch_layernorm_fwd(rows, dim, eps, dtype, x, w, b, y, mean, rstd, stream),
+                      "LayerNorm forward");
+}
+
+mc_status mc_layernorm_bwd(int64_t rows, int64_t dim, float eps, int32_t dtype, const void* x, const void* w,
+                           const float* mean, const float* rstd, const void* dy, void* dx, float* dw, float* db,
+                           void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    mc_status s = check_rows(rows, dim, "LayerNorm backward");
+    if (s != MC_OK) return s;
+    if ((s = check_dtype(dtype, "LayerNorm backward")) != MC_OK) return s;
+    MC_CHECK(eps >= 0.0f && std::isfinite(eps), MC_ERR_VALUE, "LayerNorm: eps must be finite and >= 0");
+    MC_CHECK(x && dy && dx, MC_ERR_NULL, "LayerNorm backward: x, dy and dx must not be NULL");
+    MC_CHECK(!mean == !rstd, MC_ERR_NULL, "LayerNorm backward: pass both mean and rstd, or neither");
+    MC_CHECK(aligned16(x) && aligned16(dy) && aligned16(dx) && (!w || aligned16(w)), MC_ERR_LAYOUT,
+             "LayerNorm backward: x, w, dy and dx must be 16-byte aligned");
+    if (dw || db) {
+        const size_t need = mc_layernorm_bwd_workspace_size(rows, dim);
+        MC_CHECK(workspace && workspace_bytes >= need, MC_ERR_WORKSPACE,
+                 "LayerNorm backward: workspace of %zu bytes required for dw / db, %zu given", need, workspace_bytes);
+        MC_CHECK(aligned16(workspace), MC_ERR_LAYOUT, "LayerNorm backward: workspace must be 16-byte aligned");
+    }
+    const double es = dtype == MC_F32 ? 4.0 : 2.0;
+    mc::prof::Scope sc(mc::prof::kRowOps, stream, 0.0, es * 3.0 * rows * dim);
+    return hip_status(mc::launch_layernorm_bwd(rows, dim, eps, dtype, x, w, mean, rstd, dy, dx, dw, db,
+                                               static_cast<float*>(workspace), stream),
+                      "LayerNorm backward");
+}
+
+mc_status mc_log_softmax_fwd(int64_t rows, int64_t dim, int32_t dtype, const void* x, void* y, hipStream_t stream) {
+    mc_status s = check_rows(rows, dim, "log_softmax");
+    if (s != MC_OK) return s;
+    if ((s = check_dtype(dtype, "log_softmax")) != MC_OK) return s;
+    MC_CHECK(rows < 2147483647, MC_ERR_SHAPE, "log_softmax: rows must be < 2^31");
+    MC_CHECK(x && y, MC_ERR_NULL, "log_softmax: x and y must not be NULL");
+    const double es = dtype == MC_F32 ? 4.0 : 2.0;
+    mc::prof::Scope sc(mc::prof::kRowOps, stream, 0.0, es * 2.0 * rows * dim);
+    return hip_status(mc::launch_log_softmax_fwd(rows, dim, dtype, x, y, stream), "log_softmax forward");
+}
+
+mc_status mc_log_softmax_bwd(int64_t rows, int64_t dim, int32_t dtype, const void* y, const void* dy, void* dx,
+                             hipStream_t stream) {
+    mc_status s = check_rows(rows, dim, "log_softmax backward");
+    if (s != MC_OK) return s;
+    if ((s = check_dtype(dtype, "log_softmax backward")) != MC_OK) return s;
+    MC_CHECK(rows < 2147483647, MC_ERR_SHAPE, "log_softmax: rows must be < 2^31");
+    MC_CHECK(y && dy && dx, MC_ERR_NULL, "log_softmax backward: y, dy and dx must not be NULL");
+    const double es = dtype == MC_F32 ? 4.0 : 2.0;
+    mc::prof::Scope sc(mc::prof::kRowOps, stream, 0.0, es * 3.0 * rows * dim);
+    return hip_status(mc::launch_log_softmax_bwd(rows, dim, dtype, y, dy, dx, stream), "log_softmax backward");
+}
+
+static mc_status check_xent(const mc_xent_desc* d) {
+    MC_CHECK(d != nullptr, MC_ERR_NULL, "cross_entropy: descriptor is NULL");
+    mc_status s = check_dtype(d->dtype, "cross_entropy");
+    if (s != MC_OK) return s;
+    MC_CHECK(d->rows >= 1 && d->vocab >= 1 && d->rows < 2147483647, MC_ERR_SHAPE,
+             "cross_entropy: rows (%lld) and vocab (%lld) must be >= 1, rows < 2^31", (long long)d->rows,
+             (long long)d->vocab);
+    // cross_entropy_loss_with_smoothing: "smoothing must be in [0, 1), got {}" (loss.rs:214-219)
+    MC_CHECK(d->smoothing >= 0.0f && d->smoothing < 1.0f, MC_ERR_VALUE, "smoothing must be in [0, 1), got %g",
+             (double)d->smoothing);
+    return MC_OK;
+}
+
+size_t mc_cross_entropy_workspace_size(const mc_xent_desc* d) {
+    if (check_xent(d) != MC_OK) return 0;
+    return (size_t)d->rows * 3 * sizeof(float);
+}
+
+mc_status mc_cross_entropy_fwd(const mc_xent_desc* d, const void* logits, const uint32_t* targets, float* loss,
+                               float* stats, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    mc_status s = check_xent(d);
+    if (s != MC_OK) return s;
+    MC_CHECK(logits && targets && loss, MC_ERR_NULL, "cross_entropy: logits, targets and loss must not be NULL");
+    const size_t need = mc_cross_entropy_workspace_size(d);
+    MC_CHECK(workspace && workspace_bytes >= need, MC_ERR_WORKSPACE,
+             "cross_entropy: workspace of %zu bytes required, %zu given", need, workspace_bytes);
+    MC_CHECK(aligned16(workspace), MC_ERR_LAYOUT, "cross_entropy: workspace must be 16-byte aligned");
+    const double es = d->dtype == MC_F32 ? 4.0 : 2.0;
+    mc::prof::Scope sc(mc::prof::kRowOps, stream, 0.0, es * (double)d->rows * d->vocab + 4.0 * d->rows);
+    return hip_status(mc::launch_cross_entropy_fwd(*d, logits, targets, loss, stats, static_cast<float*>(workspace),
+                                                   stream),
+                      "cross_entropy forward");
+}
+
+mc_status mc_cross_entropy_bwd(const mc_xent_desc* d, const void* logits, const uint32_t* targets,
+                               const float* stats, const float* dloss, void* dlogits, hipStream_t stream) {
+    mc_status s = check_xent(d);
+    if (s != MC_OK) return s;
+    MC_CHECK(logits && targets && stats && dloss && dlogits, MC_ERR_NULL,
+             "cross_entropy backward: logits, targets, stats, dloss and dlogits must not be NULL");
+    const double es = d->dtype == MC_F32 ? 4.0 : 2.0;
+    mc::prof::Scope sc(mc::prof::kRowOps, stream, 0.0, es * 2.0 * (double)d->rows * d->vocab + 4.0 * d->rows);
+    return hip_status(mc::launch_cross_entropy_bwd(*d, logits, targets, stats, dloss, dlogits, stream),
+                      "cross_entropy backward");
+}
+
 // Philox4x32-10 (Salmon et al., SC'11), 10 rounds of the two 32x32->64
 // multiplies 0xD2511F53 / 0xCD9E8D57 with Weyl key steps 0x9E3779B9 /
 // 0xBB67AE85.

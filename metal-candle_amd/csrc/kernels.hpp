@@ -106,4 +106,19 @@ struct AdamWBatch {
 int adamw_blocks(int64_t n);  // workgroups one tensor of n elements takes
 hipError_t launch_adamw(const AdamWBatch& batch, int blocks, hipStream_t stream);
 
+// ------------------------------------------------ LayerNorm, log-softmax, CE
+int layernorm_bwd_blocks(int64_t rows);  // dw / db partial rows in the workspace
+hipError_t launch_layernorm_fwd(int64_t rows, int64_t dim, float eps, int dtype, const void* x, const void* w,
+                                const void* b, void* y, float* mean, float* rstd, hipStream_t stream);
+hipError_t launch_layernorm_bwd(int64_t rows, int64_t dim, float eps, int dtype, const void* x, const void* w,
+                                const float* mean, const float* rstd, const void* dy, void* dx, float* dw, float* db,
+                                float* ws, hipStream_t stream);
+hipError_t launch_log_softmax_fwd(int64_t rows, int64_t dim, int dtype, const void* x, void* y, hipStream_t stream);
+hipError_t launch_log_softmax_bwd(int64_t rows, int64_t dim, int dtype, const void* y, const void* dy, void* dx,
+                                  hipStream_t stream);
+hipError_t launch_cross_entropy_fwd(const mc_xent_desc& d, const void* logits, const uint32_t* targets, float* loss,
+                                    float* stats, float* ws, hipStream_t stream);
+hipError_t launch_cross_entropy_bwd(const mc_xent_desc& d, const void* logits, const uint32_t* targets,
+                                    const float* stats, const float* dloss, void* dlogits, hipStream_t stream);
+
 }  // namespace mc

@@ -9,7 +9,7 @@
 namespace mc {
 namespace prof {
 
-enum Kind { kGemm = 0, kLowRank = 1, kRmsNorm = 2, kSoftmax = 3, kAttention = 4, kAdamW = 5, kNumKinds = 6 };
+enum Kind { kGemm = 0, kLowRank = 1, kRmsNorm = 2, kSoftmax = 3, kAttention = 4, kAdamW = 5, kRowOps = 6, kNumKinds = 7 };
 
 bool enabled();
 void set_enabled(bool on);

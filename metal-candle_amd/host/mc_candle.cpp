@@ -46,7 +46,7 @@ CandleError hip_error(const char* what, hipError_t e) {
     return bail(s.str());
 }
 
-size_t dtype_size(DType d) { return d == DType::F32 ? 4 : d == DType::BF16 ? 2 : 1; }
+size_t dtype_size(DType d) { return d == DType::F32 || d == DType::U32 ? 4 : d == DType::BF16 ? 2 : 1; }
 
 int32_t mc_dtype_of(DType d) { return d == DType::BF16 ? MC_BF16 : MC_F32; }
 
@@ -160,6 +160,9 @@ Result<Tensor, CandleError> Tensor::from_slice(const std::vector<float>& data, s
         } else if (dtype == DType::BF16) {
             const uint16_t h = f32_to_bf16(data[i]);
             memcpy(&host[i * 2], &h, 2);
+        } else if (dtype == DType::U32) {
+            const uint32_t u = (uint32_t)data[i];
+            memcpy(&host[i * 4], &u, 4);
         } else {
             host[i] = (uint8_t)data[i];
         }
@@ -187,6 +190,23 @@ Result<Tensor, CandleError> Tensor::from_bytes(const std::vector<uint8_t>& data,
         memcpy(t.data(), data.data(), data.size());
     } else {
         hipError_t e = hipMemcpy(t.data(), data.data(), data.size(), hipMemcpyHostToDevice);
+        if (e != hipSuccess) return hip_error("hipMemcpy H2D", e);
+    }
+    return r;
+}
+
+Result<Tensor, CandleError> Tensor::from_u32(const std::vector<uint32_t>& data, std::vector<int64_t> dims,
+                                             const Device& device) {
+    if ((int64_t)data.size() != product(dims, 0, dims.size()))
+        return bail("shape mismatch in from_u32 for shape " + dims_to_string(dims));
+    auto r = empty(std::move(dims), DType::U32, device);
+    if (r.is_err() || data.empty()) return r;
+    Tensor& t = r.value();
+    const size_t bytes = data.size() * 4;
+    if (device.is_cpu()) {
+        memcpy(t.data(), data.data(), bytes);
+    } else {
+        hipError_t e = hipMemcpy(t.data(), data.data(), bytes, hipMemcpyHostToDevice);
         if (e != hipSuccess) return hip_error("hipMemcpy H2D", e);
     }
     return r;
@@ -225,6 +245,10 @@ Result<std::vector<float>, CandleError> Tensor::to_vec_f32() const {
             uint16_t h;
             memcpy(&h, &host[i * 2], 2);
             out[i] = bf16_to_f32(h);
+        } else if (dtype_ == DType::U32) {
+            uint32_t u;
+            memcpy(&u, &host[i * 4], 4);
+            out[i] = (float)u;
         } else {
             out[i] = (float)host[i];
         }
@@ -543,6 +567,200 @@ Result<void, Error> LoRAConfig::validate() const {
     if (!(dropout >= 0.f && dropout < 1.f))
         return Error::from(TrainingError::invalid_config("LoRA dropout must be in [0, 1)"));
     return {};
+}
+
+// ------------------------------------------------------------------ LayerNorm
+Result<Tensor, CandleError> LayerNormOp::apply(const Tensor& input) const {
+    return input.device().is_hip() ? hip_fwd(input) : cpu_fwd(input);
+}
+
+Result<Tensor, CandleError> LayerNormOp::cpu_fwd(const Tensor&) const {
+    return bail("LayerNorm: the CPU path stays with candle; this op runs on HIP tensors");
+}
+
+Result<Tensor, CandleError> LayerNormOp::hip_fwd(const Tensor& input) const {
+    // custom_ops.rs (metal_fwd): "LayerNorm expects 2D tensors, got shape {:?}"
+    if (input.rank() != 2) return bail("LayerNorm expects 2D tensors, got shape " + dims_to_string(input.dims()));
+    auto r = forward_affine(input, nullptr, nullptr);
+    if (r.is_err()) return r.error();
+    return std::move(r.value().first);
+}
+
+Result<std::pair<Tensor, LayerNormOp::Saved>, CandleError> LayerNormOp::forward_affine(const Tensor& input,
+                                                                                     const Tensor* weight,
+                                                                                     const Tensor* bias) const {
+    if (!input.device().is_hip()) return cpu_fwd(input).error();
+    if (input.rank() == 0) return bail("LayerNorm: input must have at least 1 dimension");
+    if (input.dtype() != DType::F32 && input.dtype() != DType::BF16) return bail("layer-norm: input must be F32 or BF16");
+    const int64_t dim = input.dims().back();
+    const int64_t rows = dim ? input.elem_count() / dim : 0;
+    for (const Tensor* p : {weight, bias})
+        if (p && (p->dims() != std::vector<int64_t>{dim} || p->dtype() != input.dtype() || !same_device(*p, input)))
+            return bail("layer-norm: weight and bias must be [" + std::to_string(dim) + "] in the input's dtype");
+    auto y = Tensor::empty(input.dims(), input.dtype(), input.device());
+    auto m = Tensor::empty({rows}, DType::F32, input.device());
+    auto r = Tensor::empty({rows}, DType::F32, input.device());
+    if (y.is_err()) return y.error();
+    if (m.is_err()) return m.error();
+    if (r.is_err()) return r.error();
+    const mc_status st = mc_layernorm_fwd(rows, dim, (float)eps_, mc_dtype_of(input.dtype()), input.data(),
+                                          weight ? weight->data() : nullptr, bias ? bias->data() : nullptr,
+                                          y.value().data(), static_cast<float*>(m.value().data()),
+                                          static_cast<float*>(r.value().data()), nullptr);
+    if (st != MC_OK) return mc_error("layer-norm", st);
+    return std::make_pair(std::move(y.value()), Saved{std::move(m.value()), std::move(r.value())});
+}
+
+Result<LayerNormOp::Grads, CandleError> LayerNormOp::backward(const Tensor& input, const Tensor* weight,
+                                                              const Saved& saved, const Tensor& grad_output) const {
+    if (!input.device().is_hip()) return cpu_fwd(input).error();
+    const int64_t dim = input.dims().empty() ? 0 : input.dims().back();
+    const int64_t rows = dim ? input.elem_count() / dim : 0;
+    if (grad_output.dims() != input.dims() || grad_output.dtype() != input.dtype())
+        return bail("layer-norm backward: grad_output must match the input");
+    Grads g;
+    auto dx = Tensor::empty(input.dims(), input.dtype(), input.device());
+    auto dw = Tensor::empty({dim}, DType::F32, input.device());
+    auto db = Tensor::empty({dim}, DType::F32, input.device());
+    if (dx.is_err()) return dx.error();
+    if (dw.is_err()) return dw.error();
+    if (db.is_err()) return db.error();
+    Workspace ws;
+    const size_t need = mc_layernorm_bwd_workspace_size(rows, dim);
+    if (auto e = alloc_ws(ws, need); e.is_err()) return e.error();
+    const mc_status st = mc_layernorm_bwd(rows, dim, (float)eps_, mc_dtype_of(input.dtype()), input.data(),
+                                          weight ? weight->data() : nullptr,
+                                          static_cast<const float*>(saved.mean.data()),
+                                          static_cast<const float*>(saved.rstd.data()), grad_output.data(),
+                                          dx.value().data(), static_cast<float*>(dw.value().data()),
+                                          static_cast<float*>(db.value().data()), ws.p, need, nullptr);
+    if (st != MC_OK) return mc_error("layer-norm backward", st);
+    g.dx = std::move(dx.value());
+    g.dw = std::move(dw.value());
+    g.db = std::move(db.value());
+    return g;
+}
+
+Result<Tensor, CandleError> layer_norm(const Tensor& input, double eps) {
+    auto r = LayerNormOp::create(eps).forward_affine(input, nullptr, nullptr);
+    if (r.is_err()) return r.error();
+    return std::move(r.value().first);
+}
+
+// ---------------------------------------------------------------- cross entropy
+namespace {
+
+struct XentPrep {
+    mc_xent_desc desc{};
+    Tensor stats;
+};
+
+// loss.rs:66-95: the shape checks, with the reference's messages.
+Result<XentPrep, Error> xent_prepare(const Tensor& logits, const Tensor& targets,
+                                     std::optional<uint32_t> ignore_index, float smoothing) {
+    const auto& ls = logits.dims();
+    const auto& ts = targets.dims();
+    if (ls.size() != 3)
+        return Error::from(TrainingError::invalid_config("logits must be 3D (batch, seq_len, vocab_size), got shape " +
+                                                         dims_to_string(ls)));
+    if (ts.size() != 2)
+        return Error::from(TrainingError::invalid_config("targets must be 2D (batch, seq_len), got shape " +
+                                                         dims_to_string(ts)));
+    if (ls[0] != ts[0] || ls[1] != ts[1])
+        return Error::from(TrainingError::invalid_config("logits and targets batch/seq_len mismatch: logits " +
+                                                         dims_to_string({ls[0], ls[1]}) + " vs targets " +
+                                                         dims_to_string(ts)));
+    if (!logits.device().is_hip() || !targets.device().is_hip())
+        return Error::from(bail("cross_entropy_loss runs on HIP tensors"));
+    if (logits.dtype() != DType::F32 && logits.dtype() != DType::BF16)
+        return Error::from(bail("cross_entropy_loss: logits must be F32 or BF16"));
+    if (targets.dtype() != DType::U32) return Error::from(bail("cross_entropy_loss: targets must be U32"));
+    XentPrep p;
+    p.desc = {ls[0] * ls[1], ls[2], ignore_index ? (int64_t)*ignore_index : -1, smoothing,
+              mc_dtype_of(logits.dtype())};
+    // gather_last_dim (loss.rs:160-185) fails on a target past the vocabulary
+    auto tv = targets.to_vec_f32();
+    if (tv.is_err()) return Error::from(tv.error());
+    for (float t : tv.value())
+        if ((int64_t)t >= ls[2])
+            return Error::from(bail("index out of range: target " + std::to_string((int64_t)t) + " for vocab size " +
+                                    std::to_string(ls[2])));
+    return p;
+}
+
+Result<Tensor, Error> xent_forward(const Tensor& logits, const Tensor& targets, std::optional<uint32_t> ignore_index,
+                                   float smoothing) {
+    auto p = xent_prepare(logits, targets, ignore_index, smoothing);
+    if (p.is_err()) return p.error();
+    const mc_xent_desc& d = p.value().desc;
+    auto loss = Tensor::empty({}, DType::F32, logits.device());
+    auto stats = Tensor::empty({d.rows + 1}, DType::F32, logits.device());
+    if (loss.is_err()) return Error::from(loss.error());
+    if (stats.is_err()) return Error::from(stats.error());
+    Workspace ws;
+    const size_t need = mc_cross_entropy_workspace_size(&d);
+    if (auto e = alloc_ws(ws, need); e.is_err()) return Error::from(e.error());
+    const mc_status st = mc_cross_entropy_fwd(&d, logits.data(), static_cast<const uint32_t*>(targets.data()),
+                                              static_cast<float*>(loss.value().data()),
+                                              static_cast<float*>(stats.value().data()), ws.p, need, nullptr);
+    if (st != MC_OK) return Error::from(mc_error("cross_entropy_loss", st));
+    if (ignore_index) {  // loss.rs:123-131: the count, read back
+        float cnt = 0.f;
+        hipError_t e = hipMemcpy(&cnt, static_cast<float*>(stats.value().data()) + d.rows, 4, hipMemcpyDeviceToHost);
+        if (e != hipSuccess) return Error::from(hip_error("hipMemcpy D2H", e));
+        if (cnt == 0.f)
+            return Error::from(TrainingError::invalid_config("all tokens are ignored, cannot compute loss"));
+    }
+    return std::move(loss.value());
+}
+
+}  // namespace
+
+Result<Tensor, Error> cross_entropy_loss(const Tensor& logits, const Tensor& targets,
+                                         std::optional<uint32_t> ignore_index) {
+    return xent_forward(logits, targets, ignore_index, 0.f);
+}
+
+Result<Tensor, Error> cross_entropy_loss_with_smoothing(const Tensor& logits, const Tensor& targets, float smoothing,
+                                                        std::optional<uint32_t> ignore_index) {
+    if (!(smoothing >= 0.f && smoothing < 1.f)) {  // loss.rs:214-219
+        std::ostringstream m;
+        m << "smoothing must be in [0, 1), got " << smoothing;
+        return Error::from(TrainingError::invalid_config(m.str()));
+    }
+    return xent_forward(logits, targets, ignore_index, smoothing);
+}
+
+Result<Tensor, Error> cross_entropy_loss_backward(const Tensor& logits, const Tensor& targets, float smoothing,
+                                                  std::optional<uint32_t> ignore_index, float dloss) {
+    if (!(smoothing >= 0.f && smoothing < 1.f)) {
+        std::ostringstream m;
+        m << "smoothing must be in [0, 1), got " << smoothing;
+        return Error::from(TrainingError::invalid_config(m.str()));
+    }
+    auto p = xent_prepare(logits, targets, ignore_index, smoothing);
+    if (p.is_err()) return p.error();
+    const mc_xent_desc& d = p.value().desc;
+    auto loss = Tensor::empty({}, DType::F32, logits.device());
+    auto stats = Tensor::empty({d.rows + 1}, DType::F32, logits.device());
+    auto g = Tensor::from_slice({dloss}, {1}, logits.device());
+    auto dl = Tensor::empty(logits.dims(), logits.dtype(), logits.device());
+    if (loss.is_err()) return Error::from(loss.error());
+    if (stats.is_err()) return Error::from(stats.error());
+    if (g.is_err()) return Error::from(g.error());
+    if (dl.is_err()) return Error::from(dl.error());
+    Workspace ws;
+    const size_t need = mc_cross_entropy_workspace_size(&d);
+    if (auto e = alloc_ws(ws, need); e.is_err()) return Error::from(e.error());
+    mc_status st = mc_cross_entropy_fwd(&d, logits.data(), static_cast<const uint32_t*>(targets.data()),
+                                        static_cast<float*>(loss.value().data()),
+                                        static_cast<float*>(stats.value().data()), ws.p, need, nullptr);
+    if (st == MC_OK)
+        st = mc_cross_entropy_bwd(&d, logits.data(), static_cast<const uint32_t*>(targets.data()),
+                                  static_cast<const float*>(stats.value().data()),
+                                  static_cast<const float*>(g.value().data()), dl.value().data(), nullptr);
+    if (st != MC_OK) return Error::from(mc_error("cross_entropy_loss backward", st));
+    return std::move(dl.value());
 }
 
 // ------------------------------------------------------------------ AdamW

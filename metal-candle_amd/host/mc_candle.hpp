@@ -101,7 +101,7 @@ private:
 };
 
 // ------------------------------------------------------------------ tensors
-enum class DType { F32, BF16, U8 };
+enum class DType { F32, BF16, U8, U32 };
 
 struct Device {
     enum class Kind { Cpu, Hip };
@@ -126,6 +126,9 @@ public:
                                                   const Device& device, DType dtype = DType::F32);
     static Result<Tensor, CandleError> from_bytes(const std::vector<uint8_t>& data, std::vector<int64_t> dims,
                                                   const Device& device);
+    // U32 tensor (token ids), as Tensor::new(&[u32]) in candle.
+    static Result<Tensor, CandleError> from_u32(const std::vector<uint32_t>& data, std::vector<int64_t> dims,
+                                                const Device& device);
     static Result<Tensor, CandleError> zeros(std::vector<int64_t> dims, DType dtype, const Device& device);
     // Uninitialised storage (for outputs).
     static Result<Tensor, CandleError> empty(std::vector<int64_t> dims, DType dtype, const Device& device);
@@ -228,6 +231,51 @@ public:
     Result<Tensor, CandleError> forward_causal(const Tensor& input, bool causal) const;
     Result<Tensor, CandleError> backward(const Tensor& probs, const Tensor& grad_output, bool causal) const;
 };
+
+// LayerNormOp (custom_ops.rs:826-1079): y = (x - mean) / sqrt(var + eps) over
+// the last dim of a 2-D input, as the reference's op requires.
+class LayerNormOp {
+public:
+    static LayerNormOp create(double eps) { return LayerNormOp(eps); }  // LayerNormOp::new
+    const char* name() const { return "layer-norm"; }
+    Result<Tensor, CandleError> apply(const Tensor& input) const;
+    Result<Tensor, CandleError> cpu_fwd(const Tensor& input) const;
+    Result<Tensor, CandleError> hip_fwd(const Tensor& input) const;
+    // Extensions: the weight and bias of MetalLayerNorm (src/embeddings/
+    // metal_bert.rs:30-72), any rank (leading dims folded), the saved
+    // statistics and the backward.
+    struct Saved {
+        Tensor mean, rstd;  // fp32 [rows]
+    };
+    struct Grads {
+        Tensor dx, dw, db;  // dw, db fp32 [dim] (undefined without weight / bias)
+    };
+    Result<std::pair<Tensor, Saved>, CandleError> forward_affine(const Tensor& input, const Tensor* weight,
+                                                                 const Tensor* bias) const;
+    Result<Grads, CandleError> backward(const Tensor& input, const Tensor* weight, const Saved& saved,
+                                        const Tensor& grad_output) const;
+    double eps() const { return eps_; }
+
+private:
+    explicit LayerNormOp(double eps) : eps_(eps) {}
+    double eps_;
+};
+
+// TensorExt::layer_norm (tensor.rs:100-109): any rank, last dim, no affine.
+Result<Tensor, CandleError> layer_norm(const Tensor& input, double eps);
+
+// cross_entropy_loss (loss.rs:58-148) and cross_entropy_loss_with_smoothing
+// (loss.rs:208-245) over HIP tensors: logits [batch, seq, vocab] (F32 or
+// BF16), targets [batch, seq] U32; the scalar loss as a fp32 tensor of shape
+// []. The reference's validation messages and its "all tokens are ignored"
+// error (the count is read back, as the reference's to_scalar does).
+Result<Tensor, Error> cross_entropy_loss(const Tensor& logits, const Tensor& targets,
+                                         std::optional<uint32_t> ignore_index);
+Result<Tensor, Error> cross_entropy_loss_with_smoothing(const Tensor& logits, const Tensor& targets, float smoothing,
+                                                        std::optional<uint32_t> ignore_index);
+// Extension: d loss / d logits for a loss gradient dloss (the reference has no backward).
+Result<Tensor, Error> cross_entropy_loss_backward(const Tensor& logits, const Tensor& targets, float smoothing,
+                                                  std::optional<uint32_t> ignore_index, float dloss = 1.0f);
 
 // CustomMetalOps (metal_ops.rs:33-171), as free functions over HIP tensors.
 Result<Tensor, TrainingError> lora_forward_fused(const Tensor& input, const Tensor& lora_a, const Tensor& lora_b,

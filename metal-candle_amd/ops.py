@@ -12,7 +12,7 @@ import ctypes
 import torch
 
 from . import _lib
-from ._lib import AdamWConfig, AdamWTensor, AttnDesc, LoraDesc, McError, check, lib
+from ._lib import AdamWConfig, AdamWTensor, AttnDesc, LoraDesc, McError, XentDesc, check, lib
 
 _DTYPES = {torch.float32: _lib.MC_F32, torch.bfloat16: _lib.MC_BF16}
 
@@ -159,6 +159,77 @@ def attention_backward(q, k, v, o, lse, dout, causal=False, scale=None, mask=Non
     check(lib().mc_attention_bwd(ctypes.byref(d), _ptr(q), _ptr(k), _ptr(v), _ptr(mask), _ptr(o), _ptr(lse),
                                  _ptr(dout), _ptr(dq), _ptr(dk), _ptr(dv), _ptr(ws), ws_n, _stream(q)))
     return dq, dk, dv
+
+
+def layer_norm_forward(x, eps, w=None, b=None, save_stats=True):
+    """LayerNorm over the last dim: (y, mean, rstd)."""
+    D = x.shape[-1]
+    rows = x.numel() // D
+    y = torch.empty_like(x)
+    mean = torch.empty(rows, dtype=torch.float32, device=x.device) if save_stats else None
+    rstd = torch.empty(rows, dtype=torch.float32, device=x.device) if save_stats else None
+    check(lib().mc_layernorm_fwd(rows, D, float(eps), _dtype_code(x), _ptr(x), _ptr(w), _ptr(b), _ptr(y), _ptr(mean),
+                                 _ptr(rstd), _stream(x)))
+    return y, mean, rstd
+
+
+def layer_norm_backward(x, dy, eps, w=None, mean=None, rstd=None, need_dw=True, need_db=True):
+    """(dx, dw, db) of LayerNorm; dw / db are fp32 [D] (None when not requested)."""
+    D = x.shape[-1]
+    rows = x.numel() // D
+    dx = torch.empty_like(x)
+    dw = torch.empty(D, dtype=torch.float32, device=x.device) if need_dw else None
+    db = torch.empty(D, dtype=torch.float32, device=x.device) if need_db else None
+    ws_n = lib().mc_layernorm_bwd_workspace_size(rows, D) if (need_dw or need_db) else 0
+    ws = _workspace(ws_n, x.device)
+    check(lib().mc_layernorm_bwd(rows, D, float(eps), _dtype_code(x), _ptr(x), _ptr(w), _ptr(mean), _ptr(rstd),
+                                 _ptr(dy), _ptr(dx), _ptr(dw), _ptr(db), _ptr(ws), ws_n, _stream(x)))
+    return dx, dw, db
+
+
+def log_softmax_forward(x):
+    D = x.shape[-1]
+    y = torch.empty_like(x)
+    check(lib().mc_log_softmax_fwd(x.numel() // D, D, _dtype_code(x), _ptr(x), _ptr(y), _stream(x)))
+    return y
+
+
+def log_softmax_backward(y, dy):
+    D = y.shape[-1]
+    dx = torch.empty_like(y)
+    check(lib().mc_log_softmax_bwd(y.numel() // D, D, _dtype_code(y), _ptr(y), _ptr(dy), _ptr(dx), _stream(y)))
+    return dx
+
+
+def _xent_desc(logits, ignore_index, smoothing):
+    V = logits.shape[-1]
+    return XentDesc(logits.numel() // V, V, -1 if ignore_index is None else int(ignore_index), float(smoothing),
+                    _dtype_code(logits))
+
+
+def cross_entropy_forward(logits, targets, ignore_index=None, smoothing=0.0):
+    """cross_entropy_loss (src/training/loss.rs:58-245) over logits [..., V] and
+    uint32 targets [...]: (loss fp32 [1], stats fp32 [rows + 1])."""
+    _contig(logits, "logits"), _contig(targets, "targets")
+    d = _xent_desc(logits, ignore_index, smoothing)
+    loss = torch.empty(1, dtype=torch.float32, device=logits.device)
+    stats = torch.empty(d.rows + 1, dtype=torch.float32, device=logits.device)
+    ws_n = lib().mc_cross_entropy_workspace_size(ctypes.byref(d))
+    ws = _workspace(ws_n, logits.device)
+    check(lib().mc_cross_entropy_fwd(ctypes.byref(d), _ptr(logits), _ptr(targets), _ptr(loss), _ptr(stats), _ptr(ws),
+                                     ws_n, _stream(logits)))
+    return loss, stats
+
+
+def cross_entropy_backward(logits, targets, stats, dloss=None, ignore_index=None, smoothing=0.0):
+    """d loss / d logits (times dloss, a fp32 [1] device tensor; default 1)."""
+    d = _xent_desc(logits, ignore_index, smoothing)
+    if dloss is None:
+        dloss = torch.ones(1, dtype=torch.float32, device=logits.device)
+    dlogits = torch.empty_like(logits)
+    check(lib().mc_cross_entropy_bwd(ctypes.byref(d), _ptr(logits), _ptr(targets), _ptr(stats), _ptr(dloss),
+                                     _ptr(dlogits), _stream(logits)))
+    return dlogits
 
 
 def adamw_step(params, grads, ms, vs, steps, lr=1e-4, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=0.01,

@@ -49,6 +49,17 @@ def lib():
         _i32 = ctypes.c_int32
         L.oracle_attention_fwd.argtypes = [_i64, _i32, _i32, _i64, _i32, ctypes.c_float, ctypes.c_int,
                                            _f32p, _f32p, _f32p, _f32p, _f32p, _f32p, ctypes.c_int]
+        L.oracle_layernorm_fwd.argtypes = [_i64, _i64, ctypes.c_float, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p,
+                                           ctypes.c_int]
+        L.oracle_layernorm_bwd.argtypes = [_i64, _i64, ctypes.c_float, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p,
+                                           ctypes.c_int]
+        L.oracle_log_softmax_fwd.argtypes = [_i64, _i64, _f32p, _f32p, ctypes.c_int]
+        L.oracle_log_softmax_bwd.argtypes = [_i64, _i64, _f32p, _f32p, _f32p, ctypes.c_int]
+        L.oracle_cross_entropy_fwd.argtypes = [_i64, _i64, _f32p, _u32p, _i64, ctypes.c_float, _f32p,
+                                               ctypes.POINTER(ctypes.c_double)]
+        L.oracle_cross_entropy_fwd.restype = ctypes.c_double
+        L.oracle_cross_entropy_bwd.argtypes = [_i64, _i64, _f32p, _u32p, _i64, ctypes.c_float, ctypes.c_float,
+                                               _f32p]
         L.oracle_adamw_step.argtypes = [_i64, ctypes.c_float, ctypes.c_float, ctypes.c_float, ctypes.c_float,
                                         ctypes.c_float, _i64, _f32p, _f32p, _f32p, _f32p, _f32p]
         L.oracle_attention_bwd.argtypes = [_i64, _i32, _i32, _i64, _i32, ctypes.c_float, ctypes.c_int,
@@ -210,3 +221,67 @@ def adamw_step(param, grad, m, v, step, lr=1e-4, beta1=0.9, beta2=0.999, eps=1e-
     out = np.empty_like(p)
     lib().oracle_adamw_step(p.size, lr, beta1, beta2, eps, weight_decay, step, _f(p), _f(g), _f(m), _f(v), _f(out))
     return out, m, v
+
+
+def layernorm_fwd(x, eps, w=None, b=None, threads=0):
+    """(y, mean, rstd) of LayerNorm over the last dim."""
+    x, w, b = _c32(x), _c32(w), _c32(b)
+    D = x.shape[-1]
+    rows = x.size // D
+    y = np.empty_like(x)
+    mean = np.empty(rows, np.float32)
+    rstd = np.empty(rows, np.float32)
+    lib().oracle_layernorm_fwd(rows, D, eps, _f(x), _f(w), _f(b), _f(y), _f(mean), _f(rstd), threads)
+    return y, mean, rstd
+
+
+def layernorm_bwd(x, dy, eps, w=None, threads=0):
+    """(dx, dw, db) of LayerNorm."""
+    x, w, dy = _c32(x), _c32(w), _c32(dy)
+    D = x.shape[-1]
+    rows = x.size // D
+    dx = np.empty_like(x)
+    dw = np.empty(D, np.float32)
+    db = np.empty(D, np.float32)
+    lib().oracle_layernorm_bwd(rows, D, eps, _f(x), _f(w), _f(dy), _f(dx), _f(dw), _f(db), threads)
+    return dx, dw, db
+
+
+def log_softmax_fwd(x, threads=0):
+    x = _c32(x)
+    D = x.shape[-1]
+    y = np.empty_like(x)
+    lib().oracle_log_softmax_fwd(x.size // D, D, _f(x), _f(y), threads)
+    return y
+
+
+def log_softmax_bwd(y, dy, threads=0):
+    y, dy = _c32(y), _c32(dy)
+    D = y.shape[-1]
+    dx = np.empty_like(y)
+    lib().oracle_log_softmax_bwd(y.size // D, D, _f(y), _f(dy), _f(dx), threads)
+    return dx
+
+
+def cross_entropy_fwd(logits, targets, ignore_index=-1, smoothing=0.0):
+    """(loss, lse [rows], count) for logits [rows, V] and uint32 targets [rows]."""
+    x = _c32(logits)
+    V = x.shape[-1]
+    rows = x.size // V
+    t = np.ascontiguousarray(targets, dtype=np.uint32).reshape(-1)
+    assert t.size == rows
+    lse = np.empty(rows, np.float32)
+    cnt = ctypes.c_double()
+    loss = lib().oracle_cross_entropy_fwd(rows, V, _f(x), t.ctypes.data_as(_u32p), ignore_index, smoothing, _f(lse),
+                                          ctypes.byref(cnt))
+    return loss, lse, cnt.value
+
+
+def cross_entropy_bwd(logits, targets, ignore_index=-1, smoothing=0.0, dloss=1.0):
+    x = _c32(logits)
+    V = x.shape[-1]
+    rows = x.size // V
+    t = np.ascontiguousarray(targets, dtype=np.uint32).reshape(-1)
+    d = np.empty_like(x)
+    lib().oracle_cross_entropy_bwd(rows, V, _f(x), t.ctypes.data_as(_u32p), ignore_index, smoothing, dloss, _f(d))
+    return d

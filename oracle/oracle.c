@@ -498,6 +498,167 @@ void oracle_adamw_step(int64_t n, float lr, float beta1, float beta2, float eps,
     }
 }
 
+/* ------------------------------------------------------------- LayerNorm */
+/* LayerNormOp::cpu_fwd (src/backend/custom_ops.rs, the two-pass loop: mean,
+ * then the centred variance, then (x - mean) * 1/sqrt(var + eps)), with the
+ * weight and bias of MetalLayerNorm::forward (src/embeddings/metal_bert.rs:
+ * 30-72). fp64 accumulation. mean / rstd [rows] may be NULL. */
+void oracle_layernorm_fwd(int64_t rows, int64_t D, float eps, const float* x, const float* w, const float* b,
+                          float* y, float* mean, float* rstd, int threads) {
+#pragma omp parallel for schedule(static) num_threads(nthreads(threads))
+    for (int64_t i = 0; i < rows; ++i) {
+        const float* xr = x + i * D;
+        double m = 0.0;
+        for (int64_t j = 0; j < D; ++j) m += xr[j];
+        m /= (double)D;
+        double v = 0.0;
+        for (int64_t j = 0; j < D; ++j) v += ((double)xr[j] - m) * ((double)xr[j] - m);
+        v /= (double)D;
+        const double r = 1.0 / sqrt(v + (double)eps);
+        for (int64_t j = 0; j < D; ++j) {
+            double t = ((double)xr[j] - m) * r;
+            if (w) t *= (double)w[j];
+            if (b) t += (double)b[j];
+            y[i * D + j] = (float)t;
+        }
+        if (mean) mean[i] = (float)m;
+        if (rstd) rstd[i] = (float)r;
+    }
+}
+
+/* Gradients of the forward above (no reference kernel): xh = (x - mean) r,
+ * g = dy w: dx = r (g - mean(g) - xh mean(g xh)); dw = sum_rows dy xh,
+ * db = sum_rows dy (dw, db may be NULL). */
+void oracle_layernorm_bwd(int64_t rows, int64_t D, float eps, const float* x, const float* w, const float* dy,
+                          float* dx, float* dw, float* db, int threads) {
+    double* gw = (double*)calloc((size_t)D, sizeof(double));
+    double* gb = (double*)calloc((size_t)D, sizeof(double));
+    for (int64_t i = 0; i < rows; ++i) {
+        const float* xr = x + i * D;
+        const float* gr = dy + i * D;
+        double m = 0.0, v = 0.0;
+        for (int64_t j = 0; j < D; ++j) m += xr[j];
+        m /= (double)D;
+        for (int64_t j = 0; j < D; ++j) v += ((double)xr[j] - m) * ((double)xr[j] - m);
+        const double r = 1.0 / sqrt(v / (double)D + (double)eps);
+        double mg = 0.0, mgx = 0.0;
+        for (int64_t j = 0; j < D; ++j) {
+            const double g = (double)gr[j] * (w ? (double)w[j] : 1.0);
+            mg += g;
+            mgx += g * ((double)xr[j] - m) * r;
+        }
+        mg /= (double)D;
+        mgx /= (double)D;
+        for (int64_t j = 0; j < D; ++j) {
+            const double xh = ((double)xr[j] - m) * r;
+            const double g = (double)gr[j] * (w ? (double)w[j] : 1.0);
+            dx[i * D + j] = (float)(r * (g - mg - xh * mgx));
+            gw[j] += (double)gr[j] * xh;
+            gb[j] += (double)gr[j];
+        }
+    }
+    for (int64_t j = 0; j < D; ++j) {
+        if (dw) dw[j] = (float)gw[j];
+        if (db) db[j] = (float)gb[j];
+    }
+    free(gw);
+    free(gb);
+    (void)threads;
+}
+
+/* ----------------------------------------------- log-softmax, cross entropy */
+/* candle_nn::ops::log_softmax as cross_entropy_loss uses it
+ * (src/training/loss.rs:108; candle-nn 0.9, not vendored): max_keepdim,
+ * broadcast_sub, exp, sum_keepdim, log, broadcast_sub. Returns the row's
+ * log-sum-exp. */
+static double log_softmax_row(int64_t D, const float* x, double* out) {
+    double m = -INFINITY;
+    for (int64_t j = 0; j < D; ++j)
+        if ((double)x[j] > m) m = x[j];
+    double sum = 0.0;
+    for (int64_t j = 0; j < D; ++j) sum += exp((double)x[j] - m);
+    const double ls = log(sum);
+    if (out)
+        for (int64_t j = 0; j < D; ++j) out[j] = ((double)x[j] - m) - ls;
+    return m + ls;
+}
+
+void oracle_log_softmax_fwd(int64_t rows, int64_t D, const float* x, float* y, int threads) {
+#pragma omp parallel num_threads(nthreads(threads))
+    {
+        double* t = (double*)malloc(sizeof(double) * (size_t)D);
+#pragma omp for schedule(static)
+        for (int64_t i = 0; i < rows; ++i) {
+            log_softmax_row(D, x + i * D, t);
+            for (int64_t j = 0; j < D; ++j) y[i * D + j] = (float)t[j];
+        }
+        free(t);
+    }
+}
+
+/* dx = dy - exp(y) sum(dy) */
+void oracle_log_softmax_bwd(int64_t rows, int64_t D, const float* y, const float* dy, float* dx, int threads) {
+#pragma omp parallel for schedule(static) num_threads(nthreads(threads))
+    for (int64_t i = 0; i < rows; ++i) {
+        double s = 0.0;
+        for (int64_t j = 0; j < D; ++j) s += dy[i * D + j];
+        for (int64_t j = 0; j < D; ++j)
+            dx[i * D + j] = (float)((double)dy[i * D + j] - exp((double)y[i * D + j]) * s);
+    }
+}
+
+/* cross_entropy_loss (loss.rs:58-148): log-softmax of each row, gather of
+ * the target's log-probability, mask of targets != ignore_index (ignore < 0:
+ * none), sum / count, negated; with smoothing s (loss.rs:208-245):
+ * (1 - s) * that + s * (-mean of every log-probability of every row).
+ * Returns NaN where the reference returns an error (count 0, target out of
+ * range). lse [rows] may be NULL; *count receives the count. */
+double oracle_cross_entropy_fwd(int64_t rows, int64_t V, const float* logits, const uint32_t* targets,
+                                int64_t ignore_index, float smoothing, float* lse, double* count) {
+    double nll = 0.0, all = 0.0, cnt = 0.0;
+    int bad = 0;
+    for (int64_t i = 0; i < rows; ++i) {
+        const float* xr = logits + i * V;
+        const double l = log_softmax_row(V, xr, NULL);
+        if (lse) lse[i] = (float)l;
+        double rs = 0.0;
+        for (int64_t j = 0; j < V; ++j) rs += (double)xr[j] - l;
+        all += rs;
+        const int ignored = ignore_index >= 0 && (int64_t)targets[i] == ignore_index;
+        if (ignored) continue;
+        if ((int64_t)targets[i] >= V) {
+            bad = 1;
+            continue;
+        }
+        nll += l - (double)xr[targets[i]];
+        cnt += 1.0;
+    }
+    if (count) *count = cnt;
+    if (bad || cnt == 0.0) return NAN;
+    double loss = nll / cnt;
+    if (smoothing != 0.0f) loss = (1.0 - smoothing) * loss + smoothing * (-all / ((double)rows * (double)V));
+    return loss;
+}
+
+/* d loss / d logits, times dloss: (1 - s) [counted] (p - onehot) / count + s (p - 1/V) / rows. */
+void oracle_cross_entropy_bwd(int64_t rows, int64_t V, const float* logits, const uint32_t* targets,
+                              int64_t ignore_index, float smoothing, float dloss, float* dlogits) {
+    double cnt = 0.0;
+    for (int64_t i = 0; i < rows; ++i)
+        if (!(ignore_index >= 0 && (int64_t)targets[i] == ignore_index)) cnt += 1.0;
+    for (int64_t i = 0; i < rows; ++i) {
+        const float* xr = logits + i * V;
+        const double l = log_softmax_row(V, xr, NULL);
+        const int valid = !(ignore_index >= 0 && (int64_t)targets[i] == ignore_index);
+        for (int64_t j = 0; j < V; ++j) {
+            const double p = exp((double)xr[j] - l);
+            double g = smoothing * (p - 1.0 / (double)V) / (double)rows;
+            if (valid) g += (1.0 - smoothing) * (p - (j == (int64_t)targets[i] ? 1.0 : 0.0)) / cnt;
+            dlogits[i * V + j] = (float)(dloss * g);
+        }
+    }
+}
+
 /* ------------------------------------------------------------------ bf16 */
 void oracle_round_bf16(const float* in, float* out, int64_t n) {
     for (int64_t i = 0; i < n; ++i) {

@@ -17,6 +17,10 @@
  *   softmax      src/backend/tensor.rs:91-98    (max, sub, exp, sum, divide)
  *                src/models/transformer.rs:264-275 (causal -inf mask added first)
  *   AdamW        src/training/optimizer.rs:227-281 (fp32 op order of the step)
+ *   LayerNorm    src/backend/custom_ops.rs LayerNormOp::cpu_fwd, tensor.rs:100-109,
+ *                src/embeddings/metal_bert.rs:30-72 (weight, bias)
+ *   log-softmax  candle_nn::ops::log_softmax (src/training/loss.rs:108)
+ *   cross entropy src/training/loss.rs:58-245 (ignore_index, label smoothing)
  *   dropout      candle_nn::ops::dropout (candle-nn 0.9, not vendored): keep iff
  *                U >= p, kept values scaled by 1/(1-p); the mask itself comes
  *                from the Philox4x32-10 generator below, shared with the GPU path.
@@ -51,6 +55,16 @@
  *                        default steps lower the sum), the constant-gradient
  *                        closed form (m_hat = g, v_hat = g^2 at every step),
  *                        torch.optim.AdamW as a library cross-check.
+ *   oracle_layernorm_*   the reference's layer_norm tests (tensor.rs:165-300:
+ *                        zero row means, zeros in -> zeros out) and a
+ *                        hand-computed row; torch.nn.functional.layer_norm and
+ *                        its autograd in fp64; finite differences.
+ *   oracle_log_softmax_* torch.log_softmax and autograd in fp64; exp rows sum
+ *                        to 1; shift invariance.
+ *   oracle_cross_entropy_* the reference's loss tests (loss.rs:247-380) with
+ *                        their closed forms; torch.nn.functional.cross_entropy
+ *                        (ignore_index, label smoothing without ignored rows)
+ *                        and its autograd; finite differences.
  *   oracle_attention_bwd central finite differences of <o, dO> in fp64 for
  *                        q, k and v, torch autograd of the fp64 composite.
  *
@@ -136,6 +150,20 @@ void oracle_attention_bwd(int64_t B, int32_t H, int32_t Hkv, int64_t S, int32_t 
  * parameter written to param_out (may equal param). */
 void oracle_adamw_step(int64_t n, float lr, float beta1, float beta2, float eps, float wd, int64_t step,
                        const float* param, const float* grad, float* m, float* v, float* param_out);
+
+/* LayerNorm [rows, D] with optional weight / bias (NULL: none). */
+void oracle_layernorm_fwd(int64_t rows, int64_t D, float eps, const float* x, const float* w, const float* b,
+                          float* y, float* mean, float* rstd, int threads);
+void oracle_layernorm_bwd(int64_t rows, int64_t D, float eps, const float* x, const float* w, const float* dy,
+                          float* dx, float* dw, float* db, int threads);
+/* log-softmax over the last dim and its backward. */
+void oracle_log_softmax_fwd(int64_t rows, int64_t D, const float* x, float* y, int threads);
+void oracle_log_softmax_bwd(int64_t rows, int64_t D, const float* y, const float* dy, float* dx, int threads);
+/* Cross-entropy loss over logits [rows, V] and targets [rows]; ignore_index < 0: none. */
+double oracle_cross_entropy_fwd(int64_t rows, int64_t V, const float* logits, const uint32_t* targets,
+                                int64_t ignore_index, float smoothing, float* lse, double* count);
+void oracle_cross_entropy_bwd(int64_t rows, int64_t V, const float* logits, const uint32_t* targets,
+                              int64_t ignore_index, float smoothing, float dloss, float* dlogits);
 
 void oracle_round_bf16(const float* in, float* out, int64_t n);
 

@@ -847,6 +847,167 @@ CASE(adamw_reset_state, true) {
     (void)b;
 }
 
+// ================================================================== LayerNorm
+// custom_ops.rs LayerNormOp: name and the 2-D requirement
+CASE(layer_norm_op_name_and_rank, false) {
+    const LayerNormOp op = LayerNormOp::create(1e-5);
+    CHECK(std::string(op.name()) == "layer-norm");
+    TRY(x, Tensor::from_slice(ones(8), {2, 4}, kCpu));
+    CHECK(op.apply(x).is_err());  // CPU tensors are not computed here
+}
+
+CASE(layer_norm_op_requires_2d, true) {
+    const LayerNormOp op = LayerNormOp::create(1e-5);
+    TRY(x, Tensor::from_slice(ones(24), {2, 3, 4}, kHip));
+    auto r = op.apply(x);
+    CHECK(r.is_err());
+    if (r.is_err()) CHECK(r.error().to_string() == "LayerNorm expects 2D tensors, got shape [2, 3, 4]");
+}
+
+// tensor.rs:165-181 test_layer_norm, 214-228 _with_different_eps, 278-300 _preserves_shape / _with_zeros
+CASE(layer_norm_reference_tests, true) {
+    TRY(x, Tensor::from_slice({1, 2, 3, 4, 5, 6, 7, 8}, {2, 4}, kHip));
+    TRY(y, layer_norm(x, 1e-5));
+    TRY(v, y.to_vec_f32());
+    for (int r = 0; r < 2; ++r) {
+        double m = 0;
+        for (int j = 0; j < 4; ++j) m += v[r * 4 + j];
+        CHECK(fabs(m / 4) < 1e-4);
+    }
+    std::vector<float> ref(8);
+    const std::vector<float> xs = {1, 2, 3, 4, 5, 6, 7, 8};
+    oracle_layernorm_fwd(2, 4, 1e-5f, xs.data(), nullptr, nullptr, ref.data(), nullptr, nullptr, 0);
+    CHECK_LE(rel_err(v, ref), kTolF32);
+    TRY(x3, Tensor::from_slice({1, 2, 3}, {1, 3}, kHip));
+    TRY(a, layer_norm(x3, 1e-5));
+    TRY(b, layer_norm(x3, 1e-3));
+    CHECK(a.dims() == b.dims());
+    TRY(xr, Tensor::from_slice(randn(105, 0, 1, 71), {3, 5, 7}, kHip));
+    TRY(yr, layer_norm(xr, 1e-5));
+    CHECK(yr.dims() == xr.dims());
+    TRY(z, Tensor::from_slice({0, 0, 0}, {1, 3}, kHip));
+    TRY(yz, layer_norm(z, 1e-5));
+    TRY(vz, yz.to_vec_f32());
+    for (float t : vz) CHECK(fabs(t) < 1e-6);
+}
+
+// MetalLayerNorm (metal_bert.rs:30-72): weight, bias, and the backward
+CASE(layer_norm_affine_forward_backward, true) {
+    const int64_t R = 12, D = 384;
+    const auto x = randn((size_t)(R * D), 0.2f, 1.5f, 72), w = randn((size_t)D, 1.f, 0.1f, 73),
+               b = randn((size_t)D, 0, 0.1f, 74), dy = randn((size_t)(R * D), 0, 1, 75);
+    TRY(tx, Tensor::from_slice(x, {R, D}, kHip));
+    TRY(tw, Tensor::from_slice(w, {D}, kHip));
+    TRY(tb, Tensor::from_slice(b, {D}, kHip));
+    TRY(tdy, Tensor::from_slice(dy, {R, D}, kHip));
+    const LayerNormOp op = LayerNormOp::create(1e-12);  // BertConfig layer_norm_eps (embeddings/bert.rs:169)
+    TRY(f, op.forward_affine(tx, &tw, &tb));
+    TRY(g, op.backward(tx, &tw, f.second, tdy));
+    std::vector<float> ry(x.size()), rdx(x.size()), rdw(D), rdb(D);
+    oracle_layernorm_fwd(R, D, 1e-12f, x.data(), w.data(), b.data(), ry.data(), nullptr, nullptr, 0);
+    oracle_layernorm_bwd(R, D, 1e-12f, x.data(), w.data(), dy.data(), rdx.data(), rdw.data(), rdb.data(), 0);
+    TRY(vy, f.first.to_vec_f32());
+    TRY(vdx, g.dx.to_vec_f32());
+    TRY(vdw, g.dw.to_vec_f32());
+    TRY(vdb, g.db.to_vec_f32());
+    CHECK_LE(rel_err(vy, ry), kTolF32);
+    CHECK_LE(rel_err(vdx, rdx), kTolF32);
+    CHECK_LE(rel_err(vdw, rdw), kTolF32);
+    CHECK_LE(rel_err(vdb, rdb), kTolF32);
+}
+
+// ================================================================== cross entropy
+static double loss_of(const Result<Tensor, Error>& r) {
+    if (r.is_err()) return NAN;
+    auto v = r.value().to_vec_f32();
+    return v.is_ok() && !v.value().empty() ? v.value()[0] : NAN;
+}
+
+// loss.rs:265-278 test_cross_entropy_loss_basic, 281-294 _wrong_prediction
+CASE(cross_entropy_basic_and_wrong_prediction, true) {
+    TRY(lg, Tensor::from_slice({10, 0, 0}, {1, 1, 3}, kHip));
+    TRY(t0, Tensor::from_u32({0}, {1, 1}, kHip));
+    TRY(t2, Tensor::from_u32({2}, {1, 1}, kHip));
+    const double a = loss_of(cross_entropy_loss(lg, t0, std::nullopt));
+    const double b = loss_of(cross_entropy_loss(lg, t2, std::nullopt));
+    CHECK(a < 0.1);
+    CHECK(b > 5.0);
+    const std::vector<float> xs = {10, 0, 0};
+    const uint32_t t[1] = {2};
+    CHECK(fabs(b - oracle_cross_entropy_fwd(1, 3, xs.data(), t, -1, 0.f, nullptr, nullptr)) < 1e-5);
+    auto sc = cross_entropy_loss(lg, t0, std::nullopt);
+    CHECK(sc.is_ok() && sc.value().dims().empty());  // a scalar
+}
+
+// loss.rs:297-316 test_cross_entropy_loss_with_ignore, and the all-ignored error (loss.rs:123-131)
+CASE(cross_entropy_with_ignore, true) {
+    TRY(lg, Tensor::from_slice({1, 2, 3, 1, 2, 3, 1, 2, 3, 1, 2, 3}, {2, 2, 3}, kHip));
+    TRY(t, Tensor::from_u32({2, 0, 2, 0}, {2, 2}, kHip));
+    auto r = cross_entropy_loss(lg, t, 0u);
+    CHECK(r.is_ok());
+    const double want = log(exp(1.0) + exp(2.0) + exp(3.0)) - 3.0;
+    CHECK(fabs(loss_of(r) - want) < 1e-5);
+    TRY(t0, Tensor::from_u32({0, 0, 0, 0}, {2, 2}, kHip));
+    auto e = cross_entropy_loss(lg, t0, 0u);
+    CHECK(e.is_err());
+    if (e.is_err())
+        CHECK(e.error().to_string() ==
+              "training error: invalid training configuration: all tokens are ignored, cannot compute loss");
+}
+
+// loss.rs:319-341 test_cross_entropy_loss_invalid_shapes, _shape_mismatch
+CASE(cross_entropy_shape_errors, true) {
+    TRY(l2, Tensor::zeros({2, 10}, DType::F32, kHip));
+    TRY(t2, Tensor::from_u32(std::vector<uint32_t>(20, 0), {2, 10}, kHip));
+    auto a = cross_entropy_loss(l2, t2, std::nullopt);
+    CHECK(a.is_err());
+    if (a.is_err())
+        CHECK(a.error().to_string() == "training error: invalid training configuration: logits must be 3D (batch, "
+                                       "seq_len, vocab_size), got shape [2, 10]");
+    TRY(l3, Tensor::zeros({2, 10, 100}, DType::F32, kHip));
+    TRY(t5, Tensor::from_u32(std::vector<uint32_t>(10, 0), {2, 5}, kHip));
+    auto b = cross_entropy_loss(l3, t5, std::nullopt);
+    CHECK(b.is_err());
+    if (b.is_err())
+        CHECK(b.error().to_string() == "training error: invalid training configuration: logits and targets "
+                                       "batch/seq_len mismatch: logits [2, 10] vs targets [2, 5]");
+}
+
+// loss.rs:344-380 label smoothing: zero equals plain, 0.1 raises the loss, 1.0 and -0.1 are rejected
+CASE(cross_entropy_label_smoothing, true) {
+    TRY(lg, Tensor::from_slice({1, 2, 3}, {1, 1, 3}, kHip));
+    TRY(t, Tensor::from_u32({2}, {1, 1}, kHip));
+    CHECK(fabs(loss_of(cross_entropy_loss(lg, t, std::nullopt)) -
+               loss_of(cross_entropy_loss_with_smoothing(lg, t, 0.f, std::nullopt))) < 1e-6);
+    TRY(lg2, Tensor::from_slice({10, 0, 0}, {1, 1, 3}, kHip));
+    TRY(t0, Tensor::from_u32({0}, {1, 1}, kHip));
+    CHECK(loss_of(cross_entropy_loss_with_smoothing(lg2, t0, 0.1f, std::nullopt)) >
+          loss_of(cross_entropy_loss(lg2, t0, std::nullopt)));
+    auto a = cross_entropy_loss_with_smoothing(lg, t, 1.f, std::nullopt);
+    auto b = cross_entropy_loss_with_smoothing(lg, t, -0.1f, std::nullopt);
+    CHECK(a.is_err() && b.is_err());
+    if (a.is_err())
+        CHECK(a.error().to_string() == "training error: invalid training configuration: smoothing must be in [0, 1), got 1");
+    if (b.is_err())
+        CHECK(b.error().to_string() == "training error: invalid training configuration: smoothing must be in [0, 1), got -0.1");
+}
+
+// the gradient extension against the oracle
+CASE(cross_entropy_backward, true) {
+    const int64_t B = 2, S = 8, V = 50;
+    const auto x = randn((size_t)(B * S * V), 0, 2, 76);
+    std::vector<uint32_t> t((size_t)(B * S));
+    for (size_t i = 0; i < t.size(); ++i) t[i] = (uint32_t)((i * 7) % V);
+    t[3] = 0;
+    TRY(lg, Tensor::from_slice(x, {B, S, V}, kHip));
+    TRY(tt, Tensor::from_u32(t, {B, S}, kHip));
+    TRY(g, cross_entropy_loss_backward(lg, tt, 0.1f, 0u, 2.0f));
+    TRY(vg, g.to_vec_f32());
+    std::vector<float> rg(x.size());
+    oracle_cross_entropy_bwd(B * S, V, x.data(), t.data(), 0, 0.1f, 2.0f, rg.data());
+    CHECK_LE(rel_err(vg, rg), kTolF32);
+}
+
 // ================================================================== main
 int main(int argc, char** argv) {
     bool gpu = false;
