@@ -34,6 +34,7 @@
 
 #include <stdint.h>
 
+#include <map>
 #include <memory>
 #include <optional>
 #include <string>
@@ -373,6 +374,83 @@ private:
     size_t step_count_ = 0;
     State* find(const std::string& name);
 };
+
+// ------------------------------------------------------------------ adapter
+// TargetModule (adapter.rs:12-58).
+enum class TargetModule { QProj, KProj, VProj, OProj, GateProj, UpProj, DownProj };
+const char* target_module_name(TargetModule m);
+std::optional<TargetModule> target_module_from_name(const std::string& name);
+
+// LoRAAdapterConfig (adapter.rs:60-100): defaults rank 8, alpha 16, q and v.
+struct LoRAAdapterConfig {
+    size_t rank = 8;
+    float alpha = 16.f;
+    float dropout = 0.f;
+    std::vector<TargetModule> target_modules{TargetModule::QProj, TargetModule::VProj};
+    LoRAConfig to_lora_config() const { return LoRAConfig{rank, alpha, dropout}; }
+    bool is_target(TargetModule m) const;
+};
+
+// LoRAAdapter (adapter.rs:102-258): one LoRALayer per (layer, target module),
+// keyed "layers.{i}.{module}"; q/k/v/o are hidden x hidden, gate/up hidden x
+// intermediate, down intermediate x hidden (adapter.rs:193-206). layers()
+// iterates in key order (the reference's HashMap has none).
+class LoRAAdapter {
+public:
+    static Result<LoRAAdapter, Error> create(size_t hidden_size, size_t intermediate_size, size_t num_layers,
+                                             const LoRAAdapterConfig& config, const Device& device,
+                                             uint64_t seed = 0);
+    // forward (adapter.rs:215-231): the layer's delta, or nullopt when the
+    // module is not adapted.
+    Result<std::optional<Tensor>, Error> forward(size_t layer_idx, TargetModule module, const Tensor& input);
+    size_t num_trainable_parameters() const;
+    size_t num_frozen_parameters(size_t total_model_params) const;
+    const LoRAAdapterConfig& config() const { return config_; }
+    size_t num_layers() const { return num_layers_; }
+    const std::map<std::string, LoRALayer>& layers() const { return layers_; }
+    std::map<std::string, LoRALayer>& layers_mut() { return layers_; }
+    const LoRALayer* get_layer(size_t layer_idx, TargetModule module) const;
+    LoRALayer* get_layer_mut(size_t layer_idx, TargetModule module);
+
+private:
+    std::map<std::string, LoRALayer> layers_;
+    LoRAAdapterConfig config_;
+    size_t num_layers_ = 0;
+};
+
+// ------------------------------------------------------------------ checkpoints
+// CheckpointMetadata (checkpoint.rs:11-27), stored as the JSON string of the
+// safetensors metadata entry "checkpoint_metadata" in serde_json's form.
+struct CheckpointMetadata {
+    uint64_t global_step = 0;
+    float loss = 0.f;
+    float learning_rate = 0.f;
+    uint64_t timestamp = 0;
+    std::string to_json() const;
+    static std::optional<CheckpointMetadata> from_json(const std::string& json);
+};
+
+// save_checkpoint (checkpoint.rs:29-66): every layer's A and B as
+// "{key}.lora_a" / "{key}.lora_b" (F32) in one safetensors file, with the
+// metadata entry when given. The file's bytes are what the safetensors crate
+// writes for the same tensors (header, order, padding).
+Result<void, Error> save_checkpoint(const LoRAAdapter& adapter, const std::string& path,
+                                    const CheckpointMetadata* metadata);
+// load_checkpoint (checkpoint.rs:68-103): sets A and B of every layer whose
+// keys are in the file (others keep their values) and, as the reference,
+// returns no metadata (read_checkpoint_metadata reads it).
+Result<std::optional<CheckpointMetadata>, Error> load_checkpoint(LoRAAdapter& adapter, const std::string& path);
+Result<std::optional<CheckpointMetadata>, Error> read_checkpoint_metadata(const std::string& path);
+
+// The safetensors container (the format of the safetensors crate): an 8-byte
+// little-endian header length, a JSON header (optional "__metadata__" string
+// map, then per tensor dtype / shape / data_offsets) padded with spaces to a
+// multiple of 8, then the tensors' little-endian bytes. Tensors are written
+// in the crate's order: dtype descending, then name.
+Result<void, Error> safetensors_save(const std::vector<std::pair<std::string, Tensor>>& tensors,
+                                     const std::map<std::string, std::string>* metadata, const std::string& path);
+Result<std::map<std::string, Tensor>, Error> safetensors_load(const std::string& path, const Device& device,
+                                                              std::map<std::string, std::string>* metadata = nullptr);
 
 // ------------------------------------------------------------------ graph
 struct NodeId {

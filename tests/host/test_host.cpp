@@ -12,6 +12,7 @@
 #include <math.h>
 #include <stdio.h>
 #include <string.h>
+#include <unistd.h>
 
 #include <functional>
 #include <random>
@@ -1006,6 +1007,157 @@ CASE(cross_entropy_backward, true) {
     std::vector<float> rg(x.size());
     oracle_cross_entropy_bwd(B * S, V, x.data(), t.data(), 0, 0.1f, 2.0f, rg.data());
     CHECK_LE(rel_err(vg, rg), kTolF32);
+}
+
+// ================================================================== adapter
+// adapter.rs:358-372 test_target_module_name / _from_name
+CASE(adapter_target_modules, false) {
+    CHECK(std::string(target_module_name(TargetModule::QProj)) == "q_proj");
+    CHECK(std::string(target_module_name(TargetModule::VProj)) == "v_proj");
+    CHECK(std::string(target_module_name(TargetModule::GateProj)) == "gate_proj");
+    CHECK(target_module_from_name("q_proj") == TargetModule::QProj);
+    CHECK(target_module_from_name("v_proj") == TargetModule::VProj);
+    CHECK(!target_module_from_name("invalid").has_value());
+}
+
+// adapter.rs:375-384 test_lora_adapter_config_default; creation and parameter counts
+CASE(adapter_config_and_creation, false) {
+    const LoRAAdapterConfig c;
+    CHECK(c.rank == 8 && fabs(c.alpha - 16.0) < 1e-7 && c.target_modules.size() == 2);
+    CHECK(c.is_target(TargetModule::QProj) && c.is_target(TargetModule::VProj) && !c.is_target(TargetModule::KProj));
+    LoRAAdapterConfig all = c;
+    all.rank = 4;
+    all.target_modules = {TargetModule::QProj, TargetModule::GateProj, TargetModule::DownProj};
+    TRY(a, LoRAAdapter::create(32, 128, 2, all, kCpu));
+    CHECK(a.layers().size() == 6 && a.num_layers() == 2);
+    const LoRALayer* q = a.get_layer(1, TargetModule::QProj);
+    const LoRALayer* g = a.get_layer(0, TargetModule::GateProj);
+    const LoRALayer* d = a.get_layer(1, TargetModule::DownProj);
+    CHECK(q && g && d && !a.get_layer(0, TargetModule::VProj));
+    if (q && g && d) {
+        CHECK(q->lora_a_tensor().dims() == std::vector<int64_t>({32, 4}));
+        CHECK(g->lora_b_tensor().dims() == std::vector<int64_t>({4, 128}));
+        CHECK(d->lora_a_tensor().dims() == std::vector<int64_t>({128, 4}));
+    }
+    // q: 4 (32 + 32), gate: 4 (32 + 128), down: 4 (128 + 32), two layers
+    CHECK(a.num_trainable_parameters() == 2 * (4 * 64 + 4 * 160 + 4 * 160));
+    CHECK(a.num_frozen_parameters(10) == 0);
+    CHECK(a.num_frozen_parameters(1000000) == 1000000 - a.num_trainable_parameters());
+}
+
+// ================================================================== checkpoints
+static std::string tmp_path(const char* name) {
+    const char* d = getenv("MC_CKPT_DIR");
+    return std::string(d && *d ? d : "/tmp") + "/" + name;
+}
+
+static LoRAAdapterConfig ckpt_config() {
+    LoRAAdapterConfig c;  // checkpoint.rs tests: rank 4, alpha 8, q_proj
+    c.rank = 4;
+    c.alpha = 8.f;
+    c.target_modules = {TargetModule::QProj};
+    return c;
+}
+
+// checkpoint.rs:113-150 test_save_and_load_checkpoint
+CASE(checkpoint_save_and_load, false) {
+    TRY(a, LoRAAdapter::create(32, 128, 2, ckpt_config(), kCpu, 1));
+    const std::string path = tmp_path("mc_ckpt_meta.safetensors");
+    const CheckpointMetadata md{100, 1.5f, 1e-4f, 1234567890ull};
+    CHECK(save_checkpoint(a, path, &md).is_ok());
+    TRY(b, LoRAAdapter::create(32, 128, 2, ckpt_config(), kCpu, 2));
+    auto r = load_checkpoint(b, path);
+    CHECK(r.is_ok() && !r.value().has_value());  // metadata is not loaded (checkpoint.rs:80-82)
+    auto m = read_checkpoint_metadata(path);
+    CHECK(m.is_ok() && m.value().has_value());
+    if (m.is_ok() && m.value()) {
+        CHECK(m.value()->global_step == 100 && m.value()->loss == 1.5f && m.value()->learning_rate == 1e-4f &&
+              m.value()->timestamp == 1234567890ull);
+    }
+    CHECK(md.to_json() == "{\"global_step\":100,\"loss\":1.5,\"learning_rate\":0.0001,\"timestamp\":1234567890}");
+    remove(path.c_str());
+}
+
+// checkpoint.rs:153-177 test_save_checkpoint_without_metadata, 180-221 test_checkpoint_preserves_weights
+CASE(checkpoint_preserves_weights, false) {
+    TRY(a, LoRAAdapter::create(32, 128, 1, ckpt_config(), kCpu, 3));
+    const std::string path = tmp_path("mc_ckpt_plain.safetensors");
+    CHECK(save_checkpoint(a, path, nullptr).is_ok());
+    TRY(b, LoRAAdapter::create(32, 128, 1, ckpt_config(), kCpu, 4));
+    auto r = load_checkpoint(b, path);
+    CHECK(r.is_ok() && !r.value().has_value());
+    auto m = read_checkpoint_metadata(path);
+    CHECK(m.is_ok() && !m.value().has_value());
+    TRY(va, a.get_layer(0, TargetModule::QProj)->lora_a_tensor().to_vec_f32());
+    TRY(vb, b.get_layer(0, TargetModule::QProj)->lora_a_tensor().to_vec_f32());
+    CHECK(va == vb);  // bit for bit
+    remove(path.c_str());
+}
+
+// A HIP adapter round trip, and errors: missing file, truncated file, wrong shape
+CASE(checkpoint_hip_and_errors, true) {
+    LoRAAdapterConfig c = ckpt_config();
+    c.target_modules = {TargetModule::QProj, TargetModule::DownProj};
+    TRY(a, LoRAAdapter::create(64, 96, 2, c, kHip, 5));
+    const std::string path = tmp_path("mc_ckpt_hip.safetensors");
+    CHECK(save_checkpoint(a, path, nullptr).is_ok());
+    TRY(b, LoRAAdapter::create(64, 96, 2, c, kHip, 6));
+    CHECK(load_checkpoint(b, path).is_ok());
+    for (const auto& kv : a.layers()) {
+        TRY(x, kv.second.lora_b_tensor().to_vec_f32());
+        TRY(y, b.layers().at(kv.first).lora_b_tensor().to_vec_f32());
+        CHECK(x == y);
+    }
+    TRY(wrong, LoRAAdapter::create(32, 96, 2, c, kHip, 7));  // different hidden size: shapes differ
+    CHECK(load_checkpoint(wrong, path).is_err());
+    CHECK(load_checkpoint(b, tmp_path("mc_no_such_file.safetensors")).is_err());
+    FILE* f = fopen(path.c_str(), "r+b");
+    if (f) {
+        fseek(f, 0, SEEK_END);
+        const long n = ftell(f);
+        fclose(f);
+        CHECK(truncate(path.c_str(), n - 5) == 0);
+        CHECK(load_checkpoint(b, path).is_err());
+    }
+    remove(path.c_str());
+}
+
+// The file format against the safetensors library: tests/test_checkpoint_cpu.py
+// writes py.safetensors with safetensors.numpy for the tensors below and runs
+// this case with MC_CKPT_DIR set; this case writes cpp.safetensors for the same
+// tensors (the Python side compares the bytes) and reads py.safetensors.
+CASE(checkpoint_format, false) {
+    if (!getenv("MC_CKPT_DIR")) return;  // driven by the Python test
+    LoRAAdapterConfig c = ckpt_config();
+    c.target_modules = {TargetModule::QProj, TargetModule::VProj, TargetModule::GateProj, TargetModule::DownProj};
+    TRY(a, LoRAAdapter::create(16, 24, 2, c, kCpu, 8));
+    // tensor k of the name-sorted list holds ((131 k + 17 i + 3 j) % 97) / 100 - 0.5 at [i][j]
+    int k = 0;
+    for (auto& kv : a.layers_mut()) {
+        for (int ab = 0; ab < 2; ++ab, ++k) {
+            const Tensor& t = ab == 0 ? kv.second.lora_a_tensor() : kv.second.lora_b_tensor();
+            const int64_t R = t.dims()[0], C = t.dims()[1];
+            std::vector<float> v((size_t)(R * C));
+            for (int64_t i = 0; i < R; ++i)
+                for (int64_t j = 0; j < C; ++j)
+                    v[(size_t)(i * C + j)] = (float)((131 * k + 17 * i + 3 * j) % 97) / 100.f - 0.5f;
+            TRY(nt, Tensor::from_slice(v, {R, C}, kCpu));
+            CHECK((ab == 0 ? kv.second.set_lora_a(nt) : kv.second.set_lora_b(nt)).is_ok());
+        }
+    }
+    const CheckpointMetadata md{100, 1.5f, 1e-4f, 1234567890ull};
+    CHECK(save_checkpoint(a, tmp_path("cpp.safetensors"), &md).is_ok());
+    TRY(b, LoRAAdapter::create(16, 24, 2, c, kCpu, 9));
+    CHECK(load_checkpoint(b, tmp_path("py.safetensors")).is_ok());
+    for (const auto& kv : a.layers()) {
+        TRY(x, kv.second.lora_a_tensor().to_vec_f32());
+        TRY(y, b.layers().at(kv.first).lora_a_tensor().to_vec_f32());
+        TRY(x2, kv.second.lora_b_tensor().to_vec_f32());
+        TRY(y2, b.layers().at(kv.first).lora_b_tensor().to_vec_f32());
+        CHECK(x == y && x2 == y2);
+    }
+    auto m = read_checkpoint_metadata(tmp_path("py.safetensors"));
+    CHECK(m.is_ok() && m.value().has_value() && m.value()->global_step == 100 && m.value()->timestamp == 1234567890ull);
 }
 
 // ================================================================== main
