@@ -500,26 +500,31 @@ __global__ __launch_bounds__(256) void xent_rows_k(int64_t vocab, bool vec, cons
 __global__ __launch_bounds__(256) void xent_final_k(int64_t rows, int64_t vocab, float smoothing,
                                                     const float* __restrict__ rowv, float* __restrict__ loss,
                                                     float* __restrict__ count_out) {
-    __shared__ float part[3][256];
-    const int64_t per = (rows + 255) / 256;
-    const int64_t a = threadIdx.x * per, b = a + per < rows ? a + per : rows;
+    // thread t sums rows t, t + 256, ... (eight loads of each kind in flight,
+    // coalesced across the workgroup), then fixed-order block sums
+    __shared__ float red[4];
     float n = 0.f, sm = 0.f, c = 0.f;
-    for (int64_t i = a; i < b; ++i) {
-        n += rowv[3 * i];
-        sm += rowv[3 * i + 1];
-        c += rowv[3 * i + 2];
-    }
-    part[0][threadIdx.x] = n;
-    part[1][threadIdx.x] = sm;
-    part[2][threadIdx.x] = c;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        float tn = 0.f, ts = 0.f, tc = 0.f;
-        for (int k = 0; k < 256; ++k) {
-            tn += part[0][k];
-            ts += part[1][k];
-            tc += part[2][k];
+    for (int64_t i0 = threadIdx.x; i0 < rows; i0 += 256 * 8) {
+        float vn[8], vs[8], vc[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int64_t i = i0 + 256 * u;
+            const bool ok = i < rows;
+            vn[u] = ok ? rowv[3 * i] : 0.f;
+            vs[u] = ok ? rowv[3 * i + 1] : 0.f;
+            vc[u] = ok ? rowv[3 * i + 2] : 0.f;
         }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            n += vn[u];
+            sm += vs[u];
+            c += vc[u];
+        }
+    }
+    const float tn = block_sum256(n, red);
+    const float ts = block_sum256(sm, red);
+    const float tc = block_sum256(c, red);
+    if (threadIdx.x == 0) {
         // mean of -nll over the counted rows; all ignored: 0 / 0 = NaN
         const float nll = tn / tc;
         float l = nll;
