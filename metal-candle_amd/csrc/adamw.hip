@@ -13,7 +13,9 @@
 //   p1 = (p - (u * lr + 0)) - (p * (wd * lr) + 0)
 //
 // adamw_kernel fuses the chain into one pass over (p, g, m, v): 16 bytes in
-// and 12 out per element, HBM-bound. Contraction into FMA is off for this
+// and 12 out per element, HBM-bound (one float4 of each per thread: the
+// LoRA parameter sets are small, so more workgroups keep more CUs loading).
+// Contraction into FMA is off for this
 // file, division and square root are the correctly rounded ones, so every
 // value equals the fp32 op sequence above bit for bit. One launch updates up
 // to kSlots tensors (a table passed by value); each workgroup finds its
@@ -27,7 +29,7 @@ namespace mc {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kPerBlock = kThreads * 4 * 2;  // elements per workgroup: 2 float4 per thread
+constexpr int kPerBlock = kThreads * 4;  // elements per workgroup: one float4 per thread
 
 __device__ __forceinline__ float affine0(float x, float mul) { return x * mul + 0.0f; }
 
@@ -51,9 +53,8 @@ __global__ __launch_bounds__(kThreads) void adamw_kernel(AdamWBatch bt) {
         if ((int)blockIdx.x >= bt.slot[i].blk0) s = i;
     const AdamWSlot& t = bt.slot[s];
     const int64_t base = (int64_t)((int)blockIdx.x - t.blk0) * kPerBlock;
-#pragma unroll
-    for (int it = 0; it < 2; ++it) {
-        const int64_t e = base + ((int64_t)it * kThreads + threadIdx.x) * 4;
+    {
+        const int64_t e = base + (int64_t)threadIdx.x * 4;
         if (e + 4 <= t.n) {
             float4 p = *reinterpret_cast<const float4*>(t.p + e);
             const float4 g = *reinterpret_cast<const float4*>(t.g + e);

@@ -497,34 +497,55 @@ __global__ __launch_bounds__(256) void xent_rows_k(int64_t vocab, bool vec, cons
 
 // loss = -(sum log p[t] / count) * (1 - s) + s * (-(sum of all log p) / (rows vocab)),
 // sums in row order (each thread a contiguous run of rows, then the threads in order).
-__global__ __launch_bounds__(256) void xent_final_k(int64_t rows, int64_t vocab, float smoothing,
-                                                    const float* __restrict__ rowv, float* __restrict__ loss,
-                                                    float* __restrict__ count_out) {
-    // thread t sums rows t, t + 256, ... (eight loads of each kind in flight,
-    // coalesced across the workgroup), then fixed-order block sums
-    __shared__ float red[4];
-    float n = 0.f, sm = 0.f, c = 0.f;
-    for (int64_t i0 = threadIdx.x; i0 < rows; i0 += 256 * 8) {
-        float vn[8], vs[8], vc[8];
+__global__ __launch_bounds__(1024) void xent_final_k(int64_t rows, int64_t vocab, float smoothing,
+                                                     const float* __restrict__ rowv, float* __restrict__ loss,
+                                                     float* __restrict__ count_out) {
+    // rowv is [rows][3] = (nll, sum x - V lse, valid): read flat as float4
+    // (16 per thread in flight: one round for up to 16384 rows, the whole
+    // array being fetched from other XCDs' writes); element f belongs to
+    // component f % 3, and for f = 4 v + e that is (v + e) % 3. Fixed-order
+    // wave and block sums make the result reproducible.
+    constexpr int kT = 1024, kU = 16;
+    __shared__ float red[kT / 64][3];
+    const int64_t nf = 3 * rows, nv = nf / 4;
+    const float4* rv4 = reinterpret_cast<const float4*>(rowv);
+    float acc[3] = {0.f, 0.f, 0.f};
+    auto add = [&](int64_t f, float x) {
+        const int c = (int)(f % 3);
+        acc[0] += c == 0 ? x : 0.f;
+        acc[1] += c == 1 ? x : 0.f;
+        acc[2] += c == 2 ? x : 0.f;
+    };
+    for (int64_t v0 = threadIdx.x; v0 < nv; v0 += (int64_t)kT * kU) {
+        float4 x[kU];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const int64_t i = i0 + 256 * u;
-            const bool ok = i < rows;
-            vn[u] = ok ? rowv[3 * i] : 0.f;
-            vs[u] = ok ? rowv[3 * i + 1] : 0.f;
-            vc[u] = ok ? rowv[3 * i + 2] : 0.f;
+        for (int u = 0; u < kU; ++u) {
+            const int64_t v = v0 + (int64_t)kT * u;
+            x[u] = v < nv ? rv4[v] : make_float4(0.f, 0.f, 0.f, 0.f);
         }
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            n += vn[u];
-            sm += vs[u];
-            c += vc[u];
+        for (int u = 0; u < kU; ++u) {
+            const int64_t f = 4 * (v0 + (int64_t)kT * u);
+            add(f, x[u].x);
+            add(f + 1, x[u].y);
+            add(f + 2, x[u].z);
+            add(f + 3, x[u].w);
         }
     }
-    const float tn = block_sum256(n, red);
-    const float ts = block_sum256(sm, red);
-    const float tc = block_sum256(c, red);
+    if (threadIdx.x < nf - 4 * nv) add(4 * nv + threadIdx.x, rowv[4 * nv + threadIdx.x]);
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+        const float w = wave_sum(acc[c]);
+        if (lane_id() == 0) red[threadIdx.x >> 6][c] = w;
+    }
+    __syncthreads();
     if (threadIdx.x == 0) {
+        float tn = 0.f, ts = 0.f, tc = 0.f;
+        for (int w = 0; w < kT / 64; ++w) {
+            tn += red[w][0];
+            ts += red[w][1];
+            tc += red[w][2];
+        }
         // mean of -nll over the counted rows; all ignored: 0 / 0 = NaN
         const float nll = tn / tc;
         float l = nll;
@@ -721,7 +742,7 @@ hipError_t launch_cross_entropy_fwd(const mc_xent_desc& d, const void* logits, c
                                                         ws, stats);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    xent_final_k<<<1, 256, 0, stream>>>(d.rows, d.vocab, d.smoothing, ws, loss, stats ? stats + d.rows : nullptr);
+    xent_final_k<<<1, 1024, 0, stream>>>(d.rows, d.vocab, d.smoothing, ws, loss, stats ? stats + d.rows : nullptr);
     return hipGetLastError();
 }
 
