@@ -33,6 +33,7 @@
 // Other head dims and fp32: attn_fwd_generic, one wave per query row (lanes
 // over the head dim), online softmax in fp32.
 #include <algorithm>
+#include <type_traits>
 
 #include "common.hpp"
 #include "kernels.hpp"
@@ -218,12 +219,16 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16(AttnFwdArgs a) {
         }
         const bool edge = key0 + KB > S || (a.causal && key0 + KB - 1 > qw);
         if (edge) {
+            // key offsets in the block (32 t + 8 (j/4) + 4 half + j%4) against
+            // the first offset past S and, causal, this lane's query offset
+            const int lim = (int)min<int64_t>(S - key0, KB);
+            const int qrel = a.causal ? (int)max<int64_t>(min<int64_t>(my_q - key0, KB), -1) : KB;
 #pragma unroll
             for (int t = 0; t < 2; ++t)
 #pragma unroll
                 for (int j = 0; j < 16; ++j) {
-                    const int64_t key = key0 + 32 * t + 8 * (j >> 2) + 4 * half + (j & 3);
-                    if (key >= S || (a.causal && key > my_q)) x[t][j] = kNegInf;
+                    const int ko = 32 * t + 8 * (j >> 2) + 4 * half + (j & 3);
+                    if (ko >= lim || ko > qrel) x[t][j] = kNegInf;
                 }
         }
 
@@ -236,21 +241,25 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16(AttnFwdArgs a) {
         mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
         const float m_new = fmaxf(m_run, mx);
         const float m_use = m_new == kNegInf ? 0.f : m_new;  // a row with no key yet keeps p = 0
-        const float alpha = exp2f(m_run - m_use);
+        const float alpha = exp2_hw(m_run - m_use);
         m_run = m_new;
         float ps = 0.f;
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
             for (int j = 0; j < 16; ++j) {
-                x[t][j] = exp2f(x[t][j] - m_use);
+                x[t][j] = exp2_hw(x[t][j] - m_use);
                 ps += x[t][j];
             }
         l_run = l_run * alpha + ps;
+        // rescale O only when some lane's running max moved (alpha = 1
+        // elsewhere, so skipping the multiply changes nothing)
+        if (__any(alpha != 1.f)) {
 #pragma unroll
-        for (int t = 0; t < DT; ++t)
+            for (int t = 0; t < DT; ++t)
 #pragma unroll
-            for (int j = 0; j < 16; ++j) oacc[t][j] *= alpha;
+                for (int j = 0; j < 16; ++j) oacc[t][j] *= alpha;
+        }
 
         // P^T fragments: k-step (t, kk) takes accumulators 8 kk .. 8 kk + 7 of
         // tile t, i.e. keys 32 t + 16 kk + perm16(8 half + e), e = 0..7.
@@ -258,9 +267,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16(AttnFwdArgs a) {
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
-            for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-                for (int e = 0; e < 8; ++e) pf[t][kk][e] = static_cast<__bf16>(x[t][8 * kk + e]);
+            for (int kk = 0; kk < 2; ++kk) pf[t][kk] = pack_bf16x8(&x[t][8 * kk]);
 
         // O^T (d x query) += V^T . P^T; V^T positions 16 (2t + kk) + 8 half .. +7
 #pragma unroll
@@ -651,32 +658,47 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_bf16(AttnBwdArgs a) {
             }
 
         // accumulator j of tile t: query q0 + 32 t + 8 (j/4) + 4 half + j%4, key my_key
-        const bool edge = a.causal && q0 < kw + 31;
         bf16x8 pb[2][2], db[2][2];
+        // P and dS of the block; MASK adds the additive mask, EDGE applies the
+        // causal test (key offset from q0 against the query offset)
+        auto scores = [&](auto mask_tag, auto edge_tag) {
+            constexpr bool MASK = decltype(mask_tag)::value, EDGE = decltype(edge_tag)::value;
+            const int kq = (int)(my_key - q0);
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
+            for (int t = 0; t < 2; ++t) {
+                float p[16], ds[16];
 #pragma unroll
-            for (int jq = 0; jq < 4; ++jq) {
-                const int qi = 32 * t + 8 * jq + 4 * half;  // first of 4 consecutive queries
-                const float4 l2 = *reinterpret_cast<const float4*>(&sl[qi]);
-                const float4 dl = *reinterpret_cast<const float4*>(&sl[64 + qi]);
-                const float lv[4] = {l2.x, l2.y, l2.z, l2.w}, dv4[4] = {dl.x, dl.y, dl.z, dl.w};
+                for (int jq = 0; jq < 4; ++jq) {
+                    const int qi = 32 * t + 8 * jq + 4 * half;  // first of 4 consecutive queries
+                    const float4 l2 = *reinterpret_cast<const float4*>(&sl[qi]);
+                    const float4 dl = *reinterpret_cast<const float4*>(&sl[64 + qi]);
+                    const float lv[4] = {l2.x, l2.y, l2.z, l2.w}, dv4[4] = {dl.x, dl.y, dl.z, dl.w};
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int j = 4 * jq + e;
-                    const int64_t qq = q0 + qi + e;
-                    float x = sacc[t][j] * a.scale_log2;
-                    if (a.mask) {
-                        const uint32_t off = (qq < S && my_key < S) ? (uint32_t)((qq * S + my_key) * 4) : kOOB;
-                        x += __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(rm, (int)off, 0, 0)) * kLog2e;
+                    for (int e = 0; e < 4; ++e) {
+                        const int j = 4 * jq + e;
+                        float x = sacc[t][j] * a.scale_log2;
+                        if constexpr (MASK) {
+                            const int64_t qq = q0 + qi + e;
+                            const uint32_t off = (qq < S && my_key < S) ? (uint32_t)((qq * S + my_key) * 4) : kOOB;
+                            x += __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(rm, (int)off, 0, 0)) * kLog2e;
+                        }
+                        if constexpr (EDGE) {
+                            if ((!MASK || a.causal) && kq > qi + e) x = kNegInf;
+                        }
+                        p[j] = exp2_hw(x - lv[e]);
+                        ds[j] = p[j] * (dpacc[t][j] - dv4[e]);
                     }
-                    if (edge && my_key > qq) x = kNegInf;
-                    const float p = exp2f(x - lv[e]);
-                    const float ds = p * (dpacc[t][j] - dv4[e]);
-                    pb[t][j >> 3][j & 7] = static_cast<__bf16>(p);
-                    db[t][j >> 3][j & 7] = static_cast<__bf16>(ds);
+                }
+#pragma unroll
+                for (int kk = 0; kk < 2; ++kk) {
+                    pb[t][kk] = pack_bf16x8(&p[8 * kk]);
+                    db[t][kk] = pack_bf16x8(&ds[8 * kk]);
                 }
             }
+        };
+        if (a.mask) scores(std::true_type{}, std::true_type{});
+        else if (a.causal && q0 < kw + 31) scores(std::false_type{}, std::true_type{});
+        else scores(std::false_type{}, std::false_type{});
 
         // dV^T (d x key) += dO^T . P ; dK^T += Q^T . dS ; query positions 16 (2t + kk) + 8 half .. +7
 #pragma unroll
@@ -824,22 +846,37 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq_bf16(AttnBwdArgs a) {
 
         // accumulator j of tile t: key key0 + 32 t + 8 (j/4) + 4 half + j%4, query my_q
         const int64_t key0 = (int64_t)kb * KB;
-        const bool edge = key0 + KB > S || (a.causal && key0 + KB - 1 > qw);
         bf16x8 db[2][2];
+        // dS of the block; MASK adds the additive mask, EDGE drops keys past S
+        // and (causal) keys after this lane's query, as offsets in the block
+        auto scores = [&](auto mask_tag, auto edge_tag) {
+            constexpr bool MASK = decltype(mask_tag)::value, EDGE = decltype(edge_tag)::value;
+            const int lim = (int)min<int64_t>(S - key0, KB);
+            const int qrel = a.causal ? (int)max<int64_t>(min<int64_t>(my_q - key0, KB), -1) : KB;
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
+            for (int t = 0; t < 2; ++t) {
+                float ds[16];
 #pragma unroll
-            for (int j = 0; j < 16; ++j) {
-                const int64_t key = key0 + 32 * t + 8 * (j >> 2) + 4 * half + (j & 3);
-                float x = sacc[t][j] * a.scale_log2;
-                if (a.mask) {
-                    const uint32_t off = (my_q < S && key < S) ? (uint32_t)((my_q * S + key) * 4) : kOOB;
-                    x += __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(rm, (int)off, 0, 0)) * kLog2e;
+                for (int j = 0; j < 16; ++j) {
+                    const int ko = 32 * t + 8 * (j >> 2) + 4 * half + (j & 3);
+                    float x = sacc[t][j] * a.scale_log2;
+                    if constexpr (MASK) {
+                        const int64_t key = key0 + ko;
+                        const uint32_t off = (my_q < S && key < S) ? (uint32_t)((my_q * S + key) * 4) : kOOB;
+                        x += __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(rm, (int)off, 0, 0)) * kLog2e;
+                    }
+                    if constexpr (EDGE) {
+                        if (ko >= lim || ko > qrel) x = kNegInf;
+                    }
+                    ds[j] = exp2_hw(x - lse2) * (dpacc[t][j] - delta);
                 }
-                if (edge && (key >= S || (a.causal && key > my_q))) x = kNegInf;
-                const float p = exp2f(x - lse2);
-                db[t][j >> 3][j & 7] = static_cast<__bf16>(p * (dpacc[t][j] - delta));
+#pragma unroll
+                for (int kk = 0; kk < 2; ++kk) db[t][kk] = pack_bf16x8(&ds[8 * kk]);
             }
+        };
+        if (a.mask) scores(std::true_type{}, std::true_type{});
+        else if (key0 + KB > S || (a.causal && key0 + KB - 1 > qw)) scores(std::false_type{}, std::true_type{});
+        else scores(std::false_type{}, std::false_type{});
 
         // dQ^T (d x query) += K^T . dS^T ; key positions 16 (2t + kk) + 8 half .. +7
 #pragma unroll

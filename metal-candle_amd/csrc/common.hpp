@@ -25,9 +25,25 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
     __bf16 b = static_cast<__bf16>(f);
     return __builtin_bit_cast(uint16_t, b);
 }
+typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+typedef float f32x2v __attribute__((ext_vector_type(2)));
+// Two floats to a bf16 pair (lo in bits 0-15), one v_cvt_pk_bf16_f32.
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-    return (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
+    const f32x2v v = {lo, hi};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2v));
 }
+// Eight floats to an MFMA bf16 operand, element e from v[e].
+__device__ __forceinline__ bf16x8 pack_bf16x8(const float* v) {
+    const u32x4 w = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]),
+                     pack_bf16x2(v[6], v[7])};
+    return __builtin_bit_cast(bf16x8, w);
+}
+
+// 2^x with the hardware instruction (v_exp_f32), without the library's
+// rescaling for results below 2^-126, which come out as 0 here. Used where
+// the argument is a max-shifted score, so such terms are negligible in any
+// sum they enter; exp2(-inf) = 0.
+__device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // Storage-type traits: float or bf16 (stored as uint16_t bit patterns).
 template <typename T> struct Elem;
