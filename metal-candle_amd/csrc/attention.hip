@@ -385,32 +385,30 @@ __global__ __launch_bounds__(256) void attn_fwd_generic(const T* __restrict__ q,
 // Every sum runs in a fixed order: results are bitwise reproducible.
 //
 // bf16, D = 64 or 128:
-//  attn_bwd_prep_bf16  per (b, h, 64 queries): Delta, lse * log2 e (both
-//                      into one [2][64] fp32 block per query block), and Q^T,
-//                      dO^T [D, Sp] with the perm16 position order.
-//  attn_vt_bf16        K^T (the V^T prepass of the forward, applied to K).
+//  attn_bwd_prep_bf16  per (b, h, 64 queries): Delta and lse * log2 e, both
+//                      into one [2][64] fp32 block per query block.
 //  attn_bwd_dkdv_bf16  one workgroup per (b, h, 128 keys), 4 waves of 32 keys;
-//                      per block of 64 queries (Q, dO, Q^T, dO^T and the
-//                      lse/Delta block through LDS, two stages):
+//                      per block of 64 queries (Q, dO and the lse/Delta block
+//                      through LDS, two stages):
 //                        S = Q.K^T, dP = dO.V^T    (lane = key: K, V held in
 //                                                   registers as B operands)
 //                        dV^T += dO^T.P,  dK^T += Q^T.dS   (P, dS straight from
 //                                                   the accumulators as the
-//                                                   B operand)
+//                                                   B operand; dO^T, Q^T by
+//                                                   transposed LDS reads of
+//                                                   the dO, Q tiles)
 //                      dK, dV per query head: written directly when H = Hkv,
 //                      else as fp32 partials summed by attn_bwd_sum.
 //  attn_bwd_dq_bf16    one workgroup per (b, h, 128 queries) as the forward:
 //                        S^T = K.Q^T, dP^T = V.dO^T (lane = query: Q, dO held
 //                                                   in registers)
-//                        dQ^T += K^T.dS^T         (K^T from the prepass)
+//                        dQ^T += K^T.dS^T         (K^T by transposed LDS
+//                                                   reads of the K tile)
 struct AttnBwdArgs {
     const uint16_t* q;     // [B, H, S, D]
     const uint16_t* k;     // [B, Hkv, S, D]
     const uint16_t* v;     // [B, Hkv, S, D]
     const uint16_t* dout;  // [B, S, H, D]
-    const uint16_t* qt;    // [B, H, D, Sp]
-    const uint16_t* dot;   // [B, H, D, Sp]
-    const uint16_t* kt;    // [B, Hkv, D, Sp]
     const float* mask;     // [S, S] or null
     const float* lsd;      // [B, H, Sp / 64, 2, 64]: lse * log2 e, Delta
     uint16_t* dq;          // [B, H, S, D]
@@ -439,29 +437,39 @@ __device__ __forceinline__ void dma_rows(i32x4 r, uint32_t lds_byte, uint32_t ro
     }
 }
 
-// [D rows][64 positions] tile (positions pos0 .. pos0+63 of a transposed
-// buffer with row stride Sp) into the swizzled LDS layout.
-template <int D>
-__device__ __forceinline__ void dma_cols(i32x4 r, uint32_t lds_byte, uint32_t pos0, uint32_t Sp, int wave,
-                                         int lane) {
-    constexpr int LOADS = D / 8 / 4;
-#pragma unroll
-    for (int j = 0; j < LOADS; ++j) {
-        const int blk = wave * LOADS + j;
-        const int row = blk * 8 + lane / 8;
-        const uint32_t chunk = (uint32_t)swz<64>(row, lane % 8);
-        const uint32_t off = ((uint32_t)row * Sp + pos0 + 8u * chunk) * 2u;
-        dma16(r, __builtin_amdgcn_readfirstlane(lds_byte + (uint32_t)blk * 1024u), off);
-    }
-}
-
 template <int D>
 __device__ __forceinline__ bf16x8 frag_rows(const uint16_t* t, int row, int c) {
     return *reinterpret_cast<const bf16x8*>(&t[row * D + 8 * swz<D>(row, c)]);
 }
-__device__ __forceinline__ bf16x8 frag_cols(const uint16_t* t, int row, int c) {
-    return *reinterpret_cast<const bf16x8*>(&t[row * 64 + 8 * swz<64>(row, c)]);
+
+// ds_read_b64_tr_b16: within each 16-lane group, lane i receives element i % 4
+// of the 8-byte pieces addressed by the group's lanes i / 4, 4 + i / 4,
+// 8 + i / 4 and 12 + i / 4 (in that order).
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+__device__ __forceinline__ s16x4 ds_read_tr16(const uint16_t* p) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p));
 }
+
+// MFMA 32x32x16 operand of M^T from a row-major swizzled [rows][D] tile M
+// (the layout frag_rows reads): lane l gets column m = dcol + l % 32 of M and
+// the 8 rows kbase + 4 (l / 32) + {0, 1, 2, 3, 8, 9, 10, 11}, the query / key
+// order in which a lane half of an S (or S^T) accumulator holds its rows
+// (8 (j/4) + 4 half + j%4). Two transposed reads of 4 rows each: lane i of
+// group g addresses row kbase + 4 (g / 2) + i / 4 (+ 8), columns
+// dcol + 16 (g % 2) + 4 (i % 4) .. +3.
+template <int D>
+__device__ __forceinline__ bf16x8 frag_tr(const uint16_t* t, int kbase, int dcol, int lane) {
+    const int i = lane & 15, g = lane >> 4;
+    const int ra = kbase + 4 * (g >> 1) + (i >> 2), rb = ra + 8;
+    const int c = (dcol >> 3) + 2 * (g & 1) + ((i & 3) >> 1);
+    const int sub = 4 * (i & 1);
+    const s16x4 lo = ds_read_tr16(&t[ra * D + 8 * swz<D>(ra, c) + sub]);
+    const s16x4 hi = ds_read_tr16(&t[rb * D + 8 * swz<D>(rb, c) + sub]);
+    const s16x4 v8[2] = {lo, hi};
+    return __builtin_bit_cast(bf16x8, v8);
+}
+
 
 // Rows of a wave's transposed accumulators (acc[dt] element j = dim
 // 32 dt + 8 (j/4) + 4 half + j%4 of row `col`) through a per-wave LDS patch
@@ -504,65 +512,39 @@ __device__ __forceinline__ void store_rows(const f32x16 (&acc)[D / 32], float sc
 }
 
 // --------------------------------------------------------- backward prep
+// Per (b, h, 64 queries): Delta = rowsum(dO * O) and lse * log2 e into one
+// [2][64] fp32 block (4 threads per query row, D / 4 dims each).
 template <int D>
-__global__ __launch_bounds__(256) void attn_bwd_prep_bf16(const uint16_t* __restrict__ q,
-                                                          const uint16_t* __restrict__ o,
+__global__ __launch_bounds__(256) void attn_bwd_prep_bf16(const uint16_t* __restrict__ o,
                                                           const uint16_t* __restrict__ dout,
                                                           const float* __restrict__ lse, int H, int64_t S,
-                                                          int64_t Sp, float* __restrict__ lsd,
-                                                          uint16_t* __restrict__ qt, uint16_t* __restrict__ dot) {
+                                                          int64_t Sp, float* __restrict__ lsd) {
     constexpr int CPR = D / 8;
-    __shared__ __attribute__((aligned(16))) uint16_t tile[2][64][D + 8];
     const int64_t bh = blockIdx.y;
     const int64_t b = bh / H, h = bh % H;
     const int64_t q0 = (int64_t)blockIdx.x * 64;
     const int64_t ldo = (int64_t)H * D;
-    const __amdgpu_buffer_rsrc_t rq = make_rsrc(q + bh * S * D, S * D * 2);
     const __amdgpu_buffer_rsrc_t ro = make_rsrc(o + (b * S * H + h) * D, (S * H - h) * D * 2);
     const __amdgpu_buffer_rsrc_t rd = make_rsrc(dout + (b * S * H + h) * D, (S * H - h) * D * 2);
-    for (int i = threadIdx.x; i < 64 * CPR; i += 256) {
-        const int row = i / CPR, c = i % CPR;
-        const bool ok = q0 + row < S;
-        const uint32_t oq = ok ? (uint32_t)(((q0 + row) * D + 8 * c) * 2) : kOOB;
-        const uint32_t od = ok ? (uint32_t)(((q0 + row) * ldo + 8 * c) * 2) : kOOB;
-        *reinterpret_cast<i32x4*>(&tile[0][row][8 * c]) = buf_load16(rq, oq);
-        *reinterpret_cast<i32x4*>(&tile[1][row][8 * c]) = buf_load16(rd, od);
+    const int row = threadIdx.x >> 2, part = threadIdx.x & 3;
+    const bool ok = q0 + row < S;
+    float acc = 0.f;
+#pragma unroll
+    for (int c = 0; c < CPR / 4; ++c) {
+        const uint32_t off = ok ? (uint32_t)(((q0 + row) * ldo + 8 * (part * (CPR / 4) + c)) * 2) : kOOB;
+        float x[8], g[8];
+        BVec<uint16_t>::unpack(buf_load16(ro, off), x);
+        BVec<uint16_t>::unpack(buf_load16(rd, off), g);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc += x[e] * g[e];
     }
-    // Delta = rowsum(dO * O): 4 threads per query row, D / 4 dims each
-    {
-        const int row = threadIdx.x >> 2, part = threadIdx.x & 3;
-        const bool ok = q0 + row < S;
-        float acc = 0.f;
-#pragma unroll
-        for (int c = 0; c < CPR / 4; ++c) {
-            const uint32_t off = ok ? (uint32_t)(((q0 + row) * ldo + 8 * (part * (CPR / 4) + c)) * 2) : kOOB;
-            float a[8], g[8];
-            BVec<uint16_t>::unpack(buf_load16(ro, off), a);
-            BVec<uint16_t>::unpack(buf_load16(rd, off), g);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) acc += a[e] * g[e];
-        }
-        acc += __shfl_xor(acc, 1, kWave);
-        acc += __shfl_xor(acc, 2, kWave);
-        if (part == 0) {
-            float* blk = lsd + (bh * (Sp / 64) + blockIdx.x) * 128;
-            // padded queries: lse = +inf makes their P exactly 0
-            blk[row] = ok ? lse[bh * S + q0 + row] * kLog2e : __builtin_inff();
-            blk[64 + row] = ok ? acc : 0.f;
-        }
-    }
-    __syncthreads();
-    for (int i = threadIdx.x; i < 2 * D * 8; i += 256) {
-        const int which = i / (D * 8), d = (i >> 3) % D, c = i & 7;
-        uint32_t w[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int p0 = 8 * c + 2 * e, p1 = p0 + 1;
-            const int r0 = (p0 & ~15) | perm16(p0 & 15), r1 = (p1 & ~15) | perm16(p1 & 15);
-            w[e] = (uint32_t)tile[which][r0][d] | ((uint32_t)tile[which][r1][d] << 16);
-        }
-        uint16_t* dst = (which ? dot : qt) + bh * D * Sp + q0;
-        *reinterpret_cast<uint4*>(dst + (int64_t)d * Sp + 8 * c) = make_uint4(w[0], w[1], w[2], w[3]);
+    acc += __shfl_xor(acc, 1, kWave);
+    acc += __shfl_xor(acc, 2, kWave);
+    if (part == 0) {
+        float* blk = lsd + (bh * (Sp / 64) + blockIdx.x) * 128;
+        // padded queries: lse = +inf makes their P exactly 0
+        blk[row] = ok ? lse[bh * S + q0 + row] * kLog2e : __builtin_inff();
+        blk[64 + row] = ok ? acc : 0.f;
     }
 }
 
@@ -571,8 +553,12 @@ template <int D>
 __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_bf16(AttnBwdArgs a) {
     constexpr int KS = D / 16, DT = D / 32;
     constexpr int TILE = 64 * D;                 // one [64][D] or [D][64] tile
-    constexpr int STAGE = 4 * TILE + 512;        // Q, dO, Q^T, dO^T, lse/Delta (1 KB)
-    __shared__ __attribute__((aligned(1024))) uint16_t smem[2 * STAGE];
+    constexpr int STAGE = 2 * TILE + 512;        // Q, dO, lse/Delta (1 KB)
+    // the epilogue reuses the stages as per-wave patches of 32 rows x (D + 8)
+    // uint16 x 2 (fp32 partials with 16-byte row padding); allocate the larger
+    constexpr int PATCH = 4 * 32 * (D + 8) * 2;
+    constexpr int SMEM = 2 * STAGE > PATCH ? 2 * STAGE : PATCH;
+    __shared__ __attribute__((aligned(1024))) uint16_t smem[SMEM];
     const uint32_t smem_byte = (uint32_t)reinterpret_cast<uintptr_t>(smem);
     const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
     const int col = lane & 31, half = lane >> 5;
@@ -600,8 +586,6 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_bf16(AttnBwdArgs a) {
 
     const i32x4 rq = rsrc_words(a.q + (int64_t)bh * S * D, S * D * 2);
     const i32x4 rdo = rsrc_words(a.dout + ((int64_t)b * S * a.H + h) * D, (S * a.H - h) * D * 2);
-    const i32x4 rqt = rsrc_words(a.qt + (int64_t)bh * D * a.Sp, (int64_t)D * a.Sp * 2);
-    const i32x4 rdot = rsrc_words(a.dot + (int64_t)bh * D * a.Sp, (int64_t)D * a.Sp * 2);
     const i32x4 rl = rsrc_words(a.lsd + (int64_t)bh * (a.Sp / 64) * 128, (a.Sp / 64) * 128 * 4);
     const __amdgpu_buffer_rsrc_t rm = make_rsrc(a.mask, a.mask ? S * S * 4 : 0);
 
@@ -616,10 +600,8 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_bf16(AttnBwdArgs a) {
         const uint32_t q0 = (uint32_t)qb * 64;
         dma_rows<D>(rq, base, q0, D, wave, lane);
         dma_rows<D>(rdo, base + TILE * 2, q0, (uint32_t)(a.H * D), wave, lane);
-        dma_cols<D>(rqt, base + 2 * TILE * 2, q0, (uint32_t)a.Sp, wave, lane);
-        dma_cols<D>(rdot, base + 3 * TILE * 2, q0, (uint32_t)a.Sp, wave, lane);
         if (wave == 0)  // the [2][64] fp32 lse/Delta block (512 B; lanes 32-63 fall outside and write zeros)
-            dma16(rl, __builtin_amdgcn_readfirstlane(base + 4 * TILE * 2),
+            dma16(rl, __builtin_amdgcn_readfirstlane(base + 2 * TILE * 2),
                   lane < 32 ? (uint32_t)(qb * 512 + lane * 16) : kOOB);
     };
 
@@ -637,9 +619,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_bf16(AttnBwdArgs a) {
         if (!active || qb < wstart) continue;  // wave-uniform
         const uint16_t* sq = smem + ((qb - qstart) & 1) * STAGE;
         const uint16_t* sdo = sq + TILE;
-        const uint16_t* sqt = sq + 2 * TILE;
-        const uint16_t* sdot = sq + 3 * TILE;
-        const float* sl = reinterpret_cast<const float*>(sq + 4 * TILE);
+        const float* sl = reinterpret_cast<const float*>(sq + 2 * TILE);
         const int64_t q0 = (int64_t)qb * 64;
 
         f32x16 sacc[2], dpacc[2];
@@ -700,24 +680,24 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_bf16(AttnBwdArgs a) {
         else if (a.causal && q0 < kw + 31) scores(std::false_type{}, std::true_type{});
         else scores(std::false_type{}, std::false_type{});
 
-        // dV^T (d x key) += dO^T . P ; dK^T += Q^T . dS ; query positions 16 (2t + kk) + 8 half .. +7
+        // dV^T (d x key) += dO^T . P ; dK^T += Q^T . dS ; dO^T, Q^T by
+        // transposed reads of the dO, Q tiles, in the accumulators' query order
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
-            const int row = 32 * dt + col;
 #pragma unroll
             for (int t = 0; t < 2; ++t)
 #pragma unroll
                 for (int kk = 0; kk < 2; ++kk) {
-                    const int chunk = 4 * t + 2 * kk + half;
-                    dvacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_cols(sdot, row, chunk), pb[t][kk],
-                                                                       dvacc[dt], 0, 0, 0);
-                    dkacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_cols(sqt, row, chunk), db[t][kk],
-                                                                       dkacc[dt], 0, 0, 0);
+                    dvacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_tr<D>(sdo, 32 * t + 16 * kk, 32 * dt, lane),
+                                                                       pb[t][kk], dvacc[dt], 0, 0, 0);
+                    dkacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_tr<D>(sq, 32 * t + 16 * kk, 32 * dt, lane),
+                                                                       db[t][kk], dkacc[dt], 0, 0, 0);
                 }
         }
     }
 
     __syncthreads();
+    static_assert(32 * (D + 4) * 4 <= 32 * (D + 8) * 2 * 2, "fp32 patch rows fit a wave's share");
     void* patch = smem + wave * 32 * (D + 8) * 2;  // 32 rows of up to D + 4 floats per wave
     if (rep == 1) {
         store_rows<D, uint16_t>(dvacc, 1.f, patch, a.dv + bhk * S * D, D, kw, S, lane);
@@ -758,8 +738,9 @@ template <int D>
 __global__ __launch_bounds__(256, 1) void attn_bwd_dq_bf16(AttnBwdArgs a) {
     constexpr int KB = 64, QB = 128, KS = D / 16, DT = D / 32;
     constexpr int TILE = 64 * D;
-    constexpr int STAGE = 3 * TILE;  // K, V [64][D], K^T [D][64]
+    constexpr int STAGE = 2 * TILE;  // K, V [64][D]
     __shared__ __attribute__((aligned(1024))) uint16_t smem[2 * STAGE];
+    static_assert(4 * 32 * (D + 8) <= 2 * STAGE, "the epilogue's bf16 patches fit in the stages");
     const uint32_t smem_byte = (uint32_t)reinterpret_cast<uintptr_t>(smem);
     const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
     const int col = lane & 31, half = lane >> 5;
@@ -794,7 +775,6 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq_bf16(AttnBwdArgs a) {
 
     const i32x4 rk = rsrc_words(a.k + bhk * S * D, S * D * 2);
     const i32x4 rv = rsrc_words(a.v + bhk * S * D, S * D * 2);
-    const i32x4 rkt = rsrc_words(a.kt + bhk * D * a.Sp, (int64_t)D * a.Sp * 2);
     const __amdgpu_buffer_rsrc_t rm = make_rsrc(a.mask, a.mask ? S * S * 4 : 0);
 
     const int nkb_all = (int)((S + KB - 1) / KB);
@@ -810,7 +790,6 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq_bf16(AttnBwdArgs a) {
         const uint32_t key0 = (uint32_t)kb * KB;
         dma_rows<D>(rk, base, key0, D, wave, lane);
         dma_rows<D>(rv, base + TILE * 2, key0, D, wave, lane);
-        dma_cols<D>(rkt, base + 2 * TILE * 2, key0, (uint32_t)a.Sp, wave, lane);
     };
 
     f32x16 dqacc[DT];
@@ -827,7 +806,6 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq_bf16(AttnBwdArgs a) {
         if (kb >= wkb) continue;
         const uint16_t* sk = smem + (kb & 1) * STAGE;
         const uint16_t* sv = sk + TILE;
-        const uint16_t* skt = sk + 2 * TILE;
 
         f32x16 sacc[2], dpacc[2];
 #pragma unroll
@@ -878,15 +856,15 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq_bf16(AttnBwdArgs a) {
         else if (key0 + KB > S || (a.causal && key0 + KB - 1 > qw)) scores(std::false_type{}, std::true_type{});
         else scores(std::false_type{}, std::false_type{});
 
-        // dQ^T (d x query) += K^T . dS^T ; key positions 16 (2t + kk) + 8 half .. +7
+        // dQ^T (d x query) += K^T . dS^T ; K^T by transposed reads of the K
+        // tile, in the accumulators' key order
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
-            const int row = 32 * dt + col;
 #pragma unroll
             for (int t = 0; t < 2; ++t)
 #pragma unroll
                 for (int kk = 0; kk < 2; ++kk)
-                    dqacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_cols(skt, row, 4 * t + 2 * kk + half),
+                    dqacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_tr<D>(sk, 32 * t + 16 * kk, 32 * dt, lane),
                                                                        db[t][kk], dqacc[dt], 0, 0, 0);
         }
     }
@@ -1096,9 +1074,6 @@ AttnBwdWs attention_bwd_ws(const mc_attn_desc& d) {
     if (attention_uses_mfma(d)) {
         const size_t Sp = (S + 63) / 64 * 64;
         w.lsd = off;  off += align256(B * H * (Sp / 64) * 128 * 4);
-        w.qt = off;   off += align256(B * H * D * Sp * 2);
-        w.dot = off;  off += align256(B * H * D * Sp * 2);
-        w.kt = off;   off += align256(B * Hkv * D * Sp * 2);
         if (H != Hkv) {
             w.dk_part = off;  off += align256(B * H * S * D * 4);
             w.dv_part = off;  off += align256(B * H * S * D * 4);
@@ -1124,9 +1099,6 @@ hipError_t launch_attention_bwd(const mc_attn_desc& d, const void* q, const void
         a.k = static_cast<const uint16_t*>(k);
         a.v = static_cast<const uint16_t*>(v);
         a.dout = static_cast<const uint16_t*>(dout);
-        a.qt = reinterpret_cast<const uint16_t*>(base + w.qt);
-        a.dot = reinterpret_cast<const uint16_t*>(base + w.dot);
-        a.kt = reinterpret_cast<const uint16_t*>(base + w.kt);
         a.mask = mask;
         a.lsd = reinterpret_cast<const float*>(base + w.lsd);
         a.dq = static_cast<uint16_t*>(dq);
@@ -1142,22 +1114,15 @@ hipError_t launch_attention_bwd(const mc_attn_desc& d, const void* q, const void
         a.scale = d.scale;
         a.scale_log2 = d.scale * kLog2e;
         const dim3 gprep((unsigned)(Sp / 64), (unsigned)(B * H));
-        const dim3 gkt((unsigned)(Sp / 64), (unsigned)(B * Hkv));
         const dim3 grid((unsigned)((int64_t)a.nblk * B * H));
         float* lsd = reinterpret_cast<float*>(base + w.lsd);
-        uint16_t* qt = reinterpret_cast<uint16_t*>(base + w.qt);
-        uint16_t* dot = reinterpret_cast<uint16_t*>(base + w.dot);
-        uint16_t* kt = reinterpret_cast<uint16_t*>(base + w.kt);
-        const uint16_t* q16 = static_cast<const uint16_t*>(q);
         const uint16_t* o16 = static_cast<const uint16_t*>(o);
         const uint16_t* do16 = static_cast<const uint16_t*>(dout);
         if (D == 64) {
-            attn_bwd_prep_bf16<64><<<gprep, 256, 0, stream>>>(q16, o16, do16, lse, H, S, Sp, lsd, qt, dot);
-            attn_vt_bf16<64><<<gkt, 256, 0, stream>>>(a.k, S, Sp, kt);
+            attn_bwd_prep_bf16<64><<<gprep, 256, 0, stream>>>(o16, do16, lse, H, S, Sp, lsd);
             attn_bwd_dkdv_bf16<64><<<grid, 256, 0, stream>>>(a);
         } else {
-            attn_bwd_prep_bf16<128><<<gprep, 256, 0, stream>>>(q16, o16, do16, lse, H, S, Sp, lsd, qt, dot);
-            attn_vt_bf16<128><<<gkt, 256, 0, stream>>>(a.k, S, Sp, kt);
+            attn_bwd_prep_bf16<128><<<gprep, 256, 0, stream>>>(o16, do16, lse, H, S, Sp, lsd);
             attn_bwd_dkdv_bf16<128><<<grid, 256, 0, stream>>>(a);
         }
         if (H != Hkv) {

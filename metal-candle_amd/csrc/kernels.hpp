@@ -69,12 +69,11 @@ AttnWs attention_fwd_ws(const mc_attn_desc& d);
 hipError_t launch_attention_fwd(const mc_attn_desc& d, const void* q, const void* k, const void* v,
                                 const float* mask, void* o, float* lse, void* ws, hipStream_t stream);
 // Workspace of mc_attention_bwd (byte offsets). MFMA path: lse * log2 e and
-// Delta per 64-query block (f32 [B, H, Sp/64, 2, 64]), Q^T and dO^T
-// (bf16 [B, H, D, Sp]), K^T (bf16 [B, Hkv, D, Sp]) and, when H > Hkv, the
-// per-query-head dK / dV partials (f32 [B, H, S, D]). Generic path: Delta
-// (f32 [B, H, S]) at lsd.
+// Delta per 64-query block (f32 [B, H, Sp/64, 2, 64], Sp = S rounded up to
+// 64) and, when H > Hkv, the per-query-head dK / dV partials (f32
+// [B, H, S, D]). Generic path: Delta (f32 [B, H, S]) at lsd.
 struct AttnBwdWs {
-    size_t lsd, qt, dot, kt, dk_part, dv_part;
+    size_t lsd, dk_part, dv_part;
     size_t total;
 };
 AttnBwdWs attention_bwd_ws(const mc_attn_desc& d);
