@@ -36,7 +36,6 @@ struct LoraFwdWs {
     size_t total;
 };
 struct LoraBwdWs {
-    size_t b_hilo;    // bf16 [2][r16][N]  B split into hi/lo
     size_t wt;        // bf16 [K][N]       W^T (dX GEMM operand; bf16 path with W)
     size_t at_ext;    // bf16 [K][rext]    A, zero padded columns (dX extension operand);
                       // fp32 path: f32 [r][K] A^T

@@ -6,10 +6,11 @@
 //   2. Hd = dropout(x.A) -> h_save (fp32 [r][T]) and s*Hd (bf16 ext operand)
 //   3. y = [x | s*Hd] . [W | B^T]^T + b                    (one MFMA GEMM)
 // Backward (W frozen; candle autograd of the same composite):
-//   1. B -> bf16 hi/lo, A -> bf16 ext operand              (one prep launch)
-//   2. G = s dY.B^T, Gd = dropout'(G) -> Gd^T fp32, Gd bf16
-//   3. W -> W^T ; dX = [dY | Gd] . [W^T | A]^T             (one MFMA GEMM)
-//   4. dA = x^T.Gd and dB = s Hd^T.dY: split-T column reductions (one
+//   1. G = s dY.B^T, Gd = dropout'(G) -> Gd^T fp32, Gd bf16 (B read as
+//      fp32, split hi/lo in registers), with A -> bf16 ext operand and
+//      W -> W^T in the same launch
+//   2. dX = [dY | Gd] . [W^T | A]^T                         (one MFMA GEMM)
+//   3. dA = x^T.Gd and dB = s Hd^T.dY: split-T column reductions (one
 //      launch) and their fixed-order split sums (one launch)
 // The fp32 path runs the same sequence with fp32 operands and FMA kernels.
 #include "common.hpp"
@@ -104,7 +105,6 @@ LoraBwdWs lora_bwd_ws(const mc_lora_desc& d) {
     LoraBwdWs w{};
     size_t off = 0;
     if (m.bf16) {
-        w.b_hilo = off; off += align256((size_t)2 * m.r16 * m.N * 2);
         w.wt = off;     off += align256((size_t)m.K * m.N * 2);
         w.at_ext = off; off += align256((size_t)m.K * m.rext * 2);
         w.gd_ext = off; off += align256((size_t)m.T * m.rext * 2);
@@ -175,29 +175,23 @@ hipError_t launch_lora_bwd(const mc_lora_desc& d, const void* x, const void* W, 
     const int64_t kbase = W ? m.N : 0;
     if (m.bf16) {
         const uint16_t* dyb = static_cast<const uint16_t*>(dY);
-        uint16_t* b_hi = reinterpret_cast<uint16_t*>(base + w.b_hilo);
-        uint16_t* b_lo = b_hi + (size_t)m.r16 * m.N;
         uint16_t* at = reinterpret_cast<uint16_t*>(base + w.at_ext);
         uint16_t* gd = reinterpret_cast<uint16_t*>(base + w.gd_ext);
         float* gdt = reinterpret_cast<float*>(base + w.gd_t);
-        {
-            // B hi / lo for G; A zero-padded for the dX extension columns
-            const PrepJob jb{B, m.N, m.r, m.N, false, need_g ? b_hi : nullptr, b_lo, m.r16, m.N};
-            const PrepJob ja{A, m.r, m.K, m.r, false, dX ? at : nullptr, nullptr, m.K, m.rext};
-            auto sc = prof::Scope(prof::kLowRank, st, 0.0, need_g ? 6.0 * m.r * m.N : 0.0);
-            MC_TRY(launch_prep_bf16(jb, ja, st));
-        }
+        uint16_t* wt = reinterpret_cast<uint16_t*>(base + w.wt);
         if (need_g) {
-            auto sc = lowrank_scope(st, m.T, m.N, m.r, 2);
-            MC_TRY(launch_rowproj_bf16(dyb, m.T, m.N, b_hi, b_lo, m.r, d.scale, mask, keep, dA ? gdt : nullptr,
-                                       dX ? gd : nullptr, m.rext, 1.0f, st));
+            // one launch: G = s dY.B^T (B read as fp32), A zero-padded to the
+            // dX extension columns, and W^T for the dX GEMM
+            const PrepJob ja{A, m.r, m.K, m.r, false, dX ? at : nullptr, nullptr, m.K, m.rext};
+            const bool tw = dX && W;
+            const double bytes = 2.0 * m.T * m.N + 4.0 * m.T * m.r + 4.0 * m.r * m.N +
+                                 (dX ? 6.0 * m.r * m.K : 0.0) + (tw ? 4.0 * m.N * m.K : 0.0);
+            auto sc = prof::Scope(prof::kLowRank, st, 2.0 * m.T * m.N * m.r, bytes);
+            MC_TRY(launch_lora_bwd_operands(dyb, m.T, m.N, B, m.r, d.scale, mask, keep, dA ? gdt : nullptr,
+                                            dX ? gd : nullptr, m.rext, ja, static_cast<const uint16_t*>(W), m.K,
+                                            tw ? wt : nullptr, st));
         }
         if (dX) {
-            uint16_t* wt = reinterpret_cast<uint16_t*>(base + w.wt);
-            if (W) {
-                auto sc = prof::Scope(prof::kLowRank, st, 0.0, 4.0 * m.N * m.K);
-                MC_TRY(launch_transpose_bf16(static_cast<const uint16_t*>(W), m.N, m.K, wt, st));
-            }
             GemmSeg s0{dyb, m.N, wt, m.N, kbase};
             GemmSeg s1{gd, m.rext, at, m.rext, m.rext};
             auto sc = gemm_scope(st, m.T, m.K, kbase, m.rext, m.r, 2);

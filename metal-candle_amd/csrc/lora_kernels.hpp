@@ -37,6 +37,16 @@ hipError_t launch_rowproj_bf16(const uint16_t* X, int64_t T, int64_t C, const ui
                                float keep, float* out_t, uint16_t* out_ext, int rext, float ext_scale,
                                hipStream_t stream);
 
+// The backward's operand pass in one launch: the row projection of dY with
+// the fp32 B [r][N] read directly (G = scale dY.B^T, masked as above, into
+// gd_t [r][T] and gd_ext [T][rext]); the bf16 A extension operand (job
+// a_ext, skipped when a_ext.hi is null); and W [N][K] -> Wt [K][N] (skipped
+// when Wt is null).
+hipError_t launch_lora_bwd_operands(const uint16_t* dY, int64_t T, int64_t N, const float* B, int r, float scale,
+                                    const uint8_t* mask, float keep, float* gd_t, uint16_t* gd_ext, int rext,
+                                    const PrepJob& a_ext, const uint16_t* W, int64_t K, uint16_t* Wt,
+                                    hipStream_t stream);
+
 // ------------------------------------------------- column reduction (split T)
 // One job: partial[s][j][c] = sum_{t in split s} Pt[j*T + t] * X[t][c] for
 // j < r16, c < C (j >= r contributes 0; r16 as for rowproj). X bf16 [T][C]
@@ -83,9 +93,6 @@ hipError_t launch_gemm_bf16(int64_t M, int64_t N, GemmSeg s0, GemmSeg s1, const 
 // length K on `cus` compute units.
 enum class GemmTile { k256x256, k256x192, k256x128, k128x128 };
 GemmTile choose_gemm_tile(int64_t M, int64_t N, int64_t K, int cus);
-// out[c][r] = in[r][c] for a bf16 rows x cols matrix (cols, rows % 8 == 0).
-hipError_t launch_transpose_bf16(const uint16_t* in, int64_t rows, int64_t cols, uint16_t* out,
-                                 hipStream_t stream);
 
 // ------------------------------------------------------------- fp32 path
 // Same contracts as above with fp32 storage and plain FMA arithmetic; used

@@ -24,6 +24,8 @@
 //  issue every load of an unrolled block before its MFMAs.
 //
 // fp32 variants (plain FMA) serve act_dtype == MC_F32.
+#include <algorithm>
+
 #include "common.hpp"
 #include "lora_kernels.hpp"
 
@@ -98,21 +100,44 @@ __global__ __launch_bounds__(256) void prep_bf16(PrepJob j0, PrepJob j1, int64_t
 // MFMAs, through buffer loads whose range check zeroes rows past T and
 // columns past C (no branches). The 4 waves' partial sums are combined in
 // wave order through LDS.
-template <int RC, int RT, int U>
-__global__ __launch_bounds__(256) void rowproj_bf16(const uint16_t* __restrict__ X, int64_t T, int64_t C,
-                                                    const uint16_t* __restrict__ Phi,
-                                                    const uint16_t* __restrict__ Plo, int r, float scale,
-                                                    const uint8_t* __restrict__ mask, float keep,
-                                                    float* __restrict__ out_t, uint16_t* __restrict__ out_ext,
-                                                    int rext, float ext_scale) {
+// Arguments of one row projection. With PF32 the parameter is read as fp32
+// P [prows][C] (rows past prows load as zeros) and split into bf16 hi + lo in
+// registers; otherwise it comes prepared as bf16 P_hi / P_lo [16 RC][C].
+struct RowprojArgs {
+    const uint16_t* X;
+    int64_t T, C;
+    const uint16_t* Phi;
+    const uint16_t* Plo;
+    const float* Pf;
+    int prows;
+    int r;
+    float scale;
+    const uint8_t* mask;
+    float keep;
+    float* out_t;
+    uint16_t* out_ext;
+    int rext;
+    float ext_scale;
+};
+
+template <int RC, int RT, int U, bool PF32>
+__device__ __forceinline__ void rowproj_body(const RowprojArgs& A, int64_t blk) {
+    const uint16_t* __restrict__ X = A.X;
+    const int64_t T = A.T, C = A.C;
+    const int r = A.r, rext = A.rext;
+    const float scale = A.scale, keep = A.keep, ext_scale = A.ext_scale;
+    const uint8_t* __restrict__ mask = A.mask;
+    float* __restrict__ out_t = A.out_t;
+    uint16_t* __restrict__ out_ext = A.out_ext;
     constexpr int ROWS = 16 * RT;
     const int lane = lane_id();
     const int wave = threadIdx.x >> 6;
-    const int64_t t0 = (int64_t)blockIdx.x * ROWS;
+    const int64_t t0 = blk * ROWS;
     const int64_t nrows = T - t0 < ROWS ? T - t0 : ROWS;
     const __amdgpu_buffer_rsrc_t rx = make_rsrc(X + t0 * C, nrows * C * 2);
-    const __amdgpu_buffer_rsrc_t rhi = make_rsrc(Phi, (int64_t)16 * RC * C * 2);
-    const __amdgpu_buffer_rsrc_t rlo = make_rsrc(Plo, (int64_t)16 * RC * C * 2);
+    const __amdgpu_buffer_rsrc_t rhi = make_rsrc(PF32 ? (const void*)A.Pf : (const void*)A.Phi,
+                                                 PF32 ? (int64_t)A.prows * C * 4 : (int64_t)16 * RC * C * 2);
+    const __amdgpu_buffer_rsrc_t rlo = make_rsrc(A.Plo, PF32 ? 0 : (int64_t)16 * RC * C * 2);
     const int row = lane & 15, grp = lane >> 4;
     const int64_t nsteps = (C + 63) / 64;
 
@@ -135,9 +160,26 @@ __global__ __launch_bounds__(256) void rowproj_bf16(const uint16_t* __restrict__
                     xv[u][rt][h] = buf_load16(rx, ok ? (uint32_t)(((int64_t)(rt * 16 + row) * C + c + 8 * h) * 2) : kOOB);
 #pragma unroll
                 for (int rc = 0; rc < RC; ++rc) {
-                    const uint32_t off = ok ? (uint32_t)(((int64_t)(rc * 16 + row) * C + c + 8 * h) * 2) : kOOB;
-                    ph[u][rc][h] = buf_load16(rhi, off);
-                    pl[u][rc][h] = buf_load16(rlo, off);
+                    if constexpr (PF32) {
+                        // 8 fp32 (two 16-byte loads) -> bf16 hi + lo
+                        const uint32_t off = ok ? (uint32_t)(((int64_t)(rc * 16 + row) * C + c + 8 * h) * 4) : kOOB;
+                        const i32x4 a = buf_load16(rhi, off), b = buf_load16(rhi, ok ? off + 16 : kOOB);
+                        float v[8], rem[8];
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            v[e] = __int_as_float(a[e]);
+                            v[4 + e] = __int_as_float(b[e]);
+                        }
+                        const bf16x8 hi = pack_bf16x8(v);
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) rem[e] = v[e] - static_cast<float>(hi[e]);
+                        ph[u][rc][h] = __builtin_bit_cast(i32x4, hi);
+                        pl[u][rc][h] = __builtin_bit_cast(i32x4, pack_bf16x8(rem));
+                    } else {
+                        const uint32_t off = ok ? (uint32_t)(((int64_t)(rc * 16 + row) * C + c + 8 * h) * 2) : kOOB;
+                        ph[u][rc][h] = buf_load16(rhi, off);
+                        pl[u][rc][h] = buf_load16(rlo, off);
+                    }
                 }
             }
         }
@@ -189,6 +231,11 @@ __global__ __launch_bounds__(256) void rowproj_bf16(const uint16_t* __restrict__
             out_ext[t * rext + j] = 0;
         }
     }
+}
+
+template <int RC, int RT, int U>
+__global__ __launch_bounds__(256) void rowproj_bf16(RowprojArgs A) {
+    rowproj_body<RC, RT, U, false>(A, blockIdx.x);
 }
 
 // ------------------------------------------------------------- colreduce
@@ -365,10 +412,10 @@ __global__ __launch_bounds__(256) void split_sum(int r, SumJob j0, SumJob j1, in
 // -------------------------------------------------------- bf16 transpose
 // 64 x 64 tiles through LDS: 16-byte row chunks in, 16-byte column chunks
 // out (the frozen W of the backward GEMM, read and written once per call).
-__global__ __launch_bounds__(256) void transpose_bf16(const uint16_t* __restrict__ in, int64_t rows, int64_t cols,
-                                                      uint16_t* __restrict__ out) {
+__device__ __forceinline__ void transpose_tile(const uint16_t* __restrict__ in, int64_t rows, int64_t cols,
+                                               uint16_t* __restrict__ out, int64_t tile_r, int64_t tile_c) {
     __shared__ uint16_t tile[64][64 + 2];
-    const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
+    const int64_t r0 = tile_r * 64, c0 = tile_c * 64;
     for (int i = threadIdx.x; i < 512; i += 256) {
         const int r = i >> 3, c = (i & 7) * 8;
         uint4 v = make_uint4(0, 0, 0, 0);
@@ -389,6 +436,28 @@ __global__ __launch_bounds__(256) void transpose_bf16(const uint16_t* __restrict
             for (int e = 0; e < 4; ++e) w[e] = (uint32_t)tile[r + 2 * e][c] | ((uint32_t)tile[r + 2 * e + 1][c] << 16);
             *reinterpret_cast<uint4*>(out + (c0 + c) * rows + r0 + r) = make_uint4(w[0], w[1], w[2], w[3]);
         }
+    }
+}
+
+// ------------------------------------------- backward operands, one launch
+// The inputs of the backward GEMM and the rank-r pass of dY, as three block
+// roles of one launch (none reads another's output):
+//   [0, nrow)             G = s dY.B^T (row projection, B read as fp32)
+//   [nrow, nrow + nprep)  A -> the bf16 extension operand of the dX GEMM
+//   [.., + ntr)           W [N][K] -> W^T [K][N] (64 x 64 tiles, tcols wide)
+template <int RC, int RT>
+__global__ __launch_bounds__(256) void lora_bwd_operands(RowprojArgs rp, int64_t nrow, PrepJob ja, int64_t nprep,
+                                                         const uint16_t* __restrict__ w, int64_t wrows, int64_t wcols,
+                                                         uint16_t* __restrict__ wt, int64_t tcols) {
+    const int64_t b = blockIdx.x;
+    if (b < nrow) {
+        rowproj_body<RC, RT, 1, true>(rp, b);
+    } else if (b < nrow + nprep) {
+        const int64_t n = ja.rows_out * ja.cols_out;
+        for (int64_t idx = (b - nrow) * 256 + threadIdx.x; idx < n; idx += nprep * 256) prep_one(ja, idx);
+    } else {
+        const int64_t t = b - nrow - nprep;
+        transpose_tile(w, wrows, wcols, wt, t / tcols, t % tcols);
     }
 }
 
@@ -454,11 +523,36 @@ hipError_t launch_rowproj_bf16(const uint16_t* X, int64_t T, int64_t C, const ui
     // P_hi / P_lo hold r16 = 16, 32, 64 or 128 rows (zero past r).
     const int rc = r <= 16 ? 1 : r <= 32 ? 2 : r <= 64 ? 4 : 8;
     const dim3 g64((unsigned)((T + 63) / 64)), g32((unsigned)((T + 31) / 32));
+    const RowprojArgs A{X, T, C, P_hi, P_lo, nullptr, 0, r, scale, mask, keep, out_t, out_ext, rext, ext_scale};
     switch (rc) {
-        case 1: rowproj_bf16<1, 4, 1><<<g64, 256, 0, stream>>>(X, T, C, P_hi, P_lo, r, scale, mask, keep, out_t, out_ext, rext, ext_scale); break;
-        case 2: rowproj_bf16<2, 4, 1><<<g64, 256, 0, stream>>>(X, T, C, P_hi, P_lo, r, scale, mask, keep, out_t, out_ext, rext, ext_scale); break;
-        case 4: rowproj_bf16<4, 4, 1><<<g64, 256, 0, stream>>>(X, T, C, P_hi, P_lo, r, scale, mask, keep, out_t, out_ext, rext, ext_scale); break;
-        default: rowproj_bf16<8, 2, 1><<<g32, 256, 0, stream>>>(X, T, C, P_hi, P_lo, r, scale, mask, keep, out_t, out_ext, rext, ext_scale); break;
+        case 1: rowproj_bf16<1, 4, 1><<<g64, 256, 0, stream>>>(A); break;
+        case 2: rowproj_bf16<2, 4, 1><<<g64, 256, 0, stream>>>(A); break;
+        case 4: rowproj_bf16<4, 4, 1><<<g64, 256, 0, stream>>>(A); break;
+        default: rowproj_bf16<8, 2, 1><<<g32, 256, 0, stream>>>(A); break;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_lora_bwd_operands(const uint16_t* dY, int64_t T, int64_t N, const float* B, int r, float scale,
+                                    const uint8_t* mask, float keep, float* gd_t, uint16_t* gd_ext, int rext,
+                                    const PrepJob& a_ext, const uint16_t* W, int64_t K, uint16_t* Wt,
+                                    hipStream_t stream) {
+    // row projection blocks as launch_rowproj_bf16 chooses them; B rows past
+    // r load as zeros
+    const int rc = r <= 16 ? 1 : r <= 32 ? 2 : r <= 64 ? 4 : 8;
+    const int rows_per_block = rc == 8 ? 32 : 64;
+    const RowprojArgs A{dY, T, N, nullptr, nullptr, B, r, r, scale, mask, keep, gd_t, gd_ext, rext, 1.0f};
+    const int64_t nrow = (T + rows_per_block - 1) / rows_per_block;
+    int64_t nprep = 0;
+    if (a_ext.hi) nprep = std::min<int64_t>((a_ext.rows_out * a_ext.cols_out + 255) / 256, 64);
+    const int64_t tcols = (K + 63) / 64, trows = (N + 63) / 64;  // W is [N][K]
+    const int64_t ntr = Wt ? tcols * trows : 0;
+    const dim3 grid((unsigned)(nrow + nprep + ntr));
+    switch (rc) {
+        case 1: lora_bwd_operands<1, 4><<<grid, 256, 0, stream>>>(A, nrow, a_ext, nprep, W, N, K, Wt, tcols); break;
+        case 2: lora_bwd_operands<2, 4><<<grid, 256, 0, stream>>>(A, nrow, a_ext, nprep, W, N, K, Wt, tcols); break;
+        case 4: lora_bwd_operands<4, 4><<<grid, 256, 0, stream>>>(A, nrow, a_ext, nprep, W, N, K, Wt, tcols); break;
+        default: lora_bwd_operands<8, 2><<<grid, 256, 0, stream>>>(A, nrow, a_ext, nprep, W, N, K, Wt, tcols); break;
     }
     return hipGetLastError();
 }
@@ -518,13 +612,6 @@ hipError_t launch_split_sum(int r, const SumJob& a, const SumJob& b, hipStream_t
     int64_t blocks = (n + 255) / 256;
     if (blocks > 4096) blocks = 4096;
     split_sum<<<dim3((unsigned)blocks), 256, 0, stream>>>(r, j0, j1, n0, n);
-    return hipGetLastError();
-}
-
-hipError_t launch_transpose_bf16(const uint16_t* in, int64_t rows, int64_t cols, uint16_t* out,
-                                 hipStream_t stream) {
-    transpose_bf16<<<dim3((unsigned)((cols + 63) / 64), (unsigned)((rows + 63) / 64)), 256, 0, stream>>>(in, rows, cols,
-                                                                                                      out);
     return hipGetLastError();
 }
 
