@@ -189,6 +189,11 @@ __device__ __forceinline__ int swz(int r, int c) {
 // not see an LDS write it cannot place, which makes it wait for every such
 // load before any LDS read; the kernel waits for these loads itself
 // (wait_vmcnt + barrier) before the stage they fill is read.
+// M0 is a register the compiler reserves, so clang notes that its clobber
+// may not be honoured. The kernels that use this helper contain no
+// compiler-generated M0 use (gfx9 DS instructions do not read it): every M0
+// write in their ISA is one of these asm blocks, each immediately followed by
+// the load that reads it.
 __device__ __forceinline__ void dma16(i32x4 rsrc, uint32_t lds_byte, uint32_t voff) {
     asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
                  :
