@@ -76,7 +76,9 @@ def test_config1_fp32(mc, dev):
 
 
 @pytest.mark.parametrize("T,K,N,r", [(128, 512, 512, 8), (32, 256, 256, 4), (4 * 32, 256, 256, 16),
-                                     (8 * 32, 256, 256, 32), (100, 40, 24, 3), (1, 8, 8, 1), (65, 72, 136, 17)])
+                                     (8 * 32, 256, 256, 32), (100, 40, 24, 3), (1, 8, 8, 1), (65, 72, 136, 17),
+                                     # ranks past 64 (eight 16-rank MFMA tiles, 32-row projection blocks)
+                                     (300, 264, 200, 100), (64, 128, 128, 128)])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_reference_shapes(mc, dev, T, K, N, r, dtype):
     c = lora_case(T * 7 + r, T, K, N, r, dtype=dtype, bias=True)
@@ -152,5 +154,8 @@ def test_partial_outputs(mc, dev):
                               need_dx=False, need_dA=False)
     only_x = mc.lora_backward(None, g(c["A"]), g(c["B"]), g(c["dy"]), 2.0, W=g(c["W"]), need_dA=False,
                               need_dB=False)
+    only_a = mc.lora_backward(g(c["x"]), g(c["A"]), g(c["B"]), g(c["dy"]), 2.0, W=g(c["W"]), need_dx=False,
+                              need_dB=False)
     assert only_b[0] is None and only_b[1] is None and torch.equal(only_b[2], full[2])
     assert torch.equal(only_x[0], full[0])
+    assert only_a[0] is None and only_a[2] is None and torch.equal(only_a[1], full[1])
