@@ -73,6 +73,14 @@ mc_status check_lora_desc(const mc_lora_desc* d) {
         MC_CHECK(d->in_features % 8 == 0 && d->out_features % 8 == 0, MC_ERR_SHAPE,
                  "LoRA bf16: in_features (%lld) and out_features (%lld) must be multiples of 8",
                  (long long)d->in_features, (long long)d->out_features);
+        // The bf16 kernels address a workgroup's block of rows (256 GEMM rows
+        // of up to max(K, N) features, 32 rank rows of T fp32 values) through
+        // buffer resources with 32-bit byte offsets.
+        MC_CHECK(d->in_features < (1 << 22) && d->out_features < (1 << 22), MC_ERR_SHAPE,
+                 "LoRA bf16: in_features (%lld) and out_features (%lld) must be below 2^22",
+                 (long long)d->in_features, (long long)d->out_features);
+        MC_CHECK(d->tokens < (1 << 24), MC_ERR_SHAPE, "LoRA bf16: tokens (%lld) must be below 2^24",
+                 (long long)d->tokens);
     }
     return MC_OK;
 }

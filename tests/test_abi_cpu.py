@@ -29,6 +29,8 @@ def _desc(mc, T=16, K=16, N=16, r=4, scale=2.0, p=0.0, dtype=1):
     ("tokens", 0, 2, "must be >= 1"),
     ("act_dtype", 7, 3, "unsupported act_dtype"),
     ("in_features", 12, 2, "multiples of 8"),
+    ("out_features", 1 << 22, 2, "must be below 2^22"),   # 32-bit buffer offsets of the bf16 kernels
+    ("tokens", 1 << 24, 2, "must be below 2^24"),
 ])
 def test_lora_desc_validation(mc, field, value, code, msg):
     L = mc._lib.lib()

@@ -159,3 +159,20 @@ def test_partial_outputs(mc, dev):
     assert only_b[0] is None and only_b[1] is None and torch.equal(only_b[2], full[2])
     assert torch.equal(only_x[0], full[0])
     assert only_a[0] is None and only_a[2] is None and torch.equal(only_a[1], full[1])
+
+
+def test_wide_dB_split_bound(mc, dev):
+    """dB over a 196608-wide dY (a vocabulary-sized output): T x N x 2 bytes
+    exceeds 2^31, so the token reduction must split into chunks whose rows
+    stay inside one buffer resource. Reference: scale * h_save @ dY in fp32
+    (torch on the GPU)."""
+    T, N, r, s = 6144, 196608, 16, 2.0
+    g = torch.Generator(device=dev).manual_seed(5)
+    dy = (torch.randn(T, N, generator=g, device=dev) * 0.01).to(torch.bfloat16)
+    h = torch.randn(r, T, generator=g, device=dev)
+    A = torch.zeros(64, r, device=dev)
+    B = torch.randn(r, N, generator=g, device=dev) * 0.02
+    _, _, dB = mc.lora_backward(None, A, B, dy, s, h_save=h, need_dx=False, need_dA=False)
+    ref = s * (h @ dy.float())
+    torch.cuda.synchronize()
+    assert rel_err(dB, ref.cpu().numpy()) <= 1e-4
