@@ -574,18 +574,19 @@ int colreduce_splits(int64_t T, int64_t C) {
 }
 
 hipError_t launch_colreduce_bf16(int64_t T, int r, const ColJob& a, const ColJob& b, hipStream_t stream) {
-    // Rank tiles are processed 32 at a time (accumulators and the LDS combine
-    // buffer are sized for two 16-row MFMA tiles); each group re-reads X.
+    // Ranks are processed in groups of up to 64 (four 16-row MFMA tiles of
+    // accumulators); each group reads X once, so r <= 64 takes one pass.
     const int r16 = r <= 16 ? 16 : r <= 32 ? 32 : r <= 64 ? 64 : 128;
-    for (int g = 0; g * 32 < r; ++g) {
-        const int rs = r - 32 * g < 32 ? r - 32 * g : 32;
+    constexpr int GS = 64;
+    for (int g = 0; g * GS < r; ++g) {
+        const int rs = r - GS * g < GS ? r - GS * g : GS;
         ColJobDev d[2];
         int nblk[2] = {0, 0};
         const ColJob* jobs[2] = {&a, &b};
         for (int i = 0; i < 2; ++i) {
             const ColJob& J = *jobs[i];
-            d[i] = ColJobDev{J.X, J.C, J.Pt ? J.Pt + (int64_t)32 * g * T : nullptr, 0,
-                             J.partial ? J.partial + (int64_t)32 * g * J.C : nullptr, (int64_t)r16 * J.C,
+            d[i] = ColJobDev{J.X, J.C, J.Pt ? J.Pt + (int64_t)GS * g * T : nullptr, 0,
+                             J.partial ? J.partial + (int64_t)GS * g * J.C : nullptr, (int64_t)r16 * J.C,
                              (int)((J.C + 127) / 128)};
             if (!J.X) continue;
             d[i].chunk = round_up((T + J.splits - 1) / J.splits, 32);
@@ -598,9 +599,12 @@ hipError_t launch_colreduce_bf16(int64_t T, int r, const ColJob& a, const ColJob
         if (rs <= 16) {
             if (ptv) colreduce_bf16<1, 2, true><<<grid, 256, 0, stream>>>(T, rs, d[0], d[1], nblk[0]);
             else colreduce_bf16<1, 2, false><<<grid, 256, 0, stream>>>(T, rs, d[0], d[1], nblk[0]);
-        } else {
+        } else if (rs <= 32) {
             if (ptv) colreduce_bf16<2, 1, true><<<grid, 256, 0, stream>>>(T, rs, d[0], d[1], nblk[0]);
             else colreduce_bf16<2, 1, false><<<grid, 256, 0, stream>>>(T, rs, d[0], d[1], nblk[0]);
+        } else {
+            if (ptv) colreduce_bf16<4, 1, true><<<grid, 256, 0, stream>>>(T, rs, d[0], d[1], nblk[0]);
+            else colreduce_bf16<4, 1, false><<<grid, 256, 0, stream>>>(T, rs, d[0], d[1], nblk[0]);
         }
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
