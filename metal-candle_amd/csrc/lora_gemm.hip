@@ -154,9 +154,14 @@ __device__ __forceinline__ void store_c(const f32x16 (&acc)[TM][TN], uint16_t* s
         }
 }
 
+// LDS elements (bf16) of one tile configuration's stage buffers.
+template <int BM, int BN, int BK, int STAGES>
+constexpr int kTileSmem = STAGES * (BM + BN) * BK;
+
+// One BM x BN output tile (tm, tn) of g: the whole k loop and the epilogue,
+// with the stage buffers at smem (kTileSmem elements, 1 KB aligned).
 template <int BM, int BN, int WM, int WN, int BK, int STAGES>
-__global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, 1)
-__attribute__((amdgpu_waves_per_eu(1, 2))) void gemm_bf16_kernel(GemmArgs g) {
+__device__ __forceinline__ void gemm_tile(const GemmArgs& g, int tm, int tn, uint16_t* smem) {
     constexpr int NWN = BN / WN;
     constexpr int NT = (BM / WM) * NWN * 64;
     constexpr int TM = WM / 32, TN = WN / 32;
@@ -167,14 +172,11 @@ __attribute__((amdgpu_waves_per_eu(1, 2))) void gemm_bf16_kernel(GemmArgs g) {
     static_assert(STAGES >= 2 && STAGES <= 5 && (STAGES - 2) * LOADS < 64 && KS % 2 == 0, "pipeline depth");
     static_assert(NT / 64 * 4096 <= STAGES * STAGE * 2, "epilogue staging fits in the stage buffers");
 
-    __shared__ __attribute__((aligned(1024))) uint16_t smem[STAGES * STAGE];
     const uint32_t smem_byte = (uint32_t)reinterpret_cast<uintptr_t>(smem);
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int wm = wave / NWN, wn = wave % NWN;
-    int tm, tn;
-    tile_of(blockIdx.x, g.tiles_m, g.tiles_n, g.group_m, tm, tn);
     const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
     const int nk0 = (int)((g.k0 + BK - 1) / BK);
     const int nk = nk0 + (int)((g.k1 + BK - 1) / BK);
@@ -302,6 +304,34 @@ __attribute__((amdgpu_waves_per_eu(1, 2))) void gemm_bf16_kernel(GemmArgs g) {
     store_c<TM, TN, WM, WN>(acc, smem, g, m0, n0, wm, wn);
 }
 
+template <int BM, int BN, int WM, int WN, int BK, int STAGES>
+__global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, 1)
+__attribute__((amdgpu_waves_per_eu(1, 2))) void gemm_bf16_kernel(GemmArgs g) {
+    __shared__ __attribute__((aligned(1024))) uint16_t smem[kTileSmem<BM, BN, BK, STAGES>];
+    int tm, tn;
+    tile_of(blockIdx.x, g.tiles_m, g.tiles_n, g.group_m, tm, tn);
+    gemm_tile<BM, BN, WM, WN, BK, STAGES>(g, tm, tn, smem);
+}
+
+// Tile pairs for N = 384 q: workgroup w computes one 256 x 256 tile of the
+// first 256 q columns (2 stages, the fastest tile per FLOP), then one
+// 256 x 128 tile of the last 128 q columns (3-stage ring). With tiles_m * q
+// workgroups every workgroup does the same work, where 256 x 256 tiles alone
+// would leave the last round of CUs partly idle (N = 1536: 384 tiles on 256
+// CUs). Both phases use 8 waves and share one LDS allocation.
+constexpr int kPairSmem = kTileSmem<256, 256, 64, 2> > kTileSmem<256, 128, 64, 3> ? kTileSmem<256, 256, 64, 2>
+                                                                                   : kTileSmem<256, 128, 64, 3>;
+__global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(1, 2))) void gemm_bf16_pair(GemmArgs g,
+                                                                                                    GemmArgs g2) {
+    __shared__ __attribute__((aligned(1024))) uint16_t smem[kPairSmem];
+    int tm, tn;
+    tile_of(blockIdx.x, g.tiles_m, g.tiles_n, g.group_m, tm, tn);
+    gemm_tile<256, 256, 128, 64, 64, 2>(g, tm, tn, smem);
+    __syncthreads();  // every wave is done with the epilogue patches
+    tile_of(blockIdx.x, g2.tiles_m, g2.tiles_n, g2.group_m, tm, tn);
+    gemm_tile<256, 128, 64, 64, 64, 3>(g2, tm, tn, smem);
+}
+
 // ------------------------------------------------------------- fp32 GEMM
 // 64 x 64 tile, 16-deep k-steps, 4 x 4 outputs per thread, sequential FMA
 // chain over k (fixed order).
@@ -379,6 +409,30 @@ hipError_t launch_cfg(int64_t M, int64_t N, GemmSeg s0, GemmSeg s1, const uint16
     return hipGetLastError();
 }
 
+// The tile-pair GEMM (gemm_bf16_pair) for N % 384 == 0: columns
+// [0, 2N/3) in 256 x 256 tiles, [2N/3, N) in 256 x 128 tiles.
+hipError_t launch_pair(int64_t M, int64_t N, GemmSeg s0, GemmSeg s1, const uint16_t* bias, uint16_t* c, int64_t ldc,
+                       hipStream_t stream, int group_m) {
+    const int64_t n1 = N / 384 * 256;
+    GemmArgs g;
+    g.M = M; g.N = n1;
+    g.a0 = s0.a; g.b0 = s0.b; g.lda0 = s0.lda; g.ldb0 = s0.ldb; g.k0 = s0.k;
+    g.a1 = s1.a; g.b1 = s1.b; g.lda1 = s1.lda; g.ldb1 = s1.ldb; g.k1 = s1.k;
+    g.bias = bias; g.c = c; g.ldc = ldc;
+    g.tiles_m = (int)((M + 255) / 256);
+    g.tiles_n = (int)(n1 / 256);
+    g.group_m = group_m;
+    GemmArgs g2 = g;  // the last N / 3 columns: B rows, bias and C columns shifted by n1
+    g2.N = N - n1;
+    g2.b0 = s0.b ? s0.b + n1 * s0.ldb : nullptr;
+    g2.b1 = s1.b ? s1.b + n1 * s1.ldb : nullptr;
+    g2.bias = bias ? bias + n1 : nullptr;
+    g2.c = c + n1;
+    g2.tiles_n = (int)((N - n1) / 128);
+    gemm_bf16_pair<<<dim3((unsigned)(g.tiles_m * g.tiles_n)), 512, 0, stream>>>(g, g2);
+    return hipGetLastError();
+}
+
 namespace {
 // Compute units of the current device (the number of workgroups one round
 // of the 1-workgroup-per-CU tiles runs at once), cached per device.
@@ -394,6 +448,12 @@ int cu_count() {
 }
 }  // namespace
 
+// Tile-pair speed in the units of choose_gemm_tile's model. Medians of
+// alternating rounds at M = 16384, N = 1536: 1099-1113 TFLOP/s against
+// 1013-1031 for 256 x 128 at K = 8960; 999-1001 against 964-965 for
+// 256 x 192 at K = 1536; 477 against 459 at K = 256.
+constexpr double kPairSpeedLongK = 1.15, kPairSpeedShortK = 0.98;
+
 GemmTile choose_gemm_tile(int64_t M, int64_t N, int64_t K, int cus) {
     // Estimated time = rounds of one-workgroup-per-CU tiles x work per tile
     // / relative per-tile throughput, measured on MI355X at the Qwen2.5
@@ -403,7 +463,9 @@ GemmTile choose_gemm_tile(int64_t M, int64_t N, int64_t K, int cus) {
     //    256 x 256 would take two rounds at 75%);
     //  - 256 x 128 with a 3-stage ring is fastest on long reductions
     //    (K = 8960: 1050 vs 1010 / 950 TFLOP/s), slower at K ~ 1.5k;
-    //  - 128 x 128 (4 waves, 3 stages) keeps small problems on every CU.
+    //  - 128 x 128 (4 waves, 3 stages) keeps small problems on every CU;
+    //  - where N % 384 == 0, the tile pair (one 256 x 256 and one 256 x 128
+    //    tile per workgroup) fills whole rounds with mostly 256 x 256 work.
     const double s128 = K >= 4096 ? 1.08 : 0.9;
     struct Cand { GemmTile t; int bm, bn; double speed; };
     const Cand cands[] = {{GemmTile::k256x256, 256, 256, 1.0},
@@ -418,6 +480,14 @@ GemmTile choose_gemm_tile(int64_t M, int64_t N, int64_t K, int cus) {
         const double t = (double)rounds * c.bm * c.bn / c.speed;
         if (t < best_t) { best_t = t; best = c.t; }
     }
+    if (N % 384 == 0) {
+        // one 256 x 256 and one 256 x 128 tile per workgroup (256 x 384 of
+        // work); speed relative to the model above, measured at N = 1536
+        const double speed = K >= 4096 ? kPairSpeedLongK : kPairSpeedShortK;
+        const int64_t wgs = ((M + 255) / 256) * (N / 384);
+        const double t = (double)((wgs + cus - 1) / cus) * 256 * 384 / speed;
+        if (t < best_t) { best_t = t; best = GemmTile::kPair; }
+    }
     return best;
 }
 
@@ -430,6 +500,8 @@ hipError_t launch_gemm_bf16(int64_t M, int64_t N, GemmSeg s0, GemmSeg s1, const 
             return launch_cfg<256, 192, 64, 96, 64, 2>(M, N, s0, s1, bias, c, ldc, stream, 4);
         case GemmTile::k256x128:  // 8 waves of 64 x 64, 3 stages (144 KB LDS)
             return launch_cfg<256, 128, 64, 64, 64, 3>(M, N, s0, s1, bias, c, ldc, stream, 4);
+        case GemmTile::kPair:     // 256 x 256 then 256 x 128 per workgroup (144 KB LDS)
+            return launch_pair(M, N, s0, s1, bias, c, ldc, stream, 4);
         default:                  // 4 waves of 64 x 64, 3 stages (96 KB LDS)
             return launch_cfg<128, 128, 64, 64, 64, 3>(M, N, s0, s1, bias, c, ldc, stream, 4);
     }

@@ -91,7 +91,7 @@ hipError_t launch_gemm_bf16(int64_t M, int64_t N, GemmSeg s0, GemmSeg s1, const 
                             int64_t ldc, hipStream_t stream);
 // Workgroup tile the bf16 GEMM uses for an M x N output with reduction
 // length K on `cus` compute units.
-enum class GemmTile { k256x256, k256x192, k256x128, k128x128 };
+enum class GemmTile { k256x256, k256x192, k256x128, k128x128, kPair };
 GemmTile choose_gemm_tile(int64_t M, int64_t N, int64_t K, int cus);
 
 // ------------------------------------------------------------- fp32 path

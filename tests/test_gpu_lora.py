@@ -106,10 +106,12 @@ def test_zero_B_gives_base(mc, dev):
                                           ("c4 q_proj", 16384, 1536, 1536, 16), ("c4 k_proj", 16384, 1536, 256, 16),
                                           ("c4 down_proj", 16384, 8960, 1536, 16),
                                           # ragged sizes on each GEMM workgroup tile (256x256, 256x192, 128x128
-                                          # are chosen by tile count; rows / columns past M, N are masked)
+                                          # and the 256x256 + 256x128 tile pair for N % 384 == 0 are chosen by
+                                          # tile count; rows / columns past M, N are masked)
                                           ("ragged 256x192 fwd, 256x256 dX", 16400, 1544, 9000, 16),
                                           ("ragged 256x256", 16400, 1544, 1544, 32),
-                                          ("ragged 256x192", 16300, 1536, 1536, 16),
+                                          ("ragged tile pair", 16300, 1536, 1536, 16),
+                                          ("ragged 256x192", 16300, 1536, 1344, 16),
                                           ("ragged 128x128", 4000, 1000, 264, 8)])
 def test_config_projections_bf16(mc, dev, name, T, K, N, r):
     c = lora_case(zlib.crc32(name.encode()), T, K, N, r)
