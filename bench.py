@@ -47,12 +47,13 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
-# HBM bytes per gemm_bf16_kernel launch (average over a step's launches),
+# HBM bytes per base-GEMM launch (gemm_bf16_kernel / gemm_bf16_pair, average
+# over a step's launches),
 # measured with two rocprofv3 --pmc passes (FETCH_SIZE, then WRITE_SIZE)
 # scaled by the same counters on a 256 MiB copy (--copy-calibration); the
-# summary and commands are in profiles/gemm_bf16_kernel_c4_hbm_traffic.md.
+# summary and commands are in profiles/gemm_bf16_c4_hbm_traffic.md.
 # Re-measured whenever the GEMM's tiling changes; None for unmeasured configs.
-GEMM_TRAFFIC_BYTES = {"c4": 515.5e6}
+GEMM_TRAFFIC_BYTES = {"c4": 473.0e6}
 BF16_PEAK_TFLOPS = 2500.0
 FP32_PEAK_TFLOPS = 157.3
 
@@ -453,7 +454,7 @@ def main():
         "config": {"workload": c["workload"], "config": args.config, "tokens": layer.T, "rank": c["rank"],
                    "alpha": c["alpha"], "dropout": c["dropout"]},
         "roofline": {
-            "kernel": "gemm_bf16_kernel (base GEMMs x.W^T and dY.W with the rank-r columns folded in)",
+            "kernel": "gemm_bf16_kernel / gemm_bf16_pair (base GEMMs x.W^T and dY.W with the rank-r columns folded in)",
             "bound": "mfma",
             "achieved": achieved,
             "peak": BF16_PEAK_TFLOPS,
