@@ -47,7 +47,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
-# HBM bytes per base-GEMM launch (gemm_bf16_kernel / gemm_bf16_pair, average
+# HBM bytes per base-GEMM launch (gemm_bf16_kernel / gemm_bf16_split, average
 # over a step's launches),
 # measured with two rocprofv3 --pmc passes (FETCH_SIZE, then WRITE_SIZE)
 # scaled by the same counters on a 256 MiB copy (--copy-calibration); the
@@ -454,7 +454,7 @@ def main():
         "config": {"workload": c["workload"], "config": args.config, "tokens": layer.T, "rank": c["rank"],
                    "alpha": c["alpha"], "dropout": c["dropout"]},
         "roofline": {
-            "kernel": "gemm_bf16_kernel / gemm_bf16_pair (base GEMMs x.W^T and dY.W with the rank-r columns folded in)",
+            "kernel": "gemm_bf16_kernel / gemm_bf16_split (base GEMMs x.W^T and dY.W with the rank-r columns folded in)",
             "bound": "mfma",
             "achieved": achieved,
             "peak": BF16_PEAK_TFLOPS,

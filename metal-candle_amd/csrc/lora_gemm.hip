@@ -13,10 +13,12 @@
 //
 // bf16 kernel: a workgroup computes a BM x BN tile with (BM/WM) x (BN/WN)
 // waves, each a WM x WN block of MFMA 32x32x16 bf16 tiles with fp32
-// accumulators. The tile is chosen per shape (choose_gemm_tile): 256 x 256
-// or 256 x 192 with 8 waves and one workgroup per CU for the large layer
-// products, 128 x 128 with 4 waves where there are too few large tiles to
-// fill the 256 CUs.
+// accumulators. The tiles are chosen per shape (choose_gemm_plan): 256 x 256,
+// 256 x 192 or 256 x 128 with 8 waves and one workgroup per CU for the
+// large layer products, 128 x 128 with 4 waves where there are too few large
+// tiles to fill the 256 CUs; or 256 x 256 tiles over most columns and a
+// narrower shape over the rest in one launch (gemm_bf16_split), so that the
+// widest tile fills whole rounds of CUs.
 //  - Operands go straight from HBM/L2 into LDS with buffer_load ... lds
 //    (no VGPR staging, no ds_write), bounds handled by the buffer descriptor
 //    (out-of-range chunks load as zeros).
@@ -30,6 +32,7 @@
 //  - The epilogue goes through a per-wave LDS patch so C is written with
 //    16-byte stores and the bias is added on the way.
 #include <atomic>
+#include <cmath>
 
 #include "common.hpp"
 #include "lora_kernels.hpp"
@@ -313,24 +316,27 @@ __attribute__((amdgpu_waves_per_eu(1, 2))) void gemm_bf16_kernel(GemmArgs g) {
     gemm_tile<BM, BN, WM, WN, BK, STAGES>(g, tm, tn, smem);
 }
 
-// Tile pairs for N = 384 q: workgroup w computes one 256 x 256 tile of the
-// first 256 q columns (2 stages, the fastest tile per FLOP), then one
-// 256 x 128 tile of the last 128 q columns (3-stage ring). With tiles_m * q
-// workgroups every workgroup does the same work, where 256 x 256 tiles alone
-// would leave the last round of CUs partly idle (N = 1536: 384 tiles on 256
-// CUs). Both phases use 8 waves and share one LDS allocation.
-constexpr int kPairSmem = kTileSmem<256, 256, 64, 2> > kTileSmem<256, 128, 64, 3> ? kTileSmem<256, 256, 64, 2>
-                                                                                   : kTileSmem<256, 128, 64, 3>;
-__global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(1, 2))) void gemm_bf16_pair(GemmArgs g,
-                                                                                                    GemmArgs g2) {
-    __shared__ __attribute__((aligned(1024))) uint16_t smem[kPairSmem];
+// Two tile shapes in one launch: workgroups [0, wgs1) compute g1's tiles
+// (columns [0, n1) of the output), the rest g2's tiles (columns [n1, N)).
+// Workgroups are dispatched in id order, so the second shape fills the CUs
+// the first shape's last round leaves idle. Both shapes use 8 waves.
+template <int BM1, int BN1, int WM1, int WN1, int S1, int BM2, int BN2, int WM2, int WN2, int S2>
+__global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(1, 2))) void gemm_bf16_split(GemmArgs g1,
+                                                                                                     GemmArgs g2,
+                                                                                                     int wgs1) {
+    static_assert((BM1 / WM1) * (BN1 / WN1) == 8 && (BM2 / WM2) * (BN2 / WN2) == 8, "8 waves");
+    constexpr int SM1 = kTileSmem<BM1, BN1, 64, S1>, SM2 = kTileSmem<BM2, BN2, 64, S2>;
+    __shared__ __attribute__((aligned(1024))) uint16_t smem[SM1 > SM2 ? SM1 : SM2];
     int tm, tn;
-    tile_of(blockIdx.x, g.tiles_m, g.tiles_n, g.group_m, tm, tn);
-    gemm_tile<256, 256, 128, 64, 64, 2>(g, tm, tn, smem);
-    __syncthreads();  // every wave is done with the epilogue patches
-    tile_of(blockIdx.x, g2.tiles_m, g2.tiles_n, g2.group_m, tm, tn);
-    gemm_tile<256, 128, 64, 64, 64, 3>(g2, tm, tn, smem);
+    if ((int)blockIdx.x < wgs1) {
+        tile_of(blockIdx.x, g1.tiles_m, g1.tiles_n, g1.group_m, tm, tn);
+        gemm_tile<BM1, BN1, WM1, WN1, 64, S1>(g1, tm, tn, smem);
+    } else {
+        tile_of((int)blockIdx.x - wgs1, g2.tiles_m, g2.tiles_n, g2.group_m, tm, tn);
+        gemm_tile<BM2, BN2, WM2, WN2, 64, S2>(g2, tm, tn, smem);
+    }
 }
+
 
 // ------------------------------------------------------------- fp32 GEMM
 // 64 x 64 tile, 16-deep k-steps, 4 x 4 outputs per thread, sequential FMA
@@ -409,27 +415,29 @@ hipError_t launch_cfg(int64_t M, int64_t N, GemmSeg s0, GemmSeg s1, const uint16
     return hipGetLastError();
 }
 
-// The tile-pair GEMM (gemm_bf16_pair) for N % 384 == 0: columns
-// [0, 2N/3) in 256 x 256 tiles, [2N/3, N) in 256 x 128 tiles.
-hipError_t launch_pair(int64_t M, int64_t N, GemmSeg s0, GemmSeg s1, const uint16_t* bias, uint16_t* c, int64_t ldc,
-                       hipStream_t stream, int group_m) {
-    const int64_t n1 = N / 384 * 256;
+
+// GEMM args of columns [n0, n0 + n) of the output with BN-wide tiles.
+static GemmArgs col_range(int64_t M, int64_t n0, int64_t n, GemmSeg s0, GemmSeg s1, const uint16_t* bias,
+                          uint16_t* c, int64_t ldc, int bm, int bn, int group_m) {
     GemmArgs g;
-    g.M = M; g.N = n1;
-    g.a0 = s0.a; g.b0 = s0.b; g.lda0 = s0.lda; g.ldb0 = s0.ldb; g.k0 = s0.k;
-    g.a1 = s1.a; g.b1 = s1.b; g.lda1 = s1.lda; g.ldb1 = s1.ldb; g.k1 = s1.k;
-    g.bias = bias; g.c = c; g.ldc = ldc;
-    g.tiles_m = (int)((M + 255) / 256);
-    g.tiles_n = (int)(n1 / 256);
+    g.M = M; g.N = n;
+    g.a0 = s0.a; g.b0 = s0.b ? s0.b + n0 * s0.ldb : nullptr; g.lda0 = s0.lda; g.ldb0 = s0.ldb; g.k0 = s0.k;
+    g.a1 = s1.a; g.b1 = s1.b ? s1.b + n0 * s1.ldb : nullptr; g.lda1 = s1.lda; g.ldb1 = s1.ldb; g.k1 = s1.k;
+    g.bias = bias ? bias + n0 : nullptr; g.c = c + n0; g.ldc = ldc;
+    g.tiles_m = (int)((M + bm - 1) / bm);
+    g.tiles_n = (int)((n + bn - 1) / bn);
     g.group_m = group_m;
-    GemmArgs g2 = g;  // the last N / 3 columns: B rows, bias and C columns shifted by n1
-    g2.N = N - n1;
-    g2.b0 = s0.b ? s0.b + n1 * s0.ldb : nullptr;
-    g2.b1 = s1.b ? s1.b + n1 * s1.ldb : nullptr;
-    g2.bias = bias ? bias + n1 : nullptr;
-    g2.c = c + n1;
-    g2.tiles_n = (int)((N - n1) / 128);
-    gemm_bf16_pair<<<dim3((unsigned)(g.tiles_m * g.tiles_n)), 512, 0, stream>>>(g, g2);
+    return g;
+}
+
+template <int BM1, int BN1, int WM1, int WN1, int S1, int BM2, int BN2, int WM2, int WN2, int S2>
+hipError_t launch_split(int64_t M, int64_t N, int64_t n1, GemmSeg s0, GemmSeg s1, const uint16_t* bias, uint16_t* c,
+                        int64_t ldc, hipStream_t stream, int group_m) {
+    const GemmArgs g1 = col_range(M, 0, n1, s0, s1, bias, c, ldc, BM1, BN1, group_m);
+    const GemmArgs g2 = col_range(M, n1, N - n1, s0, s1, bias, c, ldc, BM2, BN2, group_m);
+    const int wgs1 = g1.tiles_m * g1.tiles_n;
+    gemm_bf16_split<BM1, BN1, WM1, WN1, S1, BM2, BN2, WM2, WN2, S2>
+        <<<dim3((unsigned)(wgs1 + g2.tiles_m * g2.tiles_n)), 512, 0, stream>>>(g1, g2, wgs1);
     return hipGetLastError();
 }
 
@@ -446,62 +454,90 @@ int cu_count() {
     cache[dev].store(v, std::memory_order_relaxed);
     return v;
 }
+
+// Per-tile speed relative to 256 x 256 (the fastest per FLOP), from
+// full-round medians on MI355X at the Qwen2.5 layer shapes: 256 x 192 runs
+// at 0.85-0.89 of its rate; the 256 x 128 ring at 0.81 (K ~ 1.5k), 0.85
+// (K ~ 3.5k) and 0.88 (K = 8960); 128 x 128 (4 waves) serves small grids.
+double tile_speed(GemmTile t, int64_t K) {
+    switch (t) {
+        case GemmTile::k256x256: return 1.0;
+        case GemmTile::k256x192: return K >= 4096 ? 0.85 : 0.87;
+        case GemmTile::k256x128: return K >= 6144 ? 0.88 : K >= 2048 ? 0.85 : 0.81;
+        default: return 0.8;
+    }
+}
+
+void tile_dims(GemmTile t, int& bm, int& bn) {
+    bm = t == GemmTile::k128x128 ? 128 : 256;
+    bn = t == GemmTile::k256x256 ? 256 : t == GemmTile::k256x192 ? 192 : 128;
+}
+
+// Estimated time of n1 tiles of duration t1 followed by n2 tiles of
+// duration t2, dispatched in order onto `cus` CUs one workgroup each: whole
+// rounds of the first shape, then the rest of the work spread over every CU
+// in steps of t2 (a started first-shape tile still takes t1).
+double list_time(int64_t n1, double t1, int64_t n2, double t2, int cus) {
+    const int64_t r1 = n1 / cus, q1 = n1 % cus;
+    double t = (double)r1 * t1;
+    if (q1 == 0 && n2 == 0) return t;
+    if (n2 == 0) return t + t1;
+    const double rest = (double)q1 * t1 + (double)n2 * t2;
+    double tail = std::ceil(rest / ((double)cus * t2)) * t2;
+    if (q1 > 0 && tail < t1) tail = t1;
+    return t + tail;
+}
+
 }  // namespace
 
-// Tile-pair speed in the units of choose_gemm_tile's model. Medians of
-// alternating rounds at M = 16384, N = 1536: 1099-1113 TFLOP/s against
-// 1013-1031 for 256 x 128 at K = 8960; 999-1001 against 964-965 for
-// 256 x 192 at K = 1536; 477 against 459 at K = 256.
-constexpr double kPairSpeedLongK = 1.15, kPairSpeedShortK = 0.98;
-
-GemmTile choose_gemm_tile(int64_t M, int64_t N, int64_t K, int cus) {
-    // Estimated time = rounds of one-workgroup-per-CU tiles x work per tile
-    // / relative per-tile throughput, measured on MI355X at the Qwen2.5
-    // layer shapes:
-    //  - 256 x 256 (8 waves, 2 stages) is the fastest per FLOP at K ~ 1.5k;
-    //  - 256 x 192 fills two rounds exactly where N = 1536 (384 tiles of
-    //    256 x 256 would take two rounds at 75%);
-    //  - 256 x 128 with a 3-stage ring is fastest on long reductions
-    //    (K = 8960: 1050 vs 1010 / 950 TFLOP/s), slower at K ~ 1.5k;
-    //  - 128 x 128 (4 waves, 3 stages) keeps small problems on every CU;
-    //  - where N % 384 == 0, the tile pair (one 256 x 256 and one 256 x 128
-    //    tile per workgroup) fills whole rounds with mostly 256 x 256 work.
-    const double s128 = K >= 4096 ? 1.08 : 0.9;
-    struct Cand { GemmTile t; int bm, bn; double speed; };
-    const Cand cands[] = {{GemmTile::k256x256, 256, 256, 1.0},
-                          {GemmTile::k256x192, 256, 192, 0.95},
-                          {GemmTile::k256x128, 256, 128, s128},
-                          {GemmTile::k128x128, 128, 128, 0.8}};
-    GemmTile best = GemmTile::k128x128;
+GemmPlan choose_gemm_plan(int64_t M, int64_t N, int64_t K, int cus) {
+    // One tile shape over all of N, or 256 x 256 tiles over the first n1 =
+    // 256 j columns and a narrower shape over the rest, whichever list_time
+    // estimates fastest. The split lets the wide tile fill whole rounds
+    // (e.g. N = 1536 at M = 16384: 256 tiles of 256 x 256 + 256 of 256 x 128
+    // instead of 384 tiles of 256 x 256 on 256 CUs).
+    const GemmTile singles[] = {GemmTile::k256x256, GemmTile::k256x192, GemmTile::k256x128, GemmTile::k128x128};
+    GemmPlan best{GemmTile::k128x128, GemmTile::k128x128, N};
     double best_t = 1e300;
-    for (const Cand& c : cands) {
-        const int64_t tiles = ((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn);
-        const int64_t rounds = (tiles + cus - 1) / cus;
-        const double t = (double)rounds * c.bm * c.bn / c.speed;
-        if (t < best_t) { best_t = t; best = c.t; }
+    for (GemmTile t : singles) {
+        int bm, bn;
+        tile_dims(t, bm, bn);
+        const int64_t tiles = ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
+        const double e = list_time(tiles, (double)bm * bn / tile_speed(t, K), 0, 0.0, cus);
+        if (e < best_t) { best_t = e; best = GemmPlan{t, t, N}; }
     }
-    if (N % 384 == 0) {
-        // one 256 x 256 and one 256 x 128 tile per workgroup (256 x 384 of
-        // work); speed relative to the model above, measured at N = 1536
-        const double speed = K >= 4096 ? kPairSpeedLongK : kPairSpeedShortK;
-        const int64_t wgs = ((M + 255) / 256) * (N / 384);
-        const double t = (double)((wgs + cus - 1) / cus) * 256 * 384 / speed;
-        if (t < best_t) { best_t = t; best = GemmTile::kPair; }
+    const int64_t tm = (M + 255) / 256;
+    const double t1 = 65536.0;
+    const int64_t jmax = N / 256;
+    for (int64_t j = jmax; j >= 1 && j >= jmax - 8; --j) {
+        const int64_t n1 = 256 * j;
+        if (n1 >= N) continue;
+        for (GemmTile t : {GemmTile::k256x192, GemmTile::k256x128}) {
+            int bm, bn;
+            tile_dims(t, bm, bn);
+            const int64_t n2 = tm * ((N - n1 + bn - 1) / bn);
+            const double e = list_time(tm * j, t1, n2, (double)bm * bn / tile_speed(t, K), cus);
+            if (e < best_t) { best_t = e; best = GemmPlan{GemmTile::k256x256, t, n1}; }
+        }
     }
     return best;
 }
 
 hipError_t launch_gemm_bf16(int64_t M, int64_t N, GemmSeg s0, GemmSeg s1, const uint16_t* bias, uint16_t* c,
                             int64_t ldc, hipStream_t stream) {
-    switch (choose_gemm_tile(M, N, s0.k + s1.k, cu_count())) {
+    const GemmPlan p = choose_gemm_plan(M, N, s0.k + s1.k, cu_count());
+    if (p.n1 < N) {  // 256 x 256 over [0, n1), the tail shape over [n1, N)
+        if (p.tail == GemmTile::k256x192)
+            return launch_split<256, 256, 128, 64, 2, 256, 192, 64, 96, 2>(M, N, p.n1, s0, s1, bias, c, ldc, stream, 4);
+        return launch_split<256, 256, 128, 64, 2, 256, 128, 64, 64, 3>(M, N, p.n1, s0, s1, bias, c, ldc, stream, 4);
+    }
+    switch (p.main) {
         case GemmTile::k256x256:  // 8 waves of 128 x 64, k-steps of 64, 2 stages (128 KB LDS)
             return launch_cfg<256, 256, 128, 64, 64, 2>(M, N, s0, s1, bias, c, ldc, stream, 4);
         case GemmTile::k256x192:  // 8 waves of 64 x 96, 2 stages (112 KB LDS)
             return launch_cfg<256, 192, 64, 96, 64, 2>(M, N, s0, s1, bias, c, ldc, stream, 4);
         case GemmTile::k256x128:  // 8 waves of 64 x 64, 3 stages (144 KB LDS)
             return launch_cfg<256, 128, 64, 64, 64, 3>(M, N, s0, s1, bias, c, ldc, stream, 4);
-        case GemmTile::kPair:     // 256 x 256 then 256 x 128 per workgroup (144 KB LDS)
-            return launch_pair(M, N, s0, s1, bias, c, ldc, stream, 4);
         default:                  // 4 waves of 64 x 64, 3 stages (96 KB LDS)
             return launch_cfg<128, 128, 64, 64, 64, 3>(M, N, s0, s1, bias, c, ldc, stream, 4);
     }

@@ -89,10 +89,15 @@ struct GemmSeg {
 };
 hipError_t launch_gemm_bf16(int64_t M, int64_t N, GemmSeg s0, GemmSeg s1, const uint16_t* bias, uint16_t* c,
                             int64_t ldc, hipStream_t stream);
-// Workgroup tile the bf16 GEMM uses for an M x N output with reduction
-// length K on `cus` compute units.
-enum class GemmTile { k256x256, k256x192, k256x128, k128x128, kPair };
-GemmTile choose_gemm_tile(int64_t M, int64_t N, int64_t K, int cus);
+// Workgroup tiles of the bf16 GEMM for an M x N output with reduction length
+// K on `cus` compute units: `main` over columns [0, n1), `tail` over [n1, N)
+// (n1 == N: one tile shape; otherwise main is 256 x 256).
+enum class GemmTile { k256x256, k256x192, k256x128, k128x128 };
+struct GemmPlan {
+    GemmTile main, tail;
+    int64_t n1;
+};
+GemmPlan choose_gemm_plan(int64_t M, int64_t N, int64_t K, int cus);
 
 // ------------------------------------------------------------- fp32 path
 // Same contracts as above with fp32 storage and plain FMA arithmetic; used

@@ -105,13 +105,16 @@ def test_zero_B_gives_base(mc, dev):
 @pytest.mark.parametrize("name,T,K,N,r", [("c3 q_proj", 8192, 896, 896, 8), ("c3 v_proj", 8192, 896, 128, 8),
                                           ("c4 q_proj", 16384, 1536, 1536, 16), ("c4 k_proj", 16384, 1536, 256, 16),
                                           ("c4 down_proj", 16384, 8960, 1536, 16),
-                                          # ragged sizes on each GEMM workgroup tile (256x256, 256x192, 128x128
-                                          # and the 256x256 + 256x128 tile pair for N % 384 == 0 are chosen by
-                                          # tile count; rows / columns past M, N are masked)
-                                          ("ragged 256x192 fwd, 256x256 dX", 16400, 1544, 9000, 16),
+                                          # ragged sizes on each GEMM plan (one tile shape of 256x256, 256x192,
+                                          # 256x128 or 128x128, or 256x256 tiles over most columns and a
+                                          # 256x128 / 256x192 tail, chosen by shape; rows / columns past M, N
+                                          # are masked)
+                                          ("ragged split 256x256 + 256x128 fwd, 256x256 dX", 16400, 1544, 9000, 16),
                                           ("ragged 256x256", 16400, 1544, 1544, 32),
-                                          ("ragged tile pair", 16300, 1536, 1536, 16),
-                                          ("ragged 256x192", 16300, 1536, 1344, 16),
+                                          ("ragged split, 256x128 tail", 16300, 1536, 1536, 16),
+                                          ("ragged split, 320-column tail", 16300, 1536, 1344, 16),
+                                          ("ragged 256x192", 16300, 1536, 768, 16),
+                                          ("ragged split, 256x192 tail", 16300, 1536, 8960, 16),
                                           ("ragged 128x128", 4000, 1000, 264, 8)])
 def test_config_projections_bf16(mc, dev, name, T, K, N, r):
     c = lora_case(zlib.crc32(name.encode()), T, K, N, r)
