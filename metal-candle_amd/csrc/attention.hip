@@ -49,6 +49,9 @@ constexpr float kNegInf = -__builtin_inff();
 // positions 0-3, 4-7, 8-11, 12-15 hold keys 0-3, 8-11, 4-7, 12-15 (bits 2 and
 // 3 swapped; the map is its own inverse). This is the order in which a lane
 // half of the S^T accumulator holds its keys (rows 8 (j/4) + 4 (l/32) + j%4).
+// Instruction classes of __builtin_amdgcn_sched_group_barrier.
+constexpr int kSchedMfma = 0x008, kSchedDsRead = 0x100;
+
 __device__ __forceinline__ int perm16(int p) { return (p & 3) | ((p & 4) << 1) | ((p & 8) >> 1); }
 
 // ------------------------------------------------------------ V^T prepass
@@ -421,6 +424,23 @@ struct AttnBwdArgs {
     float scale, scale_log2;
 };
 
+// Position of 16-byte chunk c of row r in the backward's [64][D] LDS tiles.
+// Two read patterns must be bank-conflict free (64 banks x 4 B): row reads
+// (frag_rows: 16 consecutive rows of one chunk per 16 lanes) need the row's
+// low bits to permute the chunk; the transposed reads (frag_tr: 4
+// consecutive rows x 4 consecutive chunks per 32 lanes) need the row's two
+// lowest bits on the chunk's bits 2-3. Swapping the row's bit pairs 0-1 and
+// 2-3 into the XOR mask serves both (D = 128: 16 chunks per 256-byte row;
+// D = 64: 8 chunks, two rows per 256 bytes). The row-major swizzle of the
+// forward (swz) put two (row, chunk) pairs of each transposed read on one
+// bank group.
+template <int D>
+__device__ __forceinline__ int aswz(int r, int c) {
+    static_assert(D == 64 || D == 128, "head dims with an MFMA backward");
+    if constexpr (D == 128) return c ^ (((r & 3) << 2) | ((r >> 2) & 3));
+    else return c ^ ((((r >> 1) & 1) << 2) | ((r >> 2) & 3));
+}
+
 // [64 rows][D] tile into the swizzled LDS layout from rows row0 .. row0+63 of
 // a buffer with row stride ld (elements); rows past the buffer load zeros.
 template <int D>
@@ -431,7 +451,7 @@ __device__ __forceinline__ void dma_rows(i32x4 r, uint32_t lds_byte, uint32_t ro
     for (int j = 0; j < LOADS; ++j) {
         const int blk = wave * LOADS + j;
         const int row = blk * RPI + lane / CPR;
-        const uint32_t chunk = (uint32_t)swz<D>(row, lane % CPR);
+        const uint32_t chunk = (uint32_t)aswz<D>(row, lane % CPR);
         const uint32_t off = ((row0 + (uint32_t)row) * ld + 8u * chunk) * 2u;
         dma16(r, __builtin_amdgcn_readfirstlane(lds_byte + (uint32_t)blk * 1024u), off);
     }
@@ -439,7 +459,7 @@ __device__ __forceinline__ void dma_rows(i32x4 r, uint32_t lds_byte, uint32_t ro
 
 template <int D>
 __device__ __forceinline__ bf16x8 frag_rows(const uint16_t* t, int row, int c) {
-    return *reinterpret_cast<const bf16x8*>(&t[row * D + 8 * swz<D>(row, c)]);
+    return *reinterpret_cast<const bf16x8*>(&t[row * D + 8 * aswz<D>(row, c)]);
 }
 
 // ds_read_b64_tr_b16: within each 16-lane group, lane i receives element i % 4
@@ -464,9 +484,37 @@ __device__ __forceinline__ bf16x8 frag_tr(const uint16_t* t, int kbase, int dcol
     const int ra = kbase + 4 * (g >> 1) + (i >> 2), rb = ra + 8;
     const int c = (dcol >> 3) + 2 * (g & 1) + ((i & 3) >> 1);
     const int sub = 4 * (i & 1);
-    const s16x4 lo = ds_read_tr16(&t[ra * D + 8 * swz<D>(ra, c) + sub]);
-    const s16x4 hi = ds_read_tr16(&t[rb * D + 8 * swz<D>(rb, c) + sub]);
+    const s16x4 lo = ds_read_tr16(&t[ra * D + 8 * aswz<D>(ra, c) + sub]);
+    const s16x4 hi = ds_read_tr16(&t[rb * D + 8 * aswz<D>(rb, c) + sub]);
     const s16x4 v8[2] = {lo, hi};
+    return __builtin_bit_cast(bf16x8, v8);
+}
+
+// The same fragments from precomputed per-lane byte offsets. Inside a tile
+// the swizzle depends only on a row's low four bits, so for rows 16 k + r
+// (frag_tr: kbase = 16 k) or 32 k + r (frag_rows) the lane's offset is fixed
+// and the tile row enters as a constant that folds into the LDS instruction's
+// offset field. Precomputing the few distinct offsets keeps the backward
+// kernels from holding one hoisted address per fragment read.
+template <int D>
+__device__ __forceinline__ uint32_t rows_off(int lane, int c) {  // frag_rows(t, 32 k + lane % 32, c)
+    const int col = lane & 31;
+    return (uint32_t)((col * D + 8 * aswz<D>(col, c)) * 2);
+}
+template <int D>
+__device__ __forceinline__ uint32_t tr_off(int lane, int dcol, int h) {  // frag_tr(t, 16 k, dcol), read h
+    const int i = lane & 15, g = lane >> 4;
+    const int r = 4 * (g >> 1) + (i >> 2) + 8 * h;
+    const int c = (dcol >> 3) + 2 * (g & 1) + ((i & 3) >> 1);
+    return (uint32_t)((r * D + 8 * aswz<D>(r, c) + 4 * (i & 1)) * 2);
+}
+__device__ __forceinline__ bf16x8 frag_at(const uint16_t* t, uint32_t byte_off) {
+    return *reinterpret_cast<const bf16x8*>(reinterpret_cast<const char*>(t) + byte_off);
+}
+__device__ __forceinline__ bf16x8 frag_tr_at(const uint16_t* t, uint32_t off_lo, uint32_t off_hi) {
+    const char* b = reinterpret_cast<const char*>(t);
+    const s16x4 v8[2] = {ds_read_tr16(reinterpret_cast<const uint16_t*>(b + off_lo)),
+                         ds_read_tr16(reinterpret_cast<const uint16_t*>(b + off_hi))};
     return __builtin_bit_cast(bf16x8, v8);
 }
 
@@ -554,10 +602,11 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_bf16(AttnBwdArgs a) {
     constexpr int KS = D / 16, DT = D / 32;
     constexpr int TILE = 64 * D;                 // one [64][D] or [D][64] tile
     constexpr int STAGE = 2 * TILE + 512;        // Q, dO, lse/Delta (1 KB)
+    constexpr int KV = 2 * 128 * D;              // the workgroup's K and V rows, [128][D] each, after the stages
     // the epilogue reuses the stages as per-wave patches of 32 rows x (D + 8)
     // uint16 x 2 (fp32 partials with 16-byte row padding); allocate the larger
     constexpr int PATCH = 4 * 32 * (D + 8) * 2;
-    constexpr int SMEM = 2 * STAGE > PATCH ? 2 * STAGE : PATCH;
+    constexpr int SMEM = 2 * STAGE + KV > PATCH ? 2 * STAGE + KV : PATCH;
     __shared__ __attribute__((aligned(1024))) uint16_t smem[SMEM];
     const uint32_t smem_byte = (uint32_t)reinterpret_cast<uintptr_t>(smem);
     const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
@@ -572,16 +621,30 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_bf16(AttnBwdArgs a) {
     const int64_t key0 = (int64_t)kb * 128;
     const int64_t kw = key0 + 32 * wave;         // first key of this wave
     const int64_t my_key = kw + col;
-
-    // K and V fragments (B operands of S = Q.K^T and dP = dO.V^T): key my_key, dims 16 s + 8 half .. +7
-    const __amdgpu_buffer_rsrc_t rk = make_rsrc(a.k + bhk * S * D, S * D * 2);
-    const __amdgpu_buffer_rsrc_t rv = make_rsrc(a.v + bhk * S * D, S * D * 2);
-    bf16x8 kf[KS], vf[KS];
+    uint32_t roff[KS], troff[DT][2];
 #pragma unroll
-    for (int s = 0; s < KS; ++s) {
-        const uint32_t off = my_key < S ? (uint32_t)((my_key * D + 16 * s + 8 * half) * 2) : kOOB;
-        kf[s] = __builtin_bit_cast(bf16x8, buf_load16(rk, off));
-        vf[s] = __builtin_bit_cast(bf16x8, buf_load16(rv, off));
+    for (int s = 0; s < KS; ++s) roff[s] = rows_off<D>(lane, 2 * s + half);
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) troff[dt][h] = tr_off<D>(lane, 32 * dt, h);
+
+    // K and V rows of the workgroup's 128 keys (B operands of S = Q.K^T and
+    // dP = dO.V^T) stay in LDS for the whole query loop; held as register
+    // fragments they pushed the kernel past 256 VGPRs into AGPR spills.
+    // Keys past S load as zeros.
+    const i32x4 rk = rsrc_words(a.k + bhk * S * D, S * D * 2);
+    const i32x4 rv = rsrc_words(a.v + bhk * S * D, S * D * 2);
+    const uint16_t* sk = smem + 2 * STAGE;
+    const uint16_t* sv = sk + 128 * D;
+    const uint16_t* skw = sk + 32 * wave * D;  // this wave's 32 keys
+    const uint16_t* svw = sv + 32 * wave * D;
+    {
+        const uint32_t kv_byte = smem_byte + (uint32_t)(2 * STAGE * 2);
+        dma_rows<D>(rk, kv_byte, (uint32_t)key0, D, wave, lane);
+        dma_rows<D>(rk, kv_byte + 64 * D * 2, (uint32_t)key0 + 64, D, wave, lane);
+        dma_rows<D>(rv, kv_byte + 128 * D * 2, (uint32_t)key0, D, wave, lane);
+        dma_rows<D>(rv, kv_byte + 192 * D * 2, (uint32_t)key0 + 64, D, wave, lane);
     }
 
     const i32x4 rq = rsrc_words(a.q + (int64_t)bh * S * D, S * D * 2);
@@ -591,9 +654,6 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_bf16(AttnBwdArgs a) {
 
     const int nqb = (int)((S + 63) / 64);
     const int qstart = a.causal ? (int)(key0 / 64) : 0;  // earlier query blocks see none of these keys
-    // this wave: query blocks whose last query reaches its first key
-    const int wstart = a.causal ? (int)(kw / 64) : 0;
-    const bool active = kw < S;
 
     auto issue = [&](int qb, int stage) {
         const uint32_t base = smem_byte + (uint32_t)(stage * STAGE * 2);
@@ -616,86 +676,96 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_bf16(AttnBwdArgs a) {
         wait_vmcnt<0>();
         __syncthreads();
         if (qb + 1 < nqb) issue(qb + 1, (qb + 1 - qstart) & 1);
-        if (!active || qb < wstart) continue;  // wave-uniform
+        // Every wave runs every block: in a block before the wave's first key
+        // (causal) every P is masked to 0, and a wave past S computes rows
+        // that are never stored. Skipping those blocks made the accumulators
+        // take a VGPR round trip on every iteration.
         const uint16_t* sq = smem + ((qb - qstart) & 1) * STAGE;
         const uint16_t* sdo = sq + TILE;
         const float* sl = reinterpret_cast<const float*>(sq + 2 * TILE);
         const int64_t q0 = (int64_t)qb * 64;
 
-        f32x16 sacc[2], dpacc[2];
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-            for (int j = 0; j < 16; ++j) sacc[t][j] = dpacc[t][j] = 0.f;
-#pragma unroll
-        for (int s = 0; s < KS; ++s)
-#pragma unroll
-            for (int t = 0; t < 2; ++t) {
-                sacc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_rows<D>(sq, 32 * t + col, 2 * s + half),
-                                                                 kf[s], sacc[t], 0, 0, 0);
-                dpacc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_rows<D>(sdo, 32 * t + col, 2 * s + half),
-                                                                  vf[s], dpacc[t], 0, 0, 0);
-            }
-
         // accumulator j of tile t: query q0 + 32 t + 8 (j/4) + 4 half + j%4, key my_key
-        bf16x8 pb[2][2], db[2][2];
-        // P and dS of the block; MASK adds the additive mask, EDGE applies the
-        // causal test (key offset from q0 against the query offset)
-        auto scores = [&](auto mask_tag, auto edge_tag) {
+        // P and dS of query tile t; MASK adds the additive mask, EDGE applies
+        // the causal test (key offset from q0 against the query offset)
+        auto scores = [&](auto mask_tag, auto edge_tag, auto t_tag, const f32x16& sacc, const f32x16& dpacc,
+                          bf16x8 (&pb)[2], bf16x8 (&db)[2]) {
             constexpr bool MASK = decltype(mask_tag)::value, EDGE = decltype(edge_tag)::value;
+            constexpr int t = decltype(t_tag)::value;
             const int kq = (int)(my_key - q0);
+            float p[16], ds[16];
 #pragma unroll
-            for (int t = 0; t < 2; ++t) {
-                float p[16], ds[16];
+            for (int jq = 0; jq < 4; ++jq) {
+                const int qi = 32 * t + 8 * jq + 4 * half;  // first of 4 consecutive queries
+                const float4 l2 = *reinterpret_cast<const float4*>(&sl[qi]);
+                const float4 dl = *reinterpret_cast<const float4*>(&sl[64 + qi]);
+                const float lv[4] = {l2.x, l2.y, l2.z, l2.w}, dv4[4] = {dl.x, dl.y, dl.z, dl.w};
 #pragma unroll
-                for (int jq = 0; jq < 4; ++jq) {
-                    const int qi = 32 * t + 8 * jq + 4 * half;  // first of 4 consecutive queries
-                    const float4 l2 = *reinterpret_cast<const float4*>(&sl[qi]);
-                    const float4 dl = *reinterpret_cast<const float4*>(&sl[64 + qi]);
-                    const float lv[4] = {l2.x, l2.y, l2.z, l2.w}, dv4[4] = {dl.x, dl.y, dl.z, dl.w};
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const int j = 4 * jq + e;
-                        float x = sacc[t][j] * a.scale_log2;
-                        if constexpr (MASK) {
-                            const int64_t qq = q0 + qi + e;
-                            const uint32_t off = (qq < S && my_key < S) ? (uint32_t)((qq * S + my_key) * 4) : kOOB;
-                            x += __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(rm, (int)off, 0, 0)) * kLog2e;
-                        }
-                        if constexpr (EDGE) {
-                            if ((!MASK || a.causal) && kq > qi + e) x = kNegInf;
-                        }
-                        p[j] = exp2_hw(x - lv[e]);
-                        ds[j] = p[j] * (dpacc[t][j] - dv4[e]);
+                for (int e = 0; e < 4; ++e) {
+                    const int j = 4 * jq + e;
+                    float x = sacc[j] * a.scale_log2;
+                    if constexpr (MASK) {
+                        const int64_t qq = q0 + qi + e;
+                        const uint32_t off = (qq < S && my_key < S) ? (uint32_t)((qq * S + my_key) * 4) : kOOB;
+                        x += __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(rm, (int)off, 0, 0)) * kLog2e;
                     }
+                    if constexpr (EDGE) {
+                        if ((!MASK || a.causal) && kq > qi + e) x = kNegInf;
+                    }
+                    p[j] = exp2_hw(x - lv[e]);
+                    ds[j] = p[j] * (dpacc[j] - dv4[e]);
                 }
+            }
 #pragma unroll
-                for (int kk = 0; kk < 2; ++kk) {
-                    pb[t][kk] = pack_bf16x8(&p[8 * kk]);
-                    db[t][kk] = pack_bf16x8(&ds[8 * kk]);
-                }
+            for (int kk = 0; kk < 2; ++kk) {
+                pb[kk] = pack_bf16x8(&p[8 * kk]);
+                db[kk] = pack_bf16x8(&ds[8 * kk]);
             }
         };
-        if (a.mask) scores(std::true_type{}, std::true_type{});
-        else if (a.causal && q0 < kw + 31) scores(std::false_type{}, std::true_type{});
-        else scores(std::false_type{}, std::false_type{});
-
-        // dV^T (d x key) += dO^T . P ; dK^T += Q^T . dS ; dO^T, Q^T by
-        // transposed reads of the dO, Q tiles, in the accumulators' query order
+        // one 32-query tile at a time: S = Q.K^T and dP = dO.V^T, its P and
+        // dS, then its share of dV^T (d x key) += dO^T . P and
+        // dK^T += Q^T . dS, with dO^T and Q^T by transposed reads of the dO,
+        // Q tiles in the accumulators' query order. With both tiles' S and dP
+        // live at once the kernel needed more than 256 VGPRs and copied the
+        // dV / dK accumulators between AGPRs and VGPRs every block.
+        auto tile = [&](auto t_tag) {
+            constexpr int t = decltype(t_tag)::value;
+            f32x16 sacc, dpacc;
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
+            for (int j = 0; j < 16; ++j) sacc[j] = dpacc[j] = 0.f;
 #pragma unroll
-            for (int t = 0; t < 2; ++t)
+            for (int s = 0; s < KS; ++s) {
+                sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_at(sq + 32 * t * D, roff[s]), frag_at(skw, roff[s]),
+                                                              sacc, 0, 0, 0);
+                dpacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_at(sdo + 32 * t * D, roff[s]),
+                                                               frag_at(svw, roff[s]), dpacc, 0, 0, 0);
+                // a k-chunk's four fragment reads, then its two MFMAs: reading
+                // every chunk's fragments ahead needs more than 256 VGPRs
+                __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 4, 0);
+                __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2, 0);
+            }
+            bf16x8 pb[2], db[2];
+            if (a.mask) scores(std::true_type{}, std::true_type{}, t_tag, sacc, dpacc, pb, db);
+            else if (a.causal && q0 < kw + 31) scores(std::false_type{}, std::true_type{}, t_tag, sacc, dpacc, pb, db);
+            else scores(std::false_type{}, std::false_type{}, t_tag, sacc, dpacc, pb, db);
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
                 for (int kk = 0; kk < 2; ++kk) {
-                    dvacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_tr<D>(sdo, 32 * t + 16 * kk, 32 * dt, lane),
-                                                                       pb[t][kk], dvacc[dt], 0, 0, 0);
-                    dkacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_tr<D>(sq, 32 * t + 16 * kk, 32 * dt, lane),
-                                                                       db[t][kk], dkacc[dt], 0, 0, 0);
+                    const int r0 = (32 * t + 16 * kk) * D;
+                    dvacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                        frag_tr_at(sdo + r0, troff[dt][0], troff[dt][1]), pb[kk], dvacc[dt], 0, 0, 0);
+                    dkacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                        frag_tr_at(sq + r0, troff[dt][0], troff[dt][1]), db[kk], dkacc[dt], 0, 0, 0);
+                    __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 4, 0);
+                    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2, 0);
                 }
-        }
+        };
+        tile(std::integral_constant<int, 0>{});
+        tile(std::integral_constant<int, 1>{});
     }
 
+    wait_vmcnt<0>();  // every DMA has landed (also when the loop ran no block)
     __syncthreads();
     static_assert(32 * (D + 4) * 4 <= 32 * (D + 8) * 2 * 2, "fp32 patch rows fit a wave's share");
     void* patch = smem + wave * 32 * (D + 8) * 2;  // 32 rows of up to D + 4 floats per wave
@@ -739,7 +809,8 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq_bf16(AttnBwdArgs a) {
     constexpr int KB = 64, QB = 128, KS = D / 16, DT = D / 32;
     constexpr int TILE = 64 * D;
     constexpr int STAGE = 2 * TILE;  // K, V [64][D]
-    __shared__ __attribute__((aligned(1024))) uint16_t smem[2 * STAGE];
+    constexpr int QDO = 2 * QB * D;  // the workgroup's Q and dO rows, [128][D] each, after the stages
+    __shared__ __attribute__((aligned(1024))) uint16_t smem[2 * STAGE + QDO];
     static_assert(4 * 32 * (D + 8) <= 2 * STAGE, "the epilogue's bf16 patches fit in the stages");
     const uint32_t smem_byte = (uint32_t)reinterpret_cast<uintptr_t>(smem);
     const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
@@ -755,16 +826,28 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq_bf16(AttnBwdArgs a) {
     const int64_t qw = q0 + 32 * wave;
     const int64_t my_q = qw + col;
 
-    // Q and dO fragments (B operands of S^T = K.Q^T and dP^T = V.dO^T)
-    const __amdgpu_buffer_rsrc_t rq = make_rsrc(a.q + (int64_t)bh * S * D, S * D * 2);
-    const __amdgpu_buffer_rsrc_t rdo = make_rsrc(a.dout + ((int64_t)b * S * a.H + h) * D, (S * a.H - h) * D * 2);
-    bf16x8 qf[KS], dof[KS];
+    uint32_t roff[KS], troff[DT][2];
 #pragma unroll
-    for (int s = 0; s < KS; ++s) {
-        const bool ok = my_q < S;
-        qf[s] = __builtin_bit_cast(bf16x8, buf_load16(rq, ok ? (uint32_t)((my_q * D + 16 * s + 8 * half) * 2) : kOOB));
-        dof[s] = __builtin_bit_cast(
-            bf16x8, buf_load16(rdo, ok ? (uint32_t)((my_q * a.H * D + 16 * s + 8 * half) * 2) : kOOB));
+    for (int s = 0; s < KS; ++s) roff[s] = rows_off<D>(lane, 2 * s + half);
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) troff[dt][h] = tr_off<D>(lane, 32 * dt, h);
+
+    // Q and dO rows of the workgroup's 128 queries (B operands of
+    // S^T = K.Q^T and dP^T = V.dO^T) stay in LDS for the whole key loop
+    // (held as register fragments they crowded the VGPRs). Queries past S
+    // load as zeros.
+    const i32x4 rq = rsrc_words(a.q + (int64_t)bh * S * D, S * D * 2);
+    const i32x4 rdo = rsrc_words(a.dout + ((int64_t)b * S * a.H + h) * D, (S * a.H - h) * D * 2);
+    const uint16_t* sqw = smem + 2 * STAGE + 32 * wave * D;  // this wave's 32 queries
+    const uint16_t* sdow = sqw + QB * D;
+    {
+        const uint32_t qd_byte = smem_byte + (uint32_t)(2 * STAGE * 2);
+        dma_rows<D>(rq, qd_byte, (uint32_t)q0, D, wave, lane);
+        dma_rows<D>(rq, qd_byte + 64 * D * 2, (uint32_t)q0 + 64, D, wave, lane);
+        dma_rows<D>(rdo, qd_byte + QB * D * 2, (uint32_t)q0, (uint32_t)(a.H * D), wave, lane);
+        dma_rows<D>(rdo, qd_byte + (QB + 64) * D * 2, (uint32_t)q0 + 64, (uint32_t)(a.H * D), wave, lane);
     }
     float lse2 = __builtin_inff(), delta = 0.f;
     if (my_q < S) {
@@ -778,12 +861,8 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq_bf16(AttnBwdArgs a) {
     const __amdgpu_buffer_rsrc_t rm = make_rsrc(a.mask, a.mask ? S * S * 4 : 0);
 
     const int nkb_all = (int)((S + KB - 1) / KB);
-    int nkb = nkb_all, wkb = nkb_all;
-    if (a.causal) {
-        nkb = min(nkb_all, (int)((min(q0 + QB, S) - 1) / KB) + 1);
-        wkb = min(nkb, (int)(min(qw + 31, S - 1) / KB) + 1);
-    }
-    if (qw >= S) wkb = 0;
+    int nkb = nkb_all;
+    if (a.causal) nkb = min(nkb_all, (int)((min(q0 + QB, S) - 1) / KB) + 1);
 
     auto issue = [&](int kb, int stage) {
         const uint32_t base = smem_byte + (uint32_t)(stage * STAGE * 2);
@@ -803,72 +882,73 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq_bf16(AttnBwdArgs a) {
         wait_vmcnt<0>();
         __syncthreads();
         if (kb + 1 < nkb) issue(kb + 1, (kb + 1) & 1);
-        if (kb >= wkb) continue;
+        // Every wave runs every block: keys after all of a wave's queries
+        // (causal) or queries past S give dS = 0. Skipping those blocks made
+        // the accumulators take a VGPR round trip on every iteration.
         const uint16_t* sk = smem + (kb & 1) * STAGE;
         const uint16_t* sv = sk + TILE;
-
-        f32x16 sacc[2], dpacc[2];
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-            for (int j = 0; j < 16; ++j) sacc[t][j] = dpacc[t][j] = 0.f;
-#pragma unroll
-        for (int s = 0; s < KS; ++s)
-#pragma unroll
-            for (int t = 0; t < 2; ++t) {
-                sacc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_rows<D>(sk, 32 * t + col, 2 * s + half),
-                                                                 qf[s], sacc[t], 0, 0, 0);
-                dpacc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_rows<D>(sv, 32 * t + col, 2 * s + half),
-                                                                  dof[s], dpacc[t], 0, 0, 0);
-            }
+        const int64_t key0 = (int64_t)kb * KB;
 
         // accumulator j of tile t: key key0 + 32 t + 8 (j/4) + 4 half + j%4, query my_q
-        const int64_t key0 = (int64_t)kb * KB;
-        bf16x8 db[2][2];
-        // dS of the block; MASK adds the additive mask, EDGE drops keys past S
-        // and (causal) keys after this lane's query, as offsets in the block
-        auto scores = [&](auto mask_tag, auto edge_tag) {
+        // dS of key tile t; MASK adds the additive mask, EDGE drops keys past
+        // S and (causal) keys after this lane's query, as offsets in the block
+        auto scores = [&](auto mask_tag, auto edge_tag, auto t_tag, const f32x16& sacc, const f32x16& dpacc,
+                          bf16x8 (&db)[2]) {
             constexpr bool MASK = decltype(mask_tag)::value, EDGE = decltype(edge_tag)::value;
+            constexpr int t = decltype(t_tag)::value;
             const int lim = (int)min<int64_t>(S - key0, KB);
             const int qrel = a.causal ? (int)max<int64_t>(min<int64_t>(my_q - key0, KB), -1) : KB;
+            float ds[16];
 #pragma unroll
-            for (int t = 0; t < 2; ++t) {
-                float ds[16];
-#pragma unroll
-                for (int j = 0; j < 16; ++j) {
-                    const int ko = 32 * t + 8 * (j >> 2) + 4 * half + (j & 3);
-                    float x = sacc[t][j] * a.scale_log2;
-                    if constexpr (MASK) {
-                        const int64_t key = key0 + ko;
-                        const uint32_t off = (my_q < S && key < S) ? (uint32_t)((my_q * S + key) * 4) : kOOB;
-                        x += __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(rm, (int)off, 0, 0)) * kLog2e;
-                    }
-                    if constexpr (EDGE) {
-                        if (ko >= lim || ko > qrel) x = kNegInf;
-                    }
-                    ds[j] = exp2_hw(x - lse2) * (dpacc[t][j] - delta);
+            for (int j = 0; j < 16; ++j) {
+                const int ko = 32 * t + 8 * (j >> 2) + 4 * half + (j & 3);
+                float x = sacc[j] * a.scale_log2;
+                if constexpr (MASK) {
+                    const int64_t key = key0 + ko;
+                    const uint32_t off = (my_q < S && key < S) ? (uint32_t)((my_q * S + key) * 4) : kOOB;
+                    x += __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(rm, (int)off, 0, 0)) * kLog2e;
                 }
-#pragma unroll
-                for (int kk = 0; kk < 2; ++kk) db[t][kk] = pack_bf16x8(&ds[8 * kk]);
+                if constexpr (EDGE) {
+                    if (ko >= lim || ko > qrel) x = kNegInf;
+                }
+                ds[j] = exp2_hw(x - lse2) * (dpacc[j] - delta);
             }
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk) db[kk] = pack_bf16x8(&ds[8 * kk]);
         };
-        if (a.mask) scores(std::true_type{}, std::true_type{});
-        else if (key0 + KB > S || (a.causal && key0 + KB - 1 > qw)) scores(std::false_type{}, std::true_type{});
-        else scores(std::false_type{}, std::false_type{});
-
-        // dQ^T (d x query) += K^T . dS^T ; K^T by transposed reads of the K
-        // tile, in the accumulators' key order
+        // one 32-key tile at a time: S^T = K.Q^T and dP^T = V.dO^T, its dS,
+        // then its share of dQ^T (d x query) += K^T . dS^T, with K^T by
+        // transposed reads of the K tile in the accumulators' key order
+        auto tile = [&](auto t_tag) {
+            constexpr int t = decltype(t_tag)::value;
+            f32x16 sacc, dpacc;
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
+            for (int j = 0; j < 16; ++j) sacc[j] = dpacc[j] = 0.f;
 #pragma unroll
-            for (int t = 0; t < 2; ++t)
+            for (int s = 0; s < KS; ++s) {
+                sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_at(sk + 32 * t * D, roff[s]), frag_at(sqw, roff[s]),
+                                                              sacc, 0, 0, 0);
+                dpacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_at(sv + 32 * t * D, roff[s]),
+                                                               frag_at(sdow, roff[s]), dpacc, 0, 0, 0);
+            }
+            bf16x8 db[2];
+            if (a.mask) scores(std::true_type{}, std::true_type{}, t_tag, sacc, dpacc, db);
+            else if (key0 + KB > S || (a.causal && key0 + KB - 1 > qw))
+                scores(std::false_type{}, std::true_type{}, t_tag, sacc, dpacc, db);
+            else scores(std::false_type{}, std::false_type{}, t_tag, sacc, dpacc, db);
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
                 for (int kk = 0; kk < 2; ++kk)
-                    dqacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_tr<D>(sk, 32 * t + 16 * kk, 32 * dt, lane),
-                                                                       db[t][kk], dqacc[dt], 0, 0, 0);
-        }
+                    dqacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                        frag_tr_at(sk + (32 * t + 16 * kk) * D, troff[dt][0], troff[dt][1]), db[kk], dqacc[dt], 0, 0,
+                        0);
+        };
+        tile(std::integral_constant<int, 0>{});
+        tile(std::integral_constant<int, 1>{});
     }
 
+    wait_vmcnt<0>();  // every DMA has landed (also when the loop ran no block)
     __syncthreads();
     store_rows<D, uint16_t>(dqacc, a.scale, smem + wave * 32 * (D + 8), a.dq + (int64_t)bh * S * D, D, qw, S, lane);
 }
