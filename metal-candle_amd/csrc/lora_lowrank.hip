@@ -558,13 +558,15 @@ hipError_t launch_lora_bwd_operands(const uint16_t* dY, int64_t T, int64_t N, co
 }
 
 // Column-tile count times splits should give >= ~1024 workgroups, with each
-// wave still walking several 32-row steps. A split's rows of X are one
+// wave walking at least eight 32-row steps (c4 medians: a cap of T / 1024
+// splits ran the low-rank kernels 1% faster than T / 512, T / 256 and
+// T / 2048 ran slower). A split's rows of X are one
 // buffer resource with 32-bit offsets, so a split never spans 2^31 bytes:
 // that bound wins over the step count (wide X, e.g. a vocabulary-sized dY).
 int colreduce_splits(int64_t T, int64_t C) {
     const int64_t ctiles = (C + 127) / 128;
     int64_t s = (1536 + ctiles - 1) / ctiles;
-    const int64_t max_s = (T + 511) / 512;  // >= 4 steps per wave
+    const int64_t max_s = (T + 1023) / 1024;  // >= 8 steps per wave
     if (s > max_s) s = max_s;
     if (s < 1) s = 1;
     const int64_t rows_cap = (int64_t)0x7fffffff / (2 * C) / 32 * 32;  // chunks are multiples of 32 rows
