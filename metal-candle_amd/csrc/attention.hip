@@ -426,14 +426,13 @@ struct AttnBwdArgs {
 
 // Position of 16-byte chunk c of row r in the backward's [64][D] LDS tiles.
 // Two read patterns must be bank-conflict free (64 banks x 4 B): row reads
-// (frag_rows: 16 consecutive rows of one chunk per 16 lanes) need the row's
-// low bits to permute the chunk; the transposed reads (frag_tr: 4
-// consecutive rows x 4 consecutive chunks per 32 lanes) need the row's two
-// lowest bits on the chunk's bits 2-3. Swapping the row's bit pairs 0-1 and
-// 2-3 into the XOR mask serves both (D = 128: 16 chunks per 256-byte row;
-// D = 64: 8 chunks, two rows per 256 bytes). The row-major swizzle of the
-// forward (swz) put two (row, chunk) pairs of each transposed read on one
-// bank group.
+// (16 consecutive rows of one chunk per 16 lanes) need the row's low bits to
+// permute the chunk; the transposed reads (4 consecutive rows x 4
+// consecutive chunks per 32 lanes) need the row's two lowest bits on the
+// chunk's bits 2-3. Swapping the row's bit pairs 0-1 and 2-3 into the XOR
+// mask serves both (D = 128: 16 chunks per 256-byte row; D = 64: 8 chunks,
+// two rows per 256 bytes). The row-major swizzle of the forward (swz) put
+// two (row, chunk) pairs of each transposed read on one bank group.
 template <int D>
 __device__ __forceinline__ int aswz(int r, int c) {
     static_assert(D == 64 || D == 128, "head dims with an MFMA backward");
@@ -457,11 +456,6 @@ __device__ __forceinline__ void dma_rows(i32x4 r, uint32_t lds_byte, uint32_t ro
     }
 }
 
-template <int D>
-__device__ __forceinline__ bf16x8 frag_rows(const uint16_t* t, int row, int c) {
-    return *reinterpret_cast<const bf16x8*>(&t[row * D + 8 * aswz<D>(row, c)]);
-}
-
 // ds_read_b64_tr_b16: within each 16-lane group, lane i receives element i % 4
 // of the 8-byte pieces addressed by the group's lanes i / 4, 4 + i / 4,
 // 8 + i / 4 and 12 + i / 4 (in that order).
@@ -471,38 +465,29 @@ __device__ __forceinline__ s16x4 ds_read_tr16(const uint16_t* p) {
     return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p));
 }
 
-// MFMA 32x32x16 operand of M^T from a row-major swizzled [rows][D] tile M
-// (the layout frag_rows reads): lane l gets column m = dcol + l % 32 of M and
-// the 8 rows kbase + 4 (l / 32) + {0, 1, 2, 3, 8, 9, 10, 11}, the query / key
-// order in which a lane half of an S (or S^T) accumulator holds its rows
-// (8 (j/4) + 4 half + j%4). Two transposed reads of 4 rows each: lane i of
-// group g addresses row kbase + 4 (g / 2) + i / 4 (+ 8), columns
-// dcol + 16 (g % 2) + 4 (i % 4) .. +3.
+// MFMA 32x32x16 fragments from a swizzled [rows][D] tile, addressed by
+// per-lane byte offsets computed once per kernel. Inside a tile the swizzle
+// depends only on a row's low four bits, so the lane's offset is the same for
+// every 32-row (row fragments) or 16-row (transposed fragments) step of the
+// tile, and the step enters as a constant that folds into the LDS
+// instruction's offset field; the kernels hold a handful of offsets rather
+// than one address per fragment read.
+//
+// Row fragment (the A or B operand from rows of the tile): lane l reads row
+// 32 k + l % 32, 16-byte chunk c.
 template <int D>
-__device__ __forceinline__ bf16x8 frag_tr(const uint16_t* t, int kbase, int dcol, int lane) {
-    const int i = lane & 15, g = lane >> 4;
-    const int ra = kbase + 4 * (g >> 1) + (i >> 2), rb = ra + 8;
-    const int c = (dcol >> 3) + 2 * (g & 1) + ((i & 3) >> 1);
-    const int sub = 4 * (i & 1);
-    const s16x4 lo = ds_read_tr16(&t[ra * D + 8 * aswz<D>(ra, c) + sub]);
-    const s16x4 hi = ds_read_tr16(&t[rb * D + 8 * aswz<D>(rb, c) + sub]);
-    const s16x4 v8[2] = {lo, hi};
-    return __builtin_bit_cast(bf16x8, v8);
-}
-
-// The same fragments from precomputed per-lane byte offsets. Inside a tile
-// the swizzle depends only on a row's low four bits, so for rows 16 k + r
-// (frag_tr: kbase = 16 k) or 32 k + r (frag_rows) the lane's offset is fixed
-// and the tile row enters as a constant that folds into the LDS instruction's
-// offset field. Precomputing the few distinct offsets keeps the backward
-// kernels from holding one hoisted address per fragment read.
-template <int D>
-__device__ __forceinline__ uint32_t rows_off(int lane, int c) {  // frag_rows(t, 32 k + lane % 32, c)
+__device__ __forceinline__ uint32_t rows_off(int lane, int c) {
     const int col = lane & 31;
     return (uint32_t)((col * D + 8 * aswz<D>(col, c)) * 2);
 }
+// Transposed fragment (operand of M^T for a row-major tile M): lane l gets
+// column dcol + l % 32 of M and the 8 rows 16 k + 4 (l / 32) +
+// {0, 1, 2, 3, 8, 9, 10, 11}, the order in which a lane half of an S (or S^T)
+// accumulator holds its rows (8 (j/4) + 4 half + j%4). Two transposed reads
+// of 4 rows each (h = 0, 1): lane i of 16-lane group g addresses row
+// 16 k + 4 (g / 2) + i / 4 + 8 h, columns dcol + 16 (g % 2) + 4 (i % 4) .. +3.
 template <int D>
-__device__ __forceinline__ uint32_t tr_off(int lane, int dcol, int h) {  // frag_tr(t, 16 k, dcol), read h
+__device__ __forceinline__ uint32_t tr_off(int lane, int dcol, int h) {
     const int i = lane & 15, g = lane >> 4;
     const int r = 4 * (g >> 1) + (i >> 2) + 8 * h;
     const int c = (dcol >> 3) + 2 * (g & 1) + ((i & 3) >> 1);
@@ -517,7 +502,6 @@ __device__ __forceinline__ bf16x8 frag_tr_at(const uint16_t* t, uint32_t off_lo,
                          ds_read_tr16(reinterpret_cast<const uint16_t*>(b + off_hi))};
     return __builtin_bit_cast(bf16x8, v8);
 }
-
 
 // Rows of a wave's transposed accumulators (acc[dt] element j = dim
 // 32 dt + 8 (j/4) + 4 half + j%4 of row `col`) through a per-wave LDS patch
@@ -739,8 +723,10 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_bf16(AttnBwdArgs a) {
                                                               sacc, 0, 0, 0);
                 dpacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_at(sdo + 32 * t * D, roff[s]),
                                                                frag_at(svw, roff[s]), dpacc, 0, 0, 0);
-                // a k-chunk's four fragment reads, then its two MFMAs: reading
-                // every chunk's fragments ahead needs more than 256 VGPRs
+                // each k-chunk's fragment reads right before its MFMAs (and
+                // below, each dV/dK pair's): left free, the scheduler keeps
+                // more fragments live (D = 128: 256 VGPRs + 188 AGPRs against
+                // 252 + 160, with more AGPR copies)
                 __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 4, 0);
                 __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2, 0);
             }
