@@ -201,6 +201,16 @@ __device__ __forceinline__ void dma16(i32x4 rsrc, uint32_t lds_byte, uint32_t vo
                  : "memory", "m0");
 }
 
+// dma16 with a wave-uniform byte offset in soffset (added to the address
+// outside the VGPR offset): loops that advance along a row pass the advance
+// here and keep each lane's VGPR offset fixed.
+__device__ __forceinline__ void dma16_s(i32x4 rsrc, uint32_t lds_byte, uint32_t voff, uint32_t soff) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                 :
+                 : "s"(lds_byte), "v"(voff), "s"(rsrc), "s"(soff)
+                 : "memory", "m0");
+}
+
 __device__ __forceinline__ i32x4 rsrc_words(const void* base, int64_t bytes) {
     const int n = bytes <= 0 ? 0 : bytes >= 0x7fffffff ? 0x7fffffff : (int)bytes;
     const uint64_t a = reinterpret_cast<uint64_t>(base);

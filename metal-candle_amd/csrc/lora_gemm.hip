@@ -96,6 +96,36 @@ __device__ __forceinline__ void dma_tile(i32x4 r, uint32_t lds_byte, uint32_t ld
     }
 }
 
+// dma_tile for a full k-tile of rows with a fixed row stride: each lane's
+// VGPR offset (row * ld + swizzled chunk, in bytes) is precomputed once per
+// kernel (tile_offsets) and the k-tile's start kb * 2 goes in soffset, so a
+// load costs no vector arithmetic. Rows past the resource's range still load
+// zeros (their VGPR offset alone is past num_records).
+template <int ROWS, int NT, int BK>
+struct TileOffsets {
+    static constexpr int CPR = BK / 8, RPI = 64 / CPR;
+    static constexpr int PER_WAVE = ROWS / RPI / (NT / 64);
+    uint32_t v[PER_WAVE];
+    __device__ __forceinline__ void init(uint32_t ld, int tid) {
+        const int wave = tid >> 6, lane = tid & 63;
+#pragma unroll
+        for (int j = 0; j < PER_WAVE; ++j) {
+            const int row = (wave * PER_WAVE + j) * RPI + lane / CPR;
+            v[j] = ((uint32_t)row * ld + 8u * (uint32_t)swz<BK>(row, lane % CPR)) * 2u;
+        }
+    }
+};
+template <int ROWS, int NT, int BK, int PARTS>
+__device__ __forceinline__ void dma_tile_full(i32x4 r, uint32_t lds_wave, const TileOffsets<ROWS, NT, BK>& o,
+                                              uint32_t kb, int part) {
+    constexpr int PER_WAVE = TileOffsets<ROWS, NT, BK>::PER_WAVE;
+#pragma unroll
+    for (int j = 0; j < PER_WAVE; ++j) {
+        if (j % PARTS != part) continue;
+        dma16_s(r, lds_wave + (uint32_t)j * 1024u, o.v[j], kb * 2u);
+    }
+}
+
 template <int N>
 __device__ __forceinline__ void wait_tiles(int remaining) {
     // vmcnt may keep `remaining` later tiles (N loads each) in flight
@@ -197,16 +227,34 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int tm, int tn, uin
     // busy meanwhile (measured +2-5% on the 2-stage tiles; the 3-stage ring,
     // whose loads are spread over every substep, was 3% slower this way).
     constexpr int DMA_NT = (STAGES == 2 && NT == 512) ? 256 : NT;
+    // Full k-tiles of the first segment (all of the base product but a
+    // ragged last tile) load through precomputed lane offsets; the ragged
+    // tile, the second segment and tiles past the end take the general path,
+    // which zeroes chunks at k >= the segment's length.
+    TileOffsets<BM, DMA_NT, BK> offa;
+    TileOffsets<BN, DMA_NT, BK> offb;
+    offa.init((uint32_t)g.lda0, tid);
+    offb.init((uint32_t)g.ldb0, tid);
+    const int nfull0 = (int)(g.k0 / BK);
+    const uint32_t lds_wave_a = (uint32_t)__builtin_amdgcn_readfirstlane(
+        (int)((uint32_t)(tid >> 6) * (uint32_t)TileOffsets<BM, DMA_NT, BK>::PER_WAVE * 1024u));
+    const uint32_t lds_wave_b = (uint32_t)__builtin_amdgcn_readfirstlane(
+        (int)((uint32_t)(tid >> 6) * (uint32_t)TileOffsets<BN, DMA_NT, BK>::PER_WAVE * 1024u));
     auto issue = [&](int kt, int stage, int part) {
         const bool second = kt >= nk0;
         const uint32_t kb = (uint32_t)(second ? kt - nk0 : kt) * BK;
         const uint32_t ks = kt < nk ? (uint32_t)(second ? g.k1 : g.k0) : 0u;
         const uint32_t base = smem_byte + (uint32_t)(stage * STAGE * 2);
         if (DMA_NT == NT || tid < DMA_NT) {  // wave-uniform
-            dma_tile<BM, DMA_NT, BK, KS>(second ? ra1 : ra0, base, (uint32_t)(second ? g.lda1 : g.lda0), kb, ks, tid,
-                                         part);
-            dma_tile<BN, DMA_NT, BK, KS>(second ? rb1 : rb0, base + BM * BK * 2,
-                                         (uint32_t)(second ? g.ldb1 : g.ldb0), kb, ks, tid, part);
+            if (kt < nfull0) {
+                dma_tile_full<BM, DMA_NT, BK, KS>(ra0, base + lds_wave_a, offa, kb, part);
+                dma_tile_full<BN, DMA_NT, BK, KS>(rb0, base + BM * BK * 2 + lds_wave_b, offb, kb, part);
+            } else {
+                dma_tile<BM, DMA_NT, BK, KS>(second ? ra1 : ra0, base, (uint32_t)(second ? g.lda1 : g.lda0), kb, ks,
+                                             tid, part);
+                dma_tile<BN, DMA_NT, BK, KS>(second ? rb1 : rb0, base + BM * BK * 2,
+                                             (uint32_t)(second ? g.ldb1 : g.ldb0), kb, ks, tid, part);
+            }
         }
     };
 
