@@ -181,3 +181,33 @@ def test_wide_dB_split_bound(mc, dev):
     ref = s * (h @ dy.float())
     torch.cuda.synchronize()
     assert rel_err(dB, ref.cpu().numpy()) <= 1e-4
+
+
+def test_random_shapes_gemm_plans(mc, dev):
+    """Seeded random shapes across the GEMM plans (one tile shape, or a
+    256x256 split with a 256x128 / 256x192 tail; ragged M, N and K, K past
+    the full k-tiles): the forward base product with bias and the dX product,
+    against torch fp32 on the GPU, bf16 tolerance."""
+    import random
+    rng = random.Random(7)
+    for it in range(16):
+        M = rng.choice([rng.randint(1, 600), rng.randint(3000, 17000)])
+        N = rng.choice([384 * rng.randint(1, 10) + rng.choice([0, 8, -8, 64, 136]), rng.randint(1, 300) * 8])
+        N = max(8, N - N % 8)
+        K = max(8, rng.randint(1, 600) * 8)
+        r = rng.choice([4, 8, 16, 33, 64])
+        g = torch.Generator(device=dev).manual_seed(it)
+        x = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
+        W = (torch.randn(N, K, generator=g, device=dev) * 0.05).to(torch.bfloat16)
+        bias = (torch.randn(N, generator=g, device=dev) * 0.1).to(torch.bfloat16)
+        A = torch.randn(K, r, generator=g, device=dev) * 0.01
+        B = torch.zeros(r, N, device=dev)  # the base product alone
+        y, h = mc.lora_forward(x, A, B, 2.0, W=W, bias=bias)
+        dy = (torch.randn(M, N, generator=g, device=dev) * 0.01).to(torch.bfloat16)
+        dX, _, _ = mc.lora_backward(x, A, B, dy, 2.0, W=W, h_save=h, need_dA=False, need_dB=False)
+        ref_y = x.float() @ W.float().t() + bias.float()
+        ref_dx = dy.float() @ W.float()
+        torch.cuda.synchronize()
+        for name, out, ref in (("y", y, ref_y), ("dX", dX, ref_dx)):
+            err = ((out.float() - ref).abs().max() / ref.abs().max()).item()
+            assert err <= BF16_TOL, f"{name} M={M} N={N} K={K} r={r}: rel-err {err:.3e}"
