@@ -211,3 +211,39 @@ def test_random_shapes_gemm_plans(mc, dev):
         for name, out, ref in (("y", y, ref_y), ("dX", dX, ref_dx)):
             err = ((out.float() - ref).abs().max() / ref.abs().max()).item()
             assert err <= BF16_TOL, f"{name} M={M} N={N} K={K} r={r}: rel-err {err:.3e}"
+
+
+def test_random_shapes_lora(mc, dev):
+    """Seeded random shapes, ranks 1-128 and dropout rates through the whole
+    bf16 LoRA forward and backward, against a torch fp32 composite of the
+    same maths on the GPU (Hd = (x.A) * M/(1-p), y = x.W^T + s Hd.B,
+    Gd = s (dY.B^T) * M/(1-p), dX = dY.W + Gd.A^T, dA = x^T.Gd,
+    dB = s Hd^T.dY). y and dX to the bf16 tolerance; dA and dB (fp32 outputs
+    of bf16 inputs with hi/lo-split fp32 factors) to 1e-4."""
+    import random
+    rng = random.Random(11)
+    for it in range(12):
+        M = rng.choice([rng.randint(1, 700), rng.randint(2000, 8000)])
+        K, N = max(8, rng.randint(1, 300) * 8), max(8, rng.randint(1, 400) * 8)
+        r, p, s = rng.randint(1, 128), rng.choice([0.0, 0.1, 0.3]), 2.0
+        g = torch.Generator(device=dev).manual_seed(100 + it)
+        x = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
+        W = (torch.randn(N, K, generator=g, device=dev) * 0.05).to(torch.bfloat16)
+        A = torch.randn(K, r, generator=g, device=dev) * 0.05
+        B = torch.randn(r, N, generator=g, device=dev) * 0.05
+        dy = (torch.randn(M, N, generator=g, device=dev) * 0.01).to(torch.bfloat16)
+        mask = mc.dropout_mask(it, p, M, r).to(dev) if p > 0 else None
+        y, h = mc.lora_forward(x, A, B, s, W=W, mask=mask, dropout_p=p)
+        dX, dA, dB = mc.lora_backward(x, A, B, dy, s, W=W, mask=mask, dropout_p=p, h_save=h)
+        xf, Wf, dyf = x.float(), W.float(), dy.float()
+        mf = mask.float() / (1.0 - p) if mask is not None else torch.ones(M, r, device=dev)
+        Hd = (xf @ A) * mf
+        Gd = s * (dyf @ B.t()) * mf
+        refs = {"y": xf @ Wf.t() + s * (Hd @ B), "dX": dyf @ Wf + Gd @ A.t(), "dA": xf.t() @ Gd,
+                "dB": s * (Hd.t() @ dyf)}
+        outs = {"y": y, "dX": dX, "dA": dA, "dB": dB}
+        torch.cuda.synchronize()
+        for name, ref in refs.items():
+            err = ((outs[name].float() - ref).abs().max() / ref.abs().max().clamp_min(1e-30)).item()
+            tol = 1e-4 if name in ("dA", "dB") else BF16_TOL
+            assert err <= tol, f"{name} M={M} K={K} N={N} r={r} p={p}: rel-err {err:.3e}"
