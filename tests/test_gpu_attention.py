@@ -279,3 +279,42 @@ def test_attention_bwd_c4_shape(mc, dev):
     assert float(ksum.abs().max()) <= 2e-2 * float(dk.float().abs().max()) * 8
     for t in (dq, dk, dv):
         assert torch.isfinite(t).all()
+
+
+def test_random_shapes_attention(mc, dev):
+    """Seeded random shapes (batch, grouped K/V heads, ragged S, causal,
+    additive mask; bf16 D = 64 / 128 through the MFMA kernels, fp32 through
+    the generic ones) through the forward and backward, against an fp32 torch
+    composite of the same maths (K/V heads repeated, scores scaled, mask
+    added, causal entries -inf, softmax, .V) and its autograd on the GPU."""
+    import random
+    rng = random.Random(5)
+    for it in range(12):
+        dt = torch.bfloat16 if it % 4 else torch.float32
+        D = rng.choice([64, 128]) if dt == torch.bfloat16 else rng.choice([32, 64, 80])
+        Hkv, rep = rng.choice([1, 2, 4]), rng.choice([1, 2, 3])
+        H, B = Hkv * rep, rng.randint(1, 3)
+        S = rng.randint(1, 700 if dt == torch.bfloat16 else 200)
+        causal, use_mask = rng.random() < 0.6, rng.random() < 0.25
+        g = torch.Generator(device=dev).manual_seed(it)
+        q = torch.randn(B, H, S, D, generator=g, device=dev).to(dt)
+        k = torch.randn(B, Hkv, S, D, generator=g, device=dev).to(dt)
+        v = torch.randn(B, Hkv, S, D, generator=g, device=dev).to(dt)
+        mask = (torch.randn(S, S, generator=g, device=dev) * 2) if use_mask else None
+        o, lse = mc.attention_forward(q, k, v, causal=causal, mask=mask)
+        do = (torch.randn(B, S, H * D, generator=g, device=dev) * 0.1).to(dt)
+        dq, dk, dv = mc.attention_backward(q, k, v, o, lse, do, causal=causal, mask=mask)
+        qf, kf, vf = (t.float().requires_grad_(True) for t in (q, k, v))
+        s = (qf @ kf.repeat_interleave(rep, dim=1).transpose(-1, -2).contiguous()) * D ** -0.5
+        if mask is not None:
+            s = s + mask
+        if causal:
+            s = s.masked_fill(torch.ones(S, S, dtype=torch.bool, device=dev).triu(1), float("-inf"))
+        of = (torch.softmax(s, -1) @ vf.repeat_interleave(rep, dim=1)).transpose(1, 2).reshape(B, S, H * D)
+        of.backward(do.float())
+        torch.cuda.synchronize()
+        # the reference itself is fp32 (not the fp64 oracle): 1e-4 for the fp32 kernels
+        tol = 1e-4 if dt == torch.float32 else BF16_TOL
+        for name, out, ref in (("o", o, of.detach()), ("dq", dq, qf.grad), ("dk", dk, kf.grad), ("dv", dv, vf.grad)):
+            err = ((out.float() - ref).abs().max() / ref.abs().max().clamp_min(1e-30)).item()
+            assert err <= tol, f"{name} {dt} B={B} H={H} Hkv={Hkv} S={S} D={D} causal={causal} mask={use_mask}: {err:.3e}"
