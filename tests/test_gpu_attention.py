@@ -7,7 +7,7 @@ Cases: the reference's attention test geometries (src/models/transformer.rs:
 sequence lengths around the 64-key / 128-query block edges for both head dims
 of the MFMA kernel (64, 128), GQA ratios 1, 2 and 6, causal / additive mask /
 both, -inf mask entries and a fully masked row, the workspace-free kernel
-(fp32, other bf16 head dims), and BASELINE c4's attention [8, 12, 2048, 128]
+(fp32, other bf16 head dims), and BASELINE.json c4's attention [8, 12, 2048, 128]
 with 2 K/V heads: there the oracle checks two whole K/V groups (6 heads, every
 query) and every output row is checked to lie within the range of the v rows
 it averages. Tolerance max|out-ref|/max|ref|: 1e-5 (fp32), 2e-2 (bf16); the
@@ -143,7 +143,7 @@ def test_attention_deterministic(mc, dev):
 
 
 def test_attention_c4_shape(mc, dev):
-    """BASELINE c4's attention: [8, 12, 2048, 128], 2 K/V heads, causal."""
+    """BASELINE.json c4's attention: [8, 12, 2048, 128], 2 K/V heads, causal."""
     B, H, Hkv, S, D = 8, 12, 2, 2048, 128
     g = gen(2048)
     q = torch.randn(B, H, S, D, generator=g).to(torch.bfloat16)
@@ -254,7 +254,7 @@ def test_attention_bwd_deterministic(mc, dev):
 
 
 def test_attention_bwd_c4_shape(mc, dev):
-    """Backward at BASELINE c4's attention shape: one whole K/V group (6 query
+    """Backward at BASELINE.json c4's attention shape: one whole K/V group (6 query
     heads, every query and key) against the oracle; on every head, the rows
     of dS sum to 0, so sum_j dK_j = scale sum_i (sum_j dS_ij) q_i = 0."""
     B, H, Hkv, S, D = 8, 12, 2, 2048, 128

@@ -3,7 +3,7 @@
 Cases: the executor known answer (tests/executor_direct.rs:345-367), the
 reference's fused-vs-candle LoRA shapes (tests/custom_ops_correctness.rs:
 15-170: [2,64,512] r8 s2, batches 1/4/8 at [b,32,256], ranks 4..32),
-BASELINE config 1 (fp32, 1e-5) and the bf16 projection shapes of configs 3-5
+BASELINE.json config 1 (fp32, 1e-5) and the bf16 projection shapes of configs 3-5
 (2e-2), with dropout masks from the shared host generator, bias, delta-only
 (W absent, as FusedLoRAOp) and ragged sizes. At full token counts the
 O(T.K.N) outputs y and dX are checked on a seeded sample of token rows (rows
@@ -60,7 +60,7 @@ def _check(mc, dev, c, scale, tol, mask=None, p=0.0, sample_rows=None):
 
 
 def test_executor_known_answer(mc, dev):
-    """executor_direct.rs:345-367 inputs; y hand-derived in the survey."""
+    """executor_direct.rs:345-367 inputs; y derived by hand from them (x·A·B·scale)."""
     x = torch.tensor([[1.0, 2, 3, 4], [5, 6, 7, 8]], device=dev)
     A = torch.tensor([[0.1, 0.2], [0.3, 0.4], [0.5, 0.6], [0.7, 0.8]], device=dev)
     B = torch.tensor([[1.0, 2, 3, 4], [5, 6, 7, 8]], device=dev)
@@ -70,7 +70,7 @@ def test_executor_known_answer(mc, dev):
 
 
 def test_config1_fp32(mc, dev):
-    """BASELINE c1: x [4,128,768] fp32, W 768x768, r8 a16, no dropout, seed 0."""
+    """BASELINE.json c1: x [4,128,768] fp32, W 768x768, r8 a16, no dropout, seed 0."""
     c = lora_case(0, 4 * 128, 768, 768, 8, dtype=torch.float32)
     _check(mc, dev, c, 2.0, F32_TOL)
 

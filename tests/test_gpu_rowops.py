@@ -168,7 +168,7 @@ def _sampled_rows(n_rows, k, seed):
 
 @pytest.mark.parametrize("dtype,shape", [(torch.float32, (8, 14, 1024, 1024)), (torch.bfloat16, (8, 12, 2048, 2048))])
 def test_softmax_config_full_size(mc, dev, dtype, shape):
-    """BASELINE c2 (fp32) and the c4 attention softmax (bf16), causal, fwd + bwd."""
+    """BASELINE.json c2 (fp32) and the c4 attention softmax (bf16), causal, fwd + bwd."""
     S = shape[-1]
     gen = torch.Generator(device=dev).manual_seed(2024)
     s = (torch.randn(*shape, generator=gen, device=dev) * 3).to(dtype)
