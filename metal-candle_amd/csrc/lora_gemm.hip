@@ -153,6 +153,18 @@ __device__ __forceinline__ void store_c(const f32x16 (&acc)[TM][TN], uint16_t* s
     const __amdgpu_buffer_rsrc_t rc = make_rsrc(g.c + m0 * g.ldc, (g.M - m0) * g.ldc * 2);
     const __amdgpu_buffer_rsrc_t rbias = make_rsrc(g.bias, g.bias ? g.N * 2 : 0);
     const int prow = lane >> 1, pcol = (lane & 1) * 16;
+    // The bias chunks depend only on the column block: all of them are loaded
+    // before the first store. vmcnt counts loads and stores in issue order,
+    // so a load issued after a store waits for that store as well; loading
+    // the bias per 32 x 32 block serialised one store completion per block.
+    i32x4 bq[TN][2];
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int64_t n = n0 + wn * WN + j * 32 + pcol + 8 * h;
+            bq[j][h] = __builtin_amdgcn_raw_buffer_load_b128(rbias, (int)(n < g.N ? n * 2 : kOOB), 0, 0);
+        }
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -172,11 +184,10 @@ __device__ __forceinline__ void store_c(const f32x16 (&acc)[TM][TN], uint16_t* s
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
                 const int64_t n = gn + 8 * h;
-                const i32x4 bq = __builtin_amdgcn_raw_buffer_load_b128(rbias, (int)(n < g.N ? n * 2 : kOOB), 0, 0);
                 uint32_t w[4];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const uint32_t bb = (uint32_t)bq[e];
+                    const uint32_t bb = (uint32_t)bq[j][h][e];
                     w[e] = pack_bf16x2(v[8 * h + 2 * e] + bf16_lo(bb), v[8 * h + 2 * e + 1] + bf16_hi(bb));
                 }
                 const i32x4 out = {(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
