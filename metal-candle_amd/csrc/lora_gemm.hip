@@ -297,6 +297,34 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int tm, int tn, uin
             fb[slot][t] = *reinterpret_cast<const bf16x8*>(&st[b_row0 + t * 32 * BK + col]);
     };
 
+    auto mfma_substep = [&](int cur) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[cur][i], fb[cur][j], acc[i][j], 0, 0, 0);
+    };
+    // The last k-tile, after which nothing is issued: its loads were the last
+    // ones, so it waits for all of them. Only its substeps that hold data are
+    // multiplied: with the rank-r segment last, a rank of 16 fills one of the
+    // four (the rest are range-checked zeros in both operands, whose products
+    // add exactly nothing).
+    auto last_tile = [&](int kt) {
+        wait_vmcnt<0>();
+        __syncthreads();
+        const uint16_t* st = smem + (kt % STAGES) * STAGE;
+        const bool second = kt >= nk0;
+        const int64_t kleft = (second ? g.k1 : g.k0) - (int64_t)(second ? kt - nk0 : kt) * BK;
+        const int nks = kleft >= BK ? KS : (int)((kleft + 15) / 16);
+        load_frags(st, 0, 0);
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            if (ks >= nks) break;
+            const int cur = ks & 1;
+            if (ks + 1 < KS && ks + 1 < nks) load_frags(st, ks + 1, cur ^ 1);
+            mfma_substep(cur);
+        }
+    };
     auto issue_all = [&](int t) {
 #pragma unroll
         for (int p = 0; p < KS; ++p) issue(t, t % STAGES, p);
@@ -311,27 +339,22 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int tm, int tn, uin
         // left the last part only one substep to land before the wait).
         static_assert(KS == 4, "the two-stage schedule assumes four substeps per tile");
         if (nk > 0) issue_all(0);
-        for (int kt = 0; kt < nk; ++kt) {
+        for (int kt = 0; kt + 1 < nk; ++kt) {
             wait_vmcnt<0>();
             __syncthreads();
             const uint16_t* st = smem + (kt & 1) * STAGE;
-            if (kt + 1 < nk) {
-                issue(kt + 1, (kt + 1) & 1, 0);
-                issue(kt + 1, (kt + 1) & 1, 1);
-            }
+            issue(kt + 1, (kt + 1) & 1, 0);
+            issue(kt + 1, (kt + 1) & 1, 1);
             load_frags(st, 0, 0);
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
                 const int cur = ks & 1;
                 if (ks + 1 < KS) load_frags(st, ks + 1, cur ^ 1);
-#pragma unroll
-                for (int i = 0; i < TM; ++i)
-#pragma unroll
-                    for (int j = 0; j < TN; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[cur][i], fb[cur][j], acc[i][j], 0, 0, 0);
-                if (ks < 2 && kt + 1 < nk) issue(kt + 1, (kt + 1) & 1, ks + 2);
+                mfma_substep(cur);
+                if (ks < 2) issue(kt + 1, (kt + 1) & 1, ks + 2);
             }
         }
+        if (nk > 0) last_tile(nk - 1);
     } else {
         // Ring of STAGES stages: tiles 0 .. STAGES-2 are issued up front;
         // tile kt waits for its own loads (later tiles stay in flight), a
@@ -341,7 +364,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int tm, int tn, uin
 #pragma unroll
         for (int s0 = 0; s0 < STAGES - 1; ++s0)
             if (s0 < nk) issue_all(s0);
-        for (int kt = 0; kt < nk; ++kt) {
+        for (int kt = 0; kt + 1 < nk; ++kt) {
             const int ahead = nk - 1 - kt;  // tiles after kt already issued, at most STAGES-2
             wait_tiles<LOADS>(ahead < STAGES - 2 ? ahead : STAGES - 2);
             __syncthreads();
@@ -352,14 +375,11 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int tm, int tn, uin
             for (int ks = 0; ks < KS; ++ks) {
                 const int cur = ks & 1;
                 if (ks + 1 < KS) load_frags(st, ks + 1, cur ^ 1);
-#pragma unroll
-                for (int i = 0; i < TM; ++i)
-#pragma unroll
-                    for (int j = 0; j < TN; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[cur][i], fb[cur][j], acc[i][j], 0, 0, 0);
+                mfma_substep(cur);
                 if (nt < nk) issue(nt, nt % STAGES, ks);
             }
         }
+        if (nk > 0) last_tile(nk - 1);
     }
 
     __syncthreads();
