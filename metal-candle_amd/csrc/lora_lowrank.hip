@@ -257,8 +257,11 @@ struct ColJobDev {
     int ctiles;
 };
 
+// Two waves per SIMD (256 registers per lane at most): at 64 ranks the
+// kernel otherwise took 142 VGPRs + 128 AGPRs, one wave per SIMD, and
+// streamed at 2.4 TB/s; with the bound it fits in 236 VGPRs, no spills.
 template <int RC, int U, bool PTV>
-__global__ __launch_bounds__(256) void colreduce_bf16(int64_t T, int r, ColJobDev j0, ColJobDev j1, int nblk0) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void colreduce_bf16(int64_t T, int r, ColJobDev j0, ColJobDev j1, int nblk0) {
     const bool second = (int)blockIdx.x >= nblk0;
     const int b = second ? (int)blockIdx.x - nblk0 : (int)blockIdx.x;
     const uint16_t* X = second ? j1.X : j0.X;
