@@ -65,45 +65,72 @@ void oracle_dropout_mask(uint64_t seed, float p, int64_t rows, int32_t rank, uin
 /* Dropout scale as candle-nn computes it: kept values times 1/(1-p) in fp32. */
 static float keep_scale(float p) { return 1.0f / (1.0f - p); }
 
+/* Row blocks of the LoRA loops: a block of token rows shares each pass over a
+ * row of W (or B^T), which keeps W in cache across the block. */
+#define ORACLE_ROWS 8
+
+/* acc[j] = sum_k xr[k] * A[k*r + j] for j < r, each sum over ascending k (the
+ * j loop is innermost so that the r independent sums vectorise; every sum
+ * still sees the same sequence of fp64 operations). */
+static void rank_proj(const float* xr, int64_t K, const float* A, int32_t r, double* acc) {
+    for (int32_t j = 0; j < r; ++j) acc[j] = 0.0;
+    for (int64_t k = 0; k < K; ++k) {
+        const double xv = (double)xr[k];
+        const float* ar = A + k * r;
+        for (int32_t j = 0; j < r; ++j) acc[j] += xv * (double)ar[j];
+    }
+}
+
 void oracle_lora_fwd(int64_t T, int64_t K, int64_t N, int32_t r, float scale, float p,
                      const float* x, const float* W, const float* bias,
                      const float* A, const float* B, const uint8_t* mask,
                      float* y, float* hd_out, int threads) {
     const float ks = mask ? keep_scale(p) : 1.0f;
-#pragma omp parallel for schedule(static) num_threads(nthreads(threads))
-    for (int64_t t = 0; t < T; ++t) {
-        const float* xr = x + t * K;
-        double hd[512];
-        double* h = hd;
-        double* hbuf = NULL;
-        if (r > 512) { hbuf = (double*)malloc(sizeof(double) * (size_t)r); h = hbuf; }
-        /* lora.rs:323  hidden = input.broadcast_matmul(A) */
-        for (int32_t j = 0; j < r; ++j) {
-            double acc = 0.0;
-            for (int64_t k = 0; k < K; ++k) acc += (double)xr[k] * (double)A[k * r + j];
-            /* fp32 storage of the matmul result, as candle keeps it */
-            float hf = (float)acc;
-            /* lora.rs:326-330  dropout on the rank-r hidden */
-            if (mask) hf = mask[t * r + j] ? hf * ks : 0.0f;
-            h[j] = hf;
-            if (hd_out) hd_out[t * r + j] = hf;
+    const int64_t nblk = (T + ORACLE_ROWS - 1) / ORACLE_ROWS;
+#pragma omp parallel for schedule(dynamic) num_threads(nthreads(threads))
+    for (int64_t blk = 0; blk < nblk; ++blk) {
+        const int64_t t0 = blk * ORACLE_ROWS;
+        const int64_t nt = T - t0 < ORACLE_ROWS ? T - t0 : ORACLE_ROWS;
+        double* h = (double*)malloc(sizeof(double) * (size_t)(ORACLE_ROWS * r));
+        double* acc = (double*)malloc(sizeof(double) * (size_t)r);
+        for (int64_t i = 0; i < nt; ++i) {
+            const int64_t t = t0 + i;
+            /* lora.rs:323  hidden = input.broadcast_matmul(A) */
+            rank_proj(x + t * K, K, A, r, acc);
+            for (int32_t j = 0; j < r; ++j) {
+                /* fp32 storage of the matmul result, as candle keeps it */
+                float hf = (float)acc[j];
+                /* lora.rs:326-330  dropout on the rank-r hidden */
+                if (mask) hf = mask[t * r + j] ? hf * ks : 0.0f;
+                h[i * r + j] = hf;
+                if (hd_out) hd_out[t * r + j] = hf;
+            }
         }
         for (int64_t n = 0; n < N; ++n) {
-            /* lora.rs:336-339  (hidden . B) then affine(scale) */
-            double d = 0.0;
-            for (int32_t j = 0; j < r; ++j) d += h[j] * (double)B[(int64_t)j * N + n];
-            double acc = (double)scale * d;
+            /* candle_nn::Linear: x . W^T (+ b); one sum per row of the block,
+             * each over ascending k */
+            double base[ORACLE_ROWS] = {0};
             if (W) {
-                /* candle_nn::Linear: x . W^T (+ b) */
                 const float* wr = W + n * K;
-                double base = 0.0;
-                for (int64_t k = 0; k < K; ++k) base += (double)xr[k] * (double)wr[k];
-                acc += base;
-                if (bias) acc += (double)bias[n];
+                for (int64_t k = 0; k < K; ++k) {
+                    const double wv = (double)wr[k];
+                    for (int64_t i = 0; i < nt; ++i) base[i] += (double)x[(t0 + i) * K + k] * wv;
+                }
             }
-            y[t * N + n] = (float)acc;
+            for (int64_t i = 0; i < nt; ++i) {
+                /* lora.rs:336-339  (hidden . B) then affine(scale) */
+                double d = 0.0;
+                for (int32_t j = 0; j < r; ++j) d += h[i * r + j] * (double)B[(int64_t)j * N + n];
+                double out = (double)scale * d;
+                if (W) {
+                    out += base[i];
+                    if (bias) out += (double)bias[n];
+                }
+                y[(t0 + i) * N + n] = (float)out;
+            }
         }
-        free(hbuf);
+        free(acc);
+        free(h);
     }
 }
 
@@ -116,37 +143,61 @@ void oracle_lora_bwd(int64_t T, int64_t K, int64_t N, int32_t r, float scale, fl
     /* Hd (forward hidden after dropout) and Gd (gradient of the hidden). */
     double* hd = (double*)malloc(sizeof(double) * (size_t)(T * r));
     double* gd = (double*)malloc(sizeof(double) * (size_t)(T * r));
-#pragma omp parallel for schedule(static) num_threads(nt)
-    for (int64_t t = 0; t < T; ++t) {
-        const float* xr = x + t * K;
-        const float* dyr = dy + t * N;
-        for (int32_t j = 0; j < r; ++j) {
-            double h = 0.0;
-            for (int64_t k = 0; k < K; ++k) h += (double)xr[k] * (double)A[k * r + j];
-            double g = 0.0;
-            for (int64_t n = 0; n < N; ++n) g += (double)dyr[n] * (double)B[(int64_t)j * N + n];
-            g *= (double)scale;
-            float hf = (float)h;
-            if (mask) {
-                int keep = mask[t * r + j];
-                hf = keep ? hf * ks : 0.0f;
-                g = keep ? g * (double)ks : 0.0;
-            }
-            hd[t * r + j] = (double)hf;
-            gd[t * r + j] = g;
-        }
-    }
-    if (dx) {
-#pragma omp parallel for schedule(static) num_threads(nt)
+    /* B^T [N][r], so that the r sums of G = dY.B^T run side by side */
+    float* bt = (float*)malloc(sizeof(float) * (size_t)(N * r));
+    for (int32_t j = 0; j < r; ++j)
+        for (int64_t n = 0; n < N; ++n) bt[n * r + j] = B[(int64_t)j * N + n];
+#pragma omp parallel num_threads(nt)
+    {
+        double* hacc = (double*)malloc(sizeof(double) * (size_t)r);
+        double* gacc = (double*)malloc(sizeof(double) * (size_t)r);
+#pragma omp for schedule(static)
         for (int64_t t = 0; t < T; ++t) {
-            const float* dyr = dy + t * N;
-            for (int64_t k = 0; k < K; ++k) {
-                double acc = 0.0;
-                if (W)
-                    for (int64_t n = 0; n < N; ++n) acc += (double)dyr[n] * (double)W[n * K + k];
-                for (int32_t j = 0; j < r; ++j) acc += gd[t * r + j] * (double)A[k * r + j];
-                dx[t * K + k] = (float)acc;
+            rank_proj(x + t * K, K, A, r, hacc);
+            rank_proj(dy + t * N, N, bt, r, gacc);
+            for (int32_t j = 0; j < r; ++j) {
+                double g = gacc[j] * (double)scale;
+                float hf = (float)hacc[j];
+                if (mask) {
+                    int keep = mask[t * r + j];
+                    hf = keep ? hf * ks : 0.0f;
+                    g = keep ? g * (double)ks : 0.0;
+                }
+                hd[t * r + j] = (double)hf;
+                gd[t * r + j] = g;
             }
+        }
+        free(gacc);
+        free(hacc);
+    }
+    free(bt);
+    if (dx) {
+        /* dx[t][k] = sum_n dy[t][n] W[n][k] (ascending n), then + sum_j
+         * gd[t][j] A[k][j] (ascending j); rows of W are read contiguously */
+        const int64_t nblk = (T + ORACLE_ROWS - 1) / ORACLE_ROWS;
+#pragma omp parallel for schedule(dynamic) num_threads(nt)
+        for (int64_t blk = 0; blk < nblk; ++blk) {
+            const int64_t t0 = blk * ORACLE_ROWS;
+            const int64_t nr = T - t0 < ORACLE_ROWS ? T - t0 : ORACLE_ROWS;
+            double* acc = (double*)calloc((size_t)(ORACLE_ROWS * K), sizeof(double));
+            if (W)
+                for (int64_t n = 0; n < N; ++n) {
+                    const float* wr = W + n * K;
+                    for (int64_t i = 0; i < nr; ++i) {
+                        const double dv = (double)dy[(t0 + i) * N + n];
+                        double* ai = acc + i * K;
+                        for (int64_t k = 0; k < K; ++k) ai[k] += dv * (double)wr[k];
+                    }
+                }
+            for (int64_t i = 0; i < nr; ++i) {
+                const int64_t t = t0 + i;
+                for (int64_t k = 0; k < K; ++k) {
+                    double a = acc[i * K + k];
+                    for (int32_t j = 0; j < r; ++j) a += gd[t * r + j] * (double)A[k * r + j];
+                    dx[t * K + k] = (float)a;
+                }
+            }
+            free(acc);
         }
     }
     /* dA[k][j] = sum_t x[t][k] gd[t][j] and dB[j][n] = s sum_t hd[t][j] dy[t][n]:
