@@ -133,6 +133,20 @@ mc_status mc_rmsnorm_bwd(int64_t rows, int64_t dim, float eps, int32_t dtype, co
                          const void* w, const float* rstd, const void* dy, void* dx, float* dw,
                          void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* mc_rmsnorm_bwd without a workspace: allocates nothing. It has no
+ * counterpart in the reference; it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops). The
+ * dw partials go to a static device scratch of 16 MiB that the library
+ * holds on each device it runs on until the process ends; shapes whose
+ * partials need more (mc_rmsnorm_bwd_workspace_size(rows, dim) > 16 MiB,
+ * e.g. dim > 8192 with rows >= 4096) are rejected with MC_ERR_SHAPE. Same
+ * kernels and row partition as mc_rmsnorm_bwd, so the results are equal bit
+ * for bit. Calls that overlap on one device share the scratch and race:
+ * serialise them (one stream, or events). */
+mc_status mc_rmsnorm_bwd_noalloc(int64_t rows, int64_t dim, float eps, int32_t dtype, const void* x,
+                                 const void* w, const float* rstd, const void* dy, void* dx, float* dw,
+                                 hipStream_t stream);
+
 /* Softmax over the last dim of s [rows, dim]. causal_rows = 0: no mask;
  * causal_rows = S > 0 (S <= dim): row i is query q = i mod S and column j is
  * masked (-inf before the softmax, so p = 0 exactly) iff j > q + (dim - S).

@@ -113,6 +113,7 @@ _SIGNATURES = {
     "mc_rmsnorm_fwd": (ctypes.c_int, [_i64, _i64, _f32, _i32, _vp, _vp, _vp, _vp, _vp]),
     "mc_rmsnorm_bwd_workspace_size": (_sz, [_i64, _i64]),
     "mc_rmsnorm_bwd": (ctypes.c_int, [_i64, _i64, _f32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "mc_rmsnorm_bwd_noalloc": (ctypes.c_int, [_i64, _i64, _f32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "mc_softmax_fwd": (ctypes.c_int, [_i64, _i64, _i64, _i32, _vp, _vp, _vp]),
     "mc_softmax_bwd": (ctypes.c_int, [_i64, _i64, _i64, _i32, _vp, _vp, _vp, _vp]),
     "mc_attention_fwd_workspace_size": (_sz, [_ap]),

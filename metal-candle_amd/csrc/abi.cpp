@@ -230,9 +230,12 @@ size_t mc_rmsnorm_bwd_workspace_size(int64_t rows, int64_t dim) {
     return (size_t)mc::rmsnorm_bwd_blocks(rows, dim) * (size_t)dim * sizeof(float);
 }
 
-mc_status mc_rmsnorm_bwd(int64_t rows, int64_t dim, float eps, int32_t dtype, const void* x, const void* w,
-                         const float* rstd, const void* dy, void* dx, float* dw, void* workspace,
-                         size_t workspace_bytes, hipStream_t stream) {
+}  // extern "C"
+
+namespace {
+
+mc_status check_rmsnorm_bwd(int64_t rows, int64_t dim, float eps, int32_t dtype, const void* x, const void* w,
+                            const void* dy, void* dx) {
     mc_status s = check_rows(rows, dim, "RMSNorm backward");
     if (s != MC_OK) return s;
     if ((s = check_dtype(dtype, "RMSNorm backward")) != MC_OK) return s;
@@ -240,6 +243,18 @@ mc_status mc_rmsnorm_bwd(int64_t rows, int64_t dim, float eps, int32_t dtype, co
     MC_CHECK(x && dy && dx, MC_ERR_NULL, "RMSNorm backward: x, dy and dx must not be NULL");
     MC_CHECK(aligned16(x) && aligned16(dy) && aligned16(dx) && (!w || aligned16(w)), MC_ERR_LAYOUT,
              "RMSNorm backward: x, w, dy and dx must be 16-byte aligned");
+    return MC_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+mc_status mc_rmsnorm_bwd(int64_t rows, int64_t dim, float eps, int32_t dtype, const void* x, const void* w,
+                         const float* rstd, const void* dy, void* dx, float* dw, void* workspace,
+                         size_t workspace_bytes, hipStream_t stream) {
+    mc_status s = check_rmsnorm_bwd(rows, dim, eps, dtype, x, w, dy, dx);
+    if (s != MC_OK) return s;
     if (dw) {
         const size_t need = mc_rmsnorm_bwd_workspace_size(rows, dim);
         MC_CHECK(workspace && workspace_bytes >= need, MC_ERR_WORKSPACE,
@@ -251,6 +266,26 @@ mc_status mc_rmsnorm_bwd(int64_t rows, int64_t dim, float eps, int32_t dtype, co
     return hip_status(mc::launch_rmsnorm_bwd(rows, dim, eps, dtype, x, w, rstd, dy, dx, dw,
                                              static_cast<float*>(workspace), stream),
                       "RMSNorm backward");
+}
+
+mc_status mc_rmsnorm_bwd_noalloc(int64_t rows, int64_t dim, float eps, int32_t dtype, const void* x,
+                                 const void* w, const float* rstd, const void* dy, void* dx, float* dw,
+                                 hipStream_t stream) {
+    mc_status s = check_rmsnorm_bwd(rows, dim, eps, dtype, x, w, dy, dx);
+    if (s != MC_OK) return s;
+    float* partial = nullptr;
+    if (dw) {
+        const size_t need = mc_rmsnorm_bwd_workspace_size(rows, dim);
+        MC_CHECK(need <= mc::kRmsNormScratchBytes, MC_ERR_SHAPE,
+                 "RMSNorm backward (no-alloc): the dw partials of %lld x %lld need %zu bytes, above the "
+                 "%zu-byte static scratch; use mc_rmsnorm_bwd with a workspace",
+                 (long long)rows, (long long)dim, need, mc::kRmsNormScratchBytes);
+        hipError_t e = mc::rmsnorm_scratch(&partial);
+        if (e != hipSuccess) return hip_status(e, "RMSNorm backward (no-alloc): scratch address");
+    }
+    // No profiling scope here: the timing hook creates events when enabled.
+    return hip_status(mc::launch_rmsnorm_bwd(rows, dim, eps, dtype, x, w, rstd, dy, dx, dw, partial, stream),
+                      "RMSNorm backward (no-alloc)");
 }
 
 mc_status mc_softmax_fwd(int64_t rows, int64_t dim, int64_t causal_rows, int32_t dtype, const void* sc,

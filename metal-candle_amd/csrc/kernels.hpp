@@ -19,6 +19,11 @@ int rmsnorm_bwd_blocks(int64_t rows, int64_t dim);
 hipError_t launch_rmsnorm_bwd(int64_t rows, int64_t dim, float eps, int dtype, const void* x,
                               const void* w, const float* rstd, const void* dy, void* dx, float* dw,
                               float* partial, hipStream_t stream);
+// Size of the static device scratch that mc_rmsnorm_bwd_noalloc uses in place
+// of a workspace, and its device address on the current device (looked up
+// once per device).
+constexpr size_t kRmsNormScratchBytes = (size_t)16 << 20;
+hipError_t rmsnorm_scratch(float** out);
 
 // ------------------------------------------------------------- softmax
 hipError_t launch_softmax_fwd(int64_t rows, int64_t dim, int64_t causal_rows, int dtype,

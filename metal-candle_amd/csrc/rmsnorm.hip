@@ -14,11 +14,43 @@
 // partials in the workspace, then a column sum), so it is bitwise
 // reproducible. Rows whose length is not a multiple of the vector width
 // use a scalar variant that reads x twice.
+#include <mutex>
+
 #include "column_sum.hpp"
 #include "common.hpp"
 #include "kernels.hpp"
 
+// Scratch of mc_rmsnorm_bwd_noalloc: the per-block dw partials
+// [rmsnorm_bwd_blocks][dim] fp32 that mc_rmsnorm_bwd keeps in the caller's
+// workspace. Each device holds its own copy for the life of the process.
+// Every element a call reads was written by the same call, so nothing in it
+// needs clearing. Calls that overlap on one device race on it.
+static __device__ __align__(256) float scratch[mc::kRmsNormScratchBytes / sizeof(float)];
+
 namespace mc {
+
+hipError_t rmsnorm_scratch(float** out) {
+    // The host-side name `scratch` is not a device address: the device copy is
+    // found once per device with hipGetSymbolAddress, with that device current
+    // (it is the caller's current device here), and only that address is used.
+    constexpr int kMaxDevices = 64;
+    static std::mutex mu;
+    static float* ptrs[kMaxDevices] = {};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(mu);
+    if (!ptrs[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        ptrs[dev] = static_cast<float*>(p);
+    }
+    *out = ptrs[dev];
+    return hipSuccess;
+}
+
 namespace {
 
 constexpr int kRowsPerBlock = 4;  // waves (rows) per 256-thread workgroup
