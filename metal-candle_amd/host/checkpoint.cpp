@@ -174,7 +174,13 @@ struct JParser {
                             ok = false;
                             return out;
                         }
-                        const unsigned cp = (unsigned)std::stoul(t.substr(i, 4), nullptr, 16);
+                        unsigned cp = 0;
+                        const char* h0 = t.data() + i;
+                        const auto hr = std::from_chars(h0, h0 + 4, cp, 16);
+                        if (hr.ec != std::errc() || hr.ptr != h0 + 4) {  // four hex digits, nothing else
+                            ok = false;
+                            return out;
+                        }
                         i += 4;
                         if (cp < 0x80) {
                             out += (char)cp;
@@ -249,11 +255,29 @@ struct JParser {
     }
 };
 
+// A JSON number that is a whole decimal in [0, 2^64): no sign, fraction or
+// exponent, and no overflow (from_chars reports it instead of throwing).
 bool to_u64(const JVal& v, uint64_t& out) {
-    if (v.kind != JVal::Num || v.s.empty() || v.s[0] == '-') return false;
+    if (v.kind != JVal::Num || v.s.empty()) return false;
     for (char c : v.s)
         if (!isdigit((unsigned char)c)) return false;
-    out = std::stoull(v.s);
+    const char* b = v.s.data();
+    const char* e = b + v.s.size();
+    const auto r = std::from_chars(b, e, out);
+    return r.ec == std::errc() && r.ptr == e;
+}
+
+// A JSON number as f32: the whole text must parse (strtod, then rounded to
+// f32 as serde does for an f32 field); out-of-range magnitudes fail.
+bool to_f32(const JVal& v, float& out) {
+    if (v.kind != JVal::Num || v.s.empty()) return false;
+    const char* b = v.s.c_str();
+    char* end = nullptr;
+    errno = 0;
+    const double d = std::strtod(b, &end);
+    if (end != b + v.s.size() || !std::isfinite(d) || std::fabs(d) > 3.4028234663852886e38) return false;
+    if (errno == ERANGE && d != 0.0) return false;
+    out = (float)d;
     return true;
 }
 
@@ -366,15 +390,13 @@ std::optional<CheckpointMetadata> CheckpointMetadata::from_json(const std::strin
     for (const auto& kv : v.o) {
         if (kv.first == "global_step" && to_u64(kv.second, m.global_step)) seen |= 1;
         if (kv.first == "timestamp" && to_u64(kv.second, m.timestamp)) seen |= 8;
-        if (kv.second.kind == JVal::Num) {
-            if (kv.first == "loss") {
-                m.loss = std::stof(kv.second.s);
-                seen |= 2;
-            }
-            if (kv.first == "learning_rate") {
-                m.learning_rate = std::stof(kv.second.s);
-                seen |= 4;
-            }
+        if (kv.first == "loss") {
+            if (!to_f32(kv.second, m.loss)) return std::nullopt;
+            seen |= 2;
+        }
+        if (kv.first == "learning_rate") {
+            if (!to_f32(kv.second, m.learning_rate)) return std::nullopt;
+            seen |= 4;
         }
     }
     if (seen != 15) return std::nullopt;
@@ -495,14 +517,19 @@ Result<std::map<std::string, Tensor>, Error> safetensors_load(const std::string&
         uint64_t count = 1;
         for (const JVal& d : sh->a) {
             uint64_t v;
-            if (!to_u64(d, v)) return load_error("safetensors: invalid shape for tensor " + kv.first);
+            if (!to_u64(d, v) || v > (uint64_t)INT64_MAX)
+                return load_error("safetensors: invalid shape for tensor " + kv.first);
             dims.push_back((int64_t)v);
-            count *= v;
+            if (__builtin_mul_overflow(count, v, &count))
+                return load_error("safetensors: element count of tensor " + kv.first + " overflows");
         }
+        uint64_t nbytes = 0;
+        if (__builtin_mul_overflow(count, (uint64_t)di->size, &nbytes))
+            return load_error("safetensors: byte size of tensor " + kv.first + " overflows");
         uint64_t b0, b1;
         if (!to_u64(of->a[0], b0) || !to_u64(of->a[1], b1) || b1 < b0 || b1 > data_len)
             return load_error("safetensors: invalid data_offsets for tensor " + kv.first);
-        if (b1 - b0 != count * di->size)
+        if (b1 - b0 != nbytes)
             return load_error("safetensors: tensor " + kv.first + " has " + std::to_string(b1 - b0) +
                               " bytes for its shape " + dims_to_string(dims));
         spans.emplace_back(b0, b1);
@@ -569,7 +596,9 @@ Result<std::optional<CheckpointMetadata>, Error> read_checkpoint_metadata(const 
     if (t.is_err()) return t.error();
     auto it = meta.find("checkpoint_metadata");
     if (it == meta.end()) return std::optional<CheckpointMetadata>();
-    return CheckpointMetadata::from_json(it->second);
+    auto m = CheckpointMetadata::from_json(it->second);
+    if (!m) return load_error("safetensors: checkpoint_metadata is not a valid CheckpointMetadata");
+    return m;
 }
 
 }  // namespace mc_candle

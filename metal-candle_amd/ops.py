@@ -40,6 +40,50 @@ def _contig(t, name):
     return t
 
 
+def _expect(t, name, shape=None, dtype=None, device=None):
+    """Raise McError unless t is contiguous with the given shape, dtype and
+    device. These checks run before the C ABI is called: the kernels read
+    each buffer over the extent its shape arguments give, so a tensor of the
+    wrong size must never reach them."""
+    if t is None:
+        return None
+    if not isinstance(t, torch.Tensor):
+        raise McError(_lib.MC_ERR_NULL, f"{name} must be a tensor")
+    _contig(t, name)
+    if shape is not None and tuple(t.shape) != tuple(shape):
+        raise McError(_lib.MC_ERR_SHAPE, f"{name} has shape {tuple(t.shape)}, expected {tuple(shape)}")
+    if dtype is not None and t.dtype != dtype:
+        raise McError(_lib.MC_ERR_DTYPE, f"{name} has dtype {t.dtype}, expected {dtype}")
+    if device is not None and t.device != device:
+        raise McError(_lib.MC_ERR_LAYOUT, f"{name} is on {t.device}, expected {device}")
+    return t
+
+
+def _lora_factors(A, B):
+    """FusedLoRAOp::new (src/backend/custom_ops.rs:118-148): A [K, r] and B [r, N]."""
+    for t, n in ((A, "A"), (B, "B")):
+        if not isinstance(t, torch.Tensor):
+            raise McError(_lib.MC_ERR_NULL, f"{n} must be a tensor")
+    if A.dim() != 2 or B.dim() != 2:
+        raise McError(_lib.MC_ERR_SHAPE,
+                      f"LoRA matrices must be 2D, got shapes {list(A.shape)} and {list(B.shape)}")
+    if A.shape[1] != B.shape[0]:
+        raise McError(_lib.MC_ERR_SHAPE, "Incompatible LoRA matrix dimensions: "
+                      f"{A.shape[0]}\u00d7{A.shape[1]} and {B.shape[0]}\u00d7{B.shape[1]}")
+    return A.shape[0], A.shape[1], B.shape[1]
+
+
+def _rows_of(x, name):
+    if not isinstance(x, torch.Tensor):
+        raise McError(_lib.MC_ERR_NULL, f"{name} must be a tensor")
+    if x.dim() < 1:
+        raise McError(_lib.MC_ERR_SHAPE, "Input must have at least 1 dimension")
+    _contig(x, name)
+    _dtype_code(x)
+    D = x.shape[-1]
+    return (x.numel() // D if D else 0), D
+
+
 def _workspace(nbytes, device):
     if nbytes == 0:
         return None
@@ -51,16 +95,31 @@ def lora_desc(tokens, in_features, out_features, rank, scale, dropout_p=0.0, dty
 
 
 def lora_forward(x, A, B, scale, W=None, bias=None, mask=None, dropout_p=0.0, save_hidden=True):
-    """y = x.W^T + bias + scale*((x.A) (.) mask/(1-p)).B ; returns (y, h_save)."""
-    _contig(x, "x"), _contig(W, "W"), _contig(A, "A"), _contig(B, "B")
-    K = x.shape[-1]
-    T = x.numel() // K
-    r, N = B.shape
-    d = LoraDesc(T, K, N, r, float(scale), float(dropout_p), _dtype_code(x))
-    y = torch.empty(*x.shape[:-1], N, dtype=x.dtype, device=x.device)
-    h = torch.empty(r, T, dtype=torch.float32, device=x.device) if save_hidden else None
+    """y = x.W^T + bias + scale*((x.A) (.) mask/(1-p)).B ; returns (y, h_save).
+
+    x [..., K] (float32 or bfloat16), A [K, r] and B [r, N] float32, W [N, K]
+    and bias [N] in x's dtype, mask uint8 [T, r] (T = the leading dims of x
+    folded); all contiguous on x's device. Shape errors keep the reference's
+    messages (custom_ops.rs:123-139, 153-174)."""
+    K, r, N = _lora_factors(A, B)
+    if not isinstance(x, torch.Tensor) or x.dim() < 1:
+        raise McError(_lib.MC_ERR_SHAPE, "Input must have at least 1 dimension")
+    _contig(x, "x")
+    code = _dtype_code(x)
+    if x.shape[-1] != K:
+        raise McError(_lib.MC_ERR_SHAPE, f"Input feature dimension mismatch: expected {K}, got {x.shape[-1]}")
+    T = x.numel() // K if K else 0
+    dev = x.device
+    _expect(A, "A", dtype=torch.float32, device=dev)
+    _expect(B, "B", dtype=torch.float32, device=dev)
+    _expect(W, "W", shape=(N, K), dtype=x.dtype, device=dev)
+    _expect(bias, "bias", shape=(N,), dtype=x.dtype, device=dev)
+    _expect(mask, "mask", shape=(T, r), dtype=torch.uint8, device=dev)
+    d = LoraDesc(T, K, N, r, float(scale), float(dropout_p), code)
+    y = torch.empty(*x.shape[:-1], N, dtype=x.dtype, device=dev)
+    h = torch.empty(r, T, dtype=torch.float32, device=dev) if save_hidden else None
     ws_n = lib().mc_lora_fwd_workspace_size(ctypes.byref(d))  # 0 for an invalid descriptor
-    ws = _workspace(ws_n, x.device)
+    ws = _workspace(ws_n, dev)
     check(lib().mc_lora_fwd(ctypes.byref(d), _ptr(x), _ptr(W), _ptr(bias), _ptr(A), _ptr(B), _ptr(mask),
                             _ptr(y), _ptr(h), _ptr(ws), ws_n, _stream(x)))
     return y, h
@@ -68,24 +127,41 @@ def lora_forward(x, A, B, scale, W=None, bias=None, mask=None, dropout_p=0.0, sa
 
 def lora_backward(x, A, B, dY, scale, W=None, mask=None, dropout_p=0.0, h_save=None,
                   need_dx=True, need_dA=True, need_dB=True):
-    """(dX, dA, dB) with W frozen; entries not requested are None."""
-    K = A.shape[0]
-    r, N = B.shape
-    T = dY.numel() // N
-    d = LoraDesc(T, K, N, r, float(scale), float(dropout_p), _dtype_code(dY))
-    dX = torch.empty(*dY.shape[:-1], K, dtype=dY.dtype, device=dY.device) if need_dx else None
-    dA = torch.empty(K, r, dtype=torch.float32, device=dY.device) if need_dA else None
-    dB = torch.empty(r, N, dtype=torch.float32, device=dY.device) if need_dB else None
+    """(dX, dA, dB) with W frozen; entries not requested are None.
+
+    dY [..., N] with x [..., K] over the same leading dims (x may be None
+    when dA is not requested), h_save [r, T] float32 from lora_forward
+    (required for dB), other tensors as in lora_forward."""
+    K, r, N = _lora_factors(A, B)
+    if not isinstance(dY, torch.Tensor) or dY.dim() < 1:
+        raise McError(_lib.MC_ERR_SHAPE, "dY must have at least 1 dimension")
+    _contig(dY, "dY")
+    code = _dtype_code(dY)
+    if dY.shape[-1] != N:
+        raise McError(_lib.MC_ERR_SHAPE, f"dY feature dimension mismatch: expected {N}, got {dY.shape[-1]}")
+    T = dY.numel() // N if N else 0
+    dev = dY.device
+    _expect(A, "A", dtype=torch.float32, device=dev)
+    _expect(B, "B", dtype=torch.float32, device=dev)
+    _expect(x, "x", shape=tuple(dY.shape[:-1]) + (K,), dtype=dY.dtype, device=dev)
+    _expect(W, "W", shape=(N, K), dtype=dY.dtype, device=dev)
+    _expect(mask, "mask", shape=(T, r), dtype=torch.uint8, device=dev)
+    _expect(h_save, "h_save", shape=(r, T), dtype=torch.float32, device=dev)
+    d = LoraDesc(T, K, N, r, float(scale), float(dropout_p), code)
+    dX = torch.empty(*dY.shape[:-1], K, dtype=dY.dtype, device=dev) if need_dx else None
+    dA = torch.empty(K, r, dtype=torch.float32, device=dev) if need_dA else None
+    dB = torch.empty(r, N, dtype=torch.float32, device=dev) if need_dB else None
     ws_n = lib().mc_lora_bwd_workspace_size(ctypes.byref(d))  # 0 for an invalid descriptor
-    ws = _workspace(ws_n, dY.device)
+    ws = _workspace(ws_n, dev)
     check(lib().mc_lora_bwd(ctypes.byref(d), _ptr(x), _ptr(W), _ptr(A), _ptr(B), _ptr(mask), _ptr(h_save),
                             _ptr(dY), _ptr(dX), _ptr(dA), _ptr(dB), _ptr(ws), ws_n, _stream(dY)))
     return dX, dA, dB
 
 
 def rms_norm_forward(x, eps, w=None, save_rstd=True):
-    D = x.shape[-1]
-    rows = x.numel() // D if D else 0
+    """RMSNorm over the last dim: (y, rstd). w [dim] in x's dtype or None."""
+    rows, D = _rows_of(x, "x")
+    _expect(w, "w", shape=(D,), dtype=x.dtype, device=x.device)
     y = torch.empty_like(x)
     rstd = torch.empty(rows, dtype=torch.float32, device=x.device) if save_rstd else None
     check(lib().mc_rmsnorm_fwd(rows, D, float(eps), _dtype_code(x), _ptr(x), _ptr(w), _ptr(y), _ptr(rstd),
@@ -94,8 +170,11 @@ def rms_norm_forward(x, eps, w=None, save_rstd=True):
 
 
 def rms_norm_backward(x, dy, eps, w=None, rstd=None, need_dw=True):
-    D = x.shape[-1]
-    rows = x.numel() // D if D else 0
+    """(dx, dw) of RMSNorm; rstd [rows] float32 from the forward or None."""
+    rows, D = _rows_of(x, "x")
+    _expect(dy, "dy", shape=x.shape, dtype=x.dtype, device=x.device)
+    _expect(w, "w", shape=(D,), dtype=x.dtype, device=x.device)
+    _expect(rstd, "rstd", shape=(rows,), dtype=torch.float32, device=x.device)
     dx = torch.empty_like(x)
     dw = torch.empty(D, dtype=torch.float32, device=x.device) if need_dw else None
     ws_n = lib().mc_rmsnorm_bwd_workspace_size(rows, D) if need_dw else 0
@@ -106,16 +185,15 @@ def rms_norm_backward(x, dy, eps, w=None, rstd=None, need_dw=True):
 
 
 def softmax_forward(s, causal_rows=0):
-    D = s.shape[-1]
-    rows = s.numel() // D if D else 0
+    rows, D = _rows_of(s, "s")
     p = torch.empty_like(s)
     check(lib().mc_softmax_fwd(rows, D, int(causal_rows), _dtype_code(s), _ptr(s), _ptr(p), _stream(s)))
     return p
 
 
 def softmax_backward(p, dp, causal_rows=0):
-    D = p.shape[-1]
-    rows = p.numel() // D if D else 0
+    rows, D = _rows_of(p, "p")
+    _expect(dp, "dp", shape=p.shape, dtype=p.dtype, device=p.device)
     ds = torch.empty_like(p)
     check(lib().mc_softmax_bwd(rows, D, int(causal_rows), _dtype_code(p), _ptr(p), _ptr(dp), _ptr(ds),
                                _stream(p)))
@@ -127,12 +205,26 @@ def attention_desc(q, k, causal, scale):
     return AttnDesc(B, S, H, k.shape[1], D, int(bool(causal)), float(scale), _dtype_code(q))
 
 
+def _attn_inputs(q, k, v, mask):
+    """q [B, H, S, D]; k, v [B, Hkv, S, D] in q's dtype; mask fp32 [S, S] or None."""
+    if not isinstance(q, torch.Tensor) or q.dim() != 4:
+        raise McError(_lib.MC_ERR_SHAPE, "q must be [batch, heads, seq, head_dim]")
+    _contig(q, "q")
+    _dtype_code(q)
+    B, H, S, D = q.shape
+    if not isinstance(k, torch.Tensor) or k.dim() != 4:
+        raise McError(_lib.MC_ERR_SHAPE, "k must be [batch, kv_heads, seq, head_dim]")
+    Hkv = k.shape[1]
+    _expect(k, "k", shape=(B, Hkv, S, D), dtype=q.dtype, device=q.device)
+    _expect(v, "v", shape=(B, Hkv, S, D), dtype=q.dtype, device=q.device)
+    _expect(mask, "mask", shape=(S, S), dtype=torch.float32, device=q.device)
+    return B, H, S, D
+
+
 def attention_forward(q, k, v, causal=False, scale=None, mask=None, save_lse=True):
     """Attention core of Attention::forward (src/models/transformer.rs:258-283):
     q [B, H, S, D], k, v [B, Hkv, S, D] -> (o [B, S, H*D], lse [B, H, S])."""
-    for t, n in ((q, "q"), (k, "k"), (v, "v"), (mask, "mask")):
-        _contig(t, n)
-    B, H, S, D = q.shape
+    B, H, S, D = _attn_inputs(q, k, v, mask)
     if scale is None:
         scale = D ** -0.5
     d = attention_desc(q, k, causal, scale)
@@ -147,9 +239,12 @@ def attention_forward(q, k, v, causal=False, scale=None, mask=None, save_lse=Tru
 
 def attention_backward(q, k, v, o, lse, dout, causal=False, scale=None, mask=None):
     """(dq, dk, dv) of attention_forward; o and lse come from the forward."""
-    for t, n in ((q, "q"), (k, "k"), (v, "v"), (o, "o"), (lse, "lse"), (dout, "dout"), (mask, "mask")):
-        _contig(t, n)
-    D = q.shape[-1]
+    B, H, S, D = _attn_inputs(q, k, v, mask)
+    _expect(o, "o", shape=(B, S, H * D), dtype=q.dtype, device=q.device)
+    _expect(dout, "dout", shape=(B, S, H * D), dtype=q.dtype, device=q.device)
+    _expect(lse, "lse", shape=(B, H, S), dtype=torch.float32, device=q.device)
+    if o is None or lse is None or dout is None:
+        raise McError(_lib.MC_ERR_NULL, "attention backward: o, lse and dout are required")
     if scale is None:
         scale = D ** -0.5
     d = attention_desc(q, k, causal, scale)
@@ -162,9 +257,10 @@ def attention_backward(q, k, v, o, lse, dout, causal=False, scale=None, mask=Non
 
 
 def layer_norm_forward(x, eps, w=None, b=None, save_stats=True):
-    """LayerNorm over the last dim: (y, mean, rstd)."""
-    D = x.shape[-1]
-    rows = x.numel() // D
+    """LayerNorm over the last dim: (y, mean, rstd). w, b [dim] in x's dtype or None."""
+    rows, D = _rows_of(x, "x")
+    _expect(w, "w", shape=(D,), dtype=x.dtype, device=x.device)
+    _expect(b, "b", shape=(D,), dtype=x.dtype, device=x.device)
     y = torch.empty_like(x)
     mean = torch.empty(rows, dtype=torch.float32, device=x.device) if save_stats else None
     rstd = torch.empty(rows, dtype=torch.float32, device=x.device) if save_stats else None
@@ -175,8 +271,11 @@ def layer_norm_forward(x, eps, w=None, b=None, save_stats=True):
 
 def layer_norm_backward(x, dy, eps, w=None, mean=None, rstd=None, need_dw=True, need_db=True):
     """(dx, dw, db) of LayerNorm; dw / db are fp32 [D] (None when not requested)."""
-    D = x.shape[-1]
-    rows = x.numel() // D
+    rows, D = _rows_of(x, "x")
+    _expect(dy, "dy", shape=x.shape, dtype=x.dtype, device=x.device)
+    _expect(w, "w", shape=(D,), dtype=x.dtype, device=x.device)
+    _expect(mean, "mean", shape=(rows,), dtype=torch.float32, device=x.device)
+    _expect(rstd, "rstd", shape=(rows,), dtype=torch.float32, device=x.device)
     dx = torch.empty_like(x)
     dw = torch.empty(D, dtype=torch.float32, device=x.device) if need_dw else None
     db = torch.empty(D, dtype=torch.float32, device=x.device) if need_db else None
@@ -188,30 +287,48 @@ def layer_norm_backward(x, dy, eps, w=None, mean=None, rstd=None, need_dw=True, 
 
 
 def log_softmax_forward(x):
-    D = x.shape[-1]
+    rows, D = _rows_of(x, "x")
     y = torch.empty_like(x)
-    check(lib().mc_log_softmax_fwd(x.numel() // D, D, _dtype_code(x), _ptr(x), _ptr(y), _stream(x)))
+    check(lib().mc_log_softmax_fwd(rows, D, _dtype_code(x), _ptr(x), _ptr(y), _stream(x)))
     return y
 
 
 def log_softmax_backward(y, dy):
-    D = y.shape[-1]
+    rows, D = _rows_of(y, "y")
+    _expect(dy, "dy", shape=y.shape, dtype=y.dtype, device=y.device)
     dx = torch.empty_like(y)
-    check(lib().mc_log_softmax_bwd(y.numel() // D, D, _dtype_code(y), _ptr(y), _ptr(dy), _ptr(dx), _stream(y)))
+    check(lib().mc_log_softmax_bwd(rows, D, _dtype_code(y), _ptr(y), _ptr(dy), _ptr(dx), _stream(y)))
     return dx
 
 
 def _xent_desc(logits, ignore_index, smoothing):
-    V = logits.shape[-1]
-    return XentDesc(logits.numel() // V, V, -1 if ignore_index is None else int(ignore_index), float(smoothing),
+    rows, V = _rows_of(logits, "logits")
+    return XentDesc(rows, V, -1 if ignore_index is None else int(ignore_index), float(smoothing),
                     _dtype_code(logits))
+
+
+def _targets(targets, logits):
+    """uint32 targets [rows] as the kernels read them: torch.uint32, or
+    torch.int32 (the same bytes for ids below 2^31); int64 ids are converted
+    explicitly (a copy), so their low 32 bits are what the kernels see."""
+    rows = logits.numel() // logits.shape[-1]
+    if not isinstance(targets, torch.Tensor):
+        raise McError(_lib.MC_ERR_NULL, "targets must be a tensor")
+    if targets.dtype == torch.int64:
+        targets = targets.to(torch.int32)
+    if targets.dtype not in (torch.int32, torch.uint32):
+        raise McError(_lib.MC_ERR_DTYPE, f"targets have dtype {targets.dtype}, expected uint32 (or int32 / int64 ids)")
+    _expect(targets, "targets", device=logits.device)
+    if targets.numel() != rows:
+        raise McError(_lib.MC_ERR_SHAPE, f"targets have {targets.numel()} entries, expected {rows} (one per row)")
+    return targets
 
 
 def cross_entropy_forward(logits, targets, ignore_index=None, smoothing=0.0):
     """cross_entropy_loss (src/training/loss.rs:58-245) over logits [..., V] and
     uint32 targets [...]: (loss fp32 [1], stats fp32 [rows + 1])."""
-    _contig(logits, "logits"), _contig(targets, "targets")
     d = _xent_desc(logits, ignore_index, smoothing)
+    targets = _targets(targets, logits)
     loss = torch.empty(1, dtype=torch.float32, device=logits.device)
     stats = torch.empty(d.rows + 1, dtype=torch.float32, device=logits.device)
     ws_n = lib().mc_cross_entropy_workspace_size(ctypes.byref(d))
@@ -224,8 +341,13 @@ def cross_entropy_forward(logits, targets, ignore_index=None, smoothing=0.0):
 def cross_entropy_backward(logits, targets, stats, dloss=None, ignore_index=None, smoothing=0.0):
     """d loss / d logits (times dloss, a fp32 [1] device tensor; default 1)."""
     d = _xent_desc(logits, ignore_index, smoothing)
+    targets = _targets(targets, logits)
+    _expect(stats, "stats", shape=(d.rows + 1,), dtype=torch.float32, device=logits.device)
+    if stats is None:
+        raise McError(_lib.MC_ERR_NULL, "stats from cross_entropy_forward are required")
     if dloss is None:
         dloss = torch.ones(1, dtype=torch.float32, device=logits.device)
+    _expect(dloss, "dloss", shape=(1,), dtype=torch.float32, device=logits.device)
     dlogits = torch.empty_like(logits)
     check(lib().mc_cross_entropy_bwd(ctypes.byref(d), _ptr(logits), _ptr(targets), _ptr(stats), _ptr(dloss),
                                      _ptr(dlogits), _stream(logits)))

@@ -1122,6 +1122,46 @@ CASE(checkpoint_hip_and_errors, true) {
     remove(path.c_str());
 }
 
+// Malformed headers are errors, never exceptions: numbers past 2^64, a bad
+// \u escape, a non-number loss, and a shape whose element count overflows
+// (the safetensors crate rejects all of them with a validation error).
+static void write_raw_safetensors(const std::string& path, std::string header, size_t data_bytes) {
+    while (header.size() % 8) header += ' ';
+    FILE* f = fopen(path.c_str(), "wb");
+    if (!f) return;
+    const uint64_t n = header.size();
+    unsigned char len[8];
+    for (int i = 0; i < 8; ++i) len[i] = (unsigned char)(n >> (8 * i));
+    fwrite(len, 1, 8, f);
+    fwrite(header.data(), 1, header.size(), f);
+    for (size_t i = 0; i < data_bytes; ++i) fputc(0, f);
+    fclose(f);
+}
+
+CASE(checkpoint_malformed_headers, false) {
+    const std::string path = tmp_path("mc_ckpt_bad.safetensors");
+    const char* bad[] = {
+        "{\"t\":{\"dtype\":\"F32\",\"shape\":[12345678901234567890123],\"data_offsets\":[0,0]}}",
+        "{\"a\\uZZZZ\":{\"dtype\":\"F32\",\"shape\":[1],\"data_offsets\":[0,4]}}",
+        "{\"t\":{\"dtype\":\"F32\",\"shape\":[4294967296,4294967296],\"data_offsets\":[0,0]}}",
+        "{\"t\":{\"dtype\":\"F32\",\"shape\":[1],\"data_offsets\":[0,99999999999999999999999]}}",
+    };
+    for (const char* h : bad) {
+        write_raw_safetensors(path, h, 4);
+        auto r = safetensors_load(path, kCpu);
+        CHECK(r.is_err());
+    }
+    // metadata with a loss that is not a number
+    write_raw_safetensors(path,
+                          "{\"__metadata__\":{\"checkpoint_metadata\":\"{\\\"global_step\\\":1,\\\"loss\\\":-,"
+                          "\\\"learning_rate\\\":0.1,\\\"timestamp\\\":1}\"},"
+                          "\"t\":{\"dtype\":\"F32\",\"shape\":[1],\"data_offsets\":[0,4]}}",
+                          4);
+    CHECK(safetensors_load(path, kCpu).is_ok());  // the container itself is valid
+    CHECK(read_checkpoint_metadata(path).is_err());
+    remove(path.c_str());
+}
+
 // The file format against the safetensors library: tests/test_checkpoint_cpu.py
 // writes py.safetensors with safetensors.numpy for the tensors below and runs
 // this case with MC_CKPT_DIR set; this case writes cpp.safetensors for the same
