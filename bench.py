@@ -47,13 +47,26 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
-# HBM bytes per base-GEMM launch (gemm_bf16_kernel / gemm_bf16_split, average
-# over a step's launches),
-# measured with two rocprofv3 --pmc passes (FETCH_SIZE, then WRITE_SIZE)
-# scaled by the same counters on a 256 MiB copy (--copy-calibration); the
-# summary and commands are in profiles/gemm_bf16_c4_hbm_traffic.md.
-# Re-measured whenever the GEMM's tiling changes; None for unmeasured configs.
-GEMM_TRAFFIC_BYTES = {"c4": 468.3e6}
+# HBM bytes per base-GEMM launch (average over a step's launches), measured
+# with two rocprofv3 --pmc passes (FETCH_SIZE, then WRITE_SIZE) scaled by the
+# same counters on a 256 MiB copy (--copy-calibration). The committed summary
+# profiles/gemm_bf16_<config>_hbm_traffic.md holds the figure on a line
+# "traffic_bytes_per_launch: <bytes> (source: <commit or build>)", re-measured
+# whenever the GEMM changes; read_gemm_traffic() takes it from there.
+def read_gemm_traffic(config):
+    path = os.path.join(ROOT, "profiles", f"gemm_bf16_{config}_hbm_traffic.md")
+    try:
+        with open(path) as f:
+            for ln in f:
+                if ln.startswith("traffic_bytes_per_launch:"):
+                    rest = ln.split(":", 1)[1].strip()
+                    value = float(rest.split()[0])
+                    src = rest[rest.find("(") + 1:rest.rfind(")")] if "(" in rest else ""
+                    return value, f"profiles/gemm_bf16_{config}_hbm_traffic.md ({src})"
+    except (OSError, ValueError):
+        pass
+    return None, None
+
 BF16_PEAK_TFLOPS = 2500.0
 FP32_PEAK_TFLOPS = 157.3
 
@@ -188,47 +201,97 @@ class Layer:
         return base, low
 
 
-def cpu_baseline(c, tokens, threads):
-    """The oracle (C, fp64 accumulation, OpenMP) on a token sample of the
-    same layer: LoRA fwd+bwd of every projection, both RMSNorms fwd+bwd and
-    the softmax rows of the sampled tokens. Returns tokens / second."""
-    import numpy as np
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
-    import oracle
 
-    rng = np.random.default_rng(0)
-    T = tokens
-    f32 = lambda *s, std=1.0: (rng.standard_normal(s) * std).astype(np.float32)  # noqa: E731
+def cpu_baseline(mc, c, tokens, threads, iters):
+    """The reference's CPU path for the same layer on a token sample, restated
+    with torch CPU fp32 ops in the candle composite's op order:
+      LoRA  H = x.A, Hd = dropout(H), y = x.W^T + b + (Hd.B).s
+            (src/training/lora.rs:320-339; candle_nn::Linear), and its
+            autograd: G = s dY.B^T (.) M/(1-p), dX = dY.W + G.A^T,
+            dA = x^T.G, dB = s Hd^T.dY (W frozen)
+      RMSNorm x / sqrt(mean(x^2) + eps) * w (src/backend/tensor.rs:111-117,
+            src/models/qwen.rs:314-325) and its closed-form gradient
+      softmax max, sub, exp, sum, div over the masked scores
+            (src/backend/tensor.rs:91-98, src/models/transformer.rs:264-275)
+            for the sampled tokens' rows, and dS = P (.) (dP - sum dP P).
+    The GEMMs run in torch's CPU BLAS (MKL / oneDNN), the elementwise ops
+    vectorised, on `threads` threads. Inputs are bf16-rounded values held in
+    fp32, as the GPU path sees them. Two warmup passes, then the median of
+    `iters` timed passes. Returns (tokens / second, median seconds)."""
+    import statistics
+
+    import torch
+
+    torch.set_num_threads(threads)
+    g = torch.Generator().manual_seed(0)
+    T, S, H = tokens, c["seq"], c["hidden"]
+    rb = lambda *shape, std=1.0: (torch.randn(*shape, generator=g) * std).bfloat16().float()  # noqa: E731
+    s, p = c["alpha"] / c["rank"], c["dropout"]
     work = []
-    for name, (K, N, bias) in proj_shapes(c).items():
+    for i, (name, (K, N, bias)) in enumerate(proj_shapes(c).items()):
         b = 1.0 / K ** 0.5
-        work.append(dict(x=f32(T, K), W=f32(N, K, std=0.02), bias=f32(N, std=0.02) if bias else None,
-                         A=((rng.random((K, c["rank"])) * 2 - 1) * b).astype(np.float32),
-                         B=f32(c["rank"], N, std=0.02), dy=f32(T, N, std=1e-2),
-                         mask=oracle.dropout_mask(1234, c["dropout"], T, c["rank"]) if c["dropout"] > 0 else None))
-    H = c["hidden"]
-    xs, dys, w = f32(T, H), f32(T, H, std=1e-2), f32(H, std=0.1) + 1
-    S = c["seq"]
+        # the same host-generated keep-masks as the GPU step (seed 1234 + index)
+        mask = mc.dropout_mask(1234 + i, p, T, c["rank"]).float() / (1.0 - p) if p > 0 else None
+        work.append(dict(x=rb(T, K), W=rb(N, K, std=0.02), bias=rb(N, std=0.02) if bias else None,
+                         A=(torch.rand(K, c["rank"], generator=g) * 2 - 1) * b, B=rb(c["rank"], N, std=0.02),
+                         dy=rb(T, N, std=1e-2), mask=mask))
+    xs, dys, w = rb(T, H), rb(T, H, std=1e-2), rb(H, std=0.1) + 1.0
     srows = T * c["heads"] if c["softmax"] else 0
-    scores = f32(srows, S, std=3.0) if srows else None
-    dP = f32(srows, S, std=1e-2) if srows else None
-    ids = (np.arange(srows) % S).astype(np.int64) if srows else None
-    s = c["alpha"] / c["rank"]
-    t0 = time.perf_counter()
-    for wk in work:
-        oracle.lora_fwd(wk["x"], wk["A"], wk["B"], s, W=wk["W"], bias=wk["bias"], mask=wk["mask"],
-                        p=c["dropout"], threads=threads)
-        oracle.lora_bwd(wk["x"], wk["A"], wk["B"], wk["dy"], s, W=wk["W"], mask=wk["mask"], p=c["dropout"],
-                        threads=threads)
-    if c["norm"]:
-        for _ in range(2):
-            oracle.rmsnorm_fwd(xs, 1e-6, w, threads=threads)
-            oracle.rmsnorm_bwd(xs, dys, 1e-6, w, threads=threads)
     if srows:
-        P = oracle.softmax_fwd(scores, causal_rows=S, threads=threads, row_ids=ids)
-        oracle.softmax_bwd(P, dP, causal_rows=S, threads=threads, row_ids=ids)
-    dt = time.perf_counter() - t0
-    return T / dt, dt
+        scores, dP = rb(c["heads"], T, S, std=3.0), rb(c["heads"], T, S, std=1e-2)
+        q = torch.arange(T)[:, None] % S
+        neg = torch.zeros(T, S).masked_fill(torch.arange(S)[None, :] > q, float("-inf"))
+
+    def one_pass():
+        for wk in work:
+            x, W, A, B, dy, m = wk["x"], wk["W"], wk["A"], wk["B"], wk["dy"], wk["mask"]
+            hd = x @ A
+            if m is not None:
+                hd = hd * m
+            y = torch.addmm(wk["bias"], x, W.t()) if wk["bias"] is not None else x @ W.t()
+            y += (hd @ B) * s
+            gd = (dy @ B.t()) * s
+            if m is not None:
+                gd = gd * m
+            dx = dy @ W + gd @ A.t()
+            dA = x.t() @ gd
+            dB = (hd.t() @ dy) * s
+            del y, dx, dA, dB
+        if c["norm"]:
+            for _ in range(2):
+                r = torch.rsqrt((xs * xs).mean(-1, keepdim=True) + 1e-6)
+                y = xs * r * w
+                gw = dys * w
+                dx = r * gw - xs * (r ** 3) * (gw * xs).mean(-1, keepdim=True)
+                dw = (dys * xs * r).sum(0)
+                del y, dx, dw
+        if srows:
+            z = scores + neg
+            z = z - z.amax(-1, keepdim=True)
+            e = z.exp()
+            P = e / e.sum(-1, keepdim=True)
+            dS = P * (dP - (dP * P).sum(-1, keepdim=True))
+            del P, dS
+
+    for _ in range(2):
+        one_pass()
+    times = []
+    for _ in range(iters):
+        t0 = time.perf_counter()
+        one_pass()
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    return T / med, med
 
 
 def queue_ahead(torch):
@@ -348,13 +411,56 @@ def row_ops(mc, c, dev, iters):
     return out
 
 
+def c2_row_ops(mc, dev, iters):
+    """BASELINE config c2 (fp32): RMSNorm over [8192, 896] (weight ~N(1, 0.1),
+    eps 1e-6) and the causal softmax over [8, 14, 1024, 1024] scores ~N(0, 3),
+    fwd and bwd, each timed per call by the library's profiling hook. GB/s
+    counts the algorithmic bytes (RMSNorm fwd: read x, write y, rstd; bwd:
+    read x, dy, write dx; softmax: the unmasked part read, every row written;
+    bwd reads P and dP over the unmasked part)."""
+    import torch
+
+    g = torch.Generator(device=dev).manual_seed(2)
+    x = torch.randn(8192, 896, device=dev, generator=g)
+    w = torch.randn(896, device=dev, generator=g) * 0.1 + 1.0
+    dy = torch.randn(8192, 896, device=dev, generator=g)
+    sc = torch.randn(8, 14, 1024, 1024, device=dev, generator=g) * 3.0
+    dP = torch.randn(8, 14, 1024, 1024, device=dev, generator=g) * 1e-2
+    _, rstd = mc.rms_norm_forward(x, 1e-6, w)
+    P = mc.softmax_forward(sc, causal_rows=1024)
+    calls = {
+        "rmsnorm_fwd": ("rmsnorm", lambda: mc.rms_norm_forward(x, 1e-6, w)),
+        "rmsnorm_bwd": ("rmsnorm", lambda: mc.rms_norm_backward(x, dy, 1e-6, w, rstd)),
+        "softmax_fwd": ("softmax", lambda: mc.softmax_forward(sc, causal_rows=1024)),
+        "softmax_bwd": ("softmax", lambda: mc.softmax_backward(P, dP, causal_rows=1024)),
+    }
+    out = {"rmsnorm_shape": [8192, 896], "softmax_shape": [8, 14, 1024, 1024], "dtype": "f32", "iters": iters}
+    for name, (kind, fn) in calls.items():
+        fn()
+        torch.cuda.synchronize()
+        mc._lib.check(mc._lib.lib().mc_profile_reset())
+        mc._lib.check(mc._lib.lib().mc_profile_enable(1))
+        queue_ahead(torch)
+        for _ in range(iters):
+            fn()
+        torch.cuda.synchronize()
+        mc._lib.check(mc._lib.lib().mc_profile_enable(0))
+        mc._lib.check(mc._lib.lib().mc_profile_collect())
+        ms, n, _, by = mc._lib.profile_read(kind)
+        out[name] = {"us_per_call": ms * 1e3 / n, "GB_s": by / (ms * 1e-3) / 1e9,
+                     "hbm_frac": by / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+    del sc, dP, P
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="c4", choices=sorted(CONFIGS))
-    ap.add_argument("--cpu-tokens", type=int, default=2048, help="token sample of the CPU-oracle baseline")
+    ap.add_argument("--cpu-tokens", type=int, default=2048, help="token sample of the CPU baseline")
+    ap.add_argument("--cpu-iters", type=int, default=10, help="timed passes of the CPU baseline (median)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--graph", action="store_true", help="time HIP graph replays of one captured step")
     ap.add_argument("--attention-iters", type=int, default=5,
@@ -460,7 +566,8 @@ def main():
             "peak": BF16_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": achieved / BF16_PEAK_TFLOPS,
-            "traffic": GEMM_TRAFFIC_BYTES.get(args.config),
+            "traffic": read_gemm_traffic(args.config)[0],
+            "traffic_source": read_gemm_traffic(args.config)[1],
         },
         "layer_TFLOP_s": (base_fl + low_fl) / (ms_step * 1e-3) / 1e12,
         "launch": "hip_graph" if args.graph else "eager",
@@ -471,13 +578,17 @@ def main():
     if args.attention_iters > 0:
         line["adamw"] = adamw_update(mc, c, dev, 20)
         line["row_ops"] = row_ops(mc, c, dev, args.attention_iters)
+    line["c2_row_ops_f32"] = c2_row_ops(mc, dev, 5)
     if not args.no_cpu_baseline:
         threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
-        v, dt = cpu_baseline(c, args.cpu_tokens, threads)
+        v, dt = cpu_baseline(mc, c, args.cpu_tokens, threads, args.cpu_iters)
         line["cpu_baseline"] = {
             "value": v, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "cpu": cpu_model(),
             "sample": f"{args.cpu_tokens} tokens of the same layer (LoRA fwd+bwd x{len(c['projections'])}, "
-                      f"RMSNorm fwd+bwd x2, softmax rows of those tokens) through the C oracle, {dt:.1f} s",
+                      f"RMSNorm fwd+bwd x2, causal softmax fwd+bwd of those tokens' score rows), torch CPU fp32 "
+                      f"composite in the reference's op order (BLAS GEMMs), median of {args.cpu_iters} passes "
+                      f"after 2 warmup passes: {dt * 1e3:.1f} ms per pass",
         }
     print(json.dumps(line))
 
