@@ -106,10 +106,11 @@ def proj_shapes(c):
 class Layer:
     """Device-resident tensors of one layer's custom ops."""
 
-    def __init__(self, mc, c, dev, seed=0):
+    def __init__(self, mc, c, dev, seed=0, group=True):
         import torch
 
         self.mc, self.c, self.dev = mc, c, dev
+        self.group = group
         self.T = c["batch"] * c["seq"]
         dt = torch.bfloat16 if c["dtype"] == "bf16" else torch.float32
         g = torch.Generator(device=dev).manual_seed(seed)
@@ -153,36 +154,58 @@ class Layer:
         return self.act
 
     def step(self):
+        """One forward + backward of the layer's custom ops. The projections
+        that read the same input (q / k / v, gate / up) run as one grouped
+        call each (mc_lora_group_fwd / _bwd: one pass over the input per
+        rank-r pass, one GEMM launch, dX summed over the group) unless the
+        layer was built with group=False."""
         mc, c = self.mc, self.c
         saved = {}
         if c["norm"]:
             self.xn1, r1 = mc.rms_norm_forward(self.h_in, 1e-6, self.ln1)
-        order_f = [p for p in ("q", "k", "v") if p in self.proj]
-        for name in order_f:
-            saved[name] = self._lora_f(name)
+        attn_in = [p for p in ("q", "k", "v") if p in self.proj]
+        mlp_in = [p for p in ("gate", "up") if p in self.proj]
+        self._fwd(attn_in, saved)
         P = mc.softmax_forward(self.scores, causal_rows=c["seq"]) if c["softmax"] else None
-        if "o" in self.proj:
-            saved["o"] = self._lora_f("o")
+        self._fwd([p for p in ("o",) if p in self.proj], saved)
         if c["norm"]:
             self.xn2, r2 = mc.rms_norm_forward(self.h_mid, 1e-6, self.ln2)
-        for name in ("gate", "up", "down"):
-            if name in self.proj:
-                saved[name] = self._lora_f(name)
+        self._fwd(mlp_in, saved)
+        self._fwd([p for p in ("down",) if p in self.proj], saved)
         # backward
-        for name in ("down", "up", "gate"):
-            if name in self.proj:
-                self._lora_b(name, saved[name])
+        self._bwd([p for p in ("down",) if p in self.proj], saved)
+        self._bwd(mlp_in, saved)
         if c["norm"]:
             mc.rms_norm_backward(self.h_mid, self.dy_ln, 1e-6, self.ln2, r2)
-        if "o" in self.proj:
-            self._lora_b("o", saved["o"])
+        self._bwd([p for p in ("o",) if p in self.proj], saved)
         if c["softmax"]:
             mc.softmax_backward(P, self.dP, causal_rows=c["seq"])
-        for name in ("v", "k", "q"):
-            if name in self.proj:
-                self._lora_b(name, saved[name])
+        self._bwd(attn_in, saved)
         if c["norm"]:
             mc.rms_norm_backward(self.h_in, self.dy_ln, 1e-6, self.ln1, r1)
+
+    def _fwd(self, names, saved):
+        if not names:
+            return
+        if len(names) == 1 or not self.group:
+            for name in names:
+                saved[name] = self._lora_f(name)
+            return
+        _, hs = self.mc.lora_group_forward(self._input_of(names[0]), [self.proj[n] for n in names], self.scale,
+                                           dropout_p=self.p)
+        for name, h in zip(names, hs):
+            saved[name] = h
+
+    def _bwd(self, names, saved):
+        if not names:
+            return
+        if len(names) == 1 or not self.group:
+            for name in names:
+                self._lora_b(name, saved[name])
+            return
+        self.mc.lora_group_backward(self._input_of(names[0]), [self.proj[n] for n in names],
+                                    [self.proj[n]["dy"] for n in names], self.scale, dropout_p=self.p,
+                                    h_saves=[saved[n] for n in names])
 
     def _lora_f(self, name):
         pr = self.proj[name]
@@ -463,6 +486,8 @@ def main():
     ap.add_argument("--cpu-iters", type=int, default=10, help="timed passes of the CPU baseline (median)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--graph", action="store_true", help="time HIP graph replays of one captured step")
+    ap.add_argument("--no-group", action="store_true",
+                    help="run q/k/v and gate/up as separate per-projection calls instead of grouped calls")
     ap.add_argument("--attention-iters", type=int, default=5,
                     help="calls of the attention core fwd / bwd timed after the step (0: skip)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
@@ -481,7 +506,7 @@ def main():
     mc = __graft_entry__.load_package()
     dev = torch.device("cuda:0")
     c = CONFIGS[args.config]
-    layer = Layer(mc, c, dev)
+    layer = Layer(mc, c, dev, group=not args.no_group)
     if args.copy_calibration > 0:
         src = torch.empty(args.copy_calibration // 2, dtype=torch.bfloat16, device=dev).fill_(1.0)
         dst = torch.empty_like(src)
@@ -571,6 +596,7 @@ def main():
         },
         "layer_TFLOP_s": (base_fl + low_fl) / (ms_step * 1e-3) / 1e12,
         "launch": "hip_graph" if args.graph else "eager",
+        "projections": "per-projection calls" if args.no_group else "grouped calls for q/k/v and gate/up",
         "kernels": kernels,
     }
     if args.attention_iters > 0 and c["softmax"]:

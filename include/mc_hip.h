@@ -118,6 +118,48 @@ mc_status mc_lora_bwd(const mc_lora_desc* d, const void* x, const void* W, const
                       const void* dY, void* dX, float* dA, float* dB,
                       void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* Grouped projections of one input: the LoRA linears that read the same x,
+ * as the q, k and v projections of the attention's normalised input and the
+ * gate and up projections of the MLP's (src/models/transformer.rs:241-243,
+ * 389-395), each with its own frozen W, bias, A, B and mask, sharing T, K,
+ * rank, scale, dropout_p and act_dtype (the layer's LoRAConfig). No
+ * reference kernel: an additive entry point for a caller that holds a
+ * layer's projections. bf16 only (MC_ERR_DTYPE otherwise); 1 <= count <=
+ * MC_LORA_MAX_GROUP; desc->out_features is not used. */
+#define MC_LORA_MAX_GROUP 4
+typedef struct mc_lora_proj {
+    int64_t out_features;   /* N_g >= 1, multiple of 8 */
+    const void* W;          /* [N_g, K] frozen base weight, or NULL (delta only) */
+    const void* bias;       /* [N_g] or NULL (requires W) */
+    const float* A;         /* [K, r] */
+    const float* B;         /* [r, N_g] */
+    const uint8_t* mask;    /* [T, r] keep-mask, required iff dropout_p > 0 */
+} mc_lora_proj;
+
+size_t mc_lora_group_fwd_workspace_size(const mc_lora_desc* d, const mc_lora_proj* projs, int32_t count);
+size_t mc_lora_group_bwd_workspace_size(const mc_lora_desc* d, const mc_lora_proj* projs, int32_t count);
+
+/* y[g] = x W_g^T + bias_g + scale ((x A_g) (.) mask_g / (1-p)) B_g for every
+ * g < count; h_save (or any entry) may be NULL, else h_save[g] [r, T]
+ * receives Hd_g^T as in mc_lora_fwd. The results equal count calls of
+ * mc_lora_fwd bit for bit; x is read once per row-projection pass (up to 64
+ * ranks of whole projections) and all the projections' base products run in
+ * one GEMM launch. */
+mc_status mc_lora_group_fwd(const mc_lora_desc* d, const void* x, const mc_lora_proj* projs, int32_t count,
+                            void* const* y, float* const* h_save, void* workspace, size_t workspace_bytes,
+                            hipStream_t stream);
+
+/* Backward of mc_lora_group_fwd with every W frozen:
+ *   dX    = sum_g (dY_g W_g + Gd_g A_g^T)   [T, K], the gradient of the shared
+ *           input (candle autograd sums the projections' contributions), as
+ *           one GEMM over the concatenated reduction; may be NULL
+ *   dA[g] = x^T Gd_g, dB[g] = scale Hd_g^T dY_g, each equal bit for bit to
+ *           mc_lora_bwd's; dA / dB or any entry may be NULL (not computed)
+ * h_save[g] is required where dB[g] is requested, x where any dA is. */
+mc_status mc_lora_group_bwd(const mc_lora_desc* d, const void* x, const mc_lora_proj* projs, int32_t count,
+                            const float* const* h_save, const void* const* dY, void* dX, float* const* dA,
+                            float* const* dB, void* workspace, size_t workspace_bytes, hipStream_t stream);
+
 /* RMSNorm over the last dim of x [rows, dim]:
  *   y = x / sqrt(mean(x^2) + eps) * w     (w == NULL: no weight, as FusedRMSNormOp)
  * x, w, y in dtype; rstd [rows] fp32 (may be NULL) receives 1/sqrt(mean + eps). */

@@ -21,6 +21,8 @@ from .ops import (  # noqa: F401
     log_softmax_forward,
     lora_backward,
     lora_forward,
+    lora_group_backward,
+    lora_group_forward,
     rms_norm_backward,
     rms_norm_forward,
     softmax_backward,

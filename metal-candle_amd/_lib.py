@@ -50,6 +50,20 @@ class LoraDesc(ctypes.Structure):
     ]
 
 
+class LoraProj(ctypes.Structure):
+    _fields_ = [
+        ("out_features", ctypes.c_int64),
+        ("W", ctypes.c_void_p),
+        ("bias", ctypes.c_void_p),
+        ("A", ctypes.c_void_p),
+        ("B", ctypes.c_void_p),
+        ("mask", ctypes.c_void_p),
+    ]
+
+
+MC_LORA_MAX_GROUP = 4
+
+
 class AttnDesc(ctypes.Structure):
     _fields_ = [
         ("batch", ctypes.c_int64),
@@ -110,6 +124,13 @@ _SIGNATURES = {
     "mc_lora_bwd_workspace_size": (_sz, [_dp]),
     "mc_lora_fwd": (ctypes.c_int, [_dp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "mc_lora_bwd": (ctypes.c_int, [_dp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "mc_lora_group_fwd_workspace_size": (_sz, [_dp, ctypes.POINTER(LoraProj), _i32]),
+    "mc_lora_group_bwd_workspace_size": (_sz, [_dp, ctypes.POINTER(LoraProj), _i32]),
+    "mc_lora_group_fwd": (ctypes.c_int, [_dp, _vp, ctypes.POINTER(LoraProj), _i32, ctypes.POINTER(_vp),
+                                         ctypes.POINTER(_vp), _vp, _sz, _vp]),
+    "mc_lora_group_bwd": (ctypes.c_int, [_dp, _vp, ctypes.POINTER(LoraProj), _i32, ctypes.POINTER(_vp),
+                                         ctypes.POINTER(_vp), _vp, ctypes.POINTER(_vp), ctypes.POINTER(_vp), _vp,
+                                         _sz, _vp]),
     "mc_rmsnorm_fwd": (ctypes.c_int, [_i64, _i64, _f32, _i32, _vp, _vp, _vp, _vp, _vp]),
     "mc_rmsnorm_bwd_workspace_size": (_sz, [_i64, _i64]),
     "mc_rmsnorm_bwd": (ctypes.c_int, [_i64, _i64, _f32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),

@@ -210,6 +210,119 @@ mc_status mc_lora_bwd(const mc_lora_desc* d, const void* x, const void* W, const
                       "LoRA backward");
 }
 
+}  // extern "C"
+
+namespace {
+
+// A grouped call's descriptor and projection table: the shared T, K, r,
+// scale, p and dtype as for one projection, then every projection's N; the
+// group runs the bf16 kernels only.
+mc_status check_lora_group(const mc_lora_desc* d, const mc_lora_proj* projs, int32_t count, const char* op,
+                           mc_lora_desc* per_proj, int64_t* Ns) {
+    MC_CHECK(d != nullptr, MC_ERR_NULL, "%s: descriptor is NULL", op);
+    MC_CHECK(projs != nullptr, MC_ERR_NULL, "%s: projection table is NULL", op);
+    MC_CHECK(count >= 1 && count <= MC_LORA_MAX_GROUP, MC_ERR_SHAPE, "%s: count must be in [1, %d], got %d", op,
+             MC_LORA_MAX_GROUP, (int)count);
+    MC_CHECK(d->act_dtype == MC_BF16, MC_ERR_DTYPE,
+             "%s: grouped projections run in bf16 only (act_dtype %d); use mc_lora_fwd / mc_lora_bwd per projection",
+             op, (int)d->act_dtype);
+    for (int32_t g = 0; g < count; ++g) {
+        *per_proj = *d;
+        per_proj->out_features = projs[g].out_features;
+        mc_status s = check_lora_desc(per_proj);
+        if (s != MC_OK) return s;
+        MC_CHECK(projs[g].A && projs[g].B, MC_ERR_NULL, "%s: projection %d: A and B must not be NULL", op, (int)g);
+        MC_CHECK(!projs[g].bias || projs[g].W, MC_ERR_NULL, "%s: projection %d: bias given without W", op, (int)g);
+        MC_CHECK(d->dropout_p == 0.0f || projs[g].mask, MC_ERR_NULL,
+                 "%s: projection %d: dropout_p > 0 requires a mask", op, (int)g);
+        MC_CHECK(!projs[g].W || aligned16(projs[g].W), MC_ERR_LAYOUT, "%s: projection %d: W must be 16-byte aligned",
+                 op, (int)g);
+        Ns[g] = projs[g].out_features;
+    }
+    *per_proj = *d;
+    per_proj->out_features = projs[0].out_features;
+    return MC_OK;
+}
+
+void to_lora_proj(const mc_lora_proj* projs, int32_t count, mc::LoraProj* out) {
+    for (int32_t g = 0; g < count; ++g)
+        out[g] = mc::LoraProj{projs[g].out_features, projs[g].W, projs[g].bias, projs[g].A, projs[g].B, projs[g].mask};
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t mc_lora_group_fwd_workspace_size(const mc_lora_desc* d, const mc_lora_proj* projs, int32_t count) {
+    mc_lora_desc dd;
+    int64_t Ns[MC_LORA_MAX_GROUP];
+    if (check_lora_group(d, projs, count, "LoRA group forward", &dd, Ns) != MC_OK) return 0;
+    return mc::lora_group_fwd_ws(dd, Ns, count).total;
+}
+
+size_t mc_lora_group_bwd_workspace_size(const mc_lora_desc* d, const mc_lora_proj* projs, int32_t count) {
+    mc_lora_desc dd;
+    int64_t Ns[MC_LORA_MAX_GROUP];
+    if (check_lora_group(d, projs, count, "LoRA group backward", &dd, Ns) != MC_OK) return 0;
+    return mc::lora_group_bwd_ws(dd, Ns, count).total;
+}
+
+mc_status mc_lora_group_fwd(const mc_lora_desc* d, const void* x, const mc_lora_proj* projs, int32_t count,
+                            void* const* y, float* const* h_save, void* workspace, size_t workspace_bytes,
+                            hipStream_t stream) {
+    mc_lora_desc dd;
+    int64_t Ns[MC_LORA_MAX_GROUP];
+    mc_status s = check_lora_group(d, projs, count, "LoRA group forward", &dd, Ns);
+    if (s != MC_OK) return s;
+    MC_CHECK(x && y, MC_ERR_NULL, "LoRA group forward: x and y must not be NULL");
+    MC_CHECK(aligned16(x), MC_ERR_LAYOUT, "LoRA group forward: x must be 16-byte aligned");
+    for (int32_t g = 0; g < count; ++g) {
+        MC_CHECK(y[g], MC_ERR_NULL, "LoRA group forward: y[%d] must not be NULL", (int)g);
+        MC_CHECK(aligned16(y[g]) && (!h_save || !h_save[g] || aligned16(h_save[g])), MC_ERR_LAYOUT,
+                 "LoRA group forward: y[%d] and h_save[%d] must be 16-byte aligned", (int)g, (int)g);
+    }
+    const size_t need = mc::lora_group_fwd_ws(dd, Ns, count).total;
+    MC_CHECK(workspace_bytes >= need && workspace, MC_ERR_WORKSPACE,
+             "LoRA group forward: workspace of %zu bytes required, %zu given", need, workspace_bytes);
+    MC_CHECK(aligned16(workspace), MC_ERR_LAYOUT, "LoRA group forward: workspace must be 16-byte aligned");
+    mc::LoraProj lp[MC_LORA_MAX_GROUP];
+    to_lora_proj(projs, count, lp);
+    return hip_status(mc::launch_lora_group_fwd(dd, x, lp, count, y, h_save, workspace, stream), "LoRA group forward");
+}
+
+mc_status mc_lora_group_bwd(const mc_lora_desc* d, const void* x, const mc_lora_proj* projs, int32_t count,
+                            const float* const* h_save, const void* const* dY, void* dX, float* const* dA,
+                            float* const* dB, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    mc_lora_desc dd;
+    int64_t Ns[MC_LORA_MAX_GROUP];
+    mc_status s = check_lora_group(d, projs, count, "LoRA group backward", &dd, Ns);
+    if (s != MC_OK) return s;
+    MC_CHECK(dY, MC_ERR_NULL, "LoRA group backward: dY must not be NULL");
+    bool any = dX != nullptr;
+    for (int32_t g = 0; g < count; ++g) {
+        MC_CHECK(dY[g], MC_ERR_NULL, "LoRA group backward: dY[%d] must not be NULL", (int)g);
+        MC_CHECK(aligned16(dY[g]), MC_ERR_LAYOUT, "LoRA group backward: dY[%d] must be 16-byte aligned", (int)g);
+        const bool wa = dA && dA[g], wb = dB && dB[g];
+        MC_CHECK(!wa || x, MC_ERR_NULL, "LoRA group backward: dA requires x");
+        MC_CHECK(!wb || (h_save && h_save[g]), MC_ERR_NULL,
+                 "LoRA group backward: dB[%d] requires h_save[%d] from the forward", (int)g, (int)g);
+        MC_CHECK(!wb || aligned16(h_save[g]), MC_ERR_LAYOUT, "LoRA group backward: h_save[%d] must be 16-byte aligned",
+                 (int)g);
+        any = any || wa || wb;
+    }
+    MC_CHECK((!x || aligned16(x)) && (!dX || aligned16(dX)), MC_ERR_LAYOUT,
+             "LoRA group backward: x and dX must be 16-byte aligned");
+    const size_t need = mc::lora_group_bwd_ws(dd, Ns, count).total;
+    MC_CHECK(workspace_bytes >= need && workspace, MC_ERR_WORKSPACE,
+             "LoRA group backward: workspace of %zu bytes required, %zu given", need, workspace_bytes);
+    MC_CHECK(aligned16(workspace), MC_ERR_LAYOUT, "LoRA group backward: workspace must be 16-byte aligned");
+    if (!any) return ok();
+    mc::LoraProj lp[MC_LORA_MAX_GROUP];
+    to_lora_proj(projs, count, lp);
+    return hip_status(mc::launch_lora_group_bwd(dd, x, lp, count, h_save, dY, dX, dA, dB, workspace, stream),
+                      "LoRA group backward");
+}
+
 mc_status mc_rmsnorm_fwd(int64_t rows, int64_t dim, float eps, int32_t dtype, const void* x, const void* w,
                          void* y, float* rstd, hipStream_t stream) {
     mc_status s = check_rows(rows, dim, "RMSNorm");

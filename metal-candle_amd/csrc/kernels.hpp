@@ -53,6 +53,43 @@ struct LoraBwdWs {
 LoraFwdWs lora_fwd_ws(const mc_lora_desc& d);
 LoraBwdWs lora_bwd_ws(const mc_lora_desc& d);
 
+// Grouped projections of one input (bf16): up to kLoraMaxProj projections
+// sharing x, T, K, r, scale and p. Workspace layouts (byte offsets).
+constexpr int kLoraMaxProj = 4;
+struct LoraProj {
+    int64_t N;
+    const void* W;
+    const void* bias;
+    const float* A;
+    const float* B;
+    const uint8_t* mask;
+};
+struct LoraGroupFwdWs {
+    size_t at_hilo[kLoraMaxProj];  // per row-projection pass: bf16 [2][16 rc][K]
+    size_t bt_ext[kLoraMaxProj];   // per projection: bf16 [N_g][rext]
+    size_t hs_ext;                 // bf16 [T][G rext]: s Hd of every projection
+    size_t total;
+};
+struct LoraGroupBwdWs {
+    size_t wt[kLoraMaxProj];       // per projection: bf16 [K][N_g] W_g^T
+    size_t at_ext;                 // bf16 [K][G rext]: A of every projection
+    size_t gd_ext;                 // bf16 [T][G rext]: Gd of every projection
+    size_t gd_t;                   // f32 [G r][T]: Gd^T of every projection
+    size_t part_a;                 // f32 [S_a][colreduce rows of G r][K]
+    size_t part_b[kLoraMaxProj];   // f32 [S_b][colreduce rows of r][N_g]
+    size_t total;
+};
+LoraGroupFwdWs lora_group_fwd_ws(const mc_lora_desc& d, const int64_t* N, int count);
+LoraGroupBwdWs lora_group_bwd_ws(const mc_lora_desc& d, const int64_t* N, int count);
+hipError_t launch_lora_group_fwd(const mc_lora_desc& d, const void* x, const LoraProj* proj, int count,
+                                 void* const* y, float* const* h_save, void* ws, hipStream_t stream);
+// dX (may be null) receives the sum over the projections; dA / dB (arrays,
+// or null; entries may be null) per projection; h_save[g] is required where
+// dB[g] is requested.
+hipError_t launch_lora_group_bwd(const mc_lora_desc& d, const void* x, const LoraProj* proj, int count,
+                                 const float* const* h_save, const void* const* dY, void* dX, float* const* dA,
+                                 float* const* dB, void* ws, hipStream_t stream);
+
 hipError_t launch_lora_fwd(const mc_lora_desc& d, const void* x, const void* W, const void* bias,
                            const float* A, const float* B, const uint8_t* mask, void* y,
                            float* h_save, void* ws, hipStream_t stream);

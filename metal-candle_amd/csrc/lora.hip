@@ -54,8 +54,7 @@ Dims dims_of(const mc_lora_desc& d) {
     m.K = d.in_features;
     m.N = d.out_features;
     m.r = d.rank;
-    // MFMA rank tiles: 16, 32, 64 or 128 rows (the rowproj instantiations)
-    m.r16 = d.rank <= 16 ? 16 : d.rank <= 32 ? 32 : d.rank <= 64 ? 64 : 128;
+    m.r16 = 16 * rowproj_rc(d.rank);  // rank rows of the row projection's parameter operand
     m.rext = (int)round_up(d.rank, 8);
     m.bf16 = d.act_dtype == MC_BF16;
     return m;
@@ -81,6 +80,26 @@ prof::Scope lowrank_scope(hipStream_t st, int64_t T, int64_t C, int r, int es) {
         if (e_ != hipSuccess) return e_;      \
     } while (0)
 
+// Projections of one row-projection pass of a grouped forward: whole
+// projections, at most 64 ranks together (the 64-row workgroups of the row
+// projection; more ranks take the 32-row form, which loads each parameter
+// fragment for half as many token rows), at least one.
+int proj_per_pass(int r) { return r >= 64 ? 1 : 64 / r < kMaxProj ? 64 / r : kMaxProj; }
+
+PrepJob prep_job(const float* src, int64_t ld_src, int64_t valid_rows, int64_t valid_cols, bool transpose,
+                 uint16_t* hi, uint16_t* lo, int64_t rows_out, int64_t cols_out, int64_t ld_out = 0) {
+    PrepJob j{};
+    j.src = src; j.ld_src = ld_src; j.valid_rows = valid_rows; j.valid_cols = valid_cols; j.transpose = transpose;
+    j.hi = hi; j.lo = lo; j.rows_out = rows_out; j.cols_out = cols_out; j.ld_out = ld_out;
+    return j;
+}
+
+hipError_t prep_all(const PrepJob* jobs, int n, hipStream_t st) {
+    for (int first = 0; first < n; first += kPrepJobs)
+        MC_TRY(launch_prep_bf16(jobs + first, n - first < kPrepJobs ? n - first : kPrepJobs, st));
+    return hipSuccess;
+}
+
 }  // namespace
 
 LoraFwdWs lora_fwd_ws(const mc_lora_desc& d) {
@@ -104,17 +123,55 @@ LoraBwdWs lora_bwd_ws(const mc_lora_desc& d) {
     const Dims m = dims_of(d);
     LoraBwdWs w{};
     size_t off = 0;
-    if (m.bf16) {
-        w.wt = off;     off += align256((size_t)m.K * m.N * 2);
-        w.at_ext = off; off += align256((size_t)m.K * m.rext * 2);
-        w.gd_ext = off; off += align256((size_t)m.T * m.rext * 2);
-        w.gd_t = off;   off += align256((size_t)m.r * m.T * 4);
-        w.part_a = off; off += align256((size_t)colreduce_splits(m.T, m.K) * m.r16 * m.K * 4);
-        w.part_b = off; off += align256((size_t)colreduce_splits(m.T, m.N) * m.r16 * m.N * 4);
+    if (m.bf16) {  // the bf16 backward runs as a grouped backward of one projection
+        const int64_t N = m.N;
+        const LoraGroupBwdWs g = lora_group_bwd_ws(d, &N, 1);
+        w.wt = g.wt[0]; w.at_ext = g.at_ext; w.gd_ext = g.gd_ext; w.gd_t = g.gd_t;
+        w.part_a = g.part_a; w.part_b = g.part_b[0];
+        off = g.total;
     } else {
         w.at_ext = off; off += align256((size_t)m.r * m.K * 4);
         w.gd_ext = off; off += align256((size_t)m.T * m.r * 4);
         w.gd_t = off;   off += align256((size_t)m.r * m.T * 4);
+    }
+    w.total = off;
+    return w;
+}
+
+LoraGroupFwdWs lora_group_fwd_ws(const mc_lora_desc& d, const int64_t* N, int count) {
+    const Dims m = dims_of(d);
+    LoraGroupFwdWs w{};
+    size_t off = 0;
+    const int ppp = proj_per_pass(m.r);
+    for (int p0 = 0, pass = 0; p0 < count; p0 += ppp, ++pass) {
+        const int np = count - p0 < ppp ? count - p0 : ppp;
+        w.at_hilo[pass] = off;
+        off += align256((size_t)2 * 16 * rowproj_rc(np * m.r) * m.K * 2);
+    }
+    for (int g = 0; g < count; ++g) {
+        w.bt_ext[g] = off;
+        off += align256((size_t)N[g] * m.rext * 2);
+    }
+    w.hs_ext = off; off += align256((size_t)m.T * count * m.rext * 2);
+    w.total = off;
+    return w;
+}
+
+LoraGroupBwdWs lora_group_bwd_ws(const mc_lora_desc& d, const int64_t* N, int count) {
+    const Dims m = dims_of(d);
+    LoraGroupBwdWs w{};
+    size_t off = 0;
+    for (int g = 0; g < count; ++g) {
+        w.wt[g] = off;
+        off += align256((size_t)m.K * N[g] * 2);
+    }
+    w.at_ext = off; off += align256((size_t)m.K * count * m.rext * 2);
+    w.gd_ext = off; off += align256((size_t)m.T * count * m.rext * 2);
+    w.gd_t = off;   off += align256((size_t)count * m.r * m.T * 4);
+    w.part_a = off; off += align256((size_t)colreduce_splits(m.T, m.K) * colreduce_rows(count * m.r) * m.K * 4);
+    for (int g = 0; g < count; ++g) {
+        w.part_b[g] = off;
+        off += align256((size_t)colreduce_splits(m.T, N[g]) * colreduce_rows(m.r) * N[g] * 4);
     }
     w.total = off;
     return w;
@@ -136,16 +193,15 @@ hipError_t launch_lora_fwd(const mc_lora_desc& d, const void* x, const void* W, 
         const uint16_t* xb = static_cast<const uint16_t*>(x);
         {
             auto sc = lowrank_scope(st, m.T, m.K, m.r, 2);
-            const PrepJob ja{A, m.r, m.r, m.K, true, at_hi, at_lo, m.r16, m.K};   // A^T hi / lo
-            const PrepJob jb{B, m.N, m.N, m.r, true, bt, nullptr, m.N, m.rext};   // B^T, zero-padded
-            MC_TRY(launch_prep_bf16(ja, jb, st));
+            const PrepJob jobs[2] = {prep_job(A, m.r, m.r, m.K, true, at_hi, at_lo, m.r16, m.K),   // A^T hi / lo
+                                     prep_job(B, m.N, m.N, m.r, true, bt, nullptr, m.N, m.rext)};  // B^T, zero-padded
+            MC_TRY(launch_prep_bf16(jobs, 2, st));
             MC_TRY(launch_rowproj_bf16(xb, m.T, m.K, at_hi, at_lo, m.r, 1.0f, mask, keep, h_save, hs, m.rext,
                                        d.scale, st));
         }
-        GemmSeg s0{xb, m.K, static_cast<const uint16_t*>(W), m.K, kbase};
-        GemmSeg s1{hs, m.rext, bt, m.rext, m.rext};
+        const GemmSeg segs[2] = {{xb, m.K, static_cast<const uint16_t*>(W), m.K, kbase}, {hs, m.rext, bt, m.rext, m.rext}};
         auto sc = gemm_scope(st, m.T, m.N, kbase, m.rext, m.r, 2);
-        return launch_gemm_bf16(m.T, m.N, s0, s1, static_cast<const uint16_t*>(bias), static_cast<uint16_t*>(y),
+        return launch_gemm_bf16(m.T, m.N, segs, 2, static_cast<const uint16_t*>(bias), static_cast<uint16_t*>(y),
                                 m.N, st);
     }
     float* bt = reinterpret_cast<float*>(base + w.bt_ext);
@@ -168,54 +224,16 @@ hipError_t launch_lora_bwd(const mc_lora_desc& d, const void* x, const void* W, 
                            const void* dY, void* dX, float* dA, float* dB, void* ws,
                            hipStream_t st) {
     const Dims m = dims_of(d);
+    const float keep = mask ? 1.0f / (1.0f - d.dropout_p) : 1.0f;
+    if (m.bf16) {
+        // one projection of the grouped backward, with its own dX
+        const LoraProj p{m.N, W, nullptr, A, B, mask};
+        return launch_lora_group_bwd(d, x, &p, 1, &h_save, &dY, dX, &dA, &dB, ws, st);
+    }
     const LoraBwdWs w = lora_bwd_ws(d);
     char* base = static_cast<char*>(ws);
-    const float keep = mask ? 1.0f / (1.0f - d.dropout_p) : 1.0f;
     const bool need_g = dX || dA;
     const int64_t kbase = W ? m.N : 0;
-    if (m.bf16) {
-        const uint16_t* dyb = static_cast<const uint16_t*>(dY);
-        uint16_t* at = reinterpret_cast<uint16_t*>(base + w.at_ext);
-        uint16_t* gd = reinterpret_cast<uint16_t*>(base + w.gd_ext);
-        float* gdt = reinterpret_cast<float*>(base + w.gd_t);
-        uint16_t* wt = reinterpret_cast<uint16_t*>(base + w.wt);
-        if (need_g) {
-            // one launch: G = s dY.B^T (B read as fp32), A zero-padded to the
-            // dX extension columns, and W^T for the dX GEMM
-            const PrepJob ja{A, m.r, m.K, m.r, false, dX ? at : nullptr, nullptr, m.K, m.rext};
-            const bool tw = dX && W;
-            const double bytes = 2.0 * m.T * m.N + 4.0 * m.T * m.r + 4.0 * m.r * m.N +
-                                 (dX ? 6.0 * m.r * m.K : 0.0) + (tw ? 4.0 * m.N * m.K : 0.0);
-            auto sc = prof::Scope(prof::kLowRank, st, 2.0 * m.T * m.N * m.r, bytes);
-            MC_TRY(launch_lora_bwd_operands(dyb, m.T, m.N, B, m.r, d.scale, mask, keep, dA ? gdt : nullptr,
-                                            dX ? gd : nullptr, m.rext, ja, static_cast<const uint16_t*>(W), m.K,
-                                            tw ? wt : nullptr, st));
-        }
-        if (dX) {
-            GemmSeg s0{dyb, m.N, wt, m.N, kbase};
-            GemmSeg s1{gd, m.rext, at, m.rext, m.rext};
-            auto sc = gemm_scope(st, m.T, m.K, kbase, m.rext, m.r, 2);
-            MC_TRY(launch_gemm_bf16(m.T, m.K, s0, s1, nullptr, static_cast<uint16_t*>(dX), m.K, st));
-        }
-        if (dA || dB) {
-            // dA = x^T.Gd and dB = s Hd^T.dY: split-T column reductions in one
-            // launch, then both fixed-order split sums in one launch
-            const int sa = colreduce_splits(m.T, m.K), sb = colreduce_splits(m.T, m.N);
-            float* pa = reinterpret_cast<float*>(base + w.part_a);
-            float* pb = reinterpret_cast<float*>(base + w.part_b);
-            const ColJob ca{dA ? static_cast<const uint16_t*>(x) : nullptr, m.K, gdt, sa, pa};
-            const ColJob cb{dB ? dyb : nullptr, m.N, h_save, sb, pb};
-            const SumJob ua{pa, sa, m.K, (int64_t)m.r16 * m.K, 1.0f, true, dA};
-            const SumJob ub{pb, sb, m.N, (int64_t)m.r16 * m.N, d.scale, false, dB};
-            const double bytes = (dA ? 2.0 * m.T * m.K + 4.0 * m.T * m.r : 0.0) +
-                                 (dB ? 2.0 * m.T * m.N + 4.0 * m.T * m.r : 0.0);
-            const double flops = (dA ? 2.0 * m.T * m.K * m.r : 0.0) + (dB ? 2.0 * m.T * m.N * m.r : 0.0);
-            auto sc = prof::Scope(prof::kLowRank, st, flops, bytes);
-            MC_TRY(launch_colreduce_bf16(m.T, m.r, ca, cb, st));
-            MC_TRY(launch_split_sum(m.r, ua, ub, st));
-        }
-        return hipSuccess;
-    }
     const float* dyf = static_cast<const float*>(dY);
     float* at = reinterpret_cast<float*>(base + w.at_ext);
     float* gd = reinterpret_cast<float*>(base + w.gd_ext);
@@ -238,6 +256,168 @@ hipError_t launch_lora_bwd(const mc_lora_desc& d, const void* x, const void* W, 
     if (dB) {
         auto sc = lowrank_scope(st, m.T, m.N, m.r, 4);
         MC_TRY(launch_colreduce_f32(dyf, m.T, m.N, h_save, m.r, d.scale, false, dB, st));
+    }
+    return hipSuccess;
+}
+
+hipError_t launch_lora_group_fwd(const mc_lora_desc& d, const void* x, const LoraProj* proj, int count,
+                                 void* const* y, float* const* h_save, void* ws, hipStream_t st) {
+    // bf16 only. Per pass of up to proj_per_pass projections: one prep launch
+    // (A^T hi / lo of the pass's projections; the B^T extension operands ride
+    // with the first pass) and one row projection that reads x once for all
+    // of their ranks; then one multi-output GEMM over every projection.
+    const Dims m = dims_of(d);
+    int64_t Ns[kMaxProj];
+    for (int g = 0; g < count; ++g) Ns[g] = proj[g].N;
+    const LoraGroupFwdWs w = lora_group_fwd_ws(d, Ns, count);
+    char* base = static_cast<char*>(ws);
+    const uint16_t* xb = static_cast<const uint16_t*>(x);
+    uint16_t* hs = reinterpret_cast<uint16_t*>(base + w.hs_ext);
+    const int ext_ld = count * m.rext;
+    const int ppp = proj_per_pass(m.r);
+    {
+        int64_t sumN = 0;
+        for (int g = 0; g < count; ++g) sumN += Ns[g];
+        auto sc = prof::Scope(prof::kLowRank, st, 2.0 * m.T * m.K * m.r * count,
+                              2.0 * m.T * m.K + 6.0 * m.T * m.r * count + 12.0 * m.r * (m.K + sumN / count) * count);
+        for (int p0 = 0, pass = 0; p0 < count; p0 += ppp, ++pass) {
+            const int np = count - p0 < ppp ? count - p0 : ppp;
+            const int rpass = np * m.r, r16 = 16 * rowproj_rc(rpass);
+            uint16_t* at_hi = reinterpret_cast<uint16_t*>(base + w.at_hilo[pass]);
+            uint16_t* at_lo = at_hi + (size_t)r16 * m.K;
+            PrepJob jobs[2 * kMaxProj + 1];
+            int nj = 0;
+            for (int i = 0; i < np; ++i)  // A_g^T hi / lo as rows [i r, (i + 1) r) of the pass's operand
+                jobs[nj++] = prep_job(proj[p0 + i].A, m.r, m.r, m.K, true, at_hi + (size_t)i * m.r * m.K,
+                                      at_lo + (size_t)i * m.r * m.K, m.r, m.K);
+            if (r16 > rpass)  // zero rows past the pass's ranks
+                jobs[nj++] = prep_job(proj[p0].A, 0, 0, 0, false, at_hi + (size_t)rpass * m.K,
+                                      at_lo + (size_t)rpass * m.K, r16 - rpass, m.K);
+            if (pass == 0)
+                for (int g = 0; g < count; ++g)  // B_g^T, zero-padded to rext columns
+                    jobs[nj++] = prep_job(proj[g].B, Ns[g], Ns[g], m.r, true,
+                                          reinterpret_cast<uint16_t*>(base + w.bt_ext[g]), nullptr, Ns[g], m.rext);
+            MC_TRY(prep_all(jobs, nj, st));
+            RowprojCall c{};
+            c.X = xb; c.T = m.T; c.C = m.K; c.P_hi = at_hi; c.P_lo = at_lo; c.r = rpass; c.rp = m.r;
+            c.scale = 1.0f; c.keep = proj[p0].mask ? 1.0f / (1.0f - d.dropout_p) : 1.0f;
+            for (int i = 0; i < np; ++i) { c.mask[i] = proj[p0 + i].mask; c.out_t[i] = h_save ? h_save[p0 + i] : nullptr; }
+            c.out_ext = hs + (size_t)p0 * m.rext; c.rext_p = m.rext; c.ext_ld = ext_ld; c.ext_scale = d.scale;
+            MC_TRY(launch_rowproj_bf16(c, st));
+        }
+    }
+    GemmOut outs[kMaxProj];
+    double flops = 0, bytes = 0;
+    for (int g = 0; g < count; ++g) {
+        const int64_t kbase = proj[g].W ? m.K : 0;
+        outs[g].N = Ns[g];
+        outs[g].seg[0] = GemmSeg{xb, m.K, static_cast<const uint16_t*>(proj[g].W), m.K, kbase};
+        outs[g].seg[1] = GemmSeg{hs + (size_t)g * m.rext, ext_ld, reinterpret_cast<const uint16_t*>(base + w.bt_ext[g]),
+                                 m.rext, m.rext};
+        outs[g].nseg = 2;
+        outs[g].bias = static_cast<const uint16_t*>(proj[g].bias);
+        outs[g].c = static_cast<uint16_t*>(y[g]);
+        outs[g].ldc = Ns[g];
+        flops += 2.0 * m.T * Ns[g] * (kbase > 0 ? kbase : m.r);
+        bytes += 2.0 * (Ns[g] * (double)(kbase + m.rext) + (double)m.T * Ns[g] + (double)m.T * m.rext);
+    }
+    bytes += 2.0 * m.T * m.K;  // x, read once by the whole grid
+    auto sc = prof::Scope(prof::kGemm, st, flops, bytes);
+    return launch_gemm_bf16_multi(m.T, outs, count, st);
+}
+
+hipError_t launch_lora_group_bwd(const mc_lora_desc& d, const void* x, const LoraProj* proj, int count,
+                                 const float* const* h_save, const void* const* dY, void* dX, float* const* dA,
+                                 float* const* dB, void* ws, hipStream_t st) {
+    // bf16 only. One operand launch for every projection (G_g = s dY_g.B_g^T,
+    // the A_g extension columns, W_g -> W_g^T), one dX GEMM whose reduction
+    // runs over [dY_0 | .. | dY_{G-1} | Gd_0 .. Gd_{G-1}] (the sum of the
+    // projections' input gradients), one column-reduction launch per rank-tile
+    // size (dA of every projection from one pass over x; dB_g over dY_g) and
+    // one fixed-order split-sum launch.
+    const Dims m = dims_of(d);
+    int64_t Ns[kMaxProj];
+    for (int g = 0; g < count; ++g) Ns[g] = proj[g].N;
+    const LoraGroupBwdWs w = lora_group_bwd_ws(d, Ns, count);
+    char* base = static_cast<char*>(ws);
+    const float keep = proj[0].mask ? 1.0f / (1.0f - d.dropout_p) : 1.0f;
+    bool any_dA = false, any_dB = false;
+    for (int g = 0; g < count; ++g) {
+        any_dA = any_dA || (dA && dA[g]);
+        any_dB = any_dB || (dB && dB[g]);
+    }
+    const bool need_g = dX || any_dA;
+    const int ext_ld = count * m.rext;
+    const int rtot = count * m.r;
+    uint16_t* at = reinterpret_cast<uint16_t*>(base + w.at_ext);
+    uint16_t* gd = reinterpret_cast<uint16_t*>(base + w.gd_ext);
+    float* gdt = reinterpret_cast<float*>(base + w.gd_t);
+    if (need_g) {
+        OperandsCall calls[kMaxProj];
+        double bytes = 0, flops = 0;
+        for (int g = 0; g < count; ++g) {
+            const bool tw = dX && proj[g].W;
+            calls[g] = OperandsCall{static_cast<const uint16_t*>(dY[g]), Ns[g], proj[g].B, proj[g].mask,
+                                    any_dA ? gdt + (size_t)g * m.r * m.T : nullptr,
+                                    dX ? gd + (size_t)g * m.rext : nullptr,
+                                    dX ? prep_job(proj[g].A, m.r, m.K, m.r, false, at + (size_t)g * m.rext, nullptr, m.K,
+                                                  m.rext, ext_ld)
+                                       : PrepJob{},
+                                    static_cast<const uint16_t*>(proj[g].W),
+                                    tw ? reinterpret_cast<uint16_t*>(base + w.wt[g]) : nullptr};
+            // algorithmic: dY_g read, G_g written (fp32 and bf16), B_g and A_g read;
+            // the W^T copy is workspace traffic, not counted
+            bytes += 2.0 * m.T * Ns[g] + 6.0 * m.T * m.r + 4.0 * m.r * Ns[g] + (dX ? 6.0 * m.r * m.K : 0.0);
+            flops += 2.0 * m.T * Ns[g] * m.r;
+        }
+        auto sc = prof::Scope(prof::kLowRank, st, flops, bytes);
+        MC_TRY(launch_lora_bwd_operands(calls, count, m.T, m.K, m.r, d.scale, keep, m.rext, ext_ld, st));
+    }
+    if (dX) {
+        GemmSeg segs[kGemmMaxSeg];
+        int nseg = 0;
+        int64_t kbase = 0;
+        for (int g = 0; g < count; ++g)
+            if (proj[g].W) {
+                segs[nseg++] = GemmSeg{static_cast<const uint16_t*>(dY[g]), Ns[g],
+                                       reinterpret_cast<const uint16_t*>(base + w.wt[g]), Ns[g], Ns[g]};
+                kbase += Ns[g];
+            }
+        segs[nseg++] = GemmSeg{gd, ext_ld, at, ext_ld, ext_ld};
+        auto sc = gemm_scope(st, m.T, m.K, kbase, ext_ld, rtot, 2);
+        MC_TRY(launch_gemm_bf16(m.T, m.K, segs, nseg, nullptr, static_cast<uint16_t*>(dX), m.K, st));
+    }
+    if (any_dA || any_dB) {
+        // dA_g = x^T.Gd_g for every g from one pass over x (all ranks), and
+        // dB_g = s Hd_g^T.dY_g: split-T column reductions, then the fixed-order
+        // split sums
+        ColJob cj[1 + kMaxProj];
+        SumJob sj[2 * kMaxProj];
+        int nc = 0, ns = 0;
+        double bytes = 0, flops = 0;
+        const int sa = colreduce_splits(m.T, m.K);
+        float* pa = reinterpret_cast<float*>(base + w.part_a);
+        if (any_dA) {
+            cj[nc++] = ColJob{static_cast<const uint16_t*>(x), m.K, gdt, rtot, sa, pa};
+            bytes += 2.0 * m.T * m.K + 4.0 * m.T * rtot;
+            flops += 2.0 * m.T * m.K * rtot;
+            for (int g = 0; g < count; ++g)
+                if (dA[g])
+                    sj[ns++] = SumJob{pa + (size_t)g * m.r * m.K, sa, m.K, (int64_t)colreduce_rows(rtot) * m.K, m.r,
+                                      1.0f, true, dA[g]};
+        }
+        for (int g = 0; g < count; ++g) {
+            if (!(dB && dB[g])) continue;
+            const int sb = colreduce_splits(m.T, Ns[g]);
+            float* pb = reinterpret_cast<float*>(base + w.part_b[g]);
+            cj[nc++] = ColJob{static_cast<const uint16_t*>(dY[g]), Ns[g], h_save[g], m.r, sb, pb};
+            sj[ns++] = SumJob{pb, sb, Ns[g], (int64_t)colreduce_rows(m.r) * Ns[g], m.r, d.scale, false, dB[g]};
+            bytes += 2.0 * m.T * Ns[g] + 4.0 * m.T * m.r;
+            flops += 2.0 * m.T * Ns[g] * m.r;
+        }
+        auto sc = prof::Scope(prof::kLowRank, st, flops, bytes);
+        MC_TRY(launch_colreduce_bf16(m.T, cj, nc, st));
+        MC_TRY(launch_split_sum(sj, ns, st));
     }
     return hipSuccess;
 }

@@ -41,10 +41,12 @@ namespace mc {
 namespace {
 
 
+// One output block: C[M][N] = sum over the reduction segments of
+// A_s . B_s^T (+ bias), the segments' k-tiles taken in segment order.
 struct GemmArgs {
     int64_t M, N;
-    const uint16_t* a0; const uint16_t* b0; int64_t lda0, ldb0, k0;
-    const uint16_t* a1; const uint16_t* b1; int64_t lda1, ldb1, k1;
+    GemmSeg seg[kGemmMaxSeg];
+    int nseg;
     const uint16_t* bias;
     uint16_t* c;
     int64_t ldc;
@@ -204,7 +206,8 @@ constexpr int kTileSmem = STAGES * (BM + BN) * BK;
 
 // One BM x BN output tile (tm, tn) of g: the whole k loop and the epilogue,
 // with the stage buffers at smem (kTileSmem elements, 1 KB aligned).
-template <int BM, int BN, int WM, int WN, int BK, int STAGES>
+// MULTI: more than two reduction segments (the cursor form below).
+template <int BM, int BN, int WM, int WN, int BK, int STAGES, bool MULTI>
 __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int tm, int tn, uint16_t* smem) {
     constexpr int NWN = BN / WN;
     constexpr int NT = (BM / WM) * NWN * 64;
@@ -222,15 +225,17 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int tm, int tn, uin
     const int lane = tid & 63, wave = tid >> 6;
     const int wm = wave / NWN, wn = wave % NWN;
     const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
-    const int nk0 = (int)((g.k0 + BK - 1) / BK);
-    const int nk = nk0 + (int)((g.k1 + BK - 1) / BK);
-
-    // Per-segment buffer resources over the workgroup's rows of A and B:
-    // rows past M / N fall outside num_records and load as zero.
-    const i32x4 ra0 = rsrc_words(g.a0 + m0 * g.lda0, (g.M - m0) * g.lda0 * 2);
-    const i32x4 ra1 = rsrc_words(g.a1 + m0 * g.lda1, (g.M - m0) * g.lda1 * 2);
-    const i32x4 rb0 = rsrc_words(g.b0 + n0 * g.ldb0, (g.N - n0) * g.ldb0 * 2);
-    const i32x4 rb1 = rsrc_words(g.b1 + n0 * g.ldb1, (g.N - n0) * g.ldb1 * 2);
+    // Tile count and the last tile's substeps with data (the last tile
+    // belongs to the last non-empty segment), read from the segment table
+    // here, before any LDS traffic: a scalar load's wait also waits for LDS.
+    int nk = 0;
+    int64_t klast = 0;
+    for (int s = 0; s < (MULTI ? g.nseg : 2); ++s) {
+        const int64_t ks = g.seg[s].k;
+        nk += (int)((ks + BK - 1) / BK);
+        if (ks > 0) klast = ks - (ks - 1) / BK * BK;
+    }
+    const int nks_last = klast >= BK ? KS : (int)((klast + 15) / 16);
 
     // Loads of tile kt into a stage, in KS parts. With two stages and 8
     // waves, only waves 0-3 (one per SIMD) issue them: a wave waits while its
@@ -238,33 +243,93 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int tm, int tn, uin
     // busy meanwhile (measured +2-5% on the 2-stage tiles; the 3-stage ring,
     // whose loads are spread over every substep, was 3% slower this way).
     constexpr int DMA_NT = (STAGES == 2 && NT == 512) ? 256 : NT;
-    // Full k-tiles of the first segment (all of the base product but a
-    // ragged last tile) load through precomputed lane offsets; the ragged
-    // tile, the second segment and tiles past the end take the general path,
-    // which zeroes chunks at k >= the segment's length.
+    // Two segments (every single projection: the base product, then the
+    // rank-r columns) are set up once at the start: buffer resources over the
+    // workgroup's rows of A and B (rows past M / N fall outside num_records
+    // and load as zero) and the lanes' DMA offsets of segment 0. More
+    // segments (a group's dX) go through a cursor that is moved once per tile:
+    // at a segment's first tile it sets up that segment's resources and
+    // offsets. Full k-tiles of the current (or first) segment load through the
+    // precomputed lane offsets; a ragged tile, and in the two-segment form the
+    // second segment, take the general path, which zeroes chunks at k >= the
+    // segment's length.
     TileOffsets<BM, DMA_NT, BK> offa;
     TileOffsets<BN, DMA_NT, BK> offb;
-    offa.init((uint32_t)g.lda0, tid);
-    offb.init((uint32_t)g.ldb0, tid);
-    const int nfull0 = (int)(g.k0 / BK);
     const uint32_t lds_wave_a = (uint32_t)__builtin_amdgcn_readfirstlane(
         (int)((uint32_t)(tid >> 6) * (uint32_t)TileOffsets<BM, DMA_NT, BK>::PER_WAVE * 1024u));
     const uint32_t lds_wave_b = (uint32_t)__builtin_amdgcn_readfirstlane(
         (int)((uint32_t)(tid >> 6) * (uint32_t)TileOffsets<BN, DMA_NT, BK>::PER_WAVE * 1024u));
+    // two-segment form: every scalar of the two segments is read into a value
+    // here (selecting between fields of the argument struct in the loop
+    // compiles to a scalar load from a selected address, and its lgkmcnt wait
+    // stalls on the fragment reads in flight)
+    const uint32_t k0 = (uint32_t)g.seg[0].k, k1 = (uint32_t)g.seg[1].k;
+    const uint32_t lda0 = (uint32_t)g.seg[0].lda, lda1 = (uint32_t)g.seg[1].lda;
+    const uint32_t ldb0 = (uint32_t)g.seg[0].ldb, ldb1 = (uint32_t)g.seg[1].ldb;
+    const int nk0 = MULTI ? 0 : (int)((k0 + BK - 1) / BK);
+    const int nfull0 = MULTI ? 0 : (int)(k0 / BK);
+    i32x4 ra0 = {0, 0, 0, 0}, rb0 = {0, 0, 0, 0}, ra1 = {0, 0, 0, 0}, rb1 = {0, 0, 0, 0};
+    if constexpr (!MULTI) {
+        ra0 = rsrc_words(g.seg[0].a + m0 * lda0, (g.M - m0) * lda0 * 2);
+        rb0 = rsrc_words(g.seg[0].b + n0 * ldb0, (g.N - n0) * ldb0 * 2);
+        ra1 = rsrc_words(g.seg[1].a + m0 * lda1, (g.M - m0) * lda1 * 2);
+        rb1 = rsrc_words(g.seg[1].b + n0 * ldb1, (g.N - n0) * ldb1 * 2);
+        offa.init(lda0, tid);
+        offb.init(ldb0, tid);
+    }
+    // cursor form
+    int cur = -1, cur_begin = 0, cur_end = 0, cur_full = 0;
+    uint32_t cur_lda = 0, cur_ldb = 0, cur_k = 0;
+    i32x4 ra = {0, 0, 0, 0}, rb = {0, 0, 0, 0};
+    // Moves the cursor to the segment of tile kt. It is called once per tile,
+    // before the tile's first load part and at a point where no LDS reads are
+    // in flight (right after a barrier or before the first tile): the scalar
+    // loads of the segment table wait on lgkmcnt, the counter the fragment
+    // reads also use.
+    auto advance = [&](int kt) {
+        if constexpr (MULTI) {
+            while (kt >= cur_end) {  // wave-uniform: the first tile of the next non-empty segment
+                ++cur;
+                const GemmSeg& sg = g.seg[cur];
+                cur_begin = cur_end;
+                cur_end = cur_begin + (int)((sg.k + BK - 1) / BK);
+                cur_full = (int)(sg.k / BK);
+                cur_lda = (uint32_t)sg.lda;
+                cur_ldb = (uint32_t)sg.ldb;
+                cur_k = (uint32_t)sg.k;
+                if (cur_end > cur_begin) {
+                    ra = rsrc_words(sg.a + m0 * sg.lda, (g.M - m0) * sg.lda * 2);
+                    rb = rsrc_words(sg.b + n0 * sg.ldb, (g.N - n0) * sg.ldb * 2);
+                    offa.init(cur_lda, tid);
+                    offb.init(cur_ldb, tid);
+                }
+            }
+        }
+    };
     auto issue = [&](int kt, int stage, int part) {
-        const bool second = kt >= nk0;
-        const uint32_t kb = (uint32_t)(second ? kt - nk0 : kt) * BK;
-        const uint32_t ks = kt < nk ? (uint32_t)(second ? g.k1 : g.k0) : 0u;
         const uint32_t base = smem_byte + (uint32_t)(stage * STAGE * 2);
-        if (DMA_NT == NT || tid < DMA_NT) {  // wave-uniform
+        if (!(DMA_NT == NT || tid < DMA_NT)) return;  // wave-uniform
+        if constexpr (MULTI) {
+            const int local = kt - cur_begin;
+            const uint32_t kb = (uint32_t)local * BK;
+            if (local < cur_full) {
+                dma_tile_full<BM, DMA_NT, BK, KS>(ra, base + lds_wave_a, offa, kb, part);
+                dma_tile_full<BN, DMA_NT, BK, KS>(rb, base + BM * BK * 2 + lds_wave_b, offb, kb, part);
+            } else {
+                dma_tile<BM, DMA_NT, BK, KS>(ra, base, cur_lda, kb, cur_k, tid, part);
+                dma_tile<BN, DMA_NT, BK, KS>(rb, base + BM * BK * 2, cur_ldb, kb, cur_k, tid, part);
+            }
+        } else {
+            const bool second = kt >= nk0;
+            const uint32_t kb = (uint32_t)(second ? kt - nk0 : kt) * BK;
+            const uint32_t ks = second ? k1 : k0;
             if (kt < nfull0) {
                 dma_tile_full<BM, DMA_NT, BK, KS>(ra0, base + lds_wave_a, offa, kb, part);
                 dma_tile_full<BN, DMA_NT, BK, KS>(rb0, base + BM * BK * 2 + lds_wave_b, offb, kb, part);
             } else {
-                dma_tile<BM, DMA_NT, BK, KS>(second ? ra1 : ra0, base, (uint32_t)(second ? g.lda1 : g.lda0), kb, ks,
+                dma_tile<BM, DMA_NT, BK, KS>(second ? ra1 : ra0, base, second ? lda1 : lda0, kb, ks, tid, part);
+                dma_tile<BN, DMA_NT, BK, KS>(second ? rb1 : rb0, base + BM * BK * 2, second ? ldb1 : ldb0, kb, ks,
                                              tid, part);
-                dma_tile<BN, DMA_NT, BK, KS>(second ? rb1 : rb0, base + BM * BK * 2,
-                                             (uint32_t)(second ? g.ldb1 : g.ldb0), kb, ks, tid, part);
             }
         }
     };
@@ -313,9 +378,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int tm, int tn, uin
         wait_vmcnt<0>();
         __syncthreads();
         const uint16_t* st = smem + (kt % STAGES) * STAGE;
-        const bool second = kt >= nk0;
-        const int64_t kleft = (second ? g.k1 : g.k0) - (int64_t)(second ? kt - nk0 : kt) * BK;
-        const int nks = kleft >= BK ? KS : (int)((kleft + 15) / 16);
+        const int nks = nks_last;
         load_frags(st, 0, 0);
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
@@ -326,6 +389,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int tm, int tn, uin
         }
     };
     auto issue_all = [&](int t) {
+        advance(t);
 #pragma unroll
         for (int p = 0; p < KS; ++p) issue(t, t % STAGES, p);
     };
@@ -343,6 +407,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int tm, int tn, uin
             wait_vmcnt<0>();
             __syncthreads();
             const uint16_t* st = smem + (kt & 1) * STAGE;
+            advance(kt + 1);
             issue(kt + 1, (kt + 1) & 1, 0);
             issue(kt + 1, (kt + 1) & 1, 1);
             load_frags(st, 0, 0);
@@ -369,8 +434,9 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int tm, int tn, uin
             wait_tiles<LOADS>(ahead < STAGES - 2 ? ahead : STAGES - 2);
             __syncthreads();
             const uint16_t* st = smem + (kt % STAGES) * STAGE;
-            load_frags(st, 0, 0);
             const int nt = kt + STAGES - 1;
+            if (nt < nk) advance(nt);
+            load_frags(st, 0, 0);
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
                 const int cur = ks & 1;
@@ -386,20 +452,20 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int tm, int tn, uin
     store_c<TM, TN, WM, WN>(acc, smem, g, m0, n0, wm, wn);
 }
 
-template <int BM, int BN, int WM, int WN, int BK, int STAGES>
+template <int BM, int BN, int WM, int WN, int BK, int STAGES, bool MULTI>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, 1)
 __attribute__((amdgpu_waves_per_eu(1, 2))) void gemm_bf16_kernel(GemmArgs g) {
     __shared__ __attribute__((aligned(1024))) uint16_t smem[kTileSmem<BM, BN, BK, STAGES>];
     int tm, tn;
     tile_of(blockIdx.x, g.tiles_m, g.tiles_n, g.group_m, tm, tn);
-    gemm_tile<BM, BN, WM, WN, BK, STAGES>(g, tm, tn, smem);
+    gemm_tile<BM, BN, WM, WN, BK, STAGES, MULTI>(g, tm, tn, smem);
 }
 
 // Two tile shapes in one launch: workgroups [0, wgs1) compute g1's tiles
 // (columns [0, n1) of the output), the rest g2's tiles (columns [n1, N)).
 // Workgroups are dispatched in id order, so the second shape fills the CUs
 // the first shape's last round leaves idle. Both shapes use 8 waves.
-template <int BM1, int BN1, int WM1, int WN1, int S1, int BM2, int BN2, int WM2, int WN2, int S2>
+template <int BM1, int BN1, int WM1, int WN1, int S1, int BM2, int BN2, int WM2, int WN2, int S2, bool MULTI>
 __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(1, 2))) void gemm_bf16_split(GemmArgs g1,
                                                                                                      GemmArgs g2,
                                                                                                      int wgs1) {
@@ -409,13 +475,36 @@ __global__ __launch_bounds__(512, 1) __attribute__((amdgpu_waves_per_eu(1, 2))) 
     int tm, tn;
     if ((int)blockIdx.x < wgs1) {
         tile_of(blockIdx.x, g1.tiles_m, g1.tiles_n, g1.group_m, tm, tn);
-        gemm_tile<BM1, BN1, WM1, WN1, 64, S1>(g1, tm, tn, smem);
+        gemm_tile<BM1, BN1, WM1, WN1, 64, S1, MULTI>(g1, tm, tn, smem);
     } else {
         tile_of((int)blockIdx.x - wgs1, g2.tiles_m, g2.tiles_n, g2.group_m, tm, tn);
-        gemm_tile<BM2, BN2, WM2, WN2, 64, S2>(g2, tm, tn, smem);
+        gemm_tile<BM2, BN2, WM2, WN2, 64, S2, MULTI>(g2, tm, tn, smem);
     }
 }
 
+// Output blocks that share the rows of their first A operand (projections of
+// one input): up to kGemmMaxOut blocks, each with its own reduction segments,
+// bias and C, as one grid of one tile shape. Tile columns run through the
+// blocks in order (block o owns columns [col_start[o], col_start[o + 1]) of
+// the grid); tile_of orders them as for one wide product, so a tile-row
+// group walks the columns of every block.
+struct GemmMulti {
+    GemmArgs out[kGemmMaxOut];
+    int nout;
+    int col_start[kGemmMaxOut + 1];
+    int tiles_m, tiles_n, group_m;
+};
+
+template <int BM, int BN, int WM, int WN, int BK, int STAGES>
+__global__ __launch_bounds__((BM / WM) * (BN / WN) * 64, 1)
+__attribute__((amdgpu_waves_per_eu(1, 2))) void gemm_bf16_multi(GemmMulti m) {
+    __shared__ __attribute__((aligned(1024))) uint16_t smem[kTileSmem<BM, BN, BK, STAGES>];
+    int tm, tn;
+    tile_of(blockIdx.x, m.tiles_m, m.tiles_n, m.group_m, tm, tn);
+    int o = 0;
+    while (o + 1 < m.nout && tn >= m.col_start[o + 1]) ++o;  // wave-uniform
+    gemm_tile<BM, BN, WM, WN, BK, STAGES, false>(m.out[o], tm, tn - m.col_start[o], smem);
+}
 
 // ------------------------------------------------------------- fp32 GEMM
 // 64 x 64 tile, 16-deep k-steps, 4 x 4 outputs per thread, sequential FMA
@@ -478,30 +567,17 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(int64_t M, int64_t N, Gem
 
 }  // namespace
 
-template <int BM, int BN, int WM, int WN, int BK, int STAGES>
-hipError_t launch_cfg(int64_t M, int64_t N, GemmSeg s0, GemmSeg s1, const uint16_t* bias, uint16_t* c, int64_t ldc,
-                      hipStream_t stream, int group_m) {
-    GemmArgs g;
-    g.M = M; g.N = N;
-    g.a0 = s0.a; g.b0 = s0.b; g.lda0 = s0.lda; g.ldb0 = s0.ldb; g.k0 = s0.k;
-    g.a1 = s1.a; g.b1 = s1.b; g.lda1 = s1.lda; g.ldb1 = s1.ldb; g.k1 = s1.k;
-    g.bias = bias; g.c = c; g.ldc = ldc;
-    g.tiles_m = (int)((M + BM - 1) / BM);
-    g.tiles_n = (int)((N + BN - 1) / BN);
-    g.group_m = group_m;
-    constexpr int NT = (BM / WM) * (BN / WN) * 64;
-    gemm_bf16_kernel<BM, BN, WM, WN, BK, STAGES><<<dim3((unsigned)(g.tiles_m * g.tiles_n)), NT, 0, stream>>>(g);
-    return hipGetLastError();
-}
-
-
-// GEMM args of columns [n0, n0 + n) of the output with BN-wide tiles.
-static GemmArgs col_range(int64_t M, int64_t n0, int64_t n, GemmSeg s0, GemmSeg s1, const uint16_t* bias,
+// GEMM args of columns [n0, n0 + n) of an output with BN-wide tiles (B rows,
+// bias and C offset to the first column).
+static GemmArgs col_range(int64_t M, int64_t n0, int64_t n, const GemmSeg* segs, int nseg, const uint16_t* bias,
                           uint16_t* c, int64_t ldc, int bm, int bn, int group_m) {
-    GemmArgs g;
+    GemmArgs g{};
     g.M = M; g.N = n;
-    g.a0 = s0.a; g.b0 = s0.b ? s0.b + n0 * s0.ldb : nullptr; g.lda0 = s0.lda; g.ldb0 = s0.ldb; g.k0 = s0.k;
-    g.a1 = s1.a; g.b1 = s1.b ? s1.b + n0 * s1.ldb : nullptr; g.lda1 = s1.lda; g.ldb1 = s1.ldb; g.k1 = s1.k;
+    g.nseg = nseg;
+    for (int i = 0; i < nseg; ++i) {
+        g.seg[i] = segs[i];
+        if (g.seg[i].b) g.seg[i].b += n0 * segs[i].ldb;
+    }
     g.bias = bias ? bias + n0 : nullptr; g.c = c + n0; g.ldc = ldc;
     g.tiles_m = (int)((M + bm - 1) / bm);
     g.tiles_n = (int)((n + bn - 1) / bn);
@@ -509,14 +585,46 @@ static GemmArgs col_range(int64_t M, int64_t n0, int64_t n, GemmSeg s0, GemmSeg 
     return g;
 }
 
+template <int BM, int BN, int WM, int WN, int BK, int STAGES>
+hipError_t launch_cfg(int64_t M, int64_t N, const GemmSeg* segs, int nseg, const uint16_t* bias, uint16_t* c,
+                      int64_t ldc, hipStream_t stream, int group_m) {
+    const GemmArgs g = col_range(M, 0, N, segs, nseg, bias, c, ldc, BM, BN, group_m);
+    constexpr int NT = (BM / WM) * (BN / WN) * 64;
+    const dim3 grid((unsigned)(g.tiles_m * g.tiles_n));
+    if (nseg > 2) gemm_bf16_kernel<BM, BN, WM, WN, BK, STAGES, true><<<grid, NT, 0, stream>>>(g);
+    else gemm_bf16_kernel<BM, BN, WM, WN, BK, STAGES, false><<<grid, NT, 0, stream>>>(g);
+    return hipGetLastError();
+}
+
 template <int BM1, int BN1, int WM1, int WN1, int S1, int BM2, int BN2, int WM2, int WN2, int S2>
-hipError_t launch_split(int64_t M, int64_t N, int64_t n1, GemmSeg s0, GemmSeg s1, const uint16_t* bias, uint16_t* c,
-                        int64_t ldc, hipStream_t stream, int group_m) {
-    const GemmArgs g1 = col_range(M, 0, n1, s0, s1, bias, c, ldc, BM1, BN1, group_m);
-    const GemmArgs g2 = col_range(M, n1, N - n1, s0, s1, bias, c, ldc, BM2, BN2, group_m);
+hipError_t launch_split(int64_t M, int64_t N, int64_t n1, const GemmSeg* segs, int nseg, const uint16_t* bias,
+                        uint16_t* c, int64_t ldc, hipStream_t stream, int group_m) {
+    const GemmArgs g1 = col_range(M, 0, n1, segs, nseg, bias, c, ldc, BM1, BN1, group_m);
+    const GemmArgs g2 = col_range(M, n1, N - n1, segs, nseg, bias, c, ldc, BM2, BN2, group_m);
     const int wgs1 = g1.tiles_m * g1.tiles_n;
-    gemm_bf16_split<BM1, BN1, WM1, WN1, S1, BM2, BN2, WM2, WN2, S2>
-        <<<dim3((unsigned)(wgs1 + g2.tiles_m * g2.tiles_n)), 512, 0, stream>>>(g1, g2, wgs1);
+    const dim3 grid((unsigned)(wgs1 + g2.tiles_m * g2.tiles_n));
+    if (nseg > 2)
+        gemm_bf16_split<BM1, BN1, WM1, WN1, S1, BM2, BN2, WM2, WN2, S2, true><<<grid, 512, 0, stream>>>(g1, g2, wgs1);
+    else
+        gemm_bf16_split<BM1, BN1, WM1, WN1, S1, BM2, BN2, WM2, WN2, S2, false><<<grid, 512, 0, stream>>>(g1, g2, wgs1);
+    return hipGetLastError();
+}
+
+template <int BM, int BN, int WM, int WN, int BK, int STAGES>
+hipError_t launch_multi(int64_t M, const GemmOut* outs, int nout, hipStream_t stream, int group_m) {
+    GemmMulti m{};
+    m.nout = nout;
+    m.col_start[0] = 0;
+    for (int o = 0; o < nout; ++o) {
+        m.out[o] = col_range(M, 0, outs[o].N, outs[o].seg, outs[o].nseg, outs[o].bias, outs[o].c, outs[o].ldc, BM, BN,
+                             group_m);
+        m.col_start[o + 1] = m.col_start[o] + m.out[o].tiles_n;
+    }
+    m.tiles_m = (int)((M + BM - 1) / BM);
+    m.tiles_n = m.col_start[nout];
+    m.group_m = group_m;
+    constexpr int NT = (BM / WM) * (BN / WN) * 64;
+    gemm_bf16_multi<BM, BN, WM, WN, BK, STAGES><<<dim3((unsigned)(m.tiles_m * m.tiles_n)), NT, 0, stream>>>(m);
     return hipGetLastError();
 }
 
@@ -569,6 +677,28 @@ double list_time(int64_t n1, double t1, int64_t n2, double t2, int cus) {
 
 }  // namespace
 
+// Estimated time of a plan (units of one 256 x 256 tile at full speed).
+double plan_time(int64_t M, int64_t N, int64_t K, const GemmPlan& p, int cus) {
+    int bm, bn;
+    if (p.n1 >= N) {
+        tile_dims(p.main, bm, bn);
+        const int64_t tiles = ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
+        return list_time(tiles, (double)bm * bn / tile_speed(p.main, K), 0, 0.0, cus);
+    }
+    tile_dims(p.tail, bm, bn);
+    const int64_t tm = (M + 255) / 256;
+    const int64_t n2 = tm * ((N - p.n1 + bn - 1) / bn);
+    return list_time(tm * (p.n1 / 256), 65536.0, n2, (double)bm * bn / tile_speed(p.tail, K), cus);
+}
+
+double plan_time_multi(int64_t M, const int64_t* Ns, int nout, int64_t K, GemmTile t, int cus) {
+    int bm, bn;
+    tile_dims(t, bm, bn);
+    int64_t cols = 0;
+    for (int o = 0; o < nout; ++o) cols += (Ns[o] + bn - 1) / bn;
+    return list_time(((M + bm - 1) / bm) * cols, (double)bm * bn / tile_speed(t, K), 0, 0.0, cus);
+}
+
 GemmPlan choose_gemm_plan(int64_t M, int64_t N, int64_t K, int cus) {
     // One tile shape over all of N, or 256 x 256 tiles over the first n1 =
     // 256 j columns and a narrower shape over the rest, whichever list_time
@@ -602,23 +732,79 @@ GemmPlan choose_gemm_plan(int64_t M, int64_t N, int64_t K, int cus) {
     return best;
 }
 
-hipError_t launch_gemm_bf16(int64_t M, int64_t N, GemmSeg s0, GemmSeg s1, const uint16_t* bias, uint16_t* c,
+hipError_t launch_gemm_bf16(int64_t M, int64_t N, const GemmSeg* segs, int nseg, const uint16_t* bias, uint16_t* c,
                             int64_t ldc, hipStream_t stream) {
-    const GemmPlan p = choose_gemm_plan(M, N, s0.k + s1.k, cu_count());
+    int64_t K = 0;
+    for (int i = 0; i < nseg; ++i) K += segs[i].k;
+    const GemmPlan p = choose_gemm_plan(M, N, K, cu_count());
     if (p.n1 < N) {  // 256 x 256 over [0, n1), the tail shape over [n1, N)
         if (p.tail == GemmTile::k256x192)
-            return launch_split<256, 256, 128, 64, 2, 256, 192, 64, 96, 2>(M, N, p.n1, s0, s1, bias, c, ldc, stream, 4);
-        return launch_split<256, 256, 128, 64, 2, 256, 128, 64, 64, 3>(M, N, p.n1, s0, s1, bias, c, ldc, stream, 4);
+            return launch_split<256, 256, 128, 64, 2, 256, 192, 64, 96, 2>(M, N, p.n1, segs, nseg, bias, c, ldc,
+                                                                            stream, 4);
+        return launch_split<256, 256, 128, 64, 2, 256, 128, 64, 64, 3>(M, N, p.n1, segs, nseg, bias, c, ldc, stream,
+                                                                        4);
     }
     switch (p.main) {
         case GemmTile::k256x256:  // 8 waves of 128 x 64, k-steps of 64, 2 stages (128 KB LDS)
-            return launch_cfg<256, 256, 128, 64, 64, 2>(M, N, s0, s1, bias, c, ldc, stream, 4);
+            return launch_cfg<256, 256, 128, 64, 64, 2>(M, N, segs, nseg, bias, c, ldc, stream, 4);
         case GemmTile::k256x192:  // 8 waves of 64 x 96, 2 stages (112 KB LDS)
-            return launch_cfg<256, 192, 64, 96, 64, 2>(M, N, s0, s1, bias, c, ldc, stream, 4);
+            return launch_cfg<256, 192, 64, 96, 64, 2>(M, N, segs, nseg, bias, c, ldc, stream, 4);
         case GemmTile::k256x128:  // 8 waves of 64 x 64, 3 stages (144 KB LDS)
-            return launch_cfg<256, 128, 64, 64, 64, 3>(M, N, s0, s1, bias, c, ldc, stream, 4);
+            return launch_cfg<256, 128, 64, 64, 64, 3>(M, N, segs, nseg, bias, c, ldc, stream, 4);
         default:                  // 4 waves of 64 x 64, 3 stages (96 KB LDS)
-            return launch_cfg<128, 128, 64, 64, 64, 3>(M, N, s0, s1, bias, c, ldc, stream, 4);
+            return launch_cfg<128, 128, 64, 64, 64, 3>(M, N, segs, nseg, bias, c, ldc, stream, 4);
+    }
+}
+
+hipError_t launch_gemm_bf16(int64_t M, int64_t N, GemmSeg s0, GemmSeg s1, const uint16_t* bias, uint16_t* c,
+                            int64_t ldc, hipStream_t stream) {
+    const GemmSeg segs[2] = {s0, s1};
+    return launch_gemm_bf16(M, N, segs, 2, bias, c, ldc, stream);
+}
+
+GemmTile choose_multi_tile(int64_t M, const int64_t* Ns, int nout, int64_t K, int cus) {
+    // one tile shape over every block's columns, by the same list-schedule
+    // estimate as choose_gemm_plan's single shapes
+    const GemmTile singles[] = {GemmTile::k256x256, GemmTile::k256x192, GemmTile::k256x128, GemmTile::k128x128};
+    GemmTile best = GemmTile::k128x128;
+    double best_t = 1e300;
+    for (GemmTile t : singles) {
+        int bm, bn;
+        tile_dims(t, bm, bn);
+        int64_t cols = 0;
+        for (int o = 0; o < nout; ++o) cols += (Ns[o] + bn - 1) / bn;
+        const int64_t tiles = ((M + bm - 1) / bm) * cols;
+        const double e = list_time(tiles, (double)bm * bn / tile_speed(t, K), 0, 0.0, cus);
+        if (e < best_t) { best_t = e; best = t; }
+    }
+    return best;
+}
+
+hipError_t launch_gemm_bf16_multi(int64_t M, const GemmOut* outs, int nout, hipStream_t stream) {
+    int64_t Ns[kGemmMaxOut];
+    int64_t K = 0;
+    for (int o = 0; o < nout; ++o) Ns[o] = outs[o].N;
+    for (int i = 0; i < outs[0].nseg; ++i) K += outs[0].seg[i].k;
+    // One launch over every block's columns with one tile shape, or one
+    // launch per block with its own plan (a split plan can fill the CUs'
+    // last round with narrower tiles), whichever the estimate says is faster.
+    const int cus = cu_count();
+    const GemmTile t = choose_multi_tile(M, Ns, nout, K, cus);
+    double sep = 0.0;
+    for (int o = 0; o < nout; ++o) sep += plan_time(M, Ns[o], K, choose_gemm_plan(M, Ns[o], K, cus), cus);
+    if (sep < plan_time_multi(M, Ns, nout, K, t, cus)) {
+        for (int o = 0; o < nout; ++o) {
+            const hipError_t e = launch_gemm_bf16(M, Ns[o], outs[o].seg, outs[o].nseg, outs[o].bias, outs[o].c,
+                                                  outs[o].ldc, stream);
+            if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
+    }
+    switch (t) {
+        case GemmTile::k256x256: return launch_multi<256, 256, 128, 64, 64, 2>(M, outs, nout, stream, 4);
+        case GemmTile::k256x192: return launch_multi<256, 192, 64, 96, 64, 2>(M, outs, nout, stream, 4);
+        case GemmTile::k256x128: return launch_multi<256, 128, 64, 64, 64, 3>(M, outs, nout, stream, 4);
+        default: return launch_multi<128, 128, 64, 64, 64, 3>(M, outs, nout, stream, 4);
     }
 }
 

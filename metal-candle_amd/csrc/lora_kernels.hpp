@@ -9,11 +9,25 @@ namespace mc {
 
 inline int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
 
+// Projections of one input in a grouped call, and job-table sizes of the
+// batched launches.
+constexpr int kMaxProj = 4;
+constexpr int kPrepJobs = 8;
+constexpr int kColJobs = 8;
+constexpr int kSumJobs = 8;
+
+// 16-row rank tiles of a row-projection pass over r ranks (r <= 128).
+inline int rowproj_rc(int r) { return r <= 16 ? 1 : r <= 32 ? 2 : r <= 48 ? 3 : r <= 64 ? 4 : 8; }
+// Rows of the split-T partials of a column reduction over r ranks: ranks go
+// in groups of 64, each taking 16, 32, 48 or 64 accumulator rows.
+inline int colreduce_rows(int r) { return r <= 16 ? 16 : r <= 32 ? 32 : r <= 48 ? 48 : (int)round_up(r, 64); }
+
 // ------------------------------------------------------ operand preparation
 // One job: out[i][j] (bf16, rows_out x cols_out, ld = cols_out) = src element
 // (transpose ? src[j*ld_src + i] : src[i*ld_src + j]) for i < valid_rows,
 // j < valid_cols, else 0. With lo != nullptr the fp32 value v is split as
 // hi = bf16(v), lo = bf16(v - hi). A job with hi == nullptr is skipped.
+// ld_out is the row stride of hi / lo (0: cols_out).
 struct PrepJob {
     const float* src;
     int64_t ld_src, valid_rows, valid_cols;
@@ -21,8 +35,10 @@ struct PrepJob {
     uint16_t* hi;
     uint16_t* lo;
     int64_t rows_out, cols_out;
+    int64_t ld_out;
 };
-// Both jobs in one launch.
+// Up to kPrepJobs jobs in one launch.
+hipError_t launch_prep_bf16(const PrepJob* jobs, int n, hipStream_t stream);
 hipError_t launch_prep_bf16(const PrepJob& j0, const PrepJob& j1, hipStream_t stream);
 
 // ------------------------------------------------------- row projection
@@ -30,56 +46,94 @@ hipError_t launch_prep_bf16(const PrepJob& j0, const PrepJob& j1, hipStream_t st
 //                    v = mask ? (mask[t*r+j] ? v*keep : 0) : v
 //   out_t[j*T + t] = v                       (fp32, may be null)
 //   out_ext[t*rext + j] = bf16(ext_scale*v)  (j < r; zero for r <= j < rext; may be null)
-// X bf16 [T][C] (C % 8 == 0), P_hi / P_lo bf16 [r16][C] with r16 = 16, 32,
-// 64 or 128 (the smallest >= r), rows past r zero.
+// X bf16 [T][C] (C % 8 == 0), P_hi / P_lo bf16 [16 rowproj_rc(r)][C], rows
+// past r zero.
 hipError_t launch_rowproj_bf16(const uint16_t* X, int64_t T, int64_t C, const uint16_t* P_hi,
                                const uint16_t* P_lo, int r, float scale, const uint8_t* mask,
                                float keep, float* out_t, uint16_t* out_ext, int rext, float ext_scale,
                                hipStream_t stream);
 
-// The backward's operand pass in one launch: the row projection of dY with
-// the fp32 B [r][N] read directly (G = scale dY.B^T, masked as above, into
-// gd_t [r][T] and gd_ext [T][rext]); the bf16 A extension operand (job
-// a_ext, skipped when a_ext.hi is null); and W [N][K] -> Wt [K][N] (skipped
-// when Wt is null).
-hipError_t launch_lora_bwd_operands(const uint16_t* dY, int64_t T, int64_t N, const float* B, int r, float scale,
-                                    const uint8_t* mask, float keep, float* gd_t, uint16_t* gd_ext, int rext,
-                                    const PrepJob& a_ext, const uint16_t* W, int64_t K, uint16_t* Wt,
-                                    hipStream_t stream);
+// A pass over one X whose r ranks may be those of several projections
+// (rp ranks each): rank j belongs to projection p = j / rp and uses its mask
+// [T][rp] and out_t [rp][T] (entries may be null), and goes to column
+// p rext_p + j % rp of out_ext (row stride ext_ld; the pad columns up to
+// (p + 1) rext_p are zeroed). With P_f32 set the parameter is read as fp32
+// [r][C] and split hi / lo in registers instead of P_hi / P_lo.
+struct RowprojCall {
+    const uint16_t* X;
+    int64_t T, C;
+    const uint16_t* P_hi;
+    const uint16_t* P_lo;
+    const float* P_f32;
+    int r, rp;
+    float scale;
+    const uint8_t* mask[kMaxProj];
+    float keep;
+    float* out_t[kMaxProj];
+    uint16_t* out_ext;
+    int rext_p, ext_ld;
+    float ext_scale;
+};
+hipError_t launch_rowproj_bf16(const RowprojCall& c, hipStream_t stream);
+
+// The backward's operand pass for up to kMaxProj projections in one launch:
+// per projection the row projection of dY with the fp32 B [r][N] read
+// directly (G = scale dY.B^T, masked, into gd_t [r][T] and the columns of
+// gd_ext), the bf16 A extension operand (job a_ext, skipped when a_ext.hi is
+// null) and W [N][K] -> Wt [K][N] (skipped when Wt is null).
+struct OperandsCall {
+    const uint16_t* dY;
+    int64_t N;
+    const float* B;
+    const uint8_t* mask;
+    float* gd_t;
+    uint16_t* gd_ext;
+    PrepJob a_ext;
+    const uint16_t* W;
+    uint16_t* Wt;
+};
+hipError_t launch_lora_bwd_operands(const OperandsCall* calls, int n, int64_t T, int64_t K, int r, float scale,
+                                    float keep, int rext_p, int ext_ld, hipStream_t stream);
 
 // ------------------------------------------------- column reduction (split T)
 // One job: partial[s][j][c] = sum_{t in split s} Pt[j*T + t] * X[t][c] for
-// j < r16, c < C (j >= r contributes 0; r16 as for rowproj). X bf16 [T][C]
-// (C % 8 == 0), Pt fp32 [r][T]. A job with X == nullptr is skipped; both
-// jobs run in one launch per group of 32 ranks.
+// j < r, c < C, in the split partition of `splits` chunks; partial rows are
+// colreduce_rows(r) apart per split. X bf16 [T][C] (C % 8 == 0), Pt fp32
+// [r][T]. A job with X == nullptr is skipped; the jobs' 64-rank groups run in
+// one launch per rank-tile size.
 struct ColJob {
     const uint16_t* X;
     int64_t C;
     const float* Pt;
+    int r;
     int splits;
     float* partial;
 };
 int colreduce_splits(int64_t T, int64_t C);
-hipError_t launch_colreduce_bf16(int64_t T, int r, const ColJob& j0, const ColJob& j1, hipStream_t stream);
+hipError_t launch_colreduce_bf16(int64_t T, const ColJob* jobs, int n, hipStream_t stream);
 // One job: out = scale * sum_s partial[s][j][c] (s ascending) for j < r,
 // c < C, written to out[c*r + j] when transpose_out (dA [K][r]) else
-// out[j*C + c] (dB [r][N]); part_stride = r16 * C. A job with out == nullptr
-// is skipped; both jobs run in one launch.
+// out[j*C + c] (dB [r][N]); part_stride = colreduce_rows * C. A job with
+// out == nullptr is skipped; up to kSumJobs jobs run in one launch.
 struct SumJob {
     const float* partial;
     int splits;
     int64_t C;
     int64_t part_stride;
+    int r;
     float scale;
     bool transpose_out;
     float* out;
 };
-hipError_t launch_split_sum(int r, const SumJob& j0, const SumJob& j1, hipStream_t stream);
+hipError_t launch_split_sum(const SumJob* jobs, int n, hipStream_t stream);
 
 // -------------------------------------------------------------- GEMM bf16
-// C[M][N] = sum over two reduction segments of A_s . B_s^T (+ bias[n]), bf16
-// out. A_s bf16 [M][k_s] (row stride lda_s), B_s bf16 [N][k_s] (row stride
+// C[M][N] = sum over up to kGemmMaxSeg reduction segments of A_s . B_s^T
+// (+ bias[n]), bf16 out, the segments' products accumulated in segment
+// order. A_s bf16 [M][k_s] (row stride lda_s), B_s bf16 [N][k_s] (row stride
 // ldb_s). Row strides and k_s are multiples of 8; k_s may be 0.
+constexpr int kGemmMaxSeg = 5;
+constexpr int kGemmMaxOut = 4;
 struct GemmSeg {
     const uint16_t* a;
     int64_t lda;
@@ -87,8 +141,22 @@ struct GemmSeg {
     int64_t ldb;
     int64_t k;
 };
+hipError_t launch_gemm_bf16(int64_t M, int64_t N, const GemmSeg* segs, int nseg, const uint16_t* bias, uint16_t* c,
+                            int64_t ldc, hipStream_t stream);
 hipError_t launch_gemm_bf16(int64_t M, int64_t N, GemmSeg s0, GemmSeg s1, const uint16_t* bias, uint16_t* c,
                             int64_t ldc, hipStream_t stream);
+// Up to kGemmMaxOut output blocks of M rows in one launch (projections of
+// one input): block o is C_o[M][N_o] = sum over its segments of
+// A_s . B_s^T (+ bias_o); all blocks use one tile shape.
+struct GemmOut {
+    int64_t N;
+    GemmSeg seg[2];
+    int nseg;
+    const uint16_t* bias;
+    uint16_t* c;
+    int64_t ldc;
+};
+hipError_t launch_gemm_bf16_multi(int64_t M, const GemmOut* outs, int nout, hipStream_t stream);
 // Workgroup tiles of the bf16 GEMM for an M x N output with reduction length
 // K on `cus` compute units: `main` over columns [0, n1), `tail` over [n1, N)
 // (n1 == N: one tile shape; otherwise main is 256 x 256).

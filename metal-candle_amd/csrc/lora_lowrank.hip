@@ -69,22 +69,31 @@ __device__ __forceinline__ void transpose8x8(const uint4 (&R)[8], uint4 (&O)[8])
 }
 
 // ------------------------------------------------------------------ prep
-// Up to two operand-preparation jobs in one launch: threads [0, n0) do job 0,
-// the rest job 1.
+// Up to kPrepJobs operand-preparation jobs in one launch: element idx of the
+// launch belongs to the job whose range [start[j], start[j + 1]) holds it.
 __device__ __forceinline__ void prep_one(const PrepJob& j, int64_t idx) {
     const int64_t i = idx / j.cols_out, c = idx % j.cols_out;
     float v = 0.f;
     if (i < j.valid_rows && c < j.valid_cols) v = j.transpose ? j.src[c * j.ld_src + i] : j.src[i * j.ld_src + c];
     const uint16_t h = f32_to_bf16(v);
-    j.hi[idx] = h;
-    if (j.lo) j.lo[idx] = f32_to_bf16(v - bf16_to_f32(h));
+    const int64_t o = i * j.ld_out + c;
+    j.hi[o] = h;
+    if (j.lo) j.lo[o] = f32_to_bf16(v - bf16_to_f32(h));
 }
 
-__global__ __launch_bounds__(256) void prep_bf16(PrepJob j0, PrepJob j1, int64_t n0, int64_t n) {
+struct PrepBatch {
+    PrepJob job[kPrepJobs];
+    int64_t start[kPrepJobs + 1];
+    int njobs;
+};
+
+__global__ __launch_bounds__(256) void prep_bf16(PrepBatch b) {
+    const int64_t n = b.start[b.njobs];
     for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < n;
          idx += (int64_t)gridDim.x * blockDim.x) {
-        if (idx < n0) prep_one(j0, idx);
-        else prep_one(j1, idx - n0);
+        int j = 0;
+        while (j + 1 < b.njobs && idx >= b.start[j + 1]) ++j;
+        prep_one(b.job[j], idx - b.start[j]);
     }
 }
 
@@ -103,6 +112,11 @@ __global__ __launch_bounds__(256) void prep_bf16(PrepJob j0, PrepJob j1, int64_t
 // Arguments of one row projection. With PF32 the parameter is read as fp32
 // P [prows][C] (rows past prows load as zeros) and split into bf16 hi + lo in
 // registers; otherwise it comes prepared as bf16 P_hi / P_lo [16 RC][C].
+// The r ranks of a pass may belong to several projections of the same x
+// (rp ranks each, projection p = j / rp): rank j then takes projection p's
+// mask row and goes to its out_t rows and to columns p rext_p .. of the
+// extension operand (row stride ext_ld), whose pad columns rp .. rext_p-1 are
+// written as zeros.
 struct RowprojArgs {
     const uint16_t* X;
     int64_t T, C;
@@ -111,12 +125,14 @@ struct RowprojArgs {
     const float* Pf;
     int prows;
     int r;
+    int rp;
     float scale;
-    const uint8_t* mask;
+    const uint8_t* mask[kMaxProj];
     float keep;
-    float* out_t;
+    float* out_t[kMaxProj];
     uint16_t* out_ext;
-    int rext;
+    int rext_p;
+    int ext_ld;
     float ext_scale;
 };
 
@@ -124,10 +140,8 @@ template <int RC, int RT, int U, bool PF32>
 __device__ __forceinline__ void rowproj_body(const RowprojArgs& A, int64_t blk) {
     const uint16_t* __restrict__ X = A.X;
     const int64_t T = A.T, C = A.C;
-    const int r = A.r, rext = A.rext;
+    const int r = A.r, rp = A.rp, rext_p = A.rext_p, ext_ld = A.ext_ld;
     const float scale = A.scale, keep = A.keep, ext_scale = A.ext_scale;
-    const uint8_t* __restrict__ mask = A.mask;
-    float* __restrict__ out_t = A.out_t;
     uint16_t* __restrict__ out_ext = A.out_ext;
     constexpr int ROWS = 16 * RT;
     const int lane = lane_id();
@@ -221,14 +235,18 @@ __device__ __forceinline__ void rowproj_body(const RowprojArgs& A, int64_t blk) 
         for (int w = 1; w < 4; ++w) v += red[w][rt][rc][q][l];
         const int j = rc * 16 + (l & 15);
         const int64_t t = t0 + rt * 16 + (l >> 4) * 4 + q;
-        if (t >= T) continue;
-        if (j < r) {
-            v *= scale;
-            if (mask) v = mask[t * r + j] ? v * keep : 0.f;
-            if (out_t) out_t[(int64_t)j * T + t] = v;
-            if (out_ext) out_ext[t * rext + j] = f32_to_bf16(v * ext_scale);
-        } else if (j < rext && out_ext) {
-            out_ext[t * rext + j] = 0;
+        if (t >= T || j >= r) continue;
+        const int p = j / rp, jj = j - p * rp;
+        const uint8_t* mask = p == 0 ? A.mask[0] : p == 1 ? A.mask[1] : p == 2 ? A.mask[2] : A.mask[3];
+        float* out_t = p == 0 ? A.out_t[0] : p == 1 ? A.out_t[1] : p == 2 ? A.out_t[2] : A.out_t[3];
+        v *= scale;
+        if (mask) v = mask[t * rp + jj] ? v * keep : 0.f;
+        if (out_t) out_t[(int64_t)jj * T + t] = v;
+        if (out_ext) {
+            uint16_t* e = out_ext + t * ext_ld + p * rext_p;
+            e[jj] = f32_to_bf16(v * ext_scale);
+            if (jj == rp - 1)
+                for (int z = rp; z < rext_p; ++z) e[z] = 0;
         }
     }
 }
@@ -251,24 +269,34 @@ struct ColJobDev {
     const uint16_t* X;
     int64_t C;
     const float* Pt;
+    int r;
     int64_t chunk;
     float* partial;
     int64_t part_stride;
     int ctiles;
+    int splits;  // every split writes its partial (splits past T write zeros)
+};
+struct ColBatch {
+    ColJobDev job[kColJobs];
+    int start[kColJobs + 1];  // first workgroup of each job
+    int njobs;
 };
 
 // Two waves per SIMD (256 registers per lane at most): at 64 ranks the
 // kernel otherwise took 142 VGPRs + 128 AGPRs, one wave per SIMD, and
 // streamed at 2.4 TB/s; with the bound it fits in 236 VGPRs, no spills.
 template <int RC, int U, bool PTV>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void colreduce_bf16(int64_t T, int r, ColJobDev j0, ColJobDev j1, int nblk0) {
-    const bool second = (int)blockIdx.x >= nblk0;
-    const int b = second ? (int)blockIdx.x - nblk0 : (int)blockIdx.x;
-    const uint16_t* X = second ? j1.X : j0.X;
-    const int64_t C = second ? j1.C : j0.C;
-    const float* Pt = second ? j1.Pt : j0.Pt;
-    const int64_t chunk = second ? j1.chunk : j0.chunk;
-    const int ctiles = second ? j1.ctiles : j0.ctiles;
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void colreduce_bf16(int64_t T, ColBatch cb) {
+    int ji = 0;
+    while (ji + 1 < cb.njobs && (int)blockIdx.x >= cb.start[ji + 1]) ++ji;  // wave-uniform
+    const ColJobDev& J = cb.job[ji];
+    const int b = (int)blockIdx.x - cb.start[ji];
+    const uint16_t* X = J.X;
+    const int64_t C = J.C;
+    const float* Pt = J.Pt;
+    const int r = J.r;
+    const int64_t chunk = J.chunk;
+    const int ctiles = J.ctiles;
     const int lane = lane_id();
     const int wave = threadIdx.x >> 6;
     const int64_t c0 = (int64_t)(b % ctiles) * 128;
@@ -367,7 +395,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void c
         __syncthreads();
     }
     if (wave == 0 && col_ok) {
-        float* out = (second ? j1.partial : j0.partial) + (int64_t)(b / ctiles) * (second ? j1.part_stride : j0.part_stride);
+        float* out = J.partial + (int64_t)(b / ctiles) * J.part_stride;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             const int64_t c = col + e;
@@ -385,7 +413,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void c
 // out = scale * sum_s partial[s][j][c] (s ascending) for up to two jobs
 // (threads [0, n0) job 0). Splits are unrolled by 8 so that their loads are
 // in flight together; the adds stay in split order.
-__device__ __forceinline__ void split_sum_one(const SumJob& J, int r, int64_t idx) {
+__device__ __forceinline__ void split_sum_one(const SumJob& J, int64_t idx) {
+    const int r = J.r;
     const int64_t j = idx / J.C, c = idx % J.C;
     const float* p = J.partial + j * J.C + c;
     const int64_t stride = J.part_stride;
@@ -404,11 +433,19 @@ __device__ __forceinline__ void split_sum_one(const SumJob& J, int r, int64_t id
     else J.out[j * J.C + c] = s;
 }
 
-__global__ __launch_bounds__(256) void split_sum(int r, SumJob j0, SumJob j1, int64_t n0, int64_t n) {
+struct SumBatch {
+    SumJob job[kSumJobs];
+    int64_t start[kSumJobs + 1];
+    int njobs;
+};
+
+__global__ __launch_bounds__(256) void split_sum(SumBatch sb) {
+    const int64_t n = sb.start[sb.njobs];
     for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < n;
          idx += (int64_t)gridDim.x * blockDim.x) {
-        if (idx < n0) split_sum_one(j0, r, idx);
-        else split_sum_one(j1, r, idx - n0);
+        int j = 0;
+        while (j + 1 < sb.njobs && idx >= sb.start[j + 1]) ++j;
+        split_sum_one(sb.job[j], idx - sb.start[j]);
     }
 }
 
@@ -443,24 +480,43 @@ __device__ __forceinline__ void transpose_tile(const uint16_t* __restrict__ in, 
 }
 
 // ------------------------------------------- backward operands, one launch
-// The inputs of the backward GEMM and the rank-r pass of dY, as three block
-// roles of one launch (none reads another's output):
-//   [0, nrow)             G = s dY.B^T (row projection, B read as fp32)
-//   [nrow, nrow + nprep)  A -> the bf16 extension operand of the dX GEMM
-//   [.., + ntr)           W [N][K] -> W^T [K][N] (64 x 64 tiles, tcols wide)
+// The inputs of the backward GEMM and the rank-r pass of each dY, as block
+// roles of one launch (none reads another's output), for every projection
+// o < nproj of a call:
+//   row projection  G_o = s dY_o.B_o^T (B_o read as fp32), masked
+//   A extension     A_o -> the bf16 extension operand of the dX GEMM
+//   transpose       W_o [N_o][K] -> W_o^T [K][N_o] (64 x 64 tiles)
+// Workgroup b finds its role and projection from the prefix table `start`:
+// entry k nproj + o begins role k (0: row projection, 1: A extension,
+// 2: transpose) of projection o. Every projection's row-projection blocks
+// come first: they are the long-running ones, and dispatched behind the
+// thousands of short transpose blocks they would run as a tail.
+struct OperandsBatch {
+    RowprojArgs rp[kMaxProj];
+    PrepJob prep[kMaxProj];
+    const uint16_t* w[kMaxProj];
+    uint16_t* wt[kMaxProj];
+    int64_t wrows[kMaxProj], wcols[kMaxProj], tcols[kMaxProj];
+    int64_t start[3 * kMaxProj + 1];
+    int nproj;
+};
+
 template <int RC, int RT>
-__global__ __launch_bounds__(256) void lora_bwd_operands(RowprojArgs rp, int64_t nrow, PrepJob ja, int64_t nprep,
-                                                         const uint16_t* __restrict__ w, int64_t wrows, int64_t wcols,
-                                                         uint16_t* __restrict__ wt, int64_t tcols) {
+__global__ __launch_bounds__(256) void lora_bwd_operands(OperandsBatch ob) {
     const int64_t b = blockIdx.x;
-    if (b < nrow) {
-        rowproj_body<RC, RT, 1, true>(rp, b);
-    } else if (b < nrow + nprep) {
+    int role = 0;
+    while (role + 1 < 3 * ob.nproj && b >= ob.start[role + 1]) ++role;  // wave-uniform
+    const int kind = role / ob.nproj, o = role % ob.nproj;
+    const int64_t lb = b - ob.start[role];
+    const int64_t nblk = ob.start[role + 1] - ob.start[role];
+    if (kind == 0) {
+        rowproj_body<RC, RT, 1, true>(ob.rp[o], lb);
+    } else if (kind == 1) {
+        const PrepJob& ja = ob.prep[o];
         const int64_t n = ja.rows_out * ja.cols_out;
-        for (int64_t idx = (b - nrow) * 256 + threadIdx.x; idx < n; idx += nprep * 256) prep_one(ja, idx);
+        for (int64_t idx = lb * 256 + threadIdx.x; idx < n; idx += nblk * 256) prep_one(ja, idx);
     } else {
-        const int64_t t = b - nrow - nprep;
-        transpose_tile(w, wrows, wcols, wt, t / tcols, t % tcols);
+        transpose_tile(ob.w[o], ob.wrows[o], ob.wcols[o], ob.wt[o], lb / ob.tcols[o], lb % ob.tcols[o]);
     }
 }
 
@@ -504,13 +560,59 @@ __global__ __launch_bounds__(256) void colreduce_f32(const float* __restrict__ X
 
 }  // namespace
 
-hipError_t launch_prep_bf16(const PrepJob& j0, const PrepJob& j1, hipStream_t stream) {
-    const int64_t n0 = j0.hi ? j0.rows_out * j0.cols_out : 0;
-    const int64_t n = n0 + (j1.hi ? j1.rows_out * j1.cols_out : 0);
-    if (n == 0) return hipSuccess;
-    int64_t blocks = (n + 255) / 256;
+hipError_t launch_prep_bf16(const PrepJob* jobs, int n, hipStream_t stream) {
+    PrepBatch b{};
+    int k = 0;
+    for (int i = 0; i < n && k < kPrepJobs; ++i) {
+        if (!jobs[i].hi) continue;
+        b.job[k] = jobs[i];
+        if (b.job[k].ld_out == 0) b.job[k].ld_out = b.job[k].cols_out;
+        b.start[k + 1] = b.start[k] + jobs[i].rows_out * jobs[i].cols_out;
+        ++k;
+    }
+    b.njobs = k;
+    const int64_t total = b.start[k];
+    if (total == 0) return hipSuccess;
+    int64_t blocks = (total + 255) / 256;
     if (blocks > 4096) blocks = 4096;
-    prep_bf16<<<dim3((unsigned)blocks), 256, 0, stream>>>(j0, j1, n0, n);
+    prep_bf16<<<dim3((unsigned)blocks), 256, 0, stream>>>(b);
+    return hipGetLastError();
+}
+
+hipError_t launch_prep_bf16(const PrepJob& j0, const PrepJob& j1, hipStream_t stream) {
+    const PrepJob jobs[2] = {j0, j1};
+    return launch_prep_bf16(jobs, 2, stream);
+}
+
+namespace {
+RowprojArgs rowproj_args(const RowprojCall& c) {
+    RowprojArgs A{};
+    A.X = c.X; A.T = c.T; A.C = c.C;
+    A.Phi = c.P_hi; A.Plo = c.P_lo; A.Pf = c.P_f32; A.prows = c.r;
+    A.r = c.r; A.rp = c.rp > 0 ? c.rp : c.r;
+    A.scale = c.scale; A.keep = c.keep;
+    for (int p = 0; p < kMaxProj; ++p) { A.mask[p] = c.mask[p]; A.out_t[p] = c.out_t[p]; }
+    A.out_ext = c.out_ext; A.rext_p = c.rext_p; A.ext_ld = c.ext_ld; A.ext_scale = c.ext_scale;
+    return A;
+}
+}  // namespace
+
+hipError_t launch_rowproj_bf16(const RowprojCall& c, hipStream_t stream) {
+    // 64 token rows per workgroup: four MFMA row tiles share each parameter
+    // fragment (measured at the c4 shapes, loading the fragments costs as
+    // much per byte as streaming x, so the rows per fragment set the speed;
+    // 16 or 32 rows per workgroup ran at 2.7 / 3.6 TB/s, 64 at 4.9 TB/s for
+    // x [16384, 8960]). More than 64 ranks keep 32 rows (register budget).
+    // P_hi / P_lo hold 16 rowproj_rc(r) rows (zero past r).
+    const dim3 g64((unsigned)((c.T + 63) / 64)), g32((unsigned)((c.T + 31) / 32));
+    const RowprojArgs A = rowproj_args(c);
+    switch (rowproj_rc(c.r)) {
+        case 1: rowproj_bf16<1, 4, 1><<<g64, 256, 0, stream>>>(A); break;
+        case 2: rowproj_bf16<2, 4, 1><<<g64, 256, 0, stream>>>(A); break;
+        case 3: rowproj_bf16<3, 4, 1><<<g64, 256, 0, stream>>>(A); break;
+        case 4: rowproj_bf16<4, 4, 1><<<g64, 256, 0, stream>>>(A); break;
+        default: rowproj_bf16<8, 2, 1><<<g32, 256, 0, stream>>>(A); break;
+    }
     return hipGetLastError();
 }
 
@@ -518,44 +620,56 @@ hipError_t launch_rowproj_bf16(const uint16_t* X, int64_t T, int64_t C, const ui
                                const uint16_t* P_lo, int r, float scale, const uint8_t* mask,
                                float keep, float* out_t, uint16_t* out_ext, int rext, float ext_scale,
                                hipStream_t stream) {
-    // 64 token rows per workgroup: four MFMA row tiles share each parameter
-    // fragment (measured at the c4 shapes, loading the fragments costs as
-    // much per byte as streaming x, so the rows per fragment set the speed;
-    // 16 or 32 rows per workgroup ran at 2.7 / 3.6 TB/s, 64 at 4.9 TB/s for
-    // x [16384, 8960]). Rank 128 keeps 32 rows (register budget).
-    // P_hi / P_lo hold r16 = 16, 32, 64 or 128 rows (zero past r).
-    const int rc = r <= 16 ? 1 : r <= 32 ? 2 : r <= 64 ? 4 : 8;
-    const dim3 g64((unsigned)((T + 63) / 64)), g32((unsigned)((T + 31) / 32));
-    const RowprojArgs A{X, T, C, P_hi, P_lo, nullptr, 0, r, scale, mask, keep, out_t, out_ext, rext, ext_scale};
-    switch (rc) {
-        case 1: rowproj_bf16<1, 4, 1><<<g64, 256, 0, stream>>>(A); break;
-        case 2: rowproj_bf16<2, 4, 1><<<g64, 256, 0, stream>>>(A); break;
-        case 4: rowproj_bf16<4, 4, 1><<<g64, 256, 0, stream>>>(A); break;
-        default: rowproj_bf16<8, 2, 1><<<g32, 256, 0, stream>>>(A); break;
-    }
-    return hipGetLastError();
+    RowprojCall c{};
+    c.X = X; c.T = T; c.C = C; c.P_hi = P_hi; c.P_lo = P_lo; c.r = r; c.rp = r; c.scale = scale;
+    c.mask[0] = mask; c.keep = keep; c.out_t[0] = out_t; c.out_ext = out_ext; c.rext_p = rext; c.ext_ld = rext;
+    c.ext_scale = ext_scale;
+    return launch_rowproj_bf16(c, stream);
 }
 
-hipError_t launch_lora_bwd_operands(const uint16_t* dY, int64_t T, int64_t N, const float* B, int r, float scale,
-                                    const uint8_t* mask, float keep, float* gd_t, uint16_t* gd_ext, int rext,
-                                    const PrepJob& a_ext, const uint16_t* W, int64_t K, uint16_t* Wt,
-                                    hipStream_t stream) {
-    // row projection blocks as launch_rowproj_bf16 chooses them; B rows past
-    // r load as zeros
-    const int rc = r <= 16 ? 1 : r <= 32 ? 2 : r <= 64 ? 4 : 8;
+hipError_t launch_lora_bwd_operands(const OperandsCall* calls, int n, int64_t T, int64_t K, int r, float scale,
+                                    float keep, int rext_p, int ext_ld, hipStream_t stream) {
+    // row projection blocks as launch_rowproj_bf16 chooses them for one
+    // projection's r ranks; B rows past r load as zeros
+    const int rc = rowproj_rc(r);
     const int rows_per_block = rc == 8 ? 32 : 64;
-    const RowprojArgs A{dY, T, N, nullptr, nullptr, B, r, r, scale, mask, keep, gd_t, gd_ext, rext, 1.0f};
-    const int64_t nrow = (T + rows_per_block - 1) / rows_per_block;
-    int64_t nprep = 0;
-    if (a_ext.hi) nprep = std::min<int64_t>((a_ext.rows_out * a_ext.cols_out + 255) / 256, 64);
-    const int64_t tcols = (K + 63) / 64, trows = (N + 63) / 64;  // W is [N][K]
-    const int64_t ntr = Wt ? tcols * trows : 0;
-    const dim3 grid((unsigned)(nrow + nprep + ntr));
+    OperandsBatch ob{};
+    ob.nproj = n;
+    int64_t at = 0;
+    for (int o = 0; o < n; ++o) {
+        const OperandsCall& c = calls[o];
+        RowprojCall rc_call{};
+        rc_call.X = c.dY; rc_call.T = T; rc_call.C = c.N; rc_call.P_f32 = c.B; rc_call.r = r; rc_call.rp = r;
+        rc_call.scale = scale; rc_call.mask[0] = c.mask; rc_call.keep = keep; rc_call.out_t[0] = c.gd_t;
+        rc_call.out_ext = c.gd_ext; rc_call.rext_p = rext_p; rc_call.ext_ld = ext_ld; rc_call.ext_scale = 1.0f;
+        ob.rp[o] = rowproj_args(rc_call);
+        ob.prep[o] = c.a_ext;
+        if (ob.prep[o].ld_out == 0) ob.prep[o].ld_out = ob.prep[o].cols_out;
+        ob.w[o] = c.W;
+        ob.wt[o] = c.Wt;
+        ob.wrows[o] = c.N;  // W is [N][K]
+        ob.wcols[o] = K;
+        ob.tcols[o] = (K + 63) / 64;
+    }
+    for (int kind = 0; kind < 3; ++kind)
+        for (int o = 0; o < n; ++o) {
+            const OperandsCall& c = calls[o];
+            int64_t nb = 0;
+            if (kind == 0) nb = (c.gd_t || c.gd_ext) ? (T + rows_per_block - 1) / rows_per_block : 0;
+            if (kind == 1) nb = c.a_ext.hi ? std::min<int64_t>((c.a_ext.rows_out * c.a_ext.cols_out + 255) / 256, 64) : 0;
+            if (kind == 2) nb = c.Wt ? ob.tcols[o] * ((c.N + 63) / 64) : 0;
+            ob.start[kind * n + o] = at;
+            at += nb;
+        }
+    ob.start[3 * n] = at;
+    if (at == 0) return hipSuccess;
+    const dim3 grid((unsigned)at);
     switch (rc) {
-        case 1: lora_bwd_operands<1, 4><<<grid, 256, 0, stream>>>(A, nrow, a_ext, nprep, W, N, K, Wt, tcols); break;
-        case 2: lora_bwd_operands<2, 4><<<grid, 256, 0, stream>>>(A, nrow, a_ext, nprep, W, N, K, Wt, tcols); break;
-        case 4: lora_bwd_operands<4, 4><<<grid, 256, 0, stream>>>(A, nrow, a_ext, nprep, W, N, K, Wt, tcols); break;
-        default: lora_bwd_operands<8, 2><<<grid, 256, 0, stream>>>(A, nrow, a_ext, nprep, W, N, K, Wt, tcols); break;
+        case 1: lora_bwd_operands<1, 4><<<grid, 256, 0, stream>>>(ob); break;
+        case 2: lora_bwd_operands<2, 4><<<grid, 256, 0, stream>>>(ob); break;
+        case 3: lora_bwd_operands<3, 4><<<grid, 256, 0, stream>>>(ob); break;
+        case 4: lora_bwd_operands<4, 4><<<grid, 256, 0, stream>>>(ob); break;
+        default: lora_bwd_operands<8, 2><<<grid, 256, 0, stream>>>(ob); break;
     }
     return hipGetLastError();
 }
@@ -578,54 +692,71 @@ int colreduce_splits(int64_t T, int64_t C) {
     return (int)s;
 }
 
-hipError_t launch_colreduce_bf16(int64_t T, int r, const ColJob& a, const ColJob& b, hipStream_t stream) {
+hipError_t launch_colreduce_bf16(int64_t T, const ColJob* jobs, int n, hipStream_t stream) {
     // Ranks are processed in groups of up to 64 (four 16-row MFMA tiles of
-    // accumulators); each group reads X once, so r <= 64 takes one pass.
-    const int r16 = r <= 16 ? 16 : r <= 32 ? 32 : r <= 64 ? 64 : 128;
+    // accumulators); each group reads X once, so r <= 64 takes one pass. The
+    // groups are binned by their rank tiles (16, 32, 48 or 64 rows), one
+    // launch per bin of up to kColJobs groups.
     constexpr int GS = 64;
-    for (int g = 0; g * GS < r; ++g) {
-        const int rs = r - GS * g < GS ? r - GS * g : GS;
-        ColJobDev d[2];
-        int nblk[2] = {0, 0};
-        const ColJob* jobs[2] = {&a, &b};
-        for (int i = 0; i < 2; ++i) {
-            const ColJob& J = *jobs[i];
-            d[i] = ColJobDev{J.X, J.C, J.Pt ? J.Pt + (int64_t)GS * g * T : nullptr, 0,
-                             J.partial ? J.partial + (int64_t)GS * g * J.C : nullptr, (int64_t)r16 * J.C,
-                             (int)((J.C + 127) / 128)};
-            if (!J.X) continue;
-            d[i].chunk = round_up((T + J.splits - 1) / J.splits, 32);
-            nblk[i] = d[i].ctiles * J.splits;
+    ColJobDev bins[4][8 * kColJobs];
+    int nb[4] = {0, 0, 0, 0};
+    for (int i = 0; i < n; ++i) {
+        const ColJob& J = jobs[i];
+        if (!J.X) continue;
+        const int64_t stride = (int64_t)colreduce_rows(J.r) * J.C;
+        for (int g = 0; g * GS < J.r; ++g) {
+            const int rs = J.r - GS * g < GS ? J.r - GS * g : GS;
+            const int bin = rs <= 16 ? 0 : rs <= 32 ? 1 : rs <= 48 ? 2 : 3;
+            ColJobDev d{J.X, J.C, J.Pt + (int64_t)GS * g * T, rs, round_up((T + J.splits - 1) / J.splits, 32),
+                        J.partial + (int64_t)GS * g * J.C, stride, (int)((J.C + 127) / 128), J.splits};
+            if (nb[bin] < 8 * kColJobs) bins[bin][nb[bin]++] = d;
         }
-        if (nblk[0] + nblk[1] == 0) return hipSuccess;
-        if (nblk[0] == 0) { d[0] = d[1]; nblk[0] = nblk[1]; nblk[1] = 0; }
-        const dim3 grid((unsigned)(nblk[0] + nblk[1]));
-        const bool ptv = (T & 3) == 0;
-        if (rs <= 16) {
-            if (ptv) colreduce_bf16<1, 2, true><<<grid, 256, 0, stream>>>(T, rs, d[0], d[1], nblk[0]);
-            else colreduce_bf16<1, 2, false><<<grid, 256, 0, stream>>>(T, rs, d[0], d[1], nblk[0]);
-        } else if (rs <= 32) {
-            if (ptv) colreduce_bf16<2, 1, true><<<grid, 256, 0, stream>>>(T, rs, d[0], d[1], nblk[0]);
-            else colreduce_bf16<2, 1, false><<<grid, 256, 0, stream>>>(T, rs, d[0], d[1], nblk[0]);
-        } else {
-            if (ptv) colreduce_bf16<4, 1, true><<<grid, 256, 0, stream>>>(T, rs, d[0], d[1], nblk[0]);
-            else colreduce_bf16<4, 1, false><<<grid, 256, 0, stream>>>(T, rs, d[0], d[1], nblk[0]);
+    }
+    const bool ptv = (T & 3) == 0;
+    for (int bin = 0; bin < 4; ++bin) {
+        for (int first = 0; first < nb[bin]; first += kColJobs) {
+            ColBatch cb{};
+            cb.njobs = std::min(kColJobs, nb[bin] - first);
+            for (int k = 0; k < cb.njobs; ++k) {
+                cb.job[k] = bins[bin][first + k];
+                cb.start[k + 1] = cb.start[k] + cb.job[k].ctiles * cb.job[k].splits;
+            }
+            const dim3 grid((unsigned)cb.start[cb.njobs]);
+            if (bin == 0) {
+                if (ptv) colreduce_bf16<1, 2, true><<<grid, 256, 0, stream>>>(T, cb);
+                else colreduce_bf16<1, 2, false><<<grid, 256, 0, stream>>>(T, cb);
+            } else if (bin == 1) {
+                if (ptv) colreduce_bf16<2, 1, true><<<grid, 256, 0, stream>>>(T, cb);
+                else colreduce_bf16<2, 1, false><<<grid, 256, 0, stream>>>(T, cb);
+            } else if (bin == 2) {
+                if (ptv) colreduce_bf16<3, 1, true><<<grid, 256, 0, stream>>>(T, cb);
+                else colreduce_bf16<3, 1, false><<<grid, 256, 0, stream>>>(T, cb);
+            } else {
+                if (ptv) colreduce_bf16<4, 1, true><<<grid, 256, 0, stream>>>(T, cb);
+                else colreduce_bf16<4, 1, false><<<grid, 256, 0, stream>>>(T, cb);
+            }
+            hipError_t e = hipGetLastError();
+            if (e != hipSuccess) return e;
         }
-        hipError_t e = hipGetLastError();
-        if (e != hipSuccess) return e;
     }
     return hipSuccess;
 }
 
-hipError_t launch_split_sum(int r, const SumJob& a, const SumJob& b, hipStream_t stream) {
-    SumJob j0 = a, j1 = b;
-    if (!j0.out) { j0 = j1; j1.out = nullptr; }
-    const int64_t n0 = j0.out ? (int64_t)r * j0.C : 0;
-    const int64_t n = n0 + (j1.out ? (int64_t)r * j1.C : 0);
-    if (n == 0) return hipSuccess;
-    int64_t blocks = (n + 255) / 256;
+hipError_t launch_split_sum(const SumJob* jobs, int n, hipStream_t stream) {
+    SumBatch sb{};
+    int k = 0;
+    for (int i = 0; i < n && k < kSumJobs; ++i) {
+        if (!jobs[i].out) continue;
+        sb.job[k] = jobs[i];
+        sb.start[k + 1] = sb.start[k] + (int64_t)jobs[i].r * jobs[i].C;
+        ++k;
+    }
+    sb.njobs = k;
+    const int64_t total = sb.start[k];
+    if (total == 0) return hipSuccess;
+    int64_t blocks = (total + 255) / 256;
     if (blocks > 4096) blocks = 4096;
-    split_sum<<<dim3((unsigned)blocks), 256, 0, stream>>>(r, j0, j1, n0, n);
+    split_sum<<<dim3((unsigned)blocks), 256, 0, stream>>>(sb);
     return hipGetLastError();
 }
 

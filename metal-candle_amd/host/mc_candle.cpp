@@ -8,8 +8,10 @@
 #include <math.h>
 #include <string.h>
 
+#include <mutex>
 #include <random>
 #include <sstream>
+#include <unordered_map>
 
 #include "mc_hip.h"
 
@@ -71,18 +73,94 @@ int64_t product(const std::vector<int64_t>& d, size_t from, size_t to) {
     return p;
 }
 
-// Device-resident workspace for one call.
+// Caching allocator of device memory, as candle's Metal device keeps a pool
+// of buffers instead of allocating per op. Blocks are sized in 256-byte
+// units below 1 MiB and in 1/8-octave steps above, and a released block goes
+// back to its device's free list rather than to hipFree, which would wait for
+// the device. Every op of this interface enqueues on the null stream, so a
+// block released after its last op and handed to a later op is reused in
+// stream order: the later op's kernels run after the earlier ones finish.
+// The pool lives until the process ends (release_cached_device_memory()
+// returns its free blocks to the runtime).
+class DevicePool {
+  public:
+    static DevicePool& get() {
+        static DevicePool* pool = new DevicePool();  // never destroyed: tensors may outlive static teardown
+        return *pool;
+    }
+    static size_t bucket(size_t bytes) {
+        if (bytes <= ((size_t)1 << 20)) return (bytes + 255) & ~(size_t)255;
+        size_t p = (size_t)1 << 20;
+        while (p * 2 <= bytes) p *= 2;
+        const size_t step = p / 8;
+        return (bytes + step - 1) / step * step;
+    }
+    hipError_t alloc(int device, size_t bytes, void** out) {
+        const size_t b = bucket(bytes);
+        {
+            std::lock_guard<std::mutex> lk(mu_);
+            auto& fl = free_[device];
+            auto it = fl.find(b);
+            if (it != fl.end() && !it->second.empty()) {
+                *out = it->second.back();
+                it->second.pop_back();
+                cached_ -= b;
+                ++hits_;
+                return hipSuccess;
+            }
+        }
+        hipError_t e = hipMalloc(out, b);
+        if (e == hipErrorOutOfMemory) {  // give the cached blocks back and try once more
+            release();
+            e = hipMalloc(out, b);
+        }
+        return e;
+    }
+    void free(int device, size_t bytes, void* p) {
+        std::lock_guard<std::mutex> lk(mu_);
+        free_[device][bucket(bytes)].push_back(p);
+        cached_ += bucket(bytes);
+    }
+    void release() {
+        std::lock_guard<std::mutex> lk(mu_);
+        for (auto& dev : free_)
+            for (auto& kv : dev.second)
+                for (void* p : kv.second) (void)hipFree(p);
+        free_.clear();
+        cached_ = 0;
+    }
+    size_t cached() {
+        std::lock_guard<std::mutex> lk(mu_);
+        return cached_;
+    }
+    size_t hits() {
+        std::lock_guard<std::mutex> lk(mu_);
+        return hits_;
+    }
+
+  private:
+    std::mutex mu_;
+    std::unordered_map<int, std::unordered_map<size_t, std::vector<void*>>> free_;
+    size_t cached_ = 0, hits_ = 0;
+};
+
+// Device-resident workspace for one call, from the pool.
 struct Workspace {
     void* p = nullptr;
+    int device = 0;
+    size_t bytes = 0;
     ~Workspace() {
-        if (p) (void)hipFree(p);
+        if (p) DevicePool::get().free(device, bytes, p);
     }
 };
 
 Result<void, CandleError> alloc_ws(Workspace& ws, size_t bytes) {
     if (bytes == 0) return {};
-    hipError_t e = hipMalloc(&ws.p, bytes);
+    hipError_t e = hipGetDevice(&ws.device);
     if (e != hipSuccess) return hip_error("workspace allocation", e);
+    e = DevicePool::get().alloc(ws.device, bytes, &ws.p);
+    if (e != hipSuccess) return hip_error("workspace allocation", e);
+    ws.bytes = bytes;
     return {};
 }
 
@@ -91,6 +169,10 @@ bool same_device(const Tensor& a, const Tensor& b) {
 }
 
 }  // namespace
+
+void release_cached_device_memory() { DevicePool::get().release(); }
+size_t cached_device_bytes() { return DevicePool::get().cached(); }
+size_t device_pool_hits() { return DevicePool::get().hits(); }
 
 std::string dims_to_string(const std::vector<int64_t>& dims) {
     std::ostringstream s;
@@ -128,9 +210,10 @@ Result<Tensor, CandleError> Tensor::empty(std::vector<int64_t> dims, DType dtype
         hipError_t e = hipSetDevice(device.ordinal);
         if (e != hipSuccess) return hip_error("hipSetDevice", e);
         void* p = nullptr;
-        e = hipMalloc(&p, bytes);
+        e = DevicePool::get().alloc(device.ordinal, bytes, &p);
         if (e != hipSuccess) return hip_error("hipMalloc", e);
-        t.storage_ = std::shared_ptr<void>(p, [](void* q) { (void)hipFree(q); });
+        const int ord = device.ordinal;
+        t.storage_ = std::shared_ptr<void>(p, [ord, bytes](void* q) { DevicePool::get().free(ord, bytes, q); });
     }
     return t;
 }
@@ -343,9 +426,6 @@ Result<std::pair<Tensor, LoRASaved>, CandleError> FusedLoRAOp::forward_with_base
                                      mask ? static_cast<const uint8_t*>(mask->data()) : nullptr, y.value().data(),
                                      static_cast<float*>(h.value().data()), ws.p, ws_bytes, nullptr);
     if (st != MC_OK) return mc_error("fused_lora_forward", st);
-    if (ws.p) {
-        // The workspace is freed at scope exit; hipFree waits for the device.
-    }
     return std::make_pair(std::move(y.value()), LoRASaved{std::move(h.value())});
 }
 

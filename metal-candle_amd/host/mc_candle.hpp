@@ -116,6 +116,16 @@ struct Device {
 
 std::string dims_to_string(const std::vector<int64_t>& dims);  // "[2, 3]", as {:?} of a dims slice
 
+// Device memory of HIP tensors and op workspaces comes from a per-device
+// caching pool (candle's Metal device pools its buffers likewise): released
+// blocks are kept for reuse in stream order instead of being freed, so ops in
+// a steady loop neither allocate nor synchronise the device. These return the
+// cached blocks to the runtime, and report the bytes cached and the number of
+// allocations served from the cache.
+void release_cached_device_memory();
+size_t cached_device_bytes();
+size_t device_pool_hits();
+
 // A contiguous row-major tensor in host memory (Device::cpu) or HIP device
 // memory (Device::hip). Copies share storage, like candle's Arc'd storage.
 class Tensor {

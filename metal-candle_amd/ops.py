@@ -12,7 +12,7 @@ import ctypes
 import torch
 
 from . import _lib
-from ._lib import AdamWConfig, AdamWTensor, AttnDesc, LoraDesc, McError, XentDesc, check, lib
+from ._lib import AdamWConfig, AdamWTensor, AttnDesc, LoraDesc, LoraProj, McError, XentDesc, check, lib
 
 _DTYPES = {torch.float32: _lib.MC_F32, torch.bfloat16: _lib.MC_BF16}
 
@@ -156,6 +156,84 @@ def lora_backward(x, A, B, dY, scale, W=None, mask=None, dropout_p=0.0, h_save=N
     check(lib().mc_lora_bwd(ctypes.byref(d), _ptr(x), _ptr(W), _ptr(A), _ptr(B), _ptr(mask), _ptr(h_save),
                             _ptr(dY), _ptr(dX), _ptr(dA), _ptr(dB), _ptr(ws), ws_n, _stream(dY)))
     return dX, dA, dB
+
+
+def _ptr_array(ts):
+    return (ctypes.c_void_p * len(ts))(*[None if t is None else t.data_ptr() for t in ts])
+
+
+def _group_table(x, projs, dropout_p):
+    """Validate a grouped call's projections (dicts with W, bias, A, B, mask)
+    against the shared x [..., K] and build the C table; returns (table, K,
+    r, T, [N_g])."""
+    if not isinstance(projs, (list, tuple)) or not 1 <= len(projs) <= _lib.MC_LORA_MAX_GROUP:
+        raise McError(_lib.MC_ERR_SHAPE, f"a group holds 1 to {_lib.MC_LORA_MAX_GROUP} projections")
+    if not isinstance(x, torch.Tensor) or x.dim() < 1:
+        raise McError(_lib.MC_ERR_SHAPE, "Input must have at least 1 dimension")
+    _contig(x, "x")
+    if x.dtype != torch.bfloat16:
+        raise McError(_lib.MC_ERR_DTYPE, "grouped projections run in bfloat16 only")
+    K = x.shape[-1]
+    T = x.numel() // K if K else 0
+    table = (LoraProj * len(projs))()
+    r0, Ns = None, []
+    for g, p in enumerate(projs):
+        Kg, r, N = _lora_factors(p["A"], p["B"])
+        if Kg != K:
+            raise McError(_lib.MC_ERR_SHAPE, f"Input feature dimension mismatch: expected {Kg}, got {K}")
+        if r0 is not None and r != r0:
+            raise McError(_lib.MC_ERR_SHAPE, f"projection {g}: rank {r} differs from the group's {r0}")
+        r0 = r
+        _expect(p["A"], "A", dtype=torch.float32, device=x.device)
+        _expect(p["B"], "B", dtype=torch.float32, device=x.device)
+        _expect(p.get("W"), "W", shape=(N, K), dtype=x.dtype, device=x.device)
+        _expect(p.get("bias"), "bias", shape=(N,), dtype=x.dtype, device=x.device)
+        _expect(p.get("mask"), "mask", shape=(T, r), dtype=torch.uint8, device=x.device)
+        table[g] = LoraProj(N, *[None if p.get(k) is None else p[k].data_ptr() for k in ("W", "bias", "A", "B", "mask")])
+        Ns.append(N)
+    return table, K, r0, T, Ns
+
+
+def lora_group_forward(x, projs, scale, dropout_p=0.0, save_hidden=True):
+    """The LoRA projections of one input x [..., K] in one call
+    (mc_lora_group_fwd): projs is a list of 1-4 dicts with W [N_g, K], bias
+    [N_g] (or None), A [K, r], B [r, N_g] and mask [T, r] (or None). Returns
+    ([y_g], [h_save_g]); each y_g equals lora_forward's for that projection."""
+    table, K, r, T, Ns = _group_table(x, projs, dropout_p)
+    d = LoraDesc(T, K, Ns[0], r, float(scale), float(dropout_p), _lib.MC_BF16)
+    ys = [torch.empty(*x.shape[:-1], N, dtype=x.dtype, device=x.device) for N in Ns]
+    hs = [torch.empty(r, T, dtype=torch.float32, device=x.device) if save_hidden else None for _ in Ns]
+    n = len(Ns)
+    ws_n = lib().mc_lora_group_fwd_workspace_size(ctypes.byref(d), table, n)
+    ws = _workspace(ws_n, x.device)
+    check(lib().mc_lora_group_fwd(ctypes.byref(d), _ptr(x), table, n, _ptr_array(ys), _ptr_array(hs), _ptr(ws), ws_n,
+                                  _stream(x)))
+    return ys, hs
+
+
+def lora_group_backward(x, projs, dYs, scale, dropout_p=0.0, h_saves=None, need_dx=True, need_dA=True, need_dB=True):
+    """Backward of lora_group_forward (mc_lora_group_bwd): returns (dX, [dA_g],
+    [dB_g]) where dX [..., K] is the sum of every projection's input gradient."""
+    table, K, r, T, Ns = _group_table(x, projs, dropout_p)
+    if not isinstance(dYs, (list, tuple)) or len(dYs) != len(Ns):
+        raise McError(_lib.MC_ERR_SHAPE, "one dY per projection")
+    for g, (dy, N) in enumerate(zip(dYs, Ns)):
+        _expect(dy, f"dY[{g}]", shape=tuple(x.shape[:-1]) + (N,), dtype=x.dtype, device=x.device)
+    if h_saves is not None:
+        for g, h in enumerate(h_saves):
+            _expect(h, f"h_save[{g}]", shape=(r, T), dtype=torch.float32, device=x.device)
+    d = LoraDesc(T, K, Ns[0], r, float(scale), float(dropout_p), _lib.MC_BF16)
+    dev = x.device
+    dX = torch.empty_like(x) if need_dx else None
+    dAs = [torch.empty(K, r, dtype=torch.float32, device=dev) if need_dA else None for _ in Ns]
+    dBs = [torch.empty(r, N, dtype=torch.float32, device=dev) if need_dB else None for N in Ns]
+    n = len(Ns)
+    ws_n = lib().mc_lora_group_bwd_workspace_size(ctypes.byref(d), table, n)
+    ws = _workspace(ws_n, dev)
+    hp = _ptr_array(h_saves) if h_saves is not None else None
+    check(lib().mc_lora_group_bwd(ctypes.byref(d), _ptr(x), table, n, hp, _ptr_array(dYs), _ptr(dX), _ptr_array(dAs),
+                                  _ptr_array(dBs), _ptr(ws), ws_n, _stream(x)))
+    return dX, dAs, dBs
 
 
 def rms_norm_forward(x, eps, w=None, save_rstd=True):

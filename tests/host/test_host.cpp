@@ -1045,6 +1045,33 @@ CASE(adapter_config_and_creation, false) {
     CHECK(a.num_frozen_parameters(1000000) == 1000000 - a.num_trainable_parameters());
 }
 
+// The device pool: a released block of a size is reused by the next
+// allocation of that size (no hipMalloc, no hipFree in a steady loop).
+CASE(device_pool_reuses_blocks, true) {
+    const size_t hits0 = device_pool_hits();
+    void* first = nullptr;
+    {
+        TRY(t, Tensor::empty({1024, 1024}, DType::F32, kHip));
+        first = t.data();
+    }
+    CHECK(cached_device_bytes() >= (size_t)4 << 20);
+    TRY(u, Tensor::empty({1024, 1024}, DType::F32, kHip));
+    CHECK(u.data() == first);
+    CHECK(device_pool_hits() == hits0 + 1);
+    // ops that need workspace draw it from the pool as well: two identical
+    // backward calls, the second served from cached blocks
+    TRY(op, FusedRMSNormOp::create(1e-6f));
+    std::vector<float> xv(64 * 256, 0.5f);
+    TRY(x, Tensor::from_slice(xv, {64, 256}, kHip));
+    TRY(fw, op.forward_weighted(x, nullptr));
+    TRY(g1, op.backward(x, nullptr, fw.second, x));
+    const size_t hits1 = device_pool_hits();
+    TRY(g2, op.backward(x, nullptr, fw.second, x));
+    CHECK(device_pool_hits() > hits1);
+    release_cached_device_memory();
+    CHECK(cached_device_bytes() == 0);
+}
+
 // ================================================================== checkpoints
 static std::string tmp_path(const char* name) {
     const char* d = getenv("MC_CKPT_DIR");

@@ -169,3 +169,55 @@ def test_adamw_table_errors(mc):
     assert L.mc_adamw_step(ctypes.byref(cfg), t, 1, None) == 4
     t[0] = mc._lib.AdamWTensor(None, None, None, None, None, 0, 1)   # empty tensors need no pointers
     assert L.mc_adamw_step(ctypes.byref(cfg), t, 1, None) == 0
+
+
+def test_lora_group_validation(mc):
+    """Grouped entry points: the shared descriptor is checked as for one
+    projection, every projection's N and pointers on their own, before any
+    launch."""
+    L = mc._lib.lib()
+    d = _desc(mc, T=16, K=16, N=0, r=4)
+    fake = 256
+    projs = (mc._lib.LoraProj * 2)(mc._lib.LoraProj(16, fake, None, fake, fake, None),
+                                   mc._lib.LoraProj(24, fake, None, fake, fake, None))
+    need_f = L.mc_lora_group_fwd_workspace_size(ctypes.byref(d), projs, 2)
+    need_b = L.mc_lora_group_bwd_workspace_size(ctypes.byref(d), projs, 2)
+    assert need_f > 0 and need_b > 0
+    ys = (ctypes.c_void_p * 2)(fake, fake)
+    hs = (ctypes.c_void_p * 2)(fake, fake)
+    w = ctypes.c_void_p(fake)
+    # count out of range
+    assert L.mc_lora_group_fwd(ctypes.byref(d), w, projs, 0, ys, hs, w, need_f, None) == 2
+    assert L.mc_lora_group_fwd(ctypes.byref(d), w, projs, 5, ys, hs, w, need_f, None) == 2
+    # fp32 is per-projection only
+    d32 = _desc(mc, T=16, K=16, N=0, r=4, dtype=0)
+    assert L.mc_lora_group_fwd(ctypes.byref(d32), w, projs, 2, ys, hs, w, need_f, None) == 3
+    assert "bf16 only" in mc._lib.last_error()
+    # a projection's N not a multiple of 8
+    projs[1].out_features = 20
+    assert L.mc_lora_group_fwd_workspace_size(ctypes.byref(d), projs, 2) == 0
+    assert L.mc_lora_group_fwd(ctypes.byref(d), w, projs, 2, ys, hs, w, need_f, None) == 2
+    projs[1].out_features = 24
+    # missing B, bias without W, dropout without a mask
+    projs[0].B = None
+    assert L.mc_lora_group_fwd(ctypes.byref(d), w, projs, 2, ys, hs, w, need_f, None) == 1
+    projs[0].B = fake
+    projs[1].W, projs[1].bias = None, fake
+    assert L.mc_lora_group_fwd(ctypes.byref(d), w, projs, 2, ys, hs, w, need_f, None) == 1
+    assert "bias given without W" in mc._lib.last_error()
+    projs[1].W, projs[1].bias = fake, None
+    d.dropout_p = 0.1
+    assert L.mc_lora_group_fwd(ctypes.byref(d), w, projs, 2, ys, hs, w, need_f, None) == 1
+    assert "requires a mask" in mc._lib.last_error()
+    d.dropout_p = 0.0
+    # workspace too small, misaligned output
+    assert L.mc_lora_group_fwd(ctypes.byref(d), w, projs, 2, ys, hs, w, need_f - 1, None) == 6
+    ys[1] = 264
+    assert L.mc_lora_group_fwd(ctypes.byref(d), w, projs, 2, ys, hs, w, need_f, None) == 4
+    # backward: dB without h_save
+    dys = (ctypes.c_void_p * 2)(fake, fake)
+    dbs = (ctypes.c_void_p * 2)(fake, None)
+    assert L.mc_lora_group_bwd(ctypes.byref(d), w, projs, 2, None, dys, None, None, dbs, w, need_b, None) == 1
+    assert "requires h_save" in mc._lib.last_error()
+    # nothing requested: no work, OK
+    assert L.mc_lora_group_bwd(ctypes.byref(d), w, projs, 2, None, dys, None, None, None, w, need_b, None) == 0
