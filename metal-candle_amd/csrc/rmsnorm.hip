@@ -133,8 +133,7 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_scalar(int64_t rows, int64_t 
 
 // ------------------------------------------------------------ backward
 // Block b owns rows [b*chunk, min(rows, (b+1)*chunk)); wave k of the block
-// takes rows k, k+4, ... of that range, two at a time (the loads of both
-// rows issued before either is used). dw partials: per lane in registers,
+// takes rows k, k+4, ... of that range in order. dw partials: per lane in registers,
 // accumulated in row order, then summed over the 4 waves in LDS in wave
 // order, written to partial[b][dim].
 template <typename T, int VPL, bool DW>
@@ -172,60 +171,59 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_vec(int64_t rows, int dim, fl
 #pragma unroll
         for (int e = 0; e < N; ++e) acc[i][e] = 0.f;
 
-    for (int64_t rr = wave; rr < nr; rr += 2 * kRowsPerBlock) {
-        // raw 16-byte vectors of both rows (converted on use: bf16 rows stay
-        // packed, which halves the registers they hold)
-        i32x4 xq[2][VPL], gq[2][VPL];
+    // Software pipeline, one row in flight: the raw 16-byte vectors of the
+    // wave's next row are requested before the current row is used (bf16
+    // rows stay packed until use, which halves the registers they hold).
+    auto load_row = [&](int64_t q, i32x4 (&xq)[VPL], i32x4 (&gq)[VPL]) {
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int64_t q = rr + h * kRowsPerBlock;  // rows past the range load zeros
+        for (int i = 0; i < VPL; ++i) {
+            const int vi = lane + i * kWave;
+            const uint32_t off = vi < nvec ? (uint32_t)((q * dim + vi * N) * ES) : kOOB;
+            xq[i] = buf_load16(rx, off);
+            gq[i] = buf_load16(rg, off);
+        }
+    };
+    i32x4 nx[VPL], ng[VPL];
+    if (wave < nr) load_row(wave, nx, ng);
+    for (int64_t q = wave; q < nr; q += kRowsPerBlock) {
+        i32x4 xq[VPL], gq[VPL];
 #pragma unroll
-            for (int i = 0; i < VPL; ++i) {
-                const int vi = lane + i * kWave;
-                const uint32_t off = vi < nvec ? (uint32_t)((q * dim + vi * N) * ES) : kOOB;
-                xq[h][i] = buf_load16(rx, off);
-                gq[h][i] = buf_load16(rg, off);
+        for (int i = 0; i < VPL; ++i) { xq[i] = nx[i]; gq[i] = ng[i]; }
+        if (q + kRowsPerBlock < nr) load_row(q + kRowsPerBlock, nx, ng);  // wave-uniform
+        float ss = 0.f, gx = 0.f;
+#pragma unroll
+        for (int i = 0; i < VPL; ++i) {
+            float xv[N], gv[N];
+            BVec<T>::unpack(xq[i], xv);
+            BVec<T>::unpack(gq[i], gv);
+#pragma unroll
+            for (int e = 0; e < N; ++e) {
+                ss += xv[e] * xv[e];
+                gx += gv[e] * wv[i][e] * xv[e];
             }
         }
+        float r;
+        if (rstd) {
+            r = rstd[r0 + q];
+            gx = wave_sum(gx);
+        } else {
+            ss = wave_sum(ss);
+            gx = wave_sum(gx);
+            r = 1.0f / sqrtf(ss / (float)dim + eps);
+        }
+        const float c = r * r * r * gx / (float)dim;
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int64_t q = rr + h * kRowsPerBlock;
-            if (q >= nr) break;  // wave-uniform
-            float ss = 0.f, gx = 0.f;
+        for (int i = 0; i < VPL; ++i) {
+            const int vi = lane + i * kWave;
+            float xv[N], gv[N], o[N];
+            BVec<T>::unpack(xq[i], xv);
+            BVec<T>::unpack(gq[i], gv);
 #pragma unroll
-            for (int i = 0; i < VPL; ++i) {
-                float xv[N], gv[N];
-                BVec<T>::unpack(xq[h][i], xv);
-                BVec<T>::unpack(gq[h][i], gv);
+            for (int e = 0; e < N; ++e) o[e] = r * gv[e] * wv[i][e] - xv[e] * c;
+            BVec<T>::store(rd, vi < nvec ? (uint32_t)((q * dim + vi * N) * ES) : kOOB, o);
+            if constexpr (DW) {
 #pragma unroll
-                for (int e = 0; e < N; ++e) {
-                    ss += xv[e] * xv[e];
-                    gx += gv[e] * wv[i][e] * xv[e];
-                }
-            }
-            float r;
-            if (rstd) {
-                r = rstd[r0 + q];
-                gx = wave_sum(gx);
-            } else {
-                ss = wave_sum(ss);
-                gx = wave_sum(gx);
-                r = 1.0f / sqrtf(ss / (float)dim + eps);
-            }
-            const float c = r * r * r * gx / (float)dim;
-#pragma unroll
-            for (int i = 0; i < VPL; ++i) {
-                const int vi = lane + i * kWave;
-                float xv[N], gv[N], o[N];
-                BVec<T>::unpack(xq[h][i], xv);
-                BVec<T>::unpack(gq[h][i], gv);
-#pragma unroll
-                for (int e = 0; e < N; ++e) o[e] = r * gv[e] * wv[i][e] - xv[e] * c;
-                BVec<T>::store(rd, vi < nvec ? (uint32_t)((q * dim + vi * N) * ES) : kOOB, o);
-                if constexpr (DW) {
-#pragma unroll
-                    for (int e = 0; e < N; ++e) acc[i][e] += gv[e] * xv[e] * r;
-                }
+                for (int e = 0; e < N; ++e) acc[i][e] += gv[e] * xv[e] * r;
             }
         }
     }
