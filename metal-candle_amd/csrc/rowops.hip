@@ -164,15 +164,26 @@ __global__ __launch_bounds__(256) void layernorm_bwd_vec(int64_t rows, int dim, 
 #pragma unroll
         for (int e = 0; e < N; ++e) aw[i][e] = ab[i][e] = 0.f;
 
-    for (int64_t q = wave; q < nr; q += kRowsPerBlock) {
-        float xv[VPL][N], gv[VPL][N];
+    // Software pipeline, one row in flight: the raw 16-byte vectors of the
+    // wave's next row are requested before the current row is used.
+    auto load_row = [&](int64_t q, i32x4 (&xq)[VPL], i32x4 (&gq)[VPL]) {
 #pragma unroll
         for (int i = 0; i < VPL; ++i) {
             const int vi = lane + i * kWave;
             const uint32_t off = vi < nvec ? (uint32_t)((q * dim + vi * N) * ES) : kOOB;
-            BVec<T>::load(rx, off, xv[i]);
-            BVec<T>::load(rg, off, gv[i]);
+            xq[i] = buf_load16(rx, off);
+            gq[i] = buf_load16(rg, off);
         }
+    };
+    i32x4 nx[VPL], ng[VPL];
+    if (wave < nr) load_row(wave, nx, ng);
+    for (int64_t q = wave; q < nr; q += kRowsPerBlock) {
+        // raw vectors of the current row, converted on use (bf16 rows stay
+        // packed, which halves the registers they hold)
+        i32x4 xq[VPL], gq[VPL];
+#pragma unroll
+        for (int i = 0; i < VPL; ++i) { xq[i] = nx[i]; gq[i] = ng[i]; }
+        if (q + kRowsPerBlock < nr) load_row(q + kRowsPerBlock, nx, ng);  // wave-uniform
         float mean, r;
         if (mean_in && rstd_in) {
             mean = mean_in[r0 + q];
@@ -180,17 +191,22 @@ __global__ __launch_bounds__(256) void layernorm_bwd_vec(int64_t rows, int dim, 
         } else {
             float s = 0.f;
 #pragma unroll
-            for (int i = 0; i < VPL; ++i)
+            for (int i = 0; i < VPL; ++i) {
+                float xv[N];
+                BVec<T>::unpack(xq[i], xv);
 #pragma unroll
-                for (int e = 0; e < N; ++e) s += xv[i][e];
+                for (int e = 0; e < N; ++e) s += xv[e];
+            }
             mean = wave_sum(s) / (float)dim;
             float c2 = 0.f;
 #pragma unroll
             for (int i = 0; i < VPL; ++i) {
                 const bool ok = lane + i * kWave < nvec;
+                float xv[N];
+                BVec<T>::unpack(xq[i], xv);
 #pragma unroll
                 for (int e = 0; e < N; ++e) {
-                    const float c = xv[i][e] - mean;
+                    const float c = xv[e] - mean;
                     c2 += ok ? c * c : 0.f;
                 }
             }
@@ -200,10 +216,13 @@ __global__ __launch_bounds__(256) void layernorm_bwd_vec(int64_t rows, int dim, 
 #pragma unroll
         for (int i = 0; i < VPL; ++i) {
             const bool ok = lane + i * kWave < nvec;
+            float xv[N], gv[N];
+            BVec<T>::unpack(xq[i], xv);
+            BVec<T>::unpack(gq[i], gv);
 #pragma unroll
             for (int e = 0; e < N; ++e) {
-                const float xh = ok ? (xv[i][e] - mean) * r : 0.f;
-                const float g = gv[i][e] * wv[i][e];
+                const float xh = ok ? (xv[e] - mean) * r : 0.f;
+                const float g = gv[e] * wv[i][e];
                 sg += g;
                 sgx += g * xh;
             }
@@ -213,41 +232,43 @@ __global__ __launch_bounds__(256) void layernorm_bwd_vec(int64_t rows, int dim, 
 #pragma unroll
         for (int i = 0; i < VPL; ++i) {
             const int vi = lane + i * kWave;
-            float o[N];
+            float xv[N], gv[N], o[N];
+            BVec<T>::unpack(xq[i], xv);
+            BVec<T>::unpack(gq[i], gv);
 #pragma unroll
             for (int e = 0; e < N; ++e) {
-                const float xh = (xv[i][e] - mean) * r;
-                o[e] = r * (gv[i][e] * wv[i][e] - mg - xh * mgx);
+                const float xh = (xv[e] - mean) * r;
+                o[e] = r * (gv[e] * wv[i][e] - mg - xh * mgx);
                 if constexpr (DW) {
-                    aw[i][e] += gv[i][e] * xh;
-                    ab[i][e] += gv[i][e];
+                    aw[i][e] += gv[e] * xh;
+                    ab[i][e] += gv[e];
                 }
             }
             BVec<T>::store(rd, vi < nvec ? (uint32_t)((q * dim + vi * N) * ES) : kOOB, o);
         }
     }
     if constexpr (DW) {
-        extern __shared__ float lds[];  // [2][kRowsPerBlock][dim]
+        // The two partials pass through one [kRowsPerBlock][dim] LDS buffer in
+        // turn (dw, then db), each summed over the waves in wave order.
+        extern __shared__ float lds[];
 #pragma unroll
-        for (int i = 0; i < VPL; ++i) {
-            const int vi = lane + i * kWave;
-            if (vi < nvec)
+        for (int pass = 0; pass < 2; ++pass) {
+            if (pass) __syncthreads();  // every wave has read the dw pass
 #pragma unroll
-                for (int e = 0; e < N; ++e) {
-                    lds[wave * dim + vi * N + e] = aw[i][e];
-                    lds[(kRowsPerBlock + wave) * dim + vi * N + e] = ab[i][e];
-                }
-        }
-        __syncthreads();
-        for (int j = threadIdx.x; j < dim; j += blockDim.x) {
-            float sw = lds[j], sb = lds[kRowsPerBlock * dim + j];
+            for (int i = 0; i < VPL; ++i) {
+                const int vi = lane + i * kWave;
+                if (vi < nvec)
 #pragma unroll
-            for (int k = 1; k < kRowsPerBlock; ++k) {
-                sw += lds[k * dim + j];
-                sb += lds[(kRowsPerBlock + k) * dim + j];
+                    for (int e = 0; e < N; ++e) lds[wave * dim + vi * N + e] = pass ? ab[i][e] : aw[i][e];
             }
-            part_w[(int64_t)blockIdx.x * dim + j] = sw;
-            part_b[(int64_t)blockIdx.x * dim + j] = sb;
+            __syncthreads();
+            float* part = pass ? part_b : part_w;
+            for (int j = threadIdx.x; j < dim; j += blockDim.x) {
+                float sum = lds[j];
+#pragma unroll
+                for (int k = 1; k < kRowsPerBlock; ++k) sum += lds[k * dim + j];
+                part[(int64_t)blockIdx.x * dim + j] = sum;
+            }
         }
     }
 }
@@ -652,7 +673,7 @@ hipError_t ln_bwd(int64_t rows, int64_t dim, float eps, const void* x, const voi
     const bool need = dw || db;
     float* pw = need ? ws : nullptr;
     float* pb = need ? ws + (size_t)nb * dim : nullptr;
-    const size_t lds = 2 * (size_t)kRowsPerBlock * dim * sizeof(float);
+    const size_t lds = (size_t)kRowsPerBlock * dim * sizeof(float);
     if (ln_vec_ok<T>(dim) && (!need || lds <= 64 * 1024)) {
         const int vpl = ln_vpl<T>(dim);
         if (need) ln_bwd_vec_launch<T, true>(vpl, grid, lds, st, rows, (int)dim, eps, chunk, xp, wp, mean, rstd, gp, dxp, pw, pb);

@@ -50,7 +50,7 @@ def test_layernorm_reference_tests(mc, dev):
 @pytest.mark.parametrize("rows,D,dtype,affine", [
     (64, 384, torch.float32, True), (33, 768, torch.bfloat16, True), (17, 1024, torch.float32, False),
     (16384, 1536, torch.bfloat16, True), (9, 5000, torch.float32, True), (5, 13, torch.bfloat16, True),
-    (8, 4096, torch.bfloat16, False),
+    (8, 4096, torch.bfloat16, False), (1024, 3584, torch.bfloat16, True), (300, 2048, torch.float32, True),
 ])
 def test_layernorm_fwd_bwd(mc, dev, rows, D, dtype, affine):
     x = (rnd((rows, D), rows + D, 2.0) + 0.3).to(dtype)
