@@ -106,11 +106,11 @@ def proj_shapes(c):
 class Layer:
     """Device-resident tensors of one layer's custom ops."""
 
-    def __init__(self, mc, c, dev, seed=0, group=True):
+    def __init__(self, mc, c, dev, seed=0, group=True, cached_wt=True):
         import torch
 
         self.mc, self.c, self.dev = mc, c, dev
-        self.group = group
+        self.group = group and c["dtype"] == "bf16"
         self.T = c["batch"] * c["seq"]
         dt = torch.bfloat16 if c["dtype"] == "bf16" else torch.float32
         g = torch.Generator(device=dev).manual_seed(seed)
@@ -130,6 +130,11 @@ class Layer:
                 dy=rn(T, N, std=1e-2).to(dt),
                 mask=(mc.dropout_mask(1234 + len(self.proj), self.p, T, c["rank"]).to(dev) if self.p > 0 else None),
             )
+        if self.group and cached_wt:
+            # W is frozen: its transpose for the backward's dX product is a
+            # load-time layout, built once here (mc_transpose_bf16), not per step
+            for pr in self.proj.values():
+                pr["Wt"] = mc.transpose_weight(pr["W"])
         self.h_in = rn(T, H).to(dt)
         self.h_mid = rn(T, H).to(dt)
         self.attn = rn(T, c["heads"] * c["head_dim"]).to(dt)
@@ -157,8 +162,10 @@ class Layer:
         """One forward + backward of the layer's custom ops. The projections
         that read the same input (q / k / v, gate / up) run as one grouped
         call each (mc_lora_group_fwd / _bwd: one pass over the input per
-        rank-r pass, one GEMM launch, dX summed over the group) unless the
-        layer was built with group=False."""
+        rank-r pass, one GEMM launch, dX summed over the group), o and down as
+        groups of one, each with its load-time W^T, unless the layer was built
+        with group=False (per-projection mc_lora_fwd / _bwd, which transpose W
+        in every backward)."""
         mc, c = self.mc, self.c
         saved = {}
         if c["norm"]:
@@ -187,7 +194,7 @@ class Layer:
     def _fwd(self, names, saved):
         if not names:
             return
-        if len(names) == 1 or not self.group:
+        if not self.group:
             for name in names:
                 saved[name] = self._lora_f(name)
             return
@@ -199,7 +206,7 @@ class Layer:
     def _bwd(self, names, saved):
         if not names:
             return
-        if len(names) == 1 or not self.group:
+        if not self.group:
             for name in names:
                 self._lora_b(name, saved[name])
             return
@@ -488,6 +495,8 @@ def main():
     ap.add_argument("--graph", action="store_true", help="time HIP graph replays of one captured step")
     ap.add_argument("--no-group", action="store_true",
                     help="run q/k/v and gate/up as separate per-projection calls instead of grouped calls")
+    ap.add_argument("--no-cached-wt", action="store_true",
+                    help="grouped calls without the load-time W^T: every backward transposes W into its workspace")
     ap.add_argument("--attention-iters", type=int, default=5,
                     help="calls of the attention core fwd / bwd timed after the step (0: skip)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
@@ -506,7 +515,7 @@ def main():
     mc = __graft_entry__.load_package()
     dev = torch.device("cuda:0")
     c = CONFIGS[args.config]
-    layer = Layer(mc, c, dev, group=not args.no_group)
+    layer = Layer(mc, c, dev, group=not args.no_group, cached_wt=not args.no_cached_wt)
     if args.copy_calibration > 0:
         src = torch.empty(args.copy_calibration // 2, dtype=torch.bfloat16, device=dev).fill_(1.0)
         dst = torch.empty_like(src)
@@ -597,6 +606,8 @@ def main():
         "layer_TFLOP_s": (base_fl + low_fl) / (ms_step * 1e-3) / 1e12,
         "launch": "hip_graph" if args.graph else "eager",
         "projections": "per-projection calls" if args.no_group else "grouped calls for q/k/v and gate/up",
+        "weights": ("W^T transposed in every backward" if args.no_group or args.no_cached_wt
+                    else "frozen W with its W^T built once at load (mc_transpose_bf16)"),
         "kernels": kernels,
     }
     if args.attention_iters > 0 and c["softmax"]:

@@ -134,6 +134,9 @@ typedef struct mc_lora_proj {
     const float* A;         /* [K, r] */
     const float* B;         /* [r, N_g] */
     const uint8_t* mask;    /* [T, r] keep-mask, required iff dropout_p > 0 */
+    const void* Wt;         /* [K, N_g] = W^T of the frozen W (mc_transpose_bf16, built once), or
+                             * NULL: the backward then transposes W into its workspace on every call.
+                             * Requires W; read by the backward's dX product only. */
 } mc_lora_proj;
 
 size_t mc_lora_group_fwd_workspace_size(const mc_lora_desc* d, const mc_lora_proj* projs, int32_t count);
@@ -159,6 +162,12 @@ mc_status mc_lora_group_fwd(const mc_lora_desc* d, const void* x, const mc_lora_
 mc_status mc_lora_group_bwd(const mc_lora_desc* d, const void* x, const mc_lora_proj* projs, int32_t count,
                             const float* const* h_save, const void* const* dY, void* dX, float* const* dA,
                             float* const* dB, void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* out[j][i] = in[i][j] for a bf16 matrix in [rows, cols] (out [cols, rows]),
+ * both 16-byte aligned with rows and cols multiples of 8. No reference
+ * counterpart: it builds the mc_lora_proj.Wt of a frozen base weight once
+ * (at load), so that the backward does not transpose W on every call. */
+mc_status mc_transpose_bf16(int64_t rows, int64_t cols, const void* in, void* out, hipStream_t stream);
 
 /* RMSNorm over the last dim of x [rows, dim]:
  *   y = x / sqrt(mean(x^2) + eps) * w     (w == NULL: no weight, as FusedRMSNormOp)

@@ -27,4 +27,5 @@ from .ops import (  # noqa: F401
     rms_norm_forward,
     softmax_backward,
     softmax_forward,
+    transpose_weight,
 )

@@ -58,6 +58,7 @@ class LoraProj(ctypes.Structure):
         ("A", ctypes.c_void_p),
         ("B", ctypes.c_void_p),
         ("mask", ctypes.c_void_p),
+        ("Wt", ctypes.c_void_p),
     ]
 
 
@@ -131,6 +132,7 @@ _SIGNATURES = {
     "mc_lora_group_bwd": (ctypes.c_int, [_dp, _vp, ctypes.POINTER(LoraProj), _i32, ctypes.POINTER(_vp),
                                          ctypes.POINTER(_vp), _vp, ctypes.POINTER(_vp), ctypes.POINTER(_vp), _vp,
                                          _sz, _vp]),
+    "mc_transpose_bf16": (ctypes.c_int, [_i64, _i64, _vp, _vp, _vp]),
     "mc_rmsnorm_fwd": (ctypes.c_int, [_i64, _i64, _f32, _i32, _vp, _vp, _vp, _vp, _vp]),
     "mc_rmsnorm_bwd_workspace_size": (_sz, [_i64, _i64]),
     "mc_rmsnorm_bwd": (ctypes.c_int, [_i64, _i64, _f32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),

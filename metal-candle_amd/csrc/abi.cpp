@@ -237,6 +237,9 @@ mc_status check_lora_group(const mc_lora_desc* d, const mc_lora_proj* projs, int
                  "%s: projection %d: dropout_p > 0 requires a mask", op, (int)g);
         MC_CHECK(!projs[g].W || aligned16(projs[g].W), MC_ERR_LAYOUT, "%s: projection %d: W must be 16-byte aligned",
                  op, (int)g);
+        MC_CHECK(!projs[g].Wt || projs[g].W, MC_ERR_NULL, "%s: projection %d: Wt given without W", op, (int)g);
+        MC_CHECK(!projs[g].Wt || aligned16(projs[g].Wt), MC_ERR_LAYOUT,
+                 "%s: projection %d: Wt must be 16-byte aligned", op, (int)g);
         Ns[g] = projs[g].out_features;
     }
     *per_proj = *d;
@@ -246,7 +249,13 @@ mc_status check_lora_group(const mc_lora_desc* d, const mc_lora_proj* projs, int
 
 void to_lora_proj(const mc_lora_proj* projs, int32_t count, mc::LoraProj* out) {
     for (int32_t g = 0; g < count; ++g)
-        out[g] = mc::LoraProj{projs[g].out_features, projs[g].W, projs[g].bias, projs[g].A, projs[g].B, projs[g].mask};
+        out[g] = mc::LoraProj{projs[g].out_features, projs[g].W, projs[g].bias, projs[g].A, projs[g].B, projs[g].mask,
+                              projs[g].Wt};
+}
+
+// Projections whose W^T the backward builds in its workspace.
+void need_wt_of(const mc_lora_proj* projs, int32_t count, bool* need) {
+    for (int32_t g = 0; g < count; ++g) need[g] = projs[g].W && !projs[g].Wt;
 }
 
 }  // namespace
@@ -264,7 +273,9 @@ size_t mc_lora_group_bwd_workspace_size(const mc_lora_desc* d, const mc_lora_pro
     mc_lora_desc dd;
     int64_t Ns[MC_LORA_MAX_GROUP];
     if (check_lora_group(d, projs, count, "LoRA group backward", &dd, Ns) != MC_OK) return 0;
-    return mc::lora_group_bwd_ws(dd, Ns, count).total;
+    bool need_wt[MC_LORA_MAX_GROUP];
+    need_wt_of(projs, count, need_wt);
+    return mc::lora_group_bwd_ws(dd, Ns, count, need_wt).total;
 }
 
 mc_status mc_lora_group_fwd(const mc_lora_desc* d, const void* x, const mc_lora_proj* projs, int32_t count,
@@ -312,7 +323,9 @@ mc_status mc_lora_group_bwd(const mc_lora_desc* d, const void* x, const mc_lora_
     }
     MC_CHECK((!x || aligned16(x)) && (!dX || aligned16(dX)), MC_ERR_LAYOUT,
              "LoRA group backward: x and dX must be 16-byte aligned");
-    const size_t need = mc::lora_group_bwd_ws(dd, Ns, count).total;
+    bool need_wt[MC_LORA_MAX_GROUP];
+    need_wt_of(projs, count, need_wt);
+    const size_t need = mc::lora_group_bwd_ws(dd, Ns, count, need_wt).total;
     MC_CHECK(workspace_bytes >= need && workspace, MC_ERR_WORKSPACE,
              "LoRA group backward: workspace of %zu bytes required, %zu given", need, workspace_bytes);
     MC_CHECK(aligned16(workspace), MC_ERR_LAYOUT, "LoRA group backward: workspace must be 16-byte aligned");
@@ -321,6 +334,18 @@ mc_status mc_lora_group_bwd(const mc_lora_desc* d, const void* x, const mc_lora_
     to_lora_proj(projs, count, lp);
     return hip_status(mc::launch_lora_group_bwd(dd, x, lp, count, h_save, dY, dX, dA, dB, workspace, stream),
                       "LoRA group backward");
+}
+
+mc_status mc_transpose_bf16(int64_t rows, int64_t cols, const void* in, void* out, hipStream_t stream) {
+    MC_CHECK(rows >= 1 && cols >= 1 && rows <= ((int64_t)1 << 40) / cols, MC_ERR_SHAPE,
+             "transpose: rows and cols must be >= 1 with rows * cols <= 2^40 (got %lld x %lld)", (long long)rows,
+             (long long)cols);
+    MC_CHECK(rows % 8 == 0 && cols % 8 == 0, MC_ERR_SHAPE, "transpose: rows and cols must be multiples of 8 (got %lld x %lld)",
+             (long long)rows, (long long)cols);
+    MC_CHECK(in && out, MC_ERR_NULL, "transpose: in and out must not be NULL");
+    MC_CHECK(aligned16(in) && aligned16(out), MC_ERR_LAYOUT, "transpose: in and out must be 16-byte aligned");
+    MC_CHECK((rows + 63) / 64 * ((cols + 63) / 64) <= 0x7fffffff, MC_ERR_SHAPE, "transpose: too many 64 x 64 tiles");
+    return hip_status(mc::launch_transpose_bf16(in, rows, cols, out, stream), "transpose");
 }
 
 mc_status mc_rmsnorm_fwd(int64_t rows, int64_t dim, float eps, int32_t dtype, const void* x, const void* w,

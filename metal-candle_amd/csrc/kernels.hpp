@@ -63,6 +63,7 @@ struct LoraProj {
     const float* A;
     const float* B;
     const uint8_t* mask;
+    const void* Wt = nullptr;  // W^T [K][N] built by the caller, or null (transposed into the workspace)
 };
 struct LoraGroupFwdWs {
     size_t at_hilo[kLoraMaxProj];  // per row-projection pass: bf16 [2][16 rc][K]
@@ -71,7 +72,7 @@ struct LoraGroupFwdWs {
     size_t total;
 };
 struct LoraGroupBwdWs {
-    size_t wt[kLoraMaxProj];       // per projection: bf16 [K][N_g] W_g^T
+    size_t wt[kLoraMaxProj];       // per projection with W and no caller W^T: bf16 [K][N_g] W_g^T
     size_t at_ext;                 // bf16 [K][G rext]: A of every projection
     size_t gd_ext;                 // bf16 [T][G rext]: Gd of every projection
     size_t gd_t;                   // f32 [G r][T]: Gd^T of every projection
@@ -80,7 +81,8 @@ struct LoraGroupBwdWs {
     size_t total;
 };
 LoraGroupFwdWs lora_group_fwd_ws(const mc_lora_desc& d, const int64_t* N, int count);
-LoraGroupBwdWs lora_group_bwd_ws(const mc_lora_desc& d, const int64_t* N, int count);
+// need_wt[g]: projection g's W^T is transposed into the workspace (null: all)
+LoraGroupBwdWs lora_group_bwd_ws(const mc_lora_desc& d, const int64_t* N, int count, const bool* need_wt = nullptr);
 hipError_t launch_lora_group_fwd(const mc_lora_desc& d, const void* x, const LoraProj* proj, int count,
                                  void* const* y, float* const* h_save, void* ws, hipStream_t stream);
 // dX (may be null) receives the sum over the projections; dA / dB (arrays,
@@ -89,6 +91,9 @@ hipError_t launch_lora_group_fwd(const mc_lora_desc& d, const void* x, const Lor
 hipError_t launch_lora_group_bwd(const mc_lora_desc& d, const void* x, const LoraProj* proj, int count,
                                  const float* const* h_save, const void* const* dY, void* dX, float* const* dA,
                                  float* const* dB, void* ws, hipStream_t stream);
+
+// out [cols][rows] = in [rows][cols]^T, bf16
+hipError_t launch_transpose_bf16(const void* in, int64_t rows, int64_t cols, void* out, hipStream_t stream);
 
 hipError_t launch_lora_fwd(const mc_lora_desc& d, const void* x, const void* W, const void* bias,
                            const float* A, const float* B, const uint8_t* mask, void* y,

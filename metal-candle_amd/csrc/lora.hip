@@ -157,13 +157,13 @@ LoraGroupFwdWs lora_group_fwd_ws(const mc_lora_desc& d, const int64_t* N, int co
     return w;
 }
 
-LoraGroupBwdWs lora_group_bwd_ws(const mc_lora_desc& d, const int64_t* N, int count) {
+LoraGroupBwdWs lora_group_bwd_ws(const mc_lora_desc& d, const int64_t* N, int count, const bool* need_wt) {
     const Dims m = dims_of(d);
     LoraGroupBwdWs w{};
     size_t off = 0;
     for (int g = 0; g < count; ++g) {
         w.wt[g] = off;
-        off += align256((size_t)m.K * N[g] * 2);
+        if (!need_wt || need_wt[g]) off += align256((size_t)m.K * N[g] * 2);
     }
     w.at_ext = off; off += align256((size_t)m.K * count * m.rext * 2);
     w.gd_ext = off; off += align256((size_t)m.T * count * m.rext * 2);
@@ -337,8 +337,12 @@ hipError_t launch_lora_group_bwd(const mc_lora_desc& d, const void* x, const Lor
     // one fixed-order split-sum launch.
     const Dims m = dims_of(d);
     int64_t Ns[kMaxProj];
-    for (int g = 0; g < count; ++g) Ns[g] = proj[g].N;
-    const LoraGroupBwdWs w = lora_group_bwd_ws(d, Ns, count);
+    bool need_wt[kMaxProj];
+    for (int g = 0; g < count; ++g) {
+        Ns[g] = proj[g].N;
+        need_wt[g] = proj[g].W && !proj[g].Wt;
+    }
+    const LoraGroupBwdWs w = lora_group_bwd_ws(d, Ns, count, need_wt);
     char* base = static_cast<char*>(ws);
     const float keep = proj[0].mask ? 1.0f / (1.0f - d.dropout_p) : 1.0f;
     bool any_dA = false, any_dB = false;
@@ -356,7 +360,7 @@ hipError_t launch_lora_group_bwd(const mc_lora_desc& d, const void* x, const Lor
         OperandsCall calls[kMaxProj];
         double bytes = 0, flops = 0;
         for (int g = 0; g < count; ++g) {
-            const bool tw = dX && proj[g].W;
+            const bool tw = dX && need_wt[g];  // W^T into the workspace (none when the caller holds it)
             calls[g] = OperandsCall{static_cast<const uint16_t*>(dY[g]), Ns[g], proj[g].B, proj[g].mask,
                                     any_dA ? gdt + (size_t)g * m.r * m.T : nullptr,
                                     dX ? gd + (size_t)g * m.rext : nullptr,
@@ -379,8 +383,9 @@ hipError_t launch_lora_group_bwd(const mc_lora_desc& d, const void* x, const Lor
         int64_t kbase = 0;
         for (int g = 0; g < count; ++g)
             if (proj[g].W) {
-                segs[nseg++] = GemmSeg{static_cast<const uint16_t*>(dY[g]), Ns[g],
-                                       reinterpret_cast<const uint16_t*>(base + w.wt[g]), Ns[g], Ns[g]};
+                const uint16_t* wt = proj[g].Wt ? static_cast<const uint16_t*>(proj[g].Wt)
+                                                : reinterpret_cast<const uint16_t*>(base + w.wt[g]);
+                segs[nseg++] = GemmSeg{static_cast<const uint16_t*>(dY[g]), Ns[g], wt, Ns[g], Ns[g]};
                 kbase += Ns[g];
             }
         segs[nseg++] = GemmSeg{gd, ext_ld, at, ext_ld, ext_ld};

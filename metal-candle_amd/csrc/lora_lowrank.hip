@@ -479,6 +479,12 @@ __device__ __forceinline__ void transpose_tile(const uint16_t* __restrict__ in, 
     }
 }
 
+// A whole matrix: workgroup b transposes tile (b / tiles_c, b % tiles_c).
+__global__ __launch_bounds__(256) void transpose_bf16_k(const uint16_t* __restrict__ in, int64_t rows, int64_t cols,
+                                                        uint16_t* __restrict__ out, int64_t tiles_c) {
+    transpose_tile(in, rows, cols, out, (int64_t)blockIdx.x / tiles_c, (int64_t)blockIdx.x % tiles_c);
+}
+
 // ------------------------------------------- backward operands, one launch
 // The inputs of the backward GEMM and the rank-r pass of each dY, as block
 // roles of one launch (none reads another's output), for every projection
@@ -625,6 +631,14 @@ hipError_t launch_rowproj_bf16(const uint16_t* X, int64_t T, int64_t C, const ui
     c.mask[0] = mask; c.keep = keep; c.out_t[0] = out_t; c.out_ext = out_ext; c.rext_p = rext; c.ext_ld = rext;
     c.ext_scale = ext_scale;
     return launch_rowproj_bf16(c, stream);
+}
+
+hipError_t launch_transpose_bf16(const void* in, int64_t rows, int64_t cols, void* out, hipStream_t stream) {
+    const int64_t tiles_c = (cols + 63) / 64, tiles = tiles_c * ((rows + 63) / 64);
+    if (tiles == 0) return hipSuccess;
+    transpose_bf16_k<<<dim3((unsigned)tiles), 256, 0, stream>>>(static_cast<const uint16_t*>(in), rows, cols,
+                                                                static_cast<uint16_t*>(out), tiles_c);
+    return hipGetLastError();
 }
 
 hipError_t launch_lora_bwd_operands(const OperandsCall* calls, int n, int64_t T, int64_t K, int r, float scale,

@@ -189,7 +189,9 @@ def _group_table(x, projs, dropout_p):
         _expect(p.get("W"), "W", shape=(N, K), dtype=x.dtype, device=x.device)
         _expect(p.get("bias"), "bias", shape=(N,), dtype=x.dtype, device=x.device)
         _expect(p.get("mask"), "mask", shape=(T, r), dtype=torch.uint8, device=x.device)
-        table[g] = LoraProj(N, *[None if p.get(k) is None else p[k].data_ptr() for k in ("W", "bias", "A", "B", "mask")])
+        _expect(p.get("Wt"), "Wt", shape=(K, N), dtype=x.dtype, device=x.device)
+        table[g] = LoraProj(N, *[None if p.get(k) is None else p[k].data_ptr()
+                                 for k in ("W", "bias", "A", "B", "mask", "Wt")])
         Ns.append(N)
     return table, K, r0, T, Ns
 
@@ -197,8 +199,9 @@ def _group_table(x, projs, dropout_p):
 def lora_group_forward(x, projs, scale, dropout_p=0.0, save_hidden=True):
     """The LoRA projections of one input x [..., K] in one call
     (mc_lora_group_fwd): projs is a list of 1-4 dicts with W [N_g, K], bias
-    [N_g] (or None), A [K, r], B [r, N_g] and mask [T, r] (or None). Returns
-    ([y_g], [h_save_g]); each y_g equals lora_forward's for that projection."""
+    [N_g] (or None), A [K, r], B [r, N_g], mask [T, r] (or None) and,
+    optionally, Wt = transpose_weight(W) for the backward. Returns ([y_g],
+    [h_save_g]); each y_g equals lora_forward's for that projection."""
     table, K, r, T, Ns = _group_table(x, projs, dropout_p)
     d = LoraDesc(T, K, Ns[0], r, float(scale), float(dropout_p), _lib.MC_BF16)
     ys = [torch.empty(*x.shape[:-1], N, dtype=x.dtype, device=x.device) for N in Ns]
@@ -234,6 +237,20 @@ def lora_group_backward(x, projs, dYs, scale, dropout_p=0.0, h_saves=None, need_
     check(lib().mc_lora_group_bwd(ctypes.byref(d), _ptr(x), table, n, hp, _ptr_array(dYs), _ptr(dX), _ptr_array(dAs),
                                   _ptr_array(dBs), _ptr(ws), ws_n, _stream(x)))
     return dX, dAs, dBs
+
+
+def transpose_weight(W):
+    """W^T [K, N] of a frozen bf16 base weight W [N, K] (mc_transpose_bf16):
+    built once and passed as a projection's Wt, the grouped backward reads it
+    instead of transposing W on every call."""
+    _contig(W, "W")
+    if W.dim() != 2:
+        raise McError(_lib.MC_ERR_SHAPE, "W must be 2-D")
+    if W.dtype != torch.bfloat16:
+        raise McError(_lib.MC_ERR_DTYPE, "transpose_weight takes a bfloat16 W")
+    Wt = torch.empty(W.shape[1], W.shape[0], dtype=W.dtype, device=W.device)
+    check(lib().mc_transpose_bf16(W.shape[0], W.shape[1], _ptr(W), _ptr(Wt), _stream(W)))
+    return Wt
 
 
 def rms_norm_forward(x, eps, w=None, save_rstd=True):

@@ -221,3 +221,24 @@ def test_lora_group_validation(mc):
     assert "requires h_save" in mc._lib.last_error()
     # nothing requested: no work, OK
     assert L.mc_lora_group_bwd(ctypes.byref(d), w, projs, 2, None, dys, None, None, None, w, need_b, None) == 0
+    # a caller's W^T: needs W and 16-byte alignment; the backward's workspace
+    # then holds no transposed copy of that W (16 x 16 bf16, 256-byte aligned)
+    projs[0].Wt = fake
+    assert L.mc_lora_group_bwd_workspace_size(ctypes.byref(d), projs, 2) == need_b - 512
+    projs[0].Wt = 264
+    assert L.mc_lora_group_bwd(ctypes.byref(d), w, projs, 2, None, dys, None, None, None, w, need_b, None) == 4
+    assert "Wt must be 16-byte aligned" in mc._lib.last_error()
+    projs[0].W, projs[0].Wt = None, fake
+    assert L.mc_lora_group_bwd(ctypes.byref(d), w, projs, 2, None, dys, None, None, None, w, need_b, None) == 1
+    assert "Wt given without W" in mc._lib.last_error()
+
+
+def test_transpose_validation(mc):
+    """mc_transpose_bf16: sizes multiples of 8, pointers present and aligned."""
+    L = mc._lib.lib()
+    fake = 256
+    assert L.mc_transpose_bf16(0, 8, fake, fake, None) == 2
+    assert L.mc_transpose_bf16(12, 8, fake, fake, None) == 2
+    assert "multiples of 8" in mc._lib.last_error()
+    assert L.mc_transpose_bf16(8, 8, None, fake, None) == 1
+    assert L.mc_transpose_bf16(8, 8, fake, 264, None) == 4

@@ -117,3 +117,30 @@ def test_group_partial_outputs(mc, dev):
     assert only_ab[0] is None
     for g in range(2):
         assert torch.equal(only_ab[1][g], full[1][g]) and torch.equal(only_ab[2][g], full[2][g])
+
+
+def test_group_with_caller_wt(mc, dev):
+    """Projections carrying a caller-built W^T (transpose_weight, built once
+    for a frozen W): the backward reads it in place of its own transposed
+    copy, so dX, dA and dB equal the call without Wt bit for bit; W^T itself
+    equals torch's transpose."""
+    x, projs, dys = _group_case(dev, 4096, 1536, [1536, 256, 256], 16, 0.0, 11)
+    for pr in projs:
+        pr["Wt"] = mc.transpose_weight(pr["W"])
+        assert torch.equal(pr["Wt"], pr["W"].t().contiguous())
+    ys, hs = mc.lora_group_forward(x, projs, 2.0)
+    with_wt = mc.lora_group_backward(x, projs, dys, 2.0, h_saves=hs)
+    plain = [dict(pr, Wt=None) for pr in projs]
+    without = mc.lora_group_backward(x, plain, dys, 2.0, h_saves=hs)
+    torch.cuda.synchronize()
+    assert torch.equal(with_wt[0], without[0])
+    for g in range(3):
+        assert torch.equal(with_wt[1][g], without[1][g]) and torch.equal(with_wt[2][g], without[2][g])
+
+
+@pytest.mark.parametrize("rows,cols", [(8, 8), (200, 72), (8960, 1536), (1536, 8960)])
+def test_transpose_weight(mc, dev, rows, cols):
+    W = torch.randn(rows, cols, device=dev).to(torch.bfloat16)
+    Wt = mc.transpose_weight(W)
+    torch.cuda.synchronize()
+    assert Wt.shape == (cols, rows) and torch.equal(Wt, W.t().contiguous())
