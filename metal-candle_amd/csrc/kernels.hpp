@@ -78,6 +78,7 @@ struct LoraGroupBwdWs {
     size_t gd_t;                   // f32 [G r][T]: Gd^T of every projection
     size_t part_a;                 // f32 [S_a][colreduce rows of G r][K]
     size_t part_b[kLoraMaxProj];   // f32 [S_b][colreduce rows of r][N_g]
+    size_t gpart[kLoraMaxProj];    // r <= 32: f32 [column groups of N_g][T][r], G partials of the fused dY pass
     size_t total;
 };
 LoraGroupFwdWs lora_group_fwd_ws(const mc_lora_desc& d, const int64_t* N, int count);

@@ -100,6 +100,19 @@ hipError_t prep_all(const PrepJob* jobs, int n, hipStream_t st) {
     return hipSuccess;
 }
 
+// The backward reads each dY_g once for both rank-r products (launch_dy_pass)
+// when that pass has the parallelism to stream at full rate: ranks <= 32 and
+// every dY_g of at least 2^26 elements (e.g. the c4 gate / up [16384, 8960]:
+// >= 512 workgroups of 512 columns x >= 256 rows). Smaller products run the
+// row projection and the column reduction as two passes, which measured
+// faster there (c3, and c4's N = 1536 projections).
+bool dy_fused(const Dims& m, const int64_t* N, int count) {
+    if (m.r > kDyMaxRank) return false;
+    for (int g = 0; g < count; ++g)
+        if (N[g] * m.T < ((int64_t)1 << 26)) return false;
+    return true;
+}
+
 }  // namespace
 
 LoraFwdWs lora_fwd_ws(const mc_lora_desc& d) {
@@ -169,9 +182,15 @@ LoraGroupBwdWs lora_group_bwd_ws(const mc_lora_desc& d, const int64_t* N, int co
     w.gd_ext = off; off += align256((size_t)m.T * count * m.rext * 2);
     w.gd_t = off;   off += align256((size_t)count * m.r * m.T * 4);
     w.part_a = off; off += align256((size_t)colreduce_splits(m.T, m.K) * colreduce_rows(count * m.r) * m.K * 4);
+    const bool fused = dy_fused(m, N, count);
     for (int g = 0; g < count; ++g) {
         w.part_b[g] = off;
-        off += align256((size_t)colreduce_splits(m.T, N[g]) * colreduce_rows(m.r) * N[g] * 4);
+        off += align256((size_t)(fused ? dy_splits(m.T, N[g]) : colreduce_splits(m.T, N[g])) * colreduce_rows(m.r) *
+                        N[g] * 4);
+    }
+    for (int g = 0; g < count; ++g) {
+        w.gpart[g] = off;
+        if (fused) off += align256((size_t)dy_groups(N[g]) * m.T * m.r * 4);
     }
     w.total = off;
     return w;
@@ -356,6 +375,81 @@ hipError_t launch_lora_group_bwd(const mc_lora_desc& d, const void* x, const Lor
     uint16_t* at = reinterpret_cast<uint16_t*>(base + w.at_ext);
     uint16_t* gd = reinterpret_cast<uint16_t*>(base + w.gd_ext);
     float* gdt = reinterpret_cast<float*>(base + w.gd_t);
+    if (dy_fused(m, Ns, count)) {
+        // One read of each dY_g for both of its rank-r products (G_g and the
+        // dB_g partials), the G partials finished into Gd (with the A
+        // extension operands), then the dX GEMM, dA from one pass over x,
+        // and the fixed-order split sums.
+        if (need_g || any_dB) {
+            DyJob jobs[kMaxProj];
+            DyFinishJob fin[kMaxProj];
+            PrepJob preps[kMaxProj];
+            double bytes = 0, flops = 0;
+            for (int g = 0; g < count; ++g) {
+                const bool wb = dB && dB[g];
+                jobs[g] = DyJob{static_cast<const uint16_t*>(dY[g]), Ns[g], proj[g].B, wb ? h_save[g] : nullptr,
+                                wb ? reinterpret_cast<float*>(base + w.part_b[g]) : nullptr,
+                                need_g ? reinterpret_cast<float*>(base + w.gpart[g]) : nullptr};
+                fin[g] = DyFinishJob{reinterpret_cast<const float*>(base + w.gpart[g]), dy_groups(Ns[g]), proj[g].mask,
+                                     any_dA ? gdt + (size_t)g * m.r * m.T : nullptr,
+                                     dX ? gd + (size_t)g * m.rext : nullptr};
+                preps[g] = dX ? prep_job(proj[g].A, m.r, m.K, m.r, false, at + (size_t)g * m.rext, nullptr, m.K, m.rext,
+                                         ext_ld)
+                              : PrepJob{};
+                // algorithmic: dY_g read once, B_g read, Hd_g read (for dB),
+                // Gd_g written (fp32 and bf16), A_g read
+                bytes += 2.0 * m.T * Ns[g] + 4.0 * m.r * Ns[g] + (wb ? 4.0 * m.T * m.r : 0.0) +
+                         (need_g ? 6.0 * m.T * m.r : 0.0) + (dX ? 6.0 * m.r * m.K : 0.0);
+                flops += 2.0 * m.T * Ns[g] * m.r * ((need_g ? 1 : 0) + (wb ? 1 : 0));
+            }
+            auto sc = prof::Scope(prof::kLowRank, st, flops, bytes);
+            MC_TRY(launch_dy_pass(m.T, m.r, jobs, count, st));
+            if (need_g)
+                MC_TRY(launch_dy_finish(m.T, m.r, d.scale, keep, m.rext, ext_ld, fin, count, preps, count, st));
+        }
+        if (dX) {
+            for (int g = 0; g < count; ++g)
+                if (need_wt[g])  // W^T into the workspace (none when the caller holds it)
+                    MC_TRY(launch_transpose_bf16(proj[g].W, Ns[g], m.K, base + w.wt[g], st));
+            GemmSeg segs[kGemmMaxSeg];
+            int nseg = 0;
+            int64_t kbase = 0;
+            for (int g = 0; g < count; ++g)
+                if (proj[g].W) {
+                    const uint16_t* wt = proj[g].Wt ? static_cast<const uint16_t*>(proj[g].Wt)
+                                                    : reinterpret_cast<const uint16_t*>(base + w.wt[g]);
+                    segs[nseg++] = GemmSeg{static_cast<const uint16_t*>(dY[g]), Ns[g], wt, Ns[g], Ns[g]};
+                    kbase += Ns[g];
+                }
+            segs[nseg++] = GemmSeg{gd, ext_ld, at, ext_ld, ext_ld};
+            auto sc = gemm_scope(st, m.T, m.K, kbase, ext_ld, rtot, 2);
+            MC_TRY(launch_gemm_bf16(m.T, m.K, segs, nseg, nullptr, static_cast<uint16_t*>(dX), m.K, st));
+        }
+        if (any_dA || any_dB) {
+            // dA_g = x^T.Gd_g for every g from one pass over x (all ranks),
+            // then the fixed-order split sums of dA and dB
+            SumJob sj[2 * kMaxProj];
+            int ns = 0;
+            const int sa = colreduce_splits(m.T, m.K);
+            float* pa = reinterpret_cast<float*>(base + w.part_a);
+            auto sc = prof::Scope(prof::kLowRank, st, any_dA ? 2.0 * m.T * m.K * rtot : 0.0,
+                                  any_dA ? 2.0 * m.T * m.K + 4.0 * m.T * rtot : 0.0);
+            if (any_dA) {
+                const ColJob cj{static_cast<const uint16_t*>(x), m.K, gdt, rtot, sa, pa};
+                MC_TRY(launch_colreduce_bf16(m.T, &cj, 1, st));
+                for (int g = 0; g < count; ++g)
+                    if (dA[g])
+                        sj[ns++] = SumJob{pa + (size_t)g * m.r * m.K, sa, m.K, (int64_t)colreduce_rows(rtot) * m.K, m.r,
+                                          1.0f, true, dA[g]};
+            }
+            for (int g = 0; g < count; ++g)
+                if (dB && dB[g])
+                    sj[ns++] = SumJob{reinterpret_cast<float*>(base + w.part_b[g]), dy_splits(m.T, Ns[g]), Ns[g],
+                                      (int64_t)colreduce_rows(m.r) * Ns[g], m.r, d.scale, false, dB[g]};
+            MC_TRY(launch_split_sum(sj, ns, st));
+        }
+        return hipSuccess;
+    }
     if (need_g) {
         OperandsCall calls[kMaxProj];
         double bytes = 0, flops = 0;

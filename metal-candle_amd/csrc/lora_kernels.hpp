@@ -115,6 +115,45 @@ hipError_t launch_colreduce_bf16(int64_t T, const ColJob* jobs, int n, hipStream
 // c < C, written to out[c*r + j] when transpose_out (dA [K][r]) else
 // out[j*C + c] (dB [r][N]); part_stride = colreduce_rows * C. A job with
 // out == nullptr is skipped; up to kSumJobs jobs run in one launch.
+// ------------------------------------------------ fused dY pass (r <= 32)
+// One read of a projection's dY [T][N] gives both rank-r products of the
+// backward that reduce it:
+//   dB partials  partB[s][j][c] = sum_{t in split s} Pt[j][t] dY[t][c]
+//                (the layout of ColJob's partials: colreduce_rows(r) rows
+//                per split, summed by split_sum)
+//   G partials   gpart[g][t][j] = sum_{c in column group g} dY[t][c] B[j][c]
+//                (groups of kDyCols columns, summed in group order by
+//                launch_dy_finish)
+// Pt fp32 [r][T] (the forward's Hd^T), B fp32 [r][N]; partB or gpart may be
+// null (that product is skipped; Pt is then not read).
+constexpr int kDyCols = 512;
+constexpr int kDyMaxRank = 32;
+inline int dy_groups(int64_t N) { return (int)((N + kDyCols - 1) / kDyCols); }
+int dy_splits(int64_t T, int64_t N);  // the split count of launch_dy_pass for this shape
+struct DyJob {
+    const uint16_t* dY;
+    int64_t N;
+    const float* B;
+    const float* Pt;
+    float* partB;
+    float* gpart;
+};
+hipError_t launch_dy_pass(int64_t T, int r, const DyJob* jobs, int n, hipStream_t stream);
+// G = scale * sum_g gpart[g][t][j] per projection, then the dropout of the
+// rank-r hidden (mask [T][r] or null; keep = 1/(1-p)): Gd^T -> gd_t fp32
+// [r][T] (may be null) and Gd -> gd_ext bf16 columns 0..r-1 of rows of
+// ext_ld elements, columns r..rext-1 zeroed (may be null); the PrepJobs
+// (the A extension operands) run in the same launch.
+struct DyFinishJob {
+    const float* gpart;
+    int groups;
+    const uint8_t* mask;
+    float* gd_t;
+    uint16_t* gd_ext;
+};
+hipError_t launch_dy_finish(int64_t T, int r, float scale, float keep, int rext, int ext_ld,
+                            const DyFinishJob* jobs, int n, const PrepJob* preps, int npreps, hipStream_t stream);
+
 struct SumJob {
     const float* partial;
     int splits;

@@ -449,6 +449,282 @@ __global__ __launch_bounds__(256) void split_sum(SumBatch sb) {
     }
 }
 
+// --------------------------------------------------------- fused dY pass
+// Workgroup: 4 waves over one column group (wave w: columns c0 + 128 w ..
+// +127) and the token range of one split; the waves walk the range together
+// in 32-row steps, the next step's loads issued before the current step is
+// used. In a step lane l holds rows 8 (l/16) + i (i < 8) at columns
+// 8 (l%16) .. +7 of its wave's 128 (colreduce_bf16's blocks) and
+//  - dB: transposes the 8 x 8 block in registers for colreduce's MFMAs
+//    (Hd^T split hi + lo as the A operand), accumulating over the split;
+//    each wave owns its columns, so there is no cross-wave combine;
+//  - G: writes the block to its wave's LDS tile [32 rows][128 columns]
+//    (16-byte chunks XOR-swizzled by row, conflict-free both ways), reads it
+//    back as MFMA 16x16x32 A fragments (row l%16, 8 columns) against the
+//    B rows (split hi + lo, in registers for the wave's columns); the four
+//    waves' sums for the step's 32 rows are added in wave order through a
+//    double-buffered LDS exchange (one barrier per step) and written to
+//    gpart[group][t][0..r).
+struct DyJobDev {
+    const uint16_t* dY;
+    int64_t N;
+    const float* B;
+    const float* Pt;
+    float* partB;
+    float* gpart;
+    int64_t chunk;
+    int64_t part_stride;
+    int groups;
+};
+struct DyBatch {
+    DyJobDev job[kMaxProj];
+    int start[kMaxProj + 1];
+    int njobs;
+    int r;
+};
+
+template <int RC, bool PTV>
+__global__ __launch_bounds__(256) void dy_pass_bf16(int64_t T, DyBatch db) {
+    int ji = 0;
+    while (ji + 1 < db.njobs && (int)blockIdx.x >= db.start[ji + 1]) ++ji;  // wave-uniform
+    const DyJobDev& J = db.job[ji];
+    const int b = (int)blockIdx.x - db.start[ji];
+    const int r = db.r;
+    const int64_t N = J.N;
+    const int lane = lane_id();
+    const int wave = threadIdx.x >> 6;
+    const int grp = b % J.groups;
+    const int64_t split = b / J.groups;
+    const int64_t cw0 = (int64_t)grp * kDyCols + 128 * wave;
+    const int64_t tb = split * J.chunk;
+    const int64_t te = tb + J.chunk < T ? tb + J.chunk : T;
+    const int64_t col = cw0 + 8 * (lane & 15);
+    const bool col_ok = col < N;
+    const int g8 = 8 * (lane >> 4);
+    const bool do_b = J.partB != nullptr, do_g = J.gpart != nullptr;
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(J.dY + tb * N, (te - tb) * N * 2);
+    const __amdgpu_buffer_rsrc_t rp = make_rsrc(J.Pt, do_b ? (int64_t)r * T * 4 : 0);
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(J.B, do_g ? (int64_t)r * N * 4 : 0);
+
+    // G's B operand of k-chunk kc (32 columns): lane l holds B[16 rc + l%16]
+    // [cw0 + 32 kc + 8 (l/16) .. +7], split hi + lo; ranks past r and
+    // columns past N load as zeros
+    uint4 bh[4][RC], bl[4][RC];
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc)
+#pragma unroll
+        for (int rc = 0; rc < RC; ++rc) {
+            const int j = rc * 16 + (lane & 15);
+            const int64_t c = cw0 + 32 * kc + 8 * (lane >> 4);
+            const bool ok = j < r && c < N;
+            const uint32_t off = ok ? (uint32_t)(((int64_t)j * N + c) * 4) : kOOB;
+            const i32x4 a = buf_load16(rb, off), q = buf_load16(rb, ok ? off + 16 : kOOB);
+            float v[8];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                v[e] = __int_as_float(a[e]);
+                v[4 + e] = __int_as_float(q[e]);
+            }
+            split_hilo8(v, bh[kc][rc], bl[kc][rc]);
+        }
+
+    f32x4 acc[8][RC];
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+#pragma unroll
+        for (int rc = 0; rc < RC; ++rc) acc[e][rc] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    __shared__ uint4 gtile[4][32 * 16];            // per wave: [32 rows][16 chunks]
+    __shared__ float gx[2][4][2][RC][4][64];       // [buffer][wave][row tile][rc][q][lane]
+    uint4* tile = gtile[wave];
+
+    auto load_step = [&](int64_t t0, uint4 (&R)[8], float (&pv)[RC][8]) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int64_t t = t0 + g8 + i - tb;
+            R[i] = __builtin_bit_cast(uint4, buf_load16(rx, col_ok ? (uint32_t)((t * N + col) * 2) : kOOB));
+        }
+        if (do_b) {
+#pragma unroll
+            for (int rc = 0; rc < RC; ++rc) {
+                const int j = rc * 16 + (lane & 15);
+                const int64_t t = t0 + g8;
+                if constexpr (PTV) {
+                    const uint32_t off = (uint32_t)(((int64_t)j * T + t) * 4);
+                    const i32x4 a = buf_load16(rp, off), q = buf_load16(rp, off + 16);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        pv[rc][e] = __int_as_float(a[e]);
+                        pv[rc][4 + e] = __int_as_float(q[e]);
+                    }
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e)
+                        pv[rc][e] = __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+                            rp, (int)(((int64_t)j * T + t + e) * 4), 0, 0));
+                }
+            }
+        }
+    };
+
+    uint4 R[8];
+    float pv[RC][8];
+    if (tb < te) load_step(tb, R, pv);
+    int buf = 0;
+    for (int64_t t0 = tb; t0 < te; t0 += 32, buf ^= 1) {
+        uint4 cR[8];
+        float cp[RC][8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) cR[i] = R[i];
+#pragma unroll
+        for (int rc = 0; rc < RC; ++rc)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) cp[rc][e] = pv[rc][e];
+        if (t0 + 32 < te) load_step(t0 + 32, R, pv);  // uniform
+        if (do_b) {
+            uint4 ahi[RC], alo[RC];
+#pragma unroll
+            for (int rc = 0; rc < RC; ++rc) {
+                // tokens past the range: dY is zero there, and Hd^T is zeroed
+                // so that a non-finite value of another token cannot leak in
+                float v[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[e] = (t0 + g8 + e < te) ? cp[rc][e] : 0.f;
+                split_hilo8(v, ahi[rc], alo[rc]);
+            }
+            uint4 Bt[8];
+            transpose8x8(cR, Bt);
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+#pragma unroll
+                for (int rc = 0; rc < RC; ++rc) {
+                    acc[e][rc] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ahi[rc]), as_bf16x8(Bt[e]), acc[e][rc], 0, 0, 0);
+                    acc[e][rc] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(alo[rc]), as_bf16x8(Bt[e]), acc[e][rc], 0, 0, 0);
+                }
+        }
+        if (do_g) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int row = g8 + i;
+                tile[row * 16 + ((lane & 15) ^ (row & 15))] = cR[i];
+            }
+            // a wave's DS operations complete in order: the reads below see
+            // the writes above
+            f32x4 ag[2][RC];
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+                for (int rc = 0; rc < RC; ++rc) ag[rt][rc] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+                for (int kc = 0; kc < 4; ++kc) {
+                    const int row = rt * 16 + (lane & 15);
+                    const uint4 a = tile[row * 16 + ((4 * kc + (lane >> 4)) ^ (row & 15))];
+#pragma unroll
+                    for (int rc = 0; rc < RC; ++rc) {
+                        ag[rt][rc] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a), as_bf16x8(bh[kc][rc]), ag[rt][rc], 0, 0, 0);
+                        ag[rt][rc] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a), as_bf16x8(bl[kc][rc]), ag[rt][rc], 0, 0, 0);
+                    }
+                }
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+                for (int rc = 0; rc < RC; ++rc)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) gx[buf][wave][rt][rc][q][lane] = ag[rt][rc][q];
+            __syncthreads();
+            for (int idx = threadIdx.x; idx < 2 * RC * 4 * 64; idx += 256) {
+                const int l = idx & 63, q = (idx >> 6) & 3, rc = (idx >> 8) % RC, rt = (idx >> 8) / RC;
+                const float v = gx[buf][0][rt][rc][q][l] + gx[buf][1][rt][rc][q][l] + gx[buf][2][rt][rc][q][l] +
+                                gx[buf][3][rt][rc][q][l];
+                const int64_t t = t0 + rt * 16 + 4 * (l >> 4) + q;
+                const int j = rc * 16 + (l & 15);
+                if (t < te && j < r) J.gpart[((int64_t)grp * T + t) * r + j] = v;
+            }
+        }
+    }
+    if (do_b && col_ok) {
+        float* out = J.partB + split * J.part_stride;
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+#pragma unroll
+            for (int rc = 0; rc < RC; ++rc)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int j = rc * 16 + (lane >> 4) * 4 + q;
+                    out[(int64_t)j * N + col + e] = acc[e][rc][q];
+                }
+    }
+}
+
+// G finishing, one workgroup per 64 tokens of one projection: the column
+// groups' partials are summed in group order, scaled and masked; Gd goes to
+// gd_ext row-wise and, through LDS, to gd_t [r][T] in 64-token row segments.
+// Blocks past the projections' run the PrepJobs (grid-stride).
+struct DyFinishBatch {
+    DyFinishJob job[kMaxProj];
+    PrepJob prep[kMaxProj];
+    int njobs, npreps;
+    int64_t prep_start[kMaxProj + 1];
+    int blocks_per_job;
+    int r, rext, ext_ld;
+    float scale, keep;
+};
+
+__global__ __launch_bounds__(256) void dy_finish(int64_t T, DyFinishBatch fb) {
+    const int b = (int)blockIdx.x;
+    const int jobs_blocks = fb.njobs * fb.blocks_per_job;
+    if (b >= jobs_blocks) {
+        const int64_t n = fb.prep_start[fb.npreps];
+        const int64_t nb = (int64_t)gridDim.x - jobs_blocks;
+        for (int64_t idx = (int64_t)(b - jobs_blocks) * 256 + threadIdx.x; idx < n; idx += nb * 256) {
+            int j = 0;
+            while (j + 1 < fb.npreps && idx >= fb.prep_start[j + 1]) ++j;
+            prep_one(fb.prep[j], idx - fb.prep_start[j]);
+        }
+        return;
+    }
+    const DyFinishJob& J = fb.job[b / fb.blocks_per_job];
+    const int64_t t0 = (int64_t)(b % fb.blocks_per_job) * 64;
+    const int r = fb.r;
+    __shared__ float tt[32][65];  // [rank][token] for the transposed store
+    for (int idx = threadIdx.x; idx < 64 * r; idx += 256) {
+        const int tl = idx / r, j = idx % r;
+        const int64_t t = t0 + tl;
+        float v = 0.f;
+        if (t < T) {
+            // groups in order, loads of eight issued together
+            const float* p = J.gpart + t * r + j;
+            const int64_t stride = T * r;
+            int g = 0;
+            for (; g + 8 <= J.groups; g += 8) {
+                float u[8];
+#pragma unroll
+                for (int k = 0; k < 8; ++k) u[k] = p[(int64_t)(g + k) * stride];
+#pragma unroll
+                for (int k = 0; k < 8; ++k) v += u[k];
+            }
+            for (; g < J.groups; ++g) v += p[(int64_t)g * stride];
+            v *= fb.scale;
+            if (J.mask) v = J.mask[t * r + j] ? v * fb.keep : 0.f;
+            if (J.gd_ext) {
+                uint16_t* e = J.gd_ext + t * fb.ext_ld;
+                e[j] = f32_to_bf16(v);
+                if (j == r - 1)
+                    for (int z = r; z < fb.rext; ++z) e[z] = 0;
+            }
+        }
+        tt[j][tl] = v;
+    }
+    if (!J.gd_t) return;  // uniform
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < 64 * r; idx += 256) {
+        const int j = idx / 64, tl = idx % 64;
+        if (t0 + tl < T) J.gd_t[(int64_t)j * T + t0 + tl] = tt[j][tl];
+    }
+}
+
 // -------------------------------------------------------- bf16 transpose
 // 64 x 64 tiles through LDS: 16-byte row chunks in, 16-byte column chunks
 // out (the frozen W of the backward GEMM, read and written once per call).
@@ -771,6 +1047,73 @@ hipError_t launch_split_sum(const SumJob* jobs, int n, hipStream_t stream) {
     int64_t blocks = (total + 255) / 256;
     if (blocks > 4096) blocks = 4096;
     split_sum<<<dim3((unsigned)blocks), 256, 0, stream>>>(sb);
+    return hipGetLastError();
+}
+
+// Splits of the fused dY pass: at least ~512 workgroups over the column
+// groups and splits, each split at least eight 32-row steps, and no split's
+// rows of dY spanning 2^31 bytes (32-bit buffer offsets).
+int dy_splits(int64_t T, int64_t N) {
+    const int64_t groups = dy_groups(N);
+    int64_t s = (512 + groups - 1) / groups;
+    const int64_t max_s = (T + 255) / 256;
+    if (s > max_s) s = max_s;
+    if (s < 1) s = 1;
+    const int64_t rows_cap = (int64_t)0x7fffffff / (2 * N) / 32 * 32;
+    const int64_t min_s = rows_cap > 0 ? (T + rows_cap - 1) / rows_cap : T;
+    if (s < min_s) s = min_s;
+    return (int)s;
+}
+
+hipError_t launch_dy_pass(int64_t T, int r, const DyJob* jobs, int n, hipStream_t stream) {
+    DyBatch db{};
+    db.r = r;
+    int k = 0;
+    for (int i = 0; i < n && k < kMaxProj; ++i) {
+        const DyJob& J = jobs[i];
+        if (!J.dY || (!J.partB && !J.gpart)) continue;
+        const int splits = dy_splits(T, J.N);
+        DyJobDev d{J.dY, J.N, J.B, J.Pt, J.partB, J.gpart, round_up((T + splits - 1) / splits, 32),
+                   (int64_t)colreduce_rows(r) * J.N, dy_groups(J.N)};
+        // the chunk is rounded to whole steps: splits past T write zero partials
+        db.job[k] = d;
+        db.start[k + 1] = db.start[k] + d.groups * splits;
+        ++k;
+    }
+    db.njobs = k;
+    if (k == 0) return hipSuccess;
+    const dim3 grid((unsigned)db.start[k]);
+    const bool ptv = (T & 3) == 0;
+    if (r <= 16) {
+        if (ptv) dy_pass_bf16<1, true><<<grid, 256, 0, stream>>>(T, db);
+        else dy_pass_bf16<1, false><<<grid, 256, 0, stream>>>(T, db);
+    } else {
+        if (ptv) dy_pass_bf16<2, true><<<grid, 256, 0, stream>>>(T, db);
+        else dy_pass_bf16<2, false><<<grid, 256, 0, stream>>>(T, db);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_dy_finish(int64_t T, int r, float scale, float keep, int rext, int ext_ld,
+                            const DyFinishJob* jobs, int n, const PrepJob* preps, int npreps, hipStream_t stream) {
+    DyFinishBatch fb{};
+    fb.r = r; fb.rext = rext; fb.ext_ld = ext_ld; fb.scale = scale; fb.keep = keep;
+    fb.blocks_per_job = (int)((T + 63) / 64);
+    for (int i = 0; i < n && fb.njobs < kMaxProj; ++i)
+        if (jobs[i].gpart && (jobs[i].gd_t || jobs[i].gd_ext)) fb.job[fb.njobs++] = jobs[i];
+    for (int i = 0; i < npreps && fb.npreps < kMaxProj; ++i) {
+        if (!preps[i].hi) continue;
+        PrepJob p = preps[i];
+        if (p.ld_out == 0) p.ld_out = p.cols_out;
+        fb.prep[fb.npreps] = p;
+        fb.prep_start[fb.npreps + 1] = fb.prep_start[fb.npreps] + p.rows_out * p.cols_out;
+        ++fb.npreps;
+    }
+    const int64_t prep_n = fb.prep_start[fb.npreps];
+    const int64_t prep_blocks = prep_n > 0 ? std::min<int64_t>((prep_n + 255) / 256, 512) : 0;
+    const int64_t blocks = (int64_t)fb.njobs * fb.blocks_per_job + prep_blocks;
+    if (blocks == 0) return hipSuccess;
+    dy_finish<<<dim3((unsigned)blocks), 256, 0, stream>>>(T, fb);
     return hipGetLastError();
 }
 

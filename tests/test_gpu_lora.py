@@ -121,6 +121,20 @@ def test_config_projections_bf16(mc, dev, name, T, K, N, r):
     _check(mc, dev, c, 2.0, BF16_TOL, sample_rows=256)
 
 
+@pytest.mark.parametrize("name,T,K,N,r,p", [
+    # dY of >= 2^26 elements at rank <= 32 takes the fused dY pass (G and the
+    # dB partials from one read of dY): odd T (scalar Hd^T loads, a last
+    # split past T), 17-32 ranks (two 16-rank tiles), dropout, a ragged last
+    # 512-column group
+    ("fused dY pass, odd T, r24, dropout", 16383, 1024, 8200, 24, 0.1),
+    ("fused dY pass, r16, no dropout", 8192, 512, 8192, 16, 0.0),
+])
+def test_fused_dy_pass(mc, dev, name, T, K, N, r, p):
+    c = lora_case(zlib.crc32(name.encode()), T, K, N, r)
+    mask = mc.dropout_mask(zlib.crc32(name.encode()), p, T, r).numpy() if p > 0 else None
+    _check(mc, dev, c, 2.0, BF16_TOL, mask=mask, p=p, sample_rows=256)
+
+
 def test_config5_dropout_bf16(mc, dev):
     """c5-style: rank 64, alpha 128, dropout 0.1 with the seed-1234 host mask."""
     T, K, N, r = 2048, 3584, 512, 64

@@ -105,18 +105,22 @@ def test_group_delta_only_member(mc, dev):
     _check_group(mc, dev, 1024, 256, [256, 64, 128], 16, 0.0, 41, no_w=(1,))
 
 
-def test_group_partial_outputs(mc, dev):
-    """dX only, dA / dB only: the same values as the full call."""
-    x, projs, dys = _group_case(dev, 2048, 512, [512, 256], 16, 0.0, 7)
+@pytest.mark.parametrize("T,K,Ns", [(2048, 512, [512, 256]),
+                                    (8192, 512, [8192, 8200])])  # the fused dY pass (dY of >= 2^26 elements)
+def test_group_partial_outputs(mc, dev, T, K, Ns):
+    """dX only, dA / dB only, dB only: the same values as the full call."""
+    x, projs, dys = _group_case(dev, T, K, Ns, 16, 0.0, 7)
     ys, hs = mc.lora_group_forward(x, projs, 2.0)
     full = mc.lora_group_backward(x, projs, dys, 2.0, h_saves=hs)
     only_dx = mc.lora_group_backward(x, projs, dys, 2.0, need_dA=False, need_dB=False)
     only_ab = mc.lora_group_backward(x, projs, dys, 2.0, h_saves=hs, need_dx=False)
+    only_b = mc.lora_group_backward(x, projs, dys, 2.0, h_saves=hs, need_dx=False, need_dA=False)
     torch.cuda.synchronize()
     assert torch.equal(only_dx[0], full[0]) and only_dx[1][0] is None
-    assert only_ab[0] is None
+    assert only_ab[0] is None and only_b[0] is None and only_b[1][0] is None
     for g in range(2):
         assert torch.equal(only_ab[1][g], full[1][g]) and torch.equal(only_ab[2][g], full[2][g])
+        assert torch.equal(only_b[2][g], full[2][g])
 
 
 def test_group_with_caller_wt(mc, dev):
