@@ -326,7 +326,7 @@ hipError_t launch_lora_group_fwd(const mc_lora_desc& d, const void* x, const Lor
         }
     }
     GemmOut outs[kMaxProj];
-    double flops = 0, bytes = 0;
+    double flops[kMaxProj], bytes[kMaxProj];
     for (int g = 0; g < count; ++g) {
         const int64_t kbase = proj[g].W ? m.K : 0;
         outs[g].N = Ns[g];
@@ -337,12 +337,20 @@ hipError_t launch_lora_group_fwd(const mc_lora_desc& d, const void* x, const Lor
         outs[g].bias = static_cast<const uint16_t*>(proj[g].bias);
         outs[g].c = static_cast<uint16_t*>(y[g]);
         outs[g].ldc = Ns[g];
-        flops += 2.0 * m.T * Ns[g] * (kbase > 0 ? kbase : m.r);
-        bytes += 2.0 * (Ns[g] * (double)(kbase + m.rext) + (double)m.T * Ns[g] + (double)m.T * m.rext);
+        flops[g] = 2.0 * m.T * Ns[g] * (kbase > 0 ? kbase : m.r);
+        bytes[g] = 2.0 * (Ns[g] * (double)(kbase + m.rext) + (double)m.T * Ns[g] + (double)m.T * m.rext);
     }
-    bytes += 2.0 * m.T * m.K;  // x, read once by the whole grid
-    auto sc = prof::Scope(prof::kGemm, st, flops, bytes);
-    return launch_gemm_bf16_multi(m.T, outs, count, st);
+    if (gemm_bf16_multi_one_launch(m.T, outs, count)) {
+        double f = 0, b = 2.0 * m.T * m.K;  // x, read once by the whole grid
+        for (int g = 0; g < count; ++g) { f += flops[g]; b += bytes[g]; }
+        auto sc = prof::Scope(prof::kGemm, st, f, b);
+        return launch_gemm_bf16_multi(m.T, outs, count, st);
+    }
+    for (int g = 0; g < count; ++g) {  // one launch (and one timed scope) per projection
+        auto sc = prof::Scope(prof::kGemm, st, flops[g], bytes[g] + 2.0 * m.T * m.K);
+        MC_TRY(launch_gemm_bf16(m.T, Ns[g], outs[g].seg, outs[g].nseg, outs[g].bias, outs[g].c, outs[g].ldc, st));
+    }
+    return hipSuccess;
 }
 
 hipError_t launch_lora_group_bwd(const mc_lora_desc& d, const void* x, const LoraProj* proj, int count,

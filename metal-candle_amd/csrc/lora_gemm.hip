@@ -780,26 +780,35 @@ GemmTile choose_multi_tile(int64_t M, const int64_t* Ns, int nout, int64_t K, in
     return best;
 }
 
-hipError_t launch_gemm_bf16_multi(int64_t M, const GemmOut* outs, int nout, hipStream_t stream) {
+bool gemm_bf16_multi_one_launch(int64_t M, const GemmOut* outs, int nout) {
+    // One launch over every block's columns with one tile shape, or one
+    // launch per block with its own plan (a split plan can fill the CUs'
+    // last round with narrower tiles), whichever the estimate says is faster.
     int64_t Ns[kGemmMaxOut];
     int64_t K = 0;
     for (int o = 0; o < nout; ++o) Ns[o] = outs[o].N;
     for (int i = 0; i < outs[0].nseg; ++i) K += outs[0].seg[i].k;
-    // One launch over every block's columns with one tile shape, or one
-    // launch per block with its own plan (a split plan can fill the CUs'
-    // last round with narrower tiles), whichever the estimate says is faster.
     const int cus = cu_count();
     const GemmTile t = choose_multi_tile(M, Ns, nout, K, cus);
     double sep = 0.0;
     for (int o = 0; o < nout; ++o) sep += plan_time(M, Ns[o], K, choose_gemm_plan(M, Ns[o], K, cus), cus);
-    if (sep < plan_time_multi(M, Ns, nout, K, t, cus)) {
+    return !(sep < plan_time_multi(M, Ns, nout, K, t, cus));
+}
+
+hipError_t launch_gemm_bf16_multi(int64_t M, const GemmOut* outs, int nout, hipStream_t stream) {
+    if (!gemm_bf16_multi_one_launch(M, outs, nout)) {
         for (int o = 0; o < nout; ++o) {
-            const hipError_t e = launch_gemm_bf16(M, Ns[o], outs[o].seg, outs[o].nseg, outs[o].bias, outs[o].c,
+            const hipError_t e = launch_gemm_bf16(M, outs[o].N, outs[o].seg, outs[o].nseg, outs[o].bias, outs[o].c,
                                                   outs[o].ldc, stream);
             if (e != hipSuccess) return e;
         }
         return hipSuccess;
     }
+    int64_t Ns[kGemmMaxOut];
+    int64_t K = 0;
+    for (int o = 0; o < nout; ++o) Ns[o] = outs[o].N;
+    for (int i = 0; i < outs[0].nseg; ++i) K += outs[0].seg[i].k;
+    const GemmTile t = choose_multi_tile(M, Ns, nout, K, cu_count());
     switch (t) {
         case GemmTile::k256x256: return launch_multi<256, 256, 128, 64, 64, 2>(M, outs, nout, stream, 4);
         case GemmTile::k256x192: return launch_multi<256, 192, 64, 96, 64, 2>(M, outs, nout, stream, 4);

@@ -111,10 +111,6 @@ struct ColJob {
 };
 int colreduce_splits(int64_t T, int64_t C);
 hipError_t launch_colreduce_bf16(int64_t T, const ColJob* jobs, int n, hipStream_t stream);
-// One job: out = scale * sum_s partial[s][j][c] (s ascending) for j < r,
-// c < C, written to out[c*r + j] when transpose_out (dA [K][r]) else
-// out[j*C + c] (dB [r][N]); part_stride = colreduce_rows * C. A job with
-// out == nullptr is skipped; up to kSumJobs jobs run in one launch.
 // ------------------------------------------------ fused dY pass (r <= 32)
 // One read of a projection's dY [T][N] gives both rank-r products of the
 // backward that reduce it:
@@ -154,6 +150,10 @@ struct DyFinishJob {
 hipError_t launch_dy_finish(int64_t T, int r, float scale, float keep, int rext, int ext_ld,
                             const DyFinishJob* jobs, int n, const PrepJob* preps, int npreps, hipStream_t stream);
 
+// One job: out = scale * sum_s partial[s][j][c] (s ascending) for j < r,
+// c < C, written to out[c*r + j] when transpose_out (dA [K][r]) else
+// out[j*C + c] (dB [r][N]); part_stride = colreduce_rows * C. A job with
+// out == nullptr is skipped; up to kSumJobs jobs run in one launch.
 struct SumJob {
     const float* partial;
     int splits;
@@ -196,6 +196,9 @@ struct GemmOut {
     int64_t ldc;
 };
 hipError_t launch_gemm_bf16_multi(int64_t M, const GemmOut* outs, int nout, hipStream_t stream);
+// Whether launch_gemm_bf16_multi runs the blocks as one launch (else one
+// launch per block, in block order).
+bool gemm_bf16_multi_one_launch(int64_t M, const GemmOut* outs, int nout);
 // Workgroup tiles of the bf16 GEMM for an M x N output with reduction length
 // K on `cus` compute units: `main` over columns [0, n1), `tail` over [n1, N)
 // (n1 == N: one tile shape; otherwise main is 256 x 256).
