@@ -65,7 +65,7 @@ mc_status check_lora_desc(const mc_lora_desc* d) {
              (long long)d->tokens, (long long)d->in_features, (long long)d->out_features);
     // LoRAConfig::validate: "LoRA rank must be greater than 0" (lora.rs:99-104)
     MC_CHECK(d->rank >= 1, MC_ERR_SHAPE, "LoRA rank must be greater than 0");
-    MC_CHECK(d->rank <= 128, MC_ERR_SHAPE, "LoRA: rank %d exceeds the supported maximum 128", (int)d->rank);
+    MC_CHECK(d->rank <= 8192, MC_ERR_SHAPE, "LoRA: rank %d exceeds the supported maximum 8192", (int)d->rank);
     MC_CHECK(std::isfinite(d->scale), MC_ERR_VALUE, "LoRA: scale must be finite");
     // LoRAConfig::validate: "LoRA dropout must be in [0, 1)" (lora.rs:113-118)
     MC_CHECK(d->dropout_p >= 0.0f && d->dropout_p < 1.0f, MC_ERR_VALUE, "LoRA dropout must be in [0, 1)");

@@ -13,6 +13,8 @@
 //   3. dA = x^T.Gd and dB = s Hd^T.dY: split-T column reductions (one
 //      launch) and their fixed-order split sums (one launch)
 // The fp32 path runs the same sequence with fp32 operands and FMA kernels.
+#include <algorithm>
+
 #include "common.hpp"
 #include "kernels.hpp"
 #include "lora_kernels.hpp"
@@ -119,10 +121,9 @@ LoraFwdWs lora_fwd_ws(const mc_lora_desc& d) {
     const Dims m = dims_of(d);
     LoraFwdWs w{};
     size_t off = 0;
-    if (m.bf16) {
-        w.at_hilo = off; off += align256((size_t)2 * m.r16 * m.K * 2);
-        w.bt_ext = off;  off += align256((size_t)m.N * m.rext * 2);
-        w.hs_ext = off;  off += align256((size_t)m.T * m.rext * 2);
+    if (m.bf16) {  // the bf16 forward runs as a grouped forward of one projection
+        const int64_t N = m.N;
+        off = lora_group_fwd_ws(d, &N, 1).total;
     } else {
         w.bt_ext = off;  off += align256((size_t)m.N * m.r * 4);
         w.hs_ext = off;  off += align256((size_t)m.T * m.r * 4);
@@ -205,23 +206,12 @@ hipError_t launch_lora_fwd(const mc_lora_desc& d, const void* x, const void* W, 
     const float keep = mask ? 1.0f / (1.0f - d.dropout_p) : 1.0f;
     const int64_t kbase = W ? m.K : 0;
     if (m.bf16) {
-        uint16_t* at_hi = reinterpret_cast<uint16_t*>(base + w.at_hilo);
-        uint16_t* at_lo = at_hi + (size_t)m.r16 * m.K;
-        uint16_t* bt = reinterpret_cast<uint16_t*>(base + w.bt_ext);
-        uint16_t* hs = reinterpret_cast<uint16_t*>(base + w.hs_ext);
-        const uint16_t* xb = static_cast<const uint16_t*>(x);
-        {
-            auto sc = lowrank_scope(st, m.T, m.K, m.r, 2);
-            const PrepJob jobs[2] = {prep_job(A, m.r, m.r, m.K, true, at_hi, at_lo, m.r16, m.K),   // A^T hi / lo
-                                     prep_job(B, m.N, m.N, m.r, true, bt, nullptr, m.N, m.rext)};  // B^T, zero-padded
-            MC_TRY(launch_prep_bf16(jobs, 2, st));
-            MC_TRY(launch_rowproj_bf16(xb, m.T, m.K, at_hi, at_lo, m.r, 1.0f, mask, keep, h_save, hs, m.rext,
-                                       d.scale, st));
-        }
-        const GemmSeg segs[2] = {{xb, m.K, static_cast<const uint16_t*>(W), m.K, kbase}, {hs, m.rext, bt, m.rext, m.rext}};
-        auto sc = gemm_scope(st, m.T, m.N, kbase, m.rext, m.r, 2);
-        return launch_gemm_bf16(m.T, m.N, segs, 2, static_cast<const uint16_t*>(bias), static_cast<uint16_t*>(y),
-                                m.N, st);
+        // one projection of the grouped forward (the same prep, row projection
+        // and GEMM launches as a group of one)
+        const LoraProj p{m.N, W, bias, A, B, mask};
+        void* const ys[1] = {y};
+        float* const hs[1] = {h_save};
+        return launch_lora_group_fwd(d, x, &p, 1, ys, hs, ws, st);
     }
     float* bt = reinterpret_cast<float*>(base + w.bt_ext);
     float* hs = reinterpret_cast<float*>(base + w.hs_ext);
@@ -301,28 +291,44 @@ hipError_t launch_lora_group_fwd(const mc_lora_desc& d, const void* x, const Lor
                               2.0 * m.T * m.K + 6.0 * m.T * m.r * count + 12.0 * m.r * (m.K + sumN / count) * count);
         for (int p0 = 0, pass = 0; p0 < count; p0 += ppp, ++pass) {
             const int np = count - p0 < ppp ? count - p0 : ppp;
-            const int rpass = np * m.r, r16 = 16 * rowproj_rc(rpass);
-            uint16_t* at_hi = reinterpret_cast<uint16_t*>(base + w.at_hilo[pass]);
-            uint16_t* at_lo = at_hi + (size_t)r16 * m.K;
-            PrepJob jobs[2 * kMaxProj + 1];
-            int nj = 0;
-            for (int i = 0; i < np; ++i)  // A_g^T hi / lo as rows [i r, (i + 1) r) of the pass's operand
-                jobs[nj++] = prep_job(proj[p0 + i].A, m.r, m.r, m.K, true, at_hi + (size_t)i * m.r * m.K,
-                                      at_lo + (size_t)i * m.r * m.K, m.r, m.K);
-            if (r16 > rpass)  // zero rows past the pass's ranks
-                jobs[nj++] = prep_job(proj[p0].A, 0, 0, 0, false, at_hi + (size_t)rpass * m.K,
-                                      at_lo + (size_t)rpass * m.K, r16 - rpass, m.K);
-            if (pass == 0)
-                for (int g = 0; g < count; ++g)  // B_g^T, zero-padded to rext columns
-                    jobs[nj++] = prep_job(proj[g].B, Ns[g], Ns[g], m.r, true,
-                                          reinterpret_cast<uint16_t*>(base + w.bt_ext[g]), nullptr, Ns[g], m.rext);
-            MC_TRY(prep_all(jobs, nj, st));
-            RowprojCall c{};
-            c.X = xb; c.T = m.T; c.C = m.K; c.P_hi = at_hi; c.P_lo = at_lo; c.r = rpass; c.rp = m.r;
-            c.scale = 1.0f; c.keep = proj[p0].mask ? 1.0f / (1.0f - d.dropout_p) : 1.0f;
-            for (int i = 0; i < np; ++i) { c.mask[i] = proj[p0 + i].mask; c.out_t[i] = h_save ? h_save[p0 + i] : nullptr; }
-            c.out_ext = hs + (size_t)p0 * m.rext; c.rext_p = m.rext; c.ext_ld = ext_ld; c.ext_scale = d.scale;
-            MC_TRY(launch_rowproj_bf16(c, st));
+            // A pass holds whole projections; a projection of more than
+            // kRowprojMaxRanks ranks (alone in its pass) takes its ranks in
+            // chunks [j0, j0 + rc), one pass over x each.
+            for (int j0 = 0; j0 < m.r; j0 += kRowprojMaxRanks) {
+                const int rc = np > 1 || m.r <= kRowprojMaxRanks ? m.r : std::min(kRowprojMaxRanks, m.r - j0);
+                const bool last = j0 + rc == m.r;
+                const int rpass = np * rc, r16 = 16 * rowproj_rc(rpass);
+                uint16_t* at_hi = reinterpret_cast<uint16_t*>(base + w.at_hilo[pass]);
+                uint16_t* at_lo = at_hi + (size_t)r16 * m.K;
+                PrepJob jobs[2 * kMaxProj + 1];
+                int nj = 0;
+                for (int i = 0; i < np; ++i)  // A_g^T hi / lo (ranks j0 ..) as rows [i rc, (i + 1) rc) of the operand
+                    jobs[nj++] = prep_job(proj[p0 + i].A + j0, m.r, rc, m.K, true, at_hi + (size_t)i * rc * m.K,
+                                          at_lo + (size_t)i * rc * m.K, rc, m.K);
+                if (r16 > rpass)  // zero rows past the pass's ranks
+                    jobs[nj++] = prep_job(proj[p0].A, 0, 0, 0, false, at_hi + (size_t)rpass * m.K,
+                                          at_lo + (size_t)rpass * m.K, r16 - rpass, m.K);
+                if (pass == 0 && j0 == 0)
+                    for (int g = 0; g < count; ++g)  // B_g^T, zero-padded to rext columns
+                        jobs[nj++] = prep_job(proj[g].B, Ns[g], Ns[g], m.r, true,
+                                              reinterpret_cast<uint16_t*>(base + w.bt_ext[g]), nullptr, Ns[g], m.rext);
+                MC_TRY(prep_all(jobs, nj, st));
+                RowprojCall c{};
+                c.X = xb; c.T = m.T; c.C = m.K; c.P_hi = at_hi; c.P_lo = at_lo; c.r = rpass; c.rp = rc;
+                c.scale = 1.0f; c.keep = proj[p0].mask ? 1.0f / (1.0f - d.dropout_p) : 1.0f;
+                c.mask_ld = m.r;
+                for (int i = 0; i < np; ++i) {
+                    c.mask[i] = proj[p0 + i].mask ? proj[p0 + i].mask + j0 : nullptr;
+                    c.out_t[i] = h_save && h_save[p0 + i] ? h_save[p0 + i] + (size_t)j0 * m.T : nullptr;
+                }
+                // projection p0 + i's columns start at i rext (+ j0); the last
+                // chunk zeroes the pad columns up to rext
+                c.out_ext = hs + (size_t)p0 * m.rext + j0;
+                c.rext_p = last ? rc + (m.rext - m.r) : rc;
+                c.ext_ld = ext_ld; c.ext_scale = d.scale;
+                MC_TRY(launch_rowproj_bf16(c, st));
+                if (last) break;
+            }
         }
     }
     GemmOut outs[kMaxProj];
@@ -459,25 +465,35 @@ hipError_t launch_lora_group_bwd(const mc_lora_desc& d, const void* x, const Lor
         return hipSuccess;
     }
     if (need_g) {
-        OperandsCall calls[kMaxProj];
         double bytes = 0, flops = 0;
         for (int g = 0; g < count; ++g) {
-            const bool tw = dX && need_wt[g];  // W^T into the workspace (none when the caller holds it)
-            calls[g] = OperandsCall{static_cast<const uint16_t*>(dY[g]), Ns[g], proj[g].B, proj[g].mask,
-                                    any_dA ? gdt + (size_t)g * m.r * m.T : nullptr,
-                                    dX ? gd + (size_t)g * m.rext : nullptr,
-                                    dX ? prep_job(proj[g].A, m.r, m.K, m.r, false, at + (size_t)g * m.rext, nullptr, m.K,
-                                                  m.rext, ext_ld)
-                                       : PrepJob{},
-                                    static_cast<const uint16_t*>(proj[g].W),
-                                    tw ? reinterpret_cast<uint16_t*>(base + w.wt[g]) : nullptr};
             // algorithmic: dY_g read, G_g written (fp32 and bf16), B_g and A_g read;
             // the W^T copy is workspace traffic, not counted
             bytes += 2.0 * m.T * Ns[g] + 6.0 * m.T * m.r + 4.0 * m.r * Ns[g] + (dX ? 6.0 * m.r * m.K : 0.0);
             flops += 2.0 * m.T * Ns[g] * m.r;
         }
         auto sc = prof::Scope(prof::kLowRank, st, flops, bytes);
-        MC_TRY(launch_lora_bwd_operands(calls, count, m.T, m.K, m.r, d.scale, keep, m.rext, ext_ld, st));
+        // ranks in chunks of at most kRowprojMaxRanks (one pass over dY each);
+        // the A extension and the W transposes ride with the first
+        for (int j0 = 0; j0 < m.r; j0 += kRowprojMaxRanks) {
+            const int rc = std::min(kRowprojMaxRanks, m.r - j0);
+            const bool first = j0 == 0, last = j0 + rc == m.r;
+            OperandsCall calls[kMaxProj];
+            for (int g = 0; g < count; ++g) {
+                const bool tw = dX && need_wt[g] && first;  // W^T into the workspace (none when the caller holds it)
+                calls[g] = OperandsCall{static_cast<const uint16_t*>(dY[g]), Ns[g], proj[g].B + (size_t)j0 * Ns[g],
+                                        proj[g].mask ? proj[g].mask + j0 : nullptr, (int64_t)m.r,
+                                        any_dA ? gdt + (size_t)g * m.r * m.T + (size_t)j0 * m.T : nullptr,
+                                        dX ? gd + (size_t)g * m.rext + j0 : nullptr,
+                                        dX && first ? prep_job(proj[g].A, m.r, m.K, m.r, false, at + (size_t)g * m.rext,
+                                                               nullptr, m.K, m.rext, ext_ld)
+                                                    : PrepJob{},
+                                        static_cast<const uint16_t*>(proj[g].W),
+                                        tw ? reinterpret_cast<uint16_t*>(base + w.wt[g]) : nullptr};
+            }
+            MC_TRY(launch_lora_bwd_operands(calls, count, m.T, m.K, rc, d.scale, keep,
+                                            last ? rc + (m.rext - m.r) : rc, ext_ld, st));
+        }
     }
     if (dX) {
         GemmSeg segs[kGemmMaxSeg];

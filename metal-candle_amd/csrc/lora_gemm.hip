@@ -784,6 +784,8 @@ bool gemm_bf16_multi_one_launch(int64_t M, const GemmOut* outs, int nout) {
     // One launch over every block's columns with one tile shape, or one
     // launch per block with its own plan (a split plan can fill the CUs'
     // last round with narrower tiles), whichever the estimate says is faster.
+    // A single block always takes its own plan.
+    if (nout <= 1) return false;
     int64_t Ns[kGemmMaxOut];
     int64_t K = 0;
     for (int o = 0; o < nout; ++o) Ns[o] = outs[o].N;

@@ -16,7 +16,9 @@ constexpr int kPrepJobs = 8;
 constexpr int kColJobs = 8;
 constexpr int kSumJobs = 8;
 
-// 16-row rank tiles of a row-projection pass over r ranks (r <= 128).
+// 16-row rank tiles of a row-projection pass over r ranks; a pass holds at
+// most kRowprojMaxRanks (more ranks take several passes over the input).
+constexpr int kRowprojMaxRanks = 128;
 inline int rowproj_rc(int r) { return r <= 16 ? 1 : r <= 32 ? 2 : r <= 48 ? 3 : r <= 64 ? 4 : 8; }
 // Rows of the split-T partials of a column reduction over r ranks: ranks go
 // in groups of 64, each taking 16, 32, 48 or 64 accumulator rows.
@@ -59,6 +61,9 @@ hipError_t launch_rowproj_bf16(const uint16_t* X, int64_t T, int64_t C, const ui
 // p rext_p + j % rp of out_ext (row stride ext_ld; the pad columns up to
 // (p + 1) rext_p are zeroed). With P_f32 set the parameter is read as fp32
 // [r][C] and split hi / lo in registers instead of P_hi / P_lo.
+// mask_ld is the mask's row stride (0: rp); a pass over ranks j0 .. of a
+// projection of more ranks passes its mask columns as mask + j0 with
+// mask_ld = the projection's rank.
 struct RowprojCall {
     const uint16_t* X;
     int64_t T, C;
@@ -68,6 +73,7 @@ struct RowprojCall {
     int r, rp;
     float scale;
     const uint8_t* mask[kMaxProj];
+    int64_t mask_ld;
     float keep;
     float* out_t[kMaxProj];
     uint16_t* out_ext;
@@ -86,6 +92,7 @@ struct OperandsCall {
     int64_t N;
     const float* B;
     const uint8_t* mask;
+    int64_t mask_ld;  // 0: the pass's ranks
     float* gd_t;
     uint16_t* gd_ext;
     PrepJob a_ext;

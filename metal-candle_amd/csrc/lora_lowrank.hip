@@ -128,6 +128,7 @@ struct RowprojArgs {
     int rp;
     float scale;
     const uint8_t* mask[kMaxProj];
+    int64_t mask_ld;  // elements between the mask rows of consecutive tokens
     float keep;
     float* out_t[kMaxProj];
     uint16_t* out_ext;
@@ -240,7 +241,7 @@ __device__ __forceinline__ void rowproj_body(const RowprojArgs& A, int64_t blk) 
         const uint8_t* mask = p == 0 ? A.mask[0] : p == 1 ? A.mask[1] : p == 2 ? A.mask[2] : A.mask[3];
         float* out_t = p == 0 ? A.out_t[0] : p == 1 ? A.out_t[1] : p == 2 ? A.out_t[2] : A.out_t[3];
         v *= scale;
-        if (mask) v = mask[t * rp + jj] ? v * keep : 0.f;
+        if (mask) v = mask[t * A.mask_ld + jj] ? v * keep : 0.f;
         if (out_t) out_t[(int64_t)jj * T + t] = v;
         if (out_ext) {
             uint16_t* e = out_ext + t * ext_ld + p * rext_p;
@@ -306,7 +307,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void c
     const bool col_ok = col < C;
     const int g8 = 8 * (lane >> 4);
     const __amdgpu_buffer_rsrc_t rx = make_rsrc(X + tb * C, (te - tb) * C * 2);
-    const __amdgpu_buffer_rsrc_t rp = make_rsrc(Pt, (int64_t)r * T * 4);
+    // Pt through one resource per 16-rank tile: a tile's offsets stay below
+    // 16 T 4 bytes (< 2^30 for T < 2^24); rows past r fall outside
+    __amdgpu_buffer_rsrc_t rp[RC];
+#pragma unroll
+    for (int rc = 0; rc < RC; ++rc) {
+        const int rows = r - rc * 16 < 16 ? (r - rc * 16 > 0 ? r - rc * 16 : 0) : 16;
+        rp[rc] = make_rsrc(Pt + (int64_t)rc * 16 * T, (int64_t)rows * T * 4);
+    }
 
     f32x4 acc[8][RC];
 #pragma unroll
@@ -328,11 +336,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void c
             }
 #pragma unroll
             for (int rc = 0; rc < RC; ++rc) {
-                const int j = rc * 16 + (lane & 15);
+                const int jl = lane & 15;  // rank within the tile
                 const int64_t t = t0 + g8;
                 if constexpr (PTV) {  // T % 4 == 0: 16-byte aligned rows of Pt
-                    const uint32_t off = (uint32_t)(((int64_t)j * T + t) * 4);
-                    const i32x4 a = buf_load16(rp, off), bq = buf_load16(rp, off + 16);
+                    const uint32_t off = (uint32_t)(((int64_t)jl * T + t) * 4);
+                    const i32x4 a = buf_load16(rp[rc], off), bq = buf_load16(rp[rc], off + 16);
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
                         pv[u][rc][e] = __int_as_float(a[e]);
@@ -342,7 +350,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void c
 #pragma unroll
                     for (int e = 0; e < 8; ++e)
                         pv[u][rc][e] = __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(
-                            rp, (int)(((int64_t)j * T + t + e) * 4), 0, 0));
+                            rp[rc], (int)(((int64_t)jl * T + t + e) * 4), 0, 0));
                 }
             }
         }
@@ -503,7 +511,13 @@ __global__ __launch_bounds__(256) void dy_pass_bf16(int64_t T, DyBatch db) {
     const int g8 = 8 * (lane >> 4);
     const bool do_b = J.partB != nullptr, do_g = J.gpart != nullptr;
     const __amdgpu_buffer_rsrc_t rx = make_rsrc(J.dY + tb * N, (te - tb) * N * 2);
-    const __amdgpu_buffer_rsrc_t rp = make_rsrc(J.Pt, do_b ? (int64_t)r * T * 4 : 0);
+    // Hd^T through one resource per 16-rank tile (offsets below 16 T 4 bytes)
+    __amdgpu_buffer_rsrc_t rp[RC];
+#pragma unroll
+    for (int rc = 0; rc < RC; ++rc) {
+        const int rows = r - rc * 16 < 16 ? (r - rc * 16 > 0 ? r - rc * 16 : 0) : 16;
+        rp[rc] = make_rsrc(J.Pt + (int64_t)rc * 16 * T, do_b ? (int64_t)rows * T * 4 : 0);
+    }
     const __amdgpu_buffer_rsrc_t rb = make_rsrc(J.B, do_g ? (int64_t)r * N * 4 : 0);
 
     // G's B operand of k-chunk kc (32 columns): lane l holds B[16 rc + l%16]
@@ -547,11 +561,11 @@ __global__ __launch_bounds__(256) void dy_pass_bf16(int64_t T, DyBatch db) {
         if (do_b) {
 #pragma unroll
             for (int rc = 0; rc < RC; ++rc) {
-                const int j = rc * 16 + (lane & 15);
+                const int jl = lane & 15;
                 const int64_t t = t0 + g8;
                 if constexpr (PTV) {
-                    const uint32_t off = (uint32_t)(((int64_t)j * T + t) * 4);
-                    const i32x4 a = buf_load16(rp, off), q = buf_load16(rp, off + 16);
+                    const uint32_t off = (uint32_t)(((int64_t)jl * T + t) * 4);
+                    const i32x4 a = buf_load16(rp[rc], off), q = buf_load16(rp[rc], off + 16);
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
                         pv[rc][e] = __int_as_float(a[e]);
@@ -561,7 +575,7 @@ __global__ __launch_bounds__(256) void dy_pass_bf16(int64_t T, DyBatch db) {
 #pragma unroll
                     for (int e = 0; e < 8; ++e)
                         pv[rc][e] = __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(
-                            rp, (int)(((int64_t)j * T + t + e) * 4), 0, 0));
+                            rp[rc], (int)(((int64_t)jl * T + t + e) * 4), 0, 0));
                 }
             }
         }
@@ -874,6 +888,7 @@ RowprojArgs rowproj_args(const RowprojCall& c) {
     A.r = c.r; A.rp = c.rp > 0 ? c.rp : c.r;
     A.scale = c.scale; A.keep = c.keep;
     for (int p = 0; p < kMaxProj; ++p) { A.mask[p] = c.mask[p]; A.out_t[p] = c.out_t[p]; }
+    A.mask_ld = c.mask_ld > 0 ? c.mask_ld : A.rp;
     A.out_ext = c.out_ext; A.rext_p = c.rext_p; A.ext_ld = c.ext_ld; A.ext_scale = c.ext_scale;
     return A;
 }
@@ -930,7 +945,8 @@ hipError_t launch_lora_bwd_operands(const OperandsCall* calls, int n, int64_t T,
         const OperandsCall& c = calls[o];
         RowprojCall rc_call{};
         rc_call.X = c.dY; rc_call.T = T; rc_call.C = c.N; rc_call.P_f32 = c.B; rc_call.r = r; rc_call.rp = r;
-        rc_call.scale = scale; rc_call.mask[0] = c.mask; rc_call.keep = keep; rc_call.out_t[0] = c.gd_t;
+        rc_call.scale = scale; rc_call.mask[0] = c.mask; rc_call.mask_ld = c.mask_ld; rc_call.keep = keep;
+        rc_call.out_t[0] = c.gd_t;
         rc_call.out_ext = c.gd_ext; rc_call.rext_p = rext_p; rc_call.ext_ld = ext_ld; rc_call.ext_scale = 1.0f;
         ob.rp[o] = rowproj_args(rc_call);
         ob.prep[o] = c.a_ext;

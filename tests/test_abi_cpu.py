@@ -25,7 +25,7 @@ def _desc(mc, T=16, K=16, N=16, r=4, scale=2.0, p=0.0, dtype=1):
     ("rank", 0, 2, "LoRA rank must be greater than 0"),        # lora.rs:99-104
     ("dropout_p", 1.0, 5, "LoRA dropout must be in [0, 1)"),    # lora.rs:113-118
     ("dropout_p", -0.1, 5, "LoRA dropout must be in [0, 1)"),
-    ("rank", 129, 2, "exceeds the supported maximum 128"),
+    ("rank", 8193, 2, "exceeds the supported maximum 8192"),
     ("tokens", 0, 2, "must be >= 1"),
     ("act_dtype", 7, 3, "unsupported act_dtype"),
     ("in_features", 12, 2, "multiples of 8"),

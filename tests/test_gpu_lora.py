@@ -78,7 +78,9 @@ def test_config1_fp32(mc, dev):
 @pytest.mark.parametrize("T,K,N,r", [(128, 512, 512, 8), (32, 256, 256, 4), (4 * 32, 256, 256, 16),
                                      (8 * 32, 256, 256, 32), (100, 40, 24, 3), (1, 8, 8, 1), (65, 72, 136, 17),
                                      # ranks past 64 (eight 16-rank MFMA tiles, 32-row projection blocks)
-                                     (300, 264, 200, 100), (64, 128, 128, 128)])
+                                     (300, 264, 200, 100), (64, 128, 128, 128),
+                                     # past 128 ranks: rank passes of 128 in the row projections
+                                     (200, 264, 136, 150)])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_reference_shapes(mc, dev, T, K, N, r, dtype):
     c = lora_case(T * 7 + r, T, K, N, r, dtype=dtype, bias=True)
@@ -130,6 +132,19 @@ def test_config_projections_bf16(mc, dev, name, T, K, N, r):
     ("fused dY pass, r16, no dropout", 8192, 512, 8192, 16, 0.0),
 ])
 def test_fused_dy_pass(mc, dev, name, T, K, N, r, p):
+    c = lora_case(zlib.crc32(name.encode()), T, K, N, r)
+    mask = mc.dropout_mask(zlib.crc32(name.encode()), p, T, r).numpy() if p > 0 else None
+    _check(mc, dev, c, 2.0, BF16_TOL, mask=mask, p=p, sample_rows=256)
+
+
+@pytest.mark.parametrize("name,T,K,N,r,p", [
+    # more than 128 ranks: the row projections take the ranks in passes of
+    # at most 128 (a ragged last pass, mask columns at a stride of r), the
+    # column reductions in groups of 64
+    ("rank 200, dropout", 3000, 512, 384, 200, 0.1),
+    ("rank 257, no dropout", 2048, 256, 520, 257, 0.0),
+])
+def test_rank_above_128(mc, dev, name, T, K, N, r, p):
     c = lora_case(zlib.crc32(name.encode()), T, K, N, r)
     mask = mc.dropout_mask(zlib.crc32(name.encode()), p, T, r).numpy() if p > 0 else None
     _check(mc, dev, c, 2.0, BF16_TOL, mask=mask, p=p, sample_rows=256)
