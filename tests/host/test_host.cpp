@@ -186,6 +186,17 @@ CASE(lora_layer_training_mode, false) {
     CHECK(!layer.is_training());
 }
 
+// lora.rs:302-310: the reference layer falls back to the candle composite on
+// any Err of the fused op. The mirror has no CPU path: a CPU input gives the
+// op's HIP-only error, which the caller's fallback then handles.
+CASE(lora_layer_cpu_input_is_an_error, false) {
+    TRY(layer, LoRALayer::create(32, 32, LoRAConfig{8, 16.f, 0.f}, kCpu));
+    TRY(x, Tensor::from_slice(ones(4 * 32), {4, 32}, kCpu));
+    auto y = layer.forward(x);
+    CHECK(y.is_err());
+    if (y.is_err()) CHECK_CONTAINS(y.error().to_string(), "FusedLoRAOp is HIP-only");
+}
+
 // custom_ops.rs:118-150: FusedLoRAOp::new validation.
 CASE(fused_lora_op_new_validation, false) {
     TRY(a3, Tensor::zeros({2, 4, 2}, DType::F32, kCpu));
