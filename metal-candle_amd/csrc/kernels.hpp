@@ -69,6 +69,7 @@ struct LoraGroupFwdWs {
     size_t at_hilo[kLoraMaxProj];  // per row-projection pass: bf16 [2][16 rc][K]
     size_t bt_ext[kLoraMaxProj];   // per projection: bf16 [N_g][rext]
     size_t hs_ext;                 // bf16 [T][G rext]: s Hd of every projection
+    size_t part;                   // split row projection: f32 [passes][splits][T][16 rc] partials of H
     size_t total;
 };
 struct LoraGroupBwdWs {
@@ -78,7 +79,8 @@ struct LoraGroupBwdWs {
     size_t gd_t;                   // f32 [G r][T]: Gd^T of every projection
     size_t part_a;                 // f32 [S_a][colreduce rows of G r][K]
     size_t part_b[kLoraMaxProj];   // f32 [S_b][colreduce rows of r][N_g]
-    size_t gpart[kLoraMaxProj];    // r <= 32: f32 [column groups of N_g][T][r], G partials of the fused dY pass
+    size_t gpart[kLoraMaxProj];    // G partials: f32 [column groups of N_g][T][r] of the fused dY pass, or
+                                   // f32 [splits][T][16 rc] of the split row projection
     size_t total;
 };
 LoraGroupFwdWs lora_group_fwd_ws(const mc_lora_desc& d, const int64_t* N, int count);

@@ -115,6 +115,20 @@ bool dy_fused(const Dims& m, const int64_t* N, int count) {
     return true;
 }
 
+// The split row projection (launch_rowsplit: 256-row workgroups sharing the
+// parameter through LDS, column splits finished by launch_dy_finish) takes
+// the rank-r passes of projections of 33-64 ranks, and in the forward also
+// those of at least 4096 columns: measured at the c4 / c5 shapes it ran the
+// 64-rank passes 2-2.5x faster than rowproj_bf16 / lora_bwd_operands and the
+// 8960-column one 14% faster, while a pass of 32 ranks or fewer over 1536
+// columns gained little once its finishing launch is counted. The choice
+// depends on the projection's rank and the shared K only, never on the
+// group, so a grouped call computes the same sums as single calls.
+bool fwd_rowsplit(const Dims& m) { return m.r <= kRowsplitRanks && (m.r > 32 || m.K >= 4096); }
+bool bwd_rowsplit(const Dims& m, const int64_t* N, int count) {
+    return m.r > 32 && m.r <= kRowsplitRanks && !dy_fused(m, N, count);
+}
+
 }  // namespace
 
 LoraFwdWs lora_fwd_ws(const mc_lora_desc& d) {
@@ -167,6 +181,12 @@ LoraGroupFwdWs lora_group_fwd_ws(const mc_lora_desc& d, const int64_t* N, int co
         off += align256((size_t)N[g] * m.rext * 2);
     }
     w.hs_ext = off; off += align256((size_t)m.T * count * m.rext * 2);
+    w.part = off;
+    if (fwd_rowsplit(m)) {
+        const int npass = (count + ppp - 1) / ppp;
+        const int ld = rowsplit_ld((count < ppp ? count : ppp) * m.r);
+        off += align256((size_t)npass * rowsplit_splits(m.T, m.K) * m.T * ld * 4);
+    }
     w.total = off;
     return w;
 }
@@ -189,9 +209,11 @@ LoraGroupBwdWs lora_group_bwd_ws(const mc_lora_desc& d, const int64_t* N, int co
         off += align256((size_t)(fused ? dy_splits(m.T, N[g]) : colreduce_splits(m.T, N[g])) * colreduce_rows(m.r) *
                         N[g] * 4);
     }
+    const bool split = bwd_rowsplit(m, N, count);
     for (int g = 0; g < count; ++g) {
         w.gpart[g] = off;
         if (fused) off += align256((size_t)dy_groups(N[g]) * m.T * m.r * 4);
+        if (split) off += align256((size_t)rowsplit_splits(m.T, N[g]) * m.T * rowsplit_ld(m.r) * 4);
     }
     w.total = off;
     return w;
@@ -289,7 +311,49 @@ hipError_t launch_lora_group_fwd(const mc_lora_desc& d, const void* x, const Lor
         for (int g = 0; g < count; ++g) sumN += Ns[g];
         auto sc = prof::Scope(prof::kLowRank, st, 2.0 * m.T * m.K * m.r * count,
                               2.0 * m.T * m.K + 6.0 * m.T * m.r * count + 12.0 * m.r * (m.K + sumN / count) * count);
-        for (int p0 = 0, pass = 0; p0 < count; p0 += ppp, ++pass) {
+        const bool split = fwd_rowsplit(m);
+        if (split) {
+            // One prep launch for every pass (A^T hi / lo, B^T extension
+            // operands), one split row projection whose passes share x (run
+            // interleaved), one finishing launch: H of each projection from
+            // its pass's partials -> h_save and the s Hd extension columns.
+            const int npass = (count + ppp - 1) / ppp;
+            const int rmax = (count < ppp ? count : ppp) * m.r;
+            const int ld = rowsplit_ld(rmax);
+            const int S = rowsplit_splits(m.T, m.K);
+            float* part = reinterpret_cast<float*>(base + w.part);
+            PrepJob jobs[3 * kMaxProj];
+            RowsplitJob rj[kMaxProj];
+            DyFinishJob fin[kMaxProj];
+            int nj = 0;
+            for (int p0 = 0, pass = 0; p0 < count; p0 += ppp, ++pass) {
+                const int np = count - p0 < ppp ? count - p0 : ppp;
+                const int rpass = np * m.r, r16 = 16 * rowproj_rc(rpass);
+                uint16_t* at_hi = reinterpret_cast<uint16_t*>(base + w.at_hilo[pass]);
+                uint16_t* at_lo = at_hi + (size_t)r16 * m.K;
+                for (int i = 0; i < np; ++i)  // A_g^T hi / lo as rows [i r, (i + 1) r) of the pass's operand
+                    jobs[nj++] = prep_job(proj[p0 + i].A, m.r, m.r, m.K, true, at_hi + (size_t)i * m.r * m.K,
+                                          at_lo + (size_t)i * m.r * m.K, m.r, m.K);
+                if (r16 > rpass)  // zero rows past the pass's ranks
+                    jobs[nj++] = prep_job(proj[p0].A, 0, 0, 0, false, at_hi + (size_t)rpass * m.K,
+                                          at_lo + (size_t)rpass * m.K, r16 - rpass, m.K);
+                float* pp = part + (size_t)pass * S * m.T * ld;
+                rj[pass] = RowsplitJob{xb, m.K, at_hi, at_lo, nullptr, r16, pp, S};
+                for (int i = 0; i < np; ++i) {
+                    const int g = p0 + i;
+                    fin[g] = DyFinishJob{pp + (size_t)i * m.r, S, proj[g].mask, h_save ? h_save[g] : nullptr,
+                                         hs + (size_t)g * m.rext, ld, m.r};
+                }
+            }
+            for (int g = 0; g < count; ++g)  // B_g^T, zero-padded to rext columns
+                jobs[nj++] = prep_job(proj[g].B, Ns[g], Ns[g], m.r, true, reinterpret_cast<uint16_t*>(base + w.bt_ext[g]),
+                                      nullptr, Ns[g], m.rext);
+            MC_TRY(prep_all(jobs, nj, st));
+            MC_TRY(launch_rowsplit(m.T, rmax, rj, npass, st));
+            MC_TRY(launch_dy_finish(m.T, m.r, 1.0f, proj[0].mask ? 1.0f / (1.0f - d.dropout_p) : 1.0f, m.rext, ext_ld,
+                                    d.scale, fin, count, nullptr, 0, st));
+        }
+        for (int p0 = 0, pass = 0; p0 < count && !split; p0 += ppp, ++pass) {
             const int np = count - p0 < ppp ? count - p0 : ppp;
             // A pass holds whole projections; a projection of more than
             // kRowprojMaxRanks ranks (alone in its pass) takes its ranks in
@@ -419,7 +483,7 @@ hipError_t launch_lora_group_bwd(const mc_lora_desc& d, const void* x, const Lor
             auto sc = prof::Scope(prof::kLowRank, st, flops, bytes);
             MC_TRY(launch_dy_pass(m.T, m.r, jobs, count, st));
             if (need_g)
-                MC_TRY(launch_dy_finish(m.T, m.r, d.scale, keep, m.rext, ext_ld, fin, count, preps, count, st));
+                MC_TRY(launch_dy_finish(m.T, m.r, d.scale, keep, m.rext, ext_ld, 1.0f, fin, count, preps, count, st));
         }
         if (dX) {
             for (int g = 0; g < count; ++g)
@@ -473,9 +537,35 @@ hipError_t launch_lora_group_bwd(const mc_lora_desc& d, const void* x, const Lor
             flops += 2.0 * m.T * Ns[g] * m.r;
         }
         auto sc = prof::Scope(prof::kLowRank, st, flops, bytes);
+        const bool split = bwd_rowsplit(m, Ns, count);
+        if (split) {
+            // G_g = s dY_g.B_g^T for every g in one split launch (B_g read as
+            // fp32), finished with the mask into Gd^T / Gd together with the
+            // A extension operands; W^T (when the caller holds none) by the
+            // transpose kernel
+            const int ld = rowsplit_ld(m.r);
+            RowsplitJob rj[kMaxProj];
+            DyFinishJob fin[kMaxProj];
+            PrepJob preps[kMaxProj];
+            for (int g = 0; g < count; ++g) {
+                const int S = rowsplit_splits(m.T, Ns[g]);
+                float* pp = reinterpret_cast<float*>(base + w.gpart[g]);
+                rj[g] = RowsplitJob{static_cast<const uint16_t*>(dY[g]), Ns[g], nullptr, nullptr, proj[g].B, m.r, pp, S};
+                fin[g] = DyFinishJob{pp, S, proj[g].mask, any_dA ? gdt + (size_t)g * m.r * m.T : nullptr,
+                                     dX ? gd + (size_t)g * m.rext : nullptr, ld, m.r};
+                preps[g] = dX ? prep_job(proj[g].A, m.r, m.K, m.r, false, at + (size_t)g * m.rext, nullptr, m.K, m.rext,
+                                         ext_ld)
+                              : PrepJob{};
+            }
+            MC_TRY(launch_rowsplit(m.T, m.r, rj, count, st));
+            MC_TRY(launch_dy_finish(m.T, m.r, d.scale, keep, m.rext, ext_ld, 1.0f, fin, count, preps, count, st));
+            if (dX)
+                for (int g = 0; g < count; ++g)
+                    if (need_wt[g]) MC_TRY(launch_transpose_bf16(proj[g].W, Ns[g], m.K, base + w.wt[g], st));
+        }
         // ranks in chunks of at most kRowprojMaxRanks (one pass over dY each);
         // the A extension and the W transposes ride with the first
-        for (int j0 = 0; j0 < m.r; j0 += kRowprojMaxRanks) {
+        for (int j0 = 0; j0 < m.r && !split; j0 += kRowprojMaxRanks) {
             const int rc = std::min(kRowprojMaxRanks, m.r - j0);
             const bool first = j0 == 0, last = j0 + rc == m.r;
             OperandsCall calls[kMaxProj];

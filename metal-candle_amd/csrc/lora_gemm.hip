@@ -72,32 +72,6 @@ __device__ __forceinline__ void tile_of(int pid, int tiles_m, int tiles_n, int g
     tn = r / gm;
 }
 
-// Loads rows [0, ROWS) x BK columns (k = kb .. kb+BK-1) of one operand tile
-// into the swizzled layout at lds_byte: a load moves RPI = 512/BK rows; each
-// wave issues ROWS/RPI/waves of them, split over PARTS calls (part p issues
-// loads p, p + PARTS, ...); lane l fetches the global chunk that the swizzle
-// places at row RPI i + l / CPR, slot l % CPR. Chunks at k >= ks load as
-// zeros.
-template <int ROWS, int NT, int BK, int PARTS = 1>
-__device__ __forceinline__ void dma_tile(i32x4 r, uint32_t lds_byte, uint32_t ld, uint32_t kb, uint32_t ks,
-                                         int tid, int part = 0) {
-    constexpr int CPR = BK / 8, RPI = 64 / CPR;
-    static_assert(ROWS % (RPI * (NT / 64)) == 0, "rows per wave");
-    constexpr int PER_WAVE = ROWS / RPI / (NT / 64);
-    static_assert(PER_WAVE >= 1, "rows per wave");
-    const int wave = tid >> 6, lane = tid & 63;
-#pragma unroll
-    for (int j = 0; j < PER_WAVE; ++j) {
-        if (j % PARTS != part) continue;  // part p issues loads p, p + PARTS, ...
-        const int blk = wave * PER_WAVE + j;
-        const int row = blk * RPI + lane / CPR;
-        const uint32_t k = kb + 8u * (uint32_t)swz<BK>(row, lane % CPR);
-        const uint32_t off = k < ks ? ((uint32_t)row * ld + k) * 2u : kOOB;
-        // the LDS address is wave-uniform: make it scalar for M0
-        dma16(r, __builtin_amdgcn_readfirstlane(lds_byte + (uint32_t)blk * 1024u), off);
-    }
-}
-
 // dma_tile for a full k-tile of rows with a fixed row stride: each lane's
 // VGPR offset (row * ld + swizzled chunk, in bytes) is precomputed once per
 // kernel (tile_offsets) and the k-tile's start kb * 2 goes in soffset, so a

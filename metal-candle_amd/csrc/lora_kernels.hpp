@@ -142,20 +142,55 @@ struct DyJob {
     float* gpart;
 };
 hipError_t launch_dy_pass(int64_t T, int r, const DyJob* jobs, int n, hipStream_t stream);
-// G = scale * sum_g gpart[g][t][j] per projection, then the dropout of the
-// rank-r hidden (mask [T][r] or null; keep = 1/(1-p)): Gd^T -> gd_t fp32
-// [r][T] (may be null) and Gd -> gd_ext bf16 columns 0..r-1 of rows of
-// ext_ld elements, columns r..rext-1 zeroed (may be null); the PrepJobs
-// (the A extension operands) run in the same launch.
+// Finishing of rank-r partials (r <= kFinishMaxRank): v = scale * sum_g
+// gpart[g][t][j] per projection (partials of token t at gpart + g T ld +
+// t ld, ld = r when 0), then the dropout of the rank-r hidden (mask rows of
+// mask_ld elements, or null; keep = 1/(1-p)): v^T -> gd_t fp32 [r][T] (may
+// be null) and ext_scale v -> gd_ext bf16 columns 0..r-1 of rows of ext_ld
+// elements, columns r..rext-1 zeroed (may be null); the PrepJobs (the A
+// extension operands) run in the same launch. It finishes both the fused
+// dY pass's G and the split row projection's H / G.
+constexpr int kFinishMaxRank = 64;
 struct DyFinishJob {
     const float* gpart;
     int groups;
     const uint8_t* mask;
     float* gd_t;
     uint16_t* gd_ext;
+    int64_t ld = 0;
+    int64_t mask_ld = 0;
 };
-hipError_t launch_dy_finish(int64_t T, int r, float scale, float keep, int rext, int ext_ld,
+hipError_t launch_dy_finish(int64_t T, int r, float scale, float keep, int rext, int ext_ld, float ext_scale,
                             const DyFinishJob* jobs, int n, const PrepJob* preps, int npreps, hipStream_t stream);
+
+// ------------------------------------------------- split row projection
+// The row projection of a pass of up to 64 ranks (r) as a skinny GEMM: each
+// workgroup streams kRowsplitRows token rows of X [T][C] and the parameter
+// through LDS for one column split, so the parameter is fetched once per
+// kRowsplitRows rows. Job i writes part[s][t][16 ceil(r / 16)] (fp32) for its
+// splits s < splits, finished by launch_dy_finish (groups = splits, ld =
+// 16 ceil(r / 16)). The parameter is bf16 hi / lo [prows][C] (P_hi, P_lo) or
+// fp32 [prows][C] (P_f32, split into hi / lo in registers; every job of a
+// launch the same kind); rows past prows and past r contribute zeros. Jobs
+// with the same X, C and splits run their tiles interleaved, so the reads of
+// one x block by several parameters meet in one L2.
+struct RowsplitJob {
+    const uint16_t* X;
+    int64_t C;
+    const uint16_t* P_hi;
+    const uint16_t* P_lo;
+    const float* P_f32;
+    int prows;
+    float* part;
+    int splits;
+};
+constexpr int kRowsplitRanks = 64;
+constexpr int kRowsplitRows = 256;
+constexpr int kRowsplitMinCols = 256;
+inline int rowsplit_ld(int r) { return 16 * ((r + 15) / 16); }
+// splits of a job of C columns (C % 8 == 0)
+int rowsplit_splits(int64_t T, int64_t C);
+hipError_t launch_rowsplit(int64_t T, int r, const RowsplitJob* jobs, int n, hipStream_t stream);
 
 // One job: out = scale * sum_s partial[s][j][c] (s ascending) for j < r,
 // c < C, written to out[c*r + j] when transpose_out (dA [K][r]) else

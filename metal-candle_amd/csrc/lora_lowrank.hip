@@ -11,6 +11,10 @@
 //             fp32 parameter split into bf16 hi + lo (two MFMAs), so the
 //             parameter keeps ~16 mantissa bits. Dropout mask and 1/(1-p) are
 //             applied in the epilogue.
+//  rowsplit   the same products for passes of up to 64 ranks as a skinny
+//             GEMM through LDS: 256-row workgroups share each parameter
+//             stage, columns split over workgroups, partials finished (sum in
+//             split order, scale, mask, both output layouts) by dy_finish.
 //  colreduce  dA = x^T.Gd and dB = scale Hd^T.dY: reductions over tokens.
 //             The token dim is the MFMA K dim, but it is the strided dim of
 //             x / dY, so each lane loads an 8 x 8 bf16 block (8 rows, 16 B
@@ -672,10 +676,15 @@ __global__ __launch_bounds__(256) void dy_pass_bf16(int64_t T, DyBatch db) {
     }
 }
 
-// G finishing, one workgroup per 64 tokens of one projection: the column
-// groups' partials are summed in group order, scaled and masked; Gd goes to
-// gd_ext row-wise and, through LDS, to gd_t [r][T] in 64-token row segments.
-// Blocks past the projections' run the PrepJobs (grid-stride).
+// Finishing of rank-r partials, one workgroup per 64 tokens of one job: the
+// groups' (splits') partials are summed in group order, scaled and masked;
+// the result goes to gd_ext row-wise and, through LDS, to gd_t [r][T] in
+// 64-token row segments. A thread takes up to four quads (four consecutive
+// ranks of one token) and issues the loads of four groups for all of them
+// before adding (buffer loads: quads and groups past the end read zeros), so
+// each thread keeps 16 loads in flight. VEC: ld is a multiple of 4 and a quad
+// is one 16-byte load; otherwise four 4-byte loads, ranks past r zeroed.
+// Blocks past the jobs' run the PrepJobs (grid-stride).
 struct DyFinishBatch {
     DyFinishJob job[kMaxProj];
     PrepJob prep[kMaxProj];
@@ -683,9 +692,10 @@ struct DyFinishBatch {
     int64_t prep_start[kMaxProj + 1];
     int blocks_per_job;
     int r, rext, ext_ld;
-    float scale, keep;
+    float scale, keep, ext_scale;
 };
 
+template <bool VEC>
 __global__ __launch_bounds__(256) void dy_finish(int64_t T, DyFinishBatch fb) {
     const int b = (int)blockIdx.x;
     const int jobs_blocks = fb.njobs * fb.blocks_per_job;
@@ -699,37 +709,69 @@ __global__ __launch_bounds__(256) void dy_finish(int64_t T, DyFinishBatch fb) {
         }
         return;
     }
-    const DyFinishJob& J = fb.job[b / fb.blocks_per_job];
+    const DyFinishJob J = fb.job[b / fb.blocks_per_job];
     const int64_t t0 = (int64_t)(b % fb.blocks_per_job) * 64;
-    const int r = fb.r;
-    __shared__ float tt[32][65];  // [rank][token] for the transposed store
-    for (int idx = threadIdx.x; idx < 64 * r; idx += 256) {
-        const int tl = idx / r, j = idx % r;
+    const int r = fb.r, nq = (r + 3) / 4;
+    const int64_t ld = J.ld > 0 ? J.ld : r, mask_ld = J.mask_ld > 0 ? J.mask_ld : r;
+    const int64_t split_bytes = T * ld * 4;
+    __shared__ float tt[kFinishMaxRank][65];  // [rank][token] for the transposed store
+    uint32_t off[4];
+    bool valid[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int item = threadIdx.x + 256 * i, tl = item / nq, q = item % nq;
+        valid[i] = item < 64 * nq && t0 + tl < T;
+        off[i] = valid[i] ? (uint32_t)(((t0 + tl) * ld + 4 * q) * 4) : kOOB;
+    }
+    f32x4 v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int g0 = 0; g0 < J.groups; g0 += 4) {
+        __amdgpu_buffer_rsrc_t rs[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            rs[k] = make_rsrc(J.gpart + (int64_t)(g0 + k) * T * ld, g0 + k < J.groups ? split_bytes : 0);
+        f32x4 u[4][4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                if constexpr (VEC) {
+                    u[k][i] = __builtin_bit_cast(f32x4, buf_load16(rs[k], off[i]));
+                } else {
+                    const int q = (int)((threadIdx.x + 256 * i) % nq);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        u[k][i][e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                                    rs[k], 4 * q + e < r ? off[i] + 4 * e : kOOB, 0, 0));
+                }
+            }
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[i] += u[k][i];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int item = threadIdx.x + 256 * i, tl = item / nq, q = item % nq;
+        if (item >= 64 * nq) break;
         const int64_t t = t0 + tl;
-        float v = 0.f;
-        if (t < T) {
-            // groups in order, loads of eight issued together
-            const float* p = J.gpart + t * r + j;
-            const int64_t stride = T * r;
-            int g = 0;
-            for (; g + 8 <= J.groups; g += 8) {
-                float u[8];
 #pragma unroll
-                for (int k = 0; k < 8; ++k) u[k] = p[(int64_t)(g + k) * stride];
-#pragma unroll
-                for (int k = 0; k < 8; ++k) v += u[k];
+        for (int e = 0; e < 4; ++e) {
+            const int j = 4 * q + e;
+            if (j >= r) break;
+            float x = valid[i] ? v[i][e] * fb.scale : 0.f;
+            if (valid[i]) {
+                if (J.mask) x = J.mask[t * mask_ld + j] ? x * fb.keep : 0.f;
+                if (J.gd_ext) {
+                    uint16_t* eo = J.gd_ext + t * fb.ext_ld;
+                    eo[j] = f32_to_bf16(x * fb.ext_scale);
+                    if (j == r - 1)
+                        for (int z = r; z < fb.rext; ++z) eo[z] = 0;
+                }
             }
-            for (; g < J.groups; ++g) v += p[(int64_t)g * stride];
-            v *= fb.scale;
-            if (J.mask) v = J.mask[t * r + j] ? v * fb.keep : 0.f;
-            if (J.gd_ext) {
-                uint16_t* e = J.gd_ext + t * fb.ext_ld;
-                e[j] = f32_to_bf16(v);
-                if (j == r - 1)
-                    for (int z = r; z < fb.rext; ++z) e[z] = 0;
-            }
+            tt[j][tl] = x;
         }
-        tt[j][tl] = v;
     }
     if (!J.gd_t) return;  // uniform
     __syncthreads();
@@ -737,6 +779,174 @@ __global__ __launch_bounds__(256) void dy_finish(int64_t T, DyFinishBatch fb) {
         const int j = idx / 64, tl = idx % 64;
         if (t0 + tl < T) J.gd_t[(int64_t)j * T + t0 + tl] = tt[j][tl];
     }
+}
+
+// ------------------------------------------------- split row projection
+// The rank-r row projection of a pass of up to 64 ranks as a skinny GEMM
+// through LDS. Workgroup: 4 waves, BM = 64 RT token rows (wave w owns row
+// tiles w RT .. w RT + RT - 1 of 16 rows) and one column split
+// [c_begin, c_end) of one job. Every BK-column stage of x (BM rows) and of
+// the parameter (64 rank rows: bf16 hi and lo planes, or one fp32 plane of
+// the same size) goes from HBM / L2 into LDS with buffer_load ... lds, whole
+// 128-byte lines per lane group, in the XOR-swizzled row layout of the GEMM
+// kernels; a ring of three stages keeps two in flight while one is
+// multiplied. The four waves read the same parameter fragments from LDS, so
+// the parameter is fetched once per BM rows (once per 64 rows when each wave
+// loads its own, as rowproj_bf16 does). MFMA 16x16x32 with the parameter as
+// the A operand (rank rows) and x as the B operand (token columns):
+// accumulator q of lane l is rank 4 (l / 16) + q, token l % 16 of its tile,
+// so each lane stores four consecutive ranks of one token (16 bytes) of the
+// split's partials part[s][t][16 RC]. Rows past T and columns past the split
+// load as zeros through the buffer range checks.
+struct RowsplitJobDev {
+    const uint16_t* X;
+    int64_t C;
+    const void* P0;      // bf16 P_hi, or fp32 P
+    const uint16_t* P1;  // bf16 P_lo (unused for fp32)
+    int64_t pbytes;      // bytes of P0 (rows past them load as zeros)
+    float* part;
+    int splits;
+    int64_t cps;  // columns per split, a multiple of BK
+};
+struct RowsplitBatch {
+    RowsplitJobDev job[kMaxProj];
+    int64_t start[kMaxProj + 1];  // first tile of each job (job-major order)
+    int njobs;
+    int interleave;  // jobs share X, C and splits: tile l is job l % njobs
+    int64_t T;
+};
+
+template <int RT, int RC, int BK, bool PF32>
+__global__ __launch_bounds__(256) void rowsplit_bf16(RowsplitBatch b) {
+    constexpr int BM = 64 * RT;
+    constexpr int XB = BM * BK * 2;        // x stage bytes
+    constexpr int PB = 64 * BK * 2;        // one bf16 parameter plane; fp32 fills both
+    constexpr int SB = XB + 2 * PB;        // stage bytes
+    constexpr int PBK = PF32 ? 2 * BK : BK;  // parameter row length in bf16 units
+    constexpr int NL = (XB + 2 * PB) / 1024 / 4;  // loads per wave per stage
+    constexpr int KS = BK / 32;            // MFMA k-substeps per stage
+    constexpr int LD = 16 * RC;            // partial row length
+    static_assert(BK == 32 || BK == 64, "stage width");
+    __shared__ __attribute__((aligned(1024))) char smem[3 * SB];
+    const uint32_t smem_byte = (uint32_t)reinterpret_cast<uintptr_t>(smem);
+
+    // logical tile: each XCD (workgroup id % 8) owns a contiguous range, so
+    // the jobs of one (row block, split) that interleave shares x through
+    // one L2
+    const int total = (int)gridDim.x, pid = (int)blockIdx.x;
+    const int per = total / 8, rem = total % 8, xcd = pid % 8;
+    const int64_t l = (xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per) + pid / 8;
+    int j = 0;
+    int64_t u = 0;
+    if (b.interleave) {
+        j = (int)(l % b.njobs);
+        u = l / b.njobs;
+    } else {
+        while (j + 1 < b.njobs && l >= b.start[j + 1]) ++j;
+        u = l - b.start[j];
+    }
+    // every field of the job into registers before any LDS traffic (a
+    // scalar load's wait also waits for the LDS reads)
+    const RowsplitJobDev J = b.job[j];
+    const int64_t T = b.T;
+    const int64_t rb = u / J.splits, s = u % J.splits;
+    const int64_t t0 = rb * BM;
+    const int64_t nrows = T - t0 < BM ? T - t0 : BM;
+    const int64_t c_begin = s * J.cps;
+    const int64_t c_end = c_begin + J.cps < J.C ? c_begin + J.cps : J.C;
+    const int nst = c_end > c_begin ? (int)((c_end - c_begin + BK - 1) / BK) : 0;
+    const i32x4 rx = rsrc_words(J.X + t0 * J.C, nrows * J.C * 2);
+    const i32x4 rp0 = rsrc_words(J.P0, J.pbytes);
+    const i32x4 rp1 = rsrc_words(PF32 ? J.P0 : (const void*)J.P1, PF32 ? 0 : J.pbytes);
+    const uint32_t ldx = (uint32_t)J.C, ldp = (uint32_t)(PF32 ? 2 * J.C : J.C);
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    auto issue = [&](int st) {
+        const uint32_t base = smem_byte + (uint32_t)((st % 3) * SB);
+        const uint32_t kb = (uint32_t)(c_begin + (int64_t)st * BK), ke = (uint32_t)c_end;
+        dma_tile<BM, 256, BK>(rx, base, ldx, kb, ke, tid);
+        if constexpr (PF32) {
+            dma_tile<64, 256, PBK>(rp0, base + XB, ldp, 2 * kb, 2 * ke, tid);
+        } else {
+            dma_tile<64, 256, BK>(rp0, base + XB, ldp, kb, ke, tid);
+            dma_tile<64, 256, BK>(rp1, base + XB + PB, ldp, kb, ke, tid);
+        }
+    };
+
+    f32x4 acc[RT][RC];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int rc = 0; rc < RC; ++rc) acc[rt][rc] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    // fragment rows of a lane differ by multiples of 16, so the swizzle term
+    // depends on the lane only
+    const int fr = lane & 15, kc = lane >> 4;
+    const int swx = (fr / (128 / BK)) % (BK / 8);
+    const int swp = (fr / (128 / PBK)) % (PBK / 8);
+
+    if (nst > 0) issue(0);
+    if (nst > 1) issue(1);
+    for (int st = 0; st < nst; ++st) {
+        if (st + 1 < nst) wait_vmcnt<NL>();  // stage st + 1 may stay in flight
+        else wait_vmcnt<0>();
+        __syncthreads();  // stage st visible to every wave; stage st - 1 free
+        if (st + 2 < nst) issue(st + 2);
+        const char* sx = smem + (st % 3) * SB;
+        const char* sp = sx + XB;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            const int chunk = 4 * ks + kc;
+            bf16x8 xf[RT], ph[RC], pl[RC];
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) {
+                const int row = (wave * RT + rt) * 16 + fr;
+                xf[rt] = *reinterpret_cast<const bf16x8*>(sx + row * (BK * 2) + ((chunk ^ swx) * 16));
+            }
+#pragma unroll
+            for (int rc = 0; rc < RC; ++rc) {
+                const int prow = rc * 16 + fr;
+                if constexpr (PF32) {
+                    const char* pr = sp + prow * (PBK * 2);
+                    const f32x4 a = *reinterpret_cast<const f32x4*>(pr + (((2 * chunk) ^ swp) * 16));
+                    const f32x4 c = *reinterpret_cast<const f32x4*>(pr + (((2 * chunk + 1) ^ swp) * 16));
+                    float v[8], rem8[8];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        v[e] = a[e];
+                        v[4 + e] = c[e];
+                    }
+                    ph[rc] = pack_bf16x8(v);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) rem8[e] = v[e] - static_cast<float>(ph[rc][e]);
+                    pl[rc] = pack_bf16x8(rem8);
+                } else {
+                    const int off = prow * (BK * 2) + ((chunk ^ swx) * 16);
+                    ph[rc] = *reinterpret_cast<const bf16x8*>(sp + off);
+                    pl[rc] = *reinterpret_cast<const bf16x8*>(sp + PB + off);
+                }
+            }
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+                for (int rc = 0; rc < RC; ++rc) {
+                    acc[rt][rc] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ph[rc], xf[rt], acc[rt][rc], 0, 0, 0);
+                    acc[rt][rc] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pl[rc], xf[rt], acc[rt][rc], 0, 0, 0);
+                }
+        }
+    }
+
+    // partials: lane l of tile (rt, rc) holds ranks rc 16 + 4 (l / 16) + q of
+    // token (wave RT + rt) 16 + l % 16; rows past T fall outside the range
+    const __amdgpu_buffer_rsrc_t ro = make_rsrc(J.part + ((int64_t)s * T + t0) * LD, nrows * LD * 4);
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int rc = 0; rc < RC; ++rc) {
+            const int t = (wave * RT + rt) * 16 + fr;
+            const i32x4 q = __builtin_bit_cast(i32x4, acc[rt][rc]);
+            __builtin_amdgcn_raw_buffer_store_b128(q, ro, (int)((t * LD + rc * 16 + 4 * kc) * 4), 0, 0);
+        }
 }
 
 // -------------------------------------------------------- bf16 transpose
@@ -1110,10 +1320,11 @@ hipError_t launch_dy_pass(int64_t T, int r, const DyJob* jobs, int n, hipStream_
     return hipGetLastError();
 }
 
-hipError_t launch_dy_finish(int64_t T, int r, float scale, float keep, int rext, int ext_ld,
+hipError_t launch_dy_finish(int64_t T, int r, float scale, float keep, int rext, int ext_ld, float ext_scale,
                             const DyFinishJob* jobs, int n, const PrepJob* preps, int npreps, hipStream_t stream) {
+    if (r < 1 || r > kFinishMaxRank) return hipErrorInvalidValue;
     DyFinishBatch fb{};
-    fb.r = r; fb.rext = rext; fb.ext_ld = ext_ld; fb.scale = scale; fb.keep = keep;
+    fb.r = r; fb.rext = rext; fb.ext_ld = ext_ld; fb.scale = scale; fb.keep = keep; fb.ext_scale = ext_scale;
     fb.blocks_per_job = (int)((T + 63) / 64);
     for (int i = 0; i < n && fb.njobs < kMaxProj; ++i)
         if (jobs[i].gpart && (jobs[i].gd_t || jobs[i].gd_ext)) fb.job[fb.njobs++] = jobs[i];
@@ -1129,8 +1340,86 @@ hipError_t launch_dy_finish(int64_t T, int r, float scale, float keep, int rext,
     const int64_t prep_blocks = prep_n > 0 ? std::min<int64_t>((prep_n + 255) / 256, 512) : 0;
     const int64_t blocks = (int64_t)fb.njobs * fb.blocks_per_job + prep_blocks;
     if (blocks == 0) return hipSuccess;
-    dy_finish<<<dim3((unsigned)blocks), 256, 0, stream>>>(T, fb);
+    for (int i = 0; i < fb.njobs; ++i)  // one split of a job is one buffer resource
+        if (T * (fb.job[i].ld > 0 ? fb.job[i].ld : r) * 4 >= ((int64_t)1 << 31)) return hipErrorInvalidValue;
+    bool vec = true;
+    for (int i = 0; i < fb.njobs; ++i) {
+        const int64_t ld = fb.job[i].ld > 0 ? fb.job[i].ld : r;
+        vec = vec && ld % 4 == 0 && reinterpret_cast<uintptr_t>(fb.job[i].gpart) % 16 == 0;
+    }
+    if (vec) dy_finish<true><<<dim3((unsigned)blocks), 256, 0, stream>>>(T, fb);
+    else dy_finish<false><<<dim3((unsigned)blocks), 256, 0, stream>>>(T, fb);
     return hipGetLastError();
+}
+
+// Splits of a rowsplit job of C columns: the smallest count whose row blocks
+// x splits fill whole rounds of 256 CUs (or three rounds), with at least
+// kRowsplitMinCols columns per split (each split adds a T x 16 ceil(r / 16)
+// partial that is written and read back). The count depends on T and C
+// only, so every job over the same x splits alike. Measured on the c5 shapes
+// (T = 16384: 64 row blocks, 4 splits): one 64-rank pass of 3584 or 18944
+// columns ran fastest at 4 splits, and the three q / k / v passes together
+// as well (2 and 3 splits were slower, 8 no faster).
+int rowsplit_splits(int64_t T, int64_t C) {
+    const int64_t rb = (T + kRowsplitRows - 1) / kRowsplitRows;
+    const int64_t max_s = C / kRowsplitMinCols > 1 ? C / kRowsplitMinCols : 1;
+    int64_t s = 1;
+    while (s < max_s) {
+        const int64_t w = rb * s;
+        if (w >= 768 || (w >= 256 && w % 256 == 0)) break;
+        ++s;
+    }
+    return (int)s;
+}
+
+namespace {
+template <int RC>
+hipError_t rowsplit_go(const RowsplitBatch& b, bool pf32, int64_t tiles, hipStream_t stream) {
+    // bf16 parameter: 64-column stages (144 KB of LDS, one workgroup per
+    // CU); fp32 parameter: 32-column stages (72 KB, two per CU), which
+    // measured faster for each
+    const dim3 grid((unsigned)tiles);
+    if (pf32) rowsplit_bf16<4, RC, 32, true><<<grid, 256, 0, stream>>>(b);
+    else rowsplit_bf16<4, RC, 64, false><<<grid, 256, 0, stream>>>(b);
+    return hipGetLastError();
+}
+}  // namespace
+
+hipError_t launch_rowsplit(int64_t T, int r, const RowsplitJob* jobs, int n, hipStream_t stream) {
+    if (n < 1 || n > kMaxProj || r < 1 || r > kRowsplitRanks) return hipErrorInvalidValue;
+    const bool pf32 = jobs[0].P_f32 != nullptr;
+    const int BK = pf32 ? 32 : 64;
+    RowsplitBatch b{};
+    b.njobs = n;
+    b.T = T;
+    b.interleave = 1;
+    const int64_t rblocks = (T + kRowsplitRows - 1) / kRowsplitRows;
+    int64_t tiles = 0;
+    for (int i = 0; i < n; ++i) {
+        const RowsplitJob& s = jobs[i];
+        // x rows of a workgroup are one buffer resource with 32-bit offsets
+        if ((s.P_f32 != nullptr) != pf32 || s.splits < 1 || s.C < 1 || s.C % 8 != 0 || s.C >= ((int64_t)1 << 22))
+            return hipErrorInvalidValue;
+        RowsplitJobDev& d = b.job[i];
+        d.X = s.X; d.C = s.C;
+        d.P0 = pf32 ? (const void*)s.P_f32 : (const void*)s.P_hi;
+        d.P1 = s.P_lo;
+        d.pbytes = (int64_t)s.prows * s.C * (pf32 ? 4 : 2);
+        d.part = s.part;
+        d.splits = s.splits;
+        d.cps = ((s.C + s.splits - 1) / s.splits + BK - 1) / BK * BK;
+        b.start[i] = tiles;
+        tiles += rblocks * s.splits;
+        if (s.X != jobs[0].X || s.C != jobs[0].C || s.splits != jobs[0].splits) b.interleave = 0;
+    }
+    b.start[n] = tiles;
+    if (tiles == 0) return hipSuccess;
+    switch ((r + 15) / 16) {
+        case 1: return rowsplit_go<1>(b, pf32, tiles, stream);
+        case 2: return rowsplit_go<2>(b, pf32, tiles, stream);
+        case 3: return rowsplit_go<3>(b, pf32, tiles, stream);
+        default: return rowsplit_go<4>(b, pf32, tiles, stream);
+    }
 }
 
 hipError_t launch_rowproj_f32(const float* X, int64_t T, int64_t C, const float* P, bool transpose_p,

@@ -159,6 +159,23 @@ def test_config5_dropout_bf16(mc, dev):
     _check(mc, dev, c, 2.0, BF16_TOL, mask=mask, p=0.1, sample_rows=256)
 
 
+@pytest.mark.parametrize("name,T,K,N,r,p", [
+    # projections of 33-64 ranks take the split row projection (256-row
+    # workgroups, column splits, a finishing pass) both ways (fp32 B in the
+    # backward), and in the forward so do those of >= 4096 columns: ragged T
+    # and last split, 33 and 40 ranks (zero rows in the last 16-rank tile),
+    # rank 8 over 4608 columns, more splits than columns (empty splits)
+    ("rank 40, ragged T and split, dropout", 3000, 1000, 264, 40, 0.1),
+    ("rank 33, 4104 columns", 517, 4104, 96, 33, 0.0),
+    ("rank 8, 4608 columns, dropout", 700, 4608, 4160, 8, 0.2),
+    ("rank 64, dY of 4104 columns", 1100, 520, 4104, 64, 0.0),
+])
+def test_split_row_projection(mc, dev, name, T, K, N, r, p):
+    c = lora_case(zlib.crc32(name.encode()), T, K, N, r)
+    mask = mc.dropout_mask(zlib.crc32(name.encode()), p, T, r).numpy() if p > 0 else None
+    _check(mc, dev, c, 2.0, BF16_TOL, mask=mask, p=p, sample_rows=256)
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_dropout_mask_semantics(mc, dev, dtype):
     """Masked hidden entries are exactly zero; kept ones scaled by 1/(1-p)."""

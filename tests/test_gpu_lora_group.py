@@ -96,6 +96,9 @@ def _check_group(mc, dev, T, K, Ns, r, p, seed, scale=2.0, bias=True, no_w=(), s
     ("four projections r8", 4096, 512, [512, 128, 384, 64], 8, 0.0),
     ("r32 pair", 2048, 896, [896, 128], 32, 0.2),
     ("r150 pair dropout (rank passes of 128 + 22)", 2048, 512, [512, 136], 150, 0.1),
+    # split row projection (K >= 4096) over passes of 48 + 24 ranks (one
+    # launch, the second pass's operand 32 rows), ragged T, dropout
+    ("r24 three projections, passes of 48 + 24", 2000, 4104, [136, 264, 72], 24, 0.1),
 ])
 def test_group_matches_single_calls(mc, dev, name, T, K, Ns, r, p):
     _check_group(mc, dev, T, K, Ns, r, p, zlib.crc32(name.encode()) % 1000)
