@@ -76,7 +76,8 @@ struct LoraGroupBwdWs {
     size_t wt[kLoraMaxProj];       // per projection with W and no caller W^T: bf16 [K][N_g] W_g^T
     size_t at_ext;                 // bf16 [K][G rext]: A of every projection
     size_t gd_ext;                 // bf16 [T][G rext]: Gd of every projection
-    size_t gd_t;                   // f32 [G r][T]: Gd^T of every projection
+    size_t gd_t;                   // f32 [G r][T]: Gd^T of every projection (or bf16 hi / lo planes [2][G r][T])
+    size_t hd_hilo;                // column-split path: bf16 [2][G r][T] hi / lo planes of every Hd_g^T
     size_t part_a;                 // f32 [S_a][colreduce rows of G r][K]
     size_t part_b[kLoraMaxProj];   // f32 [S_b][colreduce rows of r][N_g]
     size_t gpart[kLoraMaxProj];    // G partials: f32 [column groups of N_g][T][r] of the fused dY pass, or

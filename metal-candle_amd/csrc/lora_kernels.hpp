@@ -118,6 +118,21 @@ struct ColJob {
 };
 int colreduce_splits(int64_t T, int64_t C);
 hipError_t launch_colreduce_bf16(int64_t T, const ColJob* jobs, int n, hipStream_t stream);
+// The same column reductions with the token-side operand as bf16 hi / lo
+// planes [r][T] (P_hi + P_lo = Pt to ~16 mantissa bits, split once by the
+// producer) through an LDS ring shared by 512-column workgroups; T % 8 == 0.
+// Partials in ColJob's layout: [splits][colreduce_rows(r)][C].
+struct ColsplitJob {
+    const uint16_t* X;
+    int64_t C;
+    const uint16_t* P_hi;
+    const uint16_t* P_lo;
+    int r;
+    int splits;
+    float* partial;
+};
+int colsplit_splits(int64_t T, int64_t C);
+hipError_t launch_colsplit_bf16(int64_t T, const ColsplitJob* jobs, int n, hipStream_t stream);
 // ------------------------------------------------ fused dY pass (r <= 32)
 // One read of a projection's dY [T][N] gives both rank-r products of the
 // backward that reduce it:
@@ -145,11 +160,12 @@ hipError_t launch_dy_pass(int64_t T, int r, const DyJob* jobs, int n, hipStream_
 // Finishing of rank-r partials (r <= kFinishMaxRank): v = scale * sum_g
 // gpart[g][t][j] per projection (partials of token t at gpart + g T ld +
 // t ld, ld = r when 0), then the dropout of the rank-r hidden (mask rows of
-// mask_ld elements, or null; keep = 1/(1-p)): v^T -> gd_t fp32 [r][T] (may
-// be null) and ext_scale v -> gd_ext bf16 columns 0..r-1 of rows of ext_ld
-// elements, columns r..rext-1 zeroed (may be null); the PrepJobs (the A
-// extension operands) run in the same launch. It finishes both the fused
-// dY pass's G and the split row projection's H / G.
+// mask_ld elements, or null; keep = 1/(1-p)): v^T -> gd_t fp32 [r][T] and /
+// or bf16 hi / lo planes gd_hi, gd_lo [r][T] (each may be null) and
+// ext_scale v -> gd_ext bf16 columns 0..r-1 of rows of ext_ld elements,
+// columns r..rext-1 zeroed (may be null); up to kPrepJobs PrepJobs (operand
+// preparation) run in the same launch. It finishes both the fused dY pass's
+// G and the split row projection's H / G.
 constexpr int kFinishMaxRank = 64;
 struct DyFinishJob {
     const float* gpart;
@@ -159,6 +175,8 @@ struct DyFinishJob {
     uint16_t* gd_ext;
     int64_t ld = 0;
     int64_t mask_ld = 0;
+    uint16_t* gd_hi = nullptr;  // v^T as bf16 hi / lo planes [r][T] (both or neither)
+    uint16_t* gd_lo = nullptr;
 };
 hipError_t launch_dy_finish(int64_t T, int r, float scale, float keep, int rext, int ext_ld, float ext_scale,
                             const DyFinishJob* jobs, int n, const PrepJob* preps, int npreps, hipStream_t stream);

@@ -85,19 +85,50 @@ __device__ __forceinline__ void prep_one(const PrepJob& j, int64_t idx) {
     if (j.lo) j.lo[o] = f32_to_bf16(v - bf16_to_f32(h));
 }
 
+// Eight consecutive output columns 8 g' .. +7 of one output row (g' the
+// group within the row): one division per eight elements and 16-byte stores
+// of hi and lo. Used when every job of a batch has cols_out and ld_out
+// multiples of 8 and 16-byte aligned outputs (prep_vec8).
+__device__ __forceinline__ void prep_one8(const PrepJob& j, int64_t g) {
+    const int64_t cg = j.cols_out >> 3;
+    const int64_t i = g / cg, c0 = (g - i * cg) * 8;
+    const bool row_ok = i < j.valid_rows;
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const int64_t c = c0 + e;
+        const bool ok = row_ok && c < j.valid_cols;
+        const float x = j.src[ok ? (j.transpose ? c * j.ld_src + i : i * j.ld_src + c) : 0];  // an in-range address
+        v[e] = ok ? x : 0.f;
+    }
+    uint4 hi, lo;
+    split_hilo8(v, hi, lo);
+    const int64_t o = i * j.ld_out + c0;
+    *reinterpret_cast<uint4*>(j.hi + o) = hi;
+    if (j.lo) *reinterpret_cast<uint4*>(j.lo + o) = lo;
+}
+
+bool prep_vec8(const PrepJob& j) {
+    // prep_one8 reads src[0] for the zero elements: src must exist
+    return j.src && j.cols_out % 8 == 0 && j.ld_out % 8 == 0 && reinterpret_cast<uintptr_t>(j.hi) % 16 == 0 &&
+           reinterpret_cast<uintptr_t>(j.lo) % 16 == 0;
+}
+
 struct PrepBatch {
     PrepJob job[kPrepJobs];
-    int64_t start[kPrepJobs + 1];
+    int64_t start[kPrepJobs + 1];  // in elements, or in 8-element groups (vec8)
     int njobs;
 };
 
+template <bool VEC8>
 __global__ __launch_bounds__(256) void prep_bf16(PrepBatch b) {
     const int64_t n = b.start[b.njobs];
     for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < n;
          idx += (int64_t)gridDim.x * blockDim.x) {
         int j = 0;
         while (j + 1 < b.njobs && idx >= b.start[j + 1]) ++j;
-        prep_one(b.job[j], idx - b.start[j]);
+        if constexpr (VEC8) prep_one8(b.job[j], idx - b.start[j]);
+        else prep_one(b.job[j], idx - b.start[j]);
     }
 }
 
@@ -422,6 +453,135 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void c
     }
 }
 
+// ------------------------------------------------------------- colsplit
+// The column reduction of a group of up to 64 ranks with the token-side
+// operand given as bf16 hi / lo planes [rows][T] (Gd^T or Hd^T split once,
+// so the loop does no fp32 splitting). Workgroup: 4 waves over 512 columns
+// (wave w: columns c0 + 128 w .. +127) and the token range of one split,
+// walked in 32-token stages; each stage of x (32 rows x 512 columns, plain
+// row-major rows of 1 KB) and of both planes (64 rank rows x 32 tokens, the
+// GEMM kernels' swizzled layout) goes into LDS with buffer_load ... lds, in
+// a ring of three stages (two in flight while one is multiplied), so a CU
+// keeps 80 KB of loads outstanding. Lane l reads rows 8 (l/16) + i (i < 8)
+// of its wave's columns 8 (l%16) .. +7 from LDS, transposes the 8 x 8 block
+// in registers and feeds colreduce_bf16's MFMAs; the planes' fragments are
+// shared by the four waves. Rows past the split and columns past C load as
+// zeros (buffer range checks), and so do plane tokens past the split (whole
+// 8-token chunks: T % 8 == 0 and splits of whole stages).
+struct ColsplitJobDev {
+    const uint16_t* X;
+    int64_t C;
+    const uint16_t* Phi;
+    const uint16_t* Plo;
+    int r;
+    int64_t chunk;
+    float* partial;
+    int64_t part_stride;
+    int ctiles;
+    int splits;  // every split writes its partial (splits past T write zeros)
+};
+struct ColsplitBatch {
+    ColsplitJobDev job[kColJobs];
+    int start[kColJobs + 1];  // first workgroup of each job
+    int njobs;
+};
+
+template <int RC>
+__global__ __launch_bounds__(256) void colsplit_bf16(int64_t T, ColsplitBatch cb) {
+    constexpr int TOK = 32, BCOLS = 512;
+    constexpr int XB = TOK * BCOLS * 2, PB = 64 * TOK * 2, SB = XB + 2 * PB;
+    constexpr int NL = (XB + 2 * PB) / 1024 / 4;  // loads per wave per stage
+    __shared__ __attribute__((aligned(1024))) char smem[3 * SB];
+    const uint32_t sbyte = (uint32_t)reinterpret_cast<uintptr_t>(smem);
+    int ji = 0;
+    while (ji + 1 < cb.njobs && (int)blockIdx.x >= cb.start[ji + 1]) ++ji;  // wave-uniform
+    // the job's fields into registers before any LDS traffic (a scalar
+    // load's wait also waits for the LDS reads)
+    const ColsplitJobDev J = cb.job[ji];
+    const int b = (int)blockIdx.x - cb.start[ji];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t C = J.C;
+    const int64_t cb0 = (int64_t)(b % J.ctiles) * BCOLS;
+    const int64_t split = b / J.ctiles;
+    const int64_t tb = split * J.chunk;
+    const int64_t te = tb + J.chunk < T ? tb + J.chunk : T;
+    const int nst = te > tb ? (int)((te - tb + TOK - 1) / TOK) : 0;
+    const i32x4 rx = rsrc_words(J.X + tb * C, (te - tb) * C * 2);
+    const i32x4 rh = rsrc_words(J.Phi, (int64_t)J.r * T * 2);
+    const i32x4 rl = rsrc_words(J.Plo, (int64_t)J.r * T * 2);
+    // x: DMA k of wave w moves tile row 8 w + k (1 KB), lane l its chunk l
+    const bool xc_ok = cb0 + 8 * lane < C;
+    auto issue = [&](int st) {
+        const uint32_t base = sbyte + (uint32_t)((st % 3) * SB);
+        const int64_t t0 = tb + (int64_t)st * TOK;
+#pragma unroll
+        for (int k = 0; k < XB / 1024 / 4; ++k) {
+            const int row = wave * (XB / 1024 / 4) + k;
+            const uint32_t off = xc_ok ? (uint32_t)(((t0 - tb + row) * C + cb0 + 8 * lane) * 2) : kOOB;
+            dma16(rx, __builtin_amdgcn_readfirstlane(base + (uint32_t)row * 1024u), off);
+        }
+        dma_tile<64, 256, TOK>(rh, base + XB, (uint32_t)T, (uint32_t)t0, (uint32_t)te, tid);
+        dma_tile<64, 256, TOK>(rl, base + XB + PB, (uint32_t)T, (uint32_t)t0, (uint32_t)te, tid);
+    };
+
+    f32x4 acc[8][RC];
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+#pragma unroll
+        for (int rc = 0; rc < RC; ++rc) acc[e][rc] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int g8 = 8 * (lane >> 4);
+    const int psw = ((lane & 15) / (128 / TOK)) % (TOK / 8);  // swizzle term of plane rows rc 16 + l % 16
+
+    if (nst > 0) issue(0);
+    if (nst > 1) issue(1);
+    for (int st = 0; st < nst; ++st) {
+        if (st + 1 < nst) wait_vmcnt<NL>();  // stage st + 1 may stay in flight
+        else wait_vmcnt<0>();
+        __syncthreads();  // stage st visible to every wave; stage st - 1 free
+        if (st + 2 < nst) issue(st + 2);
+        const char* sx = smem + (st % 3) * SB;
+        const char* sp = sx + XB;
+        uint4 R[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            R[i] = *reinterpret_cast<const uint4*>(sx + (g8 + i) * (BCOLS * 2) + (wave * 16 + (lane & 15)) * 16);
+        bf16x8 ahi[RC], alo[RC];
+#pragma unroll
+        for (int rc = 0; rc < RC; ++rc) {
+            const int off = (rc * 16 + (lane & 15)) * (TOK * 2) + (((lane >> 4) ^ psw) * 16);
+            ahi[rc] = *reinterpret_cast<const bf16x8*>(sp + off);
+            alo[rc] = *reinterpret_cast<const bf16x8*>(sp + PB + off);
+        }
+        uint4 Bt[8];
+        transpose8x8(R, Bt);
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+#pragma unroll
+            for (int rc = 0; rc < RC; ++rc) {
+                acc[e][rc] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ahi[rc], as_bf16x8(Bt[e]), acc[e][rc], 0, 0, 0);
+                acc[e][rc] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(alo[rc], as_bf16x8(Bt[e]), acc[e][rc], 0, 0, 0);
+            }
+    }
+
+    // accumulator q of lane l, MFMA e: rank rc 16 + 4 (l/16) + q, column
+    // 8 (l%16) + e of the wave's 128
+    const int64_t col = cb0 + 128 * wave + 8 * (lane & 15);
+    if (col < C) {
+        float* out = J.partial + split * J.part_stride;
+#pragma unroll
+        for (int rc = 0; rc < RC; ++rc)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int j = rc * 16 + (lane >> 4) * 4 + q;
+                if (j >= J.r) continue;
+#pragma unroll
+                for (int e = 0; e < 8; e += 4)
+                    *reinterpret_cast<float4*>(out + (int64_t)j * C + col + e) =
+                        make_float4(acc[e][rc][q], acc[e + 1][rc][q], acc[e + 2][rc][q], acc[e + 3][rc][q]);
+            }
+    }
+}
+
 // out = scale * sum_s partial[s][j][c] (s ascending) for up to two jobs
 // (threads [0, n0) job 0). Splits are unrolled by 8 so that their loads are
 // in flight together; the adds stay in split order.
@@ -445,19 +605,52 @@ __device__ __forceinline__ void split_sum_one(const SumJob& J, int64_t idx) {
     else J.out[j * J.C + c] = s;
 }
 
+// Four consecutive columns of one row (C % 4 == 0, 16-byte aligned
+// partials and, for the untransposed output, out): the 16-byte loads of
+// eight splits are issued together (splits past the job's read zeros through
+// an empty buffer range), and each column's adds stay in split order, so the
+// sums equal split_sum_one's.
+__device__ __forceinline__ void split_sum_four(const SumJob& J, int64_t g) {
+    const int64_t cq = J.C >> 2;
+    const int64_t j = g / cq, c0 = (g - j * cq) * 4;
+    const uint32_t off = (uint32_t)((j * J.C + c0) * 4);
+    const int64_t split_bytes = J.part_stride * 4;
+    f32x4 s = {0.f, 0.f, 0.f, 0.f};
+    for (int k0 = 0; k0 < J.splits; k0 += 8) {
+        f32x4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const __amdgpu_buffer_rsrc_t rs =
+                make_rsrc(J.partial + (int64_t)(k0 + u) * J.part_stride, k0 + u < J.splits ? split_bytes : 0);
+            v[u] = __builtin_bit_cast(f32x4, buf_load16(rs, off));
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) s += v[u];
+    }
+    s *= J.scale;
+    if (J.transpose_out) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) J.out[(c0 + e) * J.r + j] = s[e];
+    } else {
+        *reinterpret_cast<f32x4*>(J.out + j * J.C + c0) = s;
+    }
+}
+
 struct SumBatch {
     SumJob job[kSumJobs];
-    int64_t start[kSumJobs + 1];
+    int64_t start[kSumJobs + 1];  // in elements, or in 4-column groups (vec4)
     int njobs;
 };
 
+template <bool VEC4>
 __global__ __launch_bounds__(256) void split_sum(SumBatch sb) {
     const int64_t n = sb.start[sb.njobs];
     for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < n;
          idx += (int64_t)gridDim.x * blockDim.x) {
         int j = 0;
         while (j + 1 < sb.njobs && idx >= sb.start[j + 1]) ++j;
-        split_sum_one(sb.job[j], idx - sb.start[j]);
+        if constexpr (VEC4) split_sum_four(sb.job[j], idx - sb.start[j]);
+        else split_sum_one(sb.job[j], idx - sb.start[j]);
     }
 }
 
@@ -687,9 +880,10 @@ __global__ __launch_bounds__(256) void dy_pass_bf16(int64_t T, DyBatch db) {
 // Blocks past the jobs' run the PrepJobs (grid-stride).
 struct DyFinishBatch {
     DyFinishJob job[kMaxProj];
-    PrepJob prep[kMaxProj];
+    PrepJob prep[kPrepJobs];
     int njobs, npreps;
-    int64_t prep_start[kMaxProj + 1];
+    int64_t prep_start[kPrepJobs + 1];  // in elements, or in 8-element groups (prep_vec8)
+    int prep8;
     int blocks_per_job;
     int r, rext, ext_ld;
     float scale, keep, ext_scale;
@@ -705,7 +899,8 @@ __global__ __launch_bounds__(256) void dy_finish(int64_t T, DyFinishBatch fb) {
         for (int64_t idx = (int64_t)(b - jobs_blocks) * 256 + threadIdx.x; idx < n; idx += nb * 256) {
             int j = 0;
             while (j + 1 < fb.npreps && idx >= fb.prep_start[j + 1]) ++j;
-            prep_one(fb.prep[j], idx - fb.prep_start[j]);
+            if (fb.prep8) prep_one8(fb.prep[j], idx - fb.prep_start[j]);
+            else prep_one(fb.prep[j], idx - fb.prep_start[j]);
         }
         return;
     }
@@ -773,12 +968,34 @@ __global__ __launch_bounds__(256) void dy_finish(int64_t T, DyFinishBatch fb) {
             tt[j][tl] = x;
         }
     }
-    if (!J.gd_t) return;  // uniform
+    if (!J.gd_t && !J.gd_hi) return;  // uniform
     __syncthreads();
-    for (int idx = threadIdx.x; idx < 64 * r; idx += 256) {
-        const int j = idx / 64, tl = idx % 64;
-        if (t0 + tl < T) J.gd_t[(int64_t)j * T + t0 + tl] = tt[j][tl];
-    }
+    if (J.gd_t)
+        for (int idx = threadIdx.x; idx < 64 * r; idx += 256) {
+            const int j = idx / 64, tl = idx % 64;
+            if (t0 + tl < T) J.gd_t[(int64_t)j * T + t0 + tl] = tt[j][tl];
+        }
+    if (J.gd_hi)  // two tokens per thread: 4-byte stores of each plane
+        for (int idx = threadIdx.x; idx < 32 * r; idx += 256) {
+            const int j = idx / 32, tl = 2 * (idx % 32);
+            const int64_t t = t0 + tl;
+            const float a = tt[j][tl], c = tt[j][tl + 1];
+            const uint16_t ha = f32_to_bf16(a), hc = f32_to_bf16(c);
+            const uint16_t la = f32_to_bf16(a - bf16_to_f32(ha)), lc = f32_to_bf16(c - bf16_to_f32(hc));
+            if (t + 1 < T && (T & 1) == 0) {
+                *reinterpret_cast<uint32_t*>(J.gd_hi + (int64_t)j * T + t) = (uint32_t)ha | ((uint32_t)hc << 16);
+                *reinterpret_cast<uint32_t*>(J.gd_lo + (int64_t)j * T + t) = (uint32_t)la | ((uint32_t)lc << 16);
+            } else {
+                if (t < T) {
+                    J.gd_hi[(int64_t)j * T + t] = ha;
+                    J.gd_lo[(int64_t)j * T + t] = la;
+                }
+                if (t + 1 < T) {
+                    J.gd_hi[(int64_t)j * T + t + 1] = hc;
+                    J.gd_lo[(int64_t)j * T + t + 1] = lc;
+                }
+            }
+        }
 }
 
 // ------------------------------------------------- split row projection
@@ -1069,19 +1286,23 @@ __global__ __launch_bounds__(256) void colreduce_f32(const float* __restrict__ X
 hipError_t launch_prep_bf16(const PrepJob* jobs, int n, hipStream_t stream) {
     PrepBatch b{};
     int k = 0;
+    bool vec8 = true;
     for (int i = 0; i < n && k < kPrepJobs; ++i) {
         if (!jobs[i].hi) continue;
         b.job[k] = jobs[i];
         if (b.job[k].ld_out == 0) b.job[k].ld_out = b.job[k].cols_out;
-        b.start[k + 1] = b.start[k] + jobs[i].rows_out * jobs[i].cols_out;
+        vec8 = vec8 && prep_vec8(b.job[k]);
         ++k;
     }
     b.njobs = k;
+    for (int i = 0; i < k; ++i)
+        b.start[i + 1] = b.start[i] + b.job[i].rows_out * b.job[i].cols_out / (vec8 ? 8 : 1);
     const int64_t total = b.start[k];
     if (total == 0) return hipSuccess;
     int64_t blocks = (total + 255) / 256;
     if (blocks > 4096) blocks = 4096;
-    prep_bf16<<<dim3((unsigned)blocks), 256, 0, stream>>>(b);
+    if (vec8) prep_bf16<true><<<dim3((unsigned)blocks), 256, 0, stream>>>(b);
+    else prep_bf16<false><<<dim3((unsigned)blocks), 256, 0, stream>>>(b);
     return hipGetLastError();
 }
 
@@ -1258,21 +1479,84 @@ hipError_t launch_colreduce_bf16(int64_t T, const ColJob* jobs, int n, hipStream
     return hipSuccess;
 }
 
+// Splits of a colsplit job: about one round of 256 workgroups over the
+// job's 512-column tiles (c5: 37 tiles x 6 splits for 18944 columns, 7 x 36
+// for 3584, which measured fastest among 1-3 rounds), each split at least
+// 256 tokens.
+int colsplit_splits(int64_t T, int64_t C) {
+    const int64_t ctiles = (C + 511) / 512;
+    int64_t s = 256 / ctiles;
+    const int64_t max_s = T / 256;
+    if (s > max_s) s = max_s;
+    if (s < 1) s = 1;
+    return (int)s;
+}
+
+hipError_t launch_colsplit_bf16(int64_t T, const ColsplitJob* jobs, int n, hipStream_t stream) {
+    // Ranks in groups of up to 64 (four 16-row MFMA tiles of accumulators),
+    // each group one pass over X, binned by its rank tiles; one launch per
+    // bin of up to kColJobs groups.
+    if (T % 8 != 0) return hipErrorInvalidValue;
+    constexpr int GS = 64;
+    ColsplitJobDev bins[4][8 * kColJobs];
+    int nb[4] = {0, 0, 0, 0};
+    for (int i = 0; i < n; ++i) {
+        const ColsplitJob& J = jobs[i];
+        if (!J.X) continue;
+        if (J.splits < 1 || J.C % 8 != 0 || J.C >= ((int64_t)1 << 22)) return hipErrorInvalidValue;
+        const int64_t stride = (int64_t)colreduce_rows(J.r) * J.C;
+        for (int g = 0; g * GS < J.r; ++g) {
+            const int rs = J.r - GS * g < GS ? J.r - GS * g : GS;
+            const int bin = rs <= 16 ? 0 : rs <= 32 ? 1 : rs <= 48 ? 2 : 3;
+            ColsplitJobDev d{J.X, J.C, J.P_hi + (int64_t)GS * g * T, J.P_lo + (int64_t)GS * g * T, rs,
+                             round_up((T + J.splits - 1) / J.splits, 32), J.partial + (int64_t)GS * g * J.C, stride,
+                             (int)((J.C + 511) / 512), J.splits};
+            if (nb[bin] < 8 * kColJobs) bins[bin][nb[bin]++] = d;
+        }
+    }
+    for (int bin = 0; bin < 4; ++bin) {
+        for (int first = 0; first < nb[bin]; first += kColJobs) {
+            ColsplitBatch cb{};
+            cb.njobs = std::min(kColJobs, nb[bin] - first);
+            for (int k = 0; k < cb.njobs; ++k) {
+                cb.job[k] = bins[bin][first + k];
+                cb.start[k + 1] = cb.start[k] + cb.job[k].ctiles * cb.job[k].splits;
+            }
+            const dim3 grid((unsigned)cb.start[cb.njobs]);
+            switch (bin) {
+                case 0: colsplit_bf16<1><<<grid, 256, 0, stream>>>(T, cb); break;
+                case 1: colsplit_bf16<2><<<grid, 256, 0, stream>>>(T, cb); break;
+                case 2: colsplit_bf16<3><<<grid, 256, 0, stream>>>(T, cb); break;
+                default: colsplit_bf16<4><<<grid, 256, 0, stream>>>(T, cb); break;
+            }
+            const hipError_t e = hipGetLastError();
+            if (e != hipSuccess) return e;
+        }
+    }
+    return hipSuccess;
+}
+
 hipError_t launch_split_sum(const SumJob* jobs, int n, hipStream_t stream) {
     SumBatch sb{};
     int k = 0;
+    bool vec4 = true;
     for (int i = 0; i < n && k < kSumJobs; ++i) {
         if (!jobs[i].out) continue;
-        sb.job[k] = jobs[i];
-        sb.start[k + 1] = sb.start[k] + (int64_t)jobs[i].r * jobs[i].C;
-        ++k;
+        const SumJob& J = jobs[i];
+        // a split's partial is one buffer resource with 32-bit offsets
+        vec4 = vec4 && J.C % 4 == 0 && J.part_stride % 4 == 0 && J.part_stride * 4 < ((int64_t)1 << 31) &&
+               reinterpret_cast<uintptr_t>(J.partial) % 16 == 0 &&
+               (J.transpose_out || reinterpret_cast<uintptr_t>(J.out) % 16 == 0);
+        sb.job[k++] = J;
     }
     sb.njobs = k;
+    for (int i = 0; i < k; ++i) sb.start[i + 1] = sb.start[i] + (int64_t)sb.job[i].r * sb.job[i].C / (vec4 ? 4 : 1);
     const int64_t total = sb.start[k];
     if (total == 0) return hipSuccess;
     int64_t blocks = (total + 255) / 256;
     if (blocks > 4096) blocks = 4096;
-    split_sum<<<dim3((unsigned)blocks), 256, 0, stream>>>(sb);
+    if (vec4) split_sum<true><<<dim3((unsigned)blocks), 256, 0, stream>>>(sb);
+    else split_sum<false><<<dim3((unsigned)blocks), 256, 0, stream>>>(sb);
     return hipGetLastError();
 }
 
@@ -1327,17 +1611,20 @@ hipError_t launch_dy_finish(int64_t T, int r, float scale, float keep, int rext,
     fb.r = r; fb.rext = rext; fb.ext_ld = ext_ld; fb.scale = scale; fb.keep = keep; fb.ext_scale = ext_scale;
     fb.blocks_per_job = (int)((T + 63) / 64);
     for (int i = 0; i < n && fb.njobs < kMaxProj; ++i)
-        if (jobs[i].gpart && (jobs[i].gd_t || jobs[i].gd_ext)) fb.job[fb.njobs++] = jobs[i];
-    for (int i = 0; i < npreps && fb.npreps < kMaxProj; ++i) {
+        if (jobs[i].gpart && (jobs[i].gd_t || jobs[i].gd_ext || jobs[i].gd_hi)) fb.job[fb.njobs++] = jobs[i];
+    bool vec8 = true;
+    for (int i = 0; i < npreps && fb.npreps < kPrepJobs; ++i) {
         if (!preps[i].hi) continue;
         PrepJob p = preps[i];
         if (p.ld_out == 0) p.ld_out = p.cols_out;
-        fb.prep[fb.npreps] = p;
-        fb.prep_start[fb.npreps + 1] = fb.prep_start[fb.npreps] + p.rows_out * p.cols_out;
-        ++fb.npreps;
+        vec8 = vec8 && prep_vec8(p);
+        fb.prep[fb.npreps++] = p;
     }
+    fb.prep8 = vec8 ? 1 : 0;
+    for (int i = 0; i < fb.npreps; ++i)
+        fb.prep_start[i + 1] = fb.prep_start[i] + fb.prep[i].rows_out * fb.prep[i].cols_out / (vec8 ? 8 : 1);
     const int64_t prep_n = fb.prep_start[fb.npreps];
-    const int64_t prep_blocks = prep_n > 0 ? std::min<int64_t>((prep_n + 255) / 256, 512) : 0;
+    const int64_t prep_blocks = prep_n > 0 ? std::min<int64_t>((prep_n + 255) / 256, 1024) : 0;
     const int64_t blocks = (int64_t)fb.njobs * fb.blocks_per_job + prep_blocks;
     if (blocks == 0) return hipSuccess;
     for (int i = 0; i < fb.njobs; ++i)  // one split of a job is one buffer resource

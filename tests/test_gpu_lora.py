@@ -169,6 +169,9 @@ def test_config5_dropout_bf16(mc, dev):
     ("rank 33, 4104 columns", 517, 4104, 96, 33, 0.0),
     ("rank 8, 4608 columns, dropout", 700, 4608, 4160, 8, 0.2),
     ("rank 64, dY of 4104 columns", 1100, 520, 4104, 64, 0.0),
+    # 42 column-reduction splits of 416 tokens: the last two are empty and
+    # must still write their (zero) partials
+    ("rank 64, empty trailing splits", 16384, 2568, 264, 64, 0.0),
 ])
 def test_split_row_projection(mc, dev, name, T, K, N, r, p):
     c = lora_case(zlib.crc32(name.encode()), T, K, N, r)

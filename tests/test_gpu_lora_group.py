@@ -109,11 +109,14 @@ def test_group_delta_only_member(mc, dev):
     _check_group(mc, dev, 1024, 256, [256, 64, 128], 16, 0.0, 41, no_w=(1,))
 
 
-@pytest.mark.parametrize("T,K,Ns", [(2048, 512, [512, 256]),
-                                    (8192, 512, [8192, 8200])])  # the fused dY pass (dY of >= 2^26 elements)
-def test_group_partial_outputs(mc, dev, T, K, Ns):
+@pytest.mark.parametrize("T,K,Ns,r", [(2048, 512, [512, 256], 16),
+                                      (8192, 512, [8192, 8200], 16),  # the fused dY pass (dY of >= 2^26 elements)
+                                      # 33-64 ranks: split row projection and the column reductions over bf16
+                                      # planes (dB only: Hd^T planes without a finishing launch)
+                                      (2048, 520, [512, 264], 48)])
+def test_group_partial_outputs(mc, dev, T, K, Ns, r):
     """dX only, dA / dB only, dB only: the same values as the full call."""
-    x, projs, dys = _group_case(dev, T, K, Ns, 16, 0.0, 7)
+    x, projs, dys = _group_case(dev, T, K, Ns, r, 0.0, 7)
     ys, hs = mc.lora_group_forward(x, projs, 2.0)
     full = mc.lora_group_backward(x, projs, dys, 2.0, h_saves=hs)
     only_dx = mc.lora_group_backward(x, projs, dys, 2.0, need_dA=False, need_dB=False)
