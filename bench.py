@@ -483,6 +483,39 @@ def c2_row_ops(mc, dev, iters):
     return out
 
 
+def blas_reference(c, dev, iters):
+    """The vendor library on the layer's forward GEMM shapes: torch.matmul
+    (hipBLASLt on ROCm) of x [T, K] bf16 by W^T for each projection's
+    [N, K] W, warm back-to-back calls, as a reference point for the base
+    GEMM's MFMA fraction (no LoRA columns, no bias)."""
+    import torch
+
+    T = c["batch"] * c["seq"]
+    out = {"library": "hipBLASLt via torch.matmul (x @ W.t(), bf16)", "iters": iters, "shapes": []}
+    seen = set()
+    for name, (K, N, _) in proj_shapes(c).items():
+        if (K, N) in seen:
+            continue
+        seen.add((K, N))
+        x = torch.randn(T, K, device=dev).to(torch.bfloat16)
+        w = torch.randn(N, K, device=dev).to(torch.bfloat16)
+        for _ in range(3):
+            torch.matmul(x, w.t())
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(iters):
+            torch.matmul(x, w.t())
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / iters
+        tf = 2.0 * T * N * K / (us * 1e-6) / 1e12
+        out["shapes"].append({"projection": name, "M": T, "N": N, "K": K, "us": us, "TFLOP_s": tf,
+                              "frac": tf / BF16_PEAK_TFLOPS})
+        del x, w
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -499,6 +532,9 @@ def main():
                     help="grouped calls without the load-time W^T: every backward transposes W into its workspace")
     ap.add_argument("--attention-iters", type=int, default=5,
                     help="calls of the attention core fwd / bwd timed after the step (0: skip)")
+    ap.add_argument("--blas-reference", type=int, default=0, metavar="ITERS",
+                    help="also time the vendor library (hipBLASLt via torch.matmul) on the layer's forward GEMM "
+                         "shapes, ITERS calls each")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="run one plain device copy of BYTES before the steps (a kernel of known HBM traffic "
                          "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
@@ -616,6 +652,8 @@ def main():
         line["adamw"] = adamw_update(mc, c, dev, 20)
         line["row_ops"] = row_ops(mc, c, dev, args.attention_iters)
     line["c2_row_ops_f32"] = c2_row_ops(mc, dev, 5)
+    if args.blas_reference > 0:
+        line["blas_reference"] = blas_reference(c, dev, args.blas_reference)
     if not args.no_cpu_baseline:
         threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
         v, dt = cpu_baseline(mc, c, args.cpu_tokens, threads, args.cpu_iters)
