@@ -401,8 +401,14 @@ __global__ __launch_bounds__(256) void attn_fwd_generic(const T* __restrict__ q,
 //                                                   transposed LDS reads of
 //                                                   the dO, Q tiles)
 //                      dK, dV per query head: written directly when H = Hkv,
-//                      else as fp32 partials summed by attn_bwd_sum.
-//  attn_bwd_dq_bf16    one workgroup per (b, h, 128 queries) as the forward:
+//                      else as fp32 partials summed by attn_bwd_sum; dS^T
+//                      (bf16, key rows) stored for the dQ pass.
+//  attn_bwd_dq_ds_bf16 one workgroup per (b, h, 128 queries):
+//                        dQ^T += K^T.dS^T         (both operands by transposed
+//                                                   LDS reads of the K and
+//                                                   stored dS^T tiles)
+//  attn_bwd_dq_bf16    the same without a stored dS^T (S * ldst * 2 bytes of a
+//                      head past 2^31), shaped as the forward:
 //                        S^T = K.Q^T, dP^T = V.dO^T (lane = query: Q, dO held
 //                                                   in registers)
 //                        dQ^T += K^T.dS^T         (K^T by transposed LDS
@@ -419,6 +425,8 @@ struct AttnBwdArgs {
     uint16_t* dv;
     float* dk_part;        // [B, H, S, D] fp32 (H > Hkv)
     float* dv_part;
+    uint16_t* dst;         // [B, H, S, ldst]: dS^T (key rows, query columns) for the dQ pass, or null
+    int64_t ldst;
     int64_t S, Sp;
     int B, H, Hkv, causal, nblk;
     float scale, scale_log2;
@@ -635,6 +643,8 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_bf16(AttnBwdArgs a) {
     const i32x4 rdo = rsrc_words(a.dout + ((int64_t)b * S * a.H + h) * D, (S * a.H - h) * D * 2);
     const i32x4 rl = rsrc_words(a.lsd + (int64_t)bh * (a.Sp / 64) * 128, (a.Sp / 64) * 128 * 4);
     const __amdgpu_buffer_rsrc_t rm = make_rsrc(a.mask, a.mask ? S * S * 4 : 0);
+    const __amdgpu_buffer_rsrc_t rds = make_rsrc(a.dst ? a.dst + (int64_t)bh * S * a.ldst : nullptr,
+                                                 a.dst ? S * a.ldst * 2 : 0);
 
     const int nqb = (int)((S + 63) / 64);
     const int qstart = a.causal ? (int)(key0 / 64) : 0;  // earlier query blocks see none of these keys
@@ -734,6 +744,22 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_bf16(AttnBwdArgs a) {
             if (a.mask) scores(std::true_type{}, std::true_type{}, t_tag, sacc, dpacc, pb, db);
             else if (a.causal && q0 < kw + 31) scores(std::false_type{}, std::true_type{}, t_tag, sacc, dpacc, pb, db);
             else scores(std::false_type{}, std::false_type{}, t_tag, sacc, dpacc, pb, db);
+            if (a.dst) {
+                // dS^T for the dQ pass: elements 4 hh .. 4 hh + 3 of db[kk] are
+                // queries q0 + 32 t + 16 kk + 8 hh + 4 half + 0..3 of this
+                // lane's key, 8 contiguous bytes of its dS^T row; keys past S
+                // fall outside the buffer range and are dropped
+#pragma unroll
+                for (int kk = 0; kk < 2; ++kk) {
+                    const uint4 w4 = __builtin_bit_cast(uint4, db[kk]);
+#pragma unroll
+                    for (int hh = 0; hh < 2; ++hh) {
+                        const int64_t qq = q0 + 32 * t + 16 * kk + 8 * hh + 4 * half;
+                        const u32x2 v2 = {hh ? w4.z : w4.x, hh ? w4.w : w4.y};
+                        __builtin_amdgcn_raw_buffer_store_b64(v2, rds, (int)(uint32_t)((my_key * a.ldst + qq) * 2), 0, 0);
+                    }
+                }
+            }
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
@@ -939,6 +965,84 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq_bf16(AttnBwdArgs a) {
     store_rows<D, uint16_t>(dqacc, a.scale, smem + wave * 32 * (D + 8), a.dq + (int64_t)bh * S * D, D, qw, S, lane);
 }
 
+// dQ from the stored dS^T (written by attn_bwd_dkdv_bf16): one workgroup
+// per (b, h, 128 queries), 4 waves of 32 queries. Per block of 64 keys (up
+// to the diagonal when causal) the K tile [64][D] and the dS^T tile
+// [64 keys][128 queries] go into LDS (two stages, the backward's swizzled
+// layout); dQ^T (d x query) += K^T . dS^T takes both operands by transposed
+// reads in the same key order, so nothing is recomputed: no S, no dP, no
+// score arithmetic or mask (dS already holds them). Keys past S load as
+// zeros from both buffers; dS^T columns of queries past S are never stored.
+template <int D>
+__global__ __launch_bounds__(256, 2) void attn_bwd_dq_ds_bf16(AttnBwdArgs a) {
+    constexpr int KB = 64, QB = 128, DT = D / 32;
+    constexpr int KT = 64 * D, DSTILE = 64 * QB;  // K tile, dS^T tile (elements)
+    constexpr int STAGE = KT + DSTILE;
+    __shared__ __attribute__((aligned(1024))) uint16_t smem[2 * STAGE];
+    static_assert(4 * 32 * (D + 8) <= 2 * STAGE, "the epilogue's bf16 patches fit in the stages");
+    const uint32_t smem_byte = (uint32_t)reinterpret_cast<uintptr_t>(smem);
+    const int lane = threadIdx.x & 63, wave = wave_id();
+    const int nbh = a.B * a.H;
+    const int nqb = (int)((a.S + QB - 1) / QB);
+    const int qb = nqb - 1 - (int)(blockIdx.x / nbh);  // heaviest query blocks first
+    const int bh = (int)(blockIdx.x % nbh);
+    const int b = bh / a.H, h = bh % a.H;
+    const int64_t bhk = (int64_t)b * a.Hkv + h / (a.H / a.Hkv);
+    const int64_t S = a.S;
+    const int64_t q0 = (int64_t)qb * QB;
+    const int64_t qw = q0 + 32 * wave;
+
+    uint32_t tk[DT][2], td[2];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) tk[dt][hh] = tr_off<D>(lane, 32 * dt, hh);
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) td[hh] = tr_off<QB>(lane, 32 * wave, hh);
+
+    const i32x4 rk = rsrc_words(a.k + bhk * S * D, S * D * 2);
+    // dS^T rows of this head from column q0: rows past S fall outside
+    const i32x4 rds = rsrc_words(a.dst + (int64_t)bh * S * a.ldst + q0, (S * a.ldst - q0) * 2);
+
+    const int nkb_all = (int)((S + KB - 1) / KB);
+    int nkb = nkb_all;
+    if (a.causal) nkb = min(nkb_all, (int)((min(q0 + QB, S) - 1) / KB) + 1);
+
+    auto issue = [&](int kb, int stage) {
+        const uint32_t base = smem_byte + (uint32_t)(stage * STAGE * 2);
+        const uint32_t key0 = (uint32_t)kb * KB;
+        dma_rows<D>(rk, base, key0, D, wave, lane);
+        dma_rows<QB>(rds, base + KT * 2, key0, (uint32_t)a.ldst, wave, lane);
+    };
+
+    f32x16 dqacc[DT];
+#pragma unroll
+    for (int t = 0; t < DT; ++t)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) dqacc[t][j] = 0.f;
+
+    if (nkb > 0) issue(0, 0);
+    for (int kb = 0; kb < nkb; ++kb) {
+        wait_vmcnt<0>();
+        __syncthreads();
+        if (kb + 1 < nkb) issue(kb + 1, (kb + 1) & 1);
+        const uint16_t* sk = smem + (kb & 1) * STAGE;
+        const uint16_t* sds = sk + KT;
+#pragma unroll
+        for (int kc = 0; kc < KB / 16; ++kc) {
+            const bf16x8 bfr = frag_tr_at(sds + 16 * kc * QB, td[0], td[1]);
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
+                dqacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_tr_at(sk + 16 * kc * D, tk[dt][0], tk[dt][1]),
+                                                                   bfr, dqacc[dt], 0, 0, 0);
+        }
+    }
+
+    wait_vmcnt<0>();  // every DMA has landed (also when the loop ran no block)
+    __syncthreads();
+    store_rows<D, uint16_t>(dqacc, a.scale, smem + wave * 32 * (D + 8), a.dq + (int64_t)bh * S * D, D, qw, S, lane);
+}
+
 // ------------------------------------------------------ generic backward
 // One wave per row; lanes over the head dim (dims l, l + 64, l + 128, l + 192).
 template <typename T>
@@ -1132,6 +1236,14 @@ namespace {
 size_t align256(size_t n) { return (n + 255) / 256 * 256; }
 }  // namespace
 
+// The MFMA backward's dQ pass reads dS^T stored by the dK/dV kernel (bf16
+// [B, H, S, ldst], ldst = S rounded up to 128) when a head's dS^T rows fit
+// 32-bit buffer offsets; beyond that (S > ~32k) it recomputes S and dP.
+int64_t dst_ld(int64_t S) { return (S + 127) / 128 * 128; }
+bool attention_dq_from_ds(const mc_attn_desc& d) {
+    return attention_uses_mfma(d) && (int64_t)d.seq * dst_ld(d.seq) * 2 < ((int64_t)1 << 31);
+}
+
 AttnBwdWs attention_bwd_ws(const mc_attn_desc& d) {
     AttnBwdWs w{};
     const size_t B = (size_t)d.batch, H = (size_t)d.heads, Hkv = (size_t)d.kv_heads, D = (size_t)d.head_dim;
@@ -1144,6 +1256,8 @@ AttnBwdWs attention_bwd_ws(const mc_attn_desc& d) {
             w.dk_part = off;  off += align256(B * H * S * D * 4);
             w.dv_part = off;  off += align256(B * H * S * D * 4);
         }
+        w.dst = off;
+        if (attention_dq_from_ds(d)) off += align256(B * H * S * (size_t)dst_ld(d.seq) * 2);
     } else {
         w.lsd = off;  off += align256(B * H * S * 4);  // Delta
     }
@@ -1172,6 +1286,9 @@ hipError_t launch_attention_bwd(const mc_attn_desc& d, const void* q, const void
         a.dv = static_cast<uint16_t*>(dv);
         a.dk_part = H != Hkv ? reinterpret_cast<float*>(base + w.dk_part) : nullptr;
         a.dv_part = H != Hkv ? reinterpret_cast<float*>(base + w.dv_part) : nullptr;
+        const bool from_ds = attention_dq_from_ds(d);
+        a.dst = from_ds ? reinterpret_cast<uint16_t*>(base + w.dst) : nullptr;
+        a.ldst = dst_ld(S);
         a.S = S;
         a.Sp = Sp;
         a.B = B; a.H = H; a.Hkv = Hkv;
@@ -1197,8 +1314,13 @@ hipError_t launch_attention_bwd(const mc_attn_desc& d, const void* q, const void
             attn_bwd_sum<<<dim3((unsigned)blocks), 256, 0, stream>>>(a.dk_part, a.dv_part, a.dk, a.dv, H / Hkv,
                                                                      S * D, n8);
         }
-        if (D == 64) attn_bwd_dq_bf16<64><<<grid, 256, 0, stream>>>(a);
-        else attn_bwd_dq_bf16<128><<<grid, 256, 0, stream>>>(a);
+        if (from_ds) {
+            if (D == 64) attn_bwd_dq_ds_bf16<64><<<grid, 256, 0, stream>>>(a);
+            else attn_bwd_dq_ds_bf16<128><<<grid, 256, 0, stream>>>(a);
+        } else {
+            if (D == 64) attn_bwd_dq_bf16<64><<<grid, 256, 0, stream>>>(a);
+            else attn_bwd_dq_bf16<128><<<grid, 256, 0, stream>>>(a);
+        }
         return hipGetLastError();
     }
     float* delta = reinterpret_cast<float*>(base + w.lsd);

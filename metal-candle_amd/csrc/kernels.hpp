@@ -124,6 +124,7 @@ hipError_t launch_attention_fwd(const mc_attn_desc& d, const void* q, const void
 // [B, H, S, D]). Generic path: Delta (f32 [B, H, S]) at lsd.
 struct AttnBwdWs {
     size_t lsd, dk_part, dv_part;
+    size_t dst;  // bf16 dS^T [B, H, S, ldst] for the dQ pass (attention_dq_from_ds), else unused
     size_t total;
 };
 AttnBwdWs attention_bwd_ws(const mc_attn_desc& d);

@@ -253,6 +253,53 @@ def test_attention_bwd_deterministic(mc, dev):
     assert all(torch.equal(x, y) for x, y in zip(a, b))
 
 
+def test_attention_bwd_long_sequence(mc, dev):
+    """S = 32800: a head's stored dS^T (S x 32896 bf16) passes 2^31 bytes, so
+    dQ takes the kernel that recomputes S and dP. Causal: the gradients of the
+    last 64 queries and of the last 64 keys involve only the last 64 query
+    rows of P and dS, which an fp32 torch composite computes on the GPU from
+    the inputs (softmax over all 32800 keys, O = P.V, Delta = rowsum(dO * O));
+    the first 2048 queries' dQ matches a 2048-long problem over the same
+    prefix (dQ_i depends on keys <= i only), which runs the dS^T path."""
+    B, H, Hkv, S, D = 1, 2, 1, 32800, 64
+    assert S * ((S + 127) // 128 * 128) * 2 >= 2 ** 31
+    g = torch.Generator(device=dev).manual_seed(32800)
+    q = torch.randn(B, H, S, D, generator=g, device=dev).to(torch.bfloat16)
+    k = torch.randn(B, Hkv, S, D, generator=g, device=dev).to(torch.bfloat16)
+    v = torch.randn(B, Hkv, S, D, generator=g, device=dev).to(torch.bfloat16)
+    do = torch.randn(B, S, H * D, generator=g, device=dev).to(torch.bfloat16)
+    o, lse = mc.attention_forward(q, k, v, causal=True)
+    dq, dk, dv = mc.attention_backward(q, k, v, o, lse, do, causal=True)
+    torch.cuda.synchronize()
+    for t in (dq, dk, dv):
+        assert torch.isfinite(t).all()
+    scale, R = D ** -0.5, 64
+    r0 = S - R
+    kf, vf = k[0, 0].float(), v[0, 0].float()
+    dk_ref, dv_ref = torch.zeros(R, D, device=dev), torch.zeros(R, D, device=dev)
+    for h in range(H):
+        qr = q[0, h, r0:].float()
+        dor = do[0, r0:].view(R, H, D)[:, h].float()
+        s = (qr @ kf.t()) * scale
+        s = s.masked_fill(torch.arange(S, device=dev)[None, :] > torch.arange(r0, S, device=dev)[:, None],
+                          float("-inf"))
+        p = torch.softmax(s, -1)
+        delta = (dor * (p @ vf)).sum(-1, keepdim=True)
+        ds = p * (dor @ vf.t() - delta)
+        assert rel_err(dq[0, h, r0:], (scale * ds @ kf).cpu().numpy()) <= BF16_TOL
+        dk_ref += scale * ds[:, r0:].t() @ qr
+        dv_ref += p[:, r0:].t() @ dor
+    assert rel_err(dk[0, 0, r0:], dk_ref.cpu().numpy()) <= BF16_TOL
+    assert rel_err(dv[0, 0, r0:], dv_ref.cpu().numpy()) <= BF16_TOL
+    P = 2048
+    qp, kp, vp = q[:, :, :P].contiguous(), k[:, :, :P].contiguous(), v[:, :, :P].contiguous()
+    dop = do[:, :P].contiguous()
+    op, lsep = mc.attention_forward(qp, kp, vp, causal=True)
+    dqp, _, _ = mc.attention_backward(qp, kp, vp, op, lsep, dop, causal=True)
+    torch.cuda.synchronize()
+    assert rel_err(dq[:, :, :P], dqp.float().cpu().numpy()) <= BF16_TOL
+
+
 def test_attention_bwd_c4_shape(mc, dev):
     """Backward at BASELINE.json c4's attention shape: one whole K/V group (6 query
     heads, every query and key) against the oracle; on every head, the rows
