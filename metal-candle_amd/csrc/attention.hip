@@ -390,9 +390,10 @@ __global__ __launch_bounds__(256) void attn_fwd_generic(const T* __restrict__ q,
 // bf16, D = 64 or 128:
 //  attn_bwd_prep_bf16  per (b, h, 64 queries): Delta and lse * log2 e, both
 //                      into one [2][64] fp32 block per query block.
-//  attn_bwd_dkdv_bf16  one workgroup per (b, h, 128 keys), 4 waves of 32 keys;
-//                      per block of 64 queries (Q, dO and the lse/Delta block
-//                      through LDS, two stages):
+//  attn_bwd_dkdv_bf16  one workgroup per (b, K/V head, group of query heads,
+//                      128 keys), 4 waves of 32 keys; for each query head of
+//                      the group, per block of 64 queries (Q, dO and the
+//                      lse/Delta block through LDS, two stages):
 //                        S = Q.K^T, dP = dO.V^T    (lane = key: K, V held in
 //                                                   registers as B operands)
 //                        dV^T += dO^T.P,  dK^T += Q^T.dS   (P, dS straight from
@@ -400,9 +401,11 @@ __global__ __launch_bounds__(256) void attn_fwd_generic(const T* __restrict__ q,
 //                                                   B operand; dO^T, Q^T by
 //                                                   transposed LDS reads of
 //                                                   the dO, Q tiles)
-//                      dK, dV per query head: written directly when H = Hkv,
-//                      else as fp32 partials summed by attn_bwd_sum; dS^T
-//                      (bf16, key rows) stored for the dQ pass.
+//                      dK, dV accumulate over the group's heads: written
+//                      directly when one group holds all H / Hkv heads of a
+//                      K/V head, else as fp32 partials per group summed by
+//                      attn_bwd_sum; dS^T (bf16, key rows) stored for the
+//                      dQ pass.
 //  attn_bwd_dq_ds_bf16 one workgroup per (b, h, 128 queries):
 //                        dQ^T += K^T.dS^T         (both operands by transposed
 //                                                   LDS reads of the K and
@@ -427,6 +430,7 @@ struct AttnBwdArgs {
     float* dv_part;
     uint16_t* dst;         // [B, H, S, ldst]: dS^T (key rows, query columns) for the dQ pass, or null
     int64_t ldst;
+    int ngroups;           // query-head groups per K/V head in the dK/dV kernel (H / Hkv / ngroups heads each)
     int64_t S, Sp;
     int B, H, Hkv, causal, nblk;
     float scale, scale_log2;
@@ -603,12 +607,14 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_bf16(AttnBwdArgs a) {
     const uint32_t smem_byte = (uint32_t)reinterpret_cast<uintptr_t>(smem);
     const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
     const int col = lane & 31, half = lane >> 5;
-    const int nbh = a.B * a.H;
-    const int kb = (int)(blockIdx.x / nbh);      // key block 0 sees the most queries: dispatched first
-    const int bh = (int)(blockIdx.x % nbh);
-    const int b = bh / a.H, h = bh % a.H;
-    const int rep = a.H / a.Hkv;
-    const int64_t bhk = (int64_t)b * a.Hkv + h / rep;
+    const int ng = a.ngroups;
+    const int nwg = a.B * a.Hkv * ng;
+    const int kb = (int)(blockIdx.x / nwg);      // key block 0 sees the most queries: dispatched first
+    const int grp = (int)(blockIdx.x % nwg) % ng;
+    const int64_t bhk = (int64_t)(blockIdx.x % nwg) / ng;  // b * Hkv + K/V head
+    const int b = (int)(bhk / a.Hkv);
+    const int rep = a.H / a.Hkv, hpg = rep / ng;
+    const int h0 = (int)(bhk % a.Hkv) * rep + grp * hpg;  // the group's first query head
     const int64_t S = a.S;
     const int64_t key0 = (int64_t)kb * 128;
     const int64_t kw = key0 + 32 * wave;         // first key of this wave
@@ -639,17 +645,20 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_bf16(AttnBwdArgs a) {
         dma_rows<D>(rv, kv_byte + 192 * D * 2, (uint32_t)key0 + 64, D, wave, lane);
     }
 
-    const i32x4 rq = rsrc_words(a.q + (int64_t)bh * S * D, S * D * 2);
-    const i32x4 rdo = rsrc_words(a.dout + ((int64_t)b * S * a.H + h) * D, (S * a.H - h) * D * 2);
-    const i32x4 rl = rsrc_words(a.lsd + (int64_t)bh * (a.Sp / 64) * 128, (a.Sp / 64) * 128 * 4);
     const __amdgpu_buffer_rsrc_t rm = make_rsrc(a.mask, a.mask ? S * S * 4 : 0);
-    const __amdgpu_buffer_rsrc_t rds = make_rsrc(a.dst ? a.dst + (int64_t)bh * S * a.ldst : nullptr,
-                                                 a.dst ? S * a.ldst * 2 : 0);
 
     const int nqb = (int)((S + 63) / 64);
     const int qstart = a.causal ? (int)(key0 / 64) : 0;  // earlier query blocks see none of these keys
+    const int nq = nqb - qstart;                          // query blocks per head
+    const int nit = hpg * nq;                             // (head, query block) steps, head-major
 
-    auto issue = [&](int qb, int stage) {
+    // step it: query head h0 + it / nq, query block qstart + it % nq
+    auto issue = [&](int it, int stage) {
+        const int h = h0 + it / nq, qb = qstart + it % nq;
+        const int64_t bh = (int64_t)b * a.H + h;
+        const i32x4 rq = rsrc_words(a.q + bh * S * D, S * D * 2);
+        const i32x4 rdo = rsrc_words(a.dout + ((int64_t)b * S * a.H + h) * D, (S * a.H - h) * D * 2);
+        const i32x4 rl = rsrc_words(a.lsd + bh * (a.Sp / 64) * 128, (a.Sp / 64) * 128 * 4);
         const uint32_t base = smem_byte + (uint32_t)(stage * STAGE * 2);
         const uint32_t q0 = (uint32_t)qb * 64;
         dma_rows<D>(rq, base, q0, D, wave, lane);
@@ -665,16 +674,20 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_bf16(AttnBwdArgs a) {
 #pragma unroll
         for (int j = 0; j < 16; ++j) dvacc[t][j] = dkacc[t][j] = 0.f;
 
-    if (qstart < nqb) issue(qstart, 0);
-    for (int qb = qstart; qb < nqb; ++qb) {
+    if (nit > 0) issue(0, 0);
+    for (int it = 0; it < nit; ++it) {
         wait_vmcnt<0>();
         __syncthreads();
-        if (qb + 1 < nqb) issue(qb + 1, (qb + 1 - qstart) & 1);
+        if (it + 1 < nit) issue(it + 1, (it + 1) & 1);
+        const int qb = qstart + it % nq;
+        const __amdgpu_buffer_rsrc_t rds =
+            make_rsrc(a.dst ? a.dst + ((int64_t)b * a.H + h0 + it / nq) * S * a.ldst : nullptr,
+                      a.dst ? S * a.ldst * 2 : 0);
         // Every wave runs every block: in a block before the wave's first key
         // (causal) every P is masked to 0, and a wave past S computes rows
         // that are never stored. Skipping those blocks made the accumulators
         // take a VGPR round trip on every iteration.
-        const uint16_t* sq = smem + ((qb - qstart) & 1) * STAGE;
+        const uint16_t* sq = smem + (it & 1) * STAGE;
         const uint16_t* sdo = sq + TILE;
         const float* sl = reinterpret_cast<const float*>(sq + 2 * TILE);
         const int64_t q0 = (int64_t)qb * 64;
@@ -781,17 +794,18 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_bf16(AttnBwdArgs a) {
     __syncthreads();
     static_assert(32 * (D + 4) * 4 <= 32 * (D + 8) * 2 * 2, "fp32 patch rows fit a wave's share");
     void* patch = smem + wave * 32 * (D + 8) * 2;  // 32 rows of up to D + 4 floats per wave
-    if (rep == 1) {
+    if (ng == 1) {
         store_rows<D, uint16_t>(dvacc, 1.f, patch, a.dv + bhk * S * D, D, kw, S, lane);
         store_rows<D, uint16_t>(dkacc, a.scale, patch, a.dk + bhk * S * D, D, kw, S, lane);
     } else {
-        store_rows<D, float>(dvacc, 1.f, patch, a.dv_part + (int64_t)bh * S * D, D, kw, S, lane);
-        store_rows<D, float>(dkacc, a.scale, patch, a.dk_part + (int64_t)bh * S * D, D, kw, S, lane);
+        const int64_t pg = (bhk * ng + grp) * S * D;  // this group's partial
+        store_rows<D, float>(dvacc, 1.f, patch, a.dv_part + pg, D, kw, S, lane);
+        store_rows<D, float>(dkacc, a.scale, patch, a.dk_part + pg, D, kw, S, lane);
     }
 }
 
-// dk / dv [B, Hkv, S, D] = sum over the rep query heads of each K/V head of
-// the fp32 partials, in head order; 8 elements per thread.
+// dk / dv [B, Hkv, S, D] = sum over the rep query-head groups of each K/V
+// head of the fp32 partials, in group order; 8 elements per thread.
 __global__ __launch_bounds__(256) void attn_bwd_sum(const float* __restrict__ dk_part,
                                                     const float* __restrict__ dv_part, uint16_t* __restrict__ dk,
                                                     uint16_t* __restrict__ dv, int rep, int64_t per_head,
@@ -1244,6 +1258,24 @@ bool attention_dq_from_ds(const mc_attn_desc& d) {
     return attention_uses_mfma(d) && (int64_t)d.seq * dst_ld(d.seq) * 2 < ((int64_t)1 << 31);
 }
 
+// Query heads per dK/dV workgroup: the largest divisor g of H / Hkv whose
+// heaviest workgroup (g heads x every query block, key block 0) does no more
+// 64-query block steps than the average share of 256 CUs, so that the
+// heaviest-first dispatch still balances. Each group's heads accumulate in
+// the workgroup's registers; one group per K/V head leaves no partials to
+// sum. A function of the shape only (not of the device), so the sums'
+// order, and the results, do not depend on where the call runs.
+int attn_dkdv_groups(const mc_attn_desc& d) {
+    const int rep = d.heads / d.kv_heads;
+    const int64_t nqb = (d.seq + 63) / 64, nkb = (d.seq + 127) / 128;
+    int64_t steps = 0;  // 64-query block steps of one (b, h) over all key blocks
+    for (int64_t kb = 0; kb < nkb; ++kb) steps += d.causal ? std::max<int64_t>(nqb - 2 * kb, 0) : nqb;
+    const double avg = (double)steps * d.batch * d.heads / 256.0;
+    for (int g = rep; g > 1; --g)
+        if (rep % g == 0 && (double)g * nqb <= avg) return rep / g;
+    return rep;
+}
+
 AttnBwdWs attention_bwd_ws(const mc_attn_desc& d) {
     AttnBwdWs w{};
     const size_t B = (size_t)d.batch, H = (size_t)d.heads, Hkv = (size_t)d.kv_heads, D = (size_t)d.head_dim;
@@ -1252,9 +1284,10 @@ AttnBwdWs attention_bwd_ws(const mc_attn_desc& d) {
     if (attention_uses_mfma(d)) {
         const size_t Sp = (S + 63) / 64 * 64;
         w.lsd = off;  off += align256(B * H * (Sp / 64) * 128 * 4);
-        if (H != Hkv) {
-            w.dk_part = off;  off += align256(B * H * S * D * 4);
-            w.dv_part = off;  off += align256(B * H * S * D * 4);
+        const size_t ng = (size_t)attn_dkdv_groups(d);
+        if (ng > 1) {
+            w.dk_part = off;  off += align256(B * Hkv * ng * S * D * 4);
+            w.dv_part = off;  off += align256(B * Hkv * ng * S * D * 4);
         }
         w.dst = off;
         if (attention_dq_from_ds(d)) off += align256(B * H * S * (size_t)dst_ld(d.seq) * 2);
@@ -1284,8 +1317,9 @@ hipError_t launch_attention_bwd(const mc_attn_desc& d, const void* q, const void
         a.dq = static_cast<uint16_t*>(dq);
         a.dk = static_cast<uint16_t*>(dk);
         a.dv = static_cast<uint16_t*>(dv);
-        a.dk_part = H != Hkv ? reinterpret_cast<float*>(base + w.dk_part) : nullptr;
-        a.dv_part = H != Hkv ? reinterpret_cast<float*>(base + w.dv_part) : nullptr;
+        a.ngroups = attn_dkdv_groups(d);
+        a.dk_part = a.ngroups > 1 ? reinterpret_cast<float*>(base + w.dk_part) : nullptr;
+        a.dv_part = a.ngroups > 1 ? reinterpret_cast<float*>(base + w.dv_part) : nullptr;
         const bool from_ds = attention_dq_from_ds(d);
         a.dst = from_ds ? reinterpret_cast<uint16_t*>(base + w.dst) : nullptr;
         a.ldst = dst_ld(S);
@@ -1298,20 +1332,21 @@ hipError_t launch_attention_bwd(const mc_attn_desc& d, const void* q, const void
         a.scale_log2 = d.scale * kLog2e;
         const dim3 gprep((unsigned)(Sp / 64), (unsigned)(B * H));
         const dim3 grid((unsigned)((int64_t)a.nblk * B * H));
+        const dim3 gkv((unsigned)((int64_t)a.nblk * B * Hkv * a.ngroups));
         float* lsd = reinterpret_cast<float*>(base + w.lsd);
         const uint16_t* o16 = static_cast<const uint16_t*>(o);
         const uint16_t* do16 = static_cast<const uint16_t*>(dout);
         if (D == 64) {
             attn_bwd_prep_bf16<64><<<gprep, 256, 0, stream>>>(o16, do16, lse, H, S, Sp, lsd);
-            attn_bwd_dkdv_bf16<64><<<grid, 256, 0, stream>>>(a);
+            attn_bwd_dkdv_bf16<64><<<gkv, 256, 0, stream>>>(a);
         } else {
             attn_bwd_prep_bf16<128><<<gprep, 256, 0, stream>>>(o16, do16, lse, H, S, Sp, lsd);
-            attn_bwd_dkdv_bf16<128><<<grid, 256, 0, stream>>>(a);
+            attn_bwd_dkdv_bf16<128><<<gkv, 256, 0, stream>>>(a);
         }
-        if (H != Hkv) {
+        if (a.ngroups > 1) {
             const int64_t n8 = (int64_t)B * Hkv * S * D / 8;
             const int64_t blocks = std::min<int64_t>((2 * n8 + 255) / 256, 4096);
-            attn_bwd_sum<<<dim3((unsigned)blocks), 256, 0, stream>>>(a.dk_part, a.dv_part, a.dk, a.dv, H / Hkv,
+            attn_bwd_sum<<<dim3((unsigned)blocks), 256, 0, stream>>>(a.dk_part, a.dv_part, a.dk, a.dv, a.ngroups,
                                                                      S * D, n8);
         }
         if (from_ds) {

@@ -120,14 +120,16 @@ hipError_t launch_attention_fwd(const mc_attn_desc& d, const void* q, const void
                                 const float* mask, void* o, float* lse, void* ws, hipStream_t stream);
 // Workspace of mc_attention_bwd (byte offsets). MFMA path: lse * log2 e and
 // Delta per 64-query block (f32 [B, H, Sp/64, 2, 64], Sp = S rounded up to
-// 64) and, when H > Hkv, the per-query-head dK / dV partials (f32
-// [B, H, S, D]). Generic path: Delta (f32 [B, H, S]) at lsd.
+// 64) and, when the dK/dV kernel splits a K/V head's query heads into more
+// than one group (attn_dkdv_groups), the per-group dK / dV partials (f32
+// [B, Hkv, groups, S, D]). Generic path: Delta (f32 [B, H, S]) at lsd.
 struct AttnBwdWs {
     size_t lsd, dk_part, dv_part;
     size_t dst;  // bf16 dS^T [B, H, S, ldst] for the dQ pass (attention_dq_from_ds), else unused
     size_t total;
 };
 AttnBwdWs attention_bwd_ws(const mc_attn_desc& d);
+int attn_dkdv_groups(const mc_attn_desc& d);
 hipError_t launch_attention_bwd(const mc_attn_desc& d, const void* q, const void* k, const void* v,
                                 const float* mask, const void* o, const float* lse, const void* dout, void* dq,
                                 void* dk, void* dv, void* ws, hipStream_t stream);

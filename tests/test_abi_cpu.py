@@ -242,3 +242,30 @@ def test_transpose_validation(mc):
     assert "multiples of 8" in mc._lib.last_error()
     assert L.mc_transpose_bf16(8, 8, None, fake, None) == 1
     assert L.mc_transpose_bf16(8, 8, fake, 264, None) == 4
+
+
+def _a256(n):
+    return (n + 255) // 256 * 256
+
+
+@pytest.mark.parametrize("B,S,H,Hkv,causal,groups", [
+    (8, 2048, 12, 2, 1, 2),    # c4: 3 query heads per dK/dV workgroup, two partials per K/V head
+    (4, 4096, 28, 4, 1, 1),    # c5: all 7 heads of a K/V head in one workgroup, no partials
+    (16, 2048, 4, 2, 1, 1),
+    (8, 1024, 8, 4, 0, 1),
+    (1, 64, 4, 2, 1, 2),       # small grids keep one query head per workgroup
+    (2, 300, 12, 12, 1, 1),
+])
+def test_attention_bwd_workspace_groups(mc, B, S, H, Hkv, causal, groups):
+    """The bf16 backward's workspace: lse/Delta blocks, the dK/dV partials of
+    the query-head groups (none when a group holds all H/Hkv heads of a K/V
+    head), and dS^T [B, H, S, S rounded up to 128] for the dQ pass."""
+    L = mc._lib.lib()
+    D = 128
+    d = _attn(mc, B=B, S=S, H=H, Hkv=Hkv, D=D, causal=causal)
+    Sp = (S + 63) // 64 * 64
+    want = _a256(B * H * (Sp // 64) * 128 * 4)
+    if groups > 1:
+        want += 2 * _a256(B * Hkv * groups * S * D * 4)
+    want += _a256(B * H * S * ((S + 127) // 128 * 128) * 2)
+    assert L.mc_attention_bwd_workspace_size(ctypes.byref(d)) == want
