@@ -675,6 +675,16 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_bf16(AttnBwdArgs a) {
         for (int j = 0; j < 16; ++j) dvacc[t][j] = dkacc[t][j] = 0.f;
 
     if (nit > 0) issue(0, 0);
+    // The wave's K and V fragments (B operands of S and dP) are the same for
+    // every block: read from LDS once, then held in registers.
+    wait_vmcnt<0>();
+    __syncthreads();
+    bf16x8 kf[KS], vf[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+        kf[s] = frag_at(skw, roff[s]);
+        vf[s] = frag_at(svw, roff[s]);
+    }
     for (int it = 0; it < nit; ++it) {
         wait_vmcnt<0>();
         __syncthreads();
@@ -742,15 +752,15 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_bf16(AttnBwdArgs a) {
             for (int j = 0; j < 16; ++j) sacc[j] = dpacc[j] = 0.f;
 #pragma unroll
             for (int s = 0; s < KS; ++s) {
-                sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_at(sq + 32 * t * D, roff[s]), frag_at(skw, roff[s]),
-                                                              sacc, 0, 0, 0);
-                dpacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_at(sdo + 32 * t * D, roff[s]),
-                                                               frag_at(svw, roff[s]), dpacc, 0, 0, 0);
+                sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_at(sq + 32 * t * D, roff[s]), kf[s], sacc, 0, 0,
+                                                              0);
+                dpacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_at(sdo + 32 * t * D, roff[s]), vf[s], dpacc, 0, 0,
+                                                               0);
                 // each k-chunk's fragment reads right before its MFMAs (and
                 // below, each dV/dK pair's): left free, the scheduler keeps
                 // more fragments live (D = 128: 256 VGPRs + 188 AGPRs against
                 // 252 + 160, with more AGPR copies)
-                __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 4, 0);
+                __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
                 __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2, 0);
             }
             bf16x8 pb[2], db[2];
