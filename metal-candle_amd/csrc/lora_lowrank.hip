@@ -1433,24 +1433,14 @@ hipError_t launch_colreduce_bf16(int64_t T, const ColJob* jobs, int n, hipStream
     // Ranks are processed in groups of up to 64 (four 16-row MFMA tiles of
     // accumulators); each group reads X once, so r <= 64 takes one pass. The
     // groups are binned by their rank tiles (16, 32, 48 or 64 rows), one
-    // launch per bin of up to kColJobs groups.
-    constexpr int GS = 64;
-    ColJobDev bins[4][8 * kColJobs];
+    // launch per kColJobs groups of a bin; a full bin is launched before
+    // more groups are queued (a rank of 8192 has 128 groups). Every group
+    // writes its own partial rows, so the launch order does not matter.
+    constexpr int GS = 64, CAP = 8 * kColJobs;
+    ColJobDev bins[4][CAP];
     int nb[4] = {0, 0, 0, 0};
-    for (int i = 0; i < n; ++i) {
-        const ColJob& J = jobs[i];
-        if (!J.X) continue;
-        const int64_t stride = (int64_t)colreduce_rows(J.r) * J.C;
-        for (int g = 0; g * GS < J.r; ++g) {
-            const int rs = J.r - GS * g < GS ? J.r - GS * g : GS;
-            const int bin = rs <= 16 ? 0 : rs <= 32 ? 1 : rs <= 48 ? 2 : 3;
-            ColJobDev d{J.X, J.C, J.Pt + (int64_t)GS * g * T, rs, round_up((T + J.splits - 1) / J.splits, 32),
-                        J.partial + (int64_t)GS * g * J.C, stride, (int)((J.C + 127) / 128), J.splits};
-            if (nb[bin] < 8 * kColJobs) bins[bin][nb[bin]++] = d;
-        }
-    }
     const bool ptv = (T & 3) == 0;
-    for (int bin = 0; bin < 4; ++bin) {
+    auto flush = [&](int bin) -> hipError_t {
         for (int first = 0; first < nb[bin]; first += kColJobs) {
             ColBatch cb{};
             cb.njobs = std::min(kColJobs, nb[bin] - first);
@@ -1475,6 +1465,29 @@ hipError_t launch_colreduce_bf16(int64_t T, const ColJob* jobs, int n, hipStream
             hipError_t e = hipGetLastError();
             if (e != hipSuccess) return e;
         }
+        nb[bin] = 0;
+        return hipSuccess;
+    };
+    for (int i = 0; i < n; ++i) {
+        const ColJob& J = jobs[i];
+        if (!J.X) continue;
+        const int64_t stride = (int64_t)colreduce_rows(J.r) * J.C;
+        for (int g = 0; g * GS < J.r; ++g) {
+            const int rs = J.r - GS * g < GS ? J.r - GS * g : GS;
+            const int bin = rs <= 16 ? 0 : rs <= 32 ? 1 : rs <= 48 ? 2 : 3;
+            if (nb[bin] == CAP) {
+                const hipError_t e = flush(bin);
+                if (e != hipSuccess) return e;
+            }
+            bins[bin][nb[bin]++] = ColJobDev{J.X, J.C, J.Pt + (int64_t)GS * g * T, rs,
+                                             round_up((T + J.splits - 1) / J.splits, 32),
+                                             J.partial + (int64_t)GS * g * J.C, stride, (int)((J.C + 127) / 128),
+                                             J.splits};
+        }
+    }
+    for (int bin = 0; bin < 4; ++bin) {
+        const hipError_t e = flush(bin);
+        if (e != hipSuccess) return e;
     }
     return hipSuccess;
 }
@@ -1495,26 +1508,12 @@ int colsplit_splits(int64_t T, int64_t C) {
 hipError_t launch_colsplit_bf16(int64_t T, const ColsplitJob* jobs, int n, hipStream_t stream) {
     // Ranks in groups of up to 64 (four 16-row MFMA tiles of accumulators),
     // each group one pass over X, binned by its rank tiles; one launch per
-    // bin of up to kColJobs groups.
+    // kColJobs groups of a bin, a full bin launched before more are queued.
     if (T % 8 != 0) return hipErrorInvalidValue;
-    constexpr int GS = 64;
-    ColsplitJobDev bins[4][8 * kColJobs];
+    constexpr int GS = 64, CAP = 8 * kColJobs;
+    ColsplitJobDev bins[4][CAP];
     int nb[4] = {0, 0, 0, 0};
-    for (int i = 0; i < n; ++i) {
-        const ColsplitJob& J = jobs[i];
-        if (!J.X) continue;
-        if (J.splits < 1 || J.C % 8 != 0 || J.C >= ((int64_t)1 << 22)) return hipErrorInvalidValue;
-        const int64_t stride = (int64_t)colreduce_rows(J.r) * J.C;
-        for (int g = 0; g * GS < J.r; ++g) {
-            const int rs = J.r - GS * g < GS ? J.r - GS * g : GS;
-            const int bin = rs <= 16 ? 0 : rs <= 32 ? 1 : rs <= 48 ? 2 : 3;
-            ColsplitJobDev d{J.X, J.C, J.P_hi + (int64_t)GS * g * T, J.P_lo + (int64_t)GS * g * T, rs,
-                             round_up((T + J.splits - 1) / J.splits, 32), J.partial + (int64_t)GS * g * J.C, stride,
-                             (int)((J.C + 511) / 512), J.splits};
-            if (nb[bin] < 8 * kColJobs) bins[bin][nb[bin]++] = d;
-        }
-    }
-    for (int bin = 0; bin < 4; ++bin) {
+    auto flush = [&](int bin) -> hipError_t {
         for (int first = 0; first < nb[bin]; first += kColJobs) {
             ColsplitBatch cb{};
             cb.njobs = std::min(kColJobs, nb[bin] - first);
@@ -1532,6 +1531,30 @@ hipError_t launch_colsplit_bf16(int64_t T, const ColsplitJob* jobs, int n, hipSt
             const hipError_t e = hipGetLastError();
             if (e != hipSuccess) return e;
         }
+        nb[bin] = 0;
+        return hipSuccess;
+    };
+    for (int i = 0; i < n; ++i) {
+        const ColsplitJob& J = jobs[i];
+        if (!J.X) continue;
+        if (J.splits < 1 || J.C % 8 != 0 || J.C >= ((int64_t)1 << 22)) return hipErrorInvalidValue;
+        const int64_t stride = (int64_t)colreduce_rows(J.r) * J.C;
+        for (int g = 0; g * GS < J.r; ++g) {
+            const int rs = J.r - GS * g < GS ? J.r - GS * g : GS;
+            const int bin = rs <= 16 ? 0 : rs <= 32 ? 1 : rs <= 48 ? 2 : 3;
+            if (nb[bin] == CAP) {
+                const hipError_t e = flush(bin);
+                if (e != hipSuccess) return e;
+            }
+            bins[bin][nb[bin]++] = ColsplitJobDev{J.X, J.C, J.P_hi + (int64_t)GS * g * T, J.P_lo + (int64_t)GS * g * T,
+                                                  rs, round_up((T + J.splits - 1) / J.splits, 32),
+                                                  J.partial + (int64_t)GS * g * J.C, stride, (int)((J.C + 511) / 512),
+                                                  J.splits};
+        }
+    }
+    for (int bin = 0; bin < 4; ++bin) {
+        const hipError_t e = flush(bin);
+        if (e != hipSuccess) return e;
     }
     return hipSuccess;
 }

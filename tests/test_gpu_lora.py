@@ -143,6 +143,9 @@ def test_fused_dy_pass(mc, dev, name, T, K, N, r, p):
     # column reductions in groups of 64
     ("rank 200, dropout", 3000, 512, 384, 200, 0.1),
     ("rank 257, no dropout", 2048, 256, 520, 257, 0.0),
+    # more than 64 groups of 64 ranks in one column-reduction bin (a full
+    # bin is launched before the rest are queued)
+    ("rank 4200, dropout", 264, 64, 72, 4200, 0.1),
 ])
 def test_rank_above_128(mc, dev, name, T, K, N, r, p):
     c = lora_case(zlib.crc32(name.encode()), T, K, N, r)

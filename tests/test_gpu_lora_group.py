@@ -99,6 +99,9 @@ def _check_group(mc, dev, T, K, Ns, r, p, seed, scale=2.0, bias=True, no_w=(), s
     # split row projection (K >= 4096) over passes of 48 + 24 ranks (one
     # launch, the second pass's operand 32 rows), ragged T, dropout
     ("r24 three projections, passes of 48 + 24", 2000, 4104, [136, 264, 72], 24, 0.1),
+    # dA over the group's 3 x 1500 ranks in one column reduction: more than
+    # 64 groups of 64 ranks, so a full bin launches before the rest queue
+    ("r1500 three projections", 264, 64, [72, 64, 80], 1500, 0.0),
 ])
 def test_group_matches_single_calls(mc, dev, name, T, K, Ns, r, p):
     _check_group(mc, dev, T, K, Ns, r, p, zlib.crc32(name.encode()) % 1000)
