@@ -1287,8 +1287,9 @@ hipError_t launch_prep_bf16(const PrepJob* jobs, int n, hipStream_t stream) {
     PrepBatch b{};
     int k = 0;
     bool vec8 = true;
-    for (int i = 0; i < n && k < kPrepJobs; ++i) {
+    for (int i = 0; i < n; ++i) {
         if (!jobs[i].hi) continue;
+        if (k == kPrepJobs) return hipErrorInvalidValue;
         b.job[k] = jobs[i];
         if (b.job[k].ld_out == 0) b.job[k].ld_out = b.job[k].cols_out;
         vec8 = vec8 && prep_vec8(b.job[k]);
@@ -1367,6 +1368,7 @@ hipError_t launch_lora_bwd_operands(const OperandsCall* calls, int n, int64_t T,
                                     float keep, int rext_p, int ext_ld, hipStream_t stream) {
     // row projection blocks as launch_rowproj_bf16 chooses them for one
     // projection's r ranks; B rows past r load as zeros
+    if (n < 1 || n > kMaxProj) return hipErrorInvalidValue;
     const int rc = rowproj_rc(r);
     const int rows_per_block = rc == 8 ? 32 : 64;
     OperandsBatch ob{};
@@ -1560,10 +1562,23 @@ hipError_t launch_colsplit_bf16(int64_t T, const ColsplitJob* jobs, int n, hipSt
 }
 
 hipError_t launch_split_sum(const SumJob* jobs, int n, hipStream_t stream) {
+    // one launch per kSumJobs jobs with an output
+    int first = 0, valid = 0;
+    for (int i = 0; i < n; ++i) {
+        if (!jobs[i].out) continue;
+        if (++valid > kSumJobs) {
+            const hipError_t e = launch_split_sum(jobs + first, i - first, stream);
+            if (e != hipSuccess) return e;
+            first = i;
+            valid = 1;
+        }
+    }
+    n -= first;
+    jobs += first;
     SumBatch sb{};
     int k = 0;
     bool vec4 = true;
-    for (int i = 0; i < n && k < kSumJobs; ++i) {
+    for (int i = 0; i < n; ++i) {
         if (!jobs[i].out) continue;
         const SumJob& J = jobs[i];
         // a split's partial is one buffer resource with 32-bit offsets
@@ -1602,9 +1617,10 @@ hipError_t launch_dy_pass(int64_t T, int r, const DyJob* jobs, int n, hipStream_
     DyBatch db{};
     db.r = r;
     int k = 0;
-    for (int i = 0; i < n && k < kMaxProj; ++i) {
+    for (int i = 0; i < n; ++i) {
         const DyJob& J = jobs[i];
         if (!J.dY || (!J.partB && !J.gpart)) continue;
+        if (k == kMaxProj) return hipErrorInvalidValue;
         const int splits = dy_splits(T, J.N);
         DyJobDev d{J.dY, J.N, J.B, J.Pt, J.partB, J.gpart, round_up((T + splits - 1) / splits, 32),
                    (int64_t)colreduce_rows(r) * J.N, dy_groups(J.N)};
@@ -1633,11 +1649,15 @@ hipError_t launch_dy_finish(int64_t T, int r, float scale, float keep, int rext,
     DyFinishBatch fb{};
     fb.r = r; fb.rext = rext; fb.ext_ld = ext_ld; fb.scale = scale; fb.keep = keep; fb.ext_scale = ext_scale;
     fb.blocks_per_job = (int)((T + 63) / 64);
-    for (int i = 0; i < n && fb.njobs < kMaxProj; ++i)
-        if (jobs[i].gpart && (jobs[i].gd_t || jobs[i].gd_ext || jobs[i].gd_hi)) fb.job[fb.njobs++] = jobs[i];
+    for (int i = 0; i < n; ++i) {
+        if (!(jobs[i].gpart && (jobs[i].gd_t || jobs[i].gd_ext || jobs[i].gd_hi))) continue;
+        if (fb.njobs == kMaxProj) return hipErrorInvalidValue;
+        fb.job[fb.njobs++] = jobs[i];
+    }
     bool vec8 = true;
-    for (int i = 0; i < npreps && fb.npreps < kPrepJobs; ++i) {
+    for (int i = 0; i < npreps; ++i) {
         if (!preps[i].hi) continue;
+        if (fb.npreps == kPrepJobs) return hipErrorInvalidValue;
         PrepJob p = preps[i];
         if (p.ld_out == 0) p.ld_out = p.cols_out;
         vec8 = vec8 && prep_vec8(p);
