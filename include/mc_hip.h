@@ -99,7 +99,8 @@ size_t mc_lora_bwd_workspace_size(const mc_lora_desc* d);
 /* y = x W^T + bias + scale * ((x A) (.) mask / (1-p)) B.
  * W == NULL: delta only (exactly what FusedLoRAOp computes); bias may be NULL.
  * h_save [r, T] fp32 (may be NULL) receives Hd^T = ((x A) (.) mask/(1-p))^T,
- * the saved activation mc_lora_bwd needs for dB. */
+ * the saved activation mc_lora_bwd needs for dB. bf16 K or N not a multiple
+ * of 8 runs on zero-padded copies in the workspace (mc_lora_bwd likewise). */
 mc_status mc_lora_fwd(const mc_lora_desc* d, const void* x, const void* W, const void* bias,
                       const float* A, const float* B, const uint8_t* mask,
                       void* y, float* h_save, void* workspace, size_t workspace_bytes,

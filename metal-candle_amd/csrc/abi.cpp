@@ -70,9 +70,8 @@ mc_status check_lora_desc(const mc_lora_desc* d) {
     // LoRAConfig::validate: "LoRA dropout must be in [0, 1)" (lora.rs:113-118)
     MC_CHECK(d->dropout_p >= 0.0f && d->dropout_p < 1.0f, MC_ERR_VALUE, "LoRA dropout must be in [0, 1)");
     if (d->act_dtype == MC_BF16) {
-        MC_CHECK(d->in_features % 8 == 0 && d->out_features % 8 == 0, MC_ERR_SHAPE,
-                 "LoRA bf16: in_features (%lld) and out_features (%lld) must be multiples of 8",
-                 (long long)d->in_features, (long long)d->out_features);
+        // (K or N not a multiple of 8: mc_lora_fwd / mc_lora_bwd run the
+        // kernels on zero-padded copies; grouped calls require multiples of 8.)
         // The bf16 kernels address a workgroup's block of rows (256 GEMM rows
         // of up to max(K, N) features, 32 rank rows of T fp32 values) through
         // buffer resources with 32-bit byte offsets.
@@ -231,6 +230,10 @@ mc_status check_lora_group(const mc_lora_desc* d, const mc_lora_proj* projs, int
         per_proj->out_features = projs[g].out_features;
         mc_status s = check_lora_desc(per_proj);
         if (s != MC_OK) return s;
+        MC_CHECK(d->in_features % 8 == 0 && projs[g].out_features % 8 == 0, MC_ERR_SHAPE,
+                 "%s: projection %d: in_features (%lld) and out_features (%lld) must be multiples of 8 "
+                 "(mc_lora_fwd / mc_lora_bwd take any size)",
+                 op, (int)g, (long long)d->in_features, (long long)projs[g].out_features);
         MC_CHECK(projs[g].A && projs[g].B, MC_ERR_NULL, "%s: projection %d: A and B must not be NULL", op, (int)g);
         MC_CHECK(!projs[g].bias || projs[g].W, MC_ERR_NULL, "%s: projection %d: bias given without W", op, (int)g);
         MC_CHECK(d->dropout_p == 0.0f || projs[g].mask, MC_ERR_NULL,

@@ -134,9 +134,90 @@ bool bwd_rowsplit(const Dims& m, const int64_t* N, int count) {
 // operand path, whose per-step operand split is the kernel's bottleneck.
 bool bwd_colsplit(const Dims& m, const int64_t* N, int count) { return bwd_rowsplit(m, N, count) && m.T % 8 == 0; }
 
+// bf16 projections whose K or N is not a multiple of 8 (rows not made of
+// 16-byte chunks) run on copies zero-padded to multiples of 8: a padded
+// feature adds exact zeros to every product, so y, dX, dA and dB are the
+// padded results' leading rows / columns.
+bool bf16_padded(const mc_lora_desc& d) {
+    return d.act_dtype == MC_BF16 && (d.in_features % 8 != 0 || d.out_features % 8 != 0);
+}
+mc_lora_desc padded_desc(const mc_lora_desc& d) {
+    mc_lora_desc p = d;
+    p.in_features = round_up(d.in_features, 8);
+    p.out_features = round_up(d.out_features, 8);
+    return p;
+}
+// dst [rows_p][cols_p] = src [rows][cols] (row-major), zero elsewhere
+template <typename T>
+__global__ __launch_bounds__(256) void pad_copy(const T* __restrict__ src, int64_t rows, int64_t cols,
+                                                T* __restrict__ dst, int64_t rows_p, int64_t cols_p) {
+    const int64_t n = rows_p * cols_p;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = i / cols_p, c = i - r * cols_p;
+        dst[i] = r < rows && c < cols ? src[r * cols + c] : T(0);
+    }
+}
+// dst [rows][cols] = the leading block of src [.][cols_p]
+template <typename T>
+__global__ __launch_bounds__(256) void unpad_copy(const T* __restrict__ src, int64_t cols_p, T* __restrict__ dst,
+                                                  int64_t rows, int64_t cols) {
+    const int64_t n = rows * cols;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = i / cols, c = i - r * cols;
+        dst[i] = src[r * cols_p + c];
+    }
+}
+unsigned copy_blocks(int64_t n) { return (unsigned)std::max<int64_t>(1, std::min<int64_t>((n + 255) / 256, 4096)); }
+template <typename T>
+hipError_t pad(const void* src, int64_t rows, int64_t cols, void* dst, int64_t rows_p, int64_t cols_p,
+               hipStream_t st) {
+    pad_copy<T><<<copy_blocks(rows_p * cols_p), 256, 0, st>>>(static_cast<const T*>(src), rows, cols,
+                                                               static_cast<T*>(dst), rows_p, cols_p);
+    return hipGetLastError();
+}
+template <typename T>
+hipError_t unpad(const void* src, int64_t cols_p, void* dst, int64_t rows, int64_t cols, hipStream_t st) {
+    unpad_copy<T><<<copy_blocks(rows * cols), 256, 0, st>>>(static_cast<const T*>(src), cols_p, static_cast<T*>(dst),
+                                                            rows, cols);
+    return hipGetLastError();
+}
+// Buffers of a padded call after the inner call's workspace (byte offsets):
+// x [T][Kp], W [Np][Kp], bias [Np] (bf16), A [Kp][r], B [r][Np] (fp32), then
+// the forward's y [T][Np], or the backward's dY [T][Np], dX [T][Kp] (bf16),
+// dA [Kp][r], dB [r][Np] (fp32).
+struct PadWs {
+    size_t x, w, bias, a, b, y, dy, dx, da, db, total;
+};
+PadWs pad_ws(const mc_lora_desc& d, size_t inner, bool bwd) {
+    const size_t T = (size_t)d.tokens, r = (size_t)d.rank;
+    const size_t Kp = (size_t)round_up(d.in_features, 8), Np = (size_t)round_up(d.out_features, 8);
+    PadWs w{};
+    size_t off = align256(inner);
+    w.x = off;    off += align256(T * Kp * 2);
+    w.w = off;    off += align256(Np * Kp * 2);
+    w.bias = off; off += align256(Np * 2);
+    w.a = off;    off += align256(Kp * r * 4);
+    w.b = off;    off += align256(r * Np * 4);
+    if (!bwd) {
+        w.y = off;  off += align256(T * Np * 2);
+    } else {
+        w.dy = off; off += align256(T * Np * 2);
+        w.dx = off; off += align256(T * Kp * 2);
+        w.da = off; off += align256(Kp * r * 4);
+        w.db = off; off += align256(r * Np * 4);
+    }
+    w.total = off;
+    return w;
+}
+
 }  // namespace
 
 LoraFwdWs lora_fwd_ws(const mc_lora_desc& d) {
+    if (bf16_padded(d)) {
+        LoraFwdWs w{};
+        w.total = pad_ws(d, lora_fwd_ws(padded_desc(d)).total, false).total;
+        return w;
+    }
     const Dims m = dims_of(d);
     LoraFwdWs w{};
     size_t off = 0;
@@ -153,6 +234,11 @@ LoraFwdWs lora_fwd_ws(const mc_lora_desc& d) {
 }
 
 LoraBwdWs lora_bwd_ws(const mc_lora_desc& d) {
+    if (bf16_padded(d)) {
+        LoraBwdWs w{};
+        w.total = pad_ws(d, lora_bwd_ws(padded_desc(d)).total, true).total;
+        return w;
+    }
     const Dims m = dims_of(d);
     LoraBwdWs w{};
     size_t off = 0;
@@ -232,6 +318,22 @@ LoraGroupBwdWs lora_group_bwd_ws(const mc_lora_desc& d, const int64_t* N, int co
 hipError_t launch_lora_fwd(const mc_lora_desc& d, const void* x, const void* W, const void* bias,
                            const float* A, const float* B, const uint8_t* mask, void* y,
                            float* h_save, void* ws, hipStream_t st) {
+    if (bf16_padded(d)) {
+        const mc_lora_desc dp = padded_desc(d);
+        const int64_t T = d.tokens, K = d.in_features, N = d.out_features, r = d.rank;
+        const int64_t Kp = dp.in_features, Np = dp.out_features;
+        const PadWs p = pad_ws(d, lora_fwd_ws(dp).total, false);
+        char* base = static_cast<char*>(ws);
+        MC_TRY(pad<uint16_t>(x, T, K, base + p.x, T, Kp, st));
+        if (W) MC_TRY(pad<uint16_t>(W, N, K, base + p.w, Np, Kp, st));
+        if (bias) MC_TRY(pad<uint16_t>(bias, 1, N, base + p.bias, 1, Np, st));
+        MC_TRY(pad<float>(A, K, r, base + p.a, Kp, r, st));
+        MC_TRY(pad<float>(B, r, N, base + p.b, r, Np, st));
+        MC_TRY(launch_lora_fwd(dp, base + p.x, W ? base + p.w : nullptr, bias ? base + p.bias : nullptr,
+                               reinterpret_cast<const float*>(base + p.a), reinterpret_cast<const float*>(base + p.b),
+                               mask, base + p.y, h_save, ws, st));
+        return unpad<uint16_t>(base + p.y, Np, y, T, N, st);
+    }
     const Dims m = dims_of(d);
     const LoraFwdWs w = lora_fwd_ws(d);
     char* base = static_cast<char*>(ws);
@@ -264,6 +366,27 @@ hipError_t launch_lora_bwd(const mc_lora_desc& d, const void* x, const void* W, 
                            const float* B, const uint8_t* mask, const float* h_save,
                            const void* dY, void* dX, float* dA, float* dB, void* ws,
                            hipStream_t st) {
+    if (bf16_padded(d)) {
+        const mc_lora_desc dp = padded_desc(d);
+        const int64_t T = d.tokens, K = d.in_features, N = d.out_features, r = d.rank;
+        const int64_t Kp = dp.in_features, Np = dp.out_features;
+        const PadWs p = pad_ws(d, lora_bwd_ws(dp).total, true);
+        char* base = static_cast<char*>(ws);
+        if (x) MC_TRY(pad<uint16_t>(x, T, K, base + p.x, T, Kp, st));
+        if (W) MC_TRY(pad<uint16_t>(W, N, K, base + p.w, Np, Kp, st));
+        MC_TRY(pad<float>(A, K, r, base + p.a, Kp, r, st));
+        MC_TRY(pad<float>(B, r, N, base + p.b, r, Np, st));
+        MC_TRY(pad<uint16_t>(dY, T, N, base + p.dy, T, Np, st));
+        MC_TRY(launch_lora_bwd(dp, x ? base + p.x : nullptr, W ? base + p.w : nullptr,
+                               reinterpret_cast<const float*>(base + p.a), reinterpret_cast<const float*>(base + p.b),
+                               mask, h_save, base + p.dy, dX ? base + p.dx : nullptr,
+                               dA ? reinterpret_cast<float*>(base + p.da) : nullptr,
+                               dB ? reinterpret_cast<float*>(base + p.db) : nullptr, ws, st));
+        if (dX) MC_TRY(unpad<uint16_t>(base + p.dx, Kp, dX, T, K, st));
+        if (dA) MC_TRY(unpad<float>(base + p.da, r, dA, K, r, st));
+        if (dB) MC_TRY(unpad<float>(base + p.db, Np, dB, r, N, st));
+        return hipSuccess;
+    }
     const Dims m = dims_of(d);
     const float keep = mask ? 1.0f / (1.0f - d.dropout_p) : 1.0f;
     if (m.bf16) {

@@ -28,7 +28,6 @@ def _desc(mc, T=16, K=16, N=16, r=4, scale=2.0, p=0.0, dtype=1):
     ("rank", 8193, 2, "exceeds the supported maximum 8192"),
     ("tokens", 0, 2, "must be >= 1"),
     ("act_dtype", 7, 3, "unsupported act_dtype"),
-    ("in_features", 12, 2, "multiples of 8"),
     ("out_features", 1 << 22, 2, "must be below 2^22"),   # 32-bit buffer offsets of the bf16 kernels
     ("tokens", 1 << 24, 2, "must be below 2^24"),
 ])
@@ -193,11 +192,15 @@ def test_lora_group_validation(mc):
     d32 = _desc(mc, T=16, K=16, N=0, r=4, dtype=0)
     assert L.mc_lora_group_fwd(ctypes.byref(d32), w, projs, 2, ys, hs, w, need_f, None) == 3
     assert "bf16 only" in mc._lib.last_error()
-    # a projection's N not a multiple of 8
+    # a projection's N, or K, not a multiple of 8 (single calls pad; groups do not)
     projs[1].out_features = 20
     assert L.mc_lora_group_fwd_workspace_size(ctypes.byref(d), projs, 2) == 0
     assert L.mc_lora_group_fwd(ctypes.byref(d), w, projs, 2, ys, hs, w, need_f, None) == 2
+    assert "multiples of 8" in mc._lib.last_error()
     projs[1].out_features = 24
+    d.in_features = 20
+    assert L.mc_lora_group_fwd(ctypes.byref(d), w, projs, 2, ys, hs, w, need_f, None) == 2
+    d.in_features = 16
     # missing B, bias without W, dropout without a mask
     projs[0].B = None
     assert L.mc_lora_group_fwd(ctypes.byref(d), w, projs, 2, ys, hs, w, need_f, None) == 1
@@ -269,3 +272,22 @@ def test_attention_bwd_workspace_groups(mc, B, S, H, Hkv, causal, groups):
         want += 2 * _a256(B * Hkv * groups * S * D * 4)
     want += _a256(B * H * S * ((S + 127) // 128 * 128) * 2)
     assert L.mc_attention_bwd_workspace_size(ctypes.byref(d)) == want
+
+
+def test_lora_odd_features_padded_workspace(mc):
+    """bf16 K or N not a multiple of 8: the single-projection calls accept the
+    shape and run on zero-padded copies, whose buffers extend the padded
+    shape's workspace."""
+    L = mc._lib.lib()
+    T, r = 300, 8
+    for K, N in ((37, 45), (40, 45), (37, 48)):
+        d = _desc(mc, T=T, K=K, N=N, r=r)
+        Kp, Np = (K + 7) // 8 * 8, (N + 7) // 8 * 8
+        dp = _desc(mc, T=T, K=Kp, N=Np, r=r)
+        inner_f = L.mc_lora_fwd_workspace_size(ctypes.byref(dp))
+        inner_b = L.mc_lora_bwd_workspace_size(ctypes.byref(dp))
+        bufs = _a256(T * Kp * 2) + _a256(Np * Kp * 2) + _a256(Np * 2) + _a256(Kp * r * 4) + _a256(r * Np * 4)
+        assert L.mc_lora_fwd_workspace_size(ctypes.byref(d)) == _a256(inner_f) + bufs + _a256(T * Np * 2)
+        assert L.mc_lora_bwd_workspace_size(ctypes.byref(d)) == (_a256(inner_b) + bufs + _a256(T * Np * 2) +
+                                                                 _a256(T * Kp * 2) + _a256(Kp * r * 4) +
+                                                                 _a256(r * Np * 4))

@@ -95,6 +95,25 @@ def test_delta_only(mc, dev, dtype):
     _check(mc, dev, c, 2.0, F32_TOL if dtype == torch.float32 else BF16_TOL)
 
 
+@pytest.mark.parametrize("name,T,K,N,r,p,bias,w", [
+    # bf16 K or N not a multiple of 8 (the reference takes any shape,
+    # custom_ops.rs:118-148): the single-projection calls run on copies
+    # zero-padded to multiples of 8
+    ("K 37 N 45, bias, dropout", 300, 37, 45, 8, 0.1, True, True),
+    ("K 40 N 45", 257, 40, 45, 16, 0.0, False, True),
+    ("K 1001 N 8", 1000, 1001, 8, 4, 0.0, True, True),
+    ("K 37 N 45 delta only", 130, 37, 45, 8, 0.0, False, False),
+    ("K 3 N 5 rank 70", 64, 3, 5, 70, 0.2, True, True),
+])
+def test_bf16_features_not_multiple_of_8(mc, dev, name, T, K, N, r, p, bias, w):
+    c = lora_case(zlib.crc32(name.encode()), T, K, N, r, bias=bias, w=w)
+    if not w:
+        c["B"] = c["B"] * 50  # make the delta O(1)
+    mask = mc.dropout_mask(zlib.crc32(name.encode()), p, T, r).numpy() if p > 0 else None
+    y, h, dX, dA, dB = _check(mc, dev, c, 2.0, BF16_TOL, mask=mask, p=p)
+    assert y.shape == (T, N) and dX.shape == (T, K) and dA.shape == (K, r) and dB.shape == (r, N)
+
+
 def test_zero_B_gives_base(mc, dev):
     """B = 0 => delta = 0 (lora.rs:244, lora.rs:656-659): y equals the base linear."""
     c = lora_case(6, 256, 256, 384, 8)
