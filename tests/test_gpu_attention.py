@@ -253,8 +253,9 @@ def test_attention_bwd_deterministic(mc, dev):
     assert all(torch.equal(x, y) for x, y in zip(a, b))
 
 
-@pytest.mark.parametrize("B,H,Hkv,S,causal", [(16, 4, 2, 2048, True), (8, 8, 4, 1024, False)])
-def test_attention_bwd_whole_kv_group(mc, dev, B, H, Hkv, S, causal):
+@pytest.mark.parametrize("B,H,Hkv,S,causal,masked", [(16, 4, 2, 2048, True, False), (8, 8, 4, 1024, False, False),
+                                                      (32, 4, 2, 1024, True, True)])
+def test_attention_bwd_whole_kv_group(mc, dev, B, H, Hkv, S, causal, masked):
     """Shapes whose dK/dV workgroups take all H/Hkv query heads of a K/V head
     (no partials, no summing launch; the workspace test pins the choice):
     one K/V group of two batches against the oracle, every head's dK summing
@@ -265,20 +266,24 @@ def test_attention_bwd_whole_kv_group(mc, dev, B, H, Hkv, S, causal):
     k = torch.randn(B, Hkv, S, D, generator=g).to(torch.bfloat16)
     v = torch.randn(B, Hkv, S, D, generator=g).to(torch.bfloat16)
     dout = torch.randn(B, S, H * D, generator=g).to(torch.bfloat16)
-    dq, dk, dv = run_bwd(mc, dev, q, k, v, None, causal, dout)
+    mask = None
+    if masked:  # additive mask with padded keys, shared by every head
+        mask = torch.randn(S, S, generator=g)
+        mask[:, S - 5:] = float("-inf")
+    dq, dk, dv = run_bwd(mc, dev, q, k, v, mask, causal, dout)
     rep = H // Hkv
     for b, hk in ((0, 0), (B - 1, Hkv - 1)):
         hs = slice(hk * rep, (hk + 1) * rep)
         rq, rk, rv = oracle.attention_bwd(q[b:b + 1, hs].float().numpy(), k[b:b + 1, hk:hk + 1].float().numpy(),
                                           v[b:b + 1, hk:hk + 1].float().numpy(),
                                           dout[b:b + 1].view(1, S, H, D)[:, :, hs].reshape(1, S, rep * D).float().numpy(),
-                                          D ** -0.5, causal=causal)
+                                          D ** -0.5, causal=causal, mask=None if mask is None else mask.numpy())
         assert rel_err(dq[b:b + 1, hs], rq) <= BF16_TOL
         assert rel_err(dk[b:b + 1, hk:hk + 1], rk) <= BF16_TOL
         assert rel_err(dv[b:b + 1, hk:hk + 1], rv) <= BF16_TOL
     ksum = dk.float().sum(dim=2)
     assert float(ksum.abs().max()) <= 2e-2 * float(dk.float().abs().max()) * 8
-    again = run_bwd(mc, dev, q, k, v, None, causal, dout)
+    again = run_bwd(mc, dev, q, k, v, mask, causal, dout)
     assert all(torch.equal(x, y) for x, y in zip((dq, dk, dv), again))
 
 
