@@ -750,17 +750,21 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_bf16(AttnBwdArgs a) {
             f32x16 sacc, dpacc;
 #pragma unroll
             for (int j = 0; j < 16; ++j) sacc[j] = dpacc[j] = 0.f;
+            // Q and dO fragments one k-chunk ahead of their MFMAs, so each
+            // pair's LDS latency runs under the previous pair's MFMAs
+            bf16x8 qf[2], df[2];
+            qf[0] = frag_at(sq + 32 * t * D, roff[0]);
+            df[0] = frag_at(sdo + 32 * t * D, roff[0]);
+            __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
 #pragma unroll
             for (int s = 0; s < KS; ++s) {
-                sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_at(sq + 32 * t * D, roff[s]), kf[s], sacc, 0, 0,
-                                                              0);
-                dpacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_at(sdo + 32 * t * D, roff[s]), vf[s], dpacc, 0, 0,
-                                                               0);
-                // each k-chunk's fragment reads right before its MFMAs (and
-                // below, each dV/dK pair's): left free, the scheduler keeps
-                // more fragments live (D = 128: 256 VGPRs + 188 AGPRs against
-                // 252 + 160, with more AGPR copies)
-                __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
+                if (s + 1 < KS) {
+                    qf[(s + 1) & 1] = frag_at(sq + 32 * t * D, roff[s + 1]);
+                    df[(s + 1) & 1] = frag_at(sdo + 32 * t * D, roff[s + 1]);
+                    __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
+                }
+                sacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qf[s & 1], kf[s], sacc, 0, 0, 0);
+                dpacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(df[s & 1], vf[s], dpacc, 0, 0, 0);
                 __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2, 0);
             }
             bf16x8 pb[2], db[2];
@@ -783,18 +787,27 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_bf16(AttnBwdArgs a) {
                     }
                 }
             }
+            // dO^T and Q^T fragments (two transposed reads each) one step
+            // ahead of their MFMAs; step u = 2 dt + kk
+            bf16x8 ot[2], qt[2];
+            auto tr_frags = [&](int u, int slot) {
+                const int dt = u >> 1, r0 = (32 * t + 16 * (u & 1)) * D;
+                ot[slot] = frag_tr_at(sdo + r0, troff[dt][0], troff[dt][1]);
+                qt[slot] = frag_tr_at(sq + r0, troff[dt][0], troff[dt][1]);
+            };
+            tr_frags(0, 0);
+            __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 4, 0);
 #pragma unroll
-            for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-                for (int kk = 0; kk < 2; ++kk) {
-                    const int r0 = (32 * t + 16 * kk) * D;
-                    dvacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                        frag_tr_at(sdo + r0, troff[dt][0], troff[dt][1]), pb[kk], dvacc[dt], 0, 0, 0);
-                    dkacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                        frag_tr_at(sq + r0, troff[dt][0], troff[dt][1]), db[kk], dkacc[dt], 0, 0, 0);
+            for (int u = 0; u < 2 * DT; ++u) {
+                if (u + 1 < 2 * DT) {
+                    tr_frags(u + 1, (u + 1) & 1);
                     __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 4, 0);
-                    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2, 0);
                 }
+                const int dt = u >> 1, kk = u & 1;
+                dvacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ot[u & 1], pb[kk], dvacc[dt], 0, 0, 0);
+                dkacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qt[u & 1], db[kk], dkacc[dt], 0, 0, 0);
+                __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2, 0);
+            }
         };
         tile(std::integral_constant<int, 0>{});
         tile(std::integral_constant<int, 1>{});
