@@ -633,24 +633,6 @@ hipError_t launch_lora_group_bwd(const mc_lora_desc& d, const void* x, const Lor
             if (need_g)
                 MC_TRY(launch_dy_finish(m.T, m.r, d.scale, keep, m.rext, ext_ld, 1.0f, fin, count, preps, count, st));
         }
-        if (dX) {
-            for (int g = 0; g < count; ++g)
-                if (need_wt[g])  // W^T into the workspace (none when the caller holds it)
-                    MC_TRY(launch_transpose_bf16(proj[g].W, Ns[g], m.K, base + w.wt[g], st));
-            GemmSeg segs[kGemmMaxSeg];
-            int nseg = 0;
-            int64_t kbase = 0;
-            for (int g = 0; g < count; ++g)
-                if (proj[g].W) {
-                    const uint16_t* wt = proj[g].Wt ? static_cast<const uint16_t*>(proj[g].Wt)
-                                                    : reinterpret_cast<const uint16_t*>(base + w.wt[g]);
-                    segs[nseg++] = GemmSeg{static_cast<const uint16_t*>(dY[g]), Ns[g], wt, Ns[g], Ns[g]};
-                    kbase += Ns[g];
-                }
-            segs[nseg++] = GemmSeg{gd, ext_ld, at, ext_ld, ext_ld};
-            auto sc = gemm_scope(st, m.T, m.K, kbase, ext_ld, rtot, 2);
-            MC_TRY(launch_gemm_bf16(m.T, m.K, segs, nseg, nullptr, static_cast<uint16_t*>(dX), m.K, st));
-        }
         if (any_dA || any_dB) {
             // dA_g = x^T.Gd_g for every g from one pass over x (all ranks),
             // then the fixed-order split sums of dA and dB
@@ -673,6 +655,24 @@ hipError_t launch_lora_group_bwd(const mc_lora_desc& d, const void* x, const Lor
                     sj[ns++] = SumJob{reinterpret_cast<float*>(base + w.part_b[g]), dy_splits(m.T, Ns[g]), Ns[g],
                                       (int64_t)colreduce_rows(m.r) * Ns[g], m.r, d.scale, false, dB[g]};
             MC_TRY(launch_split_sum(sj, ns, st));
+        }
+        if (dX) {
+            for (int g = 0; g < count; ++g)
+                if (need_wt[g])  // W^T into the workspace (none when the caller holds it)
+                    MC_TRY(launch_transpose_bf16(proj[g].W, Ns[g], m.K, base + w.wt[g], st));
+            GemmSeg segs[kGemmMaxSeg];
+            int nseg = 0;
+            int64_t kbase = 0;
+            for (int g = 0; g < count; ++g)
+                if (proj[g].W) {
+                    const uint16_t* wt = proj[g].Wt ? static_cast<const uint16_t*>(proj[g].Wt)
+                                                    : reinterpret_cast<const uint16_t*>(base + w.wt[g]);
+                    segs[nseg++] = GemmSeg{static_cast<const uint16_t*>(dY[g]), Ns[g], wt, Ns[g], Ns[g]};
+                    kbase += Ns[g];
+                }
+            segs[nseg++] = GemmSeg{gd, ext_ld, at, ext_ld, ext_ld};
+            auto sc = gemm_scope(st, m.T, m.K, kbase, ext_ld, rtot, 2);
+            MC_TRY(launch_gemm_bf16(m.T, m.K, segs, nseg, nullptr, static_cast<uint16_t*>(dX), m.K, st));
         }
         return hipSuccess;
     }
@@ -739,21 +739,6 @@ hipError_t launch_lora_group_bwd(const mc_lora_desc& d, const void* x, const Lor
             MC_TRY(launch_lora_bwd_operands(calls, count, m.T, m.K, rc, d.scale, keep,
                                             last ? rc + (m.rext - m.r) : rc, ext_ld, st));
         }
-    }
-    if (dX) {
-        GemmSeg segs[kGemmMaxSeg];
-        int nseg = 0;
-        int64_t kbase = 0;
-        for (int g = 0; g < count; ++g)
-            if (proj[g].W) {
-                const uint16_t* wt = proj[g].Wt ? static_cast<const uint16_t*>(proj[g].Wt)
-                                                : reinterpret_cast<const uint16_t*>(base + w.wt[g]);
-                segs[nseg++] = GemmSeg{static_cast<const uint16_t*>(dY[g]), Ns[g], wt, Ns[g], Ns[g]};
-                kbase += Ns[g];
-            }
-        segs[nseg++] = GemmSeg{gd, ext_ld, at, ext_ld, ext_ld};
-        auto sc = gemm_scope(st, m.T, m.K, kbase, ext_ld, rtot, 2);
-        MC_TRY(launch_gemm_bf16(m.T, m.K, segs, nseg, nullptr, static_cast<uint16_t*>(dX), m.K, st));
     }
     if ((any_dA || any_dB) && cs) {
         // the column reductions over the bf16 planes (one pass over x for
@@ -822,6 +807,21 @@ hipError_t launch_lora_group_bwd(const mc_lora_desc& d, const void* x, const Lor
         auto sc = prof::Scope(prof::kLowRank, st, flops, bytes);
         MC_TRY(launch_colreduce_bf16(m.T, cj, nc, st));
         MC_TRY(launch_split_sum(sj, ns, st));
+    }
+    if (dX) {
+        GemmSeg segs[kGemmMaxSeg];
+        int nseg = 0;
+        int64_t kbase = 0;
+        for (int g = 0; g < count; ++g)
+            if (proj[g].W) {
+                const uint16_t* wt = proj[g].Wt ? static_cast<const uint16_t*>(proj[g].Wt)
+                                                : reinterpret_cast<const uint16_t*>(base + w.wt[g]);
+                segs[nseg++] = GemmSeg{static_cast<const uint16_t*>(dY[g]), Ns[g], wt, Ns[g], Ns[g]};
+                kbase += Ns[g];
+            }
+        segs[nseg++] = GemmSeg{gd, ext_ld, at, ext_ld, ext_ld};
+        auto sc = gemm_scope(st, m.T, m.K, kbase, ext_ld, rtot, 2);
+        MC_TRY(launch_gemm_bf16(m.T, m.K, segs, nseg, nullptr, static_cast<uint16_t*>(dX), m.K, st));
     }
     return hipSuccess;
 }
