@@ -483,6 +483,70 @@ def c2_row_ops(mc, dev, iters):
     return out
 
 
+# Row widths past the one-wave RMSNorm / softmax paths: (op, dtype, rows, dim,
+# causal_rows). c5's 3584 and 5120 (14B/32B hidden) take the workgroup-per-row
+# backward; 8192-16384 the wide kernels; 131072 the streaming softmax.
+ROW_SWEEP = [
+    ("rmsnorm", "bf16", 16384, 3584, 0), ("rmsnorm", "bf16", 16384, 5120, 0), ("rmsnorm", "bf16", 16384, 8192, 0),
+    ("rmsnorm", "f32", 16384, 8192, 0), ("rmsnorm", "bf16", 8192, 16384, 0),
+    ("softmax", "bf16", 8192, 6144, 0), ("softmax", "bf16", 8192, 8192, 0), ("softmax", "f32", 8192, 4096, 0),
+    ("softmax", "bf16", 4096, 16384, 0), ("softmax", "bf16", 16384, 16384, 16384), ("softmax", "bf16", 1024, 131072, 0),
+]
+
+
+def row_sweep(mc, dev, iters):
+    """RMSNorm and softmax fwd / bwd over the row widths of ROW_SWEEP, each
+    call after a 1 GiB read-only pass (so its input comes from HBM, with no
+    dirty lines left to write back), timed with events on the launch stream;
+    the median of ITERS calls. GB/s counts the algorithmic bytes (RMSNorm fwd:
+    x in, y and rstd out; bwd: x, dy in, dx out, w and dw amortised; softmax:
+    the unmasked part read, every row written, P and dP read by the bwd)."""
+    import torch
+
+    flush = torch.empty(1 << 28, device=dev)
+    g = torch.Generator(device=dev).manual_seed(5)
+
+    def timed(fn):
+        ts = []
+        for _ in range(iters):
+            flush.sum()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            fn()
+            b.record()
+            b.synchronize()
+            ts.append(a.elapsed_time(b) * 1e3)
+        return sorted(ts)[len(ts) // 2]
+
+    out = []
+    for op, dt, rows, dim, causal in ROW_SWEEP:
+        tdt = torch.bfloat16 if dt == "bf16" else torch.float32
+        es = 2 if dt == "bf16" else 4
+        x = torch.randn(rows, dim, device=dev, generator=g).to(tdt)
+        if op == "rmsnorm":
+            x2 = torch.randn(rows, dim, device=dev, generator=g).to(tdt)
+            w = (torch.randn(dim, device=dev, generator=g) * 0.1 + 1).to(tdt)
+            _, r = mc.rms_norm_forward(x, 1e-6, w)
+            us_f = timed(lambda: mc.rms_norm_forward(x, 1e-6, w))
+            us_b = timed(lambda: mc.rms_norm_backward(x, x2, 1e-6, w, r))
+            by_f, by_b = rows * (2 * dim * es + 4), rows * (3 * dim * es + 4)
+        else:
+            x = x * 3
+            x2 = (torch.randn(rows, dim, device=dev, generator=g) * 1e-2).to(tdt)
+            p = mc.softmax_forward(x, causal_rows=causal)
+            un = rows * dim if not causal else (rows // causal) * sum(r + dim - causal + 1 for r in range(causal))
+            us_f = timed(lambda: mc.softmax_forward(x, causal_rows=causal))
+            us_b = timed(lambda: mc.softmax_backward(p, x2, causal_rows=causal))
+            by_f, by_b = es * (un + rows * dim), es * (2 * un + rows * dim)
+            del p
+        out.append({"op": op, "dtype": dt, "shape": [rows, dim], "causal_rows": causal,
+                    "fwd_us": us_f, "fwd_GB_s": by_f / us_f / 1e3, "bwd_us": us_b, "bwd_GB_s": by_b / us_b / 1e3})
+        del x, x2
+    del flush
+    return {"iters": iters, "method": "median of per-call events, each call after a 1 GiB read-only pass",
+            "rows": out}
+
+
 def blas_reference(c, dev, iters):
     """The vendor library on the layer's forward GEMM shapes: torch.matmul
     (hipBLASLt on ROCm) of x [T, K] bf16 by W^T for each projection's
@@ -535,6 +599,9 @@ def main():
     ap.add_argument("--blas-reference", type=int, default=0, metavar="ITERS",
                     help="also time the vendor library (hipBLASLt via torch.matmul) on the layer's forward GEMM "
                          "shapes, ITERS calls each")
+    ap.add_argument("--row-sweep", type=int, default=0, metavar="ITERS",
+                    help="also time RMSNorm and softmax fwd / bwd over row widths past the one-wave paths "
+                         "(ROW_SWEEP), ITERS calls each from cold caches")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="run one plain device copy of BYTES before the steps (a kernel of known HBM traffic "
                          "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
@@ -654,6 +721,8 @@ def main():
     line["c2_row_ops_f32"] = c2_row_ops(mc, dev, 5)
     if args.blas_reference > 0:
         line["blas_reference"] = blas_reference(c, dev, args.blas_reference)
+    if args.row_sweep > 0:
+        line["row_sweep"] = row_sweep(mc, dev, args.row_sweep)
     if not args.no_cpu_baseline:
         threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
         v, dt = cpu_baseline(mc, c, args.cpu_tokens, threads, args.cpu_iters)

@@ -260,6 +260,33 @@ __device__ __forceinline__ void wait_vmcnt() {
 // Wave index within the workgroup as a scalar (wave-uniform) value.
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
 
+// ------------------------------------------------- workgroup reductions
+// Over every wave of a workgroup of up to kMaxWaves waves: each wave's
+// butterfly result goes to red[wave]; after the barrier every thread combines
+// the slots in wave order, so all threads get the same, reproducible value.
+// A slot array must not be written again until every thread has read it:
+// callers give each reduction of a phase its own array, with a barrier
+// between reuses.
+constexpr int kMaxWaves = 16;
+__device__ __forceinline__ float wg_sum(float v, float* red) {
+    v = wave_sum(v);
+    if (lane_id() == 0) red[wave_id()] = v;
+    __syncthreads();
+    const int nw = (int)(blockDim.x >> 6);
+    float t = red[0];
+    for (int k = 1; k < nw; ++k) t += red[k];
+    return t;
+}
+__device__ __forceinline__ float wg_max(float v, float* red) {
+    v = wave_max(v);
+    if (lane_id() == 0) red[wave_id()] = v;
+    __syncthreads();
+    const int nw = (int)(blockDim.x >> 6);
+    float t = red[0];
+    for (int k = 1; k < nw; ++k) t = fmaxf(t, red[k]);
+    return t;
+}
+
 // 16-byte load of base[off .. off+8) (bf16) or base[off .. off+4) (fp32) that
 // yields zeros when !ok. The load itself is unconditional from an in-bounds
 // address (base[0] when !ok) and the zero is a value select: a conditional

@@ -12,7 +12,11 @@
 // is applied as a multiply by 1/sum. With a causal mask, 16-byte vectors that
 // lie entirely past the row's last unmasked column are neither read nor
 // computed; the kernel writes exact zeros there. Offsets are 64-bit: a
-// [4,28,4096,4096] score tensor has 1.9e9 elements.
+// [4,28,4096,4096] score tensor has 1.9e9 elements. Longer rows (past 8
+// vectors per lane) take one workgroup per row with the row in the
+// registers of up to 1024 threads, and rows past that (128 KB) two
+// streaming passes; rows that are not whole 16-byte vectors take a scalar
+// kernel.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -178,16 +182,288 @@ __global__ __launch_bounds__(256) void softmax_bwd_scalar(int64_t rows, int64_t 
     }
 }
 
+// ------------------------------------------------------------- wide rows
+// Rows of more than 8 vectors per lane (fp32 past 2048 columns, bf16 past
+// 4096): one workgroup of up to 1024 threads per row, vector v of the row
+// held by thread v % blockDim.x, VPL vectors per thread, so the row is still
+// read once and written once. Max, sum and dot combine the waves'
+// butterflies in wave order through LDS. A row of up to 8 x 1024 vectors
+// (32768 fp32 / 65536 bf16 columns, 128 KB) fits; one buffer resource per
+// row.
+constexpr int kWideThreads = 1024;
+
+template <typename T, int VPL>
+__global__ __launch_bounds__(kWideThreads) void softmax_fwd_wide(int64_t row0, int dim, int64_t causal_rows,
+                                                                 const T* __restrict__ s, T* __restrict__ p) {
+    constexpr int N = BVec<T>::N;
+    constexpr int ES = (int)sizeof(T);
+    __shared__ float red[2][kMaxWaves];
+    const int tid = threadIdx.x, nt = blockDim.x;
+    const int64_t row = row0 + blockIdx.x;
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(s + row * dim, (int64_t)dim * ES);
+    const __amdgpu_buffer_rsrc_t rp = make_rsrc(p + row * dim, (int64_t)dim * ES);
+    const int nvec = dim / N;
+    const int lim = (int)row_limit(row, dim, causal_rows);
+    float v[VPL][N];
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+        const int vi = tid + i * nt;
+        const bool ok = vi < nvec && vi * N <= lim;
+        BVec<T>::load(rs, ok ? (uint32_t)(vi * N * ES) : kOOB, v[i]);
+    }
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+        const int vi = tid + i * nt;
+#pragma unroll
+        for (int e = 0; e < N; ++e) {
+            v[i][e] = (vi < nvec && vi * N + e <= lim) ? v[i][e] : -INFINITY;
+            m = fmaxf(m, v[i][e]);
+        }
+    }
+    m = wg_max(m, red[0]);
+    float sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i)
+#pragma unroll
+        for (int e = 0; e < N; ++e) {
+            const float ex = fast_exp2((v[i][e] - m) * kLog2e);
+            v[i][e] = ex;
+            sum += ex;
+        }
+    sum = wg_sum(sum, red[1]);
+    const float inv = 1.0f / sum;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+        const int vi = tid + i * nt;
+        float o[N];
+#pragma unroll
+        for (int e = 0; e < N; ++e) o[e] = v[i][e] * inv;
+        BVec<T>::store(rp, vi < nvec ? (uint32_t)(vi * N * ES) : kOOB, o);
+    }
+}
+
+// p and dp stay packed (16-byte raw vectors) until use, which keeps a
+// 1024-thread workgroup within its 128 registers per thread at VPL = 8.
+template <typename T, int VPL>
+__global__ __launch_bounds__(kWideThreads) void softmax_bwd_wide(int64_t row0, int dim, int64_t causal_rows,
+                                                                 const T* __restrict__ p, const T* __restrict__ dp,
+                                                                 T* __restrict__ ds) {
+    constexpr int N = BVec<T>::N;
+    constexpr int ES = (int)sizeof(T);
+    __shared__ float red[kMaxWaves];
+    const int tid = threadIdx.x, nt = blockDim.x;
+    const int64_t row = row0 + blockIdx.x;
+    const __amdgpu_buffer_rsrc_t rp = make_rsrc(p + row * dim, (int64_t)dim * ES);
+    const __amdgpu_buffer_rsrc_t rg = make_rsrc(dp + row * dim, (int64_t)dim * ES);
+    const __amdgpu_buffer_rsrc_t rd = make_rsrc(ds + row * dim, (int64_t)dim * ES);
+    const int nvec = dim / N;
+    const int lim = (int)row_limit(row, dim, causal_rows);
+    i32x4 pq[VPL], gq[VPL];
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+        const int vi = tid + i * nt;
+        const uint32_t off = (vi < nvec && vi * N <= lim) ? (uint32_t)(vi * N * ES) : kOOB;
+        pq[i] = buf_load16(rp, off);
+        gq[i] = buf_load16(rg, off);
+    }
+    float dot = 0.f;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+        const int vi = tid + i * nt;
+        float pv[N], gv[N];
+        BVec<T>::unpack(pq[i], pv);
+        BVec<T>::unpack(gq[i], gv);
+#pragma unroll
+        for (int e = 0; e < N; ++e) dot += ((vi < nvec && vi * N + e <= lim) ? pv[e] : 0.f) * gv[e];
+    }
+    dot = wg_sum(dot, red);
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+        const int vi = tid + i * nt;
+        float pv[N], gv[N], o[N];
+        BVec<T>::unpack(pq[i], pv);
+        BVec<T>::unpack(gq[i], gv);
+#pragma unroll
+        for (int e = 0; e < N; ++e) o[e] = ((vi < nvec && vi * N + e <= lim) ? pv[e] : 0.f) * (gv[e] - dot);
+        BVec<T>::store(rd, vi < nvec ? (uint32_t)(vi * N * ES) : kOOB, o);
+    }
+}
+
+// ------------------------------------------------------------ stream rows
+// Rows past the wide path's 128 KB (vector-aligned): one 1024-thread
+// workgroup per row streams the row twice with 16-byte vectors, four in
+// flight per thread. Forward: an online (max, sum) per thread (one rescale
+// per vector, Milakov & Gimelshein's online normaliser), combined over the
+// workgroup, then a second read that writes p. Backward: the dot product,
+// then a second read of p and dp that writes ds. Wholly masked vectors are
+// not read; 64-bit addressing throughout.
+constexpr int kStreamUnroll = 4;
+
 template <typename T>
-bool vec_ok(int64_t dim) {
-    return dim % Vec16<T>::N == 0 && dim / Vec16<T>::N <= 16 * kWave;
+__global__ __launch_bounds__(kWideThreads) void softmax_fwd_stream(int64_t row0, int64_t dim, int64_t causal_rows,
+                                                                   const T* __restrict__ s, T* __restrict__ p) {
+    constexpr int N = Vec16<T>::N;
+    __shared__ float red[2][kMaxWaves];
+    const int64_t tid = threadIdx.x, nt = blockDim.x;
+    const int64_t row = row0 + blockIdx.x;
+    const T* sr = s + row * dim;
+    T* pr = p + row * dim;
+    const int64_t nvec = dim / N;
+    const int64_t lim = row_limit(row, dim, causal_rows);
+    const int64_t nread = lim / N + 1;  // vectors holding an unmasked column
+    float m = -INFINITY, sum = 0.f;
+    for (int64_t c0 = tid; c0 < nread; c0 += nt * kStreamUnroll) {
+        uint4 q[kStreamUnroll];
+#pragma unroll
+        for (int u = 0; u < kStreamUnroll; ++u) {
+            const int64_t c = c0 + u * nt;
+            q[u] = load16(sr, c * N, c < nread);
+        }
+#pragma unroll
+        for (int u = 0; u < kStreamUnroll; ++u) {
+            const int64_t c = c0 + u * nt;
+            float v[N];
+            BVec<T>::unpack(__builtin_bit_cast(i32x4, q[u]), v);
+            float vm = -INFINITY;
+#pragma unroll
+            for (int e = 0; e < N; ++e) {
+                v[e] = (c < nread && c * N + e <= lim) ? v[e] : -INFINITY;
+                vm = fmaxf(vm, v[e]);
+            }
+            if (vm > m) {  // rescale the running sum to the new max (never from -inf to -inf)
+                sum = m == -INFINITY ? 0.f : sum * fast_exp2((m - vm) * kLog2e);
+                m = vm;
+            }
+            if (m != -INFINITY) {
+#pragma unroll
+                for (int e = 0; e < N; ++e) sum += fast_exp2((v[e] - m) * kLog2e);
+            }
+        }
+    }
+    const float gm = wg_max(m, red[0]);
+    const float gs = wg_sum(m == -INFINITY ? 0.f : sum * fast_exp2((m - gm) * kLog2e), red[1]);
+    const float inv = 1.0f / gs;
+    for (int64_t c0 = tid; c0 < nvec; c0 += nt * kStreamUnroll) {
+        uint4 q[kStreamUnroll];
+#pragma unroll
+        for (int u = 0; u < kStreamUnroll; ++u) {
+            const int64_t c = c0 + u * nt;
+            q[u] = load16(sr, c * N, c < nread);
+        }
+#pragma unroll
+        for (int u = 0; u < kStreamUnroll; ++u) {
+            const int64_t c = c0 + u * nt;
+            if (c >= nvec) break;
+            float v[N];
+            BVec<T>::unpack(__builtin_bit_cast(i32x4, q[u]), v);
+#pragma unroll
+            for (int e = 0; e < N; ++e) v[e] = c * N + e <= lim ? fast_exp2((v[e] - gm) * kLog2e) * inv : 0.f;
+            Vec16<T>::store(pr + c * N, v);
+        }
+    }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kWideThreads) void softmax_bwd_stream(int64_t row0, int64_t dim, int64_t causal_rows,
+                                                                   const T* __restrict__ p, const T* __restrict__ dp,
+                                                                   T* __restrict__ ds) {
+    constexpr int N = Vec16<T>::N;
+    __shared__ float red[kMaxWaves];
+    const int64_t tid = threadIdx.x, nt = blockDim.x;
+    const int64_t row = row0 + blockIdx.x;
+    const T* pr = p + row * dim;
+    const T* gr = dp + row * dim;
+    T* dr = ds + row * dim;
+    const int64_t nvec = dim / N;
+    const int64_t lim = row_limit(row, dim, causal_rows);
+    const int64_t nread = lim / N + 1;
+    float dot = 0.f;
+    for (int64_t c0 = tid; c0 < nread; c0 += nt * kStreamUnroll) {
+        uint4 pq[kStreamUnroll], gq[kStreamUnroll];
+#pragma unroll
+        for (int u = 0; u < kStreamUnroll; ++u) {
+            const int64_t c = c0 + u * nt;
+            pq[u] = load16(pr, c * N, c < nread);
+            gq[u] = load16(gr, c * N, c < nread);
+        }
+#pragma unroll
+        for (int u = 0; u < kStreamUnroll; ++u) {
+            const int64_t c = c0 + u * nt;
+            float pv[N], gv[N];
+            BVec<T>::unpack(__builtin_bit_cast(i32x4, pq[u]), pv);
+            BVec<T>::unpack(__builtin_bit_cast(i32x4, gq[u]), gv);
+#pragma unroll
+            for (int e = 0; e < N; ++e) dot += (c * N + e <= lim ? pv[e] : 0.f) * gv[e];
+        }
+    }
+    dot = wg_sum(dot, red);
+    for (int64_t c0 = tid; c0 < nvec; c0 += nt * kStreamUnroll) {
+        uint4 pq[kStreamUnroll], gq[kStreamUnroll];
+#pragma unroll
+        for (int u = 0; u < kStreamUnroll; ++u) {
+            const int64_t c = c0 + u * nt;
+            pq[u] = load16(pr, c * N, c < nread);
+            gq[u] = load16(gr, c * N, c < nread);
+        }
+#pragma unroll
+        for (int u = 0; u < kStreamUnroll; ++u) {
+            const int64_t c = c0 + u * nt;
+            if (c >= nvec) break;
+            float pv[N], gv[N];
+            BVec<T>::unpack(__builtin_bit_cast(i32x4, pq[u]), pv);
+            BVec<T>::unpack(__builtin_bit_cast(i32x4, gq[u]), gv);
+#pragma unroll
+            for (int e = 0; e < N; ++e) pv[e] = c * N + e <= lim ? pv[e] * (gv[e] - dot) : 0.f;
+            Vec16<T>::store(dr + c * N, pv);
+        }
+    }
+}
+
+// Row paths by length (rows of 16-byte vectors; ragged rows take the scalar
+// kernels): one wave per row up to 8 vectors per lane, a workgroup per row
+// up to max_vpl vectors per thread of 1024 threads, else two streaming
+// passes. (One wave at 9-16 vectors per lane measured slower than the
+// workgroup per row: bf16 [8192, 8192] backward 137 against 61 us, forward
+// 48 against 44 us.) The bf16 backward holds at most 4 vectors of p and 4 of dp per
+// thread: at 8 it needs more than the 128 registers a 1024-thread workgroup
+// leaves each thread.
+enum class RowPath { kScalar, kWave, kWide, kStream };
+
+template <typename T>
+RowPath row_path(int64_t dim, int max_vpl) {
+    if (dim % Vec16<T>::N != 0) return RowPath::kScalar;
+    const int64_t nvec = dim / Vec16<T>::N;
+    if (nvec <= 8 * kWave) return RowPath::kWave;
+    if (nvec <= (int64_t)max_vpl * kWideThreads) return RowPath::kWide;
+    return RowPath::kStream;
+}
+
+// Vectors per thread and threads per workgroup of the wide path.
+struct WideShape {
+    int vpl, threads;
+};
+template <typename T>
+WideShape wide_shape(int64_t dim) {
+    const int64_t nvec = dim / Vec16<T>::N;
+    const int vpl = nvec <= 2 * kWideThreads ? 2 : nvec <= 4 * kWideThreads ? 4 : 8;
+    const int64_t per = (nvec + vpl - 1) / vpl;
+    return {vpl, (int)((per + kWave - 1) / kWave * kWave)};
+}
+
+// One workgroup per row: launches of at most 2^32 / threads - 1 workgroups
+// (a launch's thread count is 32-bit), each given its first row.
+template <typename F>
+void for_row_chunks(int64_t rows, int threads, F&& launch) {
+    const int64_t cap = (((int64_t)1 << 32) - 1) / threads;
+    for (int64_t r0 = 0; r0 < rows; r0 += cap) launch(r0, dim3((unsigned)(rows - r0 < cap ? rows - r0 : cap)));
 }
 
 template <typename T>
 int vpl_for(int64_t dim) {
     const int64_t nvec = dim / Vec16<T>::N;
     const int64_t per = (nvec + kWave - 1) / kWave;
-    return per <= 1 ? 1 : per <= 2 ? 2 : per <= 4 ? 4 : per <= 8 ? 8 : 16;
+    return per <= 1 ? 1 : per <= 2 ? 2 : per <= 4 ? 4 : 8;
 }
 
 template <typename T>
@@ -195,14 +471,28 @@ hipError_t fwd_impl(int64_t rows, int64_t dim, int64_t causal, const void* s, vo
     const dim3 grid((unsigned)((rows + kRowsPerBlock - 1) / kRowsPerBlock));
     const T* sp = static_cast<const T*>(s);
     T* pp = static_cast<T*>(p);
-    if (vec_ok<T>(dim)) {
+    const RowPath path = row_path<T>(dim, 8);
+    if (path == RowPath::kWide) {
+        const WideShape w = wide_shape<T>(dim);
+        const int d = (int)dim;
+        for_row_chunks(rows, w.threads, [&](int64_t r0, dim3 g) {
+            switch (w.vpl) {
+                case 2: softmax_fwd_wide<T, 2><<<g, w.threads, 0, st>>>(r0, d, causal, sp, pp); break;
+                case 4: softmax_fwd_wide<T, 4><<<g, w.threads, 0, st>>>(r0, d, causal, sp, pp); break;
+                default: softmax_fwd_wide<T, 8><<<g, w.threads, 0, st>>>(r0, d, causal, sp, pp); break;
+            }
+        });
+    } else if (path == RowPath::kStream) {
+        for_row_chunks(rows, kWideThreads, [&](int64_t r0, dim3 g) {
+            softmax_fwd_stream<T><<<g, kWideThreads, 0, st>>>(r0, dim, causal, sp, pp);
+        });
+    } else if (path == RowPath::kWave) {
         const int d = (int)dim;
         switch (vpl_for<T>(dim)) {
             case 1: softmax_fwd_vec<T, 1><<<grid, 256, 0, st>>>(rows, d, causal, sp, pp); break;
             case 2: softmax_fwd_vec<T, 2><<<grid, 256, 0, st>>>(rows, d, causal, sp, pp); break;
             case 4: softmax_fwd_vec<T, 4><<<grid, 256, 0, st>>>(rows, d, causal, sp, pp); break;
-            case 8: softmax_fwd_vec<T, 8><<<grid, 256, 0, st>>>(rows, d, causal, sp, pp); break;
-            default: softmax_fwd_vec<T, 16><<<grid, 256, 0, st>>>(rows, d, causal, sp, pp); break;
+            default: softmax_fwd_vec<T, 8><<<grid, 256, 0, st>>>(rows, d, causal, sp, pp); break;
         }
     } else {
         softmax_fwd_scalar<T><<<grid, 256, 0, st>>>(rows, dim, causal, sp, pp);
@@ -217,14 +507,31 @@ hipError_t bwd_impl(int64_t rows, int64_t dim, int64_t causal, const void* p, co
     const T* pp = static_cast<const T*>(p);
     const T* gp = static_cast<const T*>(dp);
     T* dsp = static_cast<T*>(ds);
-    if (vec_ok<T>(dim)) {
+    const RowPath path = row_path<T>(dim, sizeof(T) == 2 ? 4 : 8);
+    if (path == RowPath::kWide) {
+        const WideShape w = wide_shape<T>(dim);
+        const int d = (int)dim;
+        for_row_chunks(rows, w.threads, [&](int64_t r0, dim3 g) {
+            switch (w.vpl) {
+                case 2: softmax_bwd_wide<T, 2><<<g, w.threads, 0, st>>>(r0, d, causal, pp, gp, dsp); break;
+                case 4: softmax_bwd_wide<T, 4><<<g, w.threads, 0, st>>>(r0, d, causal, pp, gp, dsp); break;
+                default:
+                    if constexpr (sizeof(T) == 4)
+                        softmax_bwd_wide<T, 8><<<g, w.threads, 0, st>>>(r0, d, causal, pp, gp, dsp);
+                    break;
+            }
+        });
+    } else if (path == RowPath::kStream) {
+        for_row_chunks(rows, kWideThreads, [&](int64_t r0, dim3 g) {
+            softmax_bwd_stream<T><<<g, kWideThreads, 0, st>>>(r0, dim, causal, pp, gp, dsp);
+        });
+    } else if (path == RowPath::kWave) {
         const int d = (int)dim;
         switch (vpl_for<T>(dim)) {
             case 1: softmax_bwd_vec<T, 1><<<grid, 256, 0, st>>>(rows, d, causal, pp, gp, dsp); break;
             case 2: softmax_bwd_vec<T, 2><<<grid, 256, 0, st>>>(rows, d, causal, pp, gp, dsp); break;
             case 4: softmax_bwd_vec<T, 4><<<grid, 256, 0, st>>>(rows, d, causal, pp, gp, dsp); break;
-            case 8: softmax_bwd_vec<T, 8><<<grid, 256, 0, st>>>(rows, d, causal, pp, gp, dsp); break;
-            default: softmax_bwd_vec<T, 16><<<grid, 256, 0, st>>>(rows, d, causal, pp, gp, dsp); break;
+            default: softmax_bwd_vec<T, 8><<<grid, 256, 0, st>>>(rows, d, causal, pp, gp, dsp); break;
         }
     } else {
         softmax_bwd_scalar<T><<<grid, 256, 0, st>>>(rows, dim, causal, pp, gp, dsp);

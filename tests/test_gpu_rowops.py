@@ -27,7 +27,8 @@ def _tol(dtype):
 
 
 # ------------------------------------------------------------------ RMSNorm
-@pytest.mark.parametrize("shape", REF_SHAPES + [(3, 5), (2, 7, 3), (1, 1), (5, 2), (8192, 896), (37, 4100)])
+@pytest.mark.parametrize("shape", REF_SHAPES + [(3, 5), (2, 7, 3), (1, 1), (5, 2), (8192, 896), (37, 4100),
+                                   (5, 16384), (3, 32768), (2, 32772), (4, 4098)])
 @pytest.mark.parametrize("weighted", [False, True])
 def test_rmsnorm_fwd_f32(mc, dev, shape, weighted):
     g = torch.Generator().manual_seed(hash((shape, weighted)) % 2**31)
@@ -57,7 +58,8 @@ def test_rmsnorm_known_answers(mc, dev):
         assert rel_err(y, np.full((2, 256), c / np.sqrt(c * c + 1e-5))) <= F32_TOL
 
 
-@pytest.mark.parametrize("shape", [(16384, 1536), (64, 3584), (4, 1024), (2, 24)])
+@pytest.mark.parametrize("shape", [(16384, 1536), (64, 3584), (4, 1024), (2, 24), (16, 8200), (4, 16384), (8, 65536),
+                                   (2, 65544)])
 def test_rmsnorm_fwd_bf16(mc, dev, shape):
     g = torch.Generator().manual_seed(7)
     x = torch.randn(*shape, generator=g).to(torch.bfloat16)
@@ -68,7 +70,8 @@ def test_rmsnorm_fwd_bf16(mc, dev, shape):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("shape", [(8192, 896), (4, 64, 1024), (3, 5), (1, 1), (300, 8), (16, 8200)])
+@pytest.mark.parametrize("shape", [(8192, 896), (4, 64, 1024), (3, 5), (1, 1), (300, 8), (16, 8200), (600, 5120),
+                                   (4097, 5120), (64, 8192), (3, 16384), (2, 16392), (256, 3584), (40, 2056)])
 @pytest.mark.parametrize("use_rstd", [False, True])
 def test_rmsnorm_bwd(mc, dev, dtype, shape, use_rstd):
     g = torch.Generator().manual_seed(11)
@@ -162,13 +165,45 @@ def test_softmax_bwd_f32(mc, dev, shape):
     assert np.abs(to_np(ds).sum(-1)).max() <= 1e-6  # rows of dS sum to 0
 
 
+# Rows past the one-wave paths (8 vectors per lane: fp32 2048, bf16 4096
+# columns): a workgroup per row with the row in the registers of up to 1024
+# threads (fp32 to 32768, bf16 to 65536 columns; the bf16 backward to 32768),
+# two streaming passes past that, and the scalar kernels for rows that are
+# not whole 16-byte vectors (4098 fp32 columns).
+@pytest.mark.parametrize("dtype,rows,dim,causal", [
+    (torch.float32, 3, 4100, 0), (torch.float32, 3, 16384, 0), (torch.float32, 2, 32768, 0),
+    (torch.float32, 2, 40000, 0), (torch.float32, 3, 4098, 0), (torch.float32, 40, 40000, 40),
+    (torch.bfloat16, 5, 6144, 0), (torch.bfloat16, 64, 8192, 64), (torch.float32, 6, 3000, 0),
+    (torch.bfloat16, 3, 8200, 0), (torch.bfloat16, 2, 40000, 0), (torch.bfloat16, 2, 65536, 0),
+    (torch.bfloat16, 2, 70000, 0), (torch.bfloat16, 64, 20000, 20000), (torch.bfloat16, 64, 70000, 70000)])
+def test_softmax_long_rows(mc, dev, dtype, rows, dim, causal):
+    g = torch.Generator().manual_seed(rows * 7 + dim)
+    s = (torch.randn(rows, dim, generator=g) * 3).to(dtype)
+    dp = (torch.randn(rows, dim, generator=g) * 1e-2).to(dtype)
+    p = mc.softmax_forward(s.to(dev), causal_rows=causal)
+    p_ref = oracle.softmax_fwd(s.float().numpy(), causal_rows=causal)
+    assert rel_err(p, p_ref) <= _tol(dtype)
+    pn = to_np(p)
+    cols = np.arange(dim)[None, :]
+    lim = (np.arange(rows) % causal + (dim - causal))[:, None] if causal else np.full((rows, 1), dim - 1)
+    masked = cols > lim
+    assert (pn[masked] == 0).all()
+    assert np.abs(pn.astype(np.float64).sum(-1) - 1).max() <= (1e-5 if dtype == torch.float32 else 2e-2)
+    ds = mc.softmax_backward(p, dp.to(dev), causal_rows=causal)
+    ds_ref = oracle.softmax_bwd(pn, dp.float().numpy(), causal_rows=causal)
+    assert rel_err(ds, ds_ref) <= _tol(dtype)
+    assert (to_np(ds)[masked] == 0).all()
+
+
 def _sampled_rows(n_rows, k, seed):
     return np.sort(np.random.default_rng(seed).choice(n_rows, size=min(k, n_rows), replace=False))
 
 
-@pytest.mark.parametrize("dtype,shape", [(torch.float32, (8, 14, 1024, 1024)), (torch.bfloat16, (8, 12, 2048, 2048))])
+@pytest.mark.parametrize("dtype,shape", [(torch.float32, (8, 14, 1024, 1024)), (torch.bfloat16, (8, 12, 2048, 2048)),
+                                         (torch.bfloat16, (1, 1, 16384, 16384)), (torch.float32, (1, 1, 16384, 16384))])
 def test_softmax_config_full_size(mc, dev, dtype, shape):
-    """BASELINE.json c2 (fp32) and the c4 attention softmax (bf16), causal, fwd + bwd."""
+    """BASELINE.json c2 (fp32) and the c4 attention softmax (bf16), causal, fwd + bwd; and a 16384-token causal
+    score matrix, whose rows take the workgroup-per-row kernels."""
     S = shape[-1]
     gen = torch.Generator(device=dev).manual_seed(2024)
     s = (torch.randn(*shape, generator=gen, device=dev) * 3).to(dtype)
