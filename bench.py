@@ -483,14 +483,16 @@ def c2_row_ops(mc, dev, iters):
     return out
 
 
-# Row widths past the one-wave RMSNorm / softmax paths: (op, dtype, rows, dim,
-# causal_rows). c5's 3584 and 5120 (14B/32B hidden) take the workgroup-per-row
-# backward; 8192-16384 the wide kernels; 131072 the streaming softmax.
+# Row widths past the one-wave RMSNorm / softmax / LayerNorm paths: (op,
+# dtype, rows, dim, causal_rows). c5's 3584 and 5120 (14B/32B hidden) take the
+# workgroup-per-row backward; 8192-16384 the wide kernels; 131072 the
+# streaming softmax.
 ROW_SWEEP = [
     ("rmsnorm", "bf16", 16384, 3584, 0), ("rmsnorm", "bf16", 16384, 5120, 0), ("rmsnorm", "bf16", 16384, 8192, 0),
     ("rmsnorm", "f32", 16384, 8192, 0), ("rmsnorm", "bf16", 8192, 16384, 0),
     ("softmax", "bf16", 8192, 6144, 0), ("softmax", "bf16", 8192, 8192, 0), ("softmax", "f32", 8192, 4096, 0),
     ("softmax", "bf16", 4096, 16384, 0), ("softmax", "bf16", 16384, 16384, 16384), ("softmax", "bf16", 1024, 131072, 0),
+    ("layernorm", "bf16", 16384, 5120, 0), ("layernorm", "bf16", 16384, 8192, 0), ("layernorm", "f32", 8192, 8192, 0),
 ]
 
 
@@ -499,8 +501,9 @@ def row_sweep(mc, dev, iters):
     call after a 1 GiB read-only pass (so its input comes from HBM, with no
     dirty lines left to write back), timed with events on the launch stream;
     the median of ITERS calls. GB/s counts the algorithmic bytes (RMSNorm fwd:
-    x in, y and rstd out; bwd: x, dy in, dx out, w and dw amortised; softmax:
-    the unmasked part read, every row written, P and dP read by the bwd)."""
+    x in, y and rstd out; bwd: x, dy in, dx out, w and dw amortised; LayerNorm
+    likewise with mean and rstd; softmax: the unmasked part read, every row
+    written, P and dP read by the bwd)."""
     import torch
 
     flush = torch.empty(1 << 28, device=dev)
@@ -523,7 +526,15 @@ def row_sweep(mc, dev, iters):
         tdt = torch.bfloat16 if dt == "bf16" else torch.float32
         es = 2 if dt == "bf16" else 4
         x = torch.randn(rows, dim, device=dev, generator=g).to(tdt)
-        if op == "rmsnorm":
+        if op == "layernorm":
+            x2 = torch.randn(rows, dim, device=dev, generator=g).to(tdt)
+            w = (torch.randn(dim, device=dev, generator=g) * 0.1 + 1).to(tdt)
+            bb = (torch.randn(dim, device=dev, generator=g) * 0.1).to(tdt)
+            _, mu, r = mc.layer_norm_forward(x, 1e-5, w, bb)
+            us_f = timed(lambda: mc.layer_norm_forward(x, 1e-5, w, bb))
+            us_b = timed(lambda: mc.layer_norm_backward(x, x2, 1e-5, w, mu, r))
+            by_f, by_b = rows * (2 * dim * es + 8), rows * (3 * dim * es + 8)
+        elif op == "rmsnorm":
             x2 = torch.randn(rows, dim, device=dev, generator=g).to(tdt)
             w = (torch.randn(dim, device=dev, generator=g) * 0.1 + 1).to(tdt)
             _, r = mc.rms_norm_forward(x, 1e-6, w)
@@ -600,7 +611,7 @@ def main():
                     help="also time the vendor library (hipBLASLt via torch.matmul) on the layer's forward GEMM "
                          "shapes, ITERS calls each")
     ap.add_argument("--row-sweep", type=int, default=0, metavar="ITERS",
-                    help="also time RMSNorm and softmax fwd / bwd over row widths past the one-wave paths "
+                    help="also time RMSNorm, softmax and LayerNorm fwd / bwd over row widths past the one-wave paths "
                          "(ROW_SWEEP), ITERS calls each from cold caches")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="run one plain device copy of BYTES before the steps (a kernel of known HBM traffic "

@@ -302,8 +302,8 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_scalar(int64_t rows, int64_t 
 }
 
 // ------------------------------------------------------------- wide rows
-// Rows past the one-wave paths (forward: more than 16 vectors per lane,
-// fp32 past 4096 / bf16 past 8192 columns; backward: more than 4): a
+// Rows past the one-wave paths (forward: more than 8 vectors per lane, fp32
+// past 2048 / bf16 past 4096 columns; backward: more than 4): a
 // workgroup of up to 1024 threads per row (forward) or per block of rows
 // (backward), vector v of a row held by thread v % blockDim.x, so x and dy
 // are still read once. The row sums combine the waves' butterflies in wave
@@ -466,9 +466,12 @@ __global__ __launch_bounds__(kWideThreads) void rmsnorm_bwd_wide(int64_t rows, i
     }
 }
 
+// One wave per row up to 8 vectors per lane (4096 bf16 / 2048 fp32 columns).
+// At 9-16 vectors per lane the workgroup per row measured faster in the
+// forward (bf16 [16384, 5120] 74 -> 55 us, [16384, 8192] 96 -> 82 us).
 template <typename T>
 bool vec_ok(int64_t dim) {
-    return dim % Vec16<T>::N == 0 && dim / Vec16<T>::N <= 16 * kWave;
+    return dim % Vec16<T>::N == 0 && dim / Vec16<T>::N <= 8 * kWave;
 }
 
 // Vectors per thread of the wide paths: forward up to 8 (x and w packed),
@@ -499,7 +502,7 @@ template <typename T>
 int vpl_for(int64_t dim) {
     const int64_t nvec = dim / Vec16<T>::N;
     const int64_t per = (nvec + kWave - 1) / kWave;
-    return per <= 1 ? 1 : per <= 2 ? 2 : per <= 4 ? 4 : per <= 8 ? 8 : 16;
+    return per <= 1 ? 1 : per <= 2 ? 2 : per <= 4 ? 4 : 8;
 }
 
 template <typename T>
@@ -528,8 +531,7 @@ hipError_t fwd_impl(int64_t rows, int64_t dim, float eps, const void* x, const v
             case 1: rmsnorm_fwd_vec<T, 1><<<grid, 256, 0, stream>>>(rows, d, eps, xp, wp, yp, rstd); break;
             case 2: rmsnorm_fwd_vec<T, 2><<<grid, 256, 0, stream>>>(rows, d, eps, xp, wp, yp, rstd); break;
             case 4: rmsnorm_fwd_vec<T, 4><<<grid, 256, 0, stream>>>(rows, d, eps, xp, wp, yp, rstd); break;
-            case 8: rmsnorm_fwd_vec<T, 8><<<grid, 256, 0, stream>>>(rows, d, eps, xp, wp, yp, rstd); break;
-            default: rmsnorm_fwd_vec<T, 16><<<grid, 256, 0, stream>>>(rows, d, eps, xp, wp, yp, rstd); break;
+            default: rmsnorm_fwd_vec<T, 8><<<grid, 256, 0, stream>>>(rows, d, eps, xp, wp, yp, rstd); break;
         }
     } else {
         rmsnorm_fwd_scalar<T><<<grid, 256, 0, stream>>>(rows, dim, eps, xp, wp, yp, rstd);

@@ -8,7 +8,9 @@
 //   y = (x - mean) / sqrt(var + eps) * w + b.
 // One wave per row with the row held in registers (16-byte vectors), as the
 // RMSNorm kernels; the backward reduces dw and db over rows in two
-// fixed-order stages. Rows that do not fit the vector path use a scalar one.
+// fixed-order stages. Longer rows take a workgroup per row (forward) or per
+// block of rows (backward) with the row still in registers; rows that fit
+// neither, or are not whole 16-byte vectors, use a scalar path.
 //
 // log-softmax (candle_nn::ops::log_softmax as cross_entropy_loss calls it,
 // src/training/loss.rs:108): y = (x - max) - log(sum(exp(x - max))).
@@ -614,6 +616,251 @@ __global__ __launch_bounds__(256) void xent_bwd_k(int64_t rows, int64_t vocab, b
     }
 }
 
+// ---------------------------------------------------- LayerNorm, long rows
+// Rows past the one-wave paths (more than 8 vectors per lane: fp32 past 2048,
+// bf16 past 4096 columns; forward to 32768 / 65536, backward to 8192 / 8192):
+// a workgroup of up to 1024 threads per row
+// (forward) or per block of rows (backward), vector v of a row held by
+// thread v % blockDim.x, so x and dy are still read once. Row sums combine
+// the waves' butterflies in wave order through LDS (wg_sum); the backward
+// gives each of a row's reduction rounds its own slot array and alternates
+// two sets between rows, so one barrier per round suffices.
+constexpr int kLnWideThreads = 1024;
+
+template <typename T, int VPL>
+__global__ __launch_bounds__(kLnWideThreads) void layernorm_fwd_wide(int64_t row0, int dim, float eps,
+                                                                     const T* __restrict__ x, const T* __restrict__ w,
+                                                                     const T* __restrict__ b, T* __restrict__ y,
+                                                                     float* __restrict__ mean_out,
+                                                                     float* __restrict__ rstd_out) {
+    constexpr int N = BVec<T>::N;
+    constexpr int ES = (int)sizeof(T);
+    __shared__ float red[2][kMaxWaves];
+    const int tid = threadIdx.x, nt = blockDim.x;
+    const int64_t row = row0 + blockIdx.x;
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + row * dim, (int64_t)dim * ES);
+    const __amdgpu_buffer_rsrc_t ry = make_rsrc(y + row * dim, (int64_t)dim * ES);
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, w ? (int64_t)dim * ES : 0);
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(b, b ? (int64_t)dim * ES : 0);
+    const int nvec = dim / N;
+    i32x4 xq[VPL];
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+        const int vi = tid + i * nt;
+        xq[i] = buf_load16(rx, vi < nvec ? (uint32_t)(vi * N * ES) : kOOB);
+    }
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+        float v[N];
+        BVec<T>::unpack(xq[i], v);
+#pragma unroll
+        for (int e = 0; e < N; ++e) s += v[e];
+    }
+    const float mean = wg_sum(s, red[0]) / (float)dim;
+    float q = 0.f;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+        const bool ok = tid + i * nt < nvec;
+        float v[N];
+        BVec<T>::unpack(xq[i], v);
+#pragma unroll
+        for (int e = 0; e < N; ++e) {
+            const float c = v[e] - mean;
+            q += ok ? c * c : 0.f;
+        }
+    }
+    const float r = 1.0f / sqrtf(wg_sum(q, red[1]) / (float)dim + eps);
+    if (tid == 0) {
+        if (mean_out) mean_out[row] = mean;
+        if (rstd_out) rstd_out[row] = r;
+    }
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+        const int vi = tid + i * nt;
+        const uint32_t off = vi < nvec ? (uint32_t)(vi * N * ES) : kOOB;
+        float v[N], wv[N], bv[N], o[N];
+        BVec<T>::unpack(xq[i], v);
+        BVec<T>::load(rw, off, wv);
+        BVec<T>::load(rb, off, bv);
+#pragma unroll
+        for (int e = 0; e < N; ++e) {
+            float t = (v[e] - mean) * r;
+            if (w) t = t * wv[e];
+            if (b) t = t + bv[e];
+            o[e] = t;
+        }
+        BVec<T>::store(ry, off, o);
+    }
+}
+
+// Block b owns rows [b*chunk, min(rows, (b+1)*chunk)) and walks them in
+// order with the whole workgroup, the next row's loads issued before the
+// current row is used. Each thread owns the columns of its vectors, so its
+// dw / db partials accumulate in registers in row order and are written to
+// part_w[b] / part_b[b] as they are.
+template <typename T, int VPL, bool DW>
+__global__ __launch_bounds__(kLnWideThreads) void layernorm_bwd_wide(int64_t rows, int dim, float eps, int64_t chunk,
+                                                                     const T* __restrict__ x, const T* __restrict__ w,
+                                                                     const float* __restrict__ mean_in,
+                                                                     const float* __restrict__ rstd_in,
+                                                                     const T* __restrict__ dy, T* __restrict__ dx,
+                                                                     float* __restrict__ part_w,
+                                                                     float* __restrict__ part_b) {
+    constexpr int N = BVec<T>::N;
+    constexpr int ES = (int)sizeof(T);
+    __shared__ float red[2][3][2][kMaxWaves];  // [row parity][round][value][wave]
+    const int tid = threadIdx.x, nt = blockDim.x;
+    const int lane = lane_id(), wave = wave_id(), nw = nt >> 6;
+    const int nvec = dim / N;
+    const int64_t r0 = (int64_t)blockIdx.x * chunk;
+    const int64_t r1 = r0 + chunk < rows ? r0 + chunk : rows;
+    const int64_t nr = r1 > r0 ? r1 - r0 : 0;
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + r0 * dim, nr * dim * ES);
+    const __amdgpu_buffer_rsrc_t rg = make_rsrc(dy + r0 * dim, nr * dim * ES);
+    const __amdgpu_buffer_rsrc_t rd = make_rsrc(dx + r0 * dim, nr * dim * ES);
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, w ? (int64_t)dim * ES : 0);
+    float wv[VPL][N];
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+        const int vi = tid + i * nt;
+        BVec<T>::load(rw, vi < nvec ? (uint32_t)(vi * N * ES) : kOOB, wv[i]);
+#pragma unroll
+        for (int e = 0; e < N; ++e) wv[i][e] = w ? wv[i][e] : 1.f;
+    }
+    float aw[DW ? VPL : 1][N], ab[DW ? VPL : 1][N];
+#pragma unroll
+    for (int i = 0; i < (DW ? VPL : 1); ++i)
+#pragma unroll
+        for (int e = 0; e < N; ++e) aw[i][e] = ab[i][e] = 0.f;
+    // Sum of (u, v) over the workgroup into round k's slots of the row's set.
+    auto wg_sum2 = [&](float& u, float& v, float (*slot)[kMaxWaves]) {
+        u = wave_sum(u);
+        v = wave_sum(v);
+        if (lane == 0) { slot[0][wave] = u; slot[1][wave] = v; }
+        __syncthreads();
+        u = slot[0][0];
+        v = slot[1][0];
+        for (int k = 1; k < nw; ++k) { u += slot[0][k]; v += slot[1][k]; }
+    };
+    auto load_row = [&](int64_t q, i32x4 (&xq)[VPL], i32x4 (&gq)[VPL]) {
+#pragma unroll
+        for (int i = 0; i < VPL; ++i) {
+            const int vi = tid + i * nt;
+            const uint32_t off = vi < nvec ? (uint32_t)((q * dim + vi * N) * ES) : kOOB;
+            xq[i] = buf_load16(rx, off);
+            gq[i] = buf_load16(rg, off);
+        }
+    };
+    i32x4 nx[VPL], ng[VPL];
+    if (nr > 0) load_row(0, nx, ng);
+    for (int64_t q = 0; q < nr; ++q) {
+        i32x4 xq[VPL], gq[VPL];
+#pragma unroll
+        for (int i = 0; i < VPL; ++i) { xq[i] = nx[i]; gq[i] = ng[i]; }
+        if (q + 1 < nr) load_row(q + 1, nx, ng);  // workgroup-uniform
+        float (*set)[2][kMaxWaves] = red[q & 1];
+        float mean, r;
+        if (mean_in && rstd_in) {
+            mean = mean_in[r0 + q];
+            r = rstd_in[r0 + q];
+        } else {
+            float s = 0.f, unused = 0.f;
+#pragma unroll
+            for (int i = 0; i < VPL; ++i) {
+                float xv[N];
+                BVec<T>::unpack(xq[i], xv);
+#pragma unroll
+                for (int e = 0; e < N; ++e) s += xv[e];
+            }
+            wg_sum2(s, unused, set[0]);
+            mean = s / (float)dim;
+            float c2 = 0.f;
+#pragma unroll
+            for (int i = 0; i < VPL; ++i) {
+                const bool ok = tid + i * nt < nvec;
+                float xv[N];
+                BVec<T>::unpack(xq[i], xv);
+#pragma unroll
+                for (int e = 0; e < N; ++e) {
+                    const float c = xv[e] - mean;
+                    c2 += ok ? c * c : 0.f;
+                }
+            }
+            wg_sum2(c2, unused, set[1]);
+            r = 1.0f / sqrtf(c2 / (float)dim + eps);
+        }
+        float sg = 0.f, sgx = 0.f;
+#pragma unroll
+        for (int i = 0; i < VPL; ++i) {
+            const bool ok = tid + i * nt < nvec;
+            float xv[N], gv[N];
+            BVec<T>::unpack(xq[i], xv);
+            BVec<T>::unpack(gq[i], gv);
+#pragma unroll
+            for (int e = 0; e < N; ++e) {
+                const float xh = ok ? (xv[e] - mean) * r : 0.f;
+                const float g = gv[e] * wv[i][e];
+                sg += g;
+                sgx += g * xh;
+            }
+        }
+        wg_sum2(sg, sgx, set[2]);
+        const float mg = sg / (float)dim;
+        const float mgx = sgx / (float)dim;
+#pragma unroll
+        for (int i = 0; i < VPL; ++i) {
+            const int vi = tid + i * nt;
+            float xv[N], gv[N], o[N];
+            BVec<T>::unpack(xq[i], xv);
+            BVec<T>::unpack(gq[i], gv);
+#pragma unroll
+            for (int e = 0; e < N; ++e) {
+                const float xh = (xv[e] - mean) * r;
+                o[e] = r * (gv[e] * wv[i][e] - mg - xh * mgx);
+                if constexpr (DW) {
+                    aw[i][e] += gv[e] * xh;
+                    ab[i][e] += gv[e];
+                }
+            }
+            BVec<T>::store(rd, vi < nvec ? (uint32_t)((q * dim + vi * N) * ES) : kOOB, o);
+        }
+    }
+    if constexpr (DW) {
+        float* pw = part_w + (int64_t)blockIdx.x * dim;
+        float* pb = part_b + (int64_t)blockIdx.x * dim;
+#pragma unroll
+        for (int i = 0; i < VPL; ++i) {
+            const int vi = tid + i * nt;
+            if (vi < nvec)
+#pragma unroll
+                for (int e = 0; e < N; ++e) {
+                    pw[vi * N + e] = aw[i][e];
+                    pb[vi * N + e] = ab[i][e];
+                }
+        }
+    }
+}
+
+// Vectors per thread of the LayerNorm wide paths (0: the row does not fit):
+// forward up to 8 (x packed; w and b loaded at use), backward up to 2 in
+// fp32 and 1 in bf16 (w and both partials held unpacked beside two rows of
+// packed x and dy; bf16 at 2 needs more than 128 registers per thread).
+template <typename T>
+int ln_wide_vpl(int64_t dim, bool bwd) {
+    if (dim % Vec16<T>::N != 0) return 0;
+    const int64_t nvec = dim / Vec16<T>::N;
+    const int cap = bwd ? (sizeof(T) == 2 ? 1 : 2) : 8;
+    for (int v = bwd ? 1 : 2; v <= cap; v *= 2)
+        if (nvec <= (int64_t)v * kLnWideThreads) return v;
+    return 0;
+}
+template <typename T>
+int ln_wide_threads(int64_t dim, int vpl) {
+    const int64_t per = (dim / Vec16<T>::N + vpl - 1) / vpl;
+    return (int)((per + kWave - 1) / kWave * kWave);
+}
+
 template <typename T>
 bool ln_vec_ok(int64_t dim) {
     return dim % Vec16<T>::N == 0 && dim / Vec16<T>::N <= 8 * kWave;
@@ -636,7 +883,20 @@ hipError_t ln_fwd(int64_t rows, int64_t dim, float eps, const void* x, const voi
     const dim3 grid((unsigned)((rows + kRowsPerBlock - 1) / kRowsPerBlock));
     const T *xp = static_cast<const T*>(x), *wp = static_cast<const T*>(w), *bp = static_cast<const T*>(b);
     T* yp = static_cast<T*>(y);
-    if (ln_vec_ok<T>(dim)) {
+    const int wvpl = ln_vec_ok<T>(dim) ? 0 : ln_wide_vpl<T>(dim, false);
+    if (wvpl) {
+        const int nt = ln_wide_threads<T>(dim, wvpl);
+        const int d = (int)dim;
+        const int64_t cap = (((int64_t)1 << 32) - 1) / nt;  // a launch's thread count is 32-bit
+        for (int64_t r0 = 0; r0 < rows; r0 += cap) {
+            const dim3 g((unsigned)(rows - r0 < cap ? rows - r0 : cap));
+            switch (wvpl) {
+                case 2: layernorm_fwd_wide<T, 2><<<g, nt, 0, st>>>(r0, d, eps, xp, wp, bp, yp, mean, rstd); break;
+                case 4: layernorm_fwd_wide<T, 4><<<g, nt, 0, st>>>(r0, d, eps, xp, wp, bp, yp, mean, rstd); break;
+                default: layernorm_fwd_wide<T, 8><<<g, nt, 0, st>>>(r0, d, eps, xp, wp, bp, yp, mean, rstd); break;
+            }
+        }
+    } else if (ln_vec_ok<T>(dim)) {
         const int d = (int)dim;
         switch (ln_vpl<T>(dim)) {
             case 1: layernorm_fwd_vec<T, 1><<<grid, 256, 0, st>>>(rows, d, eps, xp, wp, bp, yp, mean, rstd); break;
@@ -678,6 +938,17 @@ hipError_t ln_bwd(int64_t rows, int64_t dim, float eps, const void* x, const voi
         const int vpl = ln_vpl<T>(dim);
         if (need) ln_bwd_vec_launch<T, true>(vpl, grid, lds, st, rows, (int)dim, eps, chunk, xp, wp, mean, rstd, gp, dxp, pw, pb);
         else ln_bwd_vec_launch<T, false>(vpl, grid, 0, st, rows, (int)dim, eps, chunk, xp, wp, mean, rstd, gp, dxp, nullptr, nullptr);
+    } else if (const int wvpl = ln_wide_vpl<T>(dim, true)) {
+        const int nt = ln_wide_threads<T>(dim, wvpl);
+        const int d = (int)dim;
+        constexpr int kV2 = sizeof(T) == 2 ? 1 : 2;  // bf16 rows stop at one vector per thread
+        if (need) {
+            if (wvpl == 1) layernorm_bwd_wide<T, 1, true><<<grid, nt, 0, st>>>(rows, d, eps, chunk, xp, wp, mean, rstd, gp, dxp, pw, pb);
+            else layernorm_bwd_wide<T, kV2, true><<<grid, nt, 0, st>>>(rows, d, eps, chunk, xp, wp, mean, rstd, gp, dxp, pw, pb);
+        } else {
+            if (wvpl == 1) layernorm_bwd_wide<T, 1, false><<<grid, nt, 0, st>>>(rows, d, eps, chunk, xp, wp, mean, rstd, gp, dxp, nullptr, nullptr);
+            else layernorm_bwd_wide<T, kV2, false><<<grid, nt, 0, st>>>(rows, d, eps, chunk, xp, wp, mean, rstd, gp, dxp, nullptr, nullptr);
+        }
     } else if (need) {
         layernorm_bwd_scalar<T, true><<<grid, 256, 0, st>>>(rows, dim, eps, chunk, xp, wp, mean, rstd, gp, dxp, pw, pb);
     } else {

@@ -51,6 +51,10 @@ def test_layernorm_reference_tests(mc, dev):
     (64, 384, torch.float32, True), (33, 768, torch.bfloat16, True), (17, 1024, torch.float32, False),
     (16384, 1536, torch.bfloat16, True), (9, 5000, torch.float32, True), (5, 13, torch.bfloat16, True),
     (8, 4096, torch.bfloat16, False), (1024, 3584, torch.bfloat16, True), (300, 2048, torch.float32, True),
+    # rows past the one-wave paths: workgroup-per-row forward, row-block backward (bf16 to 8192, fp32 to 8192
+    # columns), scalar backward past that; 4097 rows leave the last row blocks empty
+    (600, 5120, torch.bfloat16, True), (4097, 4104, torch.bfloat16, True), (40, 8192, torch.float32, False),
+    (3, 16384, torch.bfloat16, True), (2, 40000, torch.float32, True),
 ])
 def test_layernorm_fwd_bwd(mc, dev, rows, D, dtype, affine):
     x = (rnd((rows, D), rows + D, 2.0) + 0.3).to(dtype)
