@@ -49,6 +49,15 @@ constexpr float kNegInf = -__builtin_inff();
 // positions 0-3, 4-7, 8-11, 12-15 hold keys 0-3, 8-11, 4-7, 12-15 (bits 2 and
 // 3 swapped; the map is its own inverse). This is the order in which a lane
 // half of the S^T accumulator holds its keys (rows 8 (j/4) + 4 (l/32) + j%4).
+// Growth of a row's score max (log2 units) that the forward absorbs before it
+// moves its softmax reference point and rescales O.
+constexpr float kMaxSlack = 8.f;
+
+// 64-bit integer min / max. (The device min / max templates instantiated at
+// int64_t were lowered through double-precision min / max and conversions.)
+__device__ __forceinline__ int64_t min64(int64_t x, int64_t y) { return x < y ? x : y; }
+__device__ __forceinline__ int64_t max64(int64_t x, int64_t y) { return x > y ? x : y; }
+
 // Instruction classes of __builtin_amdgcn_sched_group_barrier.
 constexpr int kSchedMfma = 0x008, kSchedDsRead = 0x100;
 
@@ -100,7 +109,9 @@ struct AttnFwdArgs {
     float scale_log2;    // score scale * log2 e
 };
 
-template <int D>
+// RAW: no additive mask and a positive scale, so the scores can stay
+// unscaled until the exponent (see the online softmax below).
+template <int D, bool RAW>
 __global__ __launch_bounds__(256, 2) void attn_fwd_bf16(AttnFwdArgs a) {
     constexpr int KB = 64;            // keys per block
     constexpr int QB = 128;           // queries per workgroup, 32 per wave
@@ -194,23 +205,43 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16(AttnFwdArgs a) {
         for (int t = 0; t < 2; ++t)
 #pragma unroll
             for (int j = 0; j < 16; ++j) sacc[t][j] = 0.f;
-#pragma unroll
-        for (int s = 0; s < KS; ++s)
+        // K fragments one k-step ahead of their MFMAs, so each pair's LDS
+        // latency runs under the previous pair's MFMAs
+        bf16x8 kf[2][2];
+        auto kread = [&](int s, int slot) {
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
                 const int row = 32 * t + col;
-                const bf16x8 kf = *reinterpret_cast<const bf16x8*>(&sk[row * D + 8 * swz<D>(row, 2 * s + half)]);
-                sacc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[s], sacc[t], 0, 0, 0);
+                kf[slot][t] = *reinterpret_cast<const bf16x8*>(&sk[row * D + 8 * swz<D>(row, 2 * s + half)]);
             }
+        };
+        kread(0, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+            if (s + 1 < KS) {
+                kread(s + 1, (s + 1) & 1);
+                __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
+            }
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+                sacc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[s & 1][t], qf[s], sacc[t], 0, 0, 0);
+            __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2, 0);
+        }
 
-        // accumulator j of tile t is key key0 + 32 t + 8 (j/4) + 4 half + j%4
+        // accumulator j of tile t is key key0 + 32 t + 8 (j/4) + 4 half + j%4.
+        // RAW: the scores stay unscaled, the max is taken over the raw
+        // products and scaled once, and the scale goes into the exponent's
+        // fma (one fma per score instead of a multiply and a subtract).
+        // Otherwise x holds scale * log2 e * s (+ mask) and cx = 1.
         const int64_t key0 = (int64_t)kb * KB;
         float x[2][16];
+        const float cx = RAW ? a.scale_log2 : 1.f;
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
-            for (int j = 0; j < 16; ++j) x[t][j] = sacc[t][j] * a.scale_log2;
-        if (a.mask) {
+            for (int j = 0; j < 16; ++j) x[t][j] = RAW ? sacc[t][j] : sacc[t][j] * a.scale_log2;
+        if (!RAW && a.mask) {
 #pragma unroll
             for (int t = 0; t < 2; ++t)
 #pragma unroll
@@ -224,8 +255,8 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16(AttnFwdArgs a) {
         if (edge) {
             // key offsets in the block (32 t + 8 (j/4) + 4 half + j%4) against
             // the first offset past S and, causal, this lane's query offset
-            const int lim = (int)min<int64_t>(S - key0, KB);
-            const int qrel = a.causal ? (int)max<int64_t>(min<int64_t>(my_q - key0, KB), -1) : KB;
+            const int lim = (int)min64(S - key0, KB);
+            const int qrel = a.causal ? (int)max64(min64(my_q - key0, KB), -1) : KB;
 #pragma unroll
             for (int t = 0; t < 2; ++t)
 #pragma unroll
@@ -241,17 +272,26 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16(AttnFwdArgs a) {
         for (int t = 0; t < 2; ++t)
 #pragma unroll
             for (int j = 0; j < 16; ++j) mx = fmaxf(mx, x[t][j]);
-        mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
-        const float m_new = fmaxf(m_run, mx);
-        const float m_use = m_new == kNegInf ? 0.f : m_new;  // a row with no key yet keeps p = 0
-        const float alpha = exp2_hw(m_run - m_use);
-        m_run = m_new;
+        mx = fmaxf(mx, __shfl_xor(mx, 32, kWave)) * cx;  // cx > 0: -inf stays -inf
+        // The reference point m_run moves only when the block's max exceeds
+        // it by more than kMaxSlack (log2 units; first block: any finite max).
+        // Below that, p = 2^(x - m_run) stays under 2^kMaxSlack, which fp32 sums
+        // and bf16 P carry at full relative precision, and O and l keep one
+        // common reference, so the result is the same softmax; what it saves
+        // is the O rescale of every block whose max moved a little, which for
+        // 32 queries per wave was nearly every block.
+        float alpha = 1.f;
+        if (mx > m_run + kMaxSlack) {
+            alpha = exp2_hw(m_run - mx);  // m_run = -inf: 0 (O and l are 0 then)
+            m_run = mx;
+        }
+        const float m_use = m_run == kNegInf ? 0.f : m_run;  // a row with no key yet keeps p = 0
         float ps = 0.f;
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
             for (int j = 0; j < 16; ++j) {
-                x[t][j] = exp2_hw(x[t][j] - m_use);
+                x[t][j] = exp2_hw(__builtin_fmaf(x[t][j], cx, -m_use));
                 ps += x[t][j];
             }
         l_run = l_run * alpha + ps;
@@ -272,18 +312,29 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16(AttnFwdArgs a) {
 #pragma unroll
             for (int kk = 0; kk < 2; ++kk) pf[t][kk] = pack_bf16x8(&x[t][8 * kk]);
 
-        // O^T (d x query) += V^T . P^T; V^T positions 16 (2t + kk) + 8 half .. +7
+        // O^T (d x query) += V^T . P^T; V^T positions 16 (2t + kk) + 8 half .. +7.
+        // Step v = 2 dt + t multiplies two fragments (kk = 0, 1), read one
+        // step ahead of their MFMAs.
+        bf16x8 vf[2][2];
+        auto vread = [&](int v, int slot) {
+            const int row = 32 * (v >> 1) + col, t = v & 1;
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-            const int row = 32 * dt + col;
+            for (int kk = 0; kk < 2; ++kk)
+                vf[slot][kk] = *reinterpret_cast<const bf16x8*>(&sv[row * KB + 8 * swz<64>(row, 4 * t + 2 * kk + half)]);
+        };
+        vread(0, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
 #pragma unroll
-            for (int t = 0; t < 2; ++t)
+        for (int v = 0; v < 2 * DT; ++v) {
+            if (v + 1 < 2 * DT) {
+                vread(v + 1, (v + 1) & 1);
+                __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
+            }
+            const int dt = v >> 1, t = v & 1;
 #pragma unroll
-                for (int kk = 0; kk < 2; ++kk) {
-                    const int chunk = 4 * t + 2 * kk + half;
-                    const bf16x8 vf = *reinterpret_cast<const bf16x8*>(&sv[row * KB + 8 * swz<64>(row, chunk)]);
-                    oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[t][kk], oacc[dt], 0, 0, 0);
-                }
+            for (int kk = 0; kk < 2; ++kk)
+                oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[v & 1][kk], pf[t][kk], oacc[dt], 0, 0, 0);
+            __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2, 0);
         }
     }
 
@@ -452,12 +503,14 @@ __device__ __forceinline__ int aswz(int r, int c) {
     else return c ^ ((((r >> 1) & 1) << 2) | ((r >> 2) & 3));
 }
 
-// [64 rows][D] tile into the swizzled LDS layout from rows row0 .. row0+63 of
-// a buffer with row stride ld (elements); rows past the buffer load zeros.
-template <int D>
+// [ROWS][D] tile into the swizzled LDS layout from rows row0 .. row0+ROWS-1
+// of a buffer with row stride ld (elements); rows past the buffer load zeros.
+// Each of the 4 waves issues LOADS of the tile's 1 KB DMA pieces.
+template <int D, int ROWS = 64>
 __device__ __forceinline__ void dma_rows(i32x4 r, uint32_t lds_byte, uint32_t row0, uint32_t ld, int wave,
                                          int lane) {
-    constexpr int CPR = D / 8, RPI = 64 / CPR, LOADS = 64 / RPI / 4;
+    constexpr int CPR = D / 8, RPI = 64 / CPR, LOADS = ROWS / RPI / 4;
+    static_assert(LOADS >= 1 && LOADS * RPI * 4 == ROWS, "whole 1 KB pieces per wave");
 #pragma unroll
     for (int j = 0; j < LOADS; ++j) {
         const int blk = wave * LOADS + j;
@@ -945,8 +998,8 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq_bf16(AttnBwdArgs a) {
                           bf16x8 (&db)[2]) {
             constexpr bool MASK = decltype(mask_tag)::value, EDGE = decltype(edge_tag)::value;
             constexpr int t = decltype(t_tag)::value;
-            const int lim = (int)min<int64_t>(S - key0, KB);
-            const int qrel = a.causal ? (int)max<int64_t>(min<int64_t>(my_q - key0, KB), -1) : KB;
+            const int lim = (int)min64(S - key0, KB);
+            const int qrel = a.causal ? (int)max64(min64(my_q - key0, KB), -1) : KB;
             float ds[16];
 #pragma unroll
             for (int j = 0; j < 16; ++j) {
@@ -1012,11 +1065,14 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq_bf16(AttnBwdArgs a) {
 // zeros from both buffers; dS^T columns of queries past S are never stored.
 template <int D>
 __global__ __launch_bounds__(256, 2) void attn_bwd_dq_ds_bf16(AttnBwdArgs a) {
-    constexpr int KB = 64, QB = 128, DT = D / 32;
-    constexpr int KT = 64 * D, DSTILE = 64 * QB;  // K tile, dS^T tile (elements)
+    // Blocks of 32 keys in a ring of 4 stages (the same 64 KB as two stages
+    // of 64 keys), the DMA three blocks ahead of the MFMAs.
+    constexpr int KB = 32, QB = 128, DT = D / 32, NST = 4;
+    constexpr int KT = KB * D, DSTILE = KB * QB;  // K tile, dS^T tile (elements)
     constexpr int STAGE = KT + DSTILE;
-    __shared__ __attribute__((aligned(1024))) uint16_t smem[2 * STAGE];
-    static_assert(4 * 32 * (D + 8) <= 2 * STAGE, "the epilogue's bf16 patches fit in the stages");
+    constexpr int LPB = KB / (512 / D) / 4 + KB / (512 / QB) / 4;  // DMA instructions per wave per block
+    __shared__ __attribute__((aligned(1024))) uint16_t smem[NST * STAGE];
+    static_assert(4 * 32 * (D + 8) <= NST * STAGE, "the epilogue's bf16 patches fit in the stages");
     const uint32_t smem_byte = (uint32_t)reinterpret_cast<uintptr_t>(smem);
     const int lane = threadIdx.x & 63, wave = wave_id();
     const int nbh = a.B * a.H;
@@ -1048,8 +1104,8 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_ds_bf16(AttnBwdArgs a) {
     auto issue = [&](int kb, int stage) {
         const uint32_t base = smem_byte + (uint32_t)(stage * STAGE * 2);
         const uint32_t key0 = (uint32_t)kb * KB;
-        dma_rows<D>(rk, base, key0, D, wave, lane);
-        dma_rows<QB>(rds, base + KT * 2, key0, (uint32_t)a.ldst, wave, lane);
+        dma_rows<D, KB>(rk, base, key0, D, wave, lane);
+        dma_rows<QB, KB>(rds, base + KT * 2, key0, (uint32_t)a.ldst, wave, lane);
     };
 
     f32x16 dqacc[DT];
@@ -1058,20 +1114,44 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_ds_bf16(AttnBwdArgs a) {
 #pragma unroll
         for (int j = 0; j < 16; ++j) dqacc[t][j] = 0.f;
 
-    if (nkb > 0) issue(0, 0);
+#pragma unroll
+    for (int kb = 0; kb < NST - 1; ++kb)
+        if (kb < nkb) issue(kb, kb);
     for (int kb = 0; kb < nkb; ++kb) {
-        wait_vmcnt<0>();
+        // block kb has landed when at most the blocks issued after it (up to
+        // two) are outstanding; the barrier then covers every wave's share
+        const int pend = min(NST - 2, nkb - 1 - kb);
+        if (pend >= 2) wait_vmcnt<2 * LPB>();
+        else if (pend == 1) wait_vmcnt<LPB>();
+        else wait_vmcnt<0>();
         __syncthreads();
-        if (kb + 1 < nkb) issue(kb + 1, (kb + 1) & 1);
-        const uint16_t* sk = smem + (kb & 1) * STAGE;
+        // the stage of block kb + 3 was last read in iteration kb - 1, which
+        // every wave finished before this barrier
+        if (kb + NST - 1 < nkb) issue(kb + NST - 1, (kb + NST - 1) % NST);
+        const uint16_t* sk = smem + (kb % NST) * STAGE;
         const uint16_t* sds = sk + KT;
+        // Step u = kc * DT + dt multiplies K fragment (kc, dt) by dS^T
+        // fragment kc; each step's transposed reads are issued one step ahead
+        // of its MFMA, so their LDS latency runs under the previous MFMA.
+        constexpr int NU = KB / 16 * DT;
+        bf16x8 kfr[2], dfr[2];
+        auto reads = [&](int u, int slot) {
+            const int kc = u / DT, dt = u % DT;
+            kfr[slot] = frag_tr_at(sk + 16 * kc * D, tk[dt][0], tk[dt][1]);
+            if (dt == 0) dfr[kc & 1] = frag_tr_at(sds + 16 * kc * QB, td[0], td[1]);
+        };
+        reads(0, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 4, 0);
 #pragma unroll
-        for (int kc = 0; kc < KB / 16; ++kc) {
-            const bf16x8 bfr = frag_tr_at(sds + 16 * kc * QB, td[0], td[1]);
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt)
-                dqacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_tr_at(sk + 16 * kc * D, tk[dt][0], tk[dt][1]),
-                                                                   bfr, dqacc[dt], 0, 0, 0);
+        for (int u = 0; u < NU; ++u) {
+            if (u + 1 < NU) {
+                reads(u + 1, (u + 1) & 1);
+                if ((u + 1) % DT == 0) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 4, 0);
+                else __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
+            }
+            const int kc = u / DT, dt = u % DT;
+            dqacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kfr[u & 1], dfr[kc & 1], dqacc[dt], 0, 0, 0);
+            __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
         }
     }
 
@@ -1248,12 +1328,15 @@ hipError_t launch_attention_fwd(const mc_attn_desc& d, const void* q, const void
         a.scale_log2 = d.scale * kLog2e;
         const dim3 gvt((unsigned)(Sp / 64), (unsigned)(B * Hkv));
         const dim3 grid((unsigned)((int64_t)a.nqb * B * H));
+        const bool raw = mask == nullptr && a.scale_log2 > 0.f;
         if (D == 64) {
             attn_vt_bf16<64><<<gvt, 256, 0, stream>>>(static_cast<const uint16_t*>(v), S, Sp, vt);
-            attn_fwd_bf16<64><<<grid, 256, 0, stream>>>(a);
+            if (raw) attn_fwd_bf16<64, true><<<grid, 256, 0, stream>>>(a);
+            else attn_fwd_bf16<64, false><<<grid, 256, 0, stream>>>(a);
         } else {
             attn_vt_bf16<128><<<gvt, 256, 0, stream>>>(static_cast<const uint16_t*>(v), S, Sp, vt);
-            attn_fwd_bf16<128><<<grid, 256, 0, stream>>>(a);
+            if (raw) attn_fwd_bf16<128, true><<<grid, 256, 0, stream>>>(a);
+            else attn_fwd_bf16<128, false><<<grid, 256, 0, stream>>>(a);
         }
         return hipGetLastError();
     }

@@ -99,6 +99,32 @@ def test_attention_fwd_bf16(mc, dev, B, H, Hkv, S, D, causal):
     check(o, lse, o_ref, lse_ref, torch.bfloat16)
 
 
+@pytest.mark.parametrize("profile", ["rising", "falling", "spike"])
+@pytest.mark.parametrize("D,causal", [(128, True), (128, False), (64, True)])
+def test_attention_fwd_bf16_score_range(mc, dev, profile, D, causal):
+    """Score rows whose max moves by more and by less than the forward's slack
+    before it moves its softmax reference point (8 in log2 units): keys along
+    one direction u with weights rising steadily to ~60 log2 units (the
+    reference moves every few blocks), falling (it never moves after the first
+    block), or one key 10^3 above the rest (a one-hot row). Against the oracle's
+    fp64 softmax; lse included."""
+    B, H, Hkv, S = 1, 2, 1, 1024
+    g = gen(41)
+    u = torch.randn(D, generator=g)
+    u = u / u.norm()
+    w = torch.linspace(0.0, 40.0, S) if profile == "rising" else torch.linspace(40.0, 0.0, S)
+    if profile == "spike":
+        w = torch.zeros(S)
+        w[700] = 1000.0 / D ** 0.5
+    q = (u * D ** 0.5).expand(B, H, S, D).clone() + 0.05 * torch.randn(B, H, S, D, generator=g)
+    k = w[None, None, :, None] * u + 0.05 * torch.randn(B, Hkv, S, D, generator=g)
+    v = torch.randn(B, Hkv, S, D, generator=g)
+    q, k, v = q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16)
+    o, lse = run(mc, dev, q, k, v, None, causal)
+    o_ref, lse_ref = ref(q, k, v, None, causal)
+    check(o, lse, o_ref, lse_ref, torch.bfloat16)
+
+
 @pytest.mark.parametrize("S,D,causal", [(100, 128, False), (256, 128, True), (77, 64, True), (130, 64, False)])
 def test_attention_fwd_bf16_mask(mc, dev, S, D, causal):
     q, k, v, mask = case(S + D, 2, 4, 2, S, D, torch.bfloat16, masked=True)
