@@ -773,16 +773,21 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_bf16(AttnBwdArgs a) {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const int j = 4 * jq + e;
-                    float x = sacc[j] * a.scale_log2;
+                    // exponent s * scale * log2 e - lse * log2 e, as one fma
+                    // where there is no mask term
+                    float x;
                     if constexpr (MASK) {
                         const int64_t qq = q0 + qi + e;
                         const uint32_t off = (qq < S && my_key < S) ? (uint32_t)((qq * S + my_key) * 4) : kOOB;
-                        x += __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(rm, (int)off, 0, 0)) * kLog2e;
+                        x = sacc[j] * a.scale_log2 +
+                            __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(rm, (int)off, 0, 0)) * kLog2e - lv[e];
+                    } else {
+                        x = __builtin_fmaf(sacc[j], a.scale_log2, -lv[e]);
                     }
                     if constexpr (EDGE) {
                         if ((!MASK || a.causal) && kq > qi + e) x = kNegInf;
                     }
-                    p[j] = exp2_hw(x - lv[e]);
+                    p[j] = exp2_hw(x);
                     ds[j] = p[j] * (dpacc[j] - dv4[e]);
                 }
             }
@@ -1004,16 +1009,19 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq_bf16(AttnBwdArgs a) {
 #pragma unroll
             for (int j = 0; j < 16; ++j) {
                 const int ko = 32 * t + 8 * (j >> 2) + 4 * half + (j & 3);
-                float x = sacc[j] * a.scale_log2;
+                float x;
                 if constexpr (MASK) {
                     const int64_t key = key0 + ko;
                     const uint32_t off = (my_q < S && key < S) ? (uint32_t)((my_q * S + key) * 4) : kOOB;
-                    x += __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(rm, (int)off, 0, 0)) * kLog2e;
+                    x = sacc[j] * a.scale_log2 +
+                        __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(rm, (int)off, 0, 0)) * kLog2e - lse2;
+                } else {
+                    x = __builtin_fmaf(sacc[j], a.scale_log2, -lse2);
                 }
                 if constexpr (EDGE) {
                     if (ko >= lim || ko > qrel) x = kNegInf;
                 }
-                ds[j] = exp2_hw(x - lse2) * (dpacc[j] - delta);
+                ds[j] = exp2_hw(x) * (dpacc[j] - delta);
             }
 #pragma unroll
             for (int kk = 0; kk < 2; ++kk) db[kk] = pack_bf16x8(&ds[8 * kk]);
