@@ -1073,14 +1073,11 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq_bf16(AttnBwdArgs a) {
 // zeros from both buffers; dS^T columns of queries past S are never stored.
 template <int D>
 __global__ __launch_bounds__(256, 2) void attn_bwd_dq_ds_bf16(AttnBwdArgs a) {
-    // Blocks of 32 keys in a ring of 4 stages (the same 64 KB as two stages
-    // of 64 keys), the DMA three blocks ahead of the MFMAs.
-    constexpr int KB = 32, QB = 128, DT = D / 32, NST = 4;
-    constexpr int KT = KB * D, DSTILE = KB * QB;  // K tile, dS^T tile (elements)
+    constexpr int KB = 64, QB = 128, DT = D / 32;
+    constexpr int KT = 64 * D, DSTILE = 64 * QB;  // K tile, dS^T tile (elements)
     constexpr int STAGE = KT + DSTILE;
-    constexpr int LPB = KB / (512 / D) / 4 + KB / (512 / QB) / 4;  // DMA instructions per wave per block
-    __shared__ __attribute__((aligned(1024))) uint16_t smem[NST * STAGE];
-    static_assert(4 * 32 * (D + 8) <= NST * STAGE, "the epilogue's bf16 patches fit in the stages");
+    __shared__ __attribute__((aligned(1024))) uint16_t smem[2 * STAGE];
+    static_assert(4 * 32 * (D + 8) <= 2 * STAGE, "the epilogue's bf16 patches fit in the stages");
     const uint32_t smem_byte = (uint32_t)reinterpret_cast<uintptr_t>(smem);
     const int lane = threadIdx.x & 63, wave = wave_id();
     const int nbh = a.B * a.H;
@@ -1112,8 +1109,8 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_ds_bf16(AttnBwdArgs a) {
     auto issue = [&](int kb, int stage) {
         const uint32_t base = smem_byte + (uint32_t)(stage * STAGE * 2);
         const uint32_t key0 = (uint32_t)kb * KB;
-        dma_rows<D, KB>(rk, base, key0, D, wave, lane);
-        dma_rows<QB, KB>(rds, base + KT * 2, key0, (uint32_t)a.ldst, wave, lane);
+        dma_rows<D>(rk, base, key0, D, wave, lane);
+        dma_rows<QB>(rds, base + KT * 2, key0, (uint32_t)a.ldst, wave, lane);
     };
 
     f32x16 dqacc[DT];
@@ -1122,44 +1119,20 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_ds_bf16(AttnBwdArgs a) {
 #pragma unroll
         for (int j = 0; j < 16; ++j) dqacc[t][j] = 0.f;
 
-#pragma unroll
-    for (int kb = 0; kb < NST - 1; ++kb)
-        if (kb < nkb) issue(kb, kb);
+    if (nkb > 0) issue(0, 0);
     for (int kb = 0; kb < nkb; ++kb) {
-        // block kb has landed when at most the blocks issued after it (up to
-        // two) are outstanding; the barrier then covers every wave's share
-        const int pend = min(NST - 2, nkb - 1 - kb);
-        if (pend >= 2) wait_vmcnt<2 * LPB>();
-        else if (pend == 1) wait_vmcnt<LPB>();
-        else wait_vmcnt<0>();
+        wait_vmcnt<0>();
         __syncthreads();
-        // the stage of block kb + 3 was last read in iteration kb - 1, which
-        // every wave finished before this barrier
-        if (kb + NST - 1 < nkb) issue(kb + NST - 1, (kb + NST - 1) % NST);
-        const uint16_t* sk = smem + (kb % NST) * STAGE;
+        if (kb + 1 < nkb) issue(kb + 1, (kb + 1) & 1);
+        const uint16_t* sk = smem + (kb & 1) * STAGE;
         const uint16_t* sds = sk + KT;
-        // Step u = kc * DT + dt multiplies K fragment (kc, dt) by dS^T
-        // fragment kc; each step's transposed reads are issued one step ahead
-        // of its MFMA, so their LDS latency runs under the previous MFMA.
-        constexpr int NU = KB / 16 * DT;
-        bf16x8 kfr[2], dfr[2];
-        auto reads = [&](int u, int slot) {
-            const int kc = u / DT, dt = u % DT;
-            kfr[slot] = frag_tr_at(sk + 16 * kc * D, tk[dt][0], tk[dt][1]);
-            if (dt == 0) dfr[kc & 1] = frag_tr_at(sds + 16 * kc * QB, td[0], td[1]);
-        };
-        reads(0, 0);
-        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 4, 0);
 #pragma unroll
-        for (int u = 0; u < NU; ++u) {
-            if (u + 1 < NU) {
-                reads(u + 1, (u + 1) & 1);
-                if ((u + 1) % DT == 0) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 4, 0);
-                else __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
-            }
-            const int kc = u / DT, dt = u % DT;
-            dqacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kfr[u & 1], dfr[kc & 1], dqacc[dt], 0, 0, 0);
-            __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+        for (int kc = 0; kc < KB / 16; ++kc) {
+            const bf16x8 bfr = frag_tr_at(sds + 16 * kc * QB, td[0], td[1]);
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
+                dqacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(frag_tr_at(sk + 16 * kc * D, tk[dt][0], tk[dt][1]),
+                                                                   bfr, dqacc[dt], 0, 0, 0);
         }
     }
 
