@@ -86,7 +86,7 @@ typedef struct mc_lora_desc {
     int64_t tokens;        /* T >= 1 */
     int64_t in_features;   /* K >= 1 */
     int64_t out_features;  /* N >= 1 */
-    int32_t rank;          /* 1 <= r <= 128 */
+    int32_t rank;          /* 1 <= r <= 8192 */
     float scale;           /* alpha / rank (LoRAConfig::scaling, lora.rs:84-87) */
     float dropout_p;       /* 0 <= p < 1 (LoRAConfig::validate, lora.rs:97-120) */
     int32_t act_dtype;     /* mc_dtype */

@@ -75,8 +75,10 @@ mc_status check_lora_desc(const mc_lora_desc* d) {
         // The bf16 kernels address a workgroup's block of rows (256 GEMM rows
         // of up to max(K, N) features, 32 rank rows of T fp32 values) through
         // buffer resources with 32-bit byte offsets.
-        MC_CHECK(d->in_features < (1 << 22) && d->out_features < (1 << 22), MC_ERR_SHAPE,
-                 "LoRA bf16: in_features (%lld) and out_features (%lld) must be below 2^22",
+        // The bound applies to the features rounded up to 8, the widths the
+        // kernels see on the zero-padded path.
+        MC_CHECK((d->in_features + 7) / 8 * 8 < (1 << 22) && (d->out_features + 7) / 8 * 8 < (1 << 22),
+                 MC_ERR_SHAPE, "LoRA bf16: in_features (%lld) and out_features (%lld) must be below 2^22 - 7",
                  (long long)d->in_features, (long long)d->out_features);
         MC_CHECK(d->tokens < (1 << 24), MC_ERR_SHAPE, "LoRA bf16: tokens (%lld) must be below 2^24",
                  (long long)d->tokens);

@@ -124,9 +124,16 @@ bool dy_fused(const Dims& m, const int64_t* N, int count) {
 // columns gained little once its finishing launch is counted. The choice
 // depends on the projection's rank and the shared K only, never on the
 // group, so a grouped call computes the same sums as single calls.
-bool fwd_rowsplit(const Dims& m) { return m.r <= kRowsplitRanks && (m.r > 32 || m.K >= 4096); }
+// Its finishing launch addresses one split's T x 16 ceil(ranks / 16) fp32
+// partial (at most 64 ranks per pass) through one buffer resource with
+// 32-bit offsets, so token counts whose 64-rank partial reaches 2^31 bytes
+// (T >= 2^23) take the unsplit kernels instead.
+bool rowsplit_tokens_fit(const Dims& m) { return m.T * (int64_t)kRowsplitRanks * 4 < ((int64_t)1 << 31); }
+bool fwd_rowsplit(const Dims& m) {
+    return m.r <= kRowsplitRanks && (m.r > 32 || m.K >= 4096) && rowsplit_tokens_fit(m);
+}
 bool bwd_rowsplit(const Dims& m, const int64_t* N, int count) {
-    return m.r > 32 && m.r <= kRowsplitRanks && !dy_fused(m, N, count);
+    return m.r > 32 && m.r <= kRowsplitRanks && !dy_fused(m, N, count) && rowsplit_tokens_fit(m);
 }
 // With it, dA and dB take the column reduction over bf16 hi / lo planes of
 // Gd^T (written by the finishing launch) and Hd^T (h_save split by a prep
@@ -147,38 +154,86 @@ mc_lora_desc padded_desc(const mc_lora_desc& d) {
     p.out_features = round_up(d.out_features, 8);
     return p;
 }
-// dst [rows_p][cols_p] = src [rows][cols] (row-major), zero elsewhere
-template <typename T>
+// Row-band copies: a workgroup copies bands of whole rows, each row as
+// `chunks` chunks of V elements. A row of at most 256 chunks takes `chunks`
+// threads and a band holds 256 / chunks rows; a longer row takes the whole
+// workgroup, its threads striding over the chunks. Each thread divides once,
+// at the start, and the bands are walked grid-stride.
+struct Band {
+    int chunks, rows_per_band, row_in_band, chunk0, chunk_step;
+    __device__ Band(int64_t nchunks) : chunks((int)nchunks) {
+        const int t = (int)threadIdx.x;
+        if (chunks <= 256) {
+            rows_per_band = 256 / chunks;
+            row_in_band = t / chunks;
+            chunk0 = t - row_in_band * chunks;
+            chunk_step = chunks;
+        } else {
+            rows_per_band = 1;
+            row_in_band = 0;
+            chunk0 = t;
+            chunk_step = 256;
+        }
+    }
+};
+template <typename T, int V>
+struct alignas(V * sizeof(T)) VecOf {
+    T e[V];
+};
+// dst [rows_p][cols_p] = src [rows][cols] (row-major), zero elsewhere. With
+// cols_p % V == 0 (and dst 16-byte aligned: workspace buffers are 256-byte
+// aligned) each chunk is one 16-byte store; src rows of an odd width are
+// read element by element.
+template <typename T, int V>
 __global__ __launch_bounds__(256) void pad_copy(const T* __restrict__ src, int64_t rows, int64_t cols,
                                                 T* __restrict__ dst, int64_t rows_p, int64_t cols_p) {
-    const int64_t n = rows_p * cols_p;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
-        const int64_t r = i / cols_p, c = i - r * cols_p;
-        dst[i] = r < rows && c < cols ? src[r * cols + c] : T(0);
+    const Band b(cols_p / V);
+    if (b.row_in_band >= b.rows_per_band) return;
+    for (int64_t r = (int64_t)blockIdx.x * b.rows_per_band + b.row_in_band; r < rows_p;
+         r += (int64_t)gridDim.x * b.rows_per_band) {
+        for (int c = b.chunk0; c < b.chunks; c += b.chunk_step) {
+            VecOf<T, V> v;
+#pragma unroll
+            for (int j = 0; j < V; ++j) {
+                const int64_t col = (int64_t)c * V + j;
+                v.e[j] = r < rows && col < cols ? src[r * cols + col] : T(0);
+            }
+            *reinterpret_cast<VecOf<T, V>*>(dst + r * cols_p + (int64_t)c * V) = v;
+        }
     }
 }
-// dst [rows][cols] = the leading block of src [.][cols_p]
+// dst [rows][cols] = the leading block of src [.][cols_p], element by element
+// (dst rows of an odd width are not 16-byte chunks)
 template <typename T>
 __global__ __launch_bounds__(256) void unpad_copy(const T* __restrict__ src, int64_t cols_p, T* __restrict__ dst,
                                                   int64_t rows, int64_t cols) {
-    const int64_t n = rows * cols;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
-        const int64_t r = i / cols, c = i - r * cols;
-        dst[i] = src[r * cols_p + c];
-    }
+    const Band b(cols);
+    if (b.row_in_band >= b.rows_per_band) return;
+    for (int64_t r = (int64_t)blockIdx.x * b.rows_per_band + b.row_in_band; r < rows;
+         r += (int64_t)gridDim.x * b.rows_per_band)
+        for (int c = b.chunk0; c < b.chunks; c += b.chunk_step) dst[r * cols + c] = src[r * cols_p + c];
 }
-unsigned copy_blocks(int64_t n) { return (unsigned)std::max<int64_t>(1, std::min<int64_t>((n + 255) / 256, 4096)); }
+unsigned band_blocks(int64_t rows, int64_t chunks) {
+    const int64_t rpb = chunks <= 256 ? 256 / std::max<int64_t>(chunks, 1) : 1;
+    return (unsigned)std::max<int64_t>(1, std::min<int64_t>((rows + rpb - 1) / rpb, 8192));
+}
 template <typename T>
 hipError_t pad(const void* src, int64_t rows, int64_t cols, void* dst, int64_t rows_p, int64_t cols_p,
                hipStream_t st) {
-    pad_copy<T><<<copy_blocks(rows_p * cols_p), 256, 0, st>>>(static_cast<const T*>(src), rows, cols,
-                                                               static_cast<T*>(dst), rows_p, cols_p);
+    constexpr int V = 16 / (int)sizeof(T);
+    const bool vec = cols_p % V == 0 && reinterpret_cast<uintptr_t>(dst) % 16 == 0;
+    if (vec)
+        pad_copy<T, V><<<band_blocks(rows_p, cols_p / V), 256, 0, st>>>(static_cast<const T*>(src), rows, cols,
+                                                                        static_cast<T*>(dst), rows_p, cols_p);
+    else
+        pad_copy<T, 1><<<band_blocks(rows_p, cols_p), 256, 0, st>>>(static_cast<const T*>(src), rows, cols,
+                                                                    static_cast<T*>(dst), rows_p, cols_p);
     return hipGetLastError();
 }
 template <typename T>
 hipError_t unpad(const void* src, int64_t cols_p, void* dst, int64_t rows, int64_t cols, hipStream_t st) {
-    unpad_copy<T><<<copy_blocks(rows * cols), 256, 0, st>>>(static_cast<const T*>(src), cols_p, static_cast<T*>(dst),
-                                                            rows, cols);
+    unpad_copy<T><<<band_blocks(rows, cols), 256, 0, st>>>(static_cast<const T*>(src), cols_p, static_cast<T*>(dst),
+                                                           rows, cols);
     return hipGetLastError();
 }
 // Buffers of a padded call after the inner call's workspace (byte offsets):

@@ -162,19 +162,30 @@ def _ptr_array(ts):
     return (ctypes.c_void_p * len(ts))(*[None if t is None else t.data_ptr() for t in ts])
 
 
-def _group_table(x, projs, dropout_p):
+def _group_table(x, projs, dropout_p, lead=None, like=None):
     """Validate a grouped call's projections (dicts with W, bias, A, B, mask)
     against the shared x [..., K] and build the C table; returns (table, K,
-    r, T, [N_g])."""
+    r, T, [N_g]). With x None, the leading dims come from `lead`, K from the
+    first projection's A and the dtype / device from the tensor `like`."""
     if not isinstance(projs, (list, tuple)) or not 1 <= len(projs) <= _lib.MC_LORA_MAX_GROUP:
         raise McError(_lib.MC_ERR_SHAPE, f"a group holds 1 to {_lib.MC_LORA_MAX_GROUP} projections")
-    if not isinstance(x, torch.Tensor) or x.dim() < 1:
-        raise McError(_lib.MC_ERR_SHAPE, "Input must have at least 1 dimension")
-    _contig(x, "x")
-    if x.dtype != torch.bfloat16:
+    if x is None:
+        if not isinstance(projs[0], dict) or not isinstance(projs[0].get("A"), torch.Tensor) or projs[0]["A"].dim() != 2:
+            raise McError(_lib.MC_ERR_SHAPE, "lora_a must be 2D")
+        K = projs[0]["A"].shape[0]
+        T = 1
+        for n in lead:
+            T *= n
+        dtype, device = like.dtype, like.device
+    else:
+        if not isinstance(x, torch.Tensor) or x.dim() < 1:
+            raise McError(_lib.MC_ERR_SHAPE, "Input must have at least 1 dimension")
+        _contig(x, "x")
+        K = x.shape[-1]
+        T = x.numel() // K if K else 0
+        dtype, device = x.dtype, x.device
+    if dtype != torch.bfloat16:
         raise McError(_lib.MC_ERR_DTYPE, "grouped projections run in bfloat16 only")
-    K = x.shape[-1]
-    T = x.numel() // K if K else 0
     table = (LoraProj * len(projs))()
     r0, Ns = None, []
     for g, p in enumerate(projs):
@@ -184,12 +195,12 @@ def _group_table(x, projs, dropout_p):
         if r0 is not None and r != r0:
             raise McError(_lib.MC_ERR_SHAPE, f"projection {g}: rank {r} differs from the group's {r0}")
         r0 = r
-        _expect(p["A"], "A", dtype=torch.float32, device=x.device)
-        _expect(p["B"], "B", dtype=torch.float32, device=x.device)
-        _expect(p.get("W"), "W", shape=(N, K), dtype=x.dtype, device=x.device)
-        _expect(p.get("bias"), "bias", shape=(N,), dtype=x.dtype, device=x.device)
-        _expect(p.get("mask"), "mask", shape=(T, r), dtype=torch.uint8, device=x.device)
-        _expect(p.get("Wt"), "Wt", shape=(K, N), dtype=x.dtype, device=x.device)
+        _expect(p["A"], "A", dtype=torch.float32, device=device)
+        _expect(p["B"], "B", dtype=torch.float32, device=device)
+        _expect(p.get("W"), "W", shape=(N, K), dtype=dtype, device=device)
+        _expect(p.get("bias"), "bias", shape=(N,), dtype=dtype, device=device)
+        _expect(p.get("mask"), "mask", shape=(T, r), dtype=torch.uint8, device=device)
+        _expect(p.get("Wt"), "Wt", shape=(K, N), dtype=dtype, device=device)
         table[g] = LoraProj(N, *[None if p.get(k) is None else p[k].data_ptr()
                                  for k in ("W", "bias", "A", "B", "mask", "Wt")])
         Ns.append(N)
@@ -216,18 +227,31 @@ def lora_group_forward(x, projs, scale, dropout_p=0.0, save_hidden=True):
 
 def lora_group_backward(x, projs, dYs, scale, dropout_p=0.0, h_saves=None, need_dx=True, need_dA=True, need_dB=True):
     """Backward of lora_group_forward (mc_lora_group_bwd): returns (dX, [dA_g],
-    [dB_g]) where dX [..., K] is the sum of every projection's input gradient."""
-    table, K, r, T, Ns = _group_table(x, projs, dropout_p)
-    if not isinstance(dYs, (list, tuple)) or len(dYs) != len(Ns):
+    [dB_g]) where dX [..., K] is the sum of every projection's input gradient.
+    x may be None when dA is not requested (as in lora_backward); the leading
+    dims then come from dYs[0] and K from the projections' A."""
+    if not isinstance(dYs, (list, tuple)) or len(dYs) < 1:
         raise McError(_lib.MC_ERR_SHAPE, "one dY per projection")
+    if x is None:
+        if need_dA:
+            raise McError(_lib.MC_ERR_NULL, "LoRA backward: dA requires x")
+        if not isinstance(dYs[0], torch.Tensor) or dYs[0].dim() < 1:
+            raise McError(_lib.MC_ERR_SHAPE, "dY must have at least 1 dimension")
+        lead = tuple(dYs[0].shape[:-1])
+        table, K, r, T, Ns = _group_table(None, projs, dropout_p, lead=lead, like=dYs[0])
+    else:
+        table, K, r, T, Ns = _group_table(x, projs, dropout_p)
+        lead = tuple(x.shape[:-1])
+    if len(dYs) != len(Ns):
+        raise McError(_lib.MC_ERR_SHAPE, "one dY per projection")
+    dev = dYs[0].device if x is None else x.device
     for g, (dy, N) in enumerate(zip(dYs, Ns)):
-        _expect(dy, f"dY[{g}]", shape=tuple(x.shape[:-1]) + (N,), dtype=x.dtype, device=x.device)
+        _expect(dy, f"dY[{g}]", shape=lead + (N,), dtype=torch.bfloat16, device=dev)
     if h_saves is not None:
         for g, h in enumerate(h_saves):
-            _expect(h, f"h_save[{g}]", shape=(r, T), dtype=torch.float32, device=x.device)
+            _expect(h, f"h_save[{g}]", shape=(r, T), dtype=torch.float32, device=dev)
     d = LoraDesc(T, K, Ns[0], r, float(scale), float(dropout_p), _lib.MC_BF16)
-    dev = x.device
-    dX = torch.empty_like(x) if need_dx else None
+    dX = torch.empty(*lead, K, dtype=torch.bfloat16, device=dev) if need_dx else None
     dAs = [torch.empty(K, r, dtype=torch.float32, device=dev) if need_dA else None for _ in Ns]
     dBs = [torch.empty(r, N, dtype=torch.float32, device=dev) if need_dB else None for N in Ns]
     n = len(Ns)

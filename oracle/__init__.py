@@ -11,7 +11,9 @@ import os
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+# MC_ORACLE_LIB names another build of oracle.c (the sanitizer build that
+# tests/test_sanitizers_cpu.py loads); the default is the optimised library.
+_LIB_PATH = os.environ.get("MC_ORACLE_LIB") or os.path.join(_HERE, "liboracle.so")
 _lib = None
 
 _f32p = ctypes.POINTER(ctypes.c_float)

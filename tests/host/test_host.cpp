@@ -14,6 +14,7 @@
 #include <string.h>
 #include <unistd.h>
 
+#include <algorithm>
 #include <functional>
 #include <random>
 #include <string>
@@ -1198,6 +1199,68 @@ CASE(checkpoint_malformed_headers, false) {
     CHECK(safetensors_load(path, kCpu).is_ok());  // the container itself is valid
     CHECK(read_checkpoint_metadata(path).is_err());
     remove(path.c_str());
+}
+
+// Mutations of a valid checkpoint file: every truncation of the header and
+// its length prefix, and byte substitutions at every header position with
+// characters that matter to the JSON reader (quotes, brackets, digits,
+// escapes, control bytes). Each load must return Ok or Err, never throw or
+// read out of bounds (the sanitizer build of this program checks the
+// latter). Deterministic; the file is small, so this runs in seconds.
+CASE(checkpoint_mutated_files, false) {
+    TRY(a, LoRAAdapter::create(8, 12, 1, ckpt_config(), kCpu, 21));
+    const std::string good = tmp_path("mc_ckpt_mut_src.safetensors");
+    const CheckpointMetadata md{7, 0.25f, 1e-3f, 42ull};
+    CHECK(save_checkpoint(a, good, &md).is_ok());
+    std::vector<unsigned char> bytes;
+    if (FILE* f = fopen(good.c_str(), "rb")) {
+        int ch;
+        while ((ch = fgetc(f)) != EOF) bytes.push_back((unsigned char)ch);
+        fclose(f);
+    }
+    CHECK(bytes.size() > 16);
+    if (bytes.size() <= 16) return;
+    uint64_t hlen = 0;
+    for (int i = 0; i < 8; ++i) hlen |= (uint64_t)bytes[(size_t)i] << (8 * i);
+    const size_t hend = (size_t)std::min<uint64_t>(8 + hlen, bytes.size());
+    const std::string path = tmp_path("mc_ckpt_mut.safetensors");
+    auto write = [&](const std::vector<unsigned char>& b) {
+        FILE* f = fopen(path.c_str(), "wb");
+        if (!f) return false;
+        if (!b.empty()) fwrite(b.data(), 1, b.size(), f);
+        fclose(f);
+        return true;
+    };
+    int loads = 0, errs = 0;
+    auto try_load = [&](const std::vector<unsigned char>& b) {
+        if (!write(b)) return;
+        ++loads;
+        auto r = safetensors_load(path, kCpu);
+        auto m = read_checkpoint_metadata(path);
+        TRY(dst, LoRAAdapter::create(8, 12, 1, ckpt_config(), kCpu, 22));
+        auto l = load_checkpoint(dst, path);
+        if (r.is_err() || m.is_err() || l.is_err()) ++errs;
+    };
+    for (size_t n = 0; n < hend; ++n) try_load(std::vector<unsigned char>(bytes.begin(), bytes.begin() + (long)n));
+    const unsigned char subs[] = {'"', '{', '}', '[', ']', ',', ':', '\\', '-', '0', '9', 'e', 'u', 'E', ' ', 0, 0x7f,
+                                  0xff};
+    for (size_t i = 0; i < hend; ++i)
+        for (unsigned char s : subs) {
+            if (bytes[i] == s) continue;
+            std::vector<unsigned char> b = bytes;
+            b[i] = s;
+            try_load(b);
+        }
+    // length prefixes past the file, at the file, and 0
+    for (uint64_t v : {(uint64_t)0, (uint64_t)bytes.size(), (uint64_t)bytes.size() - 8, ~(uint64_t)0,
+                       (uint64_t)1 << 40}) {
+        std::vector<unsigned char> b = bytes;
+        for (int i = 0; i < 8; ++i) b[(size_t)i] = (unsigned char)(v >> (8 * i));
+        try_load(b);
+    }
+    CHECK(loads > 1000 && errs > 0);
+    remove(path.c_str());
+    remove(good.c_str());
 }
 
 // The file format against the safetensors library: tests/test_checkpoint_cpu.py

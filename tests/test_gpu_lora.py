@@ -125,6 +125,9 @@ def test_zero_B_gives_base(mc, dev):
 
 @pytest.mark.parametrize("name,T,K,N,r", [("c3 q_proj", 8192, 896, 896, 8), ("c3 v_proj", 8192, 896, 128, 8),
                                           ("c4 q_proj", 16384, 1536, 1536, 16), ("c4 k_proj", 16384, 1536, 256, 16),
+                                          ("c4 v_proj", 16384, 1536, 256, 16), ("c4 o_proj", 16384, 1536, 1536, 16),
+                                          ("c4 gate_proj", 16384, 1536, 8960, 16),
+                                          ("c4 up_proj", 16384, 1536, 8960, 16),
                                           ("c4 down_proj", 16384, 8960, 1536, 16),
                                           # ragged sizes on each GEMM plan (one tile shape of 256x256, 256x192,
                                           # 256x128 or 128x128, or 256x256 tiles over most columns and a

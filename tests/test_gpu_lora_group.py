@@ -125,12 +125,16 @@ def test_group_partial_outputs(mc, dev, T, K, Ns, r):
     only_dx = mc.lora_group_backward(x, projs, dys, 2.0, need_dA=False, need_dB=False)
     only_ab = mc.lora_group_backward(x, projs, dys, 2.0, h_saves=hs, need_dx=False)
     only_b = mc.lora_group_backward(x, projs, dys, 2.0, h_saves=hs, need_dx=False, need_dA=False)
+    # without x (dA not requested): shapes from dY and A, as lora_backward
+    no_x = mc.lora_group_backward(None, projs, dys, 2.0, h_saves=hs, need_dA=False)
     torch.cuda.synchronize()
     assert torch.equal(only_dx[0], full[0]) and only_dx[1][0] is None
     assert only_ab[0] is None and only_b[0] is None and only_b[1][0] is None
+    assert torch.equal(no_x[0], full[0]) and no_x[1][0] is None
     for g in range(2):
         assert torch.equal(only_ab[1][g], full[1][g]) and torch.equal(only_ab[2][g], full[2][g])
         assert torch.equal(only_b[2][g], full[2][g])
+        assert torch.equal(no_x[2][g], full[2][g])
 
 
 def test_group_with_caller_wt(mc, dev):

@@ -110,3 +110,24 @@ def test_attention_and_loss_errors(mc):
             torch.zeros(31, dtype=torch.bfloat16))
     _raises(mc, L.MC_ERR_SHAPE, "dy has shape (6, 31)", mc.log_softmax_backward, logits,
             torch.zeros(6, 31, dtype=torch.bfloat16))
+
+
+def test_group_backward_without_x(mc):
+    """lora_group_backward takes x = None when dA is not requested, as
+    lora_backward and mc_lora_group_bwd do: the leading dims come from dY,
+    K from A. Asking for dA without x is a null-argument error."""
+    L, c = mc._lib, _lora()
+    proj = dict(W=c["W"], bias=None, A=c["A"], B=c["B"])
+    gb = mc.lora_group_backward
+    _raises(mc, L.MC_ERR_NULL, "dA requires x", gb, None, [proj], [c["dy"]], 2.0)
+    _raises(mc, L.MC_ERR_SHAPE, "dY[1] has shape (15, 24)", gb, None, [proj, proj],
+            [c["dy"], torch.zeros(15, 24, dtype=torch.bfloat16)], 2.0, need_dA=False)
+    _raises(mc, L.MC_ERR_DTYPE, "grouped projections run in bfloat16 only", gb, None, [proj], [c["dy"].float()],
+            2.0, need_dA=False)
+    _raises(mc, L.MC_ERR_SHAPE, "h_save[0] has shape (4, 15)", gb, None, [proj], [c["dy"]], 2.0,
+            h_saves=[torch.zeros(4, 15)], need_dA=False)
+    _raises(mc, L.MC_ERR_SHAPE, "mask has shape (16, 3)", gb, None,
+            [dict(proj, mask=torch.ones(16, 3, dtype=torch.uint8))], [c["dy"]], 2.0, dropout_p=0.1, need_dA=False)
+    # with x given, the same shapes are checked against x
+    _raises(mc, L.MC_ERR_SHAPE, "dY[0] has shape (16, 24)", gb, torch.zeros(15, 32, dtype=torch.bfloat16), [proj],
+            [c["dy"]], 2.0)

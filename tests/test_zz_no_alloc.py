@@ -89,3 +89,89 @@ def test_no_alloc_rejects_oversize(mc, dev):
     dx_o, _ = oracle.rmsnorm_bwd(x.float().cpu().numpy(), dy.float().cpu().numpy(), 1e-6,
                                  w=w.float().cpu().numpy())
     assert rel_err(dx, dx_o) <= 2e-2
+
+
+def _noalloc_call(mc, L, x, w, dy, dx, dw, code, stream):
+    rows, dim = x.shape
+    mc._lib.check(L.mc_rmsnorm_bwd_noalloc(rows, dim, 1e-6, code, _vp(x), _vp(w), None, _vp(dy), _vp(dx), _vp(dw),
+                                           stream))
+
+
+def test_no_alloc_under_graph_capture(mc, dev):
+    """Captured in a HIP graph (torch.cuda.CUDAGraph on the current stream),
+    the entry point records only kernel launches: replays, with eager calls
+    of it on another shape in between (which overwrite the shared scratch),
+    give dx and dw bitwise equal to the eager call on every replay."""
+    L = mc._lib.lib()
+    code = mc._lib.MC_BF16
+    x, w, dy = _inputs(dev, 2048, 1536, torch.bfloat16, 11)
+    xo, wo, dyo = _inputs(dev, 512, 896, torch.bfloat16, 12)
+    cur = lambda: ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)  # noqa: E731
+    dx_e, dw_e = torch.empty_like(x), torch.empty(1536, dtype=torch.float32, device=dev)
+    _noalloc_call(mc, L, x, w, dy, dx_e, dw_e, code, cur())
+    torch.cuda.synchronize()
+    dx, dw = torch.full_like(x, float("nan")), torch.full((1536,), float("nan"), device=dev)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        _noalloc_call(mc, L, x, w, dy, dx, dw, code, cur())
+    torch.cuda.synchronize()
+    dx_o, dw_o = torch.empty_like(xo), torch.empty(896, dtype=torch.float32, device=dev)
+    for rep in range(3):
+        _noalloc_call(mc, L, xo, wo, dyo, dx_o, dw_o, code, cur())  # other contents in the scratch
+        torch.cuda.synchronize()
+        dx.fill_(float("nan"))
+        dw.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        print(f"no-alloc graph replay {rep}", flush=True)
+        assert torch.equal(dx, dx_e) and torch.equal(dw, dw_e), f"replay {rep} differs from the eager call"
+
+
+_FIRST_CALL_IN_CAPTURE = r"""
+import ctypes, sys
+import torch
+sys.path.insert(0, sys.argv[1])
+import __graft_entry__ as ge
+mc = ge.load_package()
+L = mc._lib.lib()
+dev = torch.device("cuda:0")
+g = torch.Generator().manual_seed(13)
+x = torch.randn(1024, 1536, generator=g).to(torch.bfloat16).to(dev)
+w = (torch.randn(1536, generator=g) * 0.1 + 1).to(torch.bfloat16).to(dev)
+dy = (torch.randn(1024, 1536, generator=g) * 1e-2).to(torch.bfloat16).to(dev)
+vp = lambda t: ctypes.c_void_p(t.data_ptr())
+dx, dw = torch.empty_like(x), torch.empty(1536, dtype=torch.float32, device=dev)
+torch.cuda.synchronize()
+graph = torch.cuda.CUDAGraph()
+with torch.cuda.graph(graph):  # the process's first call of the entry point
+    st = L.mc_rmsnorm_bwd_noalloc(1024, 1536, 1e-6, 1, vp(x), vp(w), None, vp(dy), vp(dx), vp(dw),
+                                  ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream))
+torch.cuda.synchronize()
+assert st == 0, (st, mc._lib.last_error())
+graph.replay()
+torch.cuda.synchronize()
+ws_n = L.mc_rmsnorm_bwd_workspace_size(1024, 1536)
+ws = torch.empty(ws_n, dtype=torch.uint8, device=dev)
+dx_r, dw_r = torch.empty_like(x), torch.empty(1536, dtype=torch.float32, device=dev)
+mc._lib.check(L.mc_rmsnorm_bwd(1024, 1536, 1e-6, 1, vp(x), vp(w), None, vp(dy), vp(dx_r), vp(dw_r), vp(ws), ws_n,
+                               ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)))
+torch.cuda.synchronize()
+assert torch.equal(dx, dx_r) and torch.equal(dw, dw_r), "first-call capture differs from mc_rmsnorm_bwd"
+print("FIRST_CALL_IN_CAPTURE_OK", flush=True)
+"""
+
+
+def test_no_alloc_first_call_during_capture():
+    """A process whose first call of the entry point happens under graph
+    capture (the per-device scratch address is looked up during the capture)
+    gets a graph whose replay equals mc_rmsnorm_bwd bit for bit. Run in a
+    fresh process, since any earlier call in this one has already looked the
+    address up."""
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    print("no-alloc first call under capture (subprocess)", flush=True)
+    p = subprocess.run([sys.executable, "-c", _FIRST_CALL_IN_CAPTURE, root], capture_output=True, text=True,
+                       timeout=180)
+    assert p.returncode == 0 and "FIRST_CALL_IN_CAPTURE_OK" in p.stdout, (p.stdout + p.stderr)[-3000:]
