@@ -259,7 +259,7 @@ def lora_group_backward(x, projs, dYs, scale, dropout_p=0.0, h_saves=None, need_
     ws = _workspace(ws_n, dev)
     hp = _ptr_array(h_saves) if h_saves is not None else None
     check(lib().mc_lora_group_bwd(ctypes.byref(d), _ptr(x), table, n, hp, _ptr_array(dYs), _ptr(dX), _ptr_array(dAs),
-                                  _ptr_array(dBs), _ptr(ws), ws_n, _stream(x)))
+                                  _ptr_array(dBs), _ptr(ws), ws_n, _stream(dYs[0])))
     return dX, dAs, dBs
 
 
