@@ -125,6 +125,11 @@ __device__ __forceinline__ int lane_id() { return threadIdx.x & (kWave - 1); }
 // 32-bit: callers keep every offset below 2^31 by basing the resource at
 // the block of rows a workgroup touches.
 constexpr uint32_t kOOB = 0x80000000u;
+// Cache-policy bits of a buffer store (the builtins' aux operand, gfx950
+// encoding): nt, a non-temporal (streaming) store that leaves no dirty line
+// in L2. Used for outputs written as whole 128-byte lines and not read again
+// by the kernel that writes them.
+constexpr int kStoreNT = 2;
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
     const int n = bytes <= 0 ? 0 : bytes >= 0x7fffffff ? 0x7fffffff : (int)bytes;
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, 0x00020000);
@@ -150,6 +155,18 @@ template <> struct BVec<float> {
         const i32x4 q = {__float_as_int(v[0]), __float_as_int(v[1]), __float_as_int(v[2]), __float_as_int(v[3])};
         __builtin_amdgcn_raw_buffer_store_b128(q, r, (int)off, 0, 0);
     }
+    // the same as a non-temporal store (kStoreNT)
+    static __device__ __forceinline__ void store_nt(__amdgpu_buffer_rsrc_t r, uint32_t off, const float (&v)[N]) {
+        i32x4 q;
+        if constexpr (N == 4) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) q[e] = __float_as_int(v[e]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) q[e] = (int)pack_bf16x2(v[2 * e], v[2 * e + 1]);
+        }
+        __builtin_amdgcn_raw_buffer_store_b128(q, r, (int)off, 0, kStoreNT);
+    }
 };
 template <> struct BVec<uint16_t> {
     static constexpr int N = 8;
@@ -167,6 +184,18 @@ template <> struct BVec<uint16_t> {
         const i32x4 q = {(int)pack_bf16x2(v[0], v[1]), (int)pack_bf16x2(v[2], v[3]), (int)pack_bf16x2(v[4], v[5]),
                          (int)pack_bf16x2(v[6], v[7])};
         __builtin_amdgcn_raw_buffer_store_b128(q, r, (int)off, 0, 0);
+    }
+    // the same as a non-temporal store (kStoreNT)
+    static __device__ __forceinline__ void store_nt(__amdgpu_buffer_rsrc_t r, uint32_t off, const float (&v)[N]) {
+        i32x4 q;
+        if constexpr (N == 4) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) q[e] = __float_as_int(v[e]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) q[e] = (int)pack_bf16x2(v[2 * e], v[2 * e + 1]);
+        }
+        __builtin_amdgcn_raw_buffer_store_b128(q, r, (int)off, 0, kStoreNT);
     }
 };
 

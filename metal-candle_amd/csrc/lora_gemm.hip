@@ -29,8 +29,8 @@
 //    double-buffered across the substeps.
 //  - Workgroup ids are remapped per XCD and grouped by 4 tile-rows for L2
 //    reuse (tile_of).
-//  - The epilogue goes through a per-wave LDS patch so C is written with
-//    16-byte stores and the bias is added on the way.
+//  - The epilogue goes through a per-wave LDS patch so C is written as whole
+//    128-byte lines with non-temporal 16-byte stores, the bias added on the way.
 #include <atomic>
 #include <cmath>
 
@@ -113,62 +113,73 @@ __device__ __forceinline__ void wait_tiles(int remaining) {
     }
 }
 
-// Epilogue shared by the GEMM kernels, one 32 x 32 block at a time through
-// a per-wave 4 KB LDS patch (the stage buffers are free once the main loop
-// has finished and a barrier has passed): accumulator q of lane l is row
-// 8*(q/4) + 4*(l/32) + q%4, column l%32 of the block; it is written to the
-// patch row-major, read back as lane l -> row l/2, columns 16*(l%2) .. +15,
-// and stored as two 16-byte bf16 chunks with the bias added. Rows past M and
-// columns past N are dropped by the buffer bounds / the column check.
+// Epilogue shared by the GEMM kernels (the stage buffers are free once the
+// main loop has finished and a barrier has passed). Pairs of 32 x 32
+// accumulator blocks, a 32 x 64 block whose rows are 128 bytes of bf16 (whole
+// cache lines), go through a per-wave 8 KB LDS patch: accumulator q of lane l
+// is row 8 (q / 4) + 4 (l / 32) + q % 4, column l % 32 of its block; the patch
+// is read back as lane l -> row 8 s + l / 8 (s < 4), columns 8 (l % 8) .. +7,
+// so 8 lanes store one whole line with one 16-byte store each, with the bias
+// added. An odd last block (64 x 96 wave tiles) uses half the lanes. Rows
+// past M and columns past N are dropped by the buffer bounds / column check.
+//
+// The stores are non-temporal (nt): C is not read again by this kernel, and
+// whole-line streaming stores leave no dirty lines in L2 for the next kernels
+// to write back. Measured on the c4 step against the previous epilogue
+// (32-byte pieces of rows per store, write-back policy): GEMM 2.80 -> 2.71 ms,
+// the low-rank kernels that follow the GEMMs 0.65 -> 0.61 ms, the step
+// 4.02 -> 3.88 ms; the same whole-line stores without nt gave 2.75 / 3.96 ms.
+// (nt on the 32-byte pieces had been much slower: each piece went to memory
+// as a partial line.)
 template <int TM, int TN, int WM, int WN>
 __device__ __forceinline__ void store_c(const f32x16 (&acc)[TM][TN], uint16_t* smem, const GemmArgs& g, int64_t m0,
                                         int64_t n0, int wm, int wn) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int frag_row = lane & 31;
-    float* patch = reinterpret_cast<float*>(smem) + wave * 1024;
+    float* patch = reinterpret_cast<float*>(smem) + wave * 2048;  // [32][64] fp32
     const __amdgpu_buffer_rsrc_t rc = make_rsrc(g.c + m0 * g.ldc, (g.M - m0) * g.ldc * 2);
     const __amdgpu_buffer_rsrc_t rbias = make_rsrc(g.bias, g.bias ? g.N * 2 : 0);
-    const int prow = lane >> 1, pcol = (lane & 1) * 16;
-    // The bias chunks depend only on the column block: all of them are loaded
-    // before the first store. vmcnt counts loads and stores in issue order,
-    // so a load issued after a store waits for that store as well; loading
-    // the bias per 32 x 32 block serialised one store completion per block.
-    i32x4 bq[TN][2];
+    const int lrow = lane >> 3, lcol = (lane & 7) * 8;
+    constexpr int NP = (TN + 1) / 2;
+    i32x4 bq[NP];
 #pragma unroll
-    for (int j = 0; j < TN; ++j)
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int64_t n = n0 + wn * WN + j * 32 + pcol + 8 * h;
-            bq[j][h] = __builtin_amdgcn_raw_buffer_load_b128(rbias, (int)(n < g.N ? n * 2 : kOOB), 0, 0);
-        }
+    for (int jp = 0; jp < NP; ++jp) {
+        const int64_t n = n0 + wn * WN + jp * 64 + lcol;
+        const bool ok = n < g.N && (2 * jp + 1 < TN || lcol < 32);
+        bq[jp] = __builtin_amdgcn_raw_buffer_load_b128(rbias, (int)(ok ? n * 2 : kOOB), 0, 0);
+    }
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < TN; ++j) {
-#pragma unroll
-            for (int q = 0; q < 16; ++q)
-                patch[(8 * (q >> 2) + 4 * (lane >> 5) + (q & 3)) * 32 + frag_row] = acc[i][j][q];
-            __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): patch written (same wave)
-            float v[16];
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const float4 p = *reinterpret_cast<const float4*>(&patch[prow * 32 + pcol + 4 * u]);
-                v[4 * u] = p.x; v[4 * u + 1] = p.y; v[4 * u + 2] = p.z; v[4 * u + 3] = p.w;
-            }
-            const int64_t gn = n0 + wn * WN + j * 32 + pcol;
-            const uint32_t row = (uint32_t)(wm * WM + i * 32 + prow);
+        for (int jp = 0; jp < NP; ++jp) {
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
-                const int64_t n = gn + 8 * h;
+                const int j = 2 * jp + h;
+                if (j >= TN) break;
+#pragma unroll
+                for (int q = 0; q < 16; ++q)
+                    patch[(8 * (q >> 2) + 4 * (lane >> 5) + (q & 3)) * 64 + 32 * h + frag_row] = acc[i][j][q];
+            }
+            __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): patch written (same wave)
+            const bool half = 2 * jp + 1 >= TN;   // odd last block: columns 0..31 only
+            const int64_t n = n0 + wn * WN + jp * 64 + lcol;
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
+                const int prow = 8 * st + lrow;
+                const float4 a = *reinterpret_cast<const float4*>(&patch[prow * 64 + lcol]);
+                const float4 b = *reinterpret_cast<const float4*>(&patch[prow * 64 + lcol + 4]);
+                const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
                 uint32_t w[4];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const uint32_t bb = (uint32_t)bq[j][h][e];
-                    w[e] = pack_bf16x2(v[8 * h + 2 * e] + bf16_lo(bb), v[8 * h + 2 * e + 1] + bf16_hi(bb));
+                    const uint32_t bb = (uint32_t)bq[jp][e];
+                    w[e] = pack_bf16x2(v[2 * e] + bf16_lo(bb), v[2 * e + 1] + bf16_hi(bb));
                 }
                 const i32x4 out = {(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
-                const uint32_t off = n < g.N ? (row * (uint32_t)g.ldc + (uint32_t)n) * 2u : kOOB;
-                __builtin_amdgcn_raw_buffer_store_b128(out, rc, (int)off, 0, 0);
+                const uint32_t row = (uint32_t)(wm * WM + i * 32 + prow);
+                const bool ok = n < g.N && (!half || lcol < 32);
+                const uint32_t off = ok ? (row * (uint32_t)g.ldc + (uint32_t)n) * 2u : kOOB;
+                __builtin_amdgcn_raw_buffer_store_b128(out, rc, (int)off, 0, kStoreNT);
             }
             __builtin_amdgcn_s_waitcnt(0xc07f);  // patch reads done before it is rewritten
         }
@@ -191,7 +202,7 @@ __device__ __forceinline__ void gemm_tile(const GemmArgs& g, int tm, int tn, uin
     constexpr int STAGE = (BM + BN) * BK;                // bf16 elements per stage (A tile, then B tile)
     constexpr int LOADS = (BM + BN) / (512 / BK) / (NT / 64);  // loads per wave per tile
     static_assert(STAGES >= 2 && STAGES <= 5 && (STAGES - 2) * LOADS < 64 && KS % 2 == 0, "pipeline depth");
-    static_assert(NT / 64 * 4096 <= STAGES * STAGE * 2, "epilogue staging fits in the stage buffers");
+    static_assert(NT / 64 * 8192 <= STAGES * STAGE * 2, "epilogue staging fits in the stage buffers");
 
     const uint32_t smem_byte = (uint32_t)reinterpret_cast<uintptr_t>(smem);
 

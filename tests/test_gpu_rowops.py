@@ -227,3 +227,44 @@ def test_softmax_config_full_size(mc, dev, dtype, shape):
     mask = (cols[None, :] > qpos)
     assert (p.reshape(-1, S, S)[:, mask] == 0).all()
     assert (ds.reshape(-1, S, S)[:, mask] == 0).all()
+
+
+def test_norm_bwd_many_calls_and_streams(mc, dev):
+    """The fixed-order dw (and LayerNorm's db) reductions over 8, 38 and 512
+    row blocks: 300 calls in a row over three shapes, and calls on two
+    streams in flight together, must all give the bits of the first call of
+    their shape."""
+    g = torch.Generator().manual_seed(21)
+    shapes = [(64, 896), (300, 1536), (8192, 896)]  # 8, 38 and 512 row blocks
+    cases = []
+    for rows, dim in shapes:
+        x = torch.randn(rows, dim, generator=g).to(torch.bfloat16).to(dev)
+        w = (torch.randn(dim, generator=g) * 0.1 + 1).to(torch.bfloat16).to(dev)
+        dy = torch.randn(rows, dim, generator=g).to(torch.bfloat16).to(dev)
+        ref = mc.rms_norm_backward(x, dy, 1e-6, w)
+        lref = mc.layer_norm_backward(x, dy, 1e-5, w)
+        cases.append((x, w, dy, ref, lref))
+    torch.cuda.synchronize()
+    print("norm bwd: 300 sequential calls", flush=True)
+    for i in range(300):
+        x, w, dy, ref, lref = cases[i % 3]
+        dx, dw = mc.rms_norm_backward(x, dy, 1e-6, w)
+        if i % 10 == 0:
+            _, ldw, ldb = mc.layer_norm_backward(x, dy, 1e-5, w)
+            torch.cuda.synchronize()
+            assert torch.equal(ldw, lref[1]) and torch.equal(ldb, lref[2]), f"LayerNorm call {i}"
+        torch.cuda.synchronize()
+        assert torch.equal(dw, ref[1]) and torch.equal(dx, ref[0]), f"RMSNorm call {i}"
+    print("norm bwd: two streams", flush=True)
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    s1.wait_stream(torch.cuda.current_stream())
+    s2.wait_stream(torch.cuda.current_stream())
+    outs = []
+    for rep in range(20):
+        for s, k in ((s1, 2), (s2, 1)):
+            with torch.cuda.stream(s):
+                x, w, dy, _, _ = cases[k]
+                outs.append((k, mc.rms_norm_backward(x, dy, 1e-6, w)))
+    torch.cuda.synchronize()
+    for k, (dx, dw) in outs:
+        assert torch.equal(dw, cases[k][3][1]) and torch.equal(dx, cases[k][3][0])
