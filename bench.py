@@ -35,7 +35,10 @@ score and P.V products over the causal lower triangle; the backward counts
 its four algorithmic products, not the recomputation). The "adamw" object
 times one AdamW step (mc_adamw_step) over the layer's LoRA parameters, and
 "row_ops" the LayerNorm and cross-entropy row kernels (cross entropy over a
-Qwen2.5-sized vocabulary of 151936), also outside the step.
+Qwen2.5-sized vocabulary of 151936), also outside the step. "c2_row_ops_f32"
+and "c1_lora_f32" time BASELINE.json's two fp32 configs (RMSNorm / causal
+softmax at c2's shapes; c1's single LoRA linear fwd and bwd against the fp32
+peak).
 """
 import argparse
 import json
@@ -483,6 +486,55 @@ def c2_row_ops(mc, dev, iters):
     return out
 
 
+def c1_lora_f32(mc, dev, iters):
+    """BASELINE config c1 (fp32, the reference's own fused-kernel dtype): one
+    LoRA linear, x [4, 128, 768] ~N(0, 1), frozen W [768, 768] ~N(0, 0.02),
+    A [768, 8] kaiming-uniform, B [8, 768] ~N(0, 0.02), rank 8, alpha 16, no
+    dropout; forward y and backward (dX, dA, dB) with dY ~N(0, 1e-2). Each
+    call is timed whole (every launch of it) with events on the stream,
+    median of `iters` timed repetitions of 20 calls. FLOPs count the
+    algorithmic products: forward 2TKN + 2TKr + 2TrN, backward 2TNK + 2TrK (dX),
+    2TNr (G), 2TKr (dA), 2TrN (dB); the roofline is the fp32 peak (vector
+    and matrix fp32 are both 157.3 TFLOP/s on MI355X)."""
+    import statistics
+    import torch
+
+    T, K, N, r, s = 4 * 128, 768, 768, 8, 2.0
+    g = torch.Generator(device=dev).manual_seed(0)
+    x = torch.randn(T, K, device=dev, generator=g)
+    W = torch.randn(N, K, device=dev, generator=g) * 0.02
+    bound = 1.0 / K ** 0.5
+    A = (torch.rand(K, r, device=dev, generator=g) * 2 - 1) * bound
+    B = torch.randn(r, N, device=dev, generator=g) * 0.02
+    dy = torch.randn(T, N, device=dev, generator=g) * 1e-2
+    fwd = lambda: mc.lora_forward(x, A, B, s, W=W)  # noqa: E731
+    _, h = fwd()
+    bwd = lambda: mc.lora_backward(x, A, B, dy, s, W=W, h_save=h)  # noqa: E731
+    flops = {"fwd": 2.0 * T * K * N + 2.0 * T * K * r + 2.0 * T * r * N,
+             "bwd": 2.0 * T * N * K + 2.0 * T * r * K + 2.0 * T * N * r + 2.0 * T * K * r + 2.0 * T * r * N}
+    out = {"shape": {"tokens": T, "in": K, "out": N, "rank": r}, "dtype": "f32", "iters": iters,
+           "gflop_fwd_bwd": (flops["fwd"] + flops["bwd"]) / 1e9}
+    for name, fn in (("fwd", fwd), ("bwd", bwd)):
+        for _ in range(5):
+            fn()
+        torch.cuda.synchronize()
+        times = []
+        for _ in range(iters):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(20):
+                fn()
+            e1.record()
+            torch.cuda.synchronize()
+            times.append(e0.elapsed_time(e1) / 20 * 1e3)
+        us = statistics.median(times)
+        tf = flops[name] / (us * 1e-6) / 1e12
+        out[name] = {"us_per_call": us, "TFLOP_s": tf, "fp32_frac": tf / FP32_PEAK_TFLOPS}
+    out["fwd_bwd_us"] = out["fwd"]["us_per_call"] + out["bwd"]["us_per_call"]
+    out["tokens_per_s"] = T / (out["fwd_bwd_us"] * 1e-6)
+    return out
+
+
 # Row widths past the one-wave RMSNorm / softmax / LayerNorm paths: (op,
 # dtype, rows, dim, causal_rows). c5's 3584 and 5120 (14B/32B hidden) take the
 # workgroup-per-row backward; 8192-16384 the wide kernels; 131072 the
@@ -730,6 +782,7 @@ def main():
         line["adamw"] = adamw_update(mc, c, dev, 20)
         line["row_ops"] = row_ops(mc, c, dev, args.attention_iters)
     line["c2_row_ops_f32"] = c2_row_ops(mc, dev, 5)
+    line["c1_lora_f32"] = c1_lora_f32(mc, dev, 5)
     if args.blas_reference > 0:
         line["blas_reference"] = blas_reference(c, dev, args.blas_reference)
     if args.row_sweep > 0:

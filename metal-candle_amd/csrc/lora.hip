@@ -23,25 +23,6 @@
 namespace mc {
 namespace {
 
-__global__ __launch_bounds__(256) void transpose_f32(const float* __restrict__ src, int64_t rows, int64_t cols,
-                                                     float* __restrict__ dst) {
-    // dst[j][i] = src[i][j]
-    const int64_t n = rows * cols;
-    for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < n;
-         idx += (int64_t)gridDim.x * blockDim.x) {
-        const int64_t i = idx / cols, j = idx % cols;
-        dst[j * rows + i] = src[idx];
-    }
-}
-
-hipError_t launch_transpose_f32(const float* src, int64_t rows, int64_t cols, float* dst, hipStream_t st) {
-    int64_t blocks = (rows * cols + 255) / 256;
-    if (blocks > 4096) blocks = 4096;
-    if (blocks < 1) blocks = 1;
-    transpose_f32<<<dim3((unsigned)blocks), 256, 0, st>>>(src, rows, cols, dst);
-    return hipGetLastError();
-}
-
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 struct Dims {
@@ -280,7 +261,6 @@ LoraFwdWs lora_fwd_ws(const mc_lora_desc& d) {
         const int64_t N = m.N;
         off = lora_group_fwd_ws(d, &N, 1).total;
     } else {
-        w.bt_ext = off;  off += align256((size_t)m.N * m.r * 4);
         w.hs_ext = off;  off += align256((size_t)m.T * m.r * 4);
     }
     w.hd_t = 0;
@@ -304,7 +284,6 @@ LoraBwdWs lora_bwd_ws(const mc_lora_desc& d) {
         w.part_a = g.part_a; w.part_b = g.part_b[0];
         off = g.total;
     } else {
-        w.at_ext = off; off += align256((size_t)m.r * m.K * 4);
         w.gd_ext = off; off += align256((size_t)m.T * m.r * 4);
         w.gd_t = off;   off += align256((size_t)m.r * m.T * 4);
     }
@@ -402,18 +381,17 @@ hipError_t launch_lora_fwd(const mc_lora_desc& d, const void* x, const void* W, 
         float* const hs[1] = {h_save};
         return launch_lora_group_fwd(d, x, &p, 1, ys, hs, ws, st);
     }
-    float* bt = reinterpret_cast<float*>(base + w.bt_ext);
     float* hs = reinterpret_cast<float*>(base + w.hs_ext);
     const float* xf = static_cast<const float*>(x);
     {
         auto sc = lowrank_scope(st, m.T, m.K, m.r, 4);
         MC_TRY(launch_rowproj_f32(xf, m.T, m.K, A, true, m.r, 1.0f, mask, keep, h_save, hs, d.scale, st));
-        MC_TRY(launch_transpose_f32(B, m.r, m.N, bt, st));
     }
+    // y = x.W^T (+ b) + (s Hd).B: W [N][K] is read NT, B [r][N] as stored (NN)
     GemmSegF32 s0{xf, m.K, static_cast<const float*>(W), m.K, kbase};
-    GemmSegF32 s1{hs, m.r, bt, m.r, m.r};
+    GemmSegF32 s1{hs, m.r, B, m.N, m.r};
     auto sc = gemm_scope(st, m.T, m.N, kbase, m.r, m.r, 4);
-    return launch_gemm_f32(false, m.T, m.N, s0, s1, static_cast<const float*>(bias), static_cast<float*>(y),
+    return launch_gemm_f32(false, true, m.T, m.N, s0, s1, static_cast<const float*>(bias), static_cast<float*>(y),
                            m.N, st);
 }
 
@@ -454,7 +432,6 @@ hipError_t launch_lora_bwd(const mc_lora_desc& d, const void* x, const void* W, 
     const bool need_g = dX || dA;
     const int64_t kbase = W ? m.N : 0;
     const float* dyf = static_cast<const float*>(dY);
-    float* at = reinterpret_cast<float*>(base + w.at_ext);
     float* gd = reinterpret_cast<float*>(base + w.gd_ext);
     float* gdt = reinterpret_cast<float*>(base + w.gd_t);
     if (need_g) {
@@ -462,11 +439,11 @@ hipError_t launch_lora_bwd(const mc_lora_desc& d, const void* x, const void* W, 
         MC_TRY(launch_rowproj_f32(dyf, m.T, m.N, B, false, m.r, d.scale, mask, keep, gdt, gd, 1.0f, st));
     }
     if (dX) {
-        MC_TRY(launch_transpose_f32(A, m.K, m.r, at, st));
+        // dX = dY.W + Gd.A^T: W [N][K] is read as [k][K] (NN), A [K][r] as [K][k] (NT)
         GemmSegF32 s0{dyf, m.N, static_cast<const float*>(W), m.K, kbase};
-        GemmSegF32 s1{gd, m.r, at, m.K, m.r};
+        GemmSegF32 s1{gd, m.r, A, m.r, m.r};
         auto sc = gemm_scope(st, m.T, m.K, kbase, m.r, m.r, 4);
-        MC_TRY(launch_gemm_f32(true, m.T, m.K, s0, s1, nullptr, static_cast<float*>(dX), m.K, st));
+        MC_TRY(launch_gemm_f32(true, false, m.T, m.K, s0, s1, nullptr, static_cast<float*>(dX), m.K, st));
     }
     if (dA) {
         auto sc = lowrank_scope(st, m.T, m.K, m.r, 4);

@@ -32,6 +32,7 @@
 //  - The epilogue goes through a per-wave LDS patch so C is written as whole
 //    128-byte lines with non-temporal 16-byte stores, the bias added on the way.
 #include <atomic>
+#include <type_traits>
 #include <cmath>
 
 #include "common.hpp"
@@ -492,61 +493,115 @@ __attribute__((amdgpu_waves_per_eu(1, 2))) void gemm_bf16_multi(GemmMulti m) {
 }
 
 // ------------------------------------------------------------- fp32 GEMM
-// 64 x 64 tile, 16-deep k-steps, 4 x 4 outputs per thread, sequential FMA
-// chain over k (fixed order).
-template <bool NN>
-__global__ __launch_bounds__(256) void gemm_f32_kernel(int64_t M, int64_t N, GemmSegF32 s0, GemmSegF32 s1,
-                                                       const float* __restrict__ bias, float* __restrict__ C,
-                                                       int64_t ldc) {
-    constexpr int TM = 64, TN = 64, TK = 16;
-    __shared__ float As[TK][TM + 4];
-    __shared__ float Bs[TK][TN + 4];
-    const int tid = threadIdx.x;
-    const int ty = tid >> 4, tx = tid & 15;
-    const int64_t m0 = (int64_t)blockIdx.y * TM, n0 = (int64_t)blockIdx.x * TN;
-    const int nk0 = (int)((s0.k + TK - 1) / TK);
-    const int nk = nk0 + (int)((s1.k + TK - 1) / TK);
-    float acc[4][4] = {};
-    for (int kt = 0; kt < nk; ++kt) {
-        const GemmSegF32& s = kt < nk0 ? s0 : s1;
-        const int64_t kb = (int64_t)(kt < nk0 ? kt : kt - nk0) * TK;
+// C[M][N] = sum over two segments of A_s . B_s (+ bias), fp32 throughout, on
+// the fp32 matrix cores (v_mfma_f32_32x32x2_f32). A_s is [M][k] row-major;
+// B_s is [N][k] (NT: both reduction-contiguous) or [k][N] (NN), chosen per
+// segment, so the rank-r factors are read in their stored layouts (B [r][N]
+// in the forward, A [K][r] in the backward) without transposed copies.
+//
+// A workgroup owns one 32 x 32 tile of C; its 4 waves split each segment's
+// chunks of 8 k into 4 contiguous ranges (wave w takes the w-th), each wave
+// accumulating a whole 32 x 32 partial; the 4 partials are added in wave
+// order through LDS. A wave's consecutive chunks walk along the same rows, so
+// a group of four chunks reads whole cache lines of each of its 32 rows. Small products (the reference's fp32
+// shapes, 512 x 768 x 768) thus get a workgroup per 32 x 32 tile and a
+// quarter of the reduction per SIMD.
+//
+// In a chunk at k0, lane l (row / column l % 32 of its tile, half h = l / 32)
+// holds k = k0 + 4 h + p (p < 4) of its row of A and its column of B, and
+// MFMA p multiplies that pair: MFMA p sums k0 + p (half 0) and k0 + 4 + p
+// (half 1), so the chunk's 8 products are all added, in a fixed order. Rows
+// past M, columns past N and k past a segment's length load as zeros.
+struct F32Seg {
+    const float* a;
+    const float* b;
+    int64_t lda, ldb, k;
+    int nch;  // chunks of 8
+};
+
+// 4 consecutive k of row `row` of a row-major [rows][ld] operand (zeros past
+// the rows and past k_len): one 16-byte load when the 4 lie inside k_len and
+// rows are 16-byte aligned, else 4 checked scalar loads.
+__device__ __forceinline__ void f32_load4(const float* base, int64_t rows, int64_t ld, int64_t row, int64_t k,
+                                          int64_t k_len, bool vec, float (&v)[4]) {
+    if (row < rows && k + 3 < k_len && vec) {
+        const float4 q = *reinterpret_cast<const float4*>(base + row * ld + k);
+        v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
+    } else {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int e = tid + 256 * i;
-            const int m = e >> 4, k = e & 15;
-            const int64_t gm = m0 + m, gk = kb + k;
-            As[k][m] = (gm < M && gk < s.k) ? s.a[gm * s.lda + gk] : 0.f;
-            if constexpr (!NN) {
-                const int64_t gn = n0 + m;
-                Bs[k][m] = (gn < N && gk < s.k) ? s.b[gn * s.ldb + gk] : 0.f;
-            } else {
-                const int kk = e >> 6, n = e & 63;
-                const int64_t gn = n0 + n, gk2 = kb + kk;
-                Bs[kk][n] = (gn < N && gk2 < s.k) ? s.b[gk2 * s.ldb + gn] : 0.f;
-            }
-        }
-        __syncthreads();
-#pragma unroll
-        for (int k = 0; k < TK; ++k) {
-            float a[4], b[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) { a[i] = As[k][ty * 4 + i]; b[i] = Bs[k][tx * 4 + i]; }
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(a[i], b[j], acc[i][j]);
-        }
-        __syncthreads();
+        for (int p = 0; p < 4; ++p) v[p] = (row < rows && k + p < k_len) ? base[row * ld + k + p] : 0.f;
     }
+}
+
+template <bool NN0, bool NN1>
+__global__ __launch_bounds__(256) void gemm_f32_mfma(int64_t M, int64_t N, F32Seg s0, F32Seg s1,
+                                                     const float* __restrict__ bias, float* __restrict__ C,
+                                                     int64_t ldc, int tiles_n) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int rc = lane & 31, h = lane >> 5;
+    const int64_t m0 = (int64_t)(blockIdx.x / tiles_n) * 32, n0 = (int64_t)(blockIdx.x % tiles_n) * 32;
+    f32x16 acc;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int64_t gm = m0 + ty * 4 + i;
-        if (gm >= M) continue;
+    for (int q = 0; q < 16; ++q) acc[q] = 0.f;
+    // This wave's chunks of a segment, [c_begin, c_end), in groups of four
+    // consecutive chunks; a group's operands are loaded one group ahead of
+    // its MFMAs (two register sets), so the loads' latency runs under them.
+    auto run = [&](const F32Seg& s, auto nn_tag) {
+        const int q = (s.nch + 3) / 4;
+        const int c_begin = wave * q, c_end = min(s.nch, c_begin + q);
+        constexpr bool NN = decltype(nn_tag)::value;
+        const bool va = ((s.lda & 3) == 0) && ((reinterpret_cast<uintptr_t>(s.a) & 15) == 0);
+        const bool vb = !NN && ((s.ldb & 3) == 0) && ((reinterpret_cast<uintptr_t>(s.b) & 15) == 0);
+        auto load_group = [&](int c, float (&a)[4][4], float (&b)[4][4]) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int64_t gn = n0 + tx * 4 + j;
-            if (gn < N) C[gm * ldc + gn] = acc[i][j] + (bias ? bias[gn] : 0.f);
+            for (int u = 0; u < 4; ++u) {
+                const int64_t k = (int64_t)(c + u) * 8 + 4 * h;
+                const bool live = c + u < c_end;
+                f32_load4(s.a, live ? M : 0, s.lda, m0 + rc, k, s.k, va, a[u]);
+                if constexpr (!NN) {
+                    f32_load4(s.b, live ? N : 0, s.ldb, n0 + rc, k, s.k, vb, b[u]);
+                } else {
+                    const int64_t n = n0 + rc;
+#pragma unroll
+                    for (int p = 0; p < 4; ++p)
+                        b[u][p] = (live && n < N && k + p < s.k) ? s.b[(k + p) * s.ldb + n] : 0.f;
+                }
+            }
+        };
+        auto mma_group = [&](const float (&a)[4][4], const float (&b)[4][4]) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+#pragma unroll
+                for (int p = 0; p < 4; ++p) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[u][p], b[u][p], acc, 0, 0, 0);
+        };
+        float a0[4][4], b0[4][4], a1[4][4], b1[4][4];
+        int c = c_begin;
+        if (c < c_end) load_group(c, a0, b0);
+        while (c < c_end) {
+            if (c + 4 < c_end) load_group(c + 4, a1, b1);
+            mma_group(a0, b0);
+            c += 4;
+            if (c >= c_end) break;
+            if (c + 4 < c_end) load_group(c + 4, a0, b0);
+            mma_group(a1, b1);
+            c += 4;
         }
+    };
+    run(s0, std::integral_constant<bool, NN0>{});
+    run(s1, std::integral_constant<bool, NN1>{});
+    __shared__ float red[3][16][64];
+    if (wave > 0)
+#pragma unroll
+        for (int q = 0; q < 16; ++q) red[wave - 1][q][lane] = acc[q];
+    __syncthreads();
+    if (wave != 0) return;
+    const int64_t n = n0 + rc;
+    const float bv = (bias && n < N) ? bias[n] : 0.f;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+        const float v = acc[q] + red[0][q][lane] + red[1][q][lane] + red[2][q][lane];
+        const int64_t m = m0 + 8 * (q >> 2) + 4 * h + (q & 3);
+        if (m < M && n < N) C[m * ldc + n] = v + bv;
     }
 }
 
@@ -804,11 +859,20 @@ hipError_t launch_gemm_bf16_multi(int64_t M, const GemmOut* outs, int nout, hipS
     }
 }
 
-hipError_t launch_gemm_f32(bool nn, int64_t M, int64_t N, GemmSegF32 s0, GemmSegF32 s1, const float* bias,
+hipError_t launch_gemm_f32(bool nn, bool nn1, int64_t M, int64_t N, GemmSegF32 s0, GemmSegF32 s1, const float* bias,
                            float* c, int64_t ldc, hipStream_t stream) {
-    const dim3 grid((unsigned)((N + 63) / 64), (unsigned)((M + 63) / 64));
-    if (nn) gemm_f32_kernel<true><<<grid, 256, 0, stream>>>(M, N, s0, s1, bias, c, ldc);
-    else gemm_f32_kernel<false><<<grid, 256, 0, stream>>>(M, N, s0, s1, bias, c, ldc);
+    const int64_t tiles_m = (M + 31) / 32, tiles_n = (N + 31) / 32;
+    if (tiles_m * tiles_n >= ((int64_t)1 << 31) || tiles_n >= ((int64_t)1 << 31)) return hipErrorInvalidValue;
+    auto seg = [](const GemmSegF32& g) {
+        return F32Seg{g.a, g.b, g.lda, g.ldb, g.k, (int)((g.k + 7) / 8)};
+    };
+    const dim3 grid((unsigned)(tiles_m * tiles_n));
+    const F32Seg a = seg(s0), b = seg(s1);
+    const int tn = (int)tiles_n;
+    if (nn && nn1) gemm_f32_mfma<true, true><<<grid, 256, 0, stream>>>(M, N, a, b, bias, c, ldc, tn);
+    else if (nn) gemm_f32_mfma<true, false><<<grid, 256, 0, stream>>>(M, N, a, b, bias, c, ldc, tn);
+    else if (nn1) gemm_f32_mfma<false, true><<<grid, 256, 0, stream>>>(M, N, a, b, bias, c, ldc, tn);
+    else gemm_f32_mfma<false, false><<<grid, 256, 0, stream>>>(M, N, a, b, bias, c, ldc, tn);
     return hipGetLastError();
 }
 

@@ -279,7 +279,8 @@ struct GemmSegF32 {
     int64_t ldb;
     int64_t k;
 };
-hipError_t launch_gemm_f32(bool nn, int64_t M, int64_t N, GemmSegF32 s0, GemmSegF32 s1,
+// nn / nn1: segment 0 / 1's B stored [k][N] (else [N][k]).
+hipError_t launch_gemm_f32(bool nn, bool nn1, int64_t M, int64_t N, GemmSegF32 s0, GemmSegF32 s1,
                            const float* bias, float* c, int64_t ldc, hipStream_t stream);
 // v[t][j] = scale * sum_c X[t][c] * (transpose_p ? P[c*r + j] : P[j*C + c]),
 // masked as in launch_rowproj_bf16; out_t [r][T]; out_ext [T][r] = ext_scale*v.

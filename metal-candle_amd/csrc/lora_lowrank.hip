@@ -1244,41 +1244,112 @@ __global__ __launch_bounds__(256) void lora_bwd_operands(OperandsBatch ob) {
 }
 
 // ------------------------------------------------------------ fp32 path
+// fp32 row projection: one workgroup per token t, ranks in chunks of 8. The
+// 256 threads take columns c = tid, tid + 256, ... of x's row (read once per
+// chunk, coalesced) and accumulate the chunk's 8 products per column in
+// column order; the 8 sums are reduced over each wave by butterfly and over
+// the 4 waves in wave order through LDS.
 __global__ __launch_bounds__(256) void rowproj_f32(const float* __restrict__ X, int64_t T, int64_t C,
                                                    const float* __restrict__ P, int transpose_p, int r,
                                                    float scale, const uint8_t* __restrict__ mask, float keep,
                                                    float* __restrict__ out_t, float* __restrict__ out_ext,
                                                    float ext_scale) {
-    // one wave per (token row, rank index); lanes split the reduction
-    const int lane = lane_id();
-    const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (item >= T * r) return;
-    const int64_t t = item / r;
-    const int j = (int)(item % r);
+    const int64_t t = blockIdx.x;
+    const int lane = lane_id(), wave = threadIdx.x >> 6;
     const float* xr = X + t * C;
-    float s = 0.f;
-    for (int64_t c = lane; c < C; c += kWave) s += xr[c] * (transpose_p ? P[c * r + j] : P[(int64_t)j * C + c]);
-    s = wave_sum(s);
-    if (lane == 0) {
-        float v = s * scale;
-        if (mask) v = mask[t * r + j] ? v * keep : 0.f;
-        if (out_t) out_t[(int64_t)j * T + t] = v;
-        if (out_ext) out_ext[t * r + j] = v * ext_scale;
+    __shared__ float red[4][8];
+    for (int j0 = 0; j0 < r; j0 += 8) {
+        const int nj = r - j0 < 8 ? r - j0 : 8;
+        float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        for (int64_t c = threadIdx.x; c < C; c += 256) {
+            const float xv = xr[c];
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                if (j < nj) acc[j] += xv * (transpose_p ? P[c * r + j0 + j] : P[(int64_t)(j0 + j) * C + c]);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float v = wave_sum(acc[j]);
+            if (lane == 0) red[wave][j] = v;
+        }
+        __syncthreads();
+        if (threadIdx.x < nj) {
+            const int j = j0 + (int)threadIdx.x;
+            float v = red[0][threadIdx.x] + red[1][threadIdx.x] + red[2][threadIdx.x] + red[3][threadIdx.x];
+            v *= scale;
+            if (mask) v = mask[t * r + j] ? v * keep : 0.f;
+            if (out_t) out_t[(int64_t)j * T + t] = v;
+            if (out_ext) out_ext[t * r + j] = v * ext_scale;
+        }
+        __syncthreads();
     }
 }
-
+// fp32 column reduction out[j][c] = scale * sum_t Pt[j][t] X[t][c] (or out
+// [c][j] with transpose_out): a workgroup owns 16 columns and a chunk of 8
+// ranks; its 256 threads are 4 column quads x 64 token slices, slice s
+// summing t = s, s + 64, ... in order (one 16-byte load of x per token when
+// C % 4 == 0, the 8 Pt values broadcast); the 64 slice sums are added in
+// slice order in two LDS stages (8 runs of 8, then the runs).
 __global__ __launch_bounds__(256) void colreduce_f32(const float* __restrict__ X, int64_t T, int64_t C,
                                                      const float* __restrict__ Pt, int r, float scale,
-                                                     int transpose_out, float* __restrict__ out) {
-    // thread per (j, c), c fastest: X reads are coalesced, Pt reads broadcast
-    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= (int64_t)r * C) return;
-    const int64_t j = idx / C, c = idx % C;
-    float s = 0.f;
-    for (int64_t t = 0; t < T; ++t) s += Pt[j * T + t] * X[t * C + c];
-    s *= scale;
-    if (transpose_out) out[c * r + j] = s;
-    else out[j * C + c] = s;
+                                                     int transpose_out, float* __restrict__ out, int64_t ctiles) {
+    const int64_t c0 = (blockIdx.x % ctiles) * 16;
+    const int j0 = (int)(blockIdx.x / ctiles) * 8;
+    const int nj = r - j0 < 8 ? r - j0 : 8;
+    const int cq = threadIdx.x & 3, sl = threadIdx.x >> 2;
+    const int64_t c = c0 + 4 * cq;
+    const bool vec = (C & 3) == 0 && c + 3 < C;
+    float acc[8][4];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[j][e] = 0.f;
+    for (int64_t t = sl; t < T; t += 64) {
+        float xv[4];
+        if (vec) {
+            const float4 q = *reinterpret_cast<const float4*>(X + t * C + c);
+            xv[0] = q.x; xv[1] = q.y; xv[2] = q.z; xv[3] = q.w;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) xv[e] = c + e < C ? X[t * C + c + e] : 0.f;
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float pv = j < nj ? Pt[(int64_t)(j0 + j) * T + t] : 0.f;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[j][e] += pv * xv[e];
+        }
+    }
+    __shared__ float red[64][8][17];  // [slice][rank][column]
+    __shared__ float red2[8][8][17];  // [run][rank][column]
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) red[sl][j][4 * cq + e] = acc[j][e];
+    __syncthreads();
+    {
+        // thread -> (run, rank, 2 columns): 8 x 8 x 8 = 512 sums over 2 passes
+        for (int i = threadIdx.x; i < 8 * 8 * 16; i += 256) {
+            const int col = i & 15, j = (i >> 4) & 7, run = i >> 7;
+            float v = red[8 * run][j][col];
+#pragma unroll
+            for (int k = 1; k < 8; ++k) v += red[8 * run + k][j][col];
+            red2[run][j][col] = v;
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x < 8 * 16) {
+        const int col = threadIdx.x & 15, j = threadIdx.x >> 4;
+        float v = red2[0][j][col];
+#pragma unroll
+        for (int k = 1; k < 8; ++k) v += red2[k][j][col];
+        const int64_t cc = c0 + col;
+        if (j < nj && cc < C) {
+            v *= scale;
+            if (transpose_out) out[cc * r + j0 + j] = v;
+            else out[(int64_t)(j0 + j) * C + cc] = v;
+        }
+    }
 }
 
 }  // namespace
@@ -1755,17 +1826,18 @@ hipError_t launch_rowsplit(int64_t T, int r, const RowsplitJob* jobs, int n, hip
 hipError_t launch_rowproj_f32(const float* X, int64_t T, int64_t C, const float* P, bool transpose_p,
                               int r, float scale, const uint8_t* mask, float keep, float* out_t,
                               float* out_ext, float ext_scale, hipStream_t stream) {
-    const int64_t items = T * r;
-    rowproj_f32<<<dim3((unsigned)((items + 3) / 4)), 256, 0, stream>>>(X, T, C, P, transpose_p ? 1 : 0, r, scale,
-                                                                      mask, keep, out_t, out_ext, ext_scale);
+    if (T >= ((int64_t)1 << 31)) return hipErrorInvalidValue;
+    rowproj_f32<<<dim3((unsigned)T), 256, 0, stream>>>(X, T, C, P, transpose_p ? 1 : 0, r, scale, mask, keep, out_t,
+                                                       out_ext, ext_scale);
     return hipGetLastError();
 }
 
 hipError_t launch_colreduce_f32(const float* X, int64_t T, int64_t C, const float* Pt, int r,
                                 float scale, bool transpose_out, float* out, hipStream_t stream) {
-    const int64_t n = (int64_t)r * C;
-    colreduce_f32<<<dim3((unsigned)((n + 255) / 256)), 256, 0, stream>>>(X, T, C, Pt, r, scale,
-                                                                         transpose_out ? 1 : 0, out);
+    const int64_t ctiles = (C + 15) / 16, jchunks = (r + 7) / 8;
+    if (ctiles * jchunks >= ((int64_t)1 << 31)) return hipErrorInvalidValue;
+    colreduce_f32<<<dim3((unsigned)(ctiles * jchunks)), 256, 0, stream>>>(X, T, C, Pt, r, scale,
+                                                                          transpose_out ? 1 : 0, out, ctiles);
     return hipGetLastError();
 }
 
