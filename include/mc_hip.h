@@ -172,7 +172,9 @@ mc_status mc_transpose_bf16(int64_t rows, int64_t cols, const void* in, void* ou
 
 /* RMSNorm over the last dim of x [rows, dim]:
  *   y = x / sqrt(mean(x^2) + eps) * w     (w == NULL: no weight, as FusedRMSNormOp)
- * x, w, y in dtype; rstd [rows] fp32 (may be NULL) receives 1/sqrt(mean + eps). */
+ * x, w, y in dtype; rstd [rows] fp32 (may be NULL) receives 1/sqrt(mean + eps).
+ * rows <= 67108860 (one wave per row; a launch holds at most 2^32 - 1
+ * work-items), as for mc_layernorm_fwd; larger: MC_ERR_SHAPE. */
 mc_status mc_rmsnorm_fwd(int64_t rows, int64_t dim, float eps, int32_t dtype, const void* x,
                          const void* w, void* y, float* rstd, hipStream_t stream);
 
@@ -315,7 +317,9 @@ mc_status mc_layernorm_bwd(int64_t rows, int64_t dim, float eps, int32_t dtype, 
 
 /* log-softmax over the last dim (candle_nn::ops::log_softmax as
  * cross_entropy_loss uses it, src/training/loss.rs:108):
- *   y = (x - max) - log(sum(exp(x - max)));  backward dx = dy - exp(y) sum(dy). */
+ *   y = (x - max) - log(sum(exp(x - max)));  backward dx = dy - exp(y) sum(dy).
+ * rows <= 16777215 (one 256-thread workgroup per row), as for the
+ * cross-entropy calls; larger: MC_ERR_SHAPE. */
 mc_status mc_log_softmax_fwd(int64_t rows, int64_t dim, int32_t dtype, const void* x, void* y,
                              hipStream_t stream);
 mc_status mc_log_softmax_bwd(int64_t rows, int64_t dim, int32_t dtype, const void* y,
@@ -333,7 +337,7 @@ mc_status mc_log_softmax_bwd(int64_t rows, int64_t dim, int32_t dtype, const voi
  * Where the reference returns an error the loss is NaN instead (the count is
  * only known on the device): every row ignored, or a counted target >= vocab. */
 typedef struct mc_xent_desc {
-    int64_t rows;          /* >= 1 */
+    int64_t rows;          /* 1 .. 16777215 */
     int64_t vocab;         /* >= 1 */
     int64_t ignore_index;  /* < 0: none (the reference's Option<u32> None) */
     float smoothing;       /* [0, 1) */

@@ -86,9 +86,18 @@ mc_status check_lora_desc(const mc_lora_desc* d) {
     return MC_OK;
 }
 
-mc_status check_rows(int64_t rows, int64_t dim, const char* op) {
+// One launch holds at most 2^32 - 1 work-items. The RMSNorm and LayerNorm
+// forward kernels run one 64-lane wave per row, four rows per 256-thread
+// workgroup; log_softmax and cross-entropy one 256-thread workgroup per row.
+// (Softmax splits its launches by rows and has no such bound.)
+constexpr int64_t kMaxWaveRows = ((((int64_t)1 << 32) - 1) / 256) * 4;  // 67108860
+constexpr int64_t kMaxBlockRows = (((int64_t)1 << 32) - 1) / 256;       // 16777215
+
+mc_status check_rows(int64_t rows, int64_t dim, const char* op, int64_t max_rows = INT64_MAX) {
     MC_CHECK(rows >= 1 && dim >= 1, MC_ERR_SHAPE, "%s: rows and dim must be >= 1, got %lld x %lld", op,
              (long long)rows, (long long)dim);
+    MC_CHECK(rows <= max_rows, MC_ERR_SHAPE, "%s: rows must be <= %lld, got %lld", op, (long long)max_rows,
+             (long long)rows);
     return MC_OK;
 }
 
@@ -355,7 +364,7 @@ mc_status mc_transpose_bf16(int64_t rows, int64_t cols, const void* in, void* ou
 
 mc_status mc_rmsnorm_fwd(int64_t rows, int64_t dim, float eps, int32_t dtype, const void* x, const void* w,
                          void* y, float* rstd, hipStream_t stream) {
-    mc_status s = check_rows(rows, dim, "RMSNorm");
+    mc_status s = check_rows(rows, dim, "RMSNorm", kMaxWaveRows);
     if (s != MC_OK) return s;
     if ((s = check_dtype(dtype, "RMSNorm")) != MC_OK) return s;
     MC_CHECK(eps >= 0.0f && std::isfinite(eps), MC_ERR_VALUE, "RMSNorm: eps must be finite and >= 0");
@@ -608,7 +617,7 @@ size_t mc_layernorm_bwd_workspace_size(int64_t rows, int64_t dim) {
 
 mc_status mc_layernorm_fwd(int64_t rows, int64_t dim, float eps, int32_t dtype, const void* x, const void* w,
                            const void* b, void* y, float* mean, float* rstd, hipStream_t stream) {
-    mc_status s = check_rows(rows, dim, "LayerNorm");
+    mc_status s = check_rows(rows, dim, "LayerNorm", kMaxWaveRows);
     if (s != MC_OK) return s;
     if ((s = check_dtype(dtype, "LayerNorm")) != MC_OK) return s;
     MC_CHECK(eps >= 0.0f && std::isfinite(eps), MC_ERR_VALUE, "LayerNorm: eps must be finite and >= 0");
@@ -647,10 +656,9 @@ mc_status mc_layernorm_bwd(int64_t rows, int64_t dim, float eps, int32_t dtype, 
 }
 
 mc_status mc_log_softmax_fwd(int64_t rows, int64_t dim, int32_t dtype, const void* x, void* y, hipStream_t stream) {
-    mc_status s = check_rows(rows, dim, "log_softmax");
+    mc_status s = check_rows(rows, dim, "log_softmax", kMaxBlockRows);
     if (s != MC_OK) return s;
     if ((s = check_dtype(dtype, "log_softmax")) != MC_OK) return s;
-    MC_CHECK(rows < 2147483647, MC_ERR_SHAPE, "log_softmax: rows must be < 2^31");
     MC_CHECK(x && y, MC_ERR_NULL, "log_softmax: x and y must not be NULL");
     const double es = dtype == MC_F32 ? 4.0 : 2.0;
     mc::prof::Scope sc(mc::prof::kRowOps, stream, 0.0, es * 2.0 * rows * dim);
@@ -659,10 +667,9 @@ mc_status mc_log_softmax_fwd(int64_t rows, int64_t dim, int32_t dtype, const voi
 
 mc_status mc_log_softmax_bwd(int64_t rows, int64_t dim, int32_t dtype, const void* y, const void* dy, void* dx,
                              hipStream_t stream) {
-    mc_status s = check_rows(rows, dim, "log_softmax backward");
+    mc_status s = check_rows(rows, dim, "log_softmax backward", kMaxBlockRows);
     if (s != MC_OK) return s;
     if ((s = check_dtype(dtype, "log_softmax backward")) != MC_OK) return s;
-    MC_CHECK(rows < 2147483647, MC_ERR_SHAPE, "log_softmax: rows must be < 2^31");
     MC_CHECK(y && dy && dx, MC_ERR_NULL, "log_softmax backward: y, dy and dx must not be NULL");
     const double es = dtype == MC_F32 ? 4.0 : 2.0;
     mc::prof::Scope sc(mc::prof::kRowOps, stream, 0.0, es * 3.0 * rows * dim);
@@ -673,9 +680,9 @@ static mc_status check_xent(const mc_xent_desc* d) {
     MC_CHECK(d != nullptr, MC_ERR_NULL, "cross_entropy: descriptor is NULL");
     mc_status s = check_dtype(d->dtype, "cross_entropy");
     if (s != MC_OK) return s;
-    MC_CHECK(d->rows >= 1 && d->vocab >= 1 && d->rows < 2147483647, MC_ERR_SHAPE,
-             "cross_entropy: rows (%lld) and vocab (%lld) must be >= 1, rows < 2^31", (long long)d->rows,
-             (long long)d->vocab);
+    MC_CHECK(d->rows >= 1 && d->vocab >= 1 && d->rows <= kMaxBlockRows, MC_ERR_SHAPE,
+             "cross_entropy: rows (%lld) and vocab (%lld) must be >= 1, rows <= %lld", (long long)d->rows,
+             (long long)d->vocab, (long long)kMaxBlockRows);
     // cross_entropy_loss_with_smoothing: "smoothing must be in [0, 1), got {}" (loss.rs:214-219)
     MC_CHECK(d->smoothing >= 0.0f && d->smoothing < 1.0f, MC_ERR_VALUE, "smoothing must be in [0, 1), got %g",
              (double)d->smoothing);

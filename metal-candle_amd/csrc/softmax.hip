@@ -28,6 +28,10 @@ namespace mc {
 namespace {
 
 constexpr int kRowsPerBlock = 4;
+// The backward vector kernel runs one row (one wave) per workgroup: on the
+// 8192 x 8192 fp32 rows it measured 179 -> 168 us against four rows per
+// workgroup, while the forward is faster at four (108 us against 115 at one).
+constexpr int kBwdRowsPerBlock = 1;
 constexpr float kLog2e = 1.4426950408889634f;
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -43,13 +47,13 @@ __device__ __forceinline__ int64_t row_limit(int64_t row, int64_t dim, int64_t c
 // out-of-range offsets (no memory traffic, zeros), and the masks applied as
 // value selects.
 template <typename T, int VPL>
-__global__ __launch_bounds__(256) void softmax_fwd_vec(int64_t rows, int dim, int64_t causal_rows,
+__global__ __launch_bounds__(256) void softmax_fwd_vec(int64_t rbase, int64_t rows, int dim, int64_t causal_rows,
                                                        const T* __restrict__ s, T* __restrict__ p) {
     constexpr int N = BVec<T>::N;
     constexpr int ES = (int)sizeof(T);
     const int lane = lane_id();
     const int wave = wave_id();
-    const int64_t r0 = (int64_t)blockIdx.x * kRowsPerBlock;
+    const int64_t r0 = rbase + (int64_t)blockIdx.x * kRowsPerBlock;
     const int64_t row = r0 + wave;
     if (row >= rows) return;
     const int64_t nrows = rows - r0 < kRowsPerBlock ? rows - r0 : kRowsPerBlock;
@@ -99,10 +103,11 @@ __global__ __launch_bounds__(256) void softmax_fwd_vec(int64_t rows, int dim, in
 }
 
 template <typename T>
-__global__ __launch_bounds__(256) void softmax_fwd_scalar(int64_t rows, int64_t dim, int64_t causal_rows,
-                                                          const T* __restrict__ s, T* __restrict__ p) {
+__global__ __launch_bounds__(256) void softmax_fwd_scalar(int64_t rbase, int64_t rows, int64_t dim,
+                                                          int64_t causal_rows, const T* __restrict__ s,
+                                                          T* __restrict__ p) {
     const int lane = lane_id();
-    const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+    const int64_t row = rbase + (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
     if (row >= rows) return;
     const int64_t lim = row_limit(row, dim, causal_rows);
     const T* sr = s + row * dim;
@@ -120,17 +125,19 @@ __global__ __launch_bounds__(256) void softmax_fwd_scalar(int64_t rows, int64_t 
 }
 
 template <typename T, int VPL>
-__global__ __launch_bounds__(256) void softmax_bwd_vec(int64_t rows, int dim, int64_t causal_rows,
-                                                       const T* __restrict__ p, const T* __restrict__ dp,
-                                                       T* __restrict__ ds) {
+__global__ __launch_bounds__(64 * kBwdRowsPerBlock) void softmax_bwd_vec(int64_t rbase, int64_t rows, int dim,
+                                                                          int64_t causal_rows,
+                                                                          const T* __restrict__ p,
+                                                                          const T* __restrict__ dp,
+                                                                          T* __restrict__ ds) {
     constexpr int N = BVec<T>::N;
     constexpr int ES = (int)sizeof(T);
     const int lane = lane_id();
     const int wave = wave_id();
-    const int64_t r0 = (int64_t)blockIdx.x * kRowsPerBlock;
+    const int64_t r0 = rbase + (int64_t)blockIdx.x * kBwdRowsPerBlock;
     const int64_t row = r0 + wave;
     if (row >= rows) return;
-    const int64_t nrows = rows - r0 < kRowsPerBlock ? rows - r0 : kRowsPerBlock;
+    const int64_t nrows = rows - r0 < kBwdRowsPerBlock ? rows - r0 : kBwdRowsPerBlock;
     const __amdgpu_buffer_rsrc_t rp = make_rsrc(p + r0 * dim, nrows * dim * ES);
     const __amdgpu_buffer_rsrc_t rg = make_rsrc(dp + r0 * dim, nrows * dim * ES);
     const __amdgpu_buffer_rsrc_t rd = make_rsrc(ds + r0 * dim, nrows * dim * ES);
@@ -168,11 +175,11 @@ __global__ __launch_bounds__(256) void softmax_bwd_vec(int64_t rows, int dim, in
 }
 
 template <typename T>
-__global__ __launch_bounds__(256) void softmax_bwd_scalar(int64_t rows, int64_t dim, int64_t causal_rows,
-                                                          const T* __restrict__ p, const T* __restrict__ dp,
-                                                          T* __restrict__ ds) {
+__global__ __launch_bounds__(256) void softmax_bwd_scalar(int64_t rbase, int64_t rows, int64_t dim,
+                                                          int64_t causal_rows, const T* __restrict__ p,
+                                                          const T* __restrict__ dp, T* __restrict__ ds) {
     const int lane = lane_id();
-    const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+    const int64_t row = rbase + (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
     if (row >= rows) return;
     const int64_t lim = row_limit(row, dim, causal_rows);
     const T* pr = p + row * dim;
@@ -458,9 +465,12 @@ WideShape wide_shape(int64_t dim) {
 // One workgroup per row: launches of at most 2^32 / threads - 1 workgroups
 // (a launch's thread count is 32-bit), each given its first row.
 template <typename F>
-void for_row_chunks(int64_t rows, int threads, F&& launch) {
-    const int64_t cap = (((int64_t)1 << 32) - 1) / threads;
-    for (int64_t r0 = 0; r0 < rows; r0 += cap) launch(r0, dim3((unsigned)(rows - r0 < cap ? rows - r0 : cap)));
+void for_row_chunks(int64_t rows, int threads, F&& launch, int rows_per_block = 1) {
+    const int64_t cap = (((int64_t)1 << 32) - 1) / threads * rows_per_block;
+    for (int64_t r0 = 0; r0 < rows; r0 += cap) {
+        const int64_t n = rows - r0 < cap ? rows - r0 : cap;
+        launch(r0, dim3((unsigned)((n + rows_per_block - 1) / rows_per_block)));
+    }
 }
 
 template <typename T>
@@ -472,7 +482,6 @@ int vpl_for(int64_t dim) {
 
 template <typename T>
 hipError_t fwd_impl(int64_t rows, int64_t dim, int64_t causal, const void* s, void* p, hipStream_t st) {
-    const dim3 grid((unsigned)((rows + kRowsPerBlock - 1) / kRowsPerBlock));
     const T* sp = static_cast<const T*>(s);
     T* pp = static_cast<T*>(p);
     const RowPath path = row_path<T>(dim, 8);
@@ -492,14 +501,19 @@ hipError_t fwd_impl(int64_t rows, int64_t dim, int64_t causal, const void* s, vo
         });
     } else if (path == RowPath::kWave) {
         const int d = (int)dim;
-        switch (vpl_for<T>(dim)) {
-            case 1: softmax_fwd_vec<T, 1><<<grid, 256, 0, st>>>(rows, d, causal, sp, pp); break;
-            case 2: softmax_fwd_vec<T, 2><<<grid, 256, 0, st>>>(rows, d, causal, sp, pp); break;
-            case 4: softmax_fwd_vec<T, 4><<<grid, 256, 0, st>>>(rows, d, causal, sp, pp); break;
-            default: softmax_fwd_vec<T, 8><<<grid, 256, 0, st>>>(rows, d, causal, sp, pp); break;
-        }
+        const int vpl = vpl_for<T>(dim);
+        for_row_chunks(rows, 256, [&](int64_t r0, dim3 g) {
+            switch (vpl) {
+                case 1: softmax_fwd_vec<T, 1><<<g, 256, 0, st>>>(r0, rows, d, causal, sp, pp); break;
+                case 2: softmax_fwd_vec<T, 2><<<g, 256, 0, st>>>(r0, rows, d, causal, sp, pp); break;
+                case 4: softmax_fwd_vec<T, 4><<<g, 256, 0, st>>>(r0, rows, d, causal, sp, pp); break;
+                default: softmax_fwd_vec<T, 8><<<g, 256, 0, st>>>(r0, rows, d, causal, sp, pp); break;
+            }
+        }, kRowsPerBlock);
     } else {
-        softmax_fwd_scalar<T><<<grid, 256, 0, st>>>(rows, dim, causal, sp, pp);
+        for_row_chunks(rows, 256, [&](int64_t r0, dim3 g) {
+            softmax_fwd_scalar<T><<<g, 256, 0, st>>>(r0, rows, dim, causal, sp, pp);
+        }, kRowsPerBlock);
     }
     return hipGetLastError();
 }
@@ -507,7 +521,6 @@ hipError_t fwd_impl(int64_t rows, int64_t dim, int64_t causal, const void* s, vo
 template <typename T>
 hipError_t bwd_impl(int64_t rows, int64_t dim, int64_t causal, const void* p, const void* dp, void* ds,
                     hipStream_t st) {
-    const dim3 grid((unsigned)((rows + kRowsPerBlock - 1) / kRowsPerBlock));
     const T* pp = static_cast<const T*>(p);
     const T* gp = static_cast<const T*>(dp);
     T* dsp = static_cast<T*>(ds);
@@ -531,14 +544,20 @@ hipError_t bwd_impl(int64_t rows, int64_t dim, int64_t causal, const void* p, co
         });
     } else if (path == RowPath::kWave) {
         const int d = (int)dim;
-        switch (vpl_for<T>(dim)) {
-            case 1: softmax_bwd_vec<T, 1><<<grid, 256, 0, st>>>(rows, d, causal, pp, gp, dsp); break;
-            case 2: softmax_bwd_vec<T, 2><<<grid, 256, 0, st>>>(rows, d, causal, pp, gp, dsp); break;
-            case 4: softmax_bwd_vec<T, 4><<<grid, 256, 0, st>>>(rows, d, causal, pp, gp, dsp); break;
-            default: softmax_bwd_vec<T, 8><<<grid, 256, 0, st>>>(rows, d, causal, pp, gp, dsp); break;
-        }
+        const int vpl = vpl_for<T>(dim);
+        constexpr int nt = 64 * kBwdRowsPerBlock;
+        for_row_chunks(rows, nt, [&](int64_t r0, dim3 g) {
+            switch (vpl) {
+                case 1: softmax_bwd_vec<T, 1><<<g, nt, 0, st>>>(r0, rows, d, causal, pp, gp, dsp); break;
+                case 2: softmax_bwd_vec<T, 2><<<g, nt, 0, st>>>(r0, rows, d, causal, pp, gp, dsp); break;
+                case 4: softmax_bwd_vec<T, 4><<<g, nt, 0, st>>>(r0, rows, d, causal, pp, gp, dsp); break;
+                default: softmax_bwd_vec<T, 8><<<g, nt, 0, st>>>(r0, rows, d, causal, pp, gp, dsp); break;
+            }
+        }, kBwdRowsPerBlock);
     } else {
-        softmax_bwd_scalar<T><<<grid, 256, 0, st>>>(rows, dim, causal, pp, gp, dsp);
+        for_row_chunks(rows, 256, [&](int64_t r0, dim3 g) {
+            softmax_bwd_scalar<T><<<g, 256, 0, st>>>(r0, rows, dim, causal, pp, gp, dsp);
+        }, kRowsPerBlock);
     }
     return hipGetLastError();
 }

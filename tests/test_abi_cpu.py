@@ -82,6 +82,28 @@ def test_rowop_validation(mc):
     assert L.mc_profile_read(9, None, None, None, None) == 5
 
 
+def test_rowop_row_limits(mc):
+    """One launch holds at most 2^32 - 1 work-items: the wave-per-row forward
+    kernels (4 rows per 256 threads) stop at 67108860 rows, the
+    workgroup-per-row kernels at 16777215; softmax splits its launches."""
+    L = mc._lib.lib()
+    fake = ctypes.c_void_p(256)
+    wave_max, block_max = ((2**32 - 1) // 256) * 4, (2**32 - 1) // 256
+    assert L.mc_rmsnorm_fwd(wave_max + 1, 8, 1e-6, 0, fake, None, fake, None, None) == 2
+    assert "rows must be <= 67108860" in mc._lib.last_error()
+    assert L.mc_layernorm_fwd(wave_max + 1, 8, 1e-6, 0, fake, None, None, fake, None, None, None) == 2
+    assert L.mc_log_softmax_fwd(block_max + 1, 8, 0, fake, fake, None) == 2
+    assert "rows must be <= 16777215" in mc._lib.last_error()
+    assert L.mc_log_softmax_bwd(block_max + 1, 8, 0, fake, fake, fake, None) == 2
+    d = mc._lib.XentDesc(block_max + 1, 8, -100, 0.0, 0)
+    assert L.mc_cross_entropy_fwd(ctypes.byref(d), fake, fake, fake, None, None, 0, None) == 2
+    # below the bound the shape passes and the next check (NULL output) answers
+    assert L.mc_rmsnorm_fwd(wave_max, 8, 1e-6, 0, fake, None, None, None, None) == 1
+    assert L.mc_log_softmax_fwd(block_max, 8, 0, fake, None, None) == 1
+    # softmax has no row bound: a NULL output is the first error at any row count
+    assert L.mc_softmax_fwd(2**40, 8, 0, 0, fake, None, None) == 1
+
+
 def test_dropout_mask_matches_oracle(mc):
     import oracle
 

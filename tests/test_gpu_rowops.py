@@ -229,6 +229,35 @@ def test_softmax_config_full_size(mc, dev, dtype, shape):
     assert (ds.reshape(-1, S, S)[:, mask] == 0).all()
 
 
+@pytest.mark.parametrize("dim", [4, 3])
+def test_softmax_rows_past_one_launch(mc, dev, dim):
+    """2^26 + 37 short rows: more than one launch's 2^32 - 1 work-items at one
+    wave per row, so the forward (4 rows per 256 threads) and the backward (one
+    row per 64 threads) split the rows over two launches; dim 3 takes the
+    scalar kernels. Causal over 3 columns, so each row's mask depends on its
+    global index across the launch boundary. Rows next to the boundaries and a
+    seeded sample are checked against the oracle; P's row sums on every row."""
+    rows, S = (1 << 26) + 37, 3
+    gen = torch.Generator(device=dev).manual_seed(7)
+    s = torch.randn(rows, dim, generator=gen, device=dev) * 3
+    dp = torch.randn(rows, dim, generator=gen, device=dev)
+    p = mc.softmax_forward(s, causal_rows=S)
+    ds = mc.softmax_backward(p, dp, causal_rows=S)
+    torch.cuda.synchronize()
+    fwd_cap, bwd_cap = ((2**32 - 1) // 256) * 4, (2**32 - 1) // 64
+    edge = [0, 1, 2, 3, rows - 3, rows - 2, rows - 1]
+    for c in (fwd_cap, bwd_cap):
+        edge += list(range(c - 3, c + 3))
+    ids = np.unique(np.concatenate([np.array(edge), _sampled_rows(rows, 256, 3)]))
+    idx = torch.from_numpy(ids).to(dev)
+    s2, p2, dp2, ds2 = (t.index_select(0, idx) for t in (s, p, dp, ds))
+    p_ref = oracle.softmax_fwd(to_np(s2), causal_rows=S, row_ids=ids)
+    assert rel_err(p2, p_ref) <= F32_TOL
+    ds_ref = oracle.softmax_bwd(to_np(p2), to_np(dp2), causal_rows=S, row_ids=ids)
+    assert rel_err(ds2, ds_ref) <= F32_TOL
+    assert torch.allclose(p.sum(-1), torch.ones(rows, device=dev), atol=1e-5)
+
+
 def test_norm_bwd_many_calls_and_streams(mc, dev):
     """The fixed-order dw (and LayerNorm's db) reductions over 8, 38 and 512
     row blocks: 300 calls in a row over three shapes, and calls on two
