@@ -39,7 +39,14 @@ Scope::Scope(Kind kind, hipStream_t stream, double flops, double bytes) : stream
     if (g_used >= kMaxEntries) return;  // record nothing past the cap
     if (g_used == g_entries.size()) {
         Entry e;
-        if (hipEventCreate(&e.begin) != hipSuccess || hipEventCreate(&e.end) != hipSuccess) return;
+        // Timing-only events: no system-scope fence when they are recorded.
+        // The default fence writes back and invalidates the caches at every
+        // event, which slows the kernel that follows and adds a few
+        // microseconds to every short scope.
+        constexpr unsigned kFlags = hipEventDisableSystemFence;
+        if (hipEventCreateWithFlags(&e.begin, kFlags) != hipSuccess ||
+            hipEventCreateWithFlags(&e.end, kFlags) != hipSuccess)
+            return;
         g_entries.push_back(e);
     }
     Entry& e = g_entries[g_used];
