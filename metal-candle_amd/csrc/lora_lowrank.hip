@@ -1484,15 +1484,18 @@ hipError_t launch_lora_bwd_operands(const OperandsCall* calls, int n, int64_t T,
     return hipGetLastError();
 }
 
-// Column-tile count times splits should give >= ~1024 workgroups, with each
+// Column-tile count times splits at most 512 workgroups per job, with each
 // wave walking at least eight 32-row steps (c4 medians: a cap of T / 1024
 // splits ran the low-rank kernels 1% faster than T / 512, T / 256 and
-// T / 2048 ran slower). A split's rows of X are one
+// T / 2048 ran slower). The kernel holds three workgroups per CU at r <= 32,
+// so c4's down dA (70 column tiles x 7 splits) and dB (12 x 16) share one
+// round of 768; at ~1536 per job (16 splits for the dA) the launch took 1.7
+// rounds, measured 0.538 -> 0.535 ms of low-rank time per step. A split's rows of X are one
 // buffer resource with 32-bit offsets, so a split never spans 2^31 bytes:
 // that bound wins over the step count (wide X, e.g. a vocabulary-sized dY).
 int colreduce_splits(int64_t T, int64_t C) {
     const int64_t ctiles = (C + 127) / 128;
-    int64_t s = (1536 + ctiles - 1) / ctiles;
+    int64_t s = 512 / ctiles;
     const int64_t max_s = (T + 1023) / 1024;  // >= 8 steps per wave
     if (s > max_s) s = max_s;
     if (s < 1) s = 1;
@@ -1669,12 +1672,18 @@ hipError_t launch_split_sum(const SumJob* jobs, int n, hipStream_t stream) {
     return hipGetLastError();
 }
 
-// Splits of the fused dY pass: at least ~512 workgroups over the column
-// groups and splits, each split at least eight 32-row steps, and no split's
-// rows of dY spanning 2^31 bytes (32-bit buffer offsets).
+// Splits of the fused dY pass: at most 256 workgroups per job over its
+// column groups and splits, each split at least eight 32-row steps, and no
+// split's rows of dY spanning 2^31 bytes (32-bit buffer offsets). The
+// kernel holds two workgroups per CU at r <= 16 (one at r <= 32), so the
+// grouped gate / up launch (two jobs) runs in one round of the 256 CUs.
+// The earlier ~512 per job (c4: 2 x 18 groups x 29 splits = 1044
+// workgroups) ran two full rounds and a third of 20 workgroups; the
+// one-round split measured 0.559 -> 0.541 ms of low-rank time per c4 step
+// (~256 per job; ~512 per job exactly filling two rounds: 0.549).
 int dy_splits(int64_t T, int64_t N) {
     const int64_t groups = dy_groups(N);
-    int64_t s = (512 + groups - 1) / groups;
+    int64_t s = 256 / groups;
     const int64_t max_s = (T + 255) / 256;
     if (s > max_s) s = max_s;
     if (s < 1) s = 1;
