@@ -492,7 +492,7 @@ def c1_lora_f32(mc, dev, iters):
     A [768, 8] kaiming-uniform, B [8, 768] ~N(0, 0.02), rank 8, alpha 16, no
     dropout; forward y and backward (dX, dA, dB) with dY ~N(0, 1e-2). Each
     call is timed whole (every launch of it) with events on the stream,
-    median of `iters` timed repetitions of 20 calls. FLOPs count the
+    median of `iters` timed repetitions of 20 calls queued behind a GPU spin. FLOPs count the
     algorithmic products: forward 2TKN + 2TKr + 2TrN, backward 2TNK + 2TrK (dX),
     2TNr (G), 2TKr (dA), 2TrN (dB); the roofline is the fp32 peak (vector
     and matrix fp32 are both 157.3 TFLOP/s on MI355X)."""
@@ -521,6 +521,7 @@ def c1_lora_f32(mc, dev, iters):
         times = []
         for _ in range(iters):
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            queue_ahead(torch)  # the 20 calls run back to back after the spin, not at the host's launch rate
             e0.record()
             for _ in range(20):
                 fn()

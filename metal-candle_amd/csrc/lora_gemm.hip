@@ -502,10 +502,14 @@ __attribute__((amdgpu_waves_per_eu(1, 2))) void gemm_bf16_multi(GemmMulti m) {
 // A workgroup owns one 32 x 32 tile of C; its 4 waves split each segment's
 // chunks of 8 k into 4 contiguous ranges (wave w takes the w-th), each wave
 // accumulating a whole 32 x 32 partial; the 4 partials are added in wave
-// order through LDS. A wave's consecutive chunks walk along the same rows, so
-// a group of four chunks reads whole cache lines of each of its 32 rows. Small products (the reference's fp32
-// shapes, 512 x 768 x 768) thus get a workgroup per 32 x 32 tile and a
-// quarter of the reduction per SIMD.
+// order through LDS. Small products (the reference's fp32 shapes, 512 x 768
+// x 768) thus get a workgroup per 32 x 32 tile and a quarter of the
+// reduction per SIMD. A wave moves its row-major operands a group of four
+// chunks (32 k) at a time through a private LDS tile: the global loads give
+// each 8 lanes one whole 128-byte row segment, and the MFMA layout comes back
+// by one 16-byte LDS read per operand and chunk. (Loading the MFMA layout
+// straight from memory touched 32 rows per load instruction, 32 bytes of
+// each: the c1 forward product took 29.6 us, 19.5 us staged.)
 //
 // In a chunk at k0, lane l (row / column l % 32 of its tile, half h = l / 32)
 // holds k = k0 + 4 h + p (p < 4) of its row of A and its column of B, and
@@ -543,48 +547,84 @@ __global__ __launch_bounds__(256) void gemm_f32_mfma(int64_t M, int64_t N, F32Se
     f32x16 acc;
 #pragma unroll
     for (int q = 0; q < 16; ++q) acc[q] = 0.f;
-    // This wave's chunks of a segment, [c_begin, c_end), in groups of four
-    // consecutive chunks; a group's operands are loaded one group ahead of
-    // its MFMAs (two register sets), so the loads' latency runs under them.
+    // Per-wave staging of one group (4 chunks = 32 k) of the row-major
+    // operands: [32 rows][32 k + 4] floats each (the pad staggers the rows'
+    // banks). Global -> registers with whole 128-byte row segments per 8
+    // lanes (lane l: row l / 8 + 8 i, k 4 (l % 8) .. +3), registers -> LDS,
+    // then the MFMA layout back by one 16-byte read per operand and chunk.
+    __shared__ float stage[4][2][32][36];
+    float (*sa)[36] = stage[wave][0];
+    float (*sb)[36] = stage[wave][1];
+    const int lr = lane >> 3, lk = 4 * (lane & 7);
     auto run = [&](const F32Seg& s, auto nn_tag) {
+        constexpr bool NN = decltype(nn_tag)::value;
         const int q = (s.nch + 3) / 4;
         const int c_begin = wave * q, c_end = min(s.nch, c_begin + q);
-        constexpr bool NN = decltype(nn_tag)::value;
+        if (c_begin >= c_end) return;  // wave-uniform
+        const int64_t klim = min<int64_t>(s.k, (int64_t)c_end * 8);  // this wave's k range ends here
         const bool va = ((s.lda & 3) == 0) && ((reinterpret_cast<uintptr_t>(s.a) & 15) == 0);
         const bool vb = !NN && ((s.ldb & 3) == 0) && ((reinterpret_cast<uintptr_t>(s.b) & 15) == 0);
-        auto load_group = [&](int c, float (&a)[4][4], float (&b)[4][4]) {
+        // rows [base0, base0 + 32) of a row-major [rows][ld] operand, k from k0: zeros past rows and klim
+        auto load_rows = [&](const float* base, int64_t rows, int64_t ld, int64_t row0, int64_t k0, bool vec,
+                             float (&v)[4][4]) {
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int64_t k = (int64_t)(c + u) * 8 + 4 * h;
-                const bool live = c + u < c_end;
-                f32_load4(s.a, live ? M : 0, s.lda, m0 + rc, k, s.k, va, a[u]);
-                if constexpr (!NN) {
-                    f32_load4(s.b, live ? N : 0, s.ldb, n0 + rc, k, s.k, vb, b[u]);
-                } else {
-                    const int64_t n = n0 + rc;
-#pragma unroll
-                    for (int p = 0; p < 4; ++p)
-                        b[u][p] = (live && n < N && k + p < s.k) ? s.b[(k + p) * s.ldb + n] : 0.f;
-                }
-            }
+            for (int i = 0; i < 4; ++i) f32_load4(base, rows, ld, row0 + 8 * i + lr, k0 + lk, klim, vec, v[i]);
         };
-        auto mma_group = [&](const float (&a)[4][4], const float (&b)[4][4]) {
+        auto store_rows = [&](float (*st)[36], const float (&v)[4][4]) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                *reinterpret_cast<float4*>(&st[8 * i + lr][lk]) = make_float4(v[i][0], v[i][1], v[i][2], v[i][3]);
+        };
+        // NN: B [k][N] read straight into the MFMA layout (lanes rc of a k
+        // row are consecutive columns), one group ahead in registers
+        auto load_nn = [&](int c, float (&v)[4][4]) {
+            const int64_t n = n0 + rc;
 #pragma unroll
             for (int u = 0; u < 4; ++u)
 #pragma unroll
-                for (int p = 0; p < 4; ++p) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[u][p], b[u][p], acc, 0, 0, 0);
+                for (int p = 0; p < 4; ++p) {
+                    const int64_t k = (int64_t)(c + u) * 8 + 4 * h + p;
+                    v[u][p] = (n < N && k < klim) ? s.b[k * s.ldb + n] : 0.f;
+                }
         };
-        float a0[4][4], b0[4][4], a1[4][4], b1[4][4];
-        int c = c_begin;
-        if (c < c_end) load_group(c, a0, b0);
-        while (c < c_end) {
-            if (c + 4 < c_end) load_group(c + 4, a1, b1);
-            mma_group(a0, b0);
-            c += 4;
-            if (c >= c_end) break;
-            if (c + 4 < c_end) load_group(c + 4, a0, b0);
-            mma_group(a1, b1);
-            c += 4;
+        float ra[4][4], rb[4][4], nb[4][4];
+        load_rows(s.a, M, s.lda, m0, (int64_t)c_begin * 8, va, ra);
+        if constexpr (!NN) load_rows(s.b, N, s.ldb, n0, (int64_t)c_begin * 8, vb, rb);
+        else load_nn(c_begin, rb);
+        for (int c = c_begin; c < c_end; c += 4) {
+            store_rows(sa, ra);
+            if constexpr (!NN) store_rows(sb, rb);
+            else {
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+#pragma unroll
+                    for (int p = 0; p < 4; ++p) nb[u][p] = rb[u][p];
+            }
+            if (c + 4 < c_end) {  // the next group's loads run under this group's MFMAs
+                load_rows(s.a, M, s.lda, m0, (int64_t)(c + 4) * 8, va, ra);
+                if constexpr (!NN) load_rows(s.b, N, s.ldb, n0, (int64_t)(c + 4) * 8, vb, rb);
+                else load_nn(c + 4, rb);
+            }
+            // a wave's LDS operations complete in order: the reads below
+            // see the writes above, and the next group's writes come after
+            // these reads
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int kk = 8 * u + 4 * h;
+                const float4 a4 = *reinterpret_cast<const float4*>(&sa[rc][kk]);
+                float bq[4];
+                if constexpr (!NN) {
+                    const float4 b4 = *reinterpret_cast<const float4*>(&sb[rc][kk]);
+                    bq[0] = b4.x; bq[1] = b4.y; bq[2] = b4.z; bq[3] = b4.w;
+                } else {
+#pragma unroll
+                    for (int p = 0; p < 4; ++p) bq[p] = nb[u][p];
+                }
+                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a4.x, bq[0], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a4.y, bq[1], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a4.z, bq[2], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a4.w, bq[3], acc, 0, 0, 0);
+            }
         }
     };
     run(s0, std::integral_constant<bool, NN0>{});
