@@ -8,10 +8,12 @@
 #include <math.h>
 #include <string.h>
 
+#include <functional>
 #include <mutex>
 #include <random>
 #include <sstream>
 #include <unordered_map>
+#include <unordered_set>
 
 #include "mc_hip.h"
 
@@ -1117,6 +1119,275 @@ Result<void, TrainingError> AsyncExecutor::synchronize() {
     hipError_t e = hipDeviceSynchronize();
     if (e != hipSuccess) return TrainingError::failed(std::string("synchronize: ") + hipGetErrorString(e));
     return {};
+}
+
+// ------------------------------------------------------------------ lazy graph
+std::string node_id_string(NodeId id) { return "NodeId(" + std::to_string(id.id) + ")"; }
+
+DType Operation::output_dtype(const std::vector<DType>& in) const {
+    return in.empty() ? DType::F32 : in[0];  // operation.rs:170-180
+}
+
+Result<const GraphNode*, std::string> ComputationGraph::get_node(NodeId id) const {
+    if (id.id >= nodes_.size()) return "Node " + node_id_string(id) + " not found";  // node.rs:150-156
+    return &nodes_[id.id];
+}
+
+Result<GraphNode*, std::string> ComputationGraph::get_node_mut(NodeId id) {
+    if (id.id >= nodes_.size()) return "Node " + node_id_string(id) + " not found";
+    return &nodes_[id.id];
+}
+
+NodeId ComputationGraph::add_input(const Tensor& tensor) {
+    GraphNode n;  // node.rs:97-110
+    n.id = NodeId{nodes_.size()};
+    n.operation = Operation::input();
+    n.output_shape = tensor.dims();
+    n.output_dtype = tensor.dtype();
+    n.data = GraphNode::Data::Concrete;
+    n.tensor = tensor;
+    nodes_.push_back(std::move(n));
+    return nodes_.back().id;
+}
+
+Result<NodeId, std::string> ComputationGraph::add_node(const Operation& op, const std::vector<NodeId>& inputs) {
+    std::vector<std::vector<int64_t>> shapes;  // node.rs:175-215
+    std::vector<DType> dtypes;
+    for (NodeId i : inputs) {
+        if (i.id >= nodes_.size()) return "Input node " + node_id_string(i) + " not found";
+        shapes.push_back(nodes_[i.id].output_shape);
+        dtypes.push_back(nodes_[i.id].output_dtype);
+    }
+    auto shape = op.output_shape(shapes);
+    if (shape.is_err()) return shape.error();
+    GraphNode n;
+    n.id = NodeId{nodes_.size()};
+    n.operation = op;
+    n.inputs = inputs;
+    n.output_shape = std::move(shape.value());
+    n.output_dtype = op.output_dtype(dtypes);
+    nodes_.push_back(std::move(n));
+    return nodes_.back().id;
+}
+
+Result<std::vector<NodeId>, std::string> ComputationGraph::topological_order(NodeId output) const {
+    // node.rs:222-265: depth-first, each node after its inputs; a node met
+    // again while its own inputs are being visited is a cycle
+    std::vector<NodeId> order;
+    std::unordered_set<size_t> done, active;
+    std::function<Result<void, std::string>(NodeId)> visit = [&](NodeId id) -> Result<void, std::string> {
+        if (done.count(id.id)) return {};
+        if (active.count(id.id)) return "Circular dependency detected at node " + node_id_string(id);
+        auto node = get_node(id);
+        if (node.is_err()) return node.error();
+        active.insert(id.id);
+        for (NodeId in : node.value()->inputs) {
+            auto r = visit(in);
+            if (r.is_err()) return r;
+        }
+        active.erase(id.id);
+        done.insert(id.id);
+        order.push_back(id);
+        return {};
+    };
+    auto r = visit(output);
+    if (r.is_err()) return r.error();
+    return order;
+}
+
+NodeId ComputationGraph::merge_from(const ComputationGraph& other, NodeId target) {
+    // node.rs:275-300: dependencies first, each node copied once (with its
+    // value, if it has one) and its inputs renumbered
+    std::unordered_map<size_t, NodeId> copied;
+    std::function<NodeId(NodeId)> copy = [&](NodeId id) -> NodeId {
+        auto it = copied.find(id.id);
+        if (it != copied.end()) return it->second;
+        GraphNode n = other.nodes_.at(id.id);
+        for (NodeId& in : n.inputs) in = copy(in);
+        n.id = NodeId{nodes_.size()};
+        nodes_.push_back(std::move(n));
+        copied[id.id] = nodes_.back().id;
+        return nodes_.back().id;
+    };
+    return copy(target);
+}
+
+struct LazyTensor::Shared {
+    explicit Shared(const Device& d) : graph(d) {}
+    std::mutex mu;
+    ComputationGraph graph;
+};
+
+Result<LazyTensor, CandleError> LazyTensor::from_tensor(const Tensor& tensor) {
+    LazyTensor t;  // lazy_tensor.rs:95-108: a new graph with one input node
+    t.graph_ = std::make_shared<Shared>(tensor.device());
+    t.node_ = t.graph_->graph.add_input(tensor);
+    t.shape_ = tensor.dims();
+    t.dtype_ = tensor.dtype();
+    t.device_ = tensor.device();
+    return t;
+}
+
+Result<LazyTensor, CandleError> LazyTensor::from_slice(const std::vector<float>& data, std::vector<int64_t> dims,
+                                                       const Device& device) {
+    auto t = Tensor::from_slice(data, std::move(dims), device);
+    if (t.is_err()) return t.error();
+    return from_tensor(t.value());
+}
+
+Result<LazyTensor, CandleError> LazyTensor::zeros(std::vector<int64_t> dims, DType dtype, const Device& device) {
+    auto t = Tensor::zeros(std::move(dims), dtype, device);
+    if (t.is_err()) return t.error();
+    return from_tensor(t.value());
+}
+
+Result<LazyTensor, CandleError> LazyTensor::ones(std::vector<int64_t> dims, DType dtype, const Device& device) {
+    int64_t n = 1;
+    for (int64_t d : dims) n *= d;
+    if (n < 0) return CandleError{"ones: negative dimension in " + dims_to_string(dims)};
+    auto t = Tensor::from_slice(std::vector<float>((size_t)n, 1.f), std::move(dims), device, dtype);
+    if (t.is_err()) return t.error();
+    return from_tensor(t.value());
+}
+
+Result<LazyTensor, CandleError> LazyTensor::add_tensor_to_graph(const Tensor& tensor) const {
+    LazyTensor t = *this;  // lazy_tensor.rs:120-131
+    {
+        std::lock_guard<std::mutex> lk(graph_->mu);
+        t.node_ = graph_->graph.add_input(tensor);
+    }
+    t.shape_ = tensor.dims();
+    t.dtype_ = tensor.dtype();
+    t.device_ = tensor.device();
+    return t;
+}
+
+size_t LazyTensor::graph_size() const {
+    std::lock_guard<std::mutex> lk(graph_->mu);
+    return graph_->graph.len();
+}
+
+bool LazyTensor::is_evaluated() const {
+    std::lock_guard<std::mutex> lk(graph_->mu);
+    auto n = graph_->graph.get_node(node_);
+    return n.is_ok() && n.value()->is_available();
+}
+
+Result<LazyTensor, CandleError> LazyTensor::add_operation(const Operation& op,
+                                                          const std::vector<NodeId>& inputs) const {
+    LazyTensor t = *this;  // lazy_tensor.rs:214-236
+    std::lock_guard<std::mutex> lk(graph_->mu);
+    auto id = graph_->graph.add_node(op, inputs);
+    if (id.is_err()) return CandleError{id.error()};
+    const GraphNode* n = graph_->graph.get_node(id.value()).value();
+    t.node_ = id.value();
+    t.shape_ = n->output_shape;
+    t.dtype_ = n->output_dtype;
+    return t;
+}
+
+NodeId LazyTensor::merge_graph_from(const LazyTensor& other) const {
+    if (graph_ == other.graph_) return other.node_;  // lazy_tensor.rs:238-250
+    std::scoped_lock lk(graph_->mu, other.graph_->mu);
+    return graph_->graph.merge_from(other.graph_->graph, other.node_);
+}
+
+Result<LazyTensor, CandleError> LazyTensor::matmul(const LazyTensor& other) const {
+    return add_operation(Operation::matmul(), {node_, merge_graph_from(other)});
+}
+Result<LazyTensor, CandleError> LazyTensor::add(const LazyTensor& other) const {
+    return add_operation(Operation::add(), {node_, merge_graph_from(other)});
+}
+Result<LazyTensor, CandleError> LazyTensor::mul(const LazyTensor& other) const {
+    return add_operation(Operation::mul(), {node_, merge_graph_from(other)});
+}
+Result<LazyTensor, CandleError> LazyTensor::mul_scalar(float value) const {
+    return add_operation(Operation::mul_scalar(value), {node_});
+}
+Result<LazyTensor, CandleError> LazyTensor::softmax(size_t dim) const {
+    return add_operation(Operation::softmax(dim), {node_});
+}
+Result<LazyTensor, CandleError> LazyTensor::rms_norm(float eps) const {
+    return add_operation(Operation::rms_norm(eps), {node_});
+}
+Result<LazyTensor, CandleError> LazyTensor::lora_fused(const LazyTensor& lora_a, const LazyTensor& lora_b,
+                                                       float scale) const {
+    const NodeId a = merge_graph_from(lora_a), b = merge_graph_from(lora_b);
+    return add_operation(Operation::lora(a, b, scale), {node_, a, b});
+}
+
+Result<Tensor, TrainingError> LazyTensor::eval() const {
+    // lazy_tensor.rs:342-424, with the reference's error texts
+    std::vector<NodeId> order;
+    {
+        std::lock_guard<std::mutex> lk(graph_->mu);
+        auto o = graph_->graph.topological_order(node_);
+        if (o.is_err()) return TrainingError::failed("Failed to compute execution order: " + o.error());
+        order = std::move(o.value());
+    }
+    auto ex = AsyncExecutor::create(device_);
+    if (ex.is_err()) return ex.error();
+    for (NodeId id : order) {
+        Operation op;
+        std::vector<Tensor> inputs;
+        {
+            std::lock_guard<std::mutex> lk(graph_->mu);
+            auto n = graph_->graph.get_node(id);
+            if (n.is_err()) return TrainingError::failed("Failed to get node: " + n.error());
+            if (n.value()->is_available()) continue;
+            op = n.value()->operation;
+            for (NodeId in : n.value()->inputs) {
+                auto i = graph_->graph.get_node(in);
+                if (i.is_err()) return TrainingError::failed("Failed to get input node: " + i.error());
+                if (!i.value()->is_available())
+                    return TrainingError::failed("Input not available: Data not yet available");
+                inputs.push_back(i.value()->tensor);
+            }
+        }
+        auto out = ex.value().execute_operation(op, inputs);  // the device work runs outside the lock
+        if (out.is_err()) return out.error();
+        std::lock_guard<std::mutex> lk(graph_->mu);
+        auto n = graph_->graph.get_node_mut(id);
+        if (n.is_err()) return TrainingError::failed("Failed to get node for result: " + n.error());
+        n.value()->tensor = std::move(out.value());
+        n.value()->data = GraphNode::Data::Available;
+    }
+    auto sync = ex.value().synchronize();
+    if (sync.is_err()) return sync.error();
+    std::lock_guard<std::mutex> lk(graph_->mu);
+    auto n = graph_->graph.get_node(node_);
+    if (n.is_err()) return TrainingError::failed("Failed to get output node: " + n.error());
+    if (!n.value()->is_available()) return TrainingError::failed("Failed to get output tensor: Data not yet available");
+    return n.value()->tensor;
+}
+
+std::string LazyTensor::debug_string() const {
+    std::ostringstream s;  // lazy_tensor.rs:428-438
+    s << "LazyTensor { node_id: " << node_id_string(node_) << ", shape: " << dims_to_string(shape_)
+      << ", device: " << (device_.is_cpu() ? "Cpu" : "Hip(" + std::to_string(device_.ordinal) + ")")
+      << ", graph_size: " << graph_size() << ", .. }";
+    return s.str();
+}
+
+// ------------------------------------------------------------------ LoRALayer::forward_lazy
+Result<LazyTensor, Error> LoRALayer::forward_lazy(const LazyTensor& input) const {
+    // lora.rs:372-439
+    auto a = input.add_tensor_to_graph(lora_a_);
+    if (a.is_err()) return Error::from(TrainingError::failed("Failed to add LoRA A to graph: " + a.error().msg));
+    auto b = input.add_tensor_to_graph(lora_b_);
+    if (b.is_err()) return Error::from(TrainingError::failed("Failed to add LoRA B to graph: " + b.error().msg));
+    if (input.device().is_hip() && config_.dropout == 0.f) {
+        auto y = input.lora_fused(a.value(), b.value(), config_.scaling());
+        if (y.is_err()) return Error::from(TrainingError::failed("Fused LoRA operation failed: " + y.error().msg));
+        return std::move(y.value());
+    }
+    auto hidden = input.matmul(a.value());
+    if (hidden.is_err()) return Error::from(TrainingError::failed("LoRA matmul A failed: " + hidden.error().msg));
+    auto out = hidden.value().matmul(b.value());
+    if (out.is_err()) return Error::from(TrainingError::failed("LoRA matmul B failed: " + out.error().msg));
+    auto scaled = out.value().mul_scalar(config_.scaling());
+    if (scaled.is_err()) return Error::from(TrainingError::failed("LoRA scaling failed: " + scaled.error().msg));
+    return std::move(scaled.value());
 }
 
 std::string AsyncExecutor::debug_string() const {

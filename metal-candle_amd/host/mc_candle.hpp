@@ -12,6 +12,9 @@
 //   LoRAConfig, LoRALayer                        src/training/lora.rs:49-560
 //   Operation                                    src/graph/operation.rs:5-181
 //   AsyncExecutor::execute_operation             src/graph/executor.rs:40-226
+//   ComputationGraph, GraphNode                  src/graph/node.rs:1-300
+//   LazyTensor, LoRALayer::forward_lazy          src/graph/lazy_tensor.rs:1-460,
+//                                                src/training/lora.rs:372-439
 //   TrainingError / Error display strings        src/error.rs:10-117
 //
 // Differences from the reference, all additive:
@@ -24,7 +27,11 @@
 //   * RMSNorm and softmax accept any rank >= 1 (leading dims are folded into
 //     rows); the Metal kernels stop at rank 3 (custom_ops.rs:548-556, 741-749);
 //   * Operation::output_shape of LoRA returns [..., out_features] (the
-//     reference returns the input shape, operation.rs:139-150).
+//     reference returns the input shape, operation.rs:139-150);
+//   * LazyTensor::lora_fused merges the graphs of A and B into the input's,
+//     as the binary ops do (the reference takes their node ids as they are,
+//     lazy_tensor.rs:317-331, which is only right when A and B were added to
+//     the input's graph, as forward_lazy does).
 //
 // All device work is enqueued on the null stream and every call that returns
 // a host value synchronises through hipMemcpy. Output tensors are allocated
@@ -294,6 +301,8 @@ Result<Tensor, TrainingError> lora_forward_fused(const Tensor& input, const Tens
 Result<Tensor, TrainingError> softmax_fused(const Tensor& input);
 Result<Tensor, TrainingError> rms_norm_fused(const Tensor& input, float eps);
 
+class LazyTensor;
+
 // ------------------------------------------------------------------ LoRA layer
 // LoRAConfig (lora.rs:49-121).
 struct LoRAConfig {
@@ -314,6 +323,11 @@ public:
                                            const Device& device, uint64_t seed = 0);
     // forward (lora.rs:292-342): scaling * (input A) B, dropout in training mode.
     Result<Tensor, Error> forward(const Tensor& input);
+    // forward_lazy (lora.rs:372-439): records the forward into the input's
+    // graph. On a HIP device with dropout 0 it is one fused LoRA node (A and B
+    // added as inputs); otherwise the reference's composite (input A) B *
+    // scaling, with no dropout, whose generic ops this library does not run.
+    Result<LazyTensor, Error> forward_lazy(const LazyTensor& input) const;
     // Gradients of the most recent forward for grad_output = dL/dy (the candle
     // autograd of lora.rs:323-339): dX, dA, dB.
     Result<LoRAGrads, Error> backward(const Tensor& input, const Tensor& grad_output);
@@ -490,7 +504,11 @@ struct Operation {
 
     const char* name() const;
     Result<std::vector<int64_t>, std::string> output_shape(const std::vector<std::vector<int64_t>>& input_shapes) const;
+    // operation.rs:170-180: the first input's dtype.
+    DType output_dtype(const std::vector<DType>& input_dtypes) const;
 };
+
+std::string node_id_string(NodeId id);  // "NodeId(3)", as {:?} of a NodeId
 
 // AsyncExecutor (executor.rs:20-226). The fused ops (LoRA, Softmax, RMSNorm)
 // run on HIP tensors through libmc_hip.so; the generic ops (Matmul, Add, Mul,
@@ -505,6 +523,95 @@ public:
     std::string debug_string() const;
 
 private:
+    Device device_;
+};
+
+// ------------------------------------------------------------------ lazy graph
+// GraphNode and NodeData (node.rs:1-120): an input node holds its tensor
+// (Concrete); an operation node is Lazy until eval stores its result
+// (Available).
+struct GraphNode {
+    enum class Data { Concrete, Lazy, Available };
+    NodeId id;
+    Operation operation;
+    std::vector<NodeId> inputs;
+    std::vector<int64_t> output_shape;
+    DType output_dtype = DType::F32;
+    Data data = Data::Lazy;
+    Tensor tensor;  // the node's value when data != Lazy
+    bool is_available() const { return data != Data::Lazy; }
+};
+
+// ComputationGraph (node.rs:122-300): nodes in insertion order, a node's id
+// is its index.
+class ComputationGraph {
+public:
+    explicit ComputationGraph(const Device& device) : device_(device) {}
+    const Device& device() const { return device_; }
+    size_t len() const { return nodes_.size(); }
+    bool is_empty() const { return nodes_.empty(); }
+    Result<const GraphNode*, std::string> get_node(NodeId id) const;
+    Result<GraphNode*, std::string> get_node_mut(NodeId id);
+    NodeId add_input(const Tensor& tensor);
+    // Shape and dtype inference from the inputs; an unknown input is an error.
+    Result<NodeId, std::string> add_node(const Operation& op, const std::vector<NodeId>& inputs);
+    // Dependencies first (post-order depth-first from `output`).
+    Result<std::vector<NodeId>, std::string> topological_order(NodeId output) const;
+    // Copies `target` and everything it depends on from `other` into this
+    // graph; returns target's id here.
+    NodeId merge_from(const ComputationGraph& other, NodeId target);
+
+private:
+    std::vector<GraphNode> nodes_;
+    Device device_;
+};
+
+// LazyTensor (lazy_tensor.rs): records operations into a graph shared by the
+// tensors built from one another (copies share it, as the reference's
+// Arc<RwLock<ComputationGraph>>) and runs them through AsyncExecutor on
+// eval(). Shape and dtype are known without evaluating.
+class LazyTensor {
+public:
+    static Result<LazyTensor, CandleError> from_slice(const std::vector<float>& data, std::vector<int64_t> dims,
+                                                      const Device& device);
+    static Result<LazyTensor, CandleError> from_tensor(const Tensor& tensor);
+    static Result<LazyTensor, CandleError> zeros(std::vector<int64_t> dims, DType dtype, const Device& device);
+    static Result<LazyTensor, CandleError> ones(std::vector<int64_t> dims, DType dtype, const Device& device);
+    // A tensor as a new input node of this tensor's graph.
+    Result<LazyTensor, CandleError> add_tensor_to_graph(const Tensor& tensor) const;
+
+    const std::vector<int64_t>& shape() const { return shape_; }
+    DType dtype() const { return dtype_; }
+    const Device& device() const { return device_; }
+    NodeId node_id() const { return node_; }
+    size_t graph_size() const;
+    bool is_evaluated() const;
+    bool shares_graph_with(const LazyTensor& other) const { return graph_ == other.graph_; }
+
+    Result<LazyTensor, CandleError> matmul(const LazyTensor& other) const;
+    Result<LazyTensor, CandleError> add(const LazyTensor& other) const;
+    Result<LazyTensor, CandleError> mul(const LazyTensor& other) const;
+    Result<LazyTensor, CandleError> mul_scalar(float value) const;
+    Result<LazyTensor, CandleError> softmax(size_t dim) const;
+    Result<LazyTensor, CandleError> rms_norm(float eps) const;
+    Result<LazyTensor, CandleError> lora_fused(const LazyTensor& lora_a, const LazyTensor& lora_b, float scale) const;
+
+    // Runs every node this one depends on that has no value yet, in
+    // dependency order, then synchronises (lazy_tensor.rs:342-424).
+    Result<Tensor, TrainingError> eval() const;
+    std::string debug_string() const;
+
+    struct Shared;  // the graph and its lock
+
+private:
+    LazyTensor() = default;
+    NodeId merge_graph_from(const LazyTensor& other) const;
+    Result<LazyTensor, CandleError> add_operation(const Operation& op, const std::vector<NodeId>& inputs) const;
+
+    NodeId node_;
+    std::shared_ptr<Shared> graph_;
+    std::vector<int64_t> shape_;
+    DType dtype_ = DType::F32;
     Device device_;
 };
 

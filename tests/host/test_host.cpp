@@ -68,11 +68,15 @@ void fail_at(int line, const std::string& what) {
         const double a_ = (a), b_ = (b);                                                      \
         if (!(a_ <= b_)) fail_at(__LINE__, #a " = " + std::to_string(a_) + " > " + std::to_string(b_)); \
     } while (0)
+// The text of an error value (the graph's errors are plain strings).
+template <class E>
+std::string err_text(const E& e) { return e.to_string(); }
+inline std::string err_text(const std::string& e) { return e; }
 // Unwraps a Result or fails the case (and returns from it).
 #define TRY(var, expr)                                                              \
     auto var##_r = (expr);                                                          \
     if (var##_r.is_err()) {                                                         \
-        fail_at(__LINE__, std::string(#expr " failed: ") + var##_r.error().to_string()); \
+        fail_at(__LINE__, std::string(#expr " failed: ") + err_text(var##_r.error())); \
         return;                                                                     \
     }                                                                               \
     auto var = std::move(var##_r.value())
@@ -299,6 +303,118 @@ CASE(operation_names_and_shapes, false) {
     if (add_bad.is_err()) CHECK(add_bad.error() == "Shape mismatch: [3] vs [4]");
 }
 
+// node.rs:363-458 (tests module): graph creation, nodes, order, shape
+// inference and the errors of unknown nodes.
+CASE(graph_nodes_order_and_errors, false) {
+    ComputationGraph g(kCpu);
+    CHECK(g.len() == 0 && g.is_empty());
+    TRY(a, Tensor::zeros({2, 3}, DType::F32, kCpu));
+    TRY(b, Tensor::zeros({2, 3}, DType::F32, kCpu));
+    TRY(m, Tensor::zeros({3, 4}, DType::F32, kCpu));
+    const NodeId ia = g.add_input(a), ib = g.add_input(b), im = g.add_input(m);
+    CHECK(ia.id == 0 && ib.id == 1 && g.len() == 3);
+    TRY(ic, g.add_node(Operation::add(), {ia, ib}));
+    CHECK(ic.id == 3);
+    TRY(nc, g.get_node(ic));
+    CHECK(nc->inputs.size() == 2 && nc->inputs[0].id == ia.id && nc->inputs[1].id == ib.id);
+    CHECK(!nc->is_available());
+    TRY(na, g.get_node(ia));
+    CHECK(na->is_available() && na->data == GraphNode::Data::Concrete);
+    // a diamond: d = (a + b) * a; dependencies come first, each node once
+    TRY(id, g.add_node(Operation::mul(), {ic, ia}));
+    TRY(order, g.topological_order(id));
+    CHECK(order.size() == 4);
+    if (order.size() == 4) CHECK(order[0].id == ia.id && order[1].id == ib.id && order[2].id == ic.id && order[3].id == id.id);
+    TRY(mm, g.add_node(Operation::matmul(), {ia, im}));
+    TRY(nmm, g.get_node(mm));
+    CHECK((nmm->output_shape == std::vector<int64_t>{2, 4}));
+    CHECK(nmm->output_dtype == DType::F32);
+    auto bad = g.add_node(Operation::add(), {ia, im});
+    CHECK(bad.is_err());
+    if (bad.is_err()) CHECK(bad.error() == "Shape mismatch: [2, 3] vs [3, 4]");
+    auto unknown = g.add_node(Operation::mul_scalar(2.f), {NodeId{99}});
+    CHECK(unknown.is_err());
+    if (unknown.is_err()) CHECK(unknown.error() == "Input node NodeId(99) not found");
+    auto missing = g.get_node(NodeId{999});
+    CHECK(missing.is_err());
+    if (missing.is_err()) CHECK(missing.error() == "Node NodeId(999) not found");
+    CHECK(g.get_node_mut(NodeId{999}).is_err());
+}
+
+// node.rs:461-543: merging a node of another graph copies it and everything
+// it depends on, inputs renumbered, values kept.
+CASE(graph_merge_copies_dependencies, false) {
+    ComputationGraph g1(kCpu), g2(kCpu);
+    TRY(ta, Tensor::from_slice({1.f, 2.f}, {2}, kCpu));
+    TRY(tb, Tensor::from_slice({3.f, 4.f}, {2}, kCpu));
+    TRY(tc, Tensor::from_slice({5.f, 6.f}, {2}, kCpu));
+    g1.add_input(ta);
+    const NodeId b = g2.add_input(tb), c = g2.add_input(tc);
+    TRY(d, g2.add_node(Operation::add(), {b, c}));
+    const NodeId nd = g1.merge_from(g2, d);
+    CHECK(g1.len() == 4 && g2.len() == 3);
+    TRY(n, g1.get_node(nd));
+    CHECK(n->inputs.size() == 2);
+    if (n->inputs.size() == 2) {
+        TRY(nb, g1.get_node(n->inputs[0]));
+        CHECK(nb->is_available() && nb->tensor.data() == tb.data());  // the same storage, as Arc'd tensors
+        CHECK(n->inputs[0].id >= 1 && n->inputs[1].id >= 1);
+    }
+    // a chain b -> c -> d -> e: merging e brings all four
+    ComputationGraph g3(kCpu), g4(kCpu);
+    g3.add_input(ta);
+    const NodeId e0 = g4.add_input(tb);
+    TRY(e1, g4.add_node(Operation::mul_scalar(2.f), {e0}));
+    TRY(e2, g4.add_node(Operation::mul_scalar(3.f), {e1}));
+    TRY(e3, g4.add_node(Operation::mul_scalar(4.f), {e2}));
+    const NodeId ne = g3.merge_from(g4, e3);
+    CHECK(g3.len() == 5);
+    TRY(order, g3.topological_order(ne));
+    CHECK(order.size() == 4);
+}
+
+// lazy_tensor.rs:466-530 and lazy_execution.rs:104-170: graph sharing and
+// merging, shapes and dtypes known before evaluation.
+CASE(lazy_tensor_graphs_and_shapes, false) {
+    TRY(a, LazyTensor::from_slice({1.f, 2.f}, {2}, kCpu));
+    TRY(b, a.mul_scalar(2.f));
+    CHECK(a.shares_graph_with(b) && a.graph_size() == 2);
+    TRY(c, a.add(b));  // same graph: no merge
+    CHECK(a.graph_size() == 3);
+    TRY(x, LazyTensor::from_slice({3.f, 4.f}, {2}, kCpu));
+    CHECK(!a.shares_graph_with(x) && x.graph_size() == 1);
+    TRY(y, a.add(x));  // x's node is copied into a's graph
+    CHECK(a.graph_size() == 5 && x.graph_size() == 1 && y.shares_graph_with(a));
+    TRY(m1, LazyTensor::zeros({4, 3}, DType::F32, kCpu));
+    TRY(m2, LazyTensor::ones({3, 5}, DType::F32, kCpu));
+    TRY(p, m1.matmul(m2));
+    CHECK((p.shape() == std::vector<int64_t>{4, 5}) && p.dtype() == DType::F32);
+    auto bad = m1.add(m2);
+    CHECK(bad.is_err());
+    if (bad.is_err()) CHECK(bad.error().msg == "Shape mismatch: [4, 3] vs [3, 5]");
+    CHECK(m1.is_evaluated() && !p.is_evaluated());
+    TRY(s, p.softmax(1));
+    TRY(r, s.rms_norm(1e-5f));
+    CHECK((r.shape() == std::vector<int64_t>{4, 5}));
+    CHECK_CONTAINS(r.debug_string(), "LazyTensor { node_id: NodeId(");
+    CHECK_CONTAINS(r.debug_string(), "shape: [4, 5]");
+    (void)c;
+}
+
+// lora_lazy.rs:10-160 run on the CPU device: forward_lazy records the
+// reference's composite (input A) B * scaling, whose generic ops only candle
+// runs, so eval gives the executor's error and the caller's fallback applies.
+CASE(lora_forward_lazy_on_cpu_records_the_composite, false) {
+    TRY(layer, LoRALayer::create(32, 48, LoRAConfig{4, 8.f, 0.f}, kCpu));
+    TRY(x, LazyTensor::zeros({4, 32}, DType::F32, kCpu));
+    TRY(y, layer.forward_lazy(x));
+    CHECK(y.graph_size() == 6);  // x, A, B, x A, (x A) B, * scaling
+    CHECK((y.shape() == std::vector<int64_t>{4, 48}));
+    auto v = y.eval();
+    CHECK(v.is_err());
+    if (v.is_err()) CHECK_CONTAINS(v.error().to_string(), "Matmul is a generic candle op");
+}
+
 // The keep-mask generator of the C ABI equals the oracle's, byte for byte.
 CASE(dropout_mask_matches_oracle, false) {
     const int64_t T = 1000;
@@ -327,6 +443,114 @@ CASE(executor_lora_known_answer, true) {
     const std::vector<float> want = {17.5f, 23.f, 28.5f, 34.f, 40.7f, 53.4f, 66.1f, 78.8f};
     CHECK_LE(rel_err(v, want), kTolF32);
     CHECK(ex.synchronize().is_ok());
+}
+
+// rmsnorm_lazy.rs:9-205, softmax_lazy.rs:12-250: the fused ops through the
+// graph give the eager calls' results (the same kernels, bit for bit) and the
+// oracle's; a node is evaluated once.
+CASE(lazy_fused_ops_match_eager_and_oracle, true) {
+    const int64_t rows = 4, D = 64;
+    const std::vector<float> xv = randn(rows * D, 0.f, 1.f, 21);
+    TRY(x, Tensor::from_slice(xv, {rows, D}, kHip));
+    TRY(lx, LazyTensor::from_tensor(x));
+    TRY(ln, lx.rms_norm(1e-5f));
+    TRY(ls, ln.softmax(1));
+    CHECK(!ls.is_evaluated() && ls.graph_size() == 3);
+    TRY(got, ls.eval());
+    CHECK(ls.is_evaluated() && ln.is_evaluated());
+    TRY(e1, rms_norm_fused(x, 1e-5f));
+    TRY(e2, softmax_fused(e1));
+    TRY(vg, got.to_vec_f32());
+    TRY(ve, e2.to_vec_f32());
+    CHECK(vg == ve);
+    std::vector<float> n((size_t)(rows * D)), p((size_t)(rows * D));
+    oracle_rmsnorm_fwd(rows, D, 1e-5f, xv.data(), nullptr, n.data(), nullptr, 0);
+    oracle_softmax_fwd(rows, D, 0, n.data(), p.data(), 0);
+    CHECK_LE(rel_err(vg, p), kTolF32);
+    TRY(again, ls.eval());  // nothing left to run: the stored value
+    CHECK(again.data() == got.data());
+    auto wrong_dim = lx.softmax(0);
+    CHECK(wrong_dim.is_ok());
+    if (wrong_dim.is_ok()) {
+        auto r = wrong_dim.value().eval();
+        CHECK(r.is_err());
+        if (r.is_err()) CHECK_CONTAINS(r.error().to_string(), "only the last dimension has a fused kernel");
+    }
+}
+
+// lora_lazy.rs:10-160 on the HIP device: forward_lazy is one fused LoRA node
+// and its value equals forward's (the same op) and the oracle's; ranks 2-16,
+// batched shapes, and a chain of two layers. B is set to random values (the
+// reference's tests run with its zero initialisation).
+CASE(lora_forward_lazy_matches_forward, true) {
+    uint64_t seed = 100;
+    for (size_t rank : {2, 4, 8, 16}) {
+        TRY(layer, LoRALayer::create(64, 64, LoRAConfig{rank, 2.f * rank, 0.f}, kHip, seed));
+        const std::vector<float> bv = randn(rank * 64, 0.f, 0.02f, seed + 1);
+        TRY(bt, Tensor::from_slice(bv, {(int64_t)rank, 64}, kHip));
+        CHECK(layer.set_lora_b(bt).is_ok());
+        layer.eval();
+        const std::vector<float> xv = randn(8 * 64, 0.f, 1.f, seed + 2);
+        TRY(x, Tensor::from_slice(xv, {8, 64}, kHip));
+        TRY(lx, LazyTensor::from_tensor(x));
+        TRY(ly, layer.forward_lazy(lx));
+        CHECK(ly.graph_size() == 4);  // x, A, B, lora
+        TRY(y, ly.eval());
+        TRY(ye, layer.forward(x));
+        TRY(vy, y.to_vec_f32());
+        TRY(ve, ye.to_vec_f32());
+        CHECK(vy == ve);
+        TRY(av, layer.lora_a_tensor().to_vec_f32());
+        std::vector<float> ref(8 * 64);
+        oracle_lora_fwd(8, 64, 64, (int32_t)rank, layer.config().scaling(), 0.f, xv.data(), nullptr, nullptr,
+                        av.data(), bv.data(), nullptr, ref.data(), nullptr, 0);
+        CHECK_LE(rel_err(vy, ref), kTolF32);
+        seed += 10;
+    }
+    // shapes [batch, seq, 128] are kept (lora_lazy.rs:145-165)
+    TRY(wide, LoRALayer::create(128, 128, LoRAConfig{}, kHip, 7));
+    for (auto bs : {std::pair<int64_t, int64_t>{1, 10}, {4, 20}, {8, 5}}) {
+        TRY(x, Tensor::from_slice(randn(bs.first * bs.second * 128, 0.f, 1.f, 9), {bs.first, bs.second, 128}, kHip));
+        TRY(lx, LazyTensor::from_tensor(x));
+        TRY(ly, wide.forward_lazy(lx));
+        CHECK((ly.shape() == std::vector<int64_t>{bs.first, bs.second, 128}));
+        TRY(y, ly.eval());
+        CHECK((y.dims() == std::vector<int64_t>{bs.first, bs.second, 128}));
+    }
+    // two layers chained in one graph (lora_lazy.rs:81-112)
+    TRY(l1, LoRALayer::create(32, 32, LoRAConfig{4, 8.f, 0.f}, kHip, 31));
+    TRY(l2, LoRALayer::create(32, 32, LoRAConfig{4, 8.f, 0.f}, kHip, 32));
+    for (LoRALayer* l : {&l1, &l2}) {
+        TRY(bt, Tensor::from_slice(randn(4 * 32, 0.f, 0.05f, 33), {4, 32}, kHip));
+        CHECK(l->set_lora_b(bt).is_ok());
+        l->eval();
+    }
+    TRY(x, Tensor::from_slice(randn(4 * 32, 0.f, 1.f, 34), {4, 32}, kHip));
+    TRY(lx, LazyTensor::from_tensor(x));
+    TRY(o1, l1.forward_lazy(lx));
+    TRY(o2, l2.forward_lazy(o1));
+    CHECK(o2.graph_size() == 7);
+    TRY(lazy, o2.eval());
+    TRY(e1, l1.forward(x));
+    TRY(e2, l2.forward(e1));
+    TRY(vl, lazy.to_vec_f32());
+    TRY(v2, e2.to_vec_f32());
+    CHECK(vl == v2);
+}
+
+// A and B from graphs of their own: lora_fused merges them into the input's
+// graph, so the node's inputs are A and B (executor_direct.rs:339-373's
+// known answer).
+CASE(lazy_lora_merges_separate_graphs, true) {
+    TRY(lx, LazyTensor::from_slice({1, 2, 3, 4, 5, 6, 7, 8}, {2, 4}, kHip));
+    TRY(la, LazyTensor::from_slice({.1f, .2f, .3f, .4f, .5f, .6f, .7f, .8f}, {4, 2}, kHip));
+    TRY(lb, LazyTensor::from_slice({1, 2, 3, 4, 5, 6, 7, 8}, {2, 4}, kHip));
+    TRY(ly, lx.lora_fused(la, lb, 0.5f));
+    CHECK(ly.graph_size() == 4 && la.graph_size() == 1);
+    TRY(y, ly.eval());
+    TRY(v, y.to_vec_f32());
+    const std::vector<float> want = {17.5f, 23.f, 28.5f, 34.f, 40.7f, 53.4f, 66.1f, 78.8f};
+    CHECK_LE(rel_err(v, want), kTolF32);
 }
 
 // executor_direct.rs:456-495: RMSNorm through the executor; [3, 4] at eps 0
