@@ -537,7 +537,11 @@ __device__ __forceinline__ void f32_load4(const float* base, int64_t rows, int64
     }
 }
 
-template <bool NN0, bool NN1>
+// BUF: every operand's tile rows (and an NN operand's k rows) fit 32-bit
+// byte offsets, so the loads go through buffer resources whose range checks
+// zero the rows past M / N, and no load branches; otherwise per-element
+// checked loads (f32_load4).
+template <bool NN0, bool NN1, bool BUF>
 __global__ __launch_bounds__(256) void gemm_f32_mfma(int64_t M, int64_t N, F32Seg s0, F32Seg s1,
                                                      const float* __restrict__ bias, float* __restrict__ C,
                                                      int64_t ldc, int tiles_n) {
@@ -564,11 +568,32 @@ __global__ __launch_bounds__(256) void gemm_f32_mfma(int64_t M, int64_t N, F32Se
         const int64_t klim = min<int64_t>(s.k, (int64_t)c_end * 8);  // this wave's k range ends here
         const bool va = ((s.lda & 3) == 0) && ((reinterpret_cast<uintptr_t>(s.a) & 15) == 0);
         const bool vb = !NN && ((s.ldb & 3) == 0) && ((reinterpret_cast<uintptr_t>(s.b) & 15) == 0);
-        // rows [base0, base0 + 32) of a row-major [rows][ld] operand, k from k0: zeros past rows and klim
-        auto load_rows = [&](const float* base, int64_t rows, int64_t ld, int64_t row0, int64_t k0, bool vec,
-                             float (&v)[4][4]) {
+        // Buffer resources (BUF) over the tile's rows of each operand, ending
+        // at the last row's k-th element (nothing past the operand is read);
+        // an NN operand's over its k rows from column n0.
+        auto tile_bytes = [&](int64_t rows_left, int64_t ld) {
+            const int64_t rows = rows_left < 32 ? rows_left : 32;
+            return rows <= 0 ? (int64_t)0 : ((rows - 1) * ld + s.k) * 4;
+        };
+        const __amdgpu_buffer_rsrc_t rsa = make_rsrc(s.a + m0 * s.lda, BUF ? tile_bytes(M - m0, s.lda) : 0);
+        const __amdgpu_buffer_rsrc_t rsb =
+            make_rsrc(NN ? s.b + n0 : s.b + n0 * s.ldb,
+                      !BUF ? 0 : NN ? (s.k - 1) * s.ldb * 4 + (N - n0) * 4 : tile_bytes(N - n0, s.ldb));
+        // rows [row0, row0 + 32) of a row-major [rows][ld] operand (its
+        // resource r when BUF), k from k0: zeros past rows and klim
+        auto load_rows = [&](__amdgpu_buffer_rsrc_t r, const float* base, int64_t rows, int64_t ld, int64_t row0,
+                             int64_t k0, bool vec, float (&v)[4][4]) {
+            if constexpr (BUF) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) f32_load4(base, rows, ld, row0 + 8 * i + lr, k0 + lk, klim, vec, v[i]);
+                for (int i = 0; i < 4; ++i) {
+                    const f32x4 q = __builtin_bit_cast(f32x4, buf_load16(r, (uint32_t)(((8 * i + lr) * ld + k0 + lk) * 4)));
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) v[i][e] = k0 + lk + e < klim ? q[e] : 0.f;
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) f32_load4(base, rows, ld, row0 + 8 * i + lr, k0 + lk, klim, vec, v[i]);
+            }
         };
         auto store_rows = [&](float (*st)[36], const float (&v)[4][4]) {
 #pragma unroll
@@ -587,13 +612,27 @@ __global__ __launch_bounds__(256) void gemm_f32_mfma(int64_t M, int64_t N, F32Se
                     v[u][p] = (n < N && k < klim) ? s.b[k * s.ldb + n] : 0.f;
                 }
         };
+        // BUF and NN: the group's 32 k rows x 32 columns of B, whole 128-byte
+        // row segments per 8 lanes like the row-major operands, staged as
+        // [k][n] and read back one k row (32 consecutive columns) at a time
+        auto load_nn_rows = [&](int64_t k0, float (&v)[4][4]) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int64_t k = k0 + 8 * i + lr;
+                const f32x4 q = __builtin_bit_cast(f32x4, buf_load16(rsb, (uint32_t)((k * s.ldb + lk) * 4)));
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[i][e] = (k < klim && n0 + lk + e < N) ? q[e] : 0.f;
+            }
+        };
+        constexpr bool NN_LDS = NN && BUF;
         float ra[4][4], rb[4][4], nb[4][4];
-        load_rows(s.a, M, s.lda, m0, (int64_t)c_begin * 8, va, ra);
-        if constexpr (!NN) load_rows(s.b, N, s.ldb, n0, (int64_t)c_begin * 8, vb, rb);
+        load_rows(rsa, s.a, M, s.lda, m0, (int64_t)c_begin * 8, va, ra);
+        if constexpr (!NN) load_rows(rsb, s.b, N, s.ldb, n0, (int64_t)c_begin * 8, vb, rb);
+        else if constexpr (NN_LDS) load_nn_rows((int64_t)c_begin * 8, rb);
         else load_nn(c_begin, rb);
         for (int c = c_begin; c < c_end; c += 4) {
             store_rows(sa, ra);
-            if constexpr (!NN) store_rows(sb, rb);
+            if constexpr (!NN || NN_LDS) store_rows(sb, rb);
             else {
 #pragma unroll
                 for (int u = 0; u < 4; ++u)
@@ -601,8 +640,9 @@ __global__ __launch_bounds__(256) void gemm_f32_mfma(int64_t M, int64_t N, F32Se
                     for (int p = 0; p < 4; ++p) nb[u][p] = rb[u][p];
             }
             if (c + 4 < c_end) {  // the next group's loads run under this group's MFMAs
-                load_rows(s.a, M, s.lda, m0, (int64_t)(c + 4) * 8, va, ra);
-                if constexpr (!NN) load_rows(s.b, N, s.ldb, n0, (int64_t)(c + 4) * 8, vb, rb);
+                load_rows(rsa, s.a, M, s.lda, m0, (int64_t)(c + 4) * 8, va, ra);
+                if constexpr (!NN) load_rows(rsb, s.b, N, s.ldb, n0, (int64_t)(c + 4) * 8, vb, rb);
+                else if constexpr (NN_LDS) load_nn_rows((int64_t)(c + 4) * 8, rb);
                 else load_nn(c + 4, rb);
             }
             // a wave's LDS operations complete in order: the reads below
@@ -616,6 +656,9 @@ __global__ __launch_bounds__(256) void gemm_f32_mfma(int64_t M, int64_t N, F32Se
                 if constexpr (!NN) {
                     const float4 b4 = *reinterpret_cast<const float4*>(&sb[rc][kk]);
                     bq[0] = b4.x; bq[1] = b4.y; bq[2] = b4.z; bq[3] = b4.w;
+                } else if constexpr (NN_LDS) {
+#pragma unroll
+                    for (int p = 0; p < 4; ++p) bq[p] = sb[kk + p][rc];
                 } else {
 #pragma unroll
                     for (int p = 0; p < 4; ++p) bq[p] = nb[u][p];
@@ -909,10 +952,22 @@ hipError_t launch_gemm_f32(bool nn, bool nn1, int64_t M, int64_t N, GemmSegF32 s
     const dim3 grid((unsigned)(tiles_m * tiles_n));
     const F32Seg a = seg(s0), b = seg(s1);
     const int tn = (int)tiles_n;
-    if (nn && nn1) gemm_f32_mfma<true, true><<<grid, 256, 0, stream>>>(M, N, a, b, bias, c, ldc, tn);
-    else if (nn) gemm_f32_mfma<true, false><<<grid, 256, 0, stream>>>(M, N, a, b, bias, c, ldc, tn);
-    else if (nn1) gemm_f32_mfma<false, true><<<grid, 256, 0, stream>>>(M, N, a, b, bias, c, ldc, tn);
-    else gemm_f32_mfma<false, false><<<grid, 256, 0, stream>>>(M, N, a, b, bias, c, ldc, tn);
+    // 32-bit buffer offsets: 32 rows of each row-major operand, every k row
+    // of an NN operand
+    constexpr int64_t kLim = ((int64_t)1 << 31) - 64;
+    auto fits = [&](const GemmSegF32& g, bool g_nn) {
+        return 32 * g.lda * 4 < kLim && (g_nn ? (g.k + 1) * g.ldb * 4 < kLim : 32 * g.ldb * 4 < kLim);
+    };
+    const bool buf = fits(s0, nn) && fits(s1, nn1);
+    auto go = [&](auto nn_tag, auto nn1_tag) {
+        constexpr bool A = decltype(nn_tag)::value, B = decltype(nn1_tag)::value;
+        if (buf) gemm_f32_mfma<A, B, true><<<grid, 256, 0, stream>>>(M, N, a, b, bias, c, ldc, tn);
+        else gemm_f32_mfma<A, B, false><<<grid, 256, 0, stream>>>(M, N, a, b, bias, c, ldc, tn);
+    };
+    if (nn && nn1) go(std::true_type{}, std::true_type{});
+    else if (nn) go(std::true_type{}, std::false_type{});
+    else if (nn1) go(std::false_type{}, std::true_type{});
+    else go(std::false_type{}, std::false_type{});
     return hipGetLastError();
 }
 
