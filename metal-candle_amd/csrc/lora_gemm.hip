@@ -565,7 +565,8 @@ __global__ __launch_bounds__(256) void gemm_f32_mfma(int64_t M, int64_t N, F32Se
         const int q = (s.nch + 3) / 4;
         const int c_begin = wave * q, c_end = min(s.nch, c_begin + q);
         if (c_begin >= c_end) return;  // wave-uniform
-        const int64_t klim = min<int64_t>(s.k, (int64_t)c_end * 8);  // this wave's k range ends here
+        const int64_t kend = (int64_t)c_end * 8;
+        const int64_t klim = s.k < kend ? s.k : kend;  // this wave's k range ends here
         const bool va = ((s.lda & 3) == 0) && ((reinterpret_cast<uintptr_t>(s.a) & 15) == 0);
         const bool vb = !NN && ((s.ldb & 3) == 0) && ((reinterpret_cast<uintptr_t>(s.b) & 15) == 0);
         // Buffer resources (BUF) over the tile's rows of each operand, ending

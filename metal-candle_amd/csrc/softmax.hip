@@ -29,8 +29,9 @@ namespace {
 
 constexpr int kRowsPerBlock = 4;
 // The backward vector kernel runs one row (one wave) per workgroup: on the
-// 8192 x 8192 fp32 rows it measured 179 -> 168 us against four rows per
-// workgroup, while the forward is faster at four (108 us against 115 at one).
+// causal fp32 scores [8, 14, 1024, 1024] it measured 179 -> 168 us against
+// four rows per workgroup, while the forward is faster at four (108 us
+// against 115 at one).
 constexpr int kBwdRowsPerBlock = 1;
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -462,8 +463,9 @@ WideShape wide_shape(int64_t dim) {
     return {vpl, (int)((per + kWave - 1) / kWave * kWave)};
 }
 
-// One workgroup per row: launches of at most 2^32 / threads - 1 workgroups
-// (a launch's thread count is 32-bit), each given its first row.
+// Launches over the rows, rows_per_block rows per workgroup of `threads`
+// threads, each launch at most 2^32 - 1 threads (a launch's thread count is
+// 32-bit) and given its first row.
 template <typename F>
 void for_row_chunks(int64_t rows, int threads, F&& launch, int rows_per_block = 1) {
     const int64_t cap = (((int64_t)1 << 32) - 1) / threads * rows_per_block;

@@ -1197,7 +1197,8 @@ Result<std::vector<NodeId>, std::string> ComputationGraph::topological_order(Nod
 
 NodeId ComputationGraph::merge_from(const ComputationGraph& other, NodeId target) {
     // node.rs:275-300: dependencies first, each node copied once (with its
-    // value, if it has one) and its inputs renumbered
+    // value, if it has one) and its inputs renumbered. `target` must be a
+    // node of `other` (the reference panics otherwise; here std::out_of_range).
     std::unordered_map<size_t, NodeId> copied;
     std::function<NodeId(NodeId)> copy = [&](NodeId id) -> NodeId {
         auto it = copied.find(id.id);
@@ -1243,8 +1244,10 @@ Result<LazyTensor, CandleError> LazyTensor::zeros(std::vector<int64_t> dims, DTy
 
 Result<LazyTensor, CandleError> LazyTensor::ones(std::vector<int64_t> dims, DType dtype, const Device& device) {
     int64_t n = 1;
-    for (int64_t d : dims) n *= d;
-    if (n < 0) return CandleError{"ones: negative dimension in " + dims_to_string(dims)};
+    for (int64_t d : dims) {
+        if (d < 0) return CandleError{"ones: negative dimension in " + dims_to_string(dims)};
+        n *= d;
+    }
     auto t = Tensor::from_slice(std::vector<float>((size_t)n, 1.f), std::move(dims), device, dtype);
     if (t.is_err()) return t.error();
     return from_tensor(t.value());
