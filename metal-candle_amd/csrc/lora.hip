@@ -298,8 +298,8 @@ LoraGroupFwdWs lora_group_fwd_ws(const mc_lora_desc& d, const int64_t* N, int co
     const int ppp = proj_per_pass(m.r);
     for (int p0 = 0, pass = 0; p0 < count; p0 += ppp, ++pass) {
         const int np = count - p0 < ppp ? count - p0 : ppp;
-        w.at_hilo[pass] = off;
-        off += align256((size_t)2 * 16 * rowproj_rc(np * m.r) * m.K * 2);
+        w.at_hilo[pass] = off;  // hi then lo, row-major [16 rc][K] or in fragment order over round_up(K, 64)
+        off += align256((size_t)2 * 16 * rowproj_rc(np * m.r) * round_up(m.K, 64) * 2);
     }
     for (int g = 0; g < count; ++g) {
         w.bt_ext[g] = off;
@@ -526,17 +526,23 @@ hipError_t launch_lora_group_fwd(const mc_lora_desc& d, const void* x, const Lor
             for (int j0 = 0; j0 < m.r; j0 += kRowprojMaxRanks) {
                 const int rc = np > 1 || m.r <= kRowprojMaxRanks ? m.r : std::min(kRowprojMaxRanks, m.r - j0);
                 const bool last = j0 + rc == m.r;
-                const int rpass = np * rc, r16 = 16 * rowproj_rc(rpass);
+                const int rpass = np * rc, RC = rowproj_rc(rpass), r16 = 16 * RC;
                 uint16_t* at_hi = reinterpret_cast<uint16_t*>(base + w.at_hilo[pass]);
-                uint16_t* at_lo = at_hi + (size_t)r16 * m.K;
+                uint16_t* at_lo = at_hi + (size_t)r16 * round_up(m.K, 64);
                 PrepJob jobs[2 * kMaxProj + 1];
                 int nj = 0;
-                for (int i = 0; i < np; ++i)  // A_g^T hi / lo (ranks j0 ..) as rows [i rc, (i + 1) rc) of the operand
-                    jobs[nj++] = prep_job(proj[p0 + i].A + j0, m.r, rc, m.K, true, at_hi + (size_t)i * rc * m.K,
-                                          at_lo + (size_t)i * rc * m.K, rc, m.K);
-                if (r16 > rpass)  // zero rows past the pass's ranks
-                    jobs[nj++] = prep_job(proj[p0].A, 0, 0, 0, false, at_hi + (size_t)rpass * m.K,
-                                          at_lo + (size_t)rpass * m.K, r16 - rpass, m.K);
+                // the operand in the row projection's fragment order: A_g^T hi / lo
+                // (ranks j0 ..) as rows [i rc, (i + 1) rc), zero rows past the pass's ranks
+                for (int i = 0; i < np; ++i) {
+                    jobs[nj] = prep_job(proj[p0 + i].A + j0, m.r, rc, m.K, true, at_hi, at_lo, rc, m.K);
+                    jobs[nj].frag_rc = RC;
+                    jobs[nj++].frag_row0 = (int64_t)i * rc;
+                }
+                if (r16 > rpass) {
+                    jobs[nj] = prep_job(proj[p0].A, 0, 0, 0, false, at_hi, at_lo, r16 - rpass, m.K);
+                    jobs[nj].frag_rc = RC;
+                    jobs[nj++].frag_row0 = rpass;
+                }
                 if (pass == 0 && j0 == 0)
                     for (int g = 0; g < count; ++g)  // B_g^T, zero-padded to rext columns
                         jobs[nj++] = prep_job(proj[g].B, Ns[g], Ns[g], m.r, true,

@@ -30,6 +30,9 @@ inline int colreduce_rows(int r) { return r <= 16 ? 16 : r <= 32 ? 32 : r <= 48 
 // j < valid_cols, else 0. With lo != nullptr the fp32 value v is split as
 // hi = bf16(v), lo = bf16(v - hi). A job with hi == nullptr is skipped.
 // ld_out is the row stride of hi / lo (0: cols_out).
+// frag_rc > 0 writes the row projection's parameter operand in fragment
+// order instead (rowproj_frag_index: rows i of the job are rows
+// frag_row0 + i of a 16 frag_rc-row operand; ld_out is unused).
 struct PrepJob {
     const float* src;
     int64_t ld_src, valid_rows, valid_cols;
@@ -38,7 +41,21 @@ struct PrepJob {
     uint16_t* lo;
     int64_t rows_out, cols_out;
     int64_t ld_out;
+    int frag_rc;
+    int64_t frag_row0;
 };
+
+// Fragment order of the row projection's bf16 parameter operand P
+// [16 RC][C]: element (j, c) at
+//   ((((c / 64) RC + j / 16) 2 + (c / 8) % 2) 64 + 16 ((c % 64) / 16) + j % 16) 8 + c % 8,
+// i.e. per 64-column step, 16-rank tile and 8-column half, the 16 bytes each
+// of the 64 lanes loads, lane after lane (1 KB per load instruction). The
+// operand spans round_up(C, 64) columns.
+__host__ __device__ inline int64_t rowproj_frag_index(int RC, int64_t j, int64_t c) {
+    const int64_t lane = 16 * ((c & 63) >> 4) + (j & 15);
+    return (((((c >> 6) * RC + (j >> 4)) * 2 + ((c >> 3) & 1)) * 64 + lane) << 3) + (c & 7);
+}
+
 // Up to kPrepJobs jobs in one launch.
 hipError_t launch_prep_bf16(const PrepJob* jobs, int n, hipStream_t stream);
 hipError_t launch_prep_bf16(const PrepJob& j0, const PrepJob& j1, hipStream_t stream);
@@ -48,13 +65,8 @@ hipError_t launch_prep_bf16(const PrepJob& j0, const PrepJob& j1, hipStream_t st
 //                    v = mask ? (mask[t*r+j] ? v*keep : 0) : v
 //   out_t[j*T + t] = v                       (fp32, may be null)
 //   out_ext[t*rext + j] = bf16(ext_scale*v)  (j < r; zero for r <= j < rext; may be null)
-// X bf16 [T][C] (C % 8 == 0), P_hi / P_lo bf16 [16 rowproj_rc(r)][C], rows
-// past r zero.
-hipError_t launch_rowproj_bf16(const uint16_t* X, int64_t T, int64_t C, const uint16_t* P_hi,
-                               const uint16_t* P_lo, int r, float scale, const uint8_t* mask,
-                               float keep, float* out_t, uint16_t* out_ext, int rext, float ext_scale,
-                               hipStream_t stream);
-
+// X bf16 [T][C] (C % 8 == 0), P_hi / P_lo bf16 [16 rowproj_rc(r)][C] in
+// fragment order (rowproj_frag_index), rows past r zero.
 // A pass over one X whose r ranks may be those of several projections
 // (rp ranks each): rank j belongs to projection p = j / rp and uses its mask
 // [T][rp] and out_t [rp][T] (entries may be null), and goes to column

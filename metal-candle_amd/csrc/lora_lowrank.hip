@@ -80,7 +80,7 @@ __device__ __forceinline__ void prep_one(const PrepJob& j, int64_t idx) {
     float v = 0.f;
     if (i < j.valid_rows && c < j.valid_cols) v = j.transpose ? j.src[c * j.ld_src + i] : j.src[i * j.ld_src + c];
     const uint16_t h = f32_to_bf16(v);
-    const int64_t o = i * j.ld_out + c;
+    const int64_t o = j.frag_rc ? rowproj_frag_index(j.frag_rc, j.frag_row0 + i, c) : i * j.ld_out + c;
     j.hi[o] = h;
     if (j.lo) j.lo[o] = f32_to_bf16(v - bf16_to_f32(h));
 }
@@ -103,15 +103,16 @@ __device__ __forceinline__ void prep_one8(const PrepJob& j, int64_t g) {
     }
     uint4 hi, lo;
     split_hilo8(v, hi, lo);
-    const int64_t o = i * j.ld_out + c0;
+    const int64_t o = j.frag_rc ? rowproj_frag_index(j.frag_rc, j.frag_row0 + i, c0) : i * j.ld_out + c0;
     *reinterpret_cast<uint4*>(j.hi + o) = hi;
     if (j.lo) *reinterpret_cast<uint4*>(j.lo + o) = lo;
 }
 
 bool prep_vec8(const PrepJob& j) {
-    // prep_one8 reads src[0] for the zero elements: src must exist
-    return j.src && j.cols_out % 8 == 0 && j.ld_out % 8 == 0 && reinterpret_cast<uintptr_t>(j.hi) % 16 == 0 &&
-           reinterpret_cast<uintptr_t>(j.lo) % 16 == 0;
+    // prep_one8 reads src[0] for the zero elements: src must exist; in
+    // fragment order eight columns from a multiple of 8 are 16 contiguous bytes
+    return j.src && j.cols_out % 8 == 0 && (j.frag_rc || j.ld_out % 8 == 0) &&
+           reinterpret_cast<uintptr_t>(j.hi) % 16 == 0 && reinterpret_cast<uintptr_t>(j.lo) % 16 == 0;
 }
 
 struct PrepBatch {
@@ -133,8 +134,8 @@ __global__ __launch_bounds__(256) void prep_bf16(PrepBatch b) {
 }
 
 // --------------------------------------------------------------- rowproj
-// Workgroup: 4 waves, 16 RT token rows (RT MFMA row tiles). Wave w takes the
-// 64-column steps w, w+4, ...; in a step, lane l (row l % 16 of each row
+// Workgroup: NW waves, 16 RT token rows (RT MFMA row tiles). Wave w takes the
+// 64-column steps w, w+NW, ...; in a step, lane l (row l % 16 of each row
 // tile, group g = l / 16) loads the 16 contiguous columns 64 s + 16 g .. +15
 // of x and of the parameter rows (32 bytes per lane, whole 128-byte lines per
 // wave) and feeds them to two MFMA 16x16x32 as k-chunks (columns 0-7, then
@@ -142,11 +143,15 @@ __global__ __launch_bounds__(256) void prep_bf16(PrepBatch b) {
 // and P, so the sum over columns is unchanged. The parameter fragments are
 // shared by the RT row tiles. All loads of U steps are issued before their
 // MFMAs, through buffer loads whose range check zeroes rows past T and
-// columns past C (no branches). The 4 waves' partial sums are combined in
+// columns past C (no branches). The NW waves' partial sums are combined in
 // wave order through LDS.
 // Arguments of one row projection. With PF32 the parameter is read as fp32
 // P [prows][C] (rows past prows load as zeros) and split into bf16 hi + lo in
-// registers; otherwise it comes prepared as bf16 P_hi / P_lo [16 RC][C].
+// registers; otherwise it comes prepared as bf16 P_hi / P_lo [16 RC][C] in
+// fragment order (rowproj_frag_index), so that each of its loads reads 1 KB
+// of contiguous lines: read as [16 RC][C] rows, every load touched 16 rows
+// of 64 bytes, and at c4 the parameter loads took 3.8-7.8 us of the 17-24 us
+// row projections (a copy without them ran that much faster).
 // The r ranks of a pass may belong to several projections of the same x
 // (rp ranks each, projection p = j / rp): rank j then takes projection p's
 // mask row and goes to its out_t rows and to columns p rext_p .. of the
@@ -172,7 +177,7 @@ struct RowprojArgs {
     float ext_scale;
 };
 
-template <int RC, int RT, int U, bool PF32>
+template <int RC, int RT, int U, bool PF32, int NW>
 __device__ __forceinline__ void rowproj_body(const RowprojArgs& A, int64_t blk) {
     const uint16_t* __restrict__ X = A.X;
     const int64_t T = A.T, C = A.C;
@@ -185,9 +190,10 @@ __device__ __forceinline__ void rowproj_body(const RowprojArgs& A, int64_t blk) 
     const int64_t t0 = blk * ROWS;
     const int64_t nrows = T - t0 < ROWS ? T - t0 : ROWS;
     const __amdgpu_buffer_rsrc_t rx = make_rsrc(X + t0 * C, nrows * C * 2);
+    const int64_t pbytes = (int64_t)16 * RC * ((C + 63) / 64 * 64) * 2;  // fragment-order operand
     const __amdgpu_buffer_rsrc_t rhi = make_rsrc(PF32 ? (const void*)A.Pf : (const void*)A.Phi,
-                                                 PF32 ? (int64_t)A.prows * C * 4 : (int64_t)16 * RC * C * 2);
-    const __amdgpu_buffer_rsrc_t rlo = make_rsrc(A.Plo, PF32 ? 0 : (int64_t)16 * RC * C * 2);
+                                                 PF32 ? (int64_t)A.prows * C * 4 : pbytes);
+    const __amdgpu_buffer_rsrc_t rlo = make_rsrc(A.Plo, PF32 ? 0 : pbytes);
     const int row = lane & 15, grp = lane >> 4;
     const int64_t nsteps = (C + 63) / 64;
 
@@ -197,11 +203,12 @@ __device__ __forceinline__ void rowproj_body(const RowprojArgs& A, int64_t blk) 
 #pragma unroll
         for (int rc = 0; rc < RC; ++rc) acc[rt][rc] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    for (int64_t s0 = wave; s0 < nsteps; s0 += 4 * U) {
+    for (int64_t s0 = wave; s0 < nsteps; s0 += NW * U) {
         i32x4 xv[U][RT][2], ph[U][RC][2], pl[U][RC][2];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int64_t c = (s0 + 4 * u) * 64 + grp * 16;  // steps past the end load zeros
+            const int64_t st = s0 + NW * u;
+            const int64_t c = st * 64 + grp * 16;  // steps past the end load zeros
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
                 const bool ok = c + 8 * h < C;
@@ -226,7 +233,7 @@ __device__ __forceinline__ void rowproj_body(const RowprojArgs& A, int64_t blk) 
                         ph[u][rc][h] = __builtin_bit_cast(i32x4, hi);
                         pl[u][rc][h] = __builtin_bit_cast(i32x4, pack_bf16x8(rem));
                     } else {
-                        const uint32_t off = ok ? (uint32_t)(((int64_t)(rc * 16 + row) * C + c + 8 * h) * 2) : kOOB;
+                        const uint32_t off = ok ? (uint32_t)((((st * RC + rc) * 2 + h) * 64 + lane) * 16) : kOOB;
                         ph[u][rc][h] = buf_load16(rhi, off);
                         pl[u][rc][h] = buf_load16(rlo, off);
                     }
@@ -254,9 +261,9 @@ __device__ __forceinline__ void rowproj_body(const RowprojArgs& A, int64_t blk) 
         __builtin_amdgcn_sched_group_barrier(kSchedMfma, U * 4 * RT * RC, 0);
     }
 
-    // combine the 4 waves: [wave][rt][rc][q][lane]; accumulator q of lane l
+    // combine the NW waves: [wave][rt][rc][q][lane]; accumulator q of lane l
     // is token 4 (l / 16) + q of its row tile, rank index l % 16.
-    __shared__ float red[4][RT][RC][4][64];
+    __shared__ float red[NW][RT][RC][4][64];
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
@@ -264,11 +271,11 @@ __device__ __forceinline__ void rowproj_body(const RowprojArgs& A, int64_t blk) 
 #pragma unroll
             for (int q = 0; q < 4; ++q) red[wave][rt][rc][q][lane] = acc[rt][rc][q];
     __syncthreads();
-    for (int idx = threadIdx.x; idx < RT * RC * 4 * 64; idx += 256) {
+    for (int idx = threadIdx.x; idx < RT * RC * 4 * 64; idx += 64 * NW) {
         const int l = idx & 63, q = (idx >> 6) & 3, rc = (idx >> 8) % RC, rt = (idx >> 8) / RC;
         float v = red[0][rt][rc][q][l];
 #pragma unroll
-        for (int w = 1; w < 4; ++w) v += red[w][rt][rc][q][l];
+        for (int w = 1; w < NW; ++w) v += red[w][rt][rc][q][l];
         const int j = rc * 16 + (l & 15);
         const int64_t t = t0 + rt * 16 + (l >> 4) * 4 + q;
         if (t >= T || j >= r) continue;
@@ -287,9 +294,12 @@ __device__ __forceinline__ void rowproj_body(const RowprojArgs& A, int64_t blk) 
     }
 }
 
+// Eight waves per workgroup: at c4 (1536 columns, 24 steps) the 48- and
+// 32-rank passes ran 20.6 -> 18.0 and 15.9 -> 14.5 us against four waves.
+constexpr int kRowprojWaves = 8;
 template <int RC, int RT, int U>
-__global__ __launch_bounds__(256) void rowproj_bf16(RowprojArgs A) {
-    rowproj_body<RC, RT, U, false>(A, blockIdx.x);
+__global__ __launch_bounds__(64 * kRowprojWaves) void rowproj_bf16(RowprojArgs A) {
+    rowproj_body<RC, RT, U, false, kRowprojWaves>(A, blockIdx.x);
 }
 
 // ------------------------------------------------------------- colreduce
@@ -1233,7 +1243,7 @@ __global__ __launch_bounds__(256) void lora_bwd_operands(OperandsBatch ob) {
     const int64_t lb = b - ob.start[role];
     const int64_t nblk = ob.start[role + 1] - ob.start[role];
     if (kind == 0) {
-        rowproj_body<RC, RT, 1, true>(ob.rp[o], lb);
+        rowproj_body<RC, RT, 1, true, 4>(ob.rp[o], lb);
     } else if (kind == 1) {
         const PrepJob& ja = ob.prep[o];
         const int64_t n = ja.rows_out * ja.cols_out;
@@ -1403,28 +1413,17 @@ hipError_t launch_rowproj_bf16(const RowprojCall& c, hipStream_t stream) {
     // much per byte as streaming x, so the rows per fragment set the speed;
     // 16 or 32 rows per workgroup ran at 2.7 / 3.6 TB/s, 64 at 4.9 TB/s for
     // x [16384, 8960]). More than 64 ranks keep 32 rows (register budget).
-    // P_hi / P_lo hold 16 rowproj_rc(r) rows (zero past r).
+    // P_hi / P_lo hold 16 rowproj_rc(r) rows (zero past r) in fragment order.
     const dim3 g64((unsigned)((c.T + 63) / 64)), g32((unsigned)((c.T + 31) / 32));
     const RowprojArgs A = rowproj_args(c);
     switch (rowproj_rc(c.r)) {
-        case 1: rowproj_bf16<1, 4, 1><<<g64, 256, 0, stream>>>(A); break;
-        case 2: rowproj_bf16<2, 4, 1><<<g64, 256, 0, stream>>>(A); break;
-        case 3: rowproj_bf16<3, 4, 1><<<g64, 256, 0, stream>>>(A); break;
-        case 4: rowproj_bf16<4, 4, 1><<<g64, 256, 0, stream>>>(A); break;
-        default: rowproj_bf16<8, 2, 1><<<g32, 256, 0, stream>>>(A); break;
+        case 1: rowproj_bf16<1, 4, 1><<<g64, 64 * kRowprojWaves, 0, stream>>>(A); break;
+        case 2: rowproj_bf16<2, 4, 1><<<g64, 64 * kRowprojWaves, 0, stream>>>(A); break;
+        case 3: rowproj_bf16<3, 4, 1><<<g64, 64 * kRowprojWaves, 0, stream>>>(A); break;
+        case 4: rowproj_bf16<4, 4, 1><<<g64, 64 * kRowprojWaves, 0, stream>>>(A); break;
+        default: rowproj_bf16<8, 2, 1><<<g32, 64 * kRowprojWaves, 0, stream>>>(A); break;
     }
     return hipGetLastError();
-}
-
-hipError_t launch_rowproj_bf16(const uint16_t* X, int64_t T, int64_t C, const uint16_t* P_hi,
-                               const uint16_t* P_lo, int r, float scale, const uint8_t* mask,
-                               float keep, float* out_t, uint16_t* out_ext, int rext, float ext_scale,
-                               hipStream_t stream) {
-    RowprojCall c{};
-    c.X = X; c.T = T; c.C = C; c.P_hi = P_hi; c.P_lo = P_lo; c.r = r; c.rp = r; c.scale = scale;
-    c.mask[0] = mask; c.keep = keep; c.out_t[0] = out_t; c.out_ext = out_ext; c.rext_p = rext; c.ext_ld = rext;
-    c.ext_scale = ext_scale;
-    return launch_rowproj_bf16(c, stream);
 }
 
 hipError_t launch_transpose_bf16(const void* in, int64_t rows, int64_t cols, void* out, hipStream_t stream) {
