@@ -445,13 +445,15 @@ hipError_t launch_lora_bwd(const mc_lora_desc& d, const void* x, const void* W, 
         auto sc = gemm_scope(st, m.T, m.K, kbase, m.r, m.r, 4);
         MC_TRY(launch_gemm_f32(true, false, m.T, m.K, s0, s1, nullptr, static_cast<float*>(dX), m.K, st));
     }
-    if (dA) {
-        auto sc = lowrank_scope(st, m.T, m.K, m.r, 4);
-        MC_TRY(launch_colreduce_f32(static_cast<const float*>(x), m.T, m.K, gdt, m.r, 1.0f, true, dA, st));
-    }
-    if (dB) {
-        auto sc = lowrank_scope(st, m.T, m.N, m.r, 4);
-        MC_TRY(launch_colreduce_f32(dyf, m.T, m.N, h_save, m.r, d.scale, false, dB, st));
+    // dA = x^T.Gd and dB = s Hd^T.dY in one launch (one timed scope)
+    ColF32Call cc[2];
+    int nc = 0;
+    if (dA) cc[nc++] = ColF32Call{static_cast<const float*>(x), m.K, gdt, 1.0f, true, dA};
+    if (dB) cc[nc++] = ColF32Call{dyf, m.N, h_save, d.scale, false, dB};
+    if (nc > 0) {
+        auto sc = prof::Scope(prof::kLowRank, st, 2.0 * m.T * m.r * ((dA ? m.K : 0) + (dB ? m.N : 0)),
+                              4.0 * m.T * ((dA ? m.K + m.r : 0) + (dB ? m.N + m.r : 0)));
+        MC_TRY(launch_colreduce_f32(cc, nc, m.T, m.r, st));
     }
     return hipSuccess;
 }

@@ -300,7 +300,15 @@ hipError_t launch_rowproj_f32(const float* X, int64_t T, int64_t C, const float*
                               int r, float scale, const uint8_t* mask, float keep, float* out_t,
                               float* out_ext, float ext_scale, hipStream_t stream);
 // out = scale * sum_t Pt[j*T + t] * X[t][c]; layout as launch_split_sum.
-hipError_t launch_colreduce_f32(const float* X, int64_t T, int64_t C, const float* Pt, int r,
-                                float scale, bool transpose_out, float* out, hipStream_t stream);
+// One or two such reductions over the same T and r in one launch.
+struct ColF32Call {
+    const float* X;
+    int64_t C;
+    const float* Pt;
+    float scale;
+    bool transpose_out;
+    float* out;
+};
+hipError_t launch_colreduce_f32(const ColF32Call* calls, int n, int64_t T, int r, hipStream_t stream);
 
 }  // namespace mc

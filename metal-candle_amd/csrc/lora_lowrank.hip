@@ -1326,11 +1326,26 @@ __global__ __launch_bounds__(256) void rowproj_f32(const float* __restrict__ X, 
 // summing t = s, s + 64, ... in order (one 16-byte load of x per token when
 // C % 4 == 0, the 8 Pt values broadcast); the 64 slice sums are added in
 // slice order in two LDS stages (8 runs of 8, then the runs).
-__global__ __launch_bounds__(256) void colreduce_f32(const float* __restrict__ X, int64_t T, int64_t C,
-                                                     const float* __restrict__ Pt, int r, float scale,
-                                                     int transpose_out, float* __restrict__ out, int64_t ctiles) {
-    const int64_t c0 = (blockIdx.x % ctiles) * 16;
-    const int j0 = (int)(blockIdx.x / ctiles) * 8;
+// One or two reductions (dA over x and dB over dY) in one launch: blocks
+// [0, nblk0) take job 0, the rest job 1.
+struct ColF32Job {
+    const float* X;
+    int64_t C;
+    const float* Pt;
+    float scale;
+    int transpose_out;
+    float* out;
+    int64_t ctiles;
+};
+__global__ __launch_bounds__(256) void colreduce_f32(int64_t T, int r, ColF32Job ja, ColF32Job jb, int64_t nblk0) {
+    const bool second = (int64_t)blockIdx.x >= nblk0;  // workgroup-uniform
+    const ColF32Job& J = second ? jb : ja;
+    const int64_t b = (int64_t)blockIdx.x - (second ? nblk0 : 0);
+    const float* __restrict__ X = J.X;
+    const float* __restrict__ Pt = J.Pt;
+    const int64_t C = J.C, ctiles = J.ctiles;
+    const int64_t c0 = (b % ctiles) * 16;
+    const int j0 = (int)(b / ctiles) * 8;
     const int nj = r - j0 < 8 ? r - j0 : 8;
     const int cq = threadIdx.x & 3, sl = threadIdx.x >> 2;
     const int64_t c = c0 + 4 * cq;
@@ -1381,9 +1396,9 @@ __global__ __launch_bounds__(256) void colreduce_f32(const float* __restrict__ X
         for (int k = 1; k < 8; ++k) v += red2[k][j][col];
         const int64_t cc = c0 + col;
         if (j < nj && cc < C) {
-            v *= scale;
-            if (transpose_out) out[cc * r + j0 + j] = v;
-            else out[(int64_t)(j0 + j) * C + cc] = v;
+            v *= J.scale;
+            if (J.transpose_out) J.out[cc * r + j0 + j] = v;
+            else J.out[(int64_t)(j0 + j) * C + cc] = v;
         }
     }
 }
@@ -1866,12 +1881,18 @@ hipError_t launch_rowproj_f32(const float* X, int64_t T, int64_t C, const float*
     return hipGetLastError();
 }
 
-hipError_t launch_colreduce_f32(const float* X, int64_t T, int64_t C, const float* Pt, int r,
-                                float scale, bool transpose_out, float* out, hipStream_t stream) {
-    const int64_t ctiles = (C + 15) / 16, jchunks = (r + 7) / 8;
-    if (ctiles * jchunks >= ((int64_t)1 << 31)) return hipErrorInvalidValue;
-    colreduce_f32<<<dim3((unsigned)(ctiles * jchunks)), 256, 0, stream>>>(X, T, C, Pt, r, scale,
-                                                                          transpose_out ? 1 : 0, out, ctiles);
+hipError_t launch_colreduce_f32(const ColF32Call* calls, int n, int64_t T, int r, hipStream_t stream) {
+    if (n < 1 || n > 2) return hipErrorInvalidValue;
+    ColF32Job j[2]{};
+    int64_t nblk[2] = {0, 0};
+    for (int i = 0; i < n; ++i) {
+        const ColF32Call& c = calls[i];
+        j[i] = ColF32Job{c.X, c.C, c.Pt, c.scale, c.transpose_out ? 1 : 0, c.out, (c.C + 15) / 16};
+        nblk[i] = j[i].ctiles * ((r + 7) / 8);
+    }
+    if (nblk[0] + nblk[1] >= ((int64_t)1 << 31)) return hipErrorInvalidValue;
+    if (nblk[0] + nblk[1] == 0) return hipSuccess;
+    colreduce_f32<<<dim3((unsigned)(nblk[0] + nblk[1])), 256, 0, stream>>>(T, r, j[0], n > 1 ? j[1] : j[0], nblk[0]);
     return hipGetLastError();
 }
 
