@@ -136,15 +136,17 @@ __global__ __launch_bounds__(256) void prep_bf16(PrepBatch b) {
 // --------------------------------------------------------------- rowproj
 // Workgroup: NW waves, 16 RT token rows (RT MFMA row tiles). Wave w takes the
 // 64-column steps w, w+NW, ...; in a step, lane l (row l % 16 of each row
-// tile, group g = l / 16) loads the 16 contiguous columns 64 s + 16 g .. +15
-// of x and of the parameter rows (32 bytes per lane, whole 128-byte lines per
-// wave) and feeds them to two MFMA 16x16x32 as k-chunks (columns 0-7, then
-// 8-15 of its 16): the k order inside a step is permuted identically for x
-// and P, so the sum over columns is unchanged. The parameter fragments are
-// shared by the RT row tiles. All loads of U steps are issued before their
-// MFMAs, through buffer loads whose range check zeroes rows past T and
-// columns past C (no branches). The NW waves' partial sums are combined in
-// wave order through LDS.
+// tile, group g = l / 16) takes the 16 contiguous columns 64 s + 16 g .. +15
+// of x and of the parameter rows and feeds them to two MFMA 16x16x32 as
+// k-chunks (columns 0-7, then 8-15 of its 16): the k order inside a step is
+// permuted identically for x and P, so the sum over columns is unchanged.
+// The parameter fragments are shared by the RT row tiles. x is loaded in
+// whole 128-byte lines (8 rows per load) one step ahead and reaches the
+// MFMA layout through a per-wave LDS tile; at c4 the MFMA layout loaded
+// straight from memory (16 rows x 64 bytes per load) took the operand passes
+// 19.2 us against 16.8. Buffer range checks zero rows past T and columns
+// past C (no branches). The NW waves' partial sums are combined in wave order
+// through LDS.
 // Arguments of one row projection. With PF32 the parameter is read as fp32
 // P [prows][C] (rows past prows load as zeros) and split into bf16 hi + lo in
 // registers; otherwise it comes prepared as bf16 P_hi / P_lo [16 RC][C] in
@@ -179,6 +181,7 @@ struct RowprojArgs {
 
 template <int RC, int RT, int U, bool PF32, int NW>
 __device__ __forceinline__ void rowproj_body(const RowprojArgs& A, int64_t blk) {
+    static_assert(U == 1, "one step per iteration, the next step's x in flight");
     const uint16_t* __restrict__ X = A.X;
     const int64_t T = A.T, C = A.C;
     const int r = A.r, rp = A.rp, rext_p = A.rext_p, ext_ld = A.ext_ld;
@@ -203,67 +206,94 @@ __device__ __forceinline__ void rowproj_body(const RowprojArgs& A, int64_t blk) 
 #pragma unroll
         for (int rc = 0; rc < RC; ++rc) acc[rt][rc] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    for (int64_t s0 = wave; s0 < nsteps; s0 += NW * U) {
-        i32x4 xv[U][RT][2], ph[U][RC][2], pl[U][RC][2];
+    // x goes through a per-wave LDS tile: each load covers 8 rows x 128
+    // bytes (whole lines) instead of the MFMA layout's 16 rows x 64 bytes;
+    // chunk c of tile row rr sits in slot c ^ ((rr >> 1) & 7). The next
+    // step's x is loaded while this step's is used. The tile shares its
+    // memory with the wave-combine buffer below.
+    constexpr int XST_BYTES = NW * RT * 16 * 128;
+    constexpr int RED_BYTES = NW * RT * RC * 4 * 64 * 4;
+    __shared__ __attribute__((aligned(16))) char lds_buf[XST_BYTES > RED_BYTES ? XST_BYTES : RED_BYTES];
+    uint4 (*xst)[16][8] = reinterpret_cast<uint4 (*)[16][8]>(lds_buf) + wave * RT;
+    const int nsw = nsteps > wave ? (int)((nsteps - wave + NW - 1) / NW) : 0;  // this wave's steps
+    const int xr = lane >> 3, xc8 = lane & 7;
+    i32x4 xa[RT][2], xb[RT][2];
+    auto load_x = [&](int64_t st, i32x4 (&v)[RT][2]) {
+        const int64_t col = st * 64 + 8 * xc8;
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int64_t st = s0 + NW * u;
-            const int64_t c = st * 64 + grp * 16;  // steps past the end load zeros
+        for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const bool ok = c + 8 * h < C;
+            for (int hp = 0; hp < 2; ++hp)
+                v[rt][hp] = buf_load16(rx, col < C ? (uint32_t)(((int64_t)(rt * 16 + 8 * hp + xr) * C + col) * 2) : kOOB);
+    };
+    if (nsw > 0) load_x(wave, xa);
+    for (int i = 0; i < nsw; ++i) {
+        const int64_t st = wave + (int64_t)NW * i;
+        const int64_t c = st * 64 + grp * 16;
+        i32x4 ph[RC][2], pl[RC][2];
 #pragma unroll
-                for (int rt = 0; rt < RT; ++rt)
-                    xv[u][rt][h] = buf_load16(rx, ok ? (uint32_t)(((int64_t)(rt * 16 + row) * C + c + 8 * h) * 2) : kOOB);
+        for (int h = 0; h < 2; ++h) {
+            const bool ok = c + 8 * h < C;
 #pragma unroll
-                for (int rc = 0; rc < RC; ++rc) {
-                    if constexpr (PF32) {
-                        // 8 fp32 (two 16-byte loads) -> bf16 hi + lo
-                        const uint32_t off = ok ? (uint32_t)(((int64_t)(rc * 16 + row) * C + c + 8 * h) * 4) : kOOB;
-                        const i32x4 a = buf_load16(rhi, off), b = buf_load16(rhi, ok ? off + 16 : kOOB);
-                        float v[8], rem[8];
+            for (int rc = 0; rc < RC; ++rc) {
+                if constexpr (PF32) {
+                    const uint32_t off = ok ? (uint32_t)(((int64_t)(rc * 16 + row) * C + c + 8 * h) * 4) : kOOB;
+                    const i32x4 a = buf_load16(rhi, off), b = buf_load16(rhi, ok ? off + 16 : kOOB);
+                    float v[8], rem[8];
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            v[e] = __int_as_float(a[e]);
-                            v[4 + e] = __int_as_float(b[e]);
-                        }
-                        const bf16x8 hi = pack_bf16x8(v);
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) rem[e] = v[e] - static_cast<float>(hi[e]);
-                        ph[u][rc][h] = __builtin_bit_cast(i32x4, hi);
-                        pl[u][rc][h] = __builtin_bit_cast(i32x4, pack_bf16x8(rem));
-                    } else {
-                        const uint32_t off = ok ? (uint32_t)((((st * RC + rc) * 2 + h) * 64 + lane) * 16) : kOOB;
-                        ph[u][rc][h] = buf_load16(rhi, off);
-                        pl[u][rc][h] = buf_load16(rlo, off);
+                    for (int e = 0; e < 4; ++e) {
+                        v[e] = __int_as_float(a[e]);
+                        v[4 + e] = __int_as_float(b[e]);
                     }
+                    const bf16x8 hi = pack_bf16x8(v);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) rem[e] = v[e] - static_cast<float>(hi[e]);
+                    ph[rc][h] = __builtin_bit_cast(i32x4, hi);
+                    pl[rc][h] = __builtin_bit_cast(i32x4, pack_bf16x8(rem));
+                } else {
+                    const uint32_t off = ok ? (uint32_t)((((st * RC + rc) * 2 + h) * 64 + lane) * 16) : kOOB;
+                    ph[rc][h] = buf_load16(rhi, off);
+                    pl[rc][h] = buf_load16(rlo, off);
                 }
             }
         }
+        if (i + 1 < nsw) load_x(st + NW, xb);  // wave-uniform
+        // this step's x: whole-line registers -> LDS -> MFMA layout (a
+        // wave's LDS operations complete in order)
 #pragma unroll
-        for (int u = 0; u < U; ++u)
+        for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-            for (int h = 0; h < 2; ++h)
+            for (int hp = 0; hp < 2; ++hp) {
+                const int rr = 8 * hp + xr;
+                xst[rt][rr][xc8 ^ ((rr >> 1) & 7)] = __builtin_bit_cast(uint4, xa[rt][hp]);
+            }
+        i32x4 xv[RT][2];
 #pragma unroll
-                for (int rt = 0; rt < RT; ++rt)
+        for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-                    for (int rc = 0; rc < RC; ++rc) {
-                        const bf16x8 xa = __builtin_bit_cast(bf16x8, xv[u][rt][h]);
-                        acc[rt][rc] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                            xa, __builtin_bit_cast(bf16x8, ph[u][rc][h]), acc[rt][rc], 0, 0, 0);
-                        acc[rt][rc] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                            xa, __builtin_bit_cast(bf16x8, pl[u][rc][h]), acc[rt][rc], 0, 0, 0);
-                    }
-        // keep every load of the block ahead of its MFMAs (the scheduler
-        // would otherwise sink each load next to its use to save registers,
-        // exposing one memory latency per MFMA pair)
-        __builtin_amdgcn_sched_group_barrier(kSchedVmemRead, U * 2 * (RT + 2 * RC), 0);
-        __builtin_amdgcn_sched_group_barrier(kSchedMfma, U * 4 * RT * RC, 0);
+            for (int h = 0; h < 2; ++h) xv[rt][h] = __builtin_bit_cast(i32x4, xst[rt][row][(2 * grp + h) ^ ((row >> 1) & 7)]);
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+                for (int rc = 0; rc < RC; ++rc) {
+                    const bf16x8 xq = __builtin_bit_cast(bf16x8, xv[rt][h]);
+                    acc[rt][rc] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                        xq, __builtin_bit_cast(bf16x8, ph[rc][h]), acc[rt][rc], 0, 0, 0);
+                    acc[rt][rc] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                        xq, __builtin_bit_cast(bf16x8, pl[rc][h]), acc[rt][rc], 0, 0, 0);
+                }
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+            for (int hp = 0; hp < 2; ++hp) xa[rt][hp] = xb[rt][hp];
     }
+    __syncthreads();  // every wave is done with its x tile before the buffer is reused
 
     // combine the NW waves: [wave][rt][rc][q][lane]; accumulator q of lane l
     // is token 4 (l / 16) + q of its row tile, rank index l % 16.
-    __shared__ float red[NW][RT][RC][4][64];
+    float (*red)[RT][RC][4][64] = reinterpret_cast<float (*)[RT][RC][4][64]>(lds_buf);
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
