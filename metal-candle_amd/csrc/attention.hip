@@ -482,6 +482,8 @@ struct AttnBwdArgs {
     uint16_t* dst;         // [B, H, S, ldst]: dS^T (key rows, query columns) for the dQ pass, or null
     int64_t ldst;
     int ngroups;           // query-head groups per K/V head in the dK/dV kernel (H / Hkv / ngroups heads each)
+    int64_t dq_blocks;     // the dQ pass's own workgroups; blocks past them sum the groups' partials
+    int64_t sum_n8;        // 8-element units of one of dk / dv (B Hkv S D / 8)
     int64_t S, Sp;
     int B, H, Hkv, causal, nblk;
     float scale, scale_log2;
@@ -887,12 +889,10 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_bf16(AttnBwdArgs a) {
 
 // dk / dv [B, Hkv, S, D] = sum over the rep query-head groups of each K/V
 // head of the fp32 partials, in group order; 8 elements per thread.
-__global__ __launch_bounds__(256) void attn_bwd_sum(const float* __restrict__ dk_part,
-                                                    const float* __restrict__ dv_part, uint16_t* __restrict__ dk,
-                                                    uint16_t* __restrict__ dv, int rep, int64_t per_head,
-                                                    int64_t n8) {
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < 2 * n8;
-         i += (int64_t)gridDim.x * blockDim.x) {
+__device__ __forceinline__ void bwd_sum_range(const float* __restrict__ dk_part, const float* __restrict__ dv_part,
+                                              uint16_t* __restrict__ dk, uint16_t* __restrict__ dv, int rep,
+                                              int64_t per_head, int64_t n8, int64_t first, int64_t stride) {
+    for (int64_t i = first; i < 2 * n8; i += stride) {
         const bool second = i >= n8;
         const int64_t e = (second ? i - n8 : i) * 8;  // element of [B, Hkv, S, D]
         const int64_t bhk = e / per_head, off = e % per_head;
@@ -908,6 +908,13 @@ __global__ __launch_bounds__(256) void attn_bwd_sum(const float* __restrict__ dk
         *reinterpret_cast<uint4*>(dst) = make_uint4(pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3]),
                                                     pack_bf16x2(acc[4], acc[5]), pack_bf16x2(acc[6], acc[7]));
     }
+}
+__global__ __launch_bounds__(256) void attn_bwd_sum(const float* __restrict__ dk_part,
+                                                    const float* __restrict__ dv_part, uint16_t* __restrict__ dk,
+                                                    uint16_t* __restrict__ dv, int rep, int64_t per_head,
+                                                    int64_t n8) {
+    bwd_sum_range(dk_part, dv_part, dk, dv, rep, per_head, n8, (int64_t)blockIdx.x * blockDim.x + threadIdx.x,
+                  (int64_t)gridDim.x * blockDim.x);
 }
 
 // ------------------------------------------------------------------- dQ
@@ -1073,6 +1080,14 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq_bf16(AttnBwdArgs a) {
 // zeros from both buffers; dS^T columns of queries past S are never stored.
 template <int D>
 __global__ __launch_bounds__(256, 2) void attn_bwd_dq_ds_bf16(AttnBwdArgs a) {
+    if ((int64_t)blockIdx.x >= a.dq_blocks) {
+        // the groups' dK / dV partial sums (independent of dQ), as blocks
+        // dispatched after the dQ blocks so that they fill the pass's tail
+        const int64_t sb = (int64_t)blockIdx.x - a.dq_blocks, nsb = (int64_t)gridDim.x - a.dq_blocks;
+        bwd_sum_range(a.dk_part, a.dv_part, a.dk, a.dv, a.ngroups, a.S * D, a.sum_n8, sb * 256 + threadIdx.x,
+                      nsb * 256);
+        return;
+    }
     constexpr int KB = 64, QB = 128, DT = D / 32;
     constexpr int KT = 64 * D, DSTILE = 64 * QB;  // K tile, dS^T tile (elements)
     constexpr int STAGE = KT + DSTILE;
@@ -1415,6 +1430,8 @@ hipError_t launch_attention_bwd(const mc_attn_desc& d, const void* q, const void
         a.B = B; a.H = H; a.Hkv = Hkv;
         a.causal = d.causal ? 1 : 0;
         a.nblk = (int)((S + 127) / 128);
+        a.dq_blocks = (int64_t)a.nblk * B * H;
+        a.sum_n8 = (int64_t)B * Hkv * S * D / 8;
         a.scale = d.scale;
         a.scale_log2 = d.scale * kLog2e;
         const dim3 gprep((unsigned)(Sp / 64), (unsigned)(B * H));
@@ -1430,15 +1447,19 @@ hipError_t launch_attention_bwd(const mc_attn_desc& d, const void* q, const void
             attn_bwd_prep_bf16<128><<<gprep, 256, 0, stream>>>(o16, do16, lse, H, S, Sp, lsd);
             attn_bwd_dkdv_bf16<128><<<gkv, 256, 0, stream>>>(a);
         }
-        if (a.ngroups > 1) {
-            const int64_t n8 = (int64_t)B * Hkv * S * D / 8;
+        const int64_t n8 = a.sum_n8;
+        if (a.ngroups > 1 && !from_ds) {
             const int64_t blocks = std::min<int64_t>((2 * n8 + 255) / 256, 4096);
             attn_bwd_sum<<<dim3((unsigned)blocks), 256, 0, stream>>>(a.dk_part, a.dv_part, a.dk, a.dv, a.ngroups,
                                                                      S * D, n8);
         }
         if (from_ds) {
-            if (D == 64) attn_bwd_dq_ds_bf16<64><<<grid, 256, 0, stream>>>(a);
-            else attn_bwd_dq_ds_bf16<128><<<grid, 256, 0, stream>>>(a);
+            // with partials, the dQ launch also sums them: 512 more blocks
+            // (a round of its two-per-CU slots), dispatched after the dQ blocks
+            const int64_t nsum = a.ngroups > 1 ? std::min<int64_t>((2 * n8 + 255) / 256, 512) : 0;
+            const dim3 gds((unsigned)(a.dq_blocks + nsum));
+            if (D == 64) attn_bwd_dq_ds_bf16<64><<<gds, 256, 0, stream>>>(a);
+            else attn_bwd_dq_ds_bf16<128><<<gds, 256, 0, stream>>>(a);
         } else {
             if (D == 64) attn_bwd_dq_bf16<64><<<grid, 256, 0, stream>>>(a);
             else attn_bwd_dq_bf16<128><<<grid, 256, 0, stream>>>(a);
