@@ -61,6 +61,14 @@ __device__ __forceinline__ int64_t max64(int64_t x, int64_t y) { return x > y ? 
 // Instruction classes of __builtin_amdgcn_sched_group_barrier.
 constexpr int kSchedMfma = 0x008, kSchedDsRead = 0x100;
 
+// max(v of lane l, v of lane l ^ 32) without LDS. v_permlane32_swap swaps
+// lanes 32-63 of its first register with lanes 0-31 of its second; with v in
+// both, every lane then holds v of lanes l & 31 and (l & 31) + 32.
+__device__ __forceinline__ float half_pair_max(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 __device__ __forceinline__ int perm16(int p) { return (p & 3) | ((p & 4) << 1) | ((p & 8) >> 1); }
 
 // ------------------------------------------------------------ V^T prepass
@@ -254,14 +262,16 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16(AttnFwdArgs a) {
         const bool edge = key0 + KB > S || (a.causal && key0 + KB - 1 > qw);
         if (edge) {
             // key offsets in the block (32 t + 8 (j/4) + 4 half + j%4) against
-            // the first offset past S and, causal, this lane's query offset
-            const int lim = (int)min64(S - key0, KB);
-            const int qrel = a.causal ? (int)max64(min64(my_q - key0, KB), -1) : KB;
+            // the first offset past S and, causal, this lane's query offset;
+            // the lane's 4 half moves to the bounds, so each test compares a
+            // constant
+            const int lim = (int)min64(S - key0, KB) - 4 * half;
+            const int qrel = (a.causal ? (int)max64(min64(my_q - key0, KB), -1) : KB) - 4 * half;
 #pragma unroll
             for (int t = 0; t < 2; ++t)
 #pragma unroll
                 for (int j = 0; j < 16; ++j) {
-                    const int ko = 32 * t + 8 * (j >> 2) + 4 * half + (j & 3);
+                    const int ko = 32 * t + 8 * (j >> 2) + (j & 3);
                     if (ko >= lim || ko > qrel) x[t][j] = kNegInf;
                 }
         }
@@ -272,7 +282,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16(AttnFwdArgs a) {
         for (int t = 0; t < 2; ++t)
 #pragma unroll
             for (int j = 0; j < 16; ++j) mx = fmaxf(mx, x[t][j]);
-        mx = fmaxf(mx, __shfl_xor(mx, 32, kWave)) * cx;  // cx > 0: -inf stays -inf
+        mx = half_pair_max(mx) * cx;  // cx > 0: -inf stays -inf
         // The reference point m_run moves only when the block's max exceeds
         // it by more than kMaxSlack (log2 units; first block: any finite max).
         // Below that, p = 2^(x - m_run) stays under 2^kMaxSlack, which fp32 sums
@@ -764,7 +774,9 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_bf16(AttnBwdArgs a) {
                           bf16x8 (&pb)[2], bf16x8 (&db)[2]) {
             constexpr bool MASK = decltype(mask_tag)::value, EDGE = decltype(edge_tag)::value;
             constexpr int t = decltype(t_tag)::value;
-            const int kq = (int)(my_key - q0);
+            // the lane's 4 half moves to the key side, so each causal test
+            // compares a constant
+            const int kq = (int)(my_key - q0) - 4 * half;
             float p[16], ds[16];
 #pragma unroll
             for (int jq = 0; jq < 4; ++jq) {
@@ -787,7 +799,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_bf16(AttnBwdArgs a) {
                         x = __builtin_fmaf(sacc[j], a.scale_log2, -lv[e]);
                     }
                     if constexpr (EDGE) {
-                        if ((!MASK || a.causal) && kq > qi + e) x = kNegInf;
+                        if ((!MASK || a.causal) && kq > 32 * t + 8 * jq + e) x = kNegInf;
                     }
                     p[j] = exp2_hw(x);
                     ds[j] = p[j] * (dpacc[j] - dv4[e]);
