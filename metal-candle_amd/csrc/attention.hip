@@ -751,6 +751,13 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_bf16(AttnBwdArgs a) {
         vf[s] = frag_at(svw, roff[s]);
     }
     for (int it = 0; it < nit; ++it) {
+        // The dV / dK accumulators are pinned to AGPRs at the top of every
+        // block (an empty asm with an AGPR operand). Left to itself, the
+        // register allocator gave one tile's S / dP accumulators the AGPRs of
+        // two dV / dK tiles and moved those 32 values to VGPRs and back on
+        // every block.
+#pragma unroll
+        for (int t = 0; t < DT; ++t) asm volatile("" : "+a"(dvacc[t]), "+a"(dkacc[t]));
         wait_vmcnt<0>();
         __syncthreads();
         if (it + 1 < nit) issue(it + 1, (it + 1) & 1);
