@@ -69,6 +69,15 @@ __device__ __forceinline__ float half_pair_max(float v) {
     return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
+// Position of a workgroup among the B * H (batch, head) workgroups of its
+// query-block round. Workgroups are dispatched round-robin over the 8 XCDs
+// (id mod 8); when the round is a multiple of 8 long, each XCD takes a
+// contiguous run of (b, h), so the heads that share a K / V head share that
+// XCD's L2. The rounds, heaviest query blocks first, keep their order.
+__device__ __forceinline__ int xcd_head_order(int j, int nbh) {
+    return (nbh & 7) ? j : (j & 7) * (nbh >> 3) + (j >> 3);
+}
+
 __device__ __forceinline__ int perm16(int p) { return (p & 3) | ((p & 4) << 1) | ((p & 8) >> 1); }
 
 // ------------------------------------------------------------ V^T prepass
@@ -137,7 +146,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16(AttnFwdArgs a) {
     const int col = lane & 31, half = lane >> 5;
     const int nbh = a.B * a.H;
     const int qb = a.nqb - 1 - (int)(blockIdx.x / nbh);  // heaviest query blocks first
-    const int bh = (int)(blockIdx.x % nbh);
+    const int bh = xcd_head_order((int)(blockIdx.x % nbh), nbh);
     const int b = bh / a.H, h = bh % a.H;
     const int hk = h / (a.H / a.Hkv);
     const int64_t S = a.S;
@@ -951,7 +960,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq_bf16(AttnBwdArgs a) {
     const int nbh = a.B * a.H;
     const int nqb = (int)((a.S + QB - 1) / QB);
     const int qb = nqb - 1 - (int)(blockIdx.x / nbh);  // heaviest query blocks first
-    const int bh = (int)(blockIdx.x % nbh);
+    const int bh = xcd_head_order((int)(blockIdx.x % nbh), nbh);
     const int b = bh / a.H, h = bh % a.H;
     const int64_t bhk = (int64_t)b * a.Hkv + h / (a.H / a.Hkv);
     const int64_t S = a.S;
@@ -1117,7 +1126,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_ds_bf16(AttnBwdArgs a) {
     const int nbh = a.B * a.H;
     const int nqb = (int)((a.S + QB - 1) / QB);
     const int qb = nqb - 1 - (int)(blockIdx.x / nbh);  // heaviest query blocks first
-    const int bh = (int)(blockIdx.x % nbh);
+    const int bh = xcd_head_order((int)(blockIdx.x % nbh), nbh);
     const int b = bh / a.H, h = bh % a.H;
     const int64_t bhk = (int64_t)b * a.Hkv + h / (a.H / a.Hkv);
     const int64_t S = a.S;
