@@ -750,7 +750,12 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_bf16(AttnBwdArgs a) {
 
     if (nit > 0) issue(0, 0);
     // The wave's K and V fragments (B operands of S and dP) are the same for
-    // every block: read from LDS once, then held in registers.
+    // every block: read from LDS once, then held in AGPRs (an empty asm with
+    // AGPR operands puts them there; MFMAs read their A / B operands from
+    // either file). This file is compiled with the MFMAs' accumulators in
+    // VGPRs (-amdgpu-mfma-vgpr-form), so the score arithmetic reads S and dP
+    // where the MFMAs leave them, and the VGPRs the fragments would take hold
+    // the dV / dK accumulators.
     wait_vmcnt<0>();
     __syncthreads();
     bf16x8 kf[KS], vf[KS];
@@ -758,15 +763,9 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv_bf16(AttnBwdArgs a) {
     for (int s = 0; s < KS; ++s) {
         kf[s] = frag_at(skw, roff[s]);
         vf[s] = frag_at(svw, roff[s]);
+        asm volatile("" : "+a"(kf[s]), "+a"(vf[s]));
     }
     for (int it = 0; it < nit; ++it) {
-        // The dV / dK accumulators are pinned to AGPRs at the top of every
-        // block (an empty asm with an AGPR operand). Left to itself, the
-        // register allocator gave one tile's S / dP accumulators the AGPRs of
-        // two dV / dK tiles and moved those 32 values to VGPRs and back on
-        // every block.
-#pragma unroll
-        for (int t = 0; t < DT; ++t) asm volatile("" : "+a"(dvacc[t]), "+a"(dkacc[t]));
         wait_vmcnt<0>();
         __syncthreads();
         if (it + 1 < nit) issue(it + 1, (it + 1) & 1);
