@@ -52,11 +52,17 @@ __global__ __launch_bounds__(256) void layernorm_fwd_vec(int64_t rows, int dim, 
     const __amdgpu_buffer_rsrc_t rb = make_rsrc(b, b ? (int64_t)dim * ES : 0);
     const int nvec = dim / N;
     const uint32_t rowoff = (uint32_t)(wave * dim * ES);
+    // x, w and b are all requested before the row's two reductions (w and b
+    // stay packed until use), so their latency is not paid after them
     float v[VPL][N];
+    i32x4 wq[VPL], bq[VPL];
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
         const int vi = lane + i * kWave;
-        BVec<T>::load(rx, vi < nvec ? rowoff + (uint32_t)(vi * N * ES) : kOOB, v[i]);
+        const uint32_t off = vi < nvec ? (uint32_t)(vi * N * ES) : kOOB;
+        BVec<T>::load(rx, off == kOOB ? kOOB : rowoff + off, v[i]);
+        wq[i] = buf_load16(rw, off);
+        bq[i] = buf_load16(rb, off);
     }
     float s = 0.f;
 #pragma unroll
@@ -85,8 +91,8 @@ __global__ __launch_bounds__(256) void layernorm_fwd_vec(int64_t rows, int dim, 
         const int vi = lane + i * kWave;
         const uint32_t off = vi < nvec ? (uint32_t)(vi * N * ES) : kOOB;
         float wv[N], bv[N], o[N];
-        BVec<T>::load(rw, off, wv);
-        BVec<T>::load(rb, off, bv);
+        BVec<T>::unpack(wq[i], wv);
+        BVec<T>::unpack(bq[i], bv);
 #pragma unroll
         for (int e = 0; e < N; ++e) {
             float t = (v[i][e] - mean) * r;
