@@ -644,25 +644,38 @@ __global__ __launch_bounds__(256) void attn_bwd_prep_bf16(const uint16_t* __rest
     const int64_t ldo = (int64_t)H * D;
     const __amdgpu_buffer_rsrc_t ro = make_rsrc(o + (b * S * H + h) * D, (S * H - h) * D * 2);
     const __amdgpu_buffer_rsrc_t rd = make_rsrc(dout + (b * S * H + h) * D, (S * H - h) * D * 2);
-    const int row = threadIdx.x >> 2, part = threadIdx.x & 3;
-    const bool ok = q0 + row < S;
-    float acc = 0.f;
+    // Each wave takes 16 rows. One load instruction covers RPI whole rows:
+    // lane l reads chunk l % CPR of row l / CPR, so the wave's 64 lanes read
+    // contiguous 16-byte chunks; the CPR lanes of a row then add their parts.
+    constexpr int RPI = 64 / CPR, NI = 16 / RPI;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int ch = lane % CPR, rsub = lane / CPR;
+    float acc[NI];
 #pragma unroll
-    for (int c = 0; c < CPR / 4; ++c) {
-        const uint32_t off = ok ? (uint32_t)(((q0 + row) * ldo + 8 * (part * (CPR / 4) + c)) * 2) : kOOB;
+    for (int i = 0; i < NI; ++i) {
+        const int row = wave * 16 + i * RPI + rsub;
+        const uint32_t off = q0 + row < S ? (uint32_t)(((q0 + row) * ldo + 8 * ch) * 2) : kOOB;
         float x[8], g[8];
         BVec<uint16_t>::unpack(buf_load16(ro, off), x);
         BVec<uint16_t>::unpack(buf_load16(rd, off), g);
+        acc[i] = 0.f;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc += x[e] * g[e];
+        for (int e = 0; e < 8; ++e) acc[i] += x[e] * g[e];
     }
-    acc += __shfl_xor(acc, 1, kWave);
-    acc += __shfl_xor(acc, 2, kWave);
-    if (part == 0) {
+#pragma unroll
+    for (int i = 0; i < NI; ++i)
+#pragma unroll
+        for (int m = 1; m < CPR; m <<= 1) acc[i] += __shfl_xor(acc[i], m, kWave);
+    if (ch == 0) {
         float* blk = lsd + (bh * (Sp / 64) + blockIdx.x) * 128;
-        // padded queries: lse = +inf makes their P exactly 0
-        blk[row] = ok ? lse[bh * S + q0 + row] * kLog2e : __builtin_inff();
-        blk[64 + row] = ok ? acc : 0.f;
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const int row = wave * 16 + i * RPI + rsub;
+            const bool ok = q0 + row < S;
+            // padded queries: lse = +inf makes their P exactly 0
+            blk[row] = ok ? lse[bh * S + q0 + row] * kLog2e : __builtin_inff();
+            blk[64 + row] = ok ? acc[i] : 0.f;
+        }
     }
 }
 
